@@ -1,0 +1,207 @@
+/*
+ * levo_hip.h — C ABI of the MI355X (gfx950) kernels behind LeVo2.cpp's
+ * elementwise / reduction / broadcast hot path.
+ *
+ * Conventions (all entry points):
+ *   - Every data pointer is a device pointer owned by the caller; no entry
+ *     point allocates device memory.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
+ *     runs asynchronously; entry points are reentrant across streams.
+ *   - Return LEVO_HIP_OK (0) or a negative levo_hip_status. The message of the
+ *     last failure on the calling thread is levo_hip_last_error(), the same
+ *     pattern as the reference's C ABI (include/cantor_engine.h:50-60,
+ *     src/cantor-abi.cpp:58-82).
+ *   - Arithmetic follows the reference's F32 rounding points (no FMA
+ *     contraction where the reference computes a*b+c in two roundings).
+ *
+ * Each declaration names the reference function or ggml op chain it replaces.
+ */
+#ifndef LEVO_HIP_H
+#define LEVO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LEVO_HIP_ABI_VERSION 1
+
+/* Same tag as HIP's hipStream_t, so a hipStream_t converts without a cast. */
+typedef struct ihipStream_t * levo_hip_stream_t;
+
+typedef enum levo_hip_status {
+    LEVO_HIP_OK = 0,
+    LEVO_HIP_ERR_INVALID = -1,     /* bad argument (null pointer, shape, value) */
+    LEVO_HIP_ERR_UNSUPPORTED = -2, /* type / shape combination not implemented */
+    LEVO_HIP_ERR_RUNTIME = -3      /* HIP runtime reported an error */
+} levo_hip_status;
+
+/* Element / block types, numbered as ggml's public ggml_type enum so that a
+ * ggml caller passes its tensor->type unchanged. */
+typedef enum levo_hip_type {
+    LEVO_HIP_TYPE_F32 = 0,
+    LEVO_HIP_TYPE_F16 = 1,
+    LEVO_HIP_TYPE_Q4_0 = 2,
+    LEVO_HIP_TYPE_Q8_0 = 8
+} levo_hip_type;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char * levo_hip_last_error(void);
+int levo_hip_abi_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* SnakeBeta                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Replaces levo::detail::snake_beta (src/levo-audio-ops.cpp:125-152; decl
+ * src/levo-audio-ops.h:30-33), which builds the ggml chain
+ *   y = x + sin(x * exp(alpha_log))^2 / (exp(beta_log) * 1 + 1e-9)
+ * over x of ggml shape [time, channels, 1] (each channel row contiguous).
+ * x, y: F32 [channels][time] with row strides x_stride, y_stride (elements,
+ * >= time); y may equal x. alpha_log, beta_log: [channels] of param_type
+ * (F32, or F16 promoted exactly to F32 as src/levo-audio-ops.cpp:143-144). */
+int levo_hip_snake_beta(const float * x, int64_t x_stride,
+                        const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                        float * y, int64_t y_stride,
+                        int64_t channels, int64_t time, levo_hip_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Residual add + RMSNorm / LayerNorm (rows of `dim` contiguous elements)    */
+/* ------------------------------------------------------------------------ */
+
+/* h = x + delta (delta may be NULL: h = x), written to h_out when non-NULL;
+ * y = rms_norm(h, eps) * weight.
+ * act_type F16: the LeLM F16-activation chain of rms_norm_weighted
+ *   (src/levo-kv.cpp:153-160) after the F16 residual add (:462, :507):
+ *   h = f16(x + d); y = f16(f16(h * 1/sqrtf(mean(h^2) + eps)) * w); weight F16.
+ * act_type F32: src/levo-lm.cpp:131-137 (weight F32, or F16 promoted to F32).
+ * The row reduction accumulates in double, like ggml-cpu's ggml_float sum. */
+int levo_hip_residual_rms_norm(levo_hip_type act_type, const void * x, const void * delta,
+                               const void * weight, levo_hip_type weight_type,
+                               void * h_out, void * y, int64_t rows, int64_t dim, float eps,
+                               levo_hip_stream_t stream);
+
+/* h = x + delta as above; y = norm(h, eps) * gamma + beta — the Flow
+ * estimator's layer_norm = ggml_norm -> ggml_mul -> ggml_add
+ * (src/levo-flow-estimator.cpp:106-109) fused with its residual add
+ * (:221-227, :243-247). act_type F32 (reference) or F16 (F16 storage with the
+ * same F32 chain, output rounded once to F16). gamma/beta of param_type. */
+int levo_hip_residual_layer_norm(levo_hip_type act_type, const void * x, const void * delta,
+                                 const void * gamma, const void * beta, levo_hip_type param_type,
+                                 void * h_out, void * y, int64_t rows, int64_t dim, float eps,
+                                 levo_hip_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* CFG combine + temperature softmax + argmax / top-k (LeLM sampling)        */
+/* ------------------------------------------------------------------------ */
+
+/* Elementwise out = uncond + scale * (cond - uncond): levo::apply_cfg
+ * (src/levo-sampling.cpp:22-28) and combine_renderer_cfg
+ * (src/levo-renderer-pattern.cpp:123-135). */
+int levo_hip_cfg_combine(float * out, const float * uncond, const float * cond, int64_t n,
+                         float scale, levo_hip_stream_t stream);
+
+#define LEVO_HIP_MAX_STREAMS 8
+
+/* Arguments of levo_hip_cfg_sample. Rows are ordered [position][stream]
+ * (stream = row % n_streams) and start row_pitch elements apart. */
+typedef struct levo_hip_sample_args {
+    const float * cond;   /* [rows][row_pitch] conditional logits */
+    const float * uncond; /* [rows][row_pitch]; NULL: logits = cond (no CFG) */
+    int64_t rows;
+    int64_t vocab;        /* logits per row (V), 1 <= V <= 32768 */
+    int64_t row_pitch;    /* >= vocab */
+    float cfg_scale;      /* l = u + cfg_scale * (c - u) */
+    float temperature;    /* softmax temperature for cand_probs / row_lse (> 0) */
+    int32_t n_streams;    /* 1 .. LEVO_HIP_MAX_STREAMS */
+    int32_t top_k[LEVO_HIP_MAX_STREAMS]; /* per stream; 0 or >= V keeps every id */
+    /* Optional unique-token repetition penalty (src/levo-sampling.cpp:39-47,
+     * :137-143): recent is [rows][n_recent] ids (< 0 = padding); each distinct
+     * id in [0, penalty_limit) is divided once by repetition_penalty. */
+    const int64_t * recent;
+    int32_t n_recent;
+    float repetition_penalty;
+    int64_t penalty_limit; /* 0 = V */
+    /* Optional ids forced to -inf on stream-0 rows after the penalty
+     * (src/levo-sampling.cpp:146-147). */
+    const int64_t * ignore;
+    int32_t n_ignore;
+    /* Outputs. */
+    int32_t * best;       /* [rows] first maximum (std::max_element, :94-96); -1 on NaN */
+    int32_t * count;      /* [rows] candidate count (may exceed capacity); -1 on NaN */
+    int32_t * cand_ids;   /* [rows][capacity] candidates in ascending id order (:84-93) */
+    float * cand_logits;  /* [rows][capacity] their adjusted logits, or NULL */
+    float * cand_probs;   /* [rows][capacity] exp((l-max)/T) normalised over the
+                           * candidates (:98-107), or NULL */
+    float * row_max;      /* [rows] max adjusted logit, or NULL */
+    float * row_lse;      /* [rows] log sum_v exp(l_v / T) over all V ids, or NULL */
+    int32_t capacity;     /* candidate slots per row (>= 1) */
+} levo_hip_sample_args;
+
+/* One launch per batch of rows: CFG, penalty/ignore, NaN check, row max and
+ * argmax, the top-k candidate set of sample_top_k_counted
+ * (src/levo-sampling.cpp:75-116; ties with the k-th value are kept) and the
+ * temperature softmax over it. The single uniform draw of a sampled token
+ * stays on the host so the mt19937_64 cursor is unchanged. */
+int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Flow Euler / CFG latent update                                            */
+/* ------------------------------------------------------------------------ */
+
+/* state[e] += dt * (v_uncond[e] + guidance * (v_cond[e] - v_uncond[e]))
+ * (src/levo-flow-renderer.cpp:105 with the CFG lambda :307); v_cond NULL:
+ * state += dt * v_uncond. Two roundings per product/sum, as the reference. */
+int levo_hip_flow_cfg_euler(float * state, const float * v_uncond, const float * v_cond,
+                            int64_t n, float guidance, float dt, levo_hip_stream_t stream);
+
+/* In-context prefix of one Euler step (src/levo-flow-renderer.cpp:94-101):
+ * state[e] = (1 - (1 - sigma_min) * time) * noise[e] + time * context[e]
+ * for e < n_prefix. */
+int levo_hip_flow_incontext(float * state, const float * noise, const float * context,
+                            int64_t n_prefix, float time, float sigma_min,
+                            levo_hip_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 / Q4_0 block quantization (ggml block layouts, little-endian)        */
+/*   block_q8_0 = { f16 d; int8 qs[32]; }  34 bytes                          */
+/*   block_q4_0 = { f16 d; uint8 qs[16]; } 18 bytes                          */
+/* ------------------------------------------------------------------------ */
+
+/* ggml_row_size(type, n_per_row) for the supported types; < 0 on error. */
+int64_t levo_hip_row_size(levo_hip_type type, int64_t n_per_row);
+
+/* Replaces ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row,
+ * imatrix) as called at tools/levo-quantize.cpp:386-388 (ggml's
+ * quantize_row_q8_0_ref / quantize_row_q4_0_ref). Returns the bytes written
+ * (nrows * row size) or a negative levo_hip_status. Q8_0 ignores imatrix as
+ * ggml does; Q4_0 requires imatrix == NULL. */
+int64_t levo_hip_quantize_chunk(levo_hip_type type, const float * src, void * dst,
+                                int64_t start, int64_t nrows, int64_t n_per_row,
+                                const float * imatrix, levo_hip_stream_t stream);
+
+/* write_tensor's chunk path fused into one pass (tools/levo-quantize.cpp:
+ * 355-388): rows of src_cols values (src_type F32 or F16, widened exactly),
+ * row stride src_row_stride elements, zero-padded to dst_cols (a multiple of
+ * 32, >= src_cols) and quantized. Returns bytes written or < 0. */
+int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, levo_hip_type src_type,
+                               int64_t src_cols, int64_t src_row_stride, void * dst,
+                               int64_t nrows, int64_t dst_cols, levo_hip_stream_t stream);
+
+/* dequantize_row_q8_0 / dequantize_row_q4_0 (ggml to_float): k values
+ * (multiple of 32) to dst_type F32, or F16 (exact products rounded RNE). */
+int levo_hip_dequantize(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type,
+                        int64_t k, levo_hip_stream_t stream);
+
+/* ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row (tools/levo-quantize.cpp:
+ * 358, 369): IEEE round-to-nearest-even narrowing, exact widening. */
+int levo_hip_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, levo_hip_stream_t stream);
+int levo_hip_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n, levo_hip_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEVO_HIP_H */

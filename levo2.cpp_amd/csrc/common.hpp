@@ -1,0 +1,90 @@
+// Shared helpers of the gfx950 kernels: status reporting, launch checks,
+// vector types, wave64 reductions and F16 bit conversions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "levo_hip.h"
+
+namespace levo_hip {
+
+// ---- status ---------------------------------------------------------------
+
+void set_error(const char * fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define LEVO_REQUIRE(cond, ...)                        \
+    do {                                               \
+        if (!(cond)) {                                 \
+            ::levo_hip::set_error(__VA_ARGS__);        \
+            return LEVO_HIP_ERR_INVALID;               \
+        }                                              \
+    } while (0)
+
+// Checks the launch that was just enqueued.
+int launch_status(const char * what);
+
+inline hipStream_t as_hip(levo_hip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- vector types (dwordx4 global accesses) --------------------------------
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+// ---- F16 bit conversions (IEEE round-to-nearest-even, exact widening) -----
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// ---- order-preserving float key (+0 and -0 map to the same key) -----------
+
+__device__ __forceinline__ uint32_t float_key(float v) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v + 0.0f);  // -0 -> +0 (RNE)
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ---- wave64 reductions ------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Bits of lanes below the calling lane in a 64-bit ballot mask.
+__device__ __forceinline__ int rank_in_mask(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+}  // namespace levo_hip

@@ -1,0 +1,174 @@
+// Flow matching Euler step with classifier-free guidance, elementwise CFG
+// combine, and the F16 <-> F32 row converters. All streaming kernels with
+// dwordx4 accesses and the reference's two-rounding arithmetic (the library
+// is compiled with -ffp-contract=off, so a*b+c is never fused here).
+//
+//   cfg_euler:  state += dt * (u + g * (c - u))   src/levo-flow-renderer.cpp:105, :307
+//   incontext:  state  = ns * noise + t * context  src/levo-flow-renderer.cpp:94-101
+//   cfg_combine: out   = u + s * (c - u)          src/levo-sampling.cpp:22-28,
+//                                                 src/levo-renderer-pattern.cpp:123-135
+#include "common.hpp"
+
+namespace levo_hip {
+namespace {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float cfg(float u, float c, float g) { return u + g * (c - u); }
+
+// One dwordx4 per thread; the scalar tail (n % 4) is handled by block 0.
+template <bool kCfg>
+__global__ __launch_bounds__(kThreads) void cfg_euler_kernel(float * state, const float * __restrict__ vu,
+                                                             const float * __restrict__ vc, int64_t n,
+                                                             float g, float dt) {
+    const int64_t n4 = n / 4;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n4) {
+        f32x4 s = reinterpret_cast<const f32x4 *>(state)[i];
+        const f32x4 u = reinterpret_cast<const f32x4 *>(vu)[i];
+        f32x4 v = u;
+        if (kCfg) {
+            const f32x4 c = reinterpret_cast<const f32x4 *>(vc)[i];
+            v.x = cfg(u.x, c.x, g);
+            v.y = cfg(u.y, c.y, g);
+            v.z = cfg(u.z, c.z, g);
+            v.w = cfg(u.w, c.w, g);
+        }
+        s.x += dt * v.x;
+        s.y += dt * v.y;
+        s.z += dt * v.z;
+        s.w += dt * v.w;
+        reinterpret_cast<f32x4 *>(state)[i] = s;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const int64_t e = n4 * 4 + threadIdx.x;
+        const float v = kCfg ? cfg(vu[e], vc[e], g) : vu[e];
+        state[e] += dt * v;
+    }
+}
+
+template <bool kCfg>
+__global__ __launch_bounds__(kThreads) void cfg_euler_scalar(float * state, const float * __restrict__ vu,
+                                                             const float * __restrict__ vc, int64_t n,
+                                                             float g, float dt) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e < n) {
+        const float v = kCfg ? cfg(vu[e], vc[e], g) : vu[e];
+        state[e] += dt * v;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void incontext_kernel(float * state, const float * __restrict__ noise,
+                                                             const float * __restrict__ context,
+                                                             int64_t n, float ns, float t) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e < n) state[e] = ns * noise[e] + t * context[e];
+}
+
+__global__ __launch_bounds__(kThreads) void cfg_combine_kernel(float * out, const float * __restrict__ u,
+                                                               const float * __restrict__ c, int64_t n,
+                                                               float s, bool vec) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (vec) {
+        const int64_t n4 = n / 4;
+        if (i < n4) {
+            const f32x4 a = reinterpret_cast<const f32x4 *>(u)[i];
+            const f32x4 b = reinterpret_cast<const f32x4 *>(c)[i];
+            f32x4 r;
+            r.x = cfg(a.x, b.x, s);
+            r.y = cfg(a.y, b.y, s);
+            r.z = cfg(a.z, b.z, s);
+            r.w = cfg(a.w, b.w, s);
+            reinterpret_cast<f32x4 *>(out)[i] = r;
+        }
+        if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+            const int64_t e = n4 * 4 + threadIdx.x;
+            out[e] = cfg(u[e], c[e], s);
+        }
+    } else if (i < n) {
+        out[i] = cfg(u[i], c[i], s);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void f32_to_f16_kernel(const float * __restrict__ x, uint16_t * y,
+                                                              int64_t n) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e < n) y[e] = f2h(x[e]);
+}
+
+__global__ __launch_bounds__(kThreads) void f16_to_f32_kernel(const uint16_t * __restrict__ x, float * y,
+                                                              int64_t n) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e < n) y[e] = h2f(x[e]);
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+using namespace levo_hip;
+
+extern "C" int levo_hip_flow_cfg_euler(float * state, const float * v_uncond, const float * v_cond,
+                                       int64_t n, float guidance, float dt, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n >= 0, "LeVo Flow renderer: Euler state size is negative");
+    if (n == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(state != nullptr && v_uncond != nullptr,
+                 "LeVo Flow renderer: Euler state or velocity is null");
+    const bool vec = aligned16(state) && aligned16(v_uncond) && (v_cond == nullptr || aligned16(v_cond));
+    if (vec) {
+        const int64_t grid = ceil_div(n / 4 > 0 ? n / 4 : 1, kThreads);
+        if (v_cond)
+            cfg_euler_kernel<true><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
+        else
+            cfg_euler_kernel<false><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
+    } else {
+        const int64_t grid = ceil_div(n, kThreads);
+        if (v_cond)
+            cfg_euler_scalar<true><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
+        else
+            cfg_euler_scalar<false><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
+    }
+    return launch_status("levo_hip_flow_cfg_euler");
+}
+
+extern "C" int levo_hip_flow_incontext(float * state, const float * noise, const float * context,
+                                       int64_t n_prefix, float time, float sigma_min,
+                                       levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n_prefix >= 0, "LeVo Flow renderer: in-context length is negative");
+    if (n_prefix == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(state != nullptr && noise != nullptr && context != nullptr,
+                 "LeVo Flow renderer: Euler state, noise or context is null");
+    // Host-side scalar exactly as src/levo-flow-renderer.cpp:94 (two roundings).
+    const float noise_scale = 1.0f - (1.0f - sigma_min) * time;
+    incontext_kernel<<<ceil_div(n_prefix, kThreads), kThreads, 0, as_hip(stream)>>>(
+        state, noise, context, n_prefix, noise_scale, time);
+    return launch_status("levo_hip_flow_incontext");
+}
+
+extern "C" int levo_hip_cfg_combine(float * out, const float * uncond, const float * cond, int64_t n,
+                                    float scale, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n >= 0, "CFG logits have different sizes");
+    if (n == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(out != nullptr && uncond != nullptr && cond != nullptr, "CFG: null pointer");
+    const bool vec = aligned16(out) && aligned16(uncond) && aligned16(cond);
+    const int64_t grid = vec ? ceil_div(n / 4 > 0 ? n / 4 : 1, kThreads) : ceil_div(n, kThreads);
+    cfg_combine_kernel<<<grid, kThreads, 0, as_hip(stream)>>>(out, uncond, cond, n, scale, vec);
+    return launch_status("levo_hip_cfg_combine");
+}
+
+extern "C" int levo_hip_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n,
+                                         levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n >= 0, "fp32_to_fp16_row: negative length");
+    if (n == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(x != nullptr && y != nullptr, "fp32_to_fp16_row: null pointer");
+    f32_to_f16_kernel<<<ceil_div(n, kThreads), kThreads, 0, as_hip(stream)>>>(x, y, n);
+    return launch_status("levo_hip_fp32_to_fp16_row");
+}
+
+extern "C" int levo_hip_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n,
+                                         levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n >= 0, "fp16_to_fp32_row: negative length");
+    if (n == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(x != nullptr && y != nullptr, "fp16_to_fp32_row: null pointer");
+    f16_to_f32_kernel<<<ceil_div(n, kThreads), kThreads, 0, as_hip(stream)>>>(x, y, n);
+    return launch_status("levo_hip_fp16_to_fp32_row");
+}

@@ -1,0 +1,220 @@
+// SnakeBeta activation, one HBM pass: y = x + sin^2(x * alpha_c) / beta_c.
+//
+// Replaces the five-node ggml chain of levo::detail::snake_beta
+// (src/levo-audio-ops.cpp:146-151: mul -> sin -> sqr -> div -> add, plus the
+// per-channel exp / scale_bias of the log-domain parameters) with one kernel
+// that reads x once and writes y once (8 B/element instead of ~44).
+//
+// Layout: x is [channels][time] (ggml ne0 = time contiguous). The grid walks
+// the flattened [channels x time] space in tiles of 256 * VPT dwordx4 vectors;
+// a tile's channel span is resolved once and alpha_c, beta_c and 1/beta_c are
+// computed into LDS by the tile's threads, so each element does one LDS read
+// instead of two exp evaluations.
+#include "common.hpp"
+
+namespace levo_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxTileItems = kThreads * 4;        // vectors (or scalars) per tile at VPT=4
+constexpr int kMaxTileChannels = kMaxTileItems + 1; // channels one tile can touch
+
+// Exact n / d for n < 2^31 (Granlund-Montgomery with N = 31):
+// m = ceil(2^(31+l) / d), l = ceil(log2 d), q = (n * m) >> (31 + l).
+struct fast_div {
+    uint32_t d;
+    uint32_t m;
+    uint32_t s;
+};
+
+fast_div make_fast_div(uint32_t d) {
+    uint32_t l = 0;
+    while ((uint64_t{1} << l) < d) ++l;
+    const uint64_t p = uint64_t{1} << (31 + l);
+    fast_div f;
+    f.d = d;
+    f.m = static_cast<uint32_t>((p + d - 1) / d);
+    f.s = 31 + l;
+    return f;
+}
+
+__device__ __forceinline__ uint32_t div_of(uint32_t n, fast_div f) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(n) * f.m) >> f.s);
+}
+
+template <typename P>
+__device__ __forceinline__ float param_f32(const P * p, uint32_t i);
+template <>
+__device__ __forceinline__ float param_f32<float>(const float * p, uint32_t i) {
+    return p[i];
+}
+template <>
+__device__ __forceinline__ float param_f32<uint16_t>(const uint16_t * p, uint32_t i) {
+    return h2f(p[i]);
+}
+
+struct snake_param {
+    float alpha;  // exp(alpha_log)
+    float beta;   // exp(beta_log) * 1 + 1e-9
+    float rbeta;  // RN(1 / beta)
+};
+
+// Quotient p / beta from the correctly rounded reciprocal plus one FMA
+// residual correction (Markstein): q0 = p*r, e = p - q0*beta (exact in an FMA),
+// q = q0 + e*r.
+__device__ __forceinline__ float div_by(float p, float beta, float rbeta) {
+    const float q0 = p * rbeta;
+    const float e = __builtin_fmaf(-q0, beta, p);
+    return __builtin_fmaf(e, rbeta, q0);
+}
+
+__device__ __forceinline__ float snake(float x, const snake_param & q) {
+    const float m = x * q.alpha;    // ggml_mul(input, alpha)
+    const float s = sinf(m);        // ggml_sin
+    const float p = s * s;          // ggml_sqr
+    const float d = div_by(p, q.beta, q.rbeta);  // ggml_div(periodic, beta)
+    return x + d;                   // ggml_add(input, .)
+}
+
+template <typename P>
+__device__ __forceinline__ void load_tile_params(snake_param * lds, const P * alpha_log,
+                                                 const P * beta_log, uint32_t c0, uint32_t n) {
+    for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+        snake_param q;
+        q.alpha = expf(param_f32(alpha_log, c0 + i));
+        const float e = expf(param_f32(beta_log, c0 + i));
+        q.beta = e * 1.0f + 1.0e-9f;  // ggml_scale_bias(exp(beta_log), 1, 1e-9)
+        q.rbeta = 1.0f / q.beta;
+        lds[i] = q;
+    }
+}
+
+// Vector path: time, both strides multiple of 4, pointers 16-byte aligned.
+template <typename P, int VPT>
+__global__ __launch_bounds__(kThreads) void snake_beta_vec(
+        const float * __restrict__ x, int64_t x_stride, const P * __restrict__ alpha_log,
+        const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total4,
+        fast_div div_t4) {
+    __shared__ snake_param params[kMaxTileChannels];
+    constexpr uint32_t tile = kThreads * VPT;
+    const uint32_t first = blockIdx.x * tile;
+    const uint32_t last = min(first + tile, total4) - 1;
+    const uint32_t c0 = div_of(first, div_t4);
+    const uint32_t c1 = div_of(last, div_t4);
+    load_tile_params(params, alpha_log, beta_log, c0, c1 - c0 + 1);
+
+    f32x4 v[VPT];
+    uint32_t ch[VPT];
+    uint32_t t4[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const uint32_t f = first + threadIdx.x + j * kThreads;
+        ch[j] = div_of(f, div_t4);
+        t4[j] = f - ch[j] * div_t4.d;
+        if (f < total4) {
+            v[j] = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4 *>(x + static_cast<int64_t>(ch[j]) * x_stride) + t4[j]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const uint32_t f = first + threadIdx.x + j * kThreads;
+        if (f < total4) {
+            const snake_param q = params[ch[j] - c0];
+            f32x4 r;
+            r.x = snake(v[j].x, q);
+            r.y = snake(v[j].y, q);
+            r.z = snake(v[j].z, q);
+            r.w = snake(v[j].w, q);
+            __builtin_nontemporal_store(
+                r, reinterpret_cast<f32x4 *>(y + static_cast<int64_t>(ch[j]) * y_stride) + t4[j]);
+        }
+    }
+}
+
+// Scalar path for any time / stride / alignment.
+template <typename P>
+__global__ __launch_bounds__(kThreads) void snake_beta_scalar(
+        const float * __restrict__ x, int64_t x_stride, const P * __restrict__ alpha_log,
+        const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total,
+        fast_div div_t) {
+    __shared__ snake_param params[kMaxTileChannels];
+    constexpr uint32_t tile = kThreads * 4;
+    const uint32_t first = blockIdx.x * tile;
+    const uint32_t last = min(first + tile, total) - 1;
+    const uint32_t c0 = div_of(first, div_t);
+    const uint32_t c1 = div_of(last, div_t);
+    load_tile_params(params, alpha_log, beta_log, c0, c1 - c0 + 1);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t f = first + threadIdx.x + j * kThreads;
+        if (f < total) {
+            const uint32_t c = div_of(f, div_t);
+            const uint32_t t = f - c * div_t.d;
+            const float xv = x[static_cast<int64_t>(c) * x_stride + t];
+            y[static_cast<int64_t>(c) * y_stride + t] = snake(xv, params[c - c0]);
+        }
+    }
+}
+
+template <typename P>
+int launch_snake(const float * x, int64_t x_stride, const P * a, const P * b, float * y,
+                 int64_t y_stride, int64_t channels, int64_t time, hipStream_t stream) {
+    const int64_t total = channels * time;
+    const bool vec = (time % 4 == 0) && (x_stride % 4 == 0) && (y_stride % 4 == 0) &&
+                     aligned16(x) && aligned16(y);
+    if (vec) {
+        const uint32_t total4 = static_cast<uint32_t>(total / 4);
+        const fast_div d = make_fast_div(static_cast<uint32_t>(time / 4));
+        // Fill the chip: keep >= ~4096 workgroups before widening the tile.
+        if (total4 >= 4096u * kThreads * 4u) {
+            const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads * 4));
+            snake_beta_vec<P, 4><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride, total4, d);
+        } else if (total4 >= 4096u * kThreads * 2u) {
+            const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads * 2));
+            snake_beta_vec<P, 2><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride, total4, d);
+        } else {
+            const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads));
+            snake_beta_vec<P, 1><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride, total4, d);
+        }
+    } else {
+        const fast_div d = make_fast_div(static_cast<uint32_t>(time));
+        const uint32_t grid = static_cast<uint32_t>(ceil_div(total, kThreads * 4));
+        snake_beta_scalar<P><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride,
+                                                           static_cast<uint32_t>(total), d);
+    }
+    return launch_status("levo_hip_snake_beta");
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+extern "C" int levo_hip_snake_beta(const float * x, int64_t x_stride, const void * alpha_log,
+                                   const void * beta_log, levo_hip_type param_type, float * y,
+                                   int64_t y_stride, int64_t channels, int64_t time,
+                                   levo_hip_stream_t stream) {
+    using namespace levo_hip;
+    LEVO_REQUIRE(channels >= 0 && time >= 0, "LeVo audio graph: SnakeBeta shape must be non-negative");
+    if (channels == 0 || time == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(x != nullptr, "LeVo audio graph: SnakeBeta input is null");
+    LEVO_REQUIRE(y != nullptr, "LeVo audio graph: SnakeBeta output is null");
+    LEVO_REQUIRE(alpha_log != nullptr, "LeVo audio graph: SnakeBeta alpha_log is null");
+    LEVO_REQUIRE(beta_log != nullptr, "LeVo audio graph: SnakeBeta beta_log is null");
+    LEVO_REQUIRE(param_type == LEVO_HIP_TYPE_F32 || param_type == LEVO_HIP_TYPE_F16,
+                 "LeVo audio graph: SnakeBeta alpha_log must be F32 or F16");
+    LEVO_REQUIRE(x_stride >= time && y_stride >= time,
+                 "LeVo audio graph: SnakeBeta row stride is smaller than the time length");
+    LEVO_REQUIRE(x != y || x_stride == y_stride,
+                 "LeVo audio graph: in-place SnakeBeta needs equal input and output strides");
+    LEVO_REQUIRE(channels * time < (int64_t{1} << 31) && channels < (int64_t{1} << 30),
+                 "LeVo audio graph: SnakeBeta tensor exceeds 2^31 elements");
+    if (param_type == LEVO_HIP_TYPE_F32)
+        return launch_snake(x, x_stride, static_cast<const float *>(alpha_log),
+                            static_cast<const float *>(beta_log), y, y_stride, channels, time,
+                            as_hip(stream));
+    return launch_snake(x, x_stride, static_cast<const uint16_t *>(alpha_log),
+                        static_cast<const uint16_t *>(beta_log), y, y_stride, channels, time,
+                        as_hip(stream));
+}

@@ -1,0 +1,173 @@
+"""ctypes binding of levo2.cpp_amd/liblevo_hip.so (the C ABI in include/levo_hip.h).
+
+Plumbing for tests and bench.py: arguments are torch device tensors (or raw
+device addresses) and a HIP stream; every call goes straight to the gfx950
+kernels. There is no CPU fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+KERNEL_LIB = os.path.join(PKG, "liblevo_hip.so")
+HOST_LIB = os.path.join(PKG, "liblevo_hip_host.so")
+HEADER = os.path.join(ROOT, "include", "levo_hip.h")
+
+F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
+MAX_STREAMS = 8
+BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_F = ctypes.c_float
+
+
+class LevoHipError(RuntimeError):
+    pass
+
+
+class SampleArgs(ctypes.Structure):
+    """levo_hip_sample_args (include/levo_hip.h)."""
+
+    _fields_ = [
+        ("cond", _P), ("uncond", _P), ("rows", _I64), ("vocab", _I64), ("row_pitch", _I64),
+        ("cfg_scale", _F), ("temperature", _F), ("n_streams", _I32), ("top_k", _I32 * MAX_STREAMS),
+        ("recent", _P), ("n_recent", _I32), ("repetition_penalty", _F), ("penalty_limit", _I64),
+        ("ignore", _P), ("n_ignore", _I32),
+        ("best", _P), ("count", _P), ("cand_ids", _P), ("cand_logits", _P), ("cand_probs", _P),
+        ("row_max", _P), ("row_lse", _P), ("capacity", _I32),
+    ]
+
+
+def declared_symbols(header: str = HEADER) -> list[str]:
+    """Every function name declared in include/levo_hip.h."""
+    text = open(header).read()
+    return sorted(set(re.findall(r"\b(levo_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+def _addr(t) -> int | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+class LevoHip:
+    """The C ABI with status checking."""
+
+    def __init__(self, path: str = KERNEL_LIB):
+        if not os.path.exists(path):
+            raise LevoHipError(f"{path} is not built; run __graft_entry__.build()")
+        lib = ctypes.CDLL(path)
+        self.lib = lib
+        sig = {
+            "levo_hip_last_error": (ctypes.c_char_p, []),
+            "levo_hip_abi_version": (ctypes.c_int, []),
+            "levo_hip_snake_beta": (ctypes.c_int, [_P, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _I64, _P]),
+            "levo_hip_residual_rms_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P,
+                                                          _I64, _I64, _F, _P]),
+            "levo_hip_residual_layer_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P,
+                                                            _I64, _I64, _F, _P]),
+            "levo_hip_cfg_combine": (ctypes.c_int, [_P, _P, _P, _I64, _F, _P]),
+            "levo_hip_cfg_sample": (ctypes.c_int, [ctypes.POINTER(SampleArgs), _P]),
+            "levo_hip_flow_cfg_euler": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
+            "levo_hip_flow_incontext": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
+            "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
+            "levo_hip_quantize_chunk": (_I64, [ctypes.c_int, _P, _P, _I64, _I64, _I64, _P, _P]),
+            "levo_hip_quantize_rows": (_I64, [ctypes.c_int, _P, ctypes.c_int, _I64, _I64, _P, _I64, _I64, _P]),
+            "levo_hip_dequantize": (ctypes.c_int, [ctypes.c_int, _P, _P, ctypes.c_int, _I64, _P]),
+            "levo_hip_fp32_to_fp16_row": (ctypes.c_int, [_P, _P, _I64, _P]),
+            "levo_hip_fp16_to_fp32_row": (ctypes.c_int, [_P, _P, _I64, _P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    def last_error(self) -> str:
+        return self.lib.levo_hip_last_error().decode()
+
+    def _check(self, status: int) -> int:
+        if status < 0:
+            raise LevoHipError(f"status {status}: {self.last_error()}")
+        return status
+
+    # ---- ops ---------------------------------------------------------------------
+    def snake_beta(self, x, alpha_log, beta_log, y, *, param_type=F32, channels=None, time=None,
+                   x_stride=None, y_stride=None, stream=None):
+        C = channels if channels is not None else x.shape[0]
+        T = time if time is not None else x.shape[1]
+        xs = x_stride if x_stride is not None else (x.stride(0) if hasattr(x, "stride") else T)
+        ys = y_stride if y_stride is not None else (y.stride(0) if hasattr(y, "stride") else T)
+        return self._check(self.lib.levo_hip_snake_beta(_addr(x), xs, _addr(alpha_log), _addr(beta_log), param_type,
+                                                        _addr(y), ys, C, T, _stream(stream)))
+
+    def rms_norm(self, act_type, x, delta, weight, weight_type, h_out, y, rows, dim, eps, stream=None):
+        return self._check(self.lib.levo_hip_residual_rms_norm(act_type, _addr(x), _addr(delta), _addr(weight),
+                                                               weight_type, _addr(h_out), _addr(y), rows, dim,
+                                                               eps, _stream(stream)))
+
+    def layer_norm(self, act_type, x, delta, gamma, beta, param_type, h_out, y, rows, dim, eps, stream=None):
+        return self._check(self.lib.levo_hip_residual_layer_norm(act_type, _addr(x), _addr(delta), _addr(gamma),
+                                                                 _addr(beta), param_type, _addr(h_out), _addr(y),
+                                                                 rows, dim, eps, _stream(stream)))
+
+    def cfg_combine(self, out, uncond, cond, n, scale, stream=None):
+        return self._check(self.lib.levo_hip_cfg_combine(_addr(out), _addr(uncond), _addr(cond), n, scale,
+                                                         _stream(stream)))
+
+    def cfg_sample(self, args: SampleArgs, stream=None):
+        return self._check(self.lib.levo_hip_cfg_sample(ctypes.byref(args), _stream(stream)))
+
+    def flow_cfg_euler(self, state, v_uncond, v_cond, n, guidance, dt, stream=None):
+        return self._check(self.lib.levo_hip_flow_cfg_euler(_addr(state), _addr(v_uncond), _addr(v_cond), n,
+                                                            guidance, dt, _stream(stream)))
+
+    def flow_incontext(self, state, noise, context, n_prefix, time, sigma_min, stream=None):
+        return self._check(self.lib.levo_hip_flow_incontext(_addr(state), _addr(noise), _addr(context), n_prefix,
+                                                            time, sigma_min, _stream(stream)))
+
+    def row_size(self, qtype, n):
+        return self._check(self.lib.levo_hip_row_size(qtype, n))
+
+    def quantize_chunk(self, qtype, src, dst, start, nrows, n_per_row, imatrix=None, stream=None):
+        return self._check(self.lib.levo_hip_quantize_chunk(qtype, _addr(src), _addr(dst), start, nrows, n_per_row,
+                                                            _addr(imatrix), _stream(stream)))
+
+    def quantize_rows(self, qtype, src, src_type, src_cols, src_stride, dst, nrows, dst_cols, stream=None):
+        return self._check(self.lib.levo_hip_quantize_rows(qtype, _addr(src), src_type, src_cols, src_stride,
+                                                           _addr(dst), nrows, dst_cols, _stream(stream)))
+
+    def dequantize(self, qtype, src, dst, dst_type, k, stream=None):
+        return self._check(self.lib.levo_hip_dequantize(qtype, _addr(src), _addr(dst), dst_type, k,
+                                                        _stream(stream)))
+
+    def fp32_to_fp16_row(self, x, y, n, stream=None):
+        return self._check(self.lib.levo_hip_fp32_to_fp16_row(_addr(x), _addr(y), n, _stream(stream)))
+
+    def fp16_to_fp32_row(self, x, y, n, stream=None):
+        return self._check(self.lib.levo_hip_fp16_to_fp32_row(_addr(x), _addr(y), n, _stream(stream)))
+
+
+_LIB: LevoHip | None = None
+
+
+def lib() -> LevoHip:
+    global _LIB
+    if _LIB is None:
+        _LIB = LevoHip()
+    return _LIB

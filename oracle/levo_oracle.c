@@ -1,0 +1,702 @@
+/*
+ * levo_oracle.c — CPU restatement of the reference's hot-path arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker). Built by oracle/Makefile with
+ * -std=c11 -ffp-contract=off so that every a*b+c below rounds twice, exactly
+ * like the reference's ISO C++17 build for baseline x86-64
+ * (CMakeLists.txt:8-10) and ggml's ISO C11 CPU backend.
+ */
+#define _GNU_SOURCE
+#include "levo_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------- */
+/* F16 <-> F32                                                                */
+/* ------------------------------------------------------------------------- */
+
+/* IEEE binary32 -> binary16, round to nearest, ties to even (what
+ * ggml_fp32_to_fp16_row produces with F16C or with its software fallback). */
+uint16_t lo_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t mant = x & 0x7fffffu;
+    if (exp == 0xffu) {
+        if (mant != 0) return (uint16_t)(sign | 0x7e00u | (mant >> 13));
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    if (exp >= 143u) return (uint16_t)(sign | 0x7c00u); /* >= 2^16: overflow */
+    if (exp >= 113u) {                                    /* normal half */
+        uint32_t h = ((exp - 112u) << 10) | (mant >> 13);
+        const uint32_t rem = mant & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u; /* may carry to inf */
+        return (uint16_t)(sign | h);
+    }
+    if (exp < 102u) return (uint16_t)sign; /* < 2^-25 rounds to zero */
+    /* subnormal half: value = M * 2^(exp-150), unit 2^-24 */
+    mant |= 0x800000u;
+    const uint32_t shift = 126u - exp; /* 14 .. 24 */
+    uint32_t h = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+float lo_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu;
+    const uint32_t mant = h & 0x3ffu;
+    uint32_t x;
+    if (exp == 0) {
+        const float v = ldexpf((float)mant, -24); /* exact */
+        memcpy(&x, &v, sizeof x);
+        x |= sign;
+    } else if (exp == 0x1fu) {
+        x = sign | 0x7f800000u | (mant << 13);
+    } else {
+        x = sign | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &x, sizeof f);
+    return f;
+}
+
+void lo_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lo_fp32_to_fp16(x[i]);
+}
+
+void lo_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lo_fp16_to_fp32(x[i]);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Row-partitioned worker threads (ggml-cpu hands row i to thread i % nth).   */
+/* ------------------------------------------------------------------------- */
+
+typedef void (*lo_row_fn)(void * ctx, int ith, int nth, pthread_barrier_t * barrier);
+
+typedef struct {
+    lo_row_fn fn;
+    void * ctx;
+    int ith, nth;
+    pthread_barrier_t * barrier;
+} lo_thread_arg;
+
+static void * lo_thread_main(void * p) {
+    lo_thread_arg * a = (lo_thread_arg *)p;
+    a->fn(a->ctx, a->ith, a->nth, a->barrier);
+    return NULL;
+}
+
+static void lo_parallel(lo_row_fn fn, void * ctx, int n_threads) {
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads == 1) {
+        fn(ctx, 0, 1, NULL);
+        return;
+    }
+    pthread_barrier_t barrier;
+    pthread_barrier_init(&barrier, NULL, (unsigned)n_threads);
+    pthread_t * threads = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)n_threads);
+    lo_thread_arg * args = (lo_thread_arg *)malloc(sizeof(lo_thread_arg) * (size_t)n_threads);
+    for (int i = 0; i < n_threads; ++i) {
+        args[i].fn = fn;
+        args[i].ctx = ctx;
+        args[i].ith = i;
+        args[i].nth = n_threads;
+        args[i].barrier = &barrier;
+    }
+    for (int i = 1; i < n_threads; ++i) pthread_create(&threads[i], NULL, lo_thread_main, &args[i]);
+    lo_thread_main(&args[0]);
+    for (int i = 1; i < n_threads; ++i) pthread_join(threads[i], NULL);
+    pthread_barrier_destroy(&barrier);
+    free(threads);
+    free(args);
+}
+
+static void lo_sync(pthread_barrier_t * barrier) {
+    if (barrier) pthread_barrier_wait(barrier);
+}
+
+/* ------------------------------------------------------------------------- */
+/* SnakeBeta (src/levo-audio-ops.cpp:146-151)                                 */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    const float * x;
+    const float * alpha;
+    const float * beta;
+    float * work;
+    float * y;
+    int64_t channels, time;
+} lo_snake_ctx;
+
+/* Five unfused passes, one per ggml node, each over the thread's rows with a
+ * barrier in between (ggml computes one node at a time). The intermediate
+ * lives in one buffer updated in place, as ggml's graph allocator does for
+ * unary ops whose parent has no other consumer. */
+static void lo_snake_rows(void * p, int ith, int nth, pthread_barrier_t * barrier) {
+    const lo_snake_ctx * c = (const lo_snake_ctx *)p;
+    const int64_t T = c->time;
+    for (int64_t ch = ith; ch < c->channels; ch += nth) { /* ggml_mul(input, alpha) */
+        const float a = c->alpha[ch];
+        const float * x = c->x + ch * T;
+        float * w = c->work + ch * T;
+        for (int64_t t = 0; t < T; ++t) w[t] = x[t] * a;
+    }
+    lo_sync(barrier);
+    for (int64_t ch = ith; ch < c->channels; ch += nth) { /* ggml_sin */
+        float * w = c->work + ch * T;
+        for (int64_t t = 0; t < T; ++t) w[t] = sinf(w[t]);
+    }
+    lo_sync(barrier);
+    for (int64_t ch = ith; ch < c->channels; ch += nth) { /* ggml_sqr */
+        float * w = c->work + ch * T;
+        for (int64_t t = 0; t < T; ++t) w[t] = w[t] * w[t];
+    }
+    lo_sync(barrier);
+    for (int64_t ch = ith; ch < c->channels; ch += nth) { /* ggml_div(periodic, beta) */
+        const float b = c->beta[ch];
+        float * w = c->work + ch * T;
+        for (int64_t t = 0; t < T; ++t) w[t] = w[t] / b;
+    }
+    lo_sync(barrier);
+    for (int64_t ch = ith; ch < c->channels; ch += nth) { /* ggml_add(input, .) */
+        const float * x = c->x + ch * T;
+        const float * w = c->work + ch * T;
+        float * y = c->y + ch * T;
+        for (int64_t t = 0; t < T; ++t) y[t] = x[t] + w[t];
+    }
+}
+
+void lo_snake_beta_f32(const float * x, const float * alpha_log, const float * beta_log,
+                       float * y, int64_t channels, int64_t time, int n_threads) {
+    float * alpha = (float *)malloc(sizeof(float) * (size_t)channels);
+    float * beta = (float *)malloc(sizeof(float) * (size_t)channels);
+    float * work = (float *)malloc(sizeof(float) * (size_t)(channels * time));
+    for (int64_t c = 0; c < channels; ++c) {
+        alpha[c] = expf(alpha_log[c]);                /* ggml_exp(alpha_log) */
+        const float e = expf(beta_log[c]);            /* ggml_exp(beta_log) */
+        beta[c] = e * 1.0f + 1.0e-9f;                 /* ggml_scale_bias(., 1, 1e-9) */
+    }
+    lo_snake_ctx ctx = {x, alpha, beta, work, y, channels, time};
+    lo_parallel(lo_snake_rows, &ctx, n_threads);
+    free(work);
+    free(beta);
+    free(alpha);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Residual add + RMSNorm / LayerNorm                                         */
+/* ------------------------------------------------------------------------- */
+
+/* ggml-cpu rms_norm row (scalar algorithm): sum of x*x in ggml_float (double)
+ * in index order, mean = sum/n rounded to float, scale = 1/sqrtf(mean + eps). */
+static float lo_rms_scale(const float * h, int64_t n, float eps) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) sum += (double)(h[i] * h[i]);
+    const float mean = (float)(sum / (double)n);
+    return 1.0f / sqrtf(mean + eps);
+}
+
+/* ggml-cpu norm row: mean from a ggml_float sum, y = x - mean, variance from
+ * a ggml_float sum of y*y, scale = 1/sqrtf(variance + eps), y *= scale. */
+static void lo_norm_row(const float * h, float * y, int64_t n, float eps) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) sum += (double)h[i];
+    const float mean = (float)(sum / (double)n);
+    double sum2 = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = h[i] - mean;
+        y[i] = v;
+        sum2 += (double)(v * v);
+    }
+    const float variance = (float)(sum2 / (double)n);
+    const float scale = 1.0f / sqrtf(variance + eps);
+    for (int64_t i = 0; i < n; ++i) y[i] = y[i] * scale;
+}
+
+typedef struct {
+    const void * x;
+    const void * delta;
+    const void * w;
+    const void * b;
+    void * h_out;
+    void * y;
+    int64_t rows, dim;
+    float eps;
+} lo_norm_ctx;
+
+static void lo_rms_f16_rows(void * p, int ith, int nth, pthread_barrier_t * barrier) {
+    (void)barrier;
+    const lo_norm_ctx * c = (const lo_norm_ctx *)p;
+    const int64_t D = c->dim;
+    float * h = (float *)malloc(sizeof(float) * (size_t)D);
+    for (int64_t r = ith; r < c->rows; r += nth) {
+        const uint16_t * x = (const uint16_t *)c->x + r * D;
+        const uint16_t * d = c->delta ? (const uint16_t *)c->delta + r * D : NULL;
+        const uint16_t * w = (const uint16_t *)c->w;
+        uint16_t * ho = c->h_out ? (uint16_t *)c->h_out + r * D : NULL;
+        uint16_t * y = (uint16_t *)c->y + r * D;
+        for (int64_t i = 0; i < D; ++i) {
+            /* ggml_add on F16 tensors: F32 sum rounded to F16 (src/levo-kv.cpp:462,507) */
+            const uint16_t h16 = d ? lo_fp32_to_fp16(lo_fp16_to_fp32(x[i]) + lo_fp16_to_fp32(d[i])) : x[i];
+            if (ho) ho[i] = h16;
+            h[i] = lo_fp16_to_fp32(h16); /* cast_f32 (src/levo-kv.cpp:157) */
+        }
+        const float scale = lo_rms_scale(h, D, c->eps);
+        for (int64_t i = 0; i < D; ++i) {
+            const uint16_t n16 = lo_fp32_to_fp16(h[i] * scale); /* cast_f16 (:158) */
+            /* ggml_mul F16 x F16 weight -> F16 (:159) */
+            y[i] = lo_fp32_to_fp16(lo_fp16_to_fp32(n16) * lo_fp16_to_fp32(w[i]));
+        }
+    }
+    free(h);
+}
+
+static void lo_rms_f32_rows(void * p, int ith, int nth, pthread_barrier_t * barrier) {
+    (void)barrier;
+    const lo_norm_ctx * c = (const lo_norm_ctx *)p;
+    const int64_t D = c->dim;
+    float * h = (float *)malloc(sizeof(float) * (size_t)D);
+    for (int64_t r = ith; r < c->rows; r += nth) {
+        const float * x = (const float *)c->x + r * D;
+        const float * d = c->delta ? (const float *)c->delta + r * D : NULL;
+        const float * w = (const float *)c->w;
+        float * ho = c->h_out ? (float *)c->h_out + r * D : NULL;
+        float * y = (float *)c->y + r * D;
+        for (int64_t i = 0; i < D; ++i) {
+            h[i] = d ? x[i] + d[i] : x[i];
+            if (ho) ho[i] = h[i];
+        }
+        const float scale = lo_rms_scale(h, D, c->eps);
+        for (int64_t i = 0; i < D; ++i) y[i] = (h[i] * scale) * w[i];
+    }
+    free(h);
+}
+
+static void lo_ln_f32_rows(void * p, int ith, int nth, pthread_barrier_t * barrier) {
+    (void)barrier;
+    const lo_norm_ctx * c = (const lo_norm_ctx *)p;
+    const int64_t D = c->dim;
+    float * h = (float *)malloc(sizeof(float) * (size_t)D);
+    float * n = (float *)malloc(sizeof(float) * (size_t)D);
+    for (int64_t r = ith; r < c->rows; r += nth) {
+        const float * x = (const float *)c->x + r * D;
+        const float * d = c->delta ? (const float *)c->delta + r * D : NULL;
+        const float * g = (const float *)c->w;
+        const float * b = (const float *)c->b;
+        float * ho = c->h_out ? (float *)c->h_out + r * D : NULL;
+        float * y = (float *)c->y + r * D;
+        for (int64_t i = 0; i < D; ++i) {
+            h[i] = d ? x[i] + d[i] : x[i];
+            if (ho) ho[i] = h[i];
+        }
+        lo_norm_row(h, n, D, c->eps);                                    /* ggml_norm */
+        for (int64_t i = 0; i < D; ++i) y[i] = (n[i] * g[i]) + b[i];     /* ggml_mul, ggml_add */
+    }
+    free(n);
+    free(h);
+}
+
+static void lo_ln_f16_rows(void * p, int ith, int nth, pthread_barrier_t * barrier) {
+    (void)barrier;
+    const lo_norm_ctx * c = (const lo_norm_ctx *)p;
+    const int64_t D = c->dim;
+    float * h = (float *)malloc(sizeof(float) * (size_t)D);
+    float * n = (float *)malloc(sizeof(float) * (size_t)D);
+    for (int64_t r = ith; r < c->rows; r += nth) {
+        const uint16_t * x = (const uint16_t *)c->x + r * D;
+        const uint16_t * d = c->delta ? (const uint16_t *)c->delta + r * D : NULL;
+        const uint16_t * g = (const uint16_t *)c->w;
+        const uint16_t * b = (const uint16_t *)c->b;
+        uint16_t * ho = c->h_out ? (uint16_t *)c->h_out + r * D : NULL;
+        uint16_t * y = (uint16_t *)c->y + r * D;
+        for (int64_t i = 0; i < D; ++i) {
+            const uint16_t h16 = d ? lo_fp32_to_fp16(lo_fp16_to_fp32(x[i]) + lo_fp16_to_fp32(d[i])) : x[i];
+            if (ho) ho[i] = h16;
+            h[i] = lo_fp16_to_fp32(h16);
+        }
+        lo_norm_row(h, n, D, c->eps);
+        for (int64_t i = 0; i < D; ++i)
+            y[i] = lo_fp32_to_fp16((n[i] * lo_fp16_to_fp32(g[i])) + lo_fp16_to_fp32(b[i]));
+    }
+    free(n);
+    free(h);
+}
+
+void lo_residual_rms_norm_f16(const uint16_t * x, const uint16_t * delta, const uint16_t * weight,
+                              uint16_t * h_out, uint16_t * y, int64_t rows, int64_t dim,
+                              float eps, int n_threads) {
+    lo_norm_ctx ctx = {x, delta, weight, NULL, h_out, y, rows, dim, eps};
+    lo_parallel(lo_rms_f16_rows, &ctx, n_threads);
+}
+
+void lo_residual_rms_norm_f32(const float * x, const float * delta, const float * weight,
+                              float * h_out, float * y, int64_t rows, int64_t dim,
+                              float eps, int n_threads) {
+    lo_norm_ctx ctx = {x, delta, weight, NULL, h_out, y, rows, dim, eps};
+    lo_parallel(lo_rms_f32_rows, &ctx, n_threads);
+}
+
+void lo_residual_layer_norm_f32(const float * x, const float * delta, const float * gamma,
+                                const float * beta, float * h_out, float * y, int64_t rows,
+                                int64_t dim, float eps, int n_threads) {
+    lo_norm_ctx ctx = {x, delta, gamma, beta, h_out, y, rows, dim, eps};
+    lo_parallel(lo_ln_f32_rows, &ctx, n_threads);
+}
+
+void lo_residual_layer_norm_f16(const uint16_t * x, const uint16_t * delta, const uint16_t * gamma,
+                                const uint16_t * beta, uint16_t * h_out, uint16_t * y,
+                                int64_t rows, int64_t dim, float eps, int n_threads) {
+    lo_norm_ctx ctx = {x, delta, gamma, beta, h_out, y, rows, dim, eps};
+    lo_parallel(lo_ln_f16_rows, &ctx, n_threads);
+}
+
+/* ------------------------------------------------------------------------- */
+/* CFG                                                                        */
+/* ------------------------------------------------------------------------- */
+
+void lo_apply_cfg(const float * cond, const float * uncond, float * out, int64_t n, float scale) {
+    for (int64_t i = 0; i < n; ++i) out[i] = uncond[i] + scale * (cond[i] - uncond[i]);
+}
+
+/* ------------------------------------------------------------------------- */
+/* mt19937_64 and the sampler                                                 */
+/* ------------------------------------------------------------------------- */
+
+#define LO_MT_N 312
+#define LO_MT_M 156
+
+void lo_mt_seed(lo_mt19937_64 * rng, uint64_t seed) {
+    rng->state[0] = seed;
+    for (int i = 1; i < LO_MT_N; ++i) {
+        const uint64_t prev = rng->state[i - 1];
+        rng->state[i] = 6364136223846793005ULL * (prev ^ (prev >> 62)) + (uint64_t)i;
+    }
+    rng->index = LO_MT_N;
+}
+
+uint64_t lo_mt_next(lo_mt19937_64 * rng) {
+    if (rng->index >= LO_MT_N) {
+        const uint64_t upper = 0xFFFFFFFF80000000ULL; /* w - r = 33 high bits */
+        const uint64_t lower = 0x000000007FFFFFFFULL; /* r = 31 low bits */
+        for (int i = 0; i < LO_MT_N; ++i) {
+            const uint64_t y = (rng->state[i] & upper) | (rng->state[(i + 1) % LO_MT_N] & lower);
+            uint64_t next = rng->state[(i + LO_MT_M) % LO_MT_N] ^ (y >> 1);
+            if (y & 1u) next ^= 0xB5026F5AA96619E9ULL;
+            rng->state[i] = next;
+        }
+        rng->index = 0;
+    }
+    uint64_t z = rng->state[rng->index++];
+    z ^= (z >> 29) & 0x5555555555555555ULL;
+    z ^= (z << 17) & 0x71D67FFFEDA60000ULL;
+    z ^= (z << 37) & 0xFFF7EEE000000000ULL;
+    z ^= z >> 43;
+    return z;
+}
+
+void lo_mt_discard(lo_mt19937_64 * rng, uint64_t count) {
+    for (uint64_t i = 0; i < count; ++i) (void)lo_mt_next(rng);
+}
+
+/* manual_uniform (src/levo-sampling.cpp:12-18): (53 random bits + 0.5) / 2^53. */
+double lo_manual_uniform(lo_mt19937_64 * rng, uint64_t * draws) {
+    const double denom = 9007199254740992.0;
+    if (draws) ++*draws;
+    return ((double)(lo_mt_next(rng) >> 11) + 0.5) / denom;
+}
+
+/* src/levo-sampling.cpp:39-47: each distinct id in [0, limit) is divided once. */
+int lo_repetition_penalty(float * logits, int64_t vocab, const int64_t * recent, int64_t n_recent,
+                          float penalty, int64_t vocabulary_limit) {
+    if (!(penalty > 0.0f) || !isfinite(penalty)) return LO_ERR_PENALTY;
+    const int64_t limit = vocabulary_limit == 0 ? vocab : (vocabulary_limit < vocab ? vocabulary_limit : vocab);
+    if (limit <= 0 || n_recent <= 0) return LO_OK;
+    unsigned char * seen = (unsigned char *)calloc((size_t)limit, 1);
+    for (int64_t i = 0; i < n_recent; ++i) {
+        const int64_t t = recent[i];
+        if (t >= 0 && t < limit && !seen[t]) {
+            seen[t] = 1;
+            logits[t] /= penalty;
+        }
+    }
+    free(seen);
+    return LO_OK;
+}
+
+static int lo_desc_float(const void * a, const void * b) {
+    const float x = *(const float *)a, y = *(const float *)b;
+    return (x < y) - (x > y);
+}
+
+/* Threshold of the stable descending sort (src/levo-sampling.cpp:85-89): the
+ * value at rank top_k-1, i.e. the top_k-th largest value with multiplicity. */
+static float lo_kth_largest(const float * v, int64_t n, int64_t k) {
+    float * copy = (float *)malloc(sizeof(float) * (size_t)n);
+    memcpy(copy, v, sizeof(float) * (size_t)n);
+    qsort(copy, (size_t)n, sizeof(float), lo_desc_float);
+    const float t = copy[k - 1];
+    free(copy);
+    return t;
+}
+
+int64_t lo_top_k_candidates(const float * logits, int64_t vocab, int64_t top_k,
+                            int64_t * best, int64_t * candidates, int64_t cap) {
+    if (vocab <= 0) return LO_ERR_EMPTY;
+    for (int64_t i = 0; i < vocab; ++i)
+        if (isnan(logits[i])) return LO_ERR_NAN;
+    const int filter = top_k > 0 && top_k < vocab;
+    const float threshold = filter ? lo_kth_largest(logits, vocab, top_k) : -INFINITY;
+    int64_t count = 0;
+    int64_t b = -1;
+    for (int64_t i = 0; i < vocab; ++i) {
+        if (filter && logits[i] < threshold) continue;
+        if (count < cap) candidates[count] = i;
+        ++count;
+        if (b < 0 || logits[b] < logits[i]) b = i; /* std::max_element keeps the first max */
+    }
+    *best = b;
+    return count;
+}
+
+int lo_sample_top_k(const float * input, int64_t vocab, int64_t top_k, float temperature,
+                    int use_sampling, lo_mt19937_64 * rng, uint64_t * draws, int64_t * token) {
+    if (vocab <= 0) return LO_ERR_EMPTY;
+    if (!isfinite(temperature) || temperature < 0.0f) return LO_ERR_TEMPERATURE;
+    int64_t * cand = (int64_t *)malloc(sizeof(int64_t) * (size_t)vocab);
+    int64_t best = 0;
+    const int64_t n = lo_top_k_candidates(input, vocab, top_k, &best, cand, vocab);
+    if (n < 0) {
+        free(cand);
+        return (int)n;
+    }
+    if (!use_sampling || temperature == 0.0f) {
+        *token = best;
+        free(cand);
+        return LO_OK;
+    }
+    float max_logit = -INFINITY;
+    for (int64_t i = 0; i < n; ++i)
+        if (max_logit < input[cand[i]]) max_logit = input[cand[i]]; /* std::max */
+    double * weights = (double *)malloc(sizeof(double) * (size_t)n);
+    double total = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        const float value = input[cand[i]];
+        if (isinf(value) && value < 0) weights[i] = 0.0;
+        else weights[i] = exp((double)((value - max_logit) / temperature));
+        total += weights[i];
+    }
+    if (!(total > 0.0) || !isfinite(total)) {
+        *token = best;
+    } else {
+        const double target = lo_manual_uniform(rng, draws) * total;
+        double cumulative = 0.0;
+        int64_t chosen = cand[n - 1];
+        for (int64_t i = 0; i < n; ++i) {
+            cumulative += weights[i];
+            if (target < cumulative) {
+                chosen = cand[i];
+                break;
+            }
+        }
+        *token = chosen;
+    }
+    free(weights);
+    free(cand);
+    return LO_OK;
+}
+
+int lo_sample_streams(const float * logits, int64_t n_streams, int64_t vocab,
+                      int use_sampling, float temperature, int64_t top_k_mixed,
+                      int64_t top_k_detail, float repetition_penalty,
+                      const int64_t * recent, int64_t n_recent,
+                      const int64_t * ignore_tokens, int64_t n_ignore,
+                      lo_mt19937_64 * rng, uint64_t * draws, int64_t * tokens) {
+    float * adjusted = (float *)malloc(sizeof(float) * (size_t)(vocab > 0 ? vocab : 1));
+    int status = LO_OK;
+    for (int64_t q = 0; q < n_streams && status == LO_OK; ++q) {
+        memcpy(adjusted, logits + q * vocab, sizeof(float) * (size_t)vocab);
+        if (recent) {
+            status = lo_repetition_penalty(adjusted, vocab, recent + q * n_recent, n_recent,
+                                           repetition_penalty, vocab == 0 ? 0 : vocab - 1);
+            if (status != LO_OK) break;
+        }
+        if (q == 0)
+            for (int64_t i = 0; i < n_ignore; ++i)
+                if (ignore_tokens[i] >= 0 && ignore_tokens[i] < vocab) adjusted[ignore_tokens[i]] = -INFINITY;
+        const int64_t k = q == 0 ? top_k_mixed : top_k_detail;
+        status = lo_sample_top_k(adjusted, vocab, k, temperature, use_sampling, rng, draws, &tokens[q]);
+    }
+    free(adjusted);
+    return status;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Flow Euler / CFG                                                           */
+/* ------------------------------------------------------------------------- */
+
+void lo_flow_incontext(float * state, const float * noise, const float * context,
+                       int64_t n_prefix, float time, float sigma_min) {
+    const float noise_scale = 1.0f - (1.0f - sigma_min) * time;
+    for (int64_t e = 0; e < n_prefix; ++e) state[e] = noise_scale * noise[e] + time * context[e];
+}
+
+void lo_flow_cfg_euler(float * state, const float * v_uncond, const float * v_cond, int64_t n,
+                       float guidance, float dt) {
+    for (int64_t e = 0; e < n; ++e) {
+        const float v = v_cond ? v_uncond[e] + guidance * (v_cond[e] - v_uncond[e]) : v_uncond[e];
+        state[e] += dt * v;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Q8_0 / Q4_0 block formats (ggml public layout): {f16 d; int8 qs[32]} = 34 B */
+/* and {f16 d; u8 qs[16]} = 18 B, little-endian.                              */
+/* ------------------------------------------------------------------------- */
+
+/* float -> int8 as x86-64 does it for (int8_t)f: cvttss2si (int32, invalid ->
+ * 0x80000000) then the low byte. Only non-finite products reach the invalid
+ * case (a block whose |max| is so small that 1/d overflows). */
+static int8_t lo_trunc_i8(float f) {
+    if (!(fabsf(f) < 2147483648.0f)) return 0;
+    return (int8_t)(int32_t)f;
+}
+
+void lo_quantize_row_q8_0(const float * x, void * out, int64_t k) {
+    unsigned char * y = (unsigned char *)out;
+    const int64_t nb = k / 32;
+    for (int64_t i = 0; i < nb; ++i) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = fabsf(x[i * 32 + j]);
+            amax = amax > v ? amax : v; /* MAX(amax, fabsf(v)) */
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = lo_fp32_to_fp16(d);
+        unsigned char * blk = y + i * 34;
+        blk[0] = (unsigned char)(dh & 0xffu);
+        blk[1] = (unsigned char)(dh >> 8);
+        for (int j = 0; j < 32; ++j) {
+            const float x0 = x[i * 32 + j] * id;
+            blk[2 + j] = (unsigned char)lo_trunc_i8(roundf(x0));
+        }
+    }
+}
+
+void lo_quantize_row_q4_0(const float * x, void * out, int64_t k) {
+    unsigned char * y = (unsigned char *)out;
+    const int64_t nb = k / 32;
+    for (int64_t i = 0; i < nb; ++i) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = x[i * 32 + j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint16_t dh = lo_fp32_to_fp16(d);
+        unsigned char * blk = y + i * 18;
+        blk[0] = (unsigned char)(dh & 0xffu);
+        blk[1] = (unsigned char)(dh >> 8);
+        for (int j = 0; j < 16; ++j) {
+            const float x0 = x[i * 32 + j] * id;
+            const float x1 = x[i * 32 + 16 + j] * id;
+            int q0 = lo_trunc_i8(x0 + 8.5f);
+            int q1 = lo_trunc_i8(x1 + 8.5f);
+            q0 = q0 < 15 ? q0 : 15;
+            q1 = q1 < 15 ? q1 : 15;
+            blk[2 + j] = (unsigned char)((uint8_t)q0 | (uint8_t)((uint8_t)q1 << 4));
+        }
+    }
+}
+
+void lo_dequantize_row_q8_0(const void * in, float * y, int64_t k) {
+    const unsigned char * x = (const unsigned char *)in;
+    const int64_t nb = k / 32;
+    for (int64_t i = 0; i < nb; ++i) {
+        const unsigned char * blk = x + i * 34;
+        const float d = lo_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < 32; ++j) y[i * 32 + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+void lo_dequantize_row_q4_0(const void * in, float * y, int64_t k) {
+    const unsigned char * x = (const unsigned char *)in;
+    const int64_t nb = k / 32;
+    for (int64_t i = 0; i < nb; ++i) {
+        const unsigned char * blk = x + i * 18;
+        const float d = lo_fp16_to_fp32((uint16_t)(blk[0] | (blk[1] << 8)));
+        for (int j = 0; j < 16; ++j) {
+            const int x0 = (blk[2 + j] & 0x0f) - 8;
+            const int x1 = (blk[2 + j] >> 4) - 8;
+            y[i * 32 + j] = (float)x0 * d;
+            y[i * 32 + 16 + j] = (float)x1 * d;
+        }
+    }
+}
+
+static size_t lo_row_size(int type, int64_t n) {
+    if (type == LO_TYPE_Q8_0) return (size_t)(n / 32) * 34u;
+    if (type == LO_TYPE_Q4_0) return (size_t)(n / 32) * 18u;
+    return 0;
+}
+
+size_t lo_quantize_chunk(int type, const float * src, void * dst, int64_t start, int64_t nrows,
+                         int64_t n_per_row) {
+    const size_t row_size = lo_row_size(type, n_per_row);
+    if (row_size == 0 || n_per_row % 32 != 0 || start % n_per_row != 0) return 0;
+    const int64_t start_row = start / n_per_row;
+    unsigned char * out = (unsigned char *)dst + (size_t)start_row * row_size;
+    if (type == LO_TYPE_Q8_0) lo_quantize_row_q8_0(src + start, out, nrows * n_per_row);
+    else lo_quantize_row_q4_0(src + start, out, nrows * n_per_row);
+    return (size_t)nrows * row_size;
+}
+
+size_t lo_quantize_f16_rows_padded(int type, const uint16_t * src, int64_t nrows, int64_t src_cols,
+                                   int64_t dst_cols, void * dst) {
+    if (dst_cols < src_cols) return 0;
+    float * values = (float *)calloc((size_t)(nrows * dst_cols), sizeof(float));
+    for (int64_t r = 0; r < nrows; ++r)
+        lo_fp16_to_fp32_row(src + r * src_cols, values + r * dst_cols, src_cols);
+    const size_t n = lo_quantize_chunk(type, values, dst, 0, nrows, dst_cols);
+    free(values);
+    return n;
+}
+
+/* ------------------------------------------------------------------------- */
+/* Seeded synthetic inputs (src/levo-render.cpp:87-112)                       */
+/* ------------------------------------------------------------------------- */
+
+static uint64_t lo_splitmix64(uint64_t * state) {
+    *state += 0x9e3779b97f4a7c15ULL;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+static double lo_uniform_open(uint64_t * state) {
+    return ((double)(lo_splitmix64(state) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+void lo_gaussian_noise(float * out, int64_t count, uint64_t seed) {
+    uint64_t state = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < count; i += 2) {
+        const double radius = sqrt(-2.0 * log(lo_uniform_open(&state)));
+        const double angle = two_pi * lo_uniform_open(&state);
+        out[i] = (float)(radius * cos(angle));
+        if (i + 1 < count) out[i + 1] = (float)(radius * sin(angle));
+    }
+}

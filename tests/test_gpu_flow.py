@@ -1,0 +1,127 @@
+"""Flow Euler/CFG update and the CFG combine on the GPU.
+
+The reference computes every product and sum here with two F32 roundings
+(src/levo-flow-renderer.cpp:94-105, :307; src/levo-sampling.cpp:22-28), which
+the kernels reproduce, so the bar is bit-exact.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _eq(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def test_flow_euler_reference_kat(hip, dev):
+    """tests/test-flow-renderer.cpp:33-65 driven through the device entry points."""
+    import torch
+    noise = to_dev(np.array([1, 2, 10, 20, 30, 40], np.float32), dev)
+    ctx = to_dev(np.array([4, 8, 0, 0, 0, 0], np.float32), dev)
+    ones = torch.ones(6, dtype=torch.float32, device=dev)
+    state = noise.clone()
+    steps, incontext, dim, sigma = 2, 1, 2, 0.1
+    dt = np.float32(1.0) / np.float32(steps)
+    seen = []
+    for step in range(steps):
+        t = float(np.float32(step) * dt)
+        hip.flow_incontext(state, noise, ctx, incontext * dim, t, sigma)
+        seen.append(from_dev(state).copy())
+        hip.flow_cfg_euler(state, ones, None, 6, 1.0, float(dt))
+    state[: incontext * dim] = ctx[: incontext * dim]
+    out = from_dev(state)
+    assert np.allclose(seen[0][:2], [1.0, 2.0], atol=1e-6)
+    assert np.allclose(seen[1][:2], [2.55, 5.10], atol=1e-6)
+    assert np.allclose(out, [4, 8, 11, 21, 31, 41], atol=1e-6)
+
+
+def test_config_fifty_steps_bit_exact(hip, dev, oracle):
+    """[1,64,2520] F32, dt = 1/50, g = 1.5, fresh seeded v_c, v_u every step."""
+    n, steps, g = 64 * 2520, 50, 1.5
+    dt = float(np.float32(1.0) / np.float32(steps))
+    x0 = oracle.gaussian(n, 4242)
+    want = x0.copy()
+    state = to_dev(x0, dev)
+    for s in range(steps):
+        vu = oracle.gaussian(n, 10_000 + 2 * s)
+        vc = oracle.gaussian(n, 10_001 + 2 * s)
+        hip.flow_cfg_euler(state, to_dev(vu, dev), to_dev(vc, dev), n, g, dt)
+        oracle.flow_cfg_euler(want, vu, vc, g, dt)
+    assert _eq(from_dev(state), want)
+
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (3, 0), (7, 0), (4099, 0), (1000, 1), (4097, 3)])
+def test_odd_sizes_and_unaligned(hip, dev, oracle, n, offset):
+    import torch
+    base = oracle.gaussian(n + offset, 8)
+    vu = oracle.gaussian(n + offset, 9)
+    vc = oracle.gaussian(n + offset, 10)
+    sd, ud, cd = to_dev(base, dev), to_dev(vu, dev), to_dev(vc, dev)
+    hip.flow_cfg_euler(sd[offset:], ud[offset:], cd[offset:], n, 1.5, 0.02)
+    want = base[offset:].copy()
+    oracle.flow_cfg_euler(want, vu[offset:].copy(), vc[offset:].copy(), 1.5, 0.02)
+    got = from_dev(sd)
+    assert _eq(got[offset:], want) and _eq(got[:offset], base[:offset])
+    # no CFG: state += dt * v
+    sd = to_dev(base, dev)
+    hip.flow_cfg_euler(sd[offset:], ud[offset:], None, n, 1.5, 0.02)
+    want = base[offset:].copy()
+    oracle.flow_cfg_euler(want, vu[offset:].copy(), None, 1.5, 0.02)
+    assert _eq(from_dev(sd)[offset:], want)
+    del torch
+
+
+def test_incontext_bit_exact(hip, dev, oracle):
+    n, prefix = 64 * 1000, 64 * 250
+    state0 = oracle.gaussian(n, 1)
+    noise = oracle.gaussian(n, 2)
+    ctx = oracle.gaussian(n, 3)
+    for step in (0, 7, 49):
+        t = float(np.float32(step) * (np.float32(1) / np.float32(50)))
+        sd = to_dev(state0, dev)
+        hip.flow_incontext(sd, to_dev(noise, dev), to_dev(ctx, dev), prefix, t, 1e-4)
+        want = state0.copy()
+        oracle.flow_incontext(want, noise, ctx, prefix, t, 1e-4)
+        assert _eq(from_dev(sd), want)
+
+
+def test_cfg_combine_kats_and_reference(hip, dev, oracle, ref):
+    import torch
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    hip.cfg_combine(out, to_dev(np.array([1, 1], np.float32), dev), to_dev(np.array([2, 4], np.float32), dev), 2, 1.5)
+    assert from_dev(out).tolist() == [2.5, 5.5]           # tests/test-sampling.cpp:8
+    hip.cfg_combine(out, to_dev(np.array([1, 2], np.float32), dev), to_dev(np.array([3, 6], np.float32), dev), 2, 1.5)
+    assert from_dev(out).tolist() == [4.0, 8.0]           # tests/test-renderer-pattern.cpp:88-90
+    n = 3 * 16384 + 3
+    c = oracle.gaussian(n, 31) * 3
+    u = oracle.gaussian(n, 32) * 3
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    hip.cfg_combine(out, to_dev(u, dev), to_dev(c, dev), n, 1.5)
+    got = from_dev(out)
+    assert _eq(got, ref.apply_cfg(c, u, 1.5))
+    assert _eq(got, ref.combine_renderer_cfg(u, c, 1.5))
+    out2 = torch.empty(n + 1, dtype=torch.float32, device=dev)
+    ud, cd = to_dev(np.concatenate([[0], u]).astype(np.float32), dev), to_dev(np.concatenate([[0], c]).astype(np.float32), dev)
+    hip.cfg_combine(out2[1:], ud[1:], cd[1:], n, 1.5)   # unaligned scalar path
+    assert _eq(from_dev(out2)[1:], got)
+
+
+def test_fp16_row_converters(hip, dev, oracle):
+    import torch
+    bits = np.arange(0, 2**32, 65537 * 13, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    f = f[~np.isnan(f)].copy()
+    h = torch.empty(f.size, dtype=torch.int16, device=dev)
+    hip.fp32_to_fp16_row(to_dev(f, dev), h, f.size)
+    assert np.array_equal(from_dev(h).view(np.uint16), oracle.f32_to_f16(f))
+    allh = np.arange(65536, dtype=np.uint16)
+    out = torch.empty(65536, dtype=torch.float32, device=dev)
+    hip.fp16_to_fp32_row(to_dev(allh.view(np.int16), dev), out, 65536)
+    got, want = from_dev(out), oracle.f16_to_f32(allh)
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32)) and np.all(np.isnan(got[~ok]))

@@ -1,0 +1,118 @@
+"""Fused residual add + RMSNorm / LayerNorm on the GPU vs the oracle.
+
+Bars: the residual output h is bit-exact (one F16 / F32 rounding of x + d);
+F16 outputs within 1 F16 ulp, F32 outputs within max |a-b|/max(|b|,1) <= 1e-5.
+(In practice both sides reduce in double and agree bit-for-bit; the tests
+also report how many elements differ.)
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import f16_ulp, f32_err, from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(oracle, rows, D, seed, f16):
+    x = oracle.gaussian(rows * D, seed).reshape(rows, D)
+    d = oracle.gaussian(rows * D, seed + 1).reshape(rows, D)
+    w = (oracle.gaussian(D, seed + 2) * 0.02 + 1).astype(np.float32)
+    b = (oracle.gaussian(D, seed + 3) * 0.02).astype(np.float32)
+    if f16:
+        return tuple(oracle.f32_to_f16(t) for t in (x, d, w, b))
+    return x, d, w, b
+
+
+def _run(hip, dev, layer, x, d, w, b, eps, with_delta=True, with_h=True):
+    import torch
+    f16 = x.dtype == np.uint16
+    act = 1 if f16 else 0
+    view = (lambda a: a.view(np.int16)) if f16 else (lambda a: a)
+    xd = to_dev(view(x), dev)
+    dd = to_dev(view(d), dev) if with_delta else None
+    wd, bd = to_dev(view(w), dev), to_dev(view(b), dev)
+    hd = torch.empty_like(xd) if with_h else None
+    yd = torch.empty_like(xd)
+    rows, D = x.shape
+    if layer:
+        hip.layer_norm(act, xd, dd, wd, bd, act, hd, yd, rows, D, eps)
+    else:
+        hip.rms_norm(act, xd, dd, wd, act, hd, yd, rows, D, eps)
+    back = (lambda a: a.view(np.uint16)) if f16 else (lambda a: a)
+    return (back(from_dev(hd)) if with_h else None), back(from_dev(yd))
+
+
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+@pytest.mark.parametrize("D", [1536, 2048])
+@pytest.mark.parametrize("rows", [1, 2, 756])
+def test_f16_config_shapes(hip, dev, oracle, layer, D, rows):
+    x, d, w, b = _inputs(oracle, rows, D, 100 + rows + D, True)
+    eps = 1e-6
+    h, y = _run(hip, dev, layer, x, d, w, b, eps)
+    if layer:
+        hw, yw = oracle.layer_norm(x, d, w, b, eps, threads=8)
+    else:
+        hw, yw = oracle.rms_norm(x, d, w, eps, threads=8)
+    assert np.array_equal(h, hw)
+    ulp = f16_ulp(y, yw)
+    print(f"differing elements: {np.count_nonzero(y != yw)} of {y.size}")
+    assert ulp <= 1
+
+
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+@pytest.mark.parametrize("D", [1536, 2200, 4400])
+def test_f32_reference_chains(hip, dev, oracle, layer, D):
+    rows = 37
+    x, d, w, b = _inputs(oracle, rows, D, 7 * D, False)
+    eps = 1e-5
+    h, y = _run(hip, dev, layer, x, d, w, b, eps)
+    if layer:
+        hw, yw = oracle.layer_norm(x, d, w, b, eps, threads=8)
+    else:
+        hw, yw = oracle.rms_norm(x, d, w, eps, threads=8)
+    assert np.array_equal(h.view(np.uint32), hw.view(np.uint32))
+    assert f32_err(y, yw) <= 1e-5
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+def test_scalar_path_and_optional_buffers(hip, dev, oracle, f16, layer):
+    rows, D = 5, 1003
+    x, d, w, b = _inputs(oracle, rows, D, 55, f16)
+    eps = 1e-6
+    for with_delta, with_h in ((True, True), (False, False), (True, False)):
+        h, y = _run(hip, dev, layer, x, d, w, b, eps, with_delta, with_h)
+        dd = d if with_delta else None
+        if layer:
+            hw, yw = oracle.layer_norm(x, dd, w, b, eps)
+        else:
+            hw, yw = oracle.rms_norm(x, dd, w, eps)
+        if with_h:
+            assert np.array_equal(h, hw)
+        if f16:
+            assert f16_ulp(y, yw) <= 1
+        else:
+            assert f32_err(y, yw) <= 1e-5
+
+
+def test_layer_norm_constant_rows_give_beta(hip, dev, oracle):
+    D = 2048
+    x = np.full((4, D), 0.3, np.float32)
+    _, _, w, b = _inputs(oracle, 1, D, 3, False)
+    _, y = _run(hip, dev, True, x, x, w, b, 1e-6, with_delta=False)
+    assert np.array_equal(y, np.broadcast_to(b, y.shape))
+
+
+def test_rms_f32_with_f16_weight(hip, dev, oracle):
+    """src/levo-lm.cpp:131-137 casts an F16 GGUF weight to F32 (exact)."""
+    import torch
+    rows, D = 9, 1536
+    x, d, w, _ = _inputs(oracle, rows, D, 17, False)
+    w16 = oracle.f32_to_f16(w)
+    xd, dd = to_dev(x, dev), to_dev(d, dev)
+    yd = torch.empty_like(xd)
+    hip.rms_norm(0, xd, dd, to_dev(w16.view(np.int16), dev), 1, None, yd, rows, D, 1e-5)
+    _, yw = oracle.rms_norm(x, d, oracle.f16_to_f32(w16), 1e-5)
+    assert f32_err(from_dev(yd), yw) <= 1e-5

@@ -1,0 +1,129 @@
+"""Q8_0 / Q4_0 quantize and dequantize on the GPU vs the oracle's restatement
+of ggml's reference quantizers (ggml_quantize_chunk, tools/levo-quantize.cpp:386-388).
+
+Bar: quantized blocks bit-exact (memcmp); dequantized values bit-exact (the
+products are exact in F32); F16 dequantization is the RNE rounding of them.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+Q8, Q4 = 8, 2
+BB = {Q8: 34, Q4: 18}
+
+
+def _quant_f16(hip, dev, qt, xh, dst_cols=None):
+    import torch
+    rows, cols = xh.shape
+    dst_cols = dst_cols or cols
+    out = torch.empty(rows * (dst_cols // 32) * BB[qt], dtype=torch.uint8, device=dev)
+    n = hip.quantize_rows(qt, to_dev(xh.view(np.int16), dev), 1, cols, cols, out, rows, dst_cols)
+    assert n == out.numel()
+    return from_dev(out)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+def test_config_weights_bit_exact(hip, dev, oracle, qt):
+    """F16 weights [4096, 1536] ~N(0, 0.02), 196,608 blocks."""
+    xh = oracle.f32_to_f16((oracle.gaussian(4096 * 1536, 1500) * 0.02).reshape(4096, 1536))
+    got = _quant_f16(hip, dev, qt, xh)
+    want = oracle.quantize_f16_padded(qt, xh, 1536)
+    assert np.array_equal(got, want), np.count_nonzero(got != want)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+def test_quantize_chunk_f32_with_start(hip, dev, oracle, qt):
+    import torch
+    rows, cols = 40, 2208
+    x = (oracle.gaussian(rows * cols, 1600) * 0.5).reshape(rows, cols)
+    out = torch.zeros(rows * (cols // 32) * BB[qt], dtype=torch.uint8, device=dev)
+    xd = to_dev(x, dev)
+    n1 = hip.quantize_chunk(qt, xd, out, 0, 17, cols)
+    n2 = hip.quantize_chunk(qt, xd, out, 17 * cols, rows - 17, cols)
+    row_size = hip.row_size(qt, cols)
+    assert n1 == 17 * row_size and n2 == (rows - 17) * row_size
+    assert np.array_equal(from_dev(out), oracle.quantize(qt, x))
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+def test_padded_rows_flow_hidden(hip, dev, oracle, qt):
+    """write_tensor zero-pads 2200 -> 2208 columns (src/levo-quantization.h:120-130)."""
+    xh = oracle.f32_to_f16((oracle.gaussian(33 * 2200, 1700) * 0.02).reshape(33, 2200))
+    assert np.array_equal(_quant_f16(hip, dev, qt, xh, 2208), oracle.quantize_f16_padded(qt, xh, 2208))
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+def test_special_blocks(hip, dev, oracle, qt):
+    import torch
+    x = (oracle.gaussian(64 * 32, 1800) * 0.02).reshape(64, 32)
+    x[0] = 0.0
+    x[1] = -0.0
+    x[2] = 0.0
+    x[2, 0], x[2, 1], x[2, 2], x[2, 3] = 127.0, 2.5, -2.5, 0.5     # Q8_0 ties round away from zero
+    x[3] = 1e-6 * np.arange(32)                                       # F16-subnormal scale
+    x[4] = 0.0
+    x[4, 1], x[4, 3] = -0.5, 0.5                                      # Q4_0: first of equal |x| wins
+    x[5] = 3e-39 * np.arange(1, 33)                                   # F32 subnormals: 1/d overflows
+    x[6] = 1e-38
+    x[7, :] = np.float32(-8.0) * np.arange(32) / 31                   # exact -8 multiples
+    x[8, :] = 65504.0
+    x[9, 5] = 1e30                                                    # huge outlier, F16 d overflows to inf
+    out = torch.empty(64 * BB[qt], dtype=torch.uint8, device=dev)
+    hip.quantize_chunk(qt, to_dev(x, dev), out, 0, 64, 32)
+    got, want = from_dev(out), oracle.quantize(qt, x)
+    bad = np.nonzero((got != want).reshape(64, BB[qt]).any(axis=1))[0]
+    assert bad.size == 0, bad
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+@pytest.mark.parametrize("nblocks", [1, 7, 8, 9, 15, 16, 17, 100, 4099])
+def test_tail_groups(hip, dev, oracle, qt, nblocks):
+    import torch
+    x = oracle.gaussian(nblocks * 32, 1900 + nblocks).reshape(nblocks, 32)
+    xh = oracle.f32_to_f16(x)
+    assert np.array_equal(_quant_f16(hip, dev, qt, xh), oracle.quantize_f16_padded(qt, xh, 32))
+    out = torch.full((nblocks * BB[qt] + 64,), 0xAB, dtype=torch.uint8, device=dev)
+    hip.quantize_chunk(qt, to_dev(x, dev), out, 0, nblocks, 32)
+    got = from_dev(out)
+    assert np.array_equal(got[: nblocks * BB[qt]], oracle.quantize(qt, x))
+    assert np.all(got[nblocks * BB[qt]:] == 0xAB)  # nothing written past the last block
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+@pytest.mark.parametrize("nblocks", [1, 9, 16, 17, 196608])
+def test_dequantize_bit_exact(hip, dev, oracle, qt, nblocks):
+    import torch
+    x = (oracle.gaussian(nblocks * 32, 2000 + nblocks) * 0.02).astype(np.float32)
+    q = oracle.quantize(qt, x.reshape(nblocks, 32))
+    want = oracle.dequantize(qt, q, x.size)
+    qd = to_dev(q, dev)
+    y = torch.full((x.size + 8,), 3.0, dtype=torch.float32, device=dev)
+    hip.dequantize(qt, qd, y, 0, x.size)
+    got = from_dev(y)
+    assert np.array_equal(got[: x.size].view(np.uint32), want.view(np.uint32))
+    assert np.all(got[x.size:] == 3.0)
+    h = torch.empty(x.size, dtype=torch.int16, device=dev)
+    hip.dequantize(qt, qd, h, 1, x.size)
+    assert np.array_equal(from_dev(h).view(np.uint16), want.astype(np.float16).view(np.uint16))
+
+
+def test_reference_padded_q8_product(hip, dev):
+    """tests/test-quantization.cpp:46-75 through the GPU quantizer and dequantizer."""
+    import torch
+    m = np.zeros((4, 32), np.float32)
+    for r in range(4):
+        for c in range(6):
+            m[r, c] = 0.03125 * (r + 1) * (c + 1)
+    q = torch.empty(4 * 34, dtype=torch.uint8, device=dev)
+    assert hip.quantize_chunk(Q8, to_dev(m, dev), q, 0, 4, 32) == 4 * 34
+    y = torch.empty(128, dtype=torch.float32, device=dev)
+    hip.dequantize(Q8, q, y, 0, 128)
+    deq = from_dev(y).reshape(4, 32)
+    inp = np.zeros(32, np.float32)
+    inp[:6] = [0.25, -0.5, 0.75, -1.0, 1.25, -1.5]
+    assert np.all(np.abs(deq @ inp - m @ inp) < 0.015)

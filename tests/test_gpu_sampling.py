@@ -1,0 +1,254 @@
+"""CFG + temperature softmax + argmax / top-k on the GPU vs the oracle and
+the compiled reference sampler (src/levo-sampling.cpp).
+
+Bars: argmax ids, candidate ids (top-k with ties) and candidate logits are
+bit-exact; probabilities and the log-sum-exp are F32 outputs (<= 1e-5);
+sampled tokens drawn on the host from the GPU candidates equal the
+reference Sampler's tokens and its draw cursor.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import f32_err, from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def run_sample(hip, binding, dev, cond, uncond, *, top_k, n_streams, temperature=0.9, scale=1.5, capacity=64,
+               vocab=None, pitch=None, recent=None, penalty=1.1, penalty_limit=0, ignore=None, lse=True):
+    import torch
+    rows = cond.shape[0]
+    V = vocab if vocab is not None else cond.shape[1]
+    P = pitch if pitch is not None else cond.shape[1]
+    cd = to_dev(cond, dev)
+    ud = to_dev(uncond, dev) if uncond is not None else None
+    a = binding.SampleArgs()
+    a.cond = cd.data_ptr()
+    a.uncond = ud.data_ptr() if ud is not None else None
+    a.rows, a.vocab, a.row_pitch = rows, V, P
+    a.cfg_scale, a.temperature, a.n_streams = scale, temperature, n_streams
+    for i, k in enumerate(top_k):
+        a.top_k[i] = k
+    keep = []
+    if recent is not None:
+        rd = to_dev(np.ascontiguousarray(recent, np.int64), dev)
+        keep.append(rd)
+        a.recent, a.n_recent, a.repetition_penalty, a.penalty_limit = rd.data_ptr(), recent.shape[1], penalty, penalty_limit
+    if ignore is not None and len(ignore):
+        idd = to_dev(np.asarray(ignore, np.int64), dev)
+        keep.append(idd)
+        a.ignore, a.n_ignore = idd.data_ptr(), len(ignore)
+    best = torch.empty(rows, dtype=torch.int32, device=dev)
+    count = torch.empty(rows, dtype=torch.int32, device=dev)
+    ids = torch.full((rows, capacity), -7, dtype=torch.int32, device=dev)
+    lg = torch.empty((rows, capacity), dtype=torch.float32, device=dev)
+    pr = torch.empty((rows, capacity), dtype=torch.float32, device=dev)
+    mx = torch.empty(rows, dtype=torch.float32, device=dev)
+    ls = torch.empty(rows, dtype=torch.float32, device=dev) if lse else None
+    a.best, a.count, a.cand_ids, a.cand_logits, a.cand_probs = (best.data_ptr(), count.data_ptr(), ids.data_ptr(),
+                                                                lg.data_ptr(), pr.data_ptr())
+    a.row_max = mx.data_ptr()
+    a.row_lse = ls.data_ptr() if lse else None
+    a.capacity = capacity
+    hip.cfg_sample(a)
+    out = dict(best=from_dev(best), count=from_dev(count), ids=from_dev(ids), logits=from_dev(lg),
+               probs=from_dev(pr), max=from_dev(mx))
+    if lse:
+        out["lse"] = from_dev(ls)
+    return out
+
+
+def weights_f64(vals, m, t):
+    """src/levo-sampling.cpp:102-107: exp((double)((v - max) / T)), -inf -> 0."""
+    v = np.asarray(vals, np.float32)
+    w = np.where(np.isneginf(v), 0.0, np.exp(((v - np.float32(m)) / np.float32(t)).astype(np.float64)))
+    return w
+
+
+def check_rows(out, adjusted, top_ks, oracle, temperature, rows=None, lse=True):
+    R = adjusted.shape[0]
+    for r in (range(R) if rows is None else rows):
+        row = adjusted[r]
+        k = top_ks[r]
+        best, cand = oracle.top_k_candidates(row, k)
+        assert out["best"][r] == best, r
+        assert out["count"][r] == cand.size, (r, out["count"][r], cand.size)
+        n = min(cand.size, out["ids"].shape[1])
+        assert np.array_equal(out["ids"][r, :n], cand[:n]), r
+        assert np.array_equal(out["logits"][r, :n].view(np.uint32), row[cand[:n]].view(np.uint32)), r
+        m = np.float32(row.max())
+        assert out["max"][r].view(np.uint32) == m.view(np.uint32)
+        w = weights_f64(row[cand], m, temperature)
+        if w.sum() > 0 and np.isfinite(w.sum()):
+            assert f32_err(out["probs"][r, :n], w[:n] / w.sum()) <= 1e-5, r
+        if lse:
+            z = row.astype(np.float64) / temperature
+            want = z.max() + math.log(np.exp(z - z.max()).sum())
+            assert f32_err(out["lse"][r:r + 1], np.array([want])) <= 1e-5, r
+
+
+def test_config_batch_750_positions(hip, binding, dev, oracle):
+    """cond/uncond [750][3][16384] ~N(0,3), s = 1.5, T = 0.9, top-50; argmax ids bit-exact."""
+    P, S, V = 750, 3, 16384
+    cond = (oracle.gaussian(P * S * V, 501) * 3).reshape(P * S, V)
+    uncond = (oracle.gaussian(P * S * V, 502) * 3).reshape(P * S, V)
+    out = run_sample(hip, binding, dev, cond, uncond, top_k=[50, 50, 50], n_streams=3)
+    adjusted = oracle.apply_cfg(cond, uncond, 1.5)
+    check_rows(out, adjusted, [50] * (P * S), oracle, 0.9)
+
+
+def _f16_logits(oracle, rows, V, seed):
+    return oracle.f16_to_f32(oracle.f32_to_f16((oracle.gaussian(rows * V, seed) * 3).reshape(rows, V)))
+
+
+@pytest.mark.parametrize("k", [1, 2, 50, 64, 65, 100, 300, 0, 16383, 16384])
+def test_ties_and_k(hip, binding, dev, oracle, k):
+    V, R = 16384, 24
+    cond = _f16_logits(oracle, R, V, 600 + k)
+    # plant ties: at the max, at the k-th value, whole row equal, -0 / +0
+    cond[1, 5000:5040] = cond[1].max() + 1.0
+    srt = np.sort(cond[2])[::-1]
+    if 0 < k < V:
+        cond[2, :40] = srt[k - 1]
+    cond[3, :] = 0.5
+    cond[4, :] = 0.0
+    cond[4, ::3] = -0.0
+    out = run_sample(hip, binding, dev, cond, None, top_k=[k], n_streams=1, capacity=512)
+    check_rows(out, cond, [k] * R, oracle, 0.9)
+
+
+def test_reference_stream_config_with_ties(hip, binding, dev, oracle):
+    """sampling_config defaults: mixed stream top-50, vocal/BGM top-1 (src/levo-sampling.h:17-25)."""
+    P, S, V = 120, 3, 16384
+    cond = _f16_logits(oracle, P * S, V, 700)
+    uncond = _f16_logits(oracle, P * S, V, 701)
+    out = run_sample(hip, binding, dev, cond, uncond, top_k=[50, 1, 1], n_streams=3)
+    adjusted = oracle.apply_cfg(cond, uncond, 1.5)
+    check_rows(out, adjusted, [50, 1, 1] * P, oracle, 0.9)
+
+
+def test_vocab_16385_packed_rows(hip, binding, dev, oracle):
+    """The real LeLM rows hold 16384 codes + EOS (src/levo-model.h:121): unaligned pitch."""
+    R, V = 30, 16385
+    cond = _f16_logits(oracle, R, V, 800)
+    uncond = _f16_logits(oracle, R, V, 801)
+    out = run_sample(hip, binding, dev, cond, uncond, top_k=[50, 1, 1], n_streams=3)
+    check_rows(out, oracle.apply_cfg(cond, uncond, 1.5), [50, 1, 1] * 10, oracle, 0.9)
+    # the same rows at a padded, 16-byte aligned pitch take the vector path
+    pad = np.zeros((R, 16388), np.float32)
+    padu = np.zeros((R, 16388), np.float32)
+    pad[:, :V], padu[:, :V] = cond, uncond
+    out2 = run_sample(hip, binding, dev, pad, padu, top_k=[50, 1, 1], n_streams=3, vocab=V)
+    for key in ("best", "count", "ids", "logits", "max"):
+        assert np.array_equal(out[key], out2[key])
+
+
+@pytest.mark.parametrize("V", [1, 3, 4, 100, 1000, 5000])
+def test_small_vocabularies(hip, binding, dev, oracle, V):
+    R = 12
+    cond = _f16_logits(oracle, R, V, 900 + V)
+    ks = [1, 2, 3, 0]
+    out = run_sample(hip, binding, dev, cond, None, top_k=ks, n_streams=4, capacity=max(V, 1))
+    check_rows(out, cond, ks * (R // 4), oracle, 0.9)
+
+
+def test_penalty_and_ignore_lists(hip, binding, dev, oracle):
+    P, S, V = 40, 3, 16385
+    cond = _f16_logits(oracle, P * S, V, 1000)
+    uncond = _f16_logits(oracle, P * S, V, 1001)
+    rng = np.random.default_rng(5)
+    recent = rng.integers(-1, V, size=(P * S, 50))
+    recent[:, :10] = rng.integers(0, 40, size=(P * S, 10))   # repeats: divided once
+    recent[0, :] = V - 1                                        # EOS is excluded by the limit
+    ignore = [3, 9, 77, 16000, V + 5, -2]
+    out = run_sample(hip, binding, dev, cond, uncond, top_k=[50, 1, 1], n_streams=3, recent=recent,
+                     penalty=1.1, penalty_limit=V - 1, ignore=ignore)
+    adjusted = oracle.apply_cfg(cond, uncond, 1.5)
+    for r in range(P * S):
+        adjusted[r] = oracle.repetition_penalty(adjusted[r], recent[r], 1.1, V - 1)
+        if r % 3 == 0:
+            for t in ignore:
+                if 0 <= t < V:
+                    adjusted[r, t] = -np.inf
+    check_rows(out, adjusted, [50, 1, 1] * P, oracle, 0.9)
+
+
+def test_nan_and_degenerate_rows(hip, binding, dev, oracle):
+    V = 4096
+    cond = _f16_logits(oracle, 6, V, 1100)
+    cond[0, 17] = np.nan                 # rejected like the reference ("logits contain NaN")
+    cond[1, 3] = np.nan                  # stream-1 row: the ignore list does not apply, NaN stays
+    cond[2, :] = -np.inf                 # everything -inf: all ids stay candidates
+    cond[3, :] = np.inf
+    cond[3, 10:] = 0.0                   # +inf maxima
+    out = run_sample(hip, binding, dev, cond, None, top_k=[50, 50], n_streams=2, ignore=[3], capacity=V)
+    assert out["best"][0] == -1 and out["count"][0] == -1
+    adjusted = cond.copy()
+    adjusted[[2, 4], 3] = -np.inf        # ignore list applies to stream-0 rows only (2, 4)
+    adjusted[1, 3] = np.nan              # row 1 is stream 1: its NaN stays
+    assert out["count"][1] == -1
+    check_rows(out, adjusted, [50] * 6, oracle, 0.9, rows=[2, 3, 4, 5], lse=False)
+    assert out["count"][2] == V and out["best"][2] == 0
+    assert out["probs"][2, 0] == 1.0 and np.all(out["probs"][2, 1:] == 0.0)  # falls back to best
+
+
+def test_capacity_overflow_reports_full_count(hip, binding, dev, oracle):
+    V = 3000
+    cond = _f16_logits(oracle, 2, V, 1200)
+    out = run_sample(hip, binding, dev, cond, None, top_k=[0], n_streams=1, capacity=64)
+    assert np.all(out["count"] == V)
+    assert np.array_equal(out["ids"][0], np.arange(64))
+
+
+def host_draw(oracle, rng, draws, ids, logits, best, count, temperature, use_sampling):
+    """The host half of sample_top_k_counted (src/levo-sampling.cpp:97-115):
+    returns (token, draws) from the GPU candidate list."""
+    if not use_sampling or temperature == 0.0:
+        return best, draws
+    cand = np.asarray(logits[:count], np.float32)
+    m = np.float32(cand.max())
+    w = weights_f64(cand, m, temperature)
+    total = 0.0
+    for x in w:
+        total += float(x)
+    if not (total > 0.0) or not math.isfinite(total):
+        return best, draws
+    u = ((oracle.mt_next(rng) >> 11) + 0.5) / 9007199254740992.0
+    target = u * total
+    cum = 0.0
+    for i, x in enumerate(w):
+        cum += float(x)
+        if target < cum:
+            return int(ids[i]), draws + 1
+    return int(ids[count - 1]), draws + 1
+
+
+def test_sampled_tokens_match_reference_sampler(hip, binding, dev, oracle, ref):
+    P, S, V = 60, 3, 16385
+    cond = _f16_logits(oracle, P * S, V, 1300)
+    uncond = _f16_logits(oracle, P * S, V, 1301)
+    for seed, temp, use in ((11, 0.9, True), (12, 0.3, True), (13, 0.9, False)):
+        s = ref.sampler(seed)
+        rng, draws = oracle.mt(seed), 0
+        recent = np.full((S, 50), -1, np.int64)
+        adjusted = oracle.apply_cfg(cond, uncond, 1.5)
+        for pos in range(P):
+            rows = slice(pos * S, pos * S + S)
+            want = s.sample_streams(adjusted[rows], use_sampling=use, temperature=temp, top_k_mixed=50,
+                                    top_k_detail=1, repetition_penalty=1.1, recent=recent, ignore=(3, 9))
+            out = run_sample(hip, binding, dev, cond[rows], uncond[rows], top_k=[50, 1, 1], n_streams=3,
+                             temperature=temp, capacity=256, recent=recent, penalty=1.1, penalty_limit=V - 1,
+                             ignore=(3, 9), lse=False)
+            got = []
+            for q in range(S):
+                assert 0 <= out["count"][q] <= 256
+                tok, draws = host_draw(oracle, rng, draws, out["ids"][q], out["logits"][q], int(out["best"][q]),
+                                       int(out["count"][q]), temp, use)
+                got.append(tok)
+            assert got == want.tolist(), (seed, pos)
+            recent = np.concatenate([recent[:, 1:], np.array(got, np.int64)[:, None]], axis=1)
+        assert draws == s.draw_count
