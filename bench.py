@@ -13,7 +13,9 @@ data untouched for >= 512 MB of traffic, i.e. from HBM, not the 256 MB
 Infinity Cache): SnakeBeta 1 s config, Flow CFG+Euler (50 steps), residual +
 RMSNorm / LayerNorm F16, CFG + softmax + argmax / top-50, Q8_0 / Q4_0
 quantize / dequantize. Kernel durations come from HIP events recorded on the
-stream the kernels run on (torch's current stream).
+stream the kernels run on (torch's current stream); a bounded spin kernel
+queued first keeps the GPU busy while the host enqueues each timed region, so
+the timed launches run back to back.
 
 The CPU baseline is the CPU oracle (a port of the reference's ggml-cpu op
 chains; ggml itself is not available) run on a bounded sample on this host.
@@ -57,41 +59,64 @@ def snake_bytes(C, T):
     return 8 * C * T + 8 * C
 
 
-class Timer:
-    """Per-launch HIP events on torch's current stream."""
+class HeadStart:
+    """Keeps the GPU busy with a bounded spin kernel while the host enqueues a
+    timed region, so the timed launches run back-to-back and HIP events time
+    the GPU, not the Python launch rate."""
 
-    def __init__(self, torch, n):
-        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
-        self.i = 0
+    def __init__(self, torch):
+        self.torch = torch
+        torch.cuda._sleep(1000)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cycles = 2_000_000
+        a.record()
+        torch.cuda._sleep(cycles)
+        b.record()
+        torch.cuda.synchronize()
+        self.cycles_per_ms = cycles / max(a.elapsed_time(b), 1e-3)
 
-    def mark(self):
-        self.ev[self.i].record()
-        self.i += 1
-
-    def durations_ms(self):
-        return [self.ev[k].elapsed_time(self.ev[k + 1]) for k in range(self.i - 1)]
+    def __call__(self, ms: float):
+        self.torch.cuda._sleep(int(self.cycles_per_ms * ms))
 
 
-def time_op(torch, launch, n_sets, warmup, steps):
-    """launch(set_index) enqueues one launch; returns mean ms per launch from
-    back-to-back per-launch events (>= 512 MB between reuses of a set)."""
+def time_region(torch, head, enqueue, host_ms_estimate):
+    """Time enqueue() between two events after a spin head start."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    head(min(200.0, 2.0 * host_ms_estimate + 1.0))
+    start.record()
+    t0 = time.perf_counter()
+    enqueue()
+    host_ms = (time.perf_counter() - t0) * 1e3
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end), host_ms
+
+
+def time_op(torch, head, launch, n_sets, warmup, steps):
+    """Mean ms per launch of launch(set_index) over `steps` back-to-back launches
+    cycling through n_sets buffer sets (>= 512 MB of traffic between reuses)."""
+    t0 = time.perf_counter()
     for i in range(warmup):
         launch(i % n_sets)
+    host_ms = (time.perf_counter() - t0) * 1e3 / max(warmup, 1) * steps
     torch.cuda.synchronize()
-    t = Timer(torch, steps)
-    for i in range(steps):
-        t.mark()
-        launch(i % n_sets)
-    t.mark()
-    torch.cuda.synchronize()
-    d = t.durations_ms()
-    return float(np.mean(d)), float(np.min(d))
+
+    def run():
+        for i in range(steps):
+            launch(i % n_sets)
+
+    ms, host = time_region(torch, head, run, host_ms)
+    if host > ms:  # the head start was too short: the GPU waited on the host
+        ms, host = time_region(torch, head, run, host)
+    return ms / steps
 
 
-def op_entry(bytes_per_launch, ms, ms_min, **extra):
+def op_entry(bytes_per_launch, ms, **extra):
     gbps = bytes_per_launch / (ms * 1e-3) / 1e9
     e = {"bytes_per_launch": int(bytes_per_launch), "us_per_launch": round(ms * 1e3, 3),
-         "us_min": round(ms_min * 1e3, 3), "GB/s": round(gbps, 1), "frac": round(gbps / PEAK_GBPS, 4)}
+         "GB/s": round(gbps, 1), "frac": round(gbps / PEAK_GBPS, 4)}
     e.update(extra)
     return e
 
@@ -104,7 +129,7 @@ def cpu_threads():
 
 
 # ---------------------------------------------------------------------------------------
-def bench_ladder(torch, hip, dev, warmup, steps):
+def bench_ladder(torch, hip, head, dev, warmup, steps):
     g = torch.Generator(device=dev)
     g.manual_seed(20250101)
     rng = np.random.default_rng(7)
@@ -121,40 +146,47 @@ def bench_ladder(torch, hip, dev, warmup, steps):
         sets.append(tensors)
     torch.cuda.synchronize()
 
-    def ladder(s, timer=None):
-        for (C, T), (x, a, b, y) in zip(LADDER, sets[s]):
-            if timer:
-                timer.mark()
+    def ladder(s):
+        for x, a, b, y in sets[s]:
             hip.snake_beta(x, a, b, y)
 
+    t0 = time.perf_counter()
     for i in range(warmup):
         ladder(i % n_sets)
+    host_ms = (time.perf_counter() - t0) * 1e3 / max(warmup, 1) * steps
     torch.cuda.synchronize()
-    # timed region: K ladder steps, one event before every launch and one at the end
-    timer = Timer(torch, steps * len(LADDER))
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record()
-    for i in range(steps):
-        ladder(i % n_sets, timer)
-    timer.mark()
-    end.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    ms_total = start.elapsed_time(end)
-    d = np.array(timer.durations_ms()).reshape(steps, len(LADDER))
-    per_shape = {}
-    for j, (C, T) in enumerate(LADDER):
-        per_shape[f"{C}x{T}"] = op_entry(snake_bytes(C, T), float(d[:, j].mean()), float(d[:, j].min()))
+
+    def run():
+        for i in range(steps):
+            ladder(i % n_sets)
+
+    # timed region: K ladder steps back to back, events on the kernels' stream
+    wall0 = time.perf_counter()
+    ms_total, host = time_region(torch, head, run, host_ms)
+    if host > ms_total:
+        ms_total, host = time_region(torch, head, run, host)
+    wall_ms = (time.perf_counter() - wall0) * 1e3
     host = [(t[0].cpu().numpy(), t[1].cpu().numpy(), t[2].cpu().numpy()) for t in sets[0]]
+    # per-shape launch durations: each shape K times back to back over its own
+    # rotation (>= 512 MB between reuses of a buffer)
+    per_shape = {}
+    shape_ms = []
+    for j, (C, T) in enumerate(LADDER):
+        n = max(2, math.ceil(ROTATE_BYTES / snake_bytes(C, T)) + 1)
+        xs = [sets[0][j][0]] + [torch.randn((C, T), generator=g, device=dev) for _ in range(n - 1)]
+        ys = [torch.empty((C, T), device=dev) for _ in range(n)]
+        a, b = sets[0][j][1], sets[0][j][2]
+        ms = time_op(torch, head, lambda i: hip.snake_beta(xs[i], a, b, ys[i]), n, warmup, max(steps, n))
+        per_shape[f"{C}x{T}"] = op_entry(snake_bytes(C, T), ms, rotated_sets=n)
+        shape_ms.append(ms)
+        del xs, ys
+    del sets
+    torch.cuda.empty_cache()
     return dict(ms_per_step=ms_total / steps, wall_ms=wall_ms, per_shape=per_shape,
-                ladder_bytes=per_set, host=host, n_sets=n_sets,
-                dominant=(LADDER[-1], float(d[:, -1].mean())))
+                ladder_bytes=per_set, host=host, n_sets=n_sets, dominant=(LADDER[-1], shape_ms[-1]))
 
 
-def bench_snake_1s(torch, hip, dev, warmup, steps):
+def bench_snake_1s(torch, hip, head, dev, warmup, steps):
     C, T = 128, 48000
     per = snake_bytes(C, T)
     n = math.ceil(ROTATE_BYTES / per) + 1
@@ -164,11 +196,11 @@ def bench_snake_1s(torch, hip, dev, warmup, steps):
     bufs = [(torch.randn((C, T), generator=g, device=dev), torch.from_numpy(rng.uniform(-0.5, 0.5, C).astype(np.float32)).to(dev),
              torch.from_numpy(rng.uniform(-0.5, 0.5, C).astype(np.float32)).to(dev)) for _ in range(n)]
     outs = [torch.empty((C, T), device=dev) for _ in range(n)]
-    ms, mn = time_op(torch, lambda i: hip.snake_beta(bufs[i][0], bufs[i][1], bufs[i][2], outs[i]), n, warmup, steps)
-    return op_entry(per, ms, mn, shape=[C, T], dtype="f32")
+    ms = time_op(torch, head, lambda i: hip.snake_beta(bufs[i][0], bufs[i][1], bufs[i][2], outs[i]), n, warmup, steps)
+    return op_entry(per, ms, shape=[C, T], dtype="f32")
 
 
-def bench_flow(torch, hip, dev, warmup, steps):
+def bench_flow(torch, hip, head, dev, warmup, steps):
     n_el, nsteps = 64 * 2520, 50
     per = 16 * n_el
     n_sets = math.ceil(ROTATE_BYTES / (per * nsteps)) + 1
@@ -179,26 +211,16 @@ def bench_flow(torch, hip, dev, warmup, steps):
            for _ in range(nsteps)] for _ in range(n_sets)]
     dt = float(np.float32(1) / np.float32(nsteps))
 
-    def solve(s, timer=None):
+    def solve(s):
         for k in range(nsteps):
-            if timer:
-                timer.mark()
             hip.flow_cfg_euler(xs[s], vs[s][k][0], vs[s][k][1], n_el, 1.5, dt)
 
-    for i in range(warmup):
-        solve(i % n_sets)
-    torch.cuda.synchronize()
+    # one launch per Euler step: mean kernel time over back-to-back launches
+    step_ms = time_op(torch, head, lambda i: hip.flow_cfg_euler(xs[i % n_sets], vs[i % n_sets][i % nsteps][0],
+                                                                 vs[i % n_sets][i % nsteps][1], n_el, 1.5, dt),
+                      n_sets * nsteps, warmup, max(steps, 50))
     reps = max(1, steps // 5)
-    timer = Timer(torch, reps * nsteps)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(reps):
-        solve(i % n_sets, timer)
-    timer.mark()
-    end.record()
-    torch.cuda.synchronize()
-    d = np.array(timer.durations_ms())
-    solve_ms = start.elapsed_time(end) / reps
+    solve_ms = time_op(torch, head, solve, n_sets, 1, reps)
     # the same 50 launches captured once into a HIP graph and replayed
     graph_ms = None
     try:
@@ -211,23 +233,19 @@ def bench_flow(torch, hip, dev, warmup, steps):
         for _ in range(3):
             graph.replay()
         torch.cuda.synchronize()
-        gs, ge = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        gs.record()
-        for _ in range(reps):
-            graph.replay()
-        ge.record()
-        torch.cuda.synchronize()
-        graph_ms = gs.elapsed_time(ge) / reps
+        graph_ms = time_op(torch, head, lambda i: graph.replay(), 1, 1, reps)
     except Exception as e:  # graph capture is an extra measurement only
         log(f"flow graph capture skipped: {e}")
-    e = op_entry(per, float(d.mean()), float(d.min()), shape=[1, 64, 2520], dtype="f32",
-                 solve_50_steps_ms=round(solve_ms, 4), solve_50_steps_GBps=round(per * nsteps / (solve_ms * 1e-3) / 1e9, 1))
+    e = op_entry(per, step_ms, shape=[1, 64, 2520], dtype="f32",
+                 solve_50_steps_ms=round(solve_ms, 4),
+                 solve_50_steps_GBps=round(per * nsteps / (solve_ms * 1e-3) / 1e9, 1))
     if graph_ms is not None:
         e["solve_50_steps_graph_ms"] = round(graph_ms, 4)
+        e["solve_50_steps_graph_GBps"] = round(per * nsteps / (graph_ms * 1e-3) / 1e9, 1)
     return e
 
 
-def bench_norm(torch, hip, dev, warmup, steps, layer, rows, D):
+def bench_norm(torch, hip, head, dev, warmup, steps, layer, rows, D):
     per = 8 * rows * D + (4 * D if layer else 2 * D)
     n = max(2, math.ceil(ROTATE_BYTES / per) + 1) if rows > 2 else 64
     g = torch.Generator(device=dev)
@@ -240,11 +258,11 @@ def bench_norm(torch, hip, dev, warmup, steps, layer, rows, D):
         fn = lambda i: hip.layer_norm(1, sets[i][0], sets[i][1], w, b, 1, sets[i][2], sets[i][3], rows, D, 1e-6)
     else:
         fn = lambda i: hip.rms_norm(1, sets[i][0], sets[i][1], w, 1, sets[i][2], sets[i][3], rows, D, 1e-6)
-    ms, mn = time_op(torch, fn, n, warmup, max(steps, 20))
-    return op_entry(per, ms, mn, shape=[rows, D], dtype="f16 io / f32 accumulate")
+    ms = time_op(torch, head, fn, n, warmup, max(steps, 50))
+    return op_entry(per, ms, shape=[rows, D], dtype="f16 io / f32 accumulate")
 
 
-def bench_sample(torch, hip, binding, dev, warmup, steps):
+def bench_sample(torch, hip, binding, head, dev, warmup, steps):
     P, S, V, cap = 750, 3, 16384, 64
     rows = P * S
     reads = 2 * rows * V * 4
@@ -271,11 +289,11 @@ def bench_sample(torch, hip, binding, dev, warmup, steps):
         a.best, a.count, a.cand_ids, a.cand_probs = best.data_ptr(), count.data_ptr(), ids.data_ptr(), probs.data_ptr()
         a.row_max, a.row_lse, a.capacity = mx.data_ptr(), lse.data_ptr(), cap
         args.append(a)
-    ms, mn = time_op(torch, lambda i: hip.cfg_sample(args[i]), n, warmup, steps)
-    return op_entry(per, ms, mn, shape=[P, 2, S, V], dtype="f32", top_k=50, temperature=0.9)
+    ms = time_op(torch, head, lambda i: hip.cfg_sample(args[i]), n, warmup, steps)
+    return op_entry(per, ms, shape=[P, 2, S, V], dtype="f32", top_k=50, temperature=0.9)
 
 
-def bench_quant(torch, hip, dev, warmup, steps):
+def bench_quant(torch, hip, head, dev, warmup, steps):
     R, Cc = 4096, 1536
     out = {}
     for qt, name, bb in ((8, "q8_0", 34), (2, "q4_0", 18)):
@@ -288,10 +306,11 @@ def bench_quant(torch, hip, dev, warmup, steps):
         src = [(torch.randn((R, Cc), generator=g, device=dev) * 0.02).half() for _ in range(n)]
         q = [torch.empty(qbytes, dtype=torch.uint8, device=dev) for _ in range(n)]
         deq = [torch.empty((R, Cc), dtype=torch.float32, device=dev) for _ in range(n)]
-        ms, mn = time_op(torch, lambda i: hip.quantize_rows(qt, src[i], 1, Cc, Cc, q[i], R, Cc), n, warmup, steps)
-        out[f"{name}_quantize_f16"] = op_entry(per_q, ms, mn, shape=[R, Cc])
-        ms, mn = time_op(torch, lambda i: hip.dequantize(qt, q[i], deq[i], 0, R * Cc), n, warmup, steps)
-        out[f"{name}_dequantize_f32"] = op_entry(per_d, ms, mn, shape=[R, Cc])
+        ms = time_op(torch, head, lambda i: hip.quantize_rows(qt, src[i], 1, Cc, Cc, q[i], R, Cc), n, warmup,
+                     max(steps, 50))
+        out[f"{name}_quantize_f16"] = op_entry(per_q, ms, shape=[R, Cc])
+        ms = time_op(torch, head, lambda i: hip.dequantize(qt, q[i], deq[i], 0, R * Cc), n, warmup, max(steps, 50))
+        out[f"{name}_dequantize_f32"] = op_entry(per_d, ms, shape=[R, Cc])
         del src, q, deq
         torch.cuda.empty_cache()
     return out
@@ -366,6 +385,66 @@ def cpu_ops_baselines():
     return res
 
 
+def traffic_probe(torch, hip, binding, dev) -> None:
+    """One launch of each hot-path kernel at its config shape plus a plain
+    256 MiB device-to-device copy (the calibration kernel of known size), for
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes. Prints the launch order."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    order = []
+    src = torch.randn(64 << 20, generator=g, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    order.append(("copy_256MiB", 2 * src.numel() * 4))
+    for C, T in ((128, 483840), (128, 48000)):
+        x = torch.randn((C, T), generator=g, device=dev)
+        a = torch.rand(C, generator=g, device=dev) - 0.5
+        y = torch.empty_like(x)
+        hip.snake_beta(x, a, a, y)
+        order.append((f"snake_beta_{C}x{T}", snake_bytes(C, T)))
+    rows, D = 756, 2048
+    xh = torch.randn((rows, D), generator=g, device=dev).half()
+    dh = torch.randn((rows, D), generator=g, device=dev).half()
+    w = torch.ones(D, device=dev).half()
+    hh, yh = torch.empty_like(xh), torch.empty_like(xh)
+    hip.rms_norm(1, xh, dh, w, 1, hh, yh, rows, D, 1e-6)
+    order.append(("rmsnorm_f16_756x2048", 8 * rows * D + 2 * D))
+    hip.layer_norm(1, xh, dh, w, w, 1, hh, yh, rows, D, 1e-6)
+    order.append(("layernorm_f16_756x2048", 8 * rows * D + 4 * D))
+    n = 64 * 2520
+    st, vu, vc = (torch.randn(n, generator=g, device=dev) for _ in range(3))
+    hip.flow_cfg_euler(st, vu, vc, n, 1.5, 0.02)
+    order.append(("flow_cfg_euler_64x2520", 16 * n))
+    R, Cc = 4096, 1536
+    wq = (torch.randn((R, Cc), generator=g, device=dev) * 0.02).half()
+    q = torch.empty(R * Cc // 32 * 34, dtype=torch.uint8, device=dev)
+    hip.quantize_rows(8, wq, 1, Cc, Cc, q, R, Cc)
+    order.append(("q8_0_quantize_f16", 2 * R * Cc + q.numel()))
+    deq = torch.empty((R, Cc), device=dev)
+    hip.dequantize(8, q, deq, 0, R * Cc)
+    order.append(("q8_0_dequantize_f32", q.numel() + 4 * R * Cc))
+    P, S, V = 750, 3, 16384
+    c = torch.randn((P * S, V), generator=g, device=dev) * 3
+    u = torch.randn((P * S, V), generator=g, device=dev) * 3
+    out_i = torch.empty((P * S, 64), dtype=torch.int32, device=dev)
+    out_f = torch.empty((P * S, 64), device=dev)
+    small_i = torch.empty((2, P * S), dtype=torch.int32, device=dev)
+    small_f = torch.empty((2, P * S), device=dev)
+    a = binding.SampleArgs()
+    a.cond, a.uncond, a.rows, a.vocab, a.row_pitch = c.data_ptr(), u.data_ptr(), P * S, V, V
+    a.cfg_scale, a.temperature, a.n_streams = 1.5, 0.9, 3
+    for k in range(3):
+        a.top_k[k] = 50
+    a.best, a.count = small_i[0].data_ptr(), small_i[1].data_ptr()
+    a.cand_ids, a.cand_probs, a.capacity = out_i.data_ptr(), out_f.data_ptr(), 64
+    a.row_max, a.row_lse = small_f[0].data_ptr(), small_f[1].data_ptr()
+    hip.cfg_sample(a)
+    order.append(("cfg_softmax_top50_750x3x16384", 2 * P * S * V * 4 + P * S * 416))
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_probe_launch_order": order}))
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -373,6 +452,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-ops", action="store_true", help="only the headline ladder")
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="one launch per kernel + a 256 MiB copy, for rocprofv3 --pmc runs")
     args = p.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -388,9 +469,13 @@ def main() -> int:
     hip = binding.LevoHip()
     dev = torch.device("cuda:0")
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.traffic_probe:
+        traffic_probe(torch, hip, binding, dev)
+        return 0
 
+    head = HeadStart(torch)
     log("ladder: start")
-    lad = bench_ladder(torch, hip, dev, args.warmup, args.steps)
+    lad = bench_ladder(torch, hip, head, dev, args.warmup, args.steps)
     log(f"ladder: {lad['ms_per_step']:.4f} ms/step")
     (C, T), dom_ms = lad["dominant"]
     dom_bytes = snake_bytes(C, T)
@@ -411,17 +496,18 @@ def main() -> int:
     ops = {"snake_beta_ladder_shapes": lad["per_shape"]}
     if not args.no_ops:
         log("ops: snake 1 s")
-        ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, dev, args.warmup, args.steps)
+        ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: flow")
-        ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, dev, args.warmup, args.steps)
+        ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, args.warmup, args.steps)
         for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
             for rows, D in ((756, 2048), (756, 1536), (1, 2048), (2, 2048)):
                 log(f"ops: {name} {rows}x{D}")
-                ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, dev, args.warmup, args.steps, layer, rows, D)
+                ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, args.warmup, args.steps,
+                                                                    layer, rows, D)
         log("ops: cfg sample")
-        ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, dev, args.warmup, args.steps)
+        ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup, args.steps)
         log("ops: quant")
-        ops.update(bench_quant(torch, hip, dev, args.warmup, args.steps))
+        ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
 
     cpu = None
     if not args.no_cpu:

@@ -177,7 +177,8 @@ int64_t levo_hip_row_size(levo_hip_type type, int64_t n_per_row);
  * imatrix) as called at tools/levo-quantize.cpp:386-388 (ggml's
  * quantize_row_q8_0_ref / quantize_row_q4_0_ref). Returns the bytes written
  * (nrows * row size) or a negative levo_hip_status. Q8_0 ignores imatrix as
- * ggml does; Q4_0 requires imatrix == NULL. */
+ * ggml does; Q4_0 requires imatrix == NULL. dst needs 2-byte alignment
+ * (16-byte aligned destinations take the dwordx4 store path). */
 int64_t levo_hip_quantize_chunk(levo_hip_type type, const float * src, void * dst,
                                 int64_t start, int64_t nrows, int64_t n_per_row,
                                 const float * imatrix, levo_hip_stream_t stream);

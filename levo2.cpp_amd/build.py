@@ -30,12 +30,16 @@ ARCH = "gfx950"
 # -ffp-contract=off: a*b+c rounds twice, as in the reference's ISO C++17 x86-64
 # build; FMAs are written explicitly where the algorithm wants one.
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation.
+# -fma-mix-insts: no v_fma_mix{lo,hi}_f16, which would fold f16(a*b) into one
+# mixed-precision FMA whose F16-subnormal results differ from the
+# round-to-F32-then-F16 chain the reference computes.
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
     "-Wall", "-Wextra", "-Wno-unused-parameter",
     "-I", INCLUDE, "-I", CSRC,
 ]
-DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-Xclang", "-target-feature", "-Xclang", "-fma-mix-insts"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -43,6 +47,7 @@ def _run(cmd: list[str]) -> None:
     out = "\n".join(
         line for line in (r.stdout + r.stderr).splitlines()
         if "unknown target feature" not in line and "packed-fp32-ops" not in line
+        and "fma-mix-insts" not in line
         and "argument unused during compilation: '--hip-link'" not in line
     )
     if r.returncode != 0:

@@ -86,7 +86,7 @@ __device__ __forceinline__ void lds_put16(uint8_t * lds, int off, uint32_t v16) 
 template <int QT, typename S, bool kVec>
 __global__ __launch_bounds__(kThreads) void quantize_kernel(const S * __restrict__ src, int64_t src_cols,
                                                             int64_t src_stride, uint8_t * __restrict__ dst,
-                                                            int64_t nblocks_row, int64_t nblocks) {
+                                                            int64_t nblocks_row, int64_t nblocks, bool dst_vec) {
     constexpr bool kF16 = std::is_same<S, uint16_t>::value;
     constexpr int N = kF16 ? 8 : 4;           // values per lane
     constexpr int LPB = 32 / N;               // lanes per block
@@ -177,14 +177,15 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const S * __restrict
     }
     __syncthreads();
 
-    // write the group: dwordx4 when the whole group is valid, u16 otherwise
+    // write the group: dwordx4 when the whole group is valid and dst is
+    // 16-byte aligned (groups start at multiples of 16 bytes), u16 otherwise
     uint8_t * out = dst + b0 * QB;
     const int64_t nvalid = nblocks - b0;
-    if (nvalid >= BPW) {
+    if (nvalid >= BPW && dst_vec) {
         if (lane < GB / 16)
             reinterpret_cast<u32x4 *>(out)[lane] = reinterpret_cast<const u32x4 *>(lds)[lane];
     } else if (nvalid > 0) {
-        const int nbytes = static_cast<int>(nvalid) * QB;
+        const int nbytes = static_cast<int>(nvalid < BPW ? nvalid : BPW) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)
             reinterpret_cast<uint16_t *>(out)[i] = reinterpret_cast<const uint16_t *>(lds)[i];
     }
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const S * __restrict
 // stages it in LDS, and each lane expands 8 values of one block.
 template <int QT, typename D>
 __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t * __restrict__ src, D * __restrict__ dst,
-                                                              int64_t nblocks) {
+                                                              int64_t nblocks, bool src_vec, bool dst_vec) {
     constexpr int QB = qtraits<QT>::bytes;
     constexpr int BPW = 16;
     constexpr int GB = BPW * QB;
@@ -206,11 +207,11 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t * __
     const int64_t nvalid = nblocks - b0;
     uint8_t * lds = stage[wave];
     const uint8_t * in = src + b0 * QB;
-    if (nvalid >= BPW) {
+    if (nvalid >= BPW && src_vec) {
         if (lane < GB / 16)
             reinterpret_cast<u32x4 *>(lds)[lane] = reinterpret_cast<const u32x4 *>(in)[lane];
     } else if (nvalid > 0) {
-        const int nbytes = static_cast<int>(nvalid) * QB;
+        const int nbytes = static_cast<int>(nvalid < BPW ? nvalid : BPW) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)
             reinterpret_cast<uint16_t *>(lds)[i] = reinterpret_cast<const uint16_t *>(in)[i];
     }
@@ -241,7 +242,13 @@ __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t * __
     // output values of this lane: block (b0+bi), values part*8 .. part*8+7
     // (Q4_0 part p holds values 8p..8p+7 too: parts 0,1 low nibbles, 2,3 high)
     const int64_t e0 = (b0 + bi) * 32 + part * 8;
-    if constexpr (std::is_same<D, float>::value) {
+    if (!dst_vec) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if constexpr (std::is_same<D, float>::value) dst[e0 + k] = y[k];
+            else dst[e0 + k] = f2h(y[k]);
+        }
+    } else if constexpr (std::is_same<D, float>::value) {
         f32x4 a, b;
         a.x = y[0]; a.y = y[1]; a.z = y[2]; a.w = y[3];
         b.x = y[4]; b.y = y[5]; b.z = y[6]; b.w = y[7];
@@ -270,17 +277,14 @@ int launch_quant(const void * src, int64_t src_cols, int64_t src_stride, void * 
     const int64_t nblocks = nrows * nb_row;
     const int64_t groups = ceil_div(nblocks, BPW);
     const int64_t grid = ceil_div(groups, kWaves);
-    const bool vec = src_cols % N == 0 && src_stride % N == 0 && aligned16(src) && aligned16(dst);
+    const bool vec = src_cols % N == 0 && src_stride % N == 0 && aligned16(src);
     const S * s = static_cast<const S *>(src);
     uint8_t * d = static_cast<uint8_t *>(dst);
-    if (!aligned16(dst)) {
-        set_error("quantize: destination must be 16-byte aligned");
-        return LEVO_HIP_ERR_INVALID;
-    }
+    const bool dst_vec = aligned16(dst);
     if (vec)
-        quantize_kernel<QT, S, true><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks);
+        quantize_kernel<QT, S, true><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dst_vec);
     else
-        quantize_kernel<QT, S, false><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks);
+        quantize_kernel<QT, S, false><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dst_vec);
     return launch_status("levo_hip_quantize");
 }
 
@@ -310,6 +314,9 @@ extern "C" int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, 
     const int64_t bytes = nrows * (dst_cols / 32) * block_bytes(type);
     if (bytes == 0) return 0;
     LEVO_REQUIRE(src != nullptr && dst != nullptr, "quantize: null pointer");
+    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(dst) & 1u) == 0, "quantize: destination must be 2-byte aligned");
+    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(src) & (src_type == LEVO_HIP_TYPE_F16 ? 1u : 3u)) == 0,
+                 "quantize: source is not aligned to its element size");
     const hipStream_t st = as_hip(stream);
     int r;
     if (type == LEVO_HIP_TYPE_Q8_0) {
@@ -348,21 +355,25 @@ extern "C" int levo_hip_dequantize(levo_hip_type type, const void * src, void * 
     LEVO_REQUIRE(k >= 0 && k % 32 == 0, "dequantize: k must be a multiple of 32");
     if (k == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(src != nullptr && dst != nullptr, "dequantize: null pointer");
-    LEVO_REQUIRE(aligned16(src) && aligned16(dst), "dequantize: buffers must be 16-byte aligned");
+    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(src) & 1u) == 0, "dequantize: source must be 2-byte aligned");
+    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(dst) & (dst_type == LEVO_HIP_TYPE_F16 ? 1u : 3u)) == 0,
+                 "dequantize: destination is not aligned to its element size");
+    const bool src_vec = aligned16(src);
+    const bool dst_vec = aligned16(dst);
     const int64_t nblocks = k / 32;
     const int64_t grid = ceil_div(ceil_div(nblocks, 16), kWaves);
     const hipStream_t st = as_hip(stream);
     const uint8_t * s = static_cast<const uint8_t *>(src);
     if (type == LEVO_HIP_TYPE_Q8_0) {
         if (dst_type == LEVO_HIP_TYPE_F32)
-            dequantize_kernel<LEVO_HIP_TYPE_Q8_0, float><<<grid, kThreads, 0, st>>>(s, static_cast<float *>(dst), nblocks);
+            dequantize_kernel<LEVO_HIP_TYPE_Q8_0, float><<<grid, kThreads, 0, st>>>(s, static_cast<float *>(dst), nblocks, src_vec, dst_vec);
         else
-            dequantize_kernel<LEVO_HIP_TYPE_Q8_0, uint16_t><<<grid, kThreads, 0, st>>>(s, static_cast<uint16_t *>(dst), nblocks);
+            dequantize_kernel<LEVO_HIP_TYPE_Q8_0, uint16_t><<<grid, kThreads, 0, st>>>(s, static_cast<uint16_t *>(dst), nblocks, src_vec, dst_vec);
     } else {
         if (dst_type == LEVO_HIP_TYPE_F32)
-            dequantize_kernel<LEVO_HIP_TYPE_Q4_0, float><<<grid, kThreads, 0, st>>>(s, static_cast<float *>(dst), nblocks);
+            dequantize_kernel<LEVO_HIP_TYPE_Q4_0, float><<<grid, kThreads, 0, st>>>(s, static_cast<float *>(dst), nblocks, src_vec, dst_vec);
         else
-            dequantize_kernel<LEVO_HIP_TYPE_Q4_0, uint16_t><<<grid, kThreads, 0, st>>>(s, static_cast<uint16_t *>(dst), nblocks);
+            dequantize_kernel<LEVO_HIP_TYPE_Q4_0, uint16_t><<<grid, kThreads, 0, st>>>(s, static_cast<uint16_t *>(dst), nblocks, src_vec, dst_vec);
     }
     return launch_status("levo_hip_dequantize");
 }

@@ -116,3 +116,30 @@ def test_rms_f32_with_f16_weight(hip, dev, oracle):
     hip.rms_norm(0, xd, dd, to_dev(w16.view(np.int16), dev), 1, None, yd, rows, D, 1e-5)
     _, yw = oracle.rms_norm(x, d, oracle.f16_to_f32(w16), 1e-5)
     assert f32_err(from_dev(yd), yw) <= 1e-5
+
+
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+def test_f16_subnormal_results_follow_the_f32_then_f16_chain(hip, dev, oracle, layer):
+    """Rows whose normalised values land in the F16 subnormal range: h * scale
+    is rounded to F32 and then to F16 (src/levo-kv.cpp:157-159), never fused."""
+    rows, D = 64, 2048
+    half = oracle.gaussian(rows * D // 2, 31).reshape(rows, D // 2)
+    half[:, :512] = np.geomspace(6e-8, 6e-5, 512).astype(np.float32) * np.where(np.arange(512) % 2, 1, -1)
+    half = oracle.f16_to_f32(oracle.f32_to_f16(half))
+    # +v / -v pairs of F16 values: the row mean is exactly 0 in any summation
+    # order, so LayerNorm also keeps the tiny values tiny
+    x = np.concatenate([half, -half], axis=1)
+    xh = oracle.f32_to_f16(x)
+    dh = oracle.f32_to_f16(np.zeros_like(x))
+    w = oracle.f32_to_f16(oracle.gaussian(D, 32) * 0.02 + 1)
+    b = oracle.f32_to_f16(np.zeros(D, np.float32))
+    h, y = _run(hip, dev, layer, xh, dh, w, b, 1e-6)
+    if layer:
+        hw, yw = oracle.layer_norm(xh, dh, w, b, 1e-6)
+    else:
+        hw, yw = oracle.rms_norm(xh, dh, w, 1e-6)
+    assert np.array_equal(h, hw)
+    sub = (yw & 0x7C00) == 0
+    assert np.count_nonzero(sub) > 1000
+    print(f"differing elements: {np.count_nonzero(y != yw)}")
+    assert f16_ulp(y, yw) <= 1

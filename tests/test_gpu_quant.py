@@ -127,3 +127,24 @@ def test_reference_padded_q8_product(hip, dev):
     inp = np.zeros(32, np.float32)
     inp[:6] = [0.25, -0.5, 0.75, -1.0, 1.25, -1.5]
     assert np.all(np.abs(deq @ inp - m @ inp) < 0.015)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+def test_unaligned_buffers(hip, dev, oracle, qt):
+    """ggml_quantize_chunk with start > 0 writes at start_row * row_size: 2-byte aligned only."""
+    import torch
+    nblocks = 1000
+    x = (oracle.gaussian(nblocks * 32, 2100) * 0.1).reshape(nblocks, 32)
+    want = oracle.quantize(qt, x)
+    buf = torch.zeros(nblocks * BB[qt] + 16, dtype=torch.uint8, device=dev)
+    hip.quantize_chunk(qt, to_dev(x, dev), buf[2:], 0, nblocks, 32)
+    got = from_dev(buf)
+    assert np.array_equal(got[2: 2 + nblocks * BB[qt]], want)
+    assert np.all(got[:2] == 0) and np.all(got[2 + nblocks * BB[qt]:] == 0)
+    src = torch.zeros(want.size + 16, dtype=torch.uint8, device=dev)
+    src[6: 6 + want.size] = to_dev(want, dev)
+    y = torch.full((nblocks * 32 + 8,), 5.0, dtype=torch.float32, device=dev)
+    hip.dequantize(qt, src[6:], y[1:], 0, nblocks * 32)
+    yd = from_dev(y)
+    assert np.array_equal(yd[1: 1 + nblocks * 32], oracle.dequantize(qt, want, nblocks * 32))
+    assert yd[0] == 5.0 and np.all(yd[1 + nblocks * 32:] == 5.0)

@@ -142,9 +142,13 @@ def test_vocab_16385_packed_rows(hip, binding, dev, oracle):
     pad = np.zeros((R, 16388), np.float32)
     padu = np.zeros((R, 16388), np.float32)
     pad[:, :V], padu[:, :V] = cond, uncond
-    out2 = run_sample(hip, binding, dev, pad, padu, top_k=[50, 1, 1], n_streams=3, vocab=V)
-    for key in ("best", "count", "ids", "logits", "max"):
+    out2 = run_sample(hip, binding, dev, pad, padu, top_k=[50, 1, 1], n_streams=3, vocab=V, pitch=16388)
+    for key in ("best", "count", "max"):
         assert np.array_equal(out[key], out2[key])
+    for r in range(R):
+        n = out["count"][r]
+        assert np.array_equal(out["ids"][r, :n], out2["ids"][r, :n])
+        assert np.array_equal(out["logits"][r, :n].view(np.uint32), out2["logits"][r, :n].view(np.uint32))
 
 
 @pytest.mark.parametrize("V", [1, 3, 4, 100, 1000, 5000])
