@@ -452,6 +452,9 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-ops", action="store_true", help="only the headline ladder")
+    p.add_argument("--only", default="",
+                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant); "
+                        "prints the op table without the headline ladder")
     p.add_argument("--traffic-probe", action="store_true",
                    help="one launch per kernel + a 256 MiB copy, for rocprofv3 --pmc runs")
     args = p.parse_args()
@@ -474,6 +477,25 @@ def main() -> int:
         return 0
 
     head = HeadStart(torch)
+    if args.only:
+        groups = set(args.only.split(","))
+        ops = {}
+        if "snake" in groups:
+            ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
+        if "flow" in groups:
+            ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, args.warmup, args.steps)
+        if "norm" in groups:
+            for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
+                for rows, D in ((756, 2048), (1, 2048)):
+                    ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, args.warmup,
+                                                                        args.steps, layer, rows, D)
+        if "sample" in groups:
+            ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup,
+                                                                args.steps)
+        if "quant" in groups:
+            ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
+        print(json.dumps({"ops": ops}))
+        return 0
     log("ladder: start")
     lad = bench_ladder(torch, hip, head, dev, args.warmup, args.steps)
     log(f"ladder: {lad['ms_per_step']:.4f} ms/step")

@@ -2,24 +2,32 @@
 //
 // One workgroup (4 wave64s) per logit row. The row is read once from HBM
 // (cond and uncond, dwordx4), combined l = u + s*(c - u) in registers and
-// never written back: everything the sampler needs is produced from the
-// register-resident row:
-//   1. unique-token repetition penalty and stream-0 ignore list via LDS
-//      bitmaps (src/levo-sampling.cpp:39-47, :137-147);
-//   2. NaN rejection and the first maximum (std::max_element, :94-96);
-//   3. the exact top-k threshold of the stable descending sort (:84-93):
-//      each wave finds the k-th largest of its 64 lane maxima with a ballot
-//      bisection (a lower bound of the row's k-th value), the workgroup keeps
-//      only the few elements above the largest such bound, and one wave
-//      bisects their order-preserving keys to the exact k-th value;
-//   4. every id >= that value, in ascending id order (ties with the k-th
-//      value kept, as the reference keeps them), with its logit and its
-//      probability exp((l - max)/T) / sum (:98-107, weights in double);
-//   5. optionally the full-vocabulary log-sum-exp of l/T.
+// never written back. Everything the sampler needs comes from the
+// register-resident row, touching each value only with cheap compares:
+//   A. unique-token repetition penalty and stream-0 ignore list via LDS
+//      bitmaps (src/levo-sampling.cpp:39-47, :137-147); NaN check and the
+//      row maximum;
+//   B. a lower bound of the k-th largest value: each wave bisects the
+//      order-preserving keys of its 64 lane maxima with ballots (no barrier)
+//      for its ceil(k/4)-th largest; at least k ids lie at or above the
+//      smallest of the four bounds;
+//   C. the first maximum (std::max_element, :94-96), the optional
+//      full-vocabulary log-sum-exp of l/T, and a gather of the few ids at or
+//      above the bound (value and id) into per-wave LDS segments; the row's
+//      registers are dead after this point;
+//   D. the exact k-th value of the stable descending sort (:84-89): one wave
+//      bisects the gathered keys (starting below the common high bits of the
+//      bound and the maximum);
+//   E. every gathered id >= that value (ties kept, as the reference keeps
+//      them) is marked in an LDS bitmap; a popcount prefix scan over the
+//      bitmap gives each candidate its slot in ascending id order, and its
+//      logit and probability exp((l - max)/T) / sum (:98-107; F32 weights,
+//      double sum) are written there.
+// k == 0 (keep all), k > 256, or more tied candidates than the segments hold
+// take select_general, which re-reads the row instead of holding it.
 // The host keeps the mt19937_64 draw, so the sampled token is the reference's.
 #include "common.hpp"
 
-#include <cfloat>
 #include <climits>
 
 namespace levo_hip {
@@ -27,45 +35,221 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kCandCap = 1024;    // LDS slots for threshold candidates
+constexpr int kSegCap = 256;   // gathered candidates per wave segment
+constexpr int kBisCap = 256;   // candidates the one-wave bisection holds (4 per lane)
 constexpr int kMaxVocab = 32768;
-constexpr int kBitmapWords = kMaxVocab / 32;
+
+__device__ __forceinline__ float float_of_key(uint32_t k) {
+    return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
 
 // k-th largest (1 <= k <= 64) of the 64 lane keys of this wave.
 __device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, int k) {
     uint32_t prefix = 0;
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = prefix | (1u << bit);
-        const int cnt = __popcll(__ballot(key >= cand));
-        if (cnt >= k) prefix = cand;
+        if (static_cast<int>(__popcll(__ballot(key >= cand))) >= k) prefix = cand;
     }
     return prefix;
 }
 
-__device__ __forceinline__ double cand_weight(float v, float m, float t) {
-    if (__builtin_isinf(v) && v < 0.0f) return 0.0;
-    return exp(static_cast<double>((v - m) / t));
+// exp((l - max) / T) for the F32 probability output; -inf logits give 0.
+__device__ __forceinline__ float cand_weight(float v, float m, float inv_t) {
+    return __expf((v - m) * inv_t);
+}
+
+// l = u + s * (c - u) for every id this thread owns: id of item i is
+// (i / VEC) * 256 * VEC + tid * VEC + i % VEC.
+template <int VEC, int NCH, bool kCfg>
+__device__ __forceinline__ void load_row(float (&v)[VEC * NCH], const float * __restrict__ crow,
+                                         const float * __restrict__ urow, int V, int tid, float s) {
+    constexpr int kChunk = kThreads * VEC;
+    if constexpr (VEC == 4) {
+        f32x4 c[NCH], u[NCH];
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            const int base = ch * kChunk + tid * 4;
+            const int off = base < V ? base : 0;  // row_pitch % 4 == 0: in bounds
+            c[ch] = *reinterpret_cast<const f32x4 *>(crow + off);
+            if constexpr (kCfg) u[ch] = *reinterpret_cast<const f32x4 *>(urow + off);
+        }
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            const int base = ch * kChunk + tid * 4;
+            float r[4] = {c[ch].x, c[ch].y, c[ch].z, c[ch].w};
+            if constexpr (kCfg) {
+                const float w[4] = {u[ch].x, u[ch].y, u[ch].z, u[ch].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) r[q] = w[q] + s * (r[q] - w[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[ch * 4 + q] = base + q < V ? r[q] : -INFINITY;
+        }
+    } else {
+        float c[NCH], u[NCH];
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            const int base = ch * kChunk + tid;
+            const int off = base < V ? base : 0;
+            c[ch] = crow[off];
+            if constexpr (kCfg) u[ch] = urow[off];
+        }
+#pragma unroll
+        for (int ch = 0; ch < NCH; ++ch) {
+            const int base = ch * kChunk + tid;
+            const float r = kCfg ? u[ch] + s * (c[ch] - u[ch]) : c[ch];
+            v[ch] = base < V ? r : -INFINITY;
+        }
+    }
+}
+
+// Shared-memory layout of one row's workgroup.
+template <int kWords>
+struct row_lds {
+    uint32_t sel[kWords];     // selected-id bitmap
+    uint32_t prefix[kWords];  // exclusive popcount prefix per bitmap word
+    uint32_t pen[kWords];     // repetition-penalty ids
+    uint32_t ign[kWords];     // ignored ids (stream 0)
+    float cv[kWaves][kSegCap];  // gathered candidate values, one segment per wave
+    int ci[kWaves][kSegCap];    // and their ids
+    float wmax[kWaves];
+    float wlow[kWaves];
+    int wnan[kWaves];
+    int wbest[kWaves];
+    int wcnt[kWaves];
+    float wlse[kWaves];
+    double wz[kWaves];
+    int bis[2][kWaves];
+    uint32_t tau;
+    int total;
+};
+
+template <int kWords>
+__device__ __forceinline__ float adjusted_logit(const levo_hip_sample_args & a, const row_lds<kWords> & L,
+                                                const float * crow, const float * urow, bool pen, bool ign,
+                                                int idx) {
+    const float c = crow[idx];
+    float v = urow ? urow[idx] + a.cfg_scale * (c - urow[idx]) : c;
+    const uint32_t bit = 1u << (idx & 31);
+    if (pen && (L.pen[idx >> 5] & bit)) v = v / a.repetition_penalty;
+    if (ign && (L.ign[idx >> 5] & bit)) v = -INFINITY;
+    return v;
+}
+
+// Exclusive prefix of the bitmap popcounts (wave 0), total candidate count.
+template <int kWords>
+__device__ __forceinline__ void bitmap_prefix(row_lds<kWords> & L, int words) {
+    constexpr int kWPL = (kWords + 63) / 64;  // words per lane
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {
+        int cnt[kWPL];
+        int local = 0;
+#pragma unroll
+        for (int j = 0; j < kWPL; ++j) {
+            const int w = lane * kWPL + j;
+            cnt[j] = w < words ? __popc(L.sel[w]) : 0;
+            local += cnt[j];
+        }
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        int run = incl - local;
+#pragma unroll
+        for (int j = 0; j < kWPL; ++j) {
+            const int w = lane * kWPL + j;
+            if (w < words) L.prefix[w] = static_cast<uint32_t>(run);
+            run += cnt[j];
+        }
+        if (lane == 63) L.total = incl;
+    }
+}
+
+// Slot of a selected id in ascending id order.
+template <int kWords>
+__device__ __forceinline__ int slot_of(const row_lds<kWords> & L, int idx) {
+    const uint32_t below = (1u << (idx & 31)) - 1u;
+    return static_cast<int>(L.prefix[idx >> 5]) + __popc(L.sel[idx >> 5] & below);
+}
+
+__device__ __forceinline__ void write_candidate(const levo_hip_sample_args & a, int64_t row, int pos, int idx, float v,
+                                                int best, float m, float inv_t, bool z_ok, float inv_z) {
+    if (pos >= a.capacity) return;
+    const int64_t o = row * a.capacity + pos;
+    a.cand_ids[o] = idx;
+    if (a.cand_logits) a.cand_logits[o] = v;
+    if (a.cand_probs) {
+        float p;
+        if (z_ok) p = cand_weight(v, m, inv_t) * inv_z;
+        else p = idx == best ? 1.0f : 0.0f;  // the reference falls back to best
+        a.cand_probs[o] = p;
+    }
+}
+
+// General selection (k == 0 keeps every id, k > 64, or more tied candidates
+// than the gather segments hold): loops over the row again from L2/HBM with
+// a block-wide bisection per key bit. Rare; kept out of line so that it does
+// not add register pressure to the common path.
+template <int kWords>
+__device__ __noinline__ void select_general(const levo_hip_sample_args a, row_lds<kWords> & L, int64_t row,
+                                            int V, int k, float m, int best, bool pen, bool ign) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float * crow = a.cond + row * a.row_pitch;
+    const float * urow = a.uncond ? a.uncond + row * a.row_pitch : nullptr;
+    uint32_t tau = 0u;  // k == 0: every valid (non-NaN) id
+    if (k == 1) {
+        tau = float_key(m);
+    } else if (k > 1) {
+        int buf = 0;
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t cand = tau | (1u << bit);
+            int cnt = 0;
+            for (int idx = tid; idx < V; idx += kThreads)
+                cnt += float_key(adjusted_logit(a, L, crow, urow, pen, ign, idx)) >= cand ? 1 : 0;
+            cnt = wave_sum_i32(cnt);
+            if (lane == 0) L.bis[buf][wave] = cnt;
+            __syncthreads();
+            int total = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) total += L.bis[buf][w];
+            if (total >= k) tau = cand;
+            buf ^= 1;
+        }
+    }
+    const bool want_probs = a.cand_probs != nullptr;
+    const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
+    double z = 0.0;
+    for (int idx = tid; idx < V; idx += kThreads) {
+        const float v = adjusted_logit(a, L, crow, urow, pen, ign, idx);
+        if (float_key(v) >= tau) {
+            atomicOr(&L.sel[idx >> 5], 1u << (idx & 31));
+            if (want_probs) z += static_cast<double>(cand_weight(v, m, inv_t));
+        }
+    }
+    z = wave_sum_f64(z);
+    if (lane == 0) L.wz[wave] = z;
+    __syncthreads();
+    bitmap_prefix(L, (V + 31) / 32);
+    z = 0.0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) z += L.wz[w];
+    const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+    const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
+    __syncthreads();
+    for (int idx = tid; idx < V; idx += kThreads) {
+        const float v = adjusted_logit(a, L, crow, urow, pen, ign, idx);
+        if (float_key(v) >= tau) write_candidate(a, row, slot_of(L, idx), idx, v, best, m, inv_t, z_ok, inv_z);
+    }
 }
 
 template <int VEC, int NCH>
 __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sample_args a) {
     constexpr int ITEMS = VEC * NCH;
-    constexpr int kChunk = kThreads * VEC;            // ids per chunk
-    constexpr int kCPL = (NCH + 63) / 64;             // chunks per lane in the chunk scan
-
-    __shared__ uint32_t s_pen[kBitmapWords];
-    __shared__ uint32_t s_ign[kBitmapWords];
-    __shared__ uint32_t s_cand[kCandCap];
-    __shared__ int s_chunk_count[NCH][kWaves];
-    __shared__ float s_wmax[kWaves];
-    __shared__ int s_widx[kWaves];
-    __shared__ int s_wnan[kWaves];
-    __shared__ uint32_t s_wlow[kWaves];
-    __shared__ double s_wz[kWaves];
-    __shared__ float s_wlse[kWaves];
-    __shared__ int s_bis[2][kWaves];
-    __shared__ int s_ncand;
-    __shared__ uint32_t s_tau;
+    constexpr int kChunk = kThreads * VEC;                // ids per chunk
+    constexpr int kWords = (ITEMS * kThreads + 31) / 32;  // bitmap words covering the row
+    __shared__ row_lds<kWords> L;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -75,56 +259,23 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
     const int stream = static_cast<int>(row % a.n_streams);
     int k = a.top_k[stream];
     if (k <= 0 || k >= V) k = 0;  // keep every id
+    const int words = (V + 31) / 32;
 
-    // ---- 1. load + CFG ------------------------------------------------------
+    // ---- A. load + CFG -------------------------------------------------------
+    // All loads of the row are issued before any is consumed (no branch between
+    // them: ids past V read a clamped, valid address and are masked to -inf).
     float v[ITEMS];
     const float * crow = a.cond + row * a.row_pitch;
-    const float * urow = a.uncond ? a.uncond + row * a.row_pitch : nullptr;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        const int base = ch * kChunk + tid * VEC;
-        if constexpr (VEC == 4) {
-            // pitch % 4 == 0, so a vector starting below V lies inside the row
-            // pitch; its ids >= V are masked to -inf here and by idx < V below.
-            if (base < V) {
-                const f32x4 c = *reinterpret_cast<const f32x4 *>(crow + base);
-                if (urow) {
-                    const f32x4 u = *reinterpret_cast<const f32x4 *>(urow + base);
-                    v[ch * 4 + 0] = u.x + a.cfg_scale * (c.x - u.x);
-                    v[ch * 4 + 1] = u.y + a.cfg_scale * (c.y - u.y);
-                    v[ch * 4 + 2] = u.z + a.cfg_scale * (c.z - u.z);
-                    v[ch * 4 + 3] = u.w + a.cfg_scale * (c.w - u.w);
-                } else {
-                    v[ch * 4 + 0] = c.x;
-                    v[ch * 4 + 1] = c.y;
-                    v[ch * 4 + 2] = c.z;
-                    v[ch * 4 + 3] = c.w;
-                }
-#pragma unroll
-                for (int q = 1; q < 4; ++q)
-                    if (base + q >= V) v[ch * 4 + q] = -INFINITY;
-            } else {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[ch * 4 + q] = -INFINITY;
-            }
-        } else {
-            if (base < V) {
-                const float c = crow[base];
-                v[ch] = urow ? urow[base] + a.cfg_scale * (c - urow[base]) : c;
-            } else {
-                v[ch] = -INFINITY;
-            }
-        }
-    }
+    if (a.uncond) load_row<VEC, NCH, true>(v, crow, a.uncond + row * a.row_pitch, V, tid, a.cfg_scale);
+    else load_row<VEC, NCH, false>(v, crow, crow, V, tid, a.cfg_scale);
+    for (int i = tid; i < words; i += kThreads) L.sel[i] = 0u;
 
-    // ---- 2. repetition penalty / ignore list ---------------------------------
     const bool use_pen = a.recent != nullptr && a.n_recent > 0;
     const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
     if (use_pen || use_ign) {  // uniform per workgroup
-        const int words = (V + 31) / 32;
         for (int i = tid; i < words; i += kThreads) {
-            s_pen[i] = 0u;
-            s_ign[i] = 0u;
+            L.pen[i] = 0u;
+            L.ign[i] = 0u;
         }
         __syncthreads();
         if (use_pen) {
@@ -132,13 +283,13 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
             const int64_t * rec = a.recent + row * a.n_recent;
             for (int i = tid; i < a.n_recent; i += kThreads) {
                 const int64_t t = rec[i];
-                if (t >= 0 && t < limit) atomicOr(&s_pen[t >> 5], 1u << (t & 31));
+                if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
             }
         }
         if (use_ign) {
             for (int i = tid; i < a.n_ignore; i += kThreads) {
                 const int64_t t = a.ignore[i];
-                if (t >= 0 && t < V) atomicOr(&s_ign[t >> 5], 1u << (t & 31));
+                if (t >= 0 && t < V) atomicOr(&L.ign[t >> 5], 1u << (t & 31));
             }
         }
         __syncthreads();
@@ -147,66 +298,49 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
             const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
             if (idx < V) {
                 const uint32_t bit = 1u << (idx & 31);
-                if (s_pen[idx >> 5] & bit) v[i] = v[i] / a.repetition_penalty;
-                if (s_ign[idx >> 5] & bit) v[i] = -INFINITY;
+                if (L.pen[idx >> 5] & bit) v[i] = v[i] / a.repetition_penalty;
+                if (L.ign[idx >> 5] & bit) v[i] = -INFINITY;
             }
         }
     }
 
-    // ---- 3. NaN check, thread max / first argmax ----------------------------
+    // NaN check and thread maximum (fmaxf skips NaN; NaN is flagged separately)
+    const bool tvalid = tid * VEC < V;
     bool has_nan = false;
     float tmax = -INFINITY;
-    int targ = INT_MAX;
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) {
-        const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
-        if (idx < V) {
-            if (__builtin_isnan(v[i])) has_nan = true;
-            else if (targ == INT_MAX || v[i] > tmax) {
-                tmax = v[i];
-                targ = idx;
-            }
-        }
+        has_nan = has_nan || __builtin_isnan(v[i]);
+        tmax = fmaxf(tmax, v[i]);
     }
-    // wave reduction: larger value, ties -> smaller id
-    float wm = tmax;
-    int wi = targ;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float om = __shfl_xor(wm, o, 64);
-        const int oi = __shfl_xor(wi, o, 64);
-        if (oi != INT_MAX && (wi == INT_MAX || om > wm || (om == wm && oi < wi))) {
-            wm = om;
-            wi = oi;
-        }
-    }
-    const bool wave_nan = __ballot(has_nan) != 0;
-    // per-wave lower bound of the row's k-th largest value (k <= 64)
-    uint32_t wlow = 0;
-    if (k > 1 && k <= 64) wlow = wave_kth_key(targ == INT_MAX ? 0u : float_key(tmax), k);
-    if (lane == 0) {
-        s_wmax[wave] = wm;
-        s_widx[wave] = wi;
-        s_wnan[wave] = wave_nan ? 1 : 0;
-        s_wlow[wave] = wlow;
-    }
-    if (tid == 0) s_ncand = 0;
-    __syncthreads();
 
-    float m = s_wmax[0];
-    int best = s_widx[0];
-    bool row_nan = s_wnan[0] != 0;
-    uint32_t low = s_wlow[0];
+    // ---- B. wave maximum and the per-wave lower bound of the k-th value ----------
+    const float wm = wave_max_f32(tmax);
+    const bool wnan = __ballot(has_nan) != 0;
+    // Each wave bounds its own ceil(k/4)-th largest lane maximum; the row
+    // bound is the smallest of the four, so at least 4 * ceil(k/4) >= k ids
+    // lie at or above it (lanes without valid ids contribute key 0 = -inf).
+    const int kw = (k + kWaves - 1) / kWaves;
+    float wlow = -INFINITY;
+    if (k > 1 && kw <= 64) {
+        const uint32_t kk = wave_kth_key(tvalid ? float_key(tmax) : 0u, kw);
+        wlow = kk == 0u ? -INFINITY : float_of_key(kk);
+    }
+    if (lane == 0) {
+        L.wmax[wave] = wm;
+        L.wlow[wave] = wlow;
+        L.wnan[wave] = wnan ? 1 : 0;
+    }
+    __syncthreads();  // barrier 1
+
+    float m = L.wmax[0];
+    float low = L.wlow[0];
+    bool row_nan = L.wnan[0] != 0;
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
-        const float om = s_wmax[w];
-        const int oi = s_widx[w];
-        if (oi != INT_MAX && (best == INT_MAX || om > m || (om == m && oi < best))) {
-            m = om;
-            best = oi;
-        }
-        row_nan = row_nan || s_wnan[w] != 0;
-        low = max(low, s_wlow[w]);
+        m = fmaxf(m, L.wmax[w]);
+        low = fminf(low, L.wlow[w]);
+        row_nan = row_nan || L.wnan[w] != 0;
     }
     if (row_nan) {  // uniform: the reference throws "logits contain NaN"
         if (tid == 0) {
@@ -217,208 +351,161 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
         }
         return;
     }
+    if (k == 1) low = m;  // the candidates are the ties with the maximum
 
-    // ---- optional full-vocabulary log-sum-exp of l / T ----------------------
+    // ---- C. first maximum, log-sum-exp, candidate gather ---------------------------
+    // first id equal to the maximum; its own value is the reference's max_logit
+    // (std::max keeps the first of equal values, so a -0 / +0 tie keeps its sign)
+    int tbest = INT_MAX;
+    float tbest_v = m;
+    if (tvalid && tmax == m) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+            const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
+            if (tbest == INT_MAX && idx < V && v[i] == m) {
+                tbest = idx;
+                tbest_v = v[i];
+            }
+        }
+    }
+    const int my_best = tbest;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) tbest = min(tbest, __shfl_xor(tbest, o, 64));
+    if (lane == 0) L.wbest[wave] = tbest;
+
     if (a.row_lse) {
         float s = 0.0f;
         const float inv_t = 1.0f / a.temperature;
 #pragma unroll
+        for (int i = 0; i < ITEMS; ++i) s += __expf((v[i] - m) * inv_t);  // padding: exp(-inf) = 0
+        s = wave_sum_f32(s);
+        if (lane == 0) L.wlse[wave] = s;
+    }
+
+    // Gather the ids >= low into this wave's segment, in item order. The
+    // running count is wave-uniform, so slots need no atomics.
+    const bool gather = k >= 1 && kw <= 64;
+    if (gather) {
+        int base = 0;
+#pragma unroll
         for (int i = 0; i < ITEMS; ++i) {
             const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
-            if (idx < V) s += __expf((v[i] - m) * inv_t);
+            const bool p = idx < V && v[i] >= low;
+            const uint64_t mask = __ballot(p);
+            if (mask) {
+                const int pos = base + rank_in_mask(mask);
+                if (p && pos < kSegCap) {
+                    L.cv[wave][pos] = v[i];
+                    L.ci[wave][pos] = idx;
+                }
+                base += static_cast<int>(__popcll(mask));
+            }
         }
-        s = wave_sum_f32(s);
-        if (lane == 0) s_wlse[wave] = s;
+        if (lane == 0) L.wcnt[wave] = base;
     }
+    __syncthreads();  // barrier 2
 
-    // ---- 4. exact threshold key tau ------------------------------------------
-    uint32_t tau;
-    if (k == 0) {
-        tau = 0u;  // every valid id (all keys of non-NaN floats are > 0)
-    } else if (k == 1) {
-        tau = float_key(m);
+    int best = L.wbest[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) best = min(best, L.wbest[w]);
+    int seg_start[kWaves + 1];
+    seg_start[0] = 0;
+    bool fits = gather;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const int c = fits ? L.wcnt[w] : 0;
+        fits = fits && c <= kSegCap;
+        seg_start[w + 1] = seg_start[w] + c;
+    }
+    const int ncand = seg_start[kWaves];
+    fits = fits && ncand <= kBisCap;
+
+    if (!fits) {
+        select_general(a, L, row, V, k, m, best, use_pen, use_ign);
     } else {
-        bool done = false;
-        tau = 0u;
-        if (k <= 64) {
-            // gather the keys >= low (contains every id above the k-th value)
+        // ---- D. exact k-th value (key) among the gathered candidates -------------
+        uint32_t tau;
+        if (k == 1) {
+            tau = float_key(m);
+        } else {
+            if (wave == 0) {
+                uint32_t keys[kBisCap / 64];
 #pragma unroll
-            for (int i = 0; i < ITEMS; ++i) {
-                const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
-                const uint32_t key = float_key(v[i]);
-                const bool p = idx < V && key >= low;
-                const uint64_t mask = __ballot(p);
-                if (mask) {
-                    int base = 0;
-                    if (lane == 0) base = atomicAdd(&s_ncand, __popcll(mask));
-                    base = __builtin_amdgcn_readfirstlane(base);
-                    const int pos = base + rank_in_mask(mask);
-                    if (p && pos < kCandCap) s_cand[pos] = key;
-                }
-            }
-            __syncthreads();
-            const int c = s_ncand;
-            if (c <= kCandCap) {
-                if (wave == 0) {
-                    constexpr int kSlots = kCandCap / 64;
-                    uint32_t keys[kSlots];
+                for (int s = 0; s < kBisCap / 64; ++s) {
+                    const int j = lane + 64 * s;
+                    uint32_t key = 0u;
+                    if (j < ncand) {
+                        int w = 0;
 #pragma unroll
-                    for (int s = 0; s < kSlots; ++s) {
-                        const int p = lane + 64 * s;
-                        keys[s] = p < c ? s_cand[p] : 0u;
+                        for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
+                        key = float_key(L.cv[w][j - seg_start[w]]);
                     }
-                    const int nslots = (c + 63) / 64;
-                    uint32_t prefix = 0;
-                    for (int bit = 31; bit >= 0; --bit) {
-                        const uint32_t cand = prefix | (1u << bit);
-                        int cnt = 0;
-#pragma unroll
-                        for (int s = 0; s < kSlots; ++s)
-                            if (s < nslots) cnt += __popcll(__ballot(keys[s] >= cand));
-                        if (cnt >= k) prefix = cand;
-                    }
-                    if (lane == 0) s_tau = prefix;
+                    keys[s] = key;
                 }
-                __syncthreads();
-                tau = s_tau;
-                done = true;
-            }
-        }
-        if (!done) {
-            // general path: bisection over the whole register-resident row
-            uint32_t prefix = 0;
-            int buf = 0;
-            for (int bit = 31; bit >= 0; --bit) {
-                const uint32_t cand = prefix | (1u << bit);
-                int cnt = 0;
+                // tau lies in [low, m]: it shares the common high bits of their keys
+                const uint32_t lo_key = low == -INFINITY ? 0u : float_key(low);
+                const uint32_t hi_key = float_key(m);
+                const uint32_t diff = lo_key ^ hi_key;
+                const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
+                uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
+                for (int bit = top; bit >= 0; --bit) {
+                    const uint32_t cand = prefix | (1u << bit);
+                    int cnt = 0;
 #pragma unroll
-                for (int i = 0; i < ITEMS; ++i) {
-                    const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
-                    cnt += (idx < V && float_key(v[i]) >= cand) ? 1 : 0;
+                    for (int s = 0; s < kBisCap / 64; ++s) cnt += static_cast<int>(__popcll(__ballot(keys[s] >= cand)));
+                    if (cnt >= k) prefix = cand;
                 }
-                cnt = wave_sum_i32(cnt);
-                if (lane == 0) s_bis[buf][wave] = cnt;
-                __syncthreads();
-                int total = 0;
-#pragma unroll
-                for (int w = 0; w < kWaves; ++w) total += s_bis[buf][w];
-                if (total >= k) prefix = cand;
-                buf ^= 1;
+                if (lane == 0) L.tau = prefix;
             }
-            tau = prefix;
+            __syncthreads();  // barrier 3
+            tau = L.tau;
         }
-    }
 
-    // ---- 5. candidates in ascending id order -----------------------------------
-    const float temp = a.temperature;
-    double z = 0.0;
+        // ---- E. mark the candidates >= tau; weight sum -------------------------------
+        const bool want_probs = a.cand_probs != nullptr;
+        const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
+        double z = 0.0;
+        for (int j = tid; j < ncand; j += kThreads) {
+            int w = 0;
 #pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        int cnt = 0;
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-            const int i = ch * VEC + q;
-            const int idx = ch * kChunk + tid * VEC + q;
-            const bool sel = idx < V && float_key(v[i]) >= tau;
-            const uint64_t mask = __ballot(sel);
-            cnt += __popcll(mask);
-            if (a.cand_probs && mask && sel) z += cand_weight(v[i], m, temp);
+            for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
+            const float cv = L.cv[w][j - seg_start[w]];
+            if (float_key(cv) >= tau) {
+                const int idx = L.ci[w][j - seg_start[w]];
+                atomicOr(&L.sel[idx >> 5], 1u << (idx & 31));
+                if (want_probs) z += static_cast<double>(cand_weight(cv, m, inv_t));
+            }
         }
-        if (lane == 0) s_chunk_count[ch][wave] = cnt;
-    }
-    if (a.cand_probs) {
         z = wave_sum_f64(z);
-        if (lane == 0) s_wz[wave] = z;
-    }
-    __syncthreads();
-    if (a.cand_probs) z = s_wz[0] + s_wz[1] + s_wz[2] + s_wz[3];
-    const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+        if (lane == 0) L.wz[wave] = z;
+        __syncthreads();  // barrier 4
+        bitmap_prefix(L, words);
+        z = 0.0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) z += L.wz[w];
+        const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+        const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
+        __syncthreads();  // barrier 5
 
-    // exclusive scan of chunk totals across the wave's lanes
-    int lane_tot[kCPL];
-    int lane_sum = 0;
+        // ---- write the candidates in ascending id order ------------------------------
+        for (int j = tid; j < ncand; j += kThreads) {
+            int w = 0;
 #pragma unroll
-    for (int j = 0; j < kCPL; ++j) {
-        const int ch = lane * kCPL + j;
-        int t = 0;
-        if (ch < NCH) {
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) t += s_chunk_count[ch][w];
-        }
-        lane_tot[j] = t;
-        lane_sum += t;
-    }
-    int incl = lane_sum;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    const int total = __shfl(incl, 63, 64);
-    int lane_start[kCPL];
-    {
-        int run = incl - lane_sum;
-#pragma unroll
-        for (int j = 0; j < kCPL; ++j) {
-            lane_start[j] = run;
-            run += lane_tot[j];
-        }
-    }
-
-    const int cap = a.capacity;
-    int32_t * out_ids = a.cand_ids + row * cap;
-    float * out_logits = a.cand_logits ? a.cand_logits + row * cap : nullptr;
-    float * out_probs = a.cand_probs ? a.cand_probs + row * cap : nullptr;
-#pragma unroll
-    for (int ch = 0; ch < NCH; ++ch) {
-        int start = 0;
-#pragma unroll
-        for (int j = 0; j < kCPL; ++j)
-            if ((ch % kCPL) == j) start = __builtin_amdgcn_readlane(lane_start[j], ch / kCPL);
-        if (start >= cap) break;  // uniform: later chunks only add later ids
-        int before = 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-            if (w < wave) before += s_chunk_count[ch][w];
-        uint64_t masks[VEC];
-        bool sels[VEC];
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-            const int idx = ch * kChunk + tid * VEC + q;
-            sels[q] = idx < V && float_key(v[ch * VEC + q]) >= tau;
-            masks[q] = __ballot(sels[q]);
-        }
-        int lower = 0;  // selected ids of lower lanes in this wave
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) lower += rank_in_mask(masks[q]);
-        int mine = 0;
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-            if (sels[q]) {
-                const int pos = start + before + lower + mine;
-                if (pos < cap) {
-                    const int idx = ch * kChunk + tid * VEC + q;
-                    const float lv = v[ch * VEC + q];
-                    out_ids[pos] = idx;
-                    if (out_logits) out_logits[pos] = lv;
-                    if (out_probs) {
-                        float p;
-                        if (z_ok) p = static_cast<float>(cand_weight(lv, m, temp) / z);
-                        else p = idx == best ? 1.0f : 0.0f;  // the reference falls back to best
-                        out_probs[pos] = p;
-                    }
-                }
-                ++mine;
+            for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
+            const float cv = L.cv[w][j - seg_start[w]];
+            if (float_key(cv) >= tau) {
+                const int idx = L.ci[w][j - seg_start[w]];
+                write_candidate(a, row, slot_of(L, idx), idx, cv, best, m, inv_t, z_ok, inv_z);
             }
         }
     }
 
+    if (my_best == best && a.row_max) a.row_max[row] = tbest_v;
     if (tid == 0) {
         a.best[row] = best;
-        a.count[row] = total;
-        if (a.row_max) a.row_max[row] = m;
+        a.count[row] = L.total;
         if (a.row_lse) {
-            const float s = s_wlse[0] + s_wlse[1] + s_wlse[2] + s_wlse[3];
+            const float s = L.wlse[0] + L.wlse[1] + L.wlse[2] + L.wlse[3];
             float lse;
             if (m == -INFINITY) lse = -INFINITY;
             else if (m == INFINITY) lse = INFINITY;

@@ -1,10 +1,11 @@
 // Fused residual add + RMSNorm / LayerNorm, one wave64 per row.
 //
-// Each row (dim contiguous elements) is owned by one wavefront: it is loaded
-// once with dwordx4 accesses, kept in registers, reduced with cross-lane
-// shuffles (no LDS, no barrier), normalised and written once. The reduction
-// accumulates in double like ggml-cpu's ggml_float row sums, so the F32 mean /
-// variance (and hence every rounding point after it) matches the CPU chain.
+// Each row (dim contiguous elements) is owned by one wavefront: every load
+// of the row (x, delta, weight, bias) is issued up front with dwordx4
+// accesses, the row stays in registers, is reduced with cross-lane shuffles
+// (no LDS, no barrier), normalised and written once. The reduction
+// accumulates in double like ggml-cpu's ggml_float row sums, so the F32 mean
+// / variance (and hence every rounding point after it) matches the CPU chain.
 //
 //   RMSNorm F16 (src/levo-kv.cpp:153-160, residual :462/:507):
 //     h = f16(x + d); n = f16(h * 1/sqrtf(mean(h^2) + eps)); y = f16(n * w)
@@ -12,6 +13,9 @@
 //   LayerNorm  (src/levo-flow-estimator.cpp:106-109, residual :221-227):
 //     h = x + d; v = h - mean; scale = 1/sqrtf(mean(v^2) + eps);
 //     y = ((v * scale) * gamma) + beta   (F16 storage: h and y rounded to F16)
+//
+// Rows whose length is not a multiple of 8 (or unaligned buffers) take a
+// loop kernel that reads the row from L2 again per pass.
 #include "common.hpp"
 
 #include <type_traits>
@@ -21,93 +25,73 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kVec = 8;  // elements per lane per group (16 B of F16, 32 B of F32)
 
-// Loads n consecutive values starting at p (16-byte aligned when n*size >= 16).
-template <int N>
-__device__ __forceinline__ void load_f32(const float * p, float (&o)[N]) {
-    if constexpr (N % 4 == 0) {
+template <typename T>
+__device__ __forceinline__ void load8(const T * p, float (&o)[kVec]);
+template <>
+__device__ __forceinline__ void load8<uint16_t>(const uint16_t * p, float (&o)[kVec]) {
+    const u16x8 v = *reinterpret_cast<const u16x8 *>(p);
 #pragma unroll
-        for (int k = 0; k < N / 4; ++k) {
-            const f32x4 v = reinterpret_cast<const f32x4 *>(p)[k];
-            o[4 * k] = v.x;
-            o[4 * k + 1] = v.y;
-            o[4 * k + 2] = v.z;
-            o[4 * k + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < N; ++k) o[k] = p[k];
-    }
+    for (int k = 0; k < kVec; ++k) o[k] = h2f(v[k]);
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float * p, float (&o)[kVec]) {
+    const f32x4 a = reinterpret_cast<const f32x4 *>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4 *>(p)[1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-template <int N>
-__device__ __forceinline__ void load_u16(const uint16_t * p, uint16_t (&o)[N]) {
-    if constexpr (N == 8) {
-        const u16x8 v = *reinterpret_cast<const u16x8 *>(p);
+// Raw F16 bits are kept for the residual (h = f16(x + d) is formed from them).
+__device__ __forceinline__ void load8_raw(const uint16_t * p, uint16_t (&o)[kVec]) {
+    const u16x8 v = *reinterpret_cast<const u16x8 *>(p);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = v[k];
-    } else if constexpr (N == 4) {
-        const uint2 v = *reinterpret_cast<const uint2 *>(p);
-        o[0] = v.x & 0xffffu;
-        o[1] = v.x >> 16;
-        o[2] = v.y & 0xffffu;
-        o[3] = v.y >> 16;
-    } else {
-#pragma unroll
-        for (int k = 0; k < N; ++k) o[k] = p[k];
-    }
+    for (int k = 0; k < kVec; ++k) o[k] = v[k];
 }
 
-template <int N>
-__device__ __forceinline__ void store_u16(uint16_t * p, const uint16_t (&v)[N]) {
-    if constexpr (N == 8) {
-        u16x8 w;
+__device__ __forceinline__ void store8(uint16_t * p, const float (&v)[kVec]) {
+    u16x8 w;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) w[k] = v[k];
-        *reinterpret_cast<u16x8 *>(p) = w;
-    } else {
+    for (int k = 0; k < kVec; ++k) w[k] = f2h(v[k]);
+    *reinterpret_cast<u16x8 *>(p) = w;
+}
+__device__ __forceinline__ void store8_bits(uint16_t * p, const uint16_t (&v)[kVec]) {
+    u16x8 w;
 #pragma unroll
-        for (int k = 0; k < N; ++k) p[k] = v[k];
-    }
+    for (int k = 0; k < kVec; ++k) w[k] = v[k];
+    *reinterpret_cast<u16x8 *>(p) = w;
+}
+__device__ __forceinline__ void store8(float * p, const float (&v)[kVec]) {
+    f32x4 a, b;
+    a.x = v[0]; a.y = v[1]; a.z = v[2]; a.w = v[3];
+    b.x = v[4]; b.y = v[5]; b.z = v[6]; b.w = v[7];
+    reinterpret_cast<f32x4 *>(p)[0] = a;
+    reinterpret_cast<f32x4 *>(p)[1] = b;
 }
 
-template <int N>
-__device__ __forceinline__ void store_f32(float * p, const float (&v)[N]) {
-    if constexpr (N % 4 == 0) {
-#pragma unroll
-        for (int k = 0; k < N / 4; ++k) {
-            f32x4 w;
-            w.x = v[4 * k];
-            w.y = v[4 * k + 1];
-            w.z = v[4 * k + 2];
-            w.w = v[4 * k + 3];
-            reinterpret_cast<f32x4 *>(p)[k] = w;
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < N; ++k) p[k] = v[k];
-    }
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+    if constexpr (std::is_same<T, uint16_t>::value) return h2f(v);
+    else return v;
 }
 
-// Parameter vector (F32 or F16 storage, chosen at run time) widened to F32.
-template <int N>
-__device__ __forceinline__ void load_param(const void * p, bool f16, int64_t e, float (&o)[N]) {
-    if (f16) {
-        uint16_t t[N];
-        load_u16<N>(static_cast<const uint16_t *>(p) + e, t);
-#pragma unroll
-        for (int k = 0; k < N; ++k) o[k] = h2f(t[k]);
-    } else {
-        load_f32<N>(static_cast<const float *>(p) + e, o);
-    }
+// Output rounding of the chains above, given the normalised value n.
+template <typename T, bool kLayer>
+__device__ __forceinline__ float norm_out(float n, float w, float b) {
+    if constexpr (kLayer) return (n * w) + b;
+    else if constexpr (std::is_same<T, uint16_t>::value) return h2f(f2h(n)) * w;  // cast_f16 then mul
+    else return n * w;
 }
 
-// T = uint16_t (F16 storage) or float. VEC elements per group, NV groups per lane.
-template <typename T, bool kLayer, int VEC, int NV>
-__global__ __launch_bounds__(kThreads) void norm_kernel(const T * __restrict__ x, const T * __restrict__ d,
-                                                        const void * __restrict__ w,
-                                                        const void * __restrict__ b, bool p_f16,
-                                                        T * h_out, T * y, int64_t rows, int dim, float eps) {
+// T: activation storage (uint16_t = F16, float); P: parameter storage.
+// NV groups of 8 elements per lane (dim <= 512 * NV).
+// x / d may alias h_out or y (in-place residual): every load precedes every
+// store of the row in program order, so no __restrict__ on them.
+template <typename T, typename P, bool kLayer, int NV>
+__global__ __launch_bounds__(kThreads) void norm_kernel(const T * x, const T * d, const P * __restrict__ w,
+                                                        const P * __restrict__ b, T * h_out, T * y,
+                                                        int64_t rows, int dim, float eps) {
     constexpr bool kF16 = std::is_same<T, uint16_t>::value;
     const int lane = threadIdx.x & 63;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
@@ -117,63 +101,77 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const T * __restrict__ x
     T * hr = h_out ? h_out + row * dim : nullptr;
     T * yr = y + row * dim;
 
-    float h[NV][VEC];
+    // ---- every load first: groups past dim read a clamped, valid address ----
+    bool in[NV];
+    int off[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = (lane + 64 * j) * kVec;
+        in[j] = e < dim;
+        off[j] = in[j] ? e : 0;
+    }
+    float h[NV][kVec];
+    float wv[NV][kVec];
+    float bv[NV][kVec];
+    uint16_t xb[NV][kVec], db[NV][kVec];
+    float df[NV][kVec];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if constexpr (kF16) load8_raw(xr + off[j], xb[j]);
+        else load8(xr + off[j], h[j]);
+    }
+    if (dr) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            if constexpr (kF16) load8_raw(dr + off[j], db[j]);
+            else load8(dr + off[j], df[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        load8(w + off[j], wv[j]);
+        if constexpr (kLayer) load8(b + off[j], bv[j]);
+    }
+
+    // ---- residual, statistics ---------------------------------------------------
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = (lane + 64 * j) * VEC;
-        if (e < dim) {
-            if constexpr (kF16) {
-                uint16_t xv[VEC], hv[VEC];
-                load_u16<VEC>(xr + e, xv);
-                if (dr) {
-                    uint16_t dv[VEC];
-                    load_u16<VEC>(dr + e, dv);
+        if constexpr (kF16) {
+            uint16_t hb[kVec];
 #pragma unroll
-                    for (int k = 0; k < VEC; ++k) hv[k] = f2h(h2f(xv[k]) + h2f(dv[k]));
-                } else {
+            for (int k = 0; k < kVec; ++k) hb[k] = dr ? f2h(h2f(xb[j][k]) + h2f(db[j][k])) : xb[j][k];
+            if (hr && in[j]) store8_bits(hr + off[j], hb);
 #pragma unroll
-                    for (int k = 0; k < VEC; ++k) hv[k] = xv[k];
-                }
-                if (hr) store_u16<VEC>(hr + e, hv);
+            for (int k = 0; k < kVec; ++k) h[j][k] = h2f(hb[k]);
+        } else {
+            if (dr) {
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) h[j][k] = h2f(hv[k]);
-            } else {
-                load_f32<VEC>(xr + e, h[j]);
-                if (dr) {
-                    float dv[VEC];
-                    load_f32<VEC>(dr + e, dv);
-#pragma unroll
-                    for (int k = 0; k < VEC; ++k) h[j][k] = h[j][k] + dv[k];
-                }
-                if (hr) store_f32<VEC>(hr + e, h[j]);
+                for (int k = 0; k < kVec; ++k) h[j][k] = h[j][k] + df[j][k];
             }
+            if (hr && in[j]) store8(hr + off[j], h[j]);
+        }
+        if (in[j]) {
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) {
-                if constexpr (kLayer)
-                    acc += static_cast<double>(h[j][k]);
-                else
-                    acc += static_cast<double>(h[j][k] * h[j][k]);
+            for (int k = 0; k < kVec; ++k) {
+                if constexpr (kLayer) acc += static_cast<double>(h[j][k]);
+                else acc += static_cast<double>(h[j][k] * h[j][k]);
             }
         }
     }
     acc = wave_sum_f64(acc);
 
     float scale;
-    float mean = 0.0f;
     if constexpr (kLayer) {
-        mean = static_cast<float>(acc / static_cast<double>(dim));
+        const float mean = static_cast<float>(acc / static_cast<double>(dim));
         double acc2 = 0.0;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int e = (lane + 64 * j) * VEC;
-            if (e < dim) {
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) {
-                    const float v = h[j][k] - mean;
-                    h[j][k] = v;
-                    acc2 += static_cast<double>(v * v);
-                }
+            for (int k = 0; k < kVec; ++k) {
+                const float v = h[j][k] - mean;
+                h[j][k] = v;
+                if (in[j]) acc2 += static_cast<double>(v * v);
             }
         }
         acc2 = wave_sum_f64(acc2);
@@ -184,76 +182,101 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const T * __restrict__ x
         scale = 1.0f / sqrtf(ms + eps);
     }
 
+    // ---- normalise and store ---------------------------------------------------------
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = (lane + 64 * j) * VEC;
-        if (e < dim) {
-            float wv[VEC];
-            load_param<VEC>(w, p_f16, e, wv);
-            float o[VEC];
-            if constexpr (kLayer) {
-                float bv[VEC];
-                load_param<VEC>(b, p_f16, e, bv);
+        if (in[j]) {
+            float o[kVec];
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) o[k] = ((h[j][k] * scale) * wv[k]) + bv[k];
-            } else if constexpr (kF16) {
-#pragma unroll
-                for (int k = 0; k < VEC; ++k) o[k] = h2f(f2h(h[j][k] * scale)) * wv[k];
-            } else {
-#pragma unroll
-                for (int k = 0; k < VEC; ++k) o[k] = (h[j][k] * scale) * wv[k];
-            }
-            if constexpr (kF16) {
-                uint16_t ov[VEC];
-#pragma unroll
-                for (int k = 0; k < VEC; ++k) ov[k] = f2h(o[k]);
-                store_u16<VEC>(yr + e, ov);
-            } else {
-                store_f32<VEC>(yr + e, o);
-            }
+            for (int k = 0; k < kVec; ++k)
+                o[k] = norm_out<T, kLayer>(h[j][k] * scale, wv[j][k], kLayer ? bv[j][k] : 0.0f);
+            store8(yr + off[j], o);
         }
     }
 }
 
-template <typename T, bool kLayer, int VEC>
-int launch_nv(const T * x, const T * d, const void * w, const void * b, bool p_f16, T * h, T * y,
-              int64_t rows, int dim, float eps, hipStream_t stream) {
-    const int groups = static_cast<int>(ceil_div(dim, 64 * VEC));
-    const int64_t grid = ceil_div(rows, kWaves);
-    constexpr int kMaxNV = 8192 / (64 * VEC);
-#define LEVO_NORM_CASE(NVV)                                                                           \
-    if constexpr (NVV <= kMaxNV) {                                                                    \
-        if (groups <= NVV) {                                                                          \
-            norm_kernel<T, kLayer, VEC, NVV><<<grid, kThreads, 0, stream>>>(x, d, w, b, p_f16, h, y,  \
-                                                                            rows, dim, eps);          \
-            return launch_status("levo_hip_residual_norm");                                           \
-        }                                                                                             \
+// Any dim / alignment: the wave loops over its row, re-reading it per pass.
+// Each element is read and written by the same lane, reads first, so the
+// residual may be written in place.
+template <typename T, typename P, bool kLayer>
+__global__ __launch_bounds__(kThreads) void norm_kernel_loop(const T * x, const T * d, const P * __restrict__ w,
+                                                             const P * __restrict__ b, T * h_out, T * y,
+                                                             int64_t rows, int dim, float eps) {
+    constexpr bool kF16 = std::is_same<T, uint16_t>::value;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T * xr = x + row * dim;
+    const T * dr = d ? d + row * dim : nullptr;
+    T * hr = h_out ? h_out + row * dim : nullptr;
+    T * yr = y + row * dim;
+    auto residual = [&](int e) -> float {
+        if constexpr (kF16) return dr ? h2f(f2h(h2f(xr[e]) + h2f(dr[e]))) : h2f(xr[e]);
+        else return dr ? xr[e] + dr[e] : xr[e];
+    };
+    double acc = 0.0;
+    for (int e = lane; e < dim; e += 64) {
+        const float h = residual(e);
+        if constexpr (kLayer) acc += static_cast<double>(h);
+        else acc += static_cast<double>(h * h);
     }
-    LEVO_NORM_CASE(1)
-    LEVO_NORM_CASE(2)
-    LEVO_NORM_CASE(4)
-    LEVO_NORM_CASE(8)
-    LEVO_NORM_CASE(16)
-    LEVO_NORM_CASE(32)
-    LEVO_NORM_CASE(64)
-    LEVO_NORM_CASE(128)
-#undef LEVO_NORM_CASE
-    set_error("residual norm: row length %d exceeds the supported 8192", dim);
-    return LEVO_HIP_ERR_UNSUPPORTED;
+    acc = wave_sum_f64(acc);
+    float scale, mean = 0.0f;
+    if constexpr (kLayer) {
+        mean = static_cast<float>(acc / static_cast<double>(dim));
+        double acc2 = 0.0;
+        for (int e = lane; e < dim; e += 64) {
+            const float v = residual(e) - mean;
+            acc2 += static_cast<double>(v * v);
+        }
+        acc2 = wave_sum_f64(acc2);
+        scale = 1.0f / sqrtf(static_cast<float>(acc2 / static_cast<double>(dim)) + eps);
+    } else {
+        scale = 1.0f / sqrtf(static_cast<float>(acc / static_cast<double>(dim)) + eps);
+    }
+    for (int e = lane; e < dim; e += 64) {
+        const float h = residual(e);
+        const float n = kLayer ? (h - mean) * scale : h * scale;
+        const float o = norm_out<T, kLayer>(n, to_f32(w[e]), kLayer ? to_f32(b[e]) : 0.0f);
+        if (hr) {
+            if constexpr (kF16) hr[e] = f2h(h);
+            else hr[e] = h;
+        }
+        if constexpr (kF16) yr[e] = f2h(o);
+        else yr[e] = o;
+    }
 }
 
-template <typename T, bool kLayer>
-int launch_norm(const void * x, const void * d, const void * w, const void * b, bool p_f16, void * h,
-                void * y, int64_t rows, int64_t dim, float eps, hipStream_t stream) {
-    constexpr int kVec = std::is_same<T, uint16_t>::value ? 8 : 4;
-    const bool vec = dim % 8 == 0 && aligned16(x) && (d == nullptr || aligned16(d)) && aligned16(w) &&
-                     (b == nullptr || aligned16(b)) && (h == nullptr || aligned16(h)) && aligned16(y);
-    const T * xt = static_cast<const T *>(x);
-    const T * dt = static_cast<const T *>(d);
-    T * ht = static_cast<T *>(h);
-    T * yt = static_cast<T *>(y);
-    if (vec) return launch_nv<T, kLayer, kVec>(xt, dt, w, b, p_f16, ht, yt, rows, static_cast<int>(dim), eps, stream);
-    return launch_nv<T, kLayer, 1>(xt, dt, w, b, p_f16, ht, yt, rows, static_cast<int>(dim), eps, stream);
+template <typename T, typename P, bool kLayer>
+int launch_norm(const void * xv, const void * dv, const void * wv, const void * bv, void * hv, void * yv,
+                int64_t rows, int64_t dim64, float eps, hipStream_t stream) {
+    const T * x = static_cast<const T *>(xv);
+    const T * d = static_cast<const T *>(dv);
+    const P * w = static_cast<const P *>(wv);
+    const P * b = static_cast<const P *>(bv);
+    T * h = static_cast<T *>(hv);
+    T * y = static_cast<T *>(yv);
+    const int dim = static_cast<int>(dim64);
+    const int64_t grid = ceil_div(rows, kWaves);
+    const bool vec = dim % kVec == 0 && aligned16(x) && (d == nullptr || aligned16(d)) && aligned16(w) &&
+                     (b == nullptr || aligned16(b)) && (h == nullptr || aligned16(h)) && aligned16(y) &&
+                     dim <= 64 * kVec * 16;
+    if (vec) {
+        const int groups = static_cast<int>(ceil_div(dim, 64 * kVec));
+#define LEVO_NORM_CASE(NVV)                                                                                 \
+        if (groups <= NVV) {                                                                                \
+            norm_kernel<T, P, kLayer, NVV><<<grid, kThreads, 0, stream>>>(x, d, w, b, h, y, rows, dim, eps); \
+            return launch_status("levo_hip_residual_norm");                                                 \
+        }
+        LEVO_NORM_CASE(1)
+        LEVO_NORM_CASE(2)
+        LEVO_NORM_CASE(4)
+        LEVO_NORM_CASE(8)
+        LEVO_NORM_CASE(16)
+#undef LEVO_NORM_CASE
+    }
+    norm_kernel_loop<T, P, kLayer><<<grid, kThreads, 0, stream>>>(x, d, w, b, h, y, rows, dim, eps);
+    return launch_status("levo_hip_residual_norm");
 }
 
 int check_norm_args(levo_hip_type act, const void * x, const void * w, levo_hip_type pt, const void * y,
@@ -265,6 +288,7 @@ int check_norm_args(levo_hip_type act, const void * x, const void * w, levo_hip_
     LEVO_REQUIRE(rows >= 0 && dim >= 0, "residual norm: negative shape");
     LEVO_REQUIRE(rows == 0 || dim > 0, "residual norm: empty rows");
     LEVO_REQUIRE(dim <= 8192, "residual norm: row length exceeds the supported 8192");
+    LEVO_REQUIRE(rows < (int64_t{1} << 31), "residual norm: too many rows");
     LEVO_REQUIRE(eps >= 0.0f, "residual norm: eps must be non-negative");
     LEVO_REQUIRE(rows == 0 || (x != nullptr && w != nullptr && y != nullptr),
                  "residual norm: null input, parameter or output");
@@ -283,13 +307,15 @@ extern "C" int levo_hip_residual_rms_norm(levo_hip_type act_type, const void * x
     const int st = check_norm_args(act_type, x, weight, weight_type, y, rows, dim, eps);
     if (st != LEVO_HIP_OK) return st;
     if (rows == 0) return LEVO_HIP_OK;
-    const bool p_f16 = weight_type == LEVO_HIP_TYPE_F16;
+    const hipStream_t s = as_hip(stream);
     if (act_type == LEVO_HIP_TYPE_F16) {
-        LEVO_REQUIRE(p_f16, "residual RMSNorm: F16 activations take the F16 weight (src/levo-kv.cpp:159)");
-        return launch_norm<uint16_t, false>(x, delta, weight, nullptr, p_f16, h_out, y, rows, dim, eps,
-                                            as_hip(stream));
+        LEVO_REQUIRE(weight_type == LEVO_HIP_TYPE_F16,
+                     "residual RMSNorm: F16 activations take the F16 weight (src/levo-kv.cpp:159)");
+        return launch_norm<uint16_t, uint16_t, false>(x, delta, weight, nullptr, h_out, y, rows, dim, eps, s);
     }
-    return launch_norm<float, false>(x, delta, weight, nullptr, p_f16, h_out, y, rows, dim, eps, as_hip(stream));
+    if (weight_type == LEVO_HIP_TYPE_F16)
+        return launch_norm<float, uint16_t, false>(x, delta, weight, nullptr, h_out, y, rows, dim, eps, s);
+    return launch_norm<float, float, false>(x, delta, weight, nullptr, h_out, y, rows, dim, eps, s);
 }
 
 extern "C" int levo_hip_residual_layer_norm(levo_hip_type act_type, const void * x, const void * delta,
@@ -300,9 +326,11 @@ extern "C" int levo_hip_residual_layer_norm(levo_hip_type act_type, const void *
     if (st != LEVO_HIP_OK) return st;
     if (rows == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(beta != nullptr, "residual LayerNorm: beta is null");
-    const bool p_f16 = param_type == LEVO_HIP_TYPE_F16;
+    const hipStream_t s = as_hip(stream);
+    const bool p16 = param_type == LEVO_HIP_TYPE_F16;
     if (act_type == LEVO_HIP_TYPE_F16)
-        return launch_norm<uint16_t, true>(x, delta, gamma, beta, p_f16, h_out, y, rows, dim, eps,
-                                           as_hip(stream));
-    return launch_norm<float, true>(x, delta, gamma, beta, p_f16, h_out, y, rows, dim, eps, as_hip(stream));
+        return p16 ? launch_norm<uint16_t, uint16_t, true>(x, delta, gamma, beta, h_out, y, rows, dim, eps, s)
+                   : launch_norm<uint16_t, float, true>(x, delta, gamma, beta, h_out, y, rows, dim, eps, s);
+    return p16 ? launch_norm<float, uint16_t, true>(x, delta, gamma, beta, h_out, y, rows, dim, eps, s)
+               : launch_norm<float, float, true>(x, delta, gamma, beta, h_out, y, rows, dim, eps, s);
 }

@@ -90,9 +90,10 @@ __device__ __forceinline__ void load_tile_params(snake_param * lds, const P * al
 }
 
 // Vector path: time, both strides multiple of 4, pointers 16-byte aligned.
+// y may equal x (in place): each thread loads all its vectors before storing.
 template <typename P, int VPT>
 __global__ __launch_bounds__(kThreads) void snake_beta_vec(
-        const float * __restrict__ x, int64_t x_stride, const P * __restrict__ alpha_log,
+        const float * x, int64_t x_stride, const P * __restrict__ alpha_log,
         const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total4,
         fast_div div_t4) {
     __shared__ snake_param params[kMaxTileChannels];
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void snake_beta_vec(
 // Scalar path for any time / stride / alignment.
 template <typename P>
 __global__ __launch_bounds__(kThreads) void snake_beta_scalar(
-        const float * __restrict__ x, int64_t x_stride, const P * __restrict__ alpha_log,
+        const float * x, int64_t x_stride, const P * __restrict__ alpha_log,
         const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total,
         fast_div div_t) {
     __shared__ snake_param params[kMaxTileChannels];

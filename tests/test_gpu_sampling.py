@@ -80,7 +80,9 @@ def check_rows(out, adjusted, top_ks, oracle, temperature, rows=None, lse=True):
         n = min(cand.size, out["ids"].shape[1])
         assert np.array_equal(out["ids"][r, :n], cand[:n]), r
         assert np.array_equal(out["logits"][r, :n].view(np.uint32), row[cand[:n]].view(np.uint32)), r
-        m = np.float32(row.max())
+        # max_logit of the reference: std::max over the candidates in id order
+        # keeps the first of equal values, i.e. the value at `best` (sign of a 0 tie)
+        m = np.float32(row[best])
         assert out["max"][r].view(np.uint32) == m.view(np.uint32)
         w = weights_f64(row[cand], m, temperature)
         if w.sum() > 0 and np.isfinite(w.sum()):
