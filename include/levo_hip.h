@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LEVO_HIP_ABI_VERSION 1
+#define LEVO_HIP_ABI_VERSION 2
 
 /* Same tag as HIP's hipStream_t, so a hipStream_t converts without a cast. */
 typedef struct ihipStream_t * levo_hip_stream_t;
@@ -140,6 +140,15 @@ typedef struct levo_hip_sample_args {
     int32_t capacity;     /* candidate slots per row (>= 1) */
 } levo_hip_sample_args;
 
+/* levo::apply_unique_token_repetition_penalty (src/levo-sampling.cpp:39-47)
+ * on one device row of `vocab` logits, in place: each distinct id of
+ * recent[0, n_recent) inside [0, limit) is divided once by `penalty`
+ * (limit 0 or > vocab means vocab). Fails with "repetition penalty must be
+ * finite and positive" like the reference. */
+int levo_hip_repetition_penalty(float * logits, int64_t vocab, const int64_t * recent,
+                                int32_t n_recent, float penalty, int64_t limit,
+                                levo_hip_stream_t stream);
+
 /* One launch per batch of rows: CFG, penalty/ignore, NaN check, row max and
  * argmax, the top-k candidate set of sample_top_k_counted
  * (src/levo-sampling.cpp:75-116; ties with the k-th value are kept) and the
@@ -156,6 +165,26 @@ int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_stream_t str
  * state += dt * v_uncond. Two roundings per product/sum, as the reference. */
 int levo_hip_flow_cfg_euler(float * state, const float * v_uncond, const float * v_cond,
                             int64_t n, float guidance, float dt, levo_hip_stream_t stream);
+
+/* Bits of the non-finite flag word written by the checked entry points. */
+#define LEVO_HIP_NONFINITE_VELOCITY 1 /* a combined velocity was NaN or infinite */
+#define LEVO_HIP_NONFINITE_STATE 2    /* an updated state value was NaN or infinite */
+
+/* levo_hip_flow_cfg_euler plus the reference's per-step finiteness checks
+ * (require_finite on the velocity and on the updated state,
+ * src/levo-flow-renderer.cpp:104, :106): ORs LEVO_HIP_NONFINITE_VELOCITY /
+ * LEVO_HIP_NONFINITE_STATE into *nonfinite (a device int32 the caller clears)
+ * when any combined velocity / updated state element is not finite. The
+ * update itself is identical to the unchecked entry point. */
+int levo_hip_flow_cfg_euler_checked(float * state, const float * v_uncond, const float * v_cond,
+                                    int64_t n, float guidance, float dt, int32_t * nonfinite,
+                                    levo_hip_stream_t stream);
+
+/* *flags |= bit when any x[e], e < n, is NaN or infinite (device int32 flag
+ * word): the entry checks of solve_flow_euler on the noise, the in-context
+ * latent and a resume state (src/levo-flow-renderer.cpp:24-28, 70-71, 80). */
+int levo_hip_check_finite(const float * x, int64_t n, int32_t * flags, int32_t bit,
+                          levo_hip_stream_t stream);
 
 /* In-context prefix of one Euler step (src/levo-flow-renderer.cpp:94-101):
  * state[e] = (1 - (1 - sigma_min) * time) * noise[e] + time * context[e]

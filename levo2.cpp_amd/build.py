@@ -3,7 +3,8 @@
   levo2.cpp_amd/liblevo_hip.so       C ABI (include/levo_hip.h) + HIP kernels
   levo2.cpp_amd/liblevo_hip_host.so  C++17 drop-in wrappers (levo2.cpp_amd/host/)
 
-Both are compiled with hipcc for gfx950 only. Every source is recompiled on
+Kernels are compiled with hipcc for gfx950 only; the host wrappers contain no
+device code and are plain C++17 (g++) against the HIP runtime API. Every source is recompiled on
 each call (the build is the "does it compile" check); objects are built in
 parallel into levo2.cpp_amd/_build/.
 """
@@ -25,6 +26,8 @@ KERNEL_LIB = os.path.join(PKG, "liblevo_hip.so")
 HOST_LIB = os.path.join(PKG, "liblevo_hip_host.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 # -ffp-contract=off: a*b+c rounds twice, as in the reference's ISO C++17 x86-64
@@ -63,6 +66,16 @@ def _compile(src: str, extra: list[str]) -> str:
     return obj
 
 
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+              "-I", os.path.join(ROCM, "include"), "-I", INCLUDE, "-I", HOST]
+
+
+def _compile_host(src: str) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    _run([CXX, *HOST_FLAGS, "-c", src, "-o", obj])
+    return obj
+
+
 def build(verbose: bool = False) -> None:
     os.makedirs(BUILD, exist_ok=True)
     kernel_srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
@@ -70,12 +83,12 @@ def build(verbose: bool = False) -> None:
     jobs = min(8, os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(jobs) as ex:
         kobjs = list(ex.map(lambda s: _compile(s, []), kernel_srcs))
-        hobjs = list(ex.map(lambda s: _compile(s, ["-I", HOST]), host_srcs))
+        hobjs = list(ex.map(_compile_host, host_srcs))
     _run([HIPCC, *DEVICE, "-shared", "-fPIC", "-o", KERNEL_LIB + ".tmp", *kobjs])
     os.replace(KERNEL_LIB + ".tmp", KERNEL_LIB)
     if hobjs:
-        _run([HIPCC, *DEVICE, "-shared", "-fPIC", "-o", HOST_LIB + ".tmp", *hobjs,
-              "-L", PKG, "-llevo_hip", "-Wl,-rpath,$ORIGIN"])
+        _run([CXX, "-shared", "-fPIC", "-o", HOST_LIB + ".tmp", *hobjs,
+              "-L", PKG, "-llevo_hip", "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath,$ORIGIN"])
         os.replace(HOST_LIB + ".tmp", HOST_LIB)
     if verbose:
         print("built", KERNEL_LIB, HOST_LIB if hobjs else "")

@@ -16,11 +16,25 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ float cfg(float u, float c, float g) { return u + g * (c - u); }
 
+__device__ __forceinline__ bool finite4(const f32x4 & v) {
+    return __builtin_isfinite(v.x) && __builtin_isfinite(v.y) && __builtin_isfinite(v.z) &&
+           __builtin_isfinite(v.w);
+}
+
+// Records which checked quantity held a non-finite value. Reached only on a
+// failure, so the healthy path carries one compare per vector and no atomics.
+__device__ __forceinline__ void flag_nonfinite(int32_t * flags, bool bad_v, bool bad_s) {
+    const int32_t f = (bad_v ? LEVO_HIP_NONFINITE_VELOCITY : 0) | (bad_s ? LEVO_HIP_NONFINITE_STATE : 0);
+    if (f) atomicOr(flags, f);
+}
+
 // One dwordx4 per thread; the scalar tail (n % 4) is handled by block 0.
-template <bool kCfg>
+// kCheck: also flag a non-finite combined velocity or updated state
+// (src/levo-flow-renderer.cpp:104, :106).
+template <bool kCfg, bool kCheck>
 __global__ __launch_bounds__(kThreads) void cfg_euler_kernel(float * state, const float * __restrict__ vu,
                                                              const float * __restrict__ vc, int64_t n,
-                                                             float g, float dt) {
+                                                             float g, float dt, int32_t * flags) {
     const int64_t n4 = n / 4;
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (i < n4) {
@@ -39,23 +53,44 @@ __global__ __launch_bounds__(kThreads) void cfg_euler_kernel(float * state, cons
         s.z += dt * v.z;
         s.w += dt * v.w;
         reinterpret_cast<f32x4 *>(state)[i] = s;
+        if (kCheck) flag_nonfinite(flags, !finite4(v), !finite4(s));
     }
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const int64_t e = n4 * 4 + threadIdx.x;
         const float v = kCfg ? cfg(vu[e], vc[e], g) : vu[e];
-        state[e] += dt * v;
+        const float s = state[e] + dt * v;
+        state[e] = s;
+        if (kCheck) flag_nonfinite(flags, !__builtin_isfinite(v), !__builtin_isfinite(s));
     }
 }
 
-template <bool kCfg>
+template <bool kCfg, bool kCheck>
 __global__ __launch_bounds__(kThreads) void cfg_euler_scalar(float * state, const float * __restrict__ vu,
                                                              const float * __restrict__ vc, int64_t n,
-                                                             float g, float dt) {
+                                                             float g, float dt, int32_t * flags) {
     const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
     if (e < n) {
         const float v = kCfg ? cfg(vu[e], vc[e], g) : vu[e];
-        state[e] += dt * v;
+        const float s = state[e] + dt * v;
+        state[e] = s;
+        if (kCheck) flag_nonfinite(flags, !__builtin_isfinite(v), !__builtin_isfinite(s));
     }
+}
+
+// flags |= bit when any of x[0, n) is NaN or infinite.
+__global__ __launch_bounds__(kThreads) void check_finite_kernel(const float * __restrict__ x, int64_t n,
+                                                                int32_t * flags, int32_t bit, bool vec) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    bool bad = false;
+    if (vec) {
+        const int64_t n4 = n / 4;
+        for (int64_t j = i; j < n4; j += stride) bad |= !finite4(reinterpret_cast<const f32x4 *>(x)[j]);
+        if (i < (n & 3)) bad |= !__builtin_isfinite(x[n4 * 4 + i]);
+    } else {
+        for (int64_t j = i; j < n; j += stride) bad |= !__builtin_isfinite(x[j]);
+    }
+    if (bad) atomicOr(flags, bit);
 }
 
 __global__ __launch_bounds__(kThreads) void incontext_kernel(float * state, const float * __restrict__ noise,
@@ -107,27 +142,73 @@ __global__ __launch_bounds__(kThreads) void f16_to_f32_kernel(const uint16_t * _
 
 using namespace levo_hip;
 
+namespace {
+
+int launch_euler(float * state, const float * v_uncond, const float * v_cond, int64_t n, float guidance,
+                 float dt, int32_t * flags, levo_hip_stream_t stream, const char * what) {
+    const bool vec = aligned16(state) && aligned16(v_uncond) && (v_cond == nullptr || aligned16(v_cond));
+    const hipStream_t s = as_hip(stream);
+    const bool check = flags != nullptr;
+    if (vec) {
+        const int64_t grid = ceil_div(n / 4 > 0 ? n / 4 : 1, kThreads);
+        if (v_cond && check)
+            cfg_euler_kernel<true, true><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+        else if (v_cond)
+            cfg_euler_kernel<true, false><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+        else if (check)
+            cfg_euler_kernel<false, true><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+        else
+            cfg_euler_kernel<false, false><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+    } else {
+        const int64_t grid = ceil_div(n, kThreads);
+        if (v_cond && check)
+            cfg_euler_scalar<true, true><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+        else if (v_cond)
+            cfg_euler_scalar<true, false><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+        else if (check)
+            cfg_euler_scalar<false, true><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+        else
+            cfg_euler_scalar<false, false><<<grid, kThreads, 0, s>>>(state, v_uncond, v_cond, n, guidance, dt, flags);
+    }
+    return launch_status(what);
+}
+
+}  // namespace
+
 extern "C" int levo_hip_flow_cfg_euler(float * state, const float * v_uncond, const float * v_cond,
                                        int64_t n, float guidance, float dt, levo_hip_stream_t stream) {
     LEVO_REQUIRE(n >= 0, "LeVo Flow renderer: Euler state size is negative");
     if (n == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(state != nullptr && v_uncond != nullptr,
                  "LeVo Flow renderer: Euler state or velocity is null");
-    const bool vec = aligned16(state) && aligned16(v_uncond) && (v_cond == nullptr || aligned16(v_cond));
-    if (vec) {
-        const int64_t grid = ceil_div(n / 4 > 0 ? n / 4 : 1, kThreads);
-        if (v_cond)
-            cfg_euler_kernel<true><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
-        else
-            cfg_euler_kernel<false><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
-    } else {
-        const int64_t grid = ceil_div(n, kThreads);
-        if (v_cond)
-            cfg_euler_scalar<true><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
-        else
-            cfg_euler_scalar<false><<<grid, kThreads, 0, as_hip(stream)>>>(state, v_uncond, v_cond, n, guidance, dt);
-    }
-    return launch_status("levo_hip_flow_cfg_euler");
+    return launch_euler(state, v_uncond, v_cond, n, guidance, dt, nullptr, stream, "levo_hip_flow_cfg_euler");
+}
+
+extern "C" int levo_hip_flow_cfg_euler_checked(float * state, const float * v_uncond, const float * v_cond,
+                                               int64_t n, float guidance, float dt, int32_t * nonfinite,
+                                               levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n >= 0, "LeVo Flow renderer: Euler state size is negative");
+    LEVO_REQUIRE(nonfinite != nullptr, "LeVo Flow renderer: non-finite flag pointer is null");
+    if (n == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(state != nullptr && v_uncond != nullptr,
+                 "LeVo Flow renderer: Euler state or velocity is null");
+    return launch_euler(state, v_uncond, v_cond, n, guidance, dt, nonfinite, stream,
+                        "levo_hip_flow_cfg_euler_checked");
+}
+
+extern "C" int levo_hip_check_finite(const float * x, int64_t n, int32_t * flags, int32_t bit,
+                                     levo_hip_stream_t stream) {
+    LEVO_REQUIRE(n >= 0, "check_finite: negative length");
+    LEVO_REQUIRE(flags != nullptr, "check_finite: flag pointer is null");
+    LEVO_REQUIRE(bit != 0, "check_finite: flag bit is zero");
+    if (n == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(x != nullptr, "check_finite: input is null");
+    const bool vec = aligned16(x);
+    const int64_t items = vec ? (n / 4 > 0 ? n / 4 : 1) : n;
+    // Up to 8 workgroups per CU, each thread then strides over the rest.
+    const int64_t grid = ceil_div(items, kThreads) < 2048 ? ceil_div(items, kThreads) : 2048;
+    check_finite_kernel<<<grid, kThreads, 0, as_hip(stream)>>>(x, n, flags, bit, vec);
+    return launch_status("levo_hip_check_finite");
 }
 
 extern "C" int levo_hip_flow_incontext(float * state, const float * noise, const float * context,

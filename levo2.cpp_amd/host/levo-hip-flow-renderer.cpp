@@ -1,0 +1,222 @@
+// Euler solver of src/levo-flow-renderer.cpp:57-120 with the state on the GPU:
+// levo_hip_flow_incontext for the prefix interpolation, levo_hip_check_finite
+// for the entry checks and levo_hip_flow_cfg_euler_checked for the update and
+// its per-step finiteness checks.
+#include "levo-hip-flow-renderer.h"
+
+#include <cmath>
+#include <limits>
+#include <string>
+
+namespace levo::hip::flow {
+namespace {
+
+[[noreturn]] void fail(const std::string & message) {
+    throw std::runtime_error("LeVo Flow renderer: " + message);
+}
+
+std::size_t element_count(std::size_t frames, std::size_t width) {
+    if (frames == 0 || width == 0) fail("Euler state dimensions must be positive");
+    if (width > std::numeric_limits<std::size_t>::max() / frames) fail("Euler state size overflow");
+    const std::size_t n = frames * width;
+    if (n > static_cast<std::size_t>(std::numeric_limits<int64_t>::max() / 4)) fail("Euler state size overflow");
+    return n;
+}
+
+void validate_common(std::size_t steps, bool has_velocity) {
+    if (steps == 0) fail("Euler step count must be positive");
+    if (!has_velocity) fail("Euler velocity callback is required");
+}
+
+void validate_prefix(std::size_t frames, std::size_t incontext_frames, float sigma_min) {
+    if (incontext_frames > frames) fail("Euler in-context length exceeds frame count");
+    if (!std::isfinite(sigma_min) || sigma_min <= 0.0F) fail("Euler sigma_min must be finite and positive");
+}
+
+// Per-solve device state: the flag word and its pinned host mirror.
+class flag_word {
+public:
+    flag_word() : device_(1), host_(1) {}
+    void clear(stream_t stream) {
+        check_hip(hipMemsetAsync(device_.data(), 0, sizeof(int32_t), stream), "flag clear");
+    }
+    int32_t * device() { return device_.data(); }
+    int32_t read(stream_t stream) {
+        device_.download(host_.data(), 1, stream);
+        synchronize(stream);
+        return host_[0];
+    }
+
+private:
+    device_buffer<int32_t> device_;
+    pinned_buffer<int32_t> host_;
+};
+
+constexpr int32_t kNoiseBit = 1;
+constexpr int32_t kContextBit = 2;
+constexpr int32_t kResumeBit = 4;
+
+// Entry checks of the reference, in its order (src/levo-flow-renderer.cpp:70-80).
+void check_inputs_finite(flag_word & flags, const float * noise, const float * context, std::size_t n,
+                         stream_t stream) {
+    flags.clear(stream);
+    const auto count = static_cast<int64_t>(n);
+    check_status(levo_hip_check_finite(noise, count, flags.device(), kNoiseBit, stream), error_kind::runtime_error);
+    check_status(levo_hip_check_finite(context, count, flags.device(), kContextBit, stream), error_kind::runtime_error);
+    const int32_t f = flags.read(stream);
+    if (f & kNoiseBit) fail("Euler noise contains a non-finite value");
+    if (f & kContextBit) fail("Euler in-context latent contains a non-finite value");
+}
+
+// A resume state uploaded to `state` must be finite (:80).
+void check_resume_finite(flag_word & flags, const float * state, std::size_t n, stream_t stream) {
+    flags.clear(stream);
+    check_status(levo_hip_check_finite(state, static_cast<int64_t>(n), flags.device(), kResumeBit, stream),
+                 error_kind::runtime_error);
+    if (flags.read(stream) & kResumeBit) fail("Euler resume state contains a non-finite value");
+}
+
+// One Euler update with the reference's post-update checks (:104-106).
+void update(flag_word & flags, float * state, const float * v_uncond, const float * v_cond, std::size_t n,
+            float guidance, float dt, stream_t stream) {
+    flags.clear(stream);
+    check_status(levo_hip_flow_cfg_euler_checked(state, v_uncond, v_cond, static_cast<int64_t>(n), guidance, dt,
+                                                 flags.device(), stream),
+                 error_kind::runtime_error);
+    const int32_t f = flags.read(stream);
+    if (f & LEVO_HIP_NONFINITE_VELOCITY) fail("Euler velocity contains a non-finite value");
+    if (f & LEVO_HIP_NONFINITE_STATE) fail("Euler state contains a non-finite value");
+}
+
+void interpolate_prefix(float * state, const float * noise, const float * context, std::size_t prefix, float time,
+                        float sigma_min, stream_t stream) {
+    check_status(levo_hip_flow_incontext(state, noise, context, static_cast<int64_t>(prefix), time, sigma_min,
+                                         stream),
+                 error_kind::runtime_error);
+}
+
+void save(euler_resume_state * checkpoint, std::size_t completed, const float * state, std::size_t n,
+          stream_t stream) {
+    if (!checkpoint) return;
+    checkpoint->normalized_state.resize(n);
+    check_hip(hipMemcpyAsync(checkpoint->normalized_state.data(), state, n * sizeof(float), hipMemcpyDeviceToHost,
+                             stream),
+              "device-to-host copy");
+    synchronize(stream);
+    checkpoint->completed_steps = completed;
+}
+
+} // namespace
+
+std::vector<float> solve_flow_euler(const euler_input & input, std::size_t steps, const velocity_callback & velocity,
+                                    const euler_progress_callback & progress, const cancellation_callback & cancelled,
+                                    const euler_resume_state * resume, euler_resume_state * checkpoint) {
+    validate_common(steps, static_cast<bool>(velocity));
+    const std::size_t n = element_count(input.frames, input.latent_dim);
+    if (input.initial_noise.size() != n || input.normalized_incontext.size() != n) {
+        fail("Euler tensors must have shape [frames, latent_dim]");
+    }
+    validate_prefix(input.frames, input.incontext_frames, input.sigma_min);
+
+    const stream_t stream = nullptr;
+    device_buffer<float> noise(n), context(n), state(n), vel(n);
+    noise.upload(input.initial_noise.data(), n, stream);
+    context.upload(input.normalized_incontext.data(), n, stream);
+    flag_word flags;
+    check_inputs_finite(flags, noise.data(), context.data(), n, stream);
+
+    std::size_t completed_steps = 0;
+    std::vector<float> host_state = input.initial_noise;
+    if (resume) {
+        if (resume->completed_steps > steps) fail("Euler resume step exceeds total steps");
+        if (resume->normalized_state.size() != n) fail("Euler resume state has an unexpected shape");
+        state.upload(resume->normalized_state.data(), n, stream);
+        check_resume_finite(flags, state.data(), n, stream);
+        completed_steps = resume->completed_steps;
+        host_state = resume->normalized_state;
+    } else {
+        state.upload(input.initial_noise.data(), n, stream);
+    }
+    if (checkpoint) {
+        checkpoint->completed_steps = completed_steps;
+        checkpoint->normalized_state = host_state;
+    }
+
+    const std::size_t prefix = input.incontext_frames * input.latent_dim;
+    const float dt = 1.0F / static_cast<float>(steps);
+    for (std::size_t step = completed_steps; step < steps; ++step) {
+        if (cancelled && cancelled()) throw operation_cancelled();
+        const float time = static_cast<float>(step) * dt;
+        interpolate_prefix(state.data(), noise.data(), context.data(), prefix, time, input.sigma_min, stream);
+        state.download(host_state.data(), n, stream);
+        synchronize(stream);
+        const std::vector<float> current_velocity = velocity(host_state, time);
+        if (current_velocity.size() != n) fail("Euler velocity callback returned an unexpected shape");
+        vel.upload(current_velocity.data(), n, stream);
+        update(flags, state.data(), vel.data(), nullptr, n, 1.0F, dt, stream);
+        save(checkpoint, step + 1U, state.data(), n, stream);
+        if (progress) progress(step + 1U, steps);
+    }
+    check_hip(hipMemcpyAsync(state.data(), context.data(), prefix * sizeof(float), hipMemcpyDeviceToDevice, stream),
+              "device-to-device copy");
+    state.download(host_state.data(), n, stream);
+    synchronize(stream);
+    if (checkpoint) {
+        checkpoint->completed_steps = steps;
+        checkpoint->normalized_state = host_state;
+    }
+    return host_state;
+}
+
+void solve_flow_euler_device(const device_euler_input & input, std::size_t steps, float guidance_scale,
+                             const device_velocity_callback & velocity, float * state,
+                             const euler_progress_callback & progress, const cancellation_callback & cancelled,
+                             const euler_resume_state * resume, euler_resume_state * checkpoint, stream_t stream) {
+    validate_common(steps, static_cast<bool>(velocity));
+    const std::size_t n = element_count(input.frames, input.latent_dim);
+    if (!input.initial_noise || !input.normalized_incontext || !state) {
+        fail("Euler tensors must have shape [frames, latent_dim]");
+    }
+    validate_prefix(input.frames, input.incontext_frames, input.sigma_min);
+
+    flag_word flags;
+    check_inputs_finite(flags, input.initial_noise, input.normalized_incontext, n, stream);
+
+    std::size_t completed_steps = 0;
+    if (resume) {
+        if (resume->completed_steps > steps) fail("Euler resume step exceeds total steps");
+        if (resume->normalized_state.size() != n) fail("Euler resume state has an unexpected shape");
+        check_hip(hipMemcpyAsync(state, resume->normalized_state.data(), n * sizeof(float), hipMemcpyHostToDevice,
+                                 stream),
+                  "host-to-device copy");
+        check_resume_finite(flags, state, n, stream);
+        completed_steps = resume->completed_steps;
+    } else {
+        check_hip(hipMemcpyAsync(state, input.initial_noise, n * sizeof(float), hipMemcpyDeviceToDevice, stream),
+                  "device-to-device copy");
+    }
+    save(checkpoint, completed_steps, state, n, stream);
+
+    device_buffer<float> vel(2 * n);
+    float * v_uncond = vel.data();
+    float * v_cond = vel.data() + n;
+    const std::size_t prefix = input.incontext_frames * input.latent_dim;
+    const float dt = 1.0F / static_cast<float>(steps);
+    for (std::size_t step = completed_steps; step < steps; ++step) {
+        if (cancelled && cancelled()) throw operation_cancelled();
+        const float time = static_cast<float>(step) * dt;
+        interpolate_prefix(state, input.initial_noise, input.normalized_incontext, prefix, time, input.sigma_min,
+                           stream);
+        velocity(state, time, v_uncond, v_cond, stream);
+        update(flags, state, v_uncond, v_cond, n, guidance_scale, dt, stream);
+        save(checkpoint, step + 1U, state, n, stream);
+        if (progress) progress(step + 1U, steps);
+    }
+    check_hip(hipMemcpyAsync(state, input.normalized_incontext, prefix * sizeof(float), hipMemcpyDeviceToDevice,
+                             stream),
+              "device-to-device copy");
+    save(checkpoint, steps, state, n, stream);
+    synchronize(stream);
+}
+
+} // namespace levo::hip::flow

@@ -1,0 +1,40 @@
+#include "levo-hip-quantize.h"
+
+namespace levo::hip {
+
+std::size_t row_size(levo_hip_type type, int64_t n_per_row) {
+    return static_cast<std::size_t>(check_status(levo_hip_row_size(type, n_per_row)));
+}
+
+int64_t padded_input_columns(int64_t columns, levo_hip_type type) {
+    if (type != LEVO_HIP_TYPE_Q8_0 && type != LEVO_HIP_TYPE_Q4_0) return columns;
+    constexpr int64_t block = 32;
+    if (columns <= 0) return columns;
+    return (columns + block - 1) / block * block;
+}
+
+std::size_t quantize_chunk(levo_hip_type type, const float * src, void * dst, int64_t start, int64_t nrows,
+                           int64_t n_per_row, const float * imatrix, stream_t stream) {
+    return static_cast<std::size_t>(
+            check_status(levo_hip_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix, stream)));
+}
+
+std::size_t quantize_rows(levo_hip_type type, const void * src, levo_hip_type src_type, int64_t src_cols,
+                          int64_t src_row_stride, void * dst, int64_t nrows, int64_t dst_cols, stream_t stream) {
+    return static_cast<std::size_t>(check_status(
+            levo_hip_quantize_rows(type, src, src_type, src_cols, src_row_stride, dst, nrows, dst_cols, stream)));
+}
+
+void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream) {
+    check_status(levo_hip_dequantize(type, src, dst, LEVO_HIP_TYPE_F32, k, stream));
+}
+
+void fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, stream_t stream) {
+    check_status(levo_hip_fp32_to_fp16_row(x, y, n, stream));
+}
+
+void fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n, stream_t stream) {
+    check_status(levo_hip_fp16_to_fp32_row(x, y, n, stream));
+}
+
+} // namespace levo::hip

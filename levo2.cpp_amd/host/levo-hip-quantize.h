@@ -1,0 +1,41 @@
+// The quantizer surface the LeVo conversion tool calls, on device memory:
+// ggml_quantize_chunk / ggml_row_size (tools/levo-quantize.cpp:386-388),
+// padded_input_columns (src/levo-quantization.h:120-125), write_tensor's
+// widen -> pad -> quantize chunk (tools/levo-quantize.cpp:355-388), the
+// dequantizers and the F16 row converters (:358, :369). Q8_0 and Q4_0 blocks
+// are ggml's byte layouts. Errors are std::invalid_argument.
+#pragma once
+
+#include "levo-hip-device.h"
+
+#include <cstddef>
+#include <cstdint>
+
+namespace levo::hip {
+
+// Bytes of one row of n_per_row values (ggml_row_size).
+std::size_t row_size(levo_hip_type type, int64_t n_per_row);
+
+// Columns after zero-padding a row to whole blocks of `type`.
+int64_t padded_input_columns(int64_t columns, levo_hip_type type);
+
+// ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix) with
+// src and dst in device memory: quantizes rows [start / n_per_row, + nrows)
+// and returns nrows * row_size(type, n_per_row).
+std::size_t quantize_chunk(levo_hip_type type, const float * src, void * dst, int64_t start, int64_t nrows,
+                           int64_t n_per_row, const float * imatrix = nullptr, stream_t stream = nullptr);
+
+// write_tensor's quantized branch in one pass: nrows rows of src_cols values
+// (F32, or F16 widened exactly) at src_row_stride elements, zero-padded to
+// dst_cols and quantized. Returns the bytes written.
+std::size_t quantize_rows(levo_hip_type type, const void * src, levo_hip_type src_type, int64_t src_cols,
+                          int64_t src_row_stride, void * dst, int64_t nrows, int64_t dst_cols,
+                          stream_t stream = nullptr);
+
+// ggml's to_float for Q8_0 / Q4_0: k values (a multiple of 32).
+void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream = nullptr);
+
+void fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, stream_t stream = nullptr);
+void fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n, stream_t stream = nullptr);
+
+} // namespace levo::hip

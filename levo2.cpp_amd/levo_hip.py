@@ -43,6 +43,12 @@ class SampleArgs(ctypes.Structure):
     ]
 
 
+def header_abi_version(header: str = HEADER) -> int:
+    """LEVO_HIP_ABI_VERSION as declared in include/levo_hip.h."""
+    m = re.search(r"#define\s+LEVO_HIP_ABI_VERSION\s+(\d+)", open(header).read())
+    return int(m.group(1))
+
+
 def declared_symbols(header: str = HEADER) -> list[str]:
     """Every function name declared in include/levo_hip.h."""
     text = open(header).read()
@@ -85,6 +91,9 @@ class LevoHip:
             "levo_hip_cfg_combine": (ctypes.c_int, [_P, _P, _P, _I64, _F, _P]),
             "levo_hip_cfg_sample": (ctypes.c_int, [ctypes.POINTER(SampleArgs), _P]),
             "levo_hip_flow_cfg_euler": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
+            "levo_hip_flow_cfg_euler_checked": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P, _P]),
+            "levo_hip_check_finite": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _P]),
+            "levo_hip_repetition_penalty": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _F, _I64, _P]),
             "levo_hip_flow_incontext": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
             "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
             "levo_hip_quantize_chunk": (_I64, [ctypes.c_int, _P, _P, _I64, _I64, _I64, _P, _P]),
@@ -136,6 +145,17 @@ class LevoHip:
     def flow_cfg_euler(self, state, v_uncond, v_cond, n, guidance, dt, stream=None):
         return self._check(self.lib.levo_hip_flow_cfg_euler(_addr(state), _addr(v_uncond), _addr(v_cond), n,
                                                             guidance, dt, _stream(stream)))
+
+    def flow_cfg_euler_checked(self, state, v_uncond, v_cond, n, guidance, dt, flags, stream=None):
+        return self._check(self.lib.levo_hip_flow_cfg_euler_checked(_addr(state), _addr(v_uncond), _addr(v_cond),
+                                                                    n, guidance, dt, _addr(flags), _stream(stream)))
+
+    def check_finite(self, x, n, flags, bit, stream=None):
+        return self._check(self.lib.levo_hip_check_finite(_addr(x), n, _addr(flags), bit, _stream(stream)))
+
+    def repetition_penalty(self, logits, vocab, recent, n_recent, penalty, limit=0, stream=None):
+        return self._check(self.lib.levo_hip_repetition_penalty(_addr(logits), vocab, _addr(recent), n_recent,
+                                                                penalty, limit, _stream(stream)))
 
     def flow_incontext(self, state, noise, context, n_prefix, time, sigma_min, stream=None):
         return self._check(self.lib.levo_hip_flow_incontext(_addr(state), _addr(noise), _addr(context), n_prefix,

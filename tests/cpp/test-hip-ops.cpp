@@ -1,0 +1,271 @@
+// levo::hip op drop-ins on device tensor views: SnakeBeta (the reference KAT of
+// tests/test-audio-ops.cpp:113-221 and the validation of
+// src/levo-audio-ops.cpp:10-30, 129-141), the fused residual norms and the
+// quantizer surface (tests/test-quantization.cpp:32-81), each also against
+// the oracle at a LeVo shape.
+#include "check.h"
+#include "levo-hip-audio-ops.h"
+#include "levo-hip-norms.h"
+#include "levo-hip-quantize.h"
+#include "levo_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <iostream>
+#include <vector>
+
+using namespace levo::hip;
+
+namespace {
+
+template <typename T>
+struct device_vec {
+    explicit device_vec(const std::vector<T> & host) : buf(host.size()), size(host.size()) {
+        buf.upload(host.data(), host.size(), nullptr);
+        synchronize(nullptr);
+    }
+    explicit device_vec(std::size_t n) : buf(n), size(n) {}
+    std::vector<T> get() const {
+        std::vector<T> out(size);
+        buf.download(out.data(), size, nullptr);
+        synchronize(nullptr);
+        return out;
+    }
+    T * data() { return buf.data(); }
+    device_buffer<T> buf;
+    std::size_t size;
+};
+
+std::vector<float> gaussian(std::size_t n, uint64_t seed, float scale = 1.0F, float shift = 0.0F) {
+    std::vector<float> v(n);
+    lo_gaussian_noise(v.data(), static_cast<int64_t>(n), seed);
+    for (auto & x : v) x = x * scale + shift;
+    return v;
+}
+
+std::vector<uint16_t> to_f16(const std::vector<float> & v) {
+    std::vector<uint16_t> h(v.size());
+    lo_fp32_to_fp16_row(v.data(), h.data(), static_cast<int64_t>(v.size()));
+    return h;
+}
+
+float rel_err(const std::vector<float> & got, const std::vector<float> & want) {
+    float worst = 0.0F;
+    for (std::size_t i = 0; i < got.size(); ++i) {
+        worst = std::max(worst, std::fabs(got[i] - want[i]) / std::max(std::fabs(want[i]), 1.0F));
+    }
+    return worst;
+}
+
+int32_t f16_order(uint16_t h) { return (h & 0x8000) ? -static_cast<int32_t>(h & 0x7fff) : static_cast<int32_t>(h); }
+
+int max_f16_ulp(const std::vector<uint16_t> & a, const std::vector<uint16_t> & b) {
+    int worst = 0;
+    for (std::size_t i = 0; i < a.size(); ++i) worst = std::max(worst, std::abs(f16_order(a[i]) - f16_order(b[i])));
+    return worst;
+}
+
+void snake_reference_kat() {
+    const std::vector<float> x = {-1.0F, 0.0F, 1.0F, -0.5F, 0.5F, 1.5F};
+    const std::vector<float> a = {std::log(2.0F), std::log(0.5F)};
+    const std::vector<float> b = {std::log(1.5F), std::log(0.75F)};
+    std::vector<float> expected;
+    for (std::size_t c = 0; c < 2; ++c) {
+        const float alpha = std::exp(a[c]);
+        const float beta = std::exp(b[c]) + 1.0e-9F;
+        for (std::size_t t = 0; t < 3; ++t) {
+            const float v = x[c * 3 + t];
+            const float s = std::sin(v * alpha);
+            expected.push_back(v + s * s / beta);
+        }
+    }
+    device_vec<float> dx(x), da(a), db(b), dy(std::size_t{6});
+    device_vec<uint16_t> ha(to_f16(a)), hb(to_f16(b));
+    const tensor_view in = make_tensor_view(dx.data(), LEVO_HIP_TYPE_F32, 3, 2, 1);
+    const tensor_view out = make_tensor_view(dy.data(), LEVO_HIP_TYPE_F32, 3, 2, 1);
+    const tensor_view alpha = make_tensor_view(da.data(), LEVO_HIP_TYPE_F32, 1, 2, 1);
+    const tensor_view beta = make_tensor_view(db.data(), LEVO_HIP_TYPE_F32, 1, 2, 1);
+    detail::snake_beta(&in, &alpha, &beta, &out);
+    std::vector<float> y = dy.get();
+    for (std::size_t i = 0; i < 6; ++i) CHECK(std::fabs(y[i] - expected[i]) <= 1.0e-6F);
+    const tensor_view alpha16 = make_tensor_view(ha.data(), LEVO_HIP_TYPE_F16, 1, 2, 1);
+    const tensor_view beta16 = make_tensor_view(hb.data(), LEVO_HIP_TYPE_F16, 1, 2, 1);
+    detail::snake_beta(&in, &alpha16, &beta16, &out);
+    y = dy.get();
+    for (std::size_t i = 0; i < 6; ++i) CHECK(std::fabs(y[i] - expected[i]) <= 2.0e-3F);
+    // Mixed parameter types widen the F16 one exactly.
+    detail::snake_beta(&in, &alpha, &beta16, &out);
+    y = dy.get();
+    for (std::size_t i = 0; i < 6; ++i) CHECK(std::fabs(y[i] - expected[i]) <= 2.0e-3F);
+
+    // Validation messages.
+    tensor_view bad = in;
+    bad.type = LEVO_HIP_TYPE_F16;
+    expect_throw<std::invalid_argument>("LeVo audio graph: SnakeBeta input is null",
+                                        [&] { detail::snake_beta(nullptr, &alpha, &beta, &out); });
+    expect_throw<std::invalid_argument>("LeVo audio graph: SnakeBeta input must be F32",
+                                        [&] { detail::snake_beta(&bad, &alpha, &beta, &out); });
+    tensor_view q = alpha;
+    q.type = LEVO_HIP_TYPE_Q8_0;
+    expect_throw<std::invalid_argument>("LeVo audio graph: SnakeBeta alpha_log must be F32 or F16",
+                                        [&] { detail::snake_beta(&in, &q, &beta, &out); });
+    expect_throw<std::invalid_argument>("LeVo audio graph: SnakeBeta beta_log is null",
+                                        [&] { detail::snake_beta(&in, &alpha, nullptr, &out); });
+    tensor_view wide = alpha;
+    wide.ne[0] = 2;
+    expect_throw<std::invalid_argument>("LeVo audio graph: SnakeBeta parameters must have shape [1, channels, 1]",
+                                        [&] { detail::snake_beta(&in, &wide, &beta, &out); });
+}
+
+// Two batches of a [T=2016, C=512] activation with padded rows, in place.
+void snake_parity() {
+    const int64_t T = 2016, C = 512, pitch = 2020, B = 2;
+    const std::vector<float> x = gaussian(static_cast<std::size_t>(pitch * C * B), 5, 2.0F);
+    const std::vector<float> a = gaussian(static_cast<std::size_t>(C), 6, 0.3F);
+    const std::vector<float> b = gaussian(static_cast<std::size_t>(C), 7, 0.3F);
+    device_vec<float> dx(x), da(a), db(b);
+    tensor_view in = make_tensor_view(dx.data(), LEVO_HIP_TYPE_F32, T, C, B);
+    in.nb[1] = static_cast<std::size_t>(pitch) * 4;
+    in.nb[2] = in.nb[1] * static_cast<std::size_t>(C);
+    in.nb[3] = in.nb[2] * static_cast<std::size_t>(B);
+    const tensor_view alpha = make_tensor_view(da.data(), LEVO_HIP_TYPE_F32, 1, C, 1);
+    const tensor_view beta = make_tensor_view(db.data(), LEVO_HIP_TYPE_F32, 1, C, 1);
+    detail::snake_beta(&in, &alpha, &beta, &in);
+    const std::vector<float> got = dx.get();
+    std::vector<float> packed(static_cast<std::size_t>(T * C)), want(static_cast<std::size_t>(T * C)), g(want.size());
+    for (int64_t bt = 0; bt < B; ++bt) {
+        for (int64_t c = 0; c < C; ++c) {
+            std::copy_n(x.begin() + (bt * C + c) * pitch, T, packed.begin() + c * T);
+            std::copy_n(got.begin() + (bt * C + c) * pitch, T, g.begin() + c * T);
+        }
+        lo_snake_beta_f32(packed.data(), a.data(), b.data(), want.data(), C, T, 4);
+        CHECK(rel_err(g, want) <= 1.0e-5F);
+        for (int64_t c = 0; c < C; ++c) {  // the row padding is untouched
+            for (int64_t t = T; t < pitch; ++t) {
+                const std::size_t i = static_cast<std::size_t>((bt * C + c) * pitch + t);
+                CHECK(got[i] == x[i]);
+            }
+        }
+    }
+}
+
+void norm_parity() {
+    const int64_t D = 2048, R = 756;
+    const std::size_t n = static_cast<std::size_t>(D * R);
+    const std::vector<uint16_t> x = to_f16(gaussian(n, 21)), d = to_f16(gaussian(n, 22));
+    const std::vector<uint16_t> w = to_f16(gaussian(static_cast<std::size_t>(D), 23, 0.02F, 1.0F));
+    const std::vector<uint16_t> bias = to_f16(gaussian(static_cast<std::size_t>(D), 24, 0.02F));
+    device_vec<uint16_t> dx(x), dd(d), dw(w), db(bias), dh(n), dy(n);
+    const tensor_view vx = make_tensor_view(dx.data(), LEVO_HIP_TYPE_F16, D, R);
+    const tensor_view vd = make_tensor_view(dd.data(), LEVO_HIP_TYPE_F16, D, R);
+    const tensor_view vh = make_tensor_view(dh.data(), LEVO_HIP_TYPE_F16, D, R);
+    const tensor_view vy = make_tensor_view(dy.data(), LEVO_HIP_TYPE_F16, D, R);
+    const tensor_view vw = make_tensor_view(dw.data(), LEVO_HIP_TYPE_F16, D);
+    const tensor_view vb = make_tensor_view(db.data(), LEVO_HIP_TYPE_F16, D);
+    std::vector<uint16_t> wh(n), wy(n);
+
+    residual_rms_norm(&vx, &vd, &vw, 1.0e-6F, &vh, &vy);
+    lo_residual_rms_norm_f16(x.data(), d.data(), w.data(), wh.data(), wy.data(), R, D, 1.0e-6F, 4);
+    CHECK(dh.get() == wh);
+    CHECK(max_f16_ulp(dy.get(), wy) <= 1);
+
+    residual_layer_norm(&vx, &vd, &vw, &vb, 1.0e-6F, &vh, &vy);
+    lo_residual_layer_norm_f16(x.data(), d.data(), w.data(), bias.data(), wh.data(), wy.data(), R, D, 1.0e-6F, 4);
+    CHECK(dh.get() == wh);
+    CHECK(max_f16_ulp(dy.get(), wy) <= 1);
+
+    // F32 tower, no residual.
+    const std::vector<float> xf = gaussian(n, 25), wf = gaussian(static_cast<std::size_t>(D), 26, 0.02F, 1.0F);
+    device_vec<float> fx(xf), fw(wf), fy(n);
+    const tensor_view vfx = make_tensor_view(fx.data(), LEVO_HIP_TYPE_F32, D, R);
+    const tensor_view vfy = make_tensor_view(fy.data(), LEVO_HIP_TYPE_F32, D, R);
+    const tensor_view vfw = make_tensor_view(fw.data(), LEVO_HIP_TYPE_F32, D);
+    residual_rms_norm(&vfx, nullptr, &vfw, 1.0e-5F, nullptr, &vfy);
+    std::vector<float> want(n);
+    lo_residual_rms_norm_f32(xf.data(), nullptr, wf.data(), nullptr, want.data(), R, D, 1.0e-5F, 4);
+    CHECK(rel_err(fy.get(), want) <= 1.0e-5F);
+
+    expect_throw<std::invalid_argument>("LeVo HIP norm: activation tensors must share one type",
+                                        [&] { residual_rms_norm(&vx, &vfx, &vw, 1.0e-6F, nullptr, &vy); });
+    expect_throw<std::invalid_argument>("LeVo HIP norm: weight must have shape [dim]", [&] {
+        const tensor_view short_w = make_tensor_view(dw.data(), LEVO_HIP_TYPE_F16, D - 1);
+        residual_rms_norm(&vx, nullptr, &short_w, 1.0e-6F, nullptr, &vy);
+    });
+}
+
+void quantize_surface() {
+    // tests/test-quantization.cpp:45-51: a 4 x 32 matrix with six live columns.
+    std::vector<float> original(32 * 4, 0.0F);
+    for (int row = 0; row < 4; ++row) {
+        for (int column = 0; column < 6; ++column) {
+            original[static_cast<std::size_t>(row * 32 + column)] = 0.03125F * static_cast<float>((row + 1) * (column + 1));
+        }
+    }
+    CHECK(row_size(LEVO_HIP_TYPE_Q8_0, 32) == 34 && row_size(LEVO_HIP_TYPE_Q4_0, 32) == 18);
+    CHECK(padded_input_columns(2200, LEVO_HIP_TYPE_Q8_0) == 2208);
+    CHECK(padded_input_columns(4400, LEVO_HIP_TYPE_Q4_0) == 4416);
+    CHECK(padded_input_columns(2200, LEVO_HIP_TYPE_F16) == 2200);
+    device_vec<float> src(original), deq(std::size_t{128});
+    device_vec<uint8_t> q(std::size_t{34 * 4});
+    CHECK(quantize_chunk(LEVO_HIP_TYPE_Q8_0, src.data(), q.data(), 0, 4, 32, nullptr) == 34 * 4);
+    std::vector<uint8_t> want(34 * 4);
+    CHECK(lo_quantize_chunk(LEVO_HIP_TYPE_Q8_0, original.data(), want.data(), 0, 4, 32) == want.size());
+    CHECK(q.get() == want);
+    dequantize_row(LEVO_HIP_TYPE_Q8_0, q.data(), deq.data(), 128);
+    const std::vector<float> back = deq.get();
+    const float input[6] = {0.25F, -0.5F, 0.75F, -1.0F, 1.25F, -1.5F};
+    for (int row = 0; row < 4; ++row) {
+        float expected = 0.0F, actual = 0.0F;
+        for (int column = 0; column < 6; ++column) {
+            expected += original[static_cast<std::size_t>(row * 32 + column)] * input[column];
+            actual += back[static_cast<std::size_t>(row * 32 + column)] * input[column];
+        }
+        CHECK(std::fabs(actual - expected) < 0.015F);
+    }
+    expect_throw<std::invalid_argument>(nullptr, [&] {
+        (void) quantize_chunk(LEVO_HIP_TYPE_Q8_0, src.data(), q.data(), 0, 4, 31, nullptr);
+    });
+
+    // write_tensor's chunk path: F16 [rows, 2200] -> zero-padded 2208-column Q4_0 / Q8_0.
+    const int64_t rows = 64, cols = 2200, padded = 2208;
+    const std::vector<uint16_t> h = to_f16(gaussian(static_cast<std::size_t>(rows * cols), 31, 0.02F));
+    device_vec<uint16_t> dh(h);
+    for (levo_hip_type t : {LEVO_HIP_TYPE_Q8_0, LEVO_HIP_TYPE_Q4_0}) {
+        const std::size_t bytes = row_size(t, padded) * static_cast<std::size_t>(rows);
+        device_vec<uint8_t> dq(bytes);
+        CHECK(quantize_rows(t, dh.data(), LEVO_HIP_TYPE_F16, cols, cols, dq.data(), rows, padded) == bytes);
+        std::vector<uint8_t> w(bytes);
+        CHECK(lo_quantize_f16_rows_padded(t, h.data(), rows, cols, padded, w.data()) == bytes);
+        CHECK(dq.get() == w);
+    }
+
+    // F16 row converters round-trip against the oracle.
+    const std::vector<float> f = gaussian(4099, 41, 100.0F);
+    device_vec<float> df(f), dback(std::size_t{4099});
+    device_vec<uint16_t> dhalf(std::size_t{4099});
+    fp32_to_fp16_row(df.data(), dhalf.data(), 4099);
+    fp16_to_fp32_row(dhalf.data(), dback.data(), 4099);
+    const std::vector<uint16_t> want_h = to_f16(f);
+    CHECK(dhalf.get() == want_h);
+    std::vector<float> want_back(4099);
+    lo_fp16_to_fp32_row(want_h.data(), want_back.data(), 4099);
+    const std::vector<float> got_back = dback.get();
+    CHECK(bit_equal(got_back.data(), want_back.data(), 4099));
+}
+
+} // namespace
+
+int main() {
+    try {
+        snake_reference_kat();
+        snake_parity();
+        norm_parity();
+        quantize_surface();
+    } catch (const std::exception & e) {
+        std::cerr << "unexpected exception: " << e.what() << '\n';
+        return 1;
+    }
+    std::cout << "hip ops ok\n";
+    return 0;
+}

@@ -21,14 +21,48 @@ def test_library_exports_every_declared_symbol(binding):
     assert not missing, missing
     for s in declared:
         assert hasattr(lib.lib, s)
-    assert lib.lib.levo_hip_abi_version() == 1
+    assert lib.lib.levo_hip_abi_version() == binding.header_abi_version()
 
 
 def test_host_library_links_kernel_library(binding):
-    if not os.path.exists(binding.HOST_LIB):
-        pytest.skip("host library not built")
+    assert os.path.exists(binding.HOST_LIB), "run __graft_entry__.build()"
     out = subprocess.run(["ldd", binding.HOST_LIB], capture_output=True, text=True, check=True).stdout
     assert "liblevo_hip.so" in out
+
+
+# The C++17 drop-in surface: each entry mirrors a reference declaration
+# (src/levo-sampling.h:13-64, src/levo-flow-renderer.h:44-51,
+# src/levo-audio-ops.h:30-33, tools/levo-quantize.cpp:386-388).
+HOST_API = [
+    "levo::hip::apply_cfg(std::vector<float, std::allocator<float> > const&, std::vector<float, std::allocator<float> > const&, float)",
+    "levo::hip::apply_unique_token_repetition_penalty(std::vector<float, std::allocator<float> >&, std::vector<long, std::allocator<long> > const&, float, unsigned long)",
+    "levo::hip::Sampler::sample(std::vector<float, std::allocator<float> > const&, unsigned long, float, bool)",
+    "levo::hip::Sampler::sample_streams(",
+    "levo::hip::Sampler::sample_device(",
+    "levo::hip::Sampler::restore(unsigned long, unsigned long)",
+    "levo::hip::Sampler::uniform_bits()",
+    "levo::hip::Sampler::uniform01()",
+    "levo::hip::sample_top_k(",
+    "levo::hip::flow::solve_flow_euler(",
+    "levo::hip::flow::solve_flow_euler_device(",
+    "levo::hip::detail::snake_beta(",
+    "levo::hip::residual_rms_norm(",
+    "levo::hip::residual_layer_norm(",
+    "levo::hip::quantize_chunk(",
+    "levo::hip::quantize_rows(",
+    "levo::hip::padded_input_columns(",
+    "levo::hip::row_size(",
+    "levo::hip::dequantize_row(",
+    "levo::hip::fp32_to_fp16_row(",
+    "levo::hip::fp16_to_fp32_row(",
+]
+
+
+def test_host_library_exports_the_dropin_api(binding):
+    out = subprocess.run(["nm", "-DC", "--defined-only", binding.HOST_LIB], capture_output=True, text=True,
+                         check=True).stdout
+    missing = [name for name in HOST_API if name not in out]
+    assert not missing, missing
 
 
 def test_validation_errors(binding):

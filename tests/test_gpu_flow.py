@@ -125,3 +125,66 @@ def test_fp16_row_converters(hip, dev, oracle):
     got, want = from_dev(out), oracle.f16_to_f32(allh)
     ok = ~np.isnan(want)
     assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32)) and np.all(np.isnan(got[~ok]))
+
+
+@pytest.mark.parametrize("n,offset", [(64 * 2520, 0), (4099, 0), (1001, 1)])
+def test_checked_euler_matches_unchecked_and_stays_clear(hip, dev, oracle, n, offset):
+    """The checked entry point updates bit-identically and leaves the flag 0."""
+    import torch
+    x0 = oracle.gaussian(n + offset, 31)
+    vu = oracle.gaussian(n + offset, 32)
+    vc = oracle.gaussian(n + offset, 33)
+    a, b = to_dev(x0, dev), to_dev(x0, dev)
+    du, dc = to_dev(vu, dev), to_dev(vc, dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    hip.flow_cfg_euler(a[offset:], du[offset:], dc[offset:], n, 1.5, 0.02)
+    hip.flow_cfg_euler_checked(b[offset:], du[offset:], dc[offset:], n, 1.5, 0.02, flags)
+    assert _eq(from_dev(a), from_dev(b))
+    assert int(flags.item()) == 0
+
+
+VEL, STATE = 1, 2
+
+
+@pytest.mark.parametrize("where", ["vector", "tail"])
+def test_checked_euler_flags_nonfinite_velocity_and_state(hip, dev, where):
+    """src/levo-flow-renderer.cpp:104, :106: a NaN/inf velocity or an
+    overflowing state is reported through the flag word."""
+    import torch
+    n = 4099
+    pos = 1234 if where == "vector" else n - 1
+    state = torch.zeros(n, dtype=torch.float32, device=dev)
+    vu = torch.ones(n, dtype=torch.float32, device=dev)
+    vc = torch.ones(n, dtype=torch.float32, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    hip.flow_cfg_euler_checked(state, vu, vc, n, 1.5, 0.02, flags)
+    assert int(flags.item()) == 0
+    vc[pos] = float("nan")
+    hip.flow_cfg_euler_checked(state, vu, vc, n, 1.5, 0.02, flags)
+    assert int(flags.item()) & VEL
+    vc[pos] = 1.0
+    flags.zero_()
+    state[pos] = 3.0e38
+    vu[pos] = 3.0e38
+    vc[pos] = 3.0e38
+    hip.flow_cfg_euler_checked(state, vu, vc, n, 1.5, 1.0, flags)  # finite v, state overflows
+    assert int(flags.item()) == STATE
+    flags.zero_()
+    hip.flow_cfg_euler_checked(state, vu, None, n, 1.5, 0.02, flags)  # inf state stays inf
+    assert int(flags.item()) == STATE
+
+
+@pytest.mark.parametrize("n,offset", [(1, 0), (5, 0), (4096, 0), (161_283, 0), (1003, 1), (10_000_000, 0)])
+def test_check_finite(hip, dev, n, offset):
+    import torch
+    x = torch.randn(n + offset, dtype=torch.float32, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    hip.check_finite(x[offset:], n, flags, 4)
+    assert int(flags.item()) == 0
+    for pos, bad in [(0, float("nan")), (n // 2, float("inf")), (n - 1, float("-inf"))]:
+        flags.zero_()
+        keep = float(x[offset + pos].item())
+        x[offset + pos] = bad
+        hip.check_finite(x[offset:], n, flags, 4)
+        assert int(flags.item()) == 4, (pos, bad)
+        x[offset + pos] = keep

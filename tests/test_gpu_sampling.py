@@ -258,3 +258,35 @@ def test_sampled_tokens_match_reference_sampler(hip, binding, dev, oracle, ref):
             assert got == want.tolist(), (seed, pos)
             recent = np.concatenate([recent[:, 1:], np.array(got, np.int64)[:, None]], axis=1)
         assert draws == s.draw_count
+
+
+@pytest.mark.parametrize("vocab,limit", [(16385, 16384), (16385, 0), (5, 3), (600_000, 0)])
+def test_standalone_repetition_penalty_matches_oracle(hip, dev, oracle, vocab, limit):
+    """levo_hip_repetition_penalty == apply_unique_token_repetition_penalty
+    (src/levo-sampling.cpp:39-47): duplicates divide once, ids outside
+    [0, limit) are ignored. 600,000 ids exercises the first-occurrence scan."""
+    import torch
+    rng = np.random.default_rng(vocab + limit)
+    logits = (rng.standard_normal(vocab) * 3).astype(np.float32)
+    top = limit if limit else vocab
+    recent = np.concatenate([rng.integers(0, top, 40), rng.integers(0, top, 10),
+                             [-1, -7, vocab, vocab + 5, top - 1, top - 1, 0, 0]]).astype(np.int64)
+    recent[45:50] = recent[0:5]  # forced duplicates
+    want = oracle.repetition_penalty(logits.copy(), recent, 1.1, limit)
+    d = to_dev(logits, dev)
+    r = torch.from_numpy(recent).to(dev)
+    hip.repetition_penalty(d, vocab, r, len(recent), 1.1, limit)
+    got = from_dev(d)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_standalone_repetition_penalty_reference_kat(hip, dev, binding):
+    """tests/test-sampling.cpp:9-11: {10,8,6} with {0,0,1}, penalty 2 -> {5,4,6};
+    a non-positive penalty is rejected with the reference's message."""
+    import torch
+    d = torch.tensor([10.0, 8.0, 6.0], device=dev)
+    r = torch.tensor([0, 0, 1], dtype=torch.int64, device=dev)
+    hip.repetition_penalty(d, 3, r, 3, 2.0)
+    assert from_dev(d).tolist() == [5.0, 4.0, 6.0]
+    with pytest.raises(binding.LevoHipError, match="repetition penalty must be finite and positive"):
+        hip.repetition_penalty(d, 3, r, 3, 0.0)
