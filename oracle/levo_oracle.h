@@ -13,7 +13,7 @@
  * (rms_norm/norm row reductions, quantize_row_q8_0_ref/q4_0_ref, fp16
  * conversion) are restated from ggml's published scalar algorithms.
  *
- * Pinning status per function (what checks it, see tests/test_oracle_*.py):
+ * Pinning status per function (what checks it: tests/test_oracle.py):
  *   lo_fp32_to_fp16 / lo_fp16_to_fp32 .... numpy float16 (IEEE RNE), exhaustive
  *   lo_snake_beta_f32 .................... reference KAT (tests/test-audio-ops.cpp:163-215),
  *                                          float64 closed form, special cases
