@@ -16,8 +16,11 @@ namespace levo_hip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxTileItems = kThreads * 4;        // vectors (or scalars) per tile at VPT=4
-constexpr int kMaxTileChannels = kMaxTileItems + 1; // channels one tile can touch
+
+// LDS bytes for the parameters of every channel a tile of `items` consecutive
+// vectors (or scalars) can touch, with `row` items per channel: a range of E
+// flattened indices spans at most (E - 1) / row + 2 rows.
+size_t tile_param_bytes(int64_t items, int64_t row, int64_t channels);
 
 // Exact n / d for n < 2^31 (Granlund-Montgomery with N = 31):
 // m = ceil(2^(31+l) / d), l = ceil(log2 d), q = (n * m) >> (31 + l).
@@ -68,10 +71,53 @@ __device__ __forceinline__ float div_by(float p, float beta, float rbeta) {
     return __builtin_fmaf(e, rbeta, q0);
 }
 
+// sin(m)^2 for |m| <= kSinSqFastMax. sin^2 has period pi, so one Cody-Waite
+// reduction m = k*pi + r (pi split into three F32 parts, each product and
+// subtraction one FMA) leaves |r| <= pi/2, where sin(r) = r + r^3 * P(r^2)
+// with P of degree 4. The coefficients are a least-squares fit with Lawson
+// reweighting towards the minimax absolute error on [0, pi/2] (1.9e-11 in
+// double); after F32 rounding of coefficients and arithmetic the result is
+// within 2.4e-7 of sin^2 over |m| <= 8192, the same size as the error of
+// squaring a correctly rounded F32 sine.
+constexpr float kSinSqFastMax = 8192.0f;
+
+__device__ __forceinline__ float sin_sq_reduced(float m) {
+    constexpr float kInvPi = 0x1.45f306p-2f;
+    constexpr float kPi1 = 0x1.921fb6p+1f;   // pi rounded to F32
+    constexpr float kPi2 = -0x1.777a5cp-24f; // pi - kPi1 rounded to F32
+    constexpr float kPi3 = -0x1.ee59dap-49f; // pi - kPi1 - kPi2
+    constexpr float c3 = -0x1.555556p-3f;
+    constexpr float c5 = 0x1.11110ap-7f;
+    constexpr float c7 = -0x1.a01770p-13f;
+    constexpr float c9 = 0x1.7164e2p-19f;
+    constexpr float c11 = -0x1.9982bcp-26f;
+    const float k = __builtin_rintf(m * kInvPi);
+    float r = __builtin_fmaf(-k, kPi1, m);
+    r = __builtin_fmaf(-k, kPi2, r);
+    r = __builtin_fmaf(-k, kPi3, r);
+    const float r2 = r * r;
+    float p = __builtin_fmaf(r2, c11, c9);
+    p = __builtin_fmaf(r2, p, c7);
+    p = __builtin_fmaf(r2, p, c5);
+    p = __builtin_fmaf(r2, p, c3);
+    const float s = __builtin_fmaf(r * r2, p, r);
+    return s * s;
+}
+
+// ggml_sqr(ggml_sin(m)): the reduced form, or sinf for |m| beyond it and for
+// NaN / infinity (the branch is skipped unless a lane needs it).
+__device__ __forceinline__ float sin_sq(float m) {
+    float p = sin_sq_reduced(m);
+    if (!(__builtin_fabsf(m) <= kSinSqFastMax)) {
+        const float s = sinf(m);
+        p = s * s;
+    }
+    return p;
+}
+
 __device__ __forceinline__ float snake(float x, const snake_param & q) {
     const float m = x * q.alpha;    // ggml_mul(input, alpha)
-    const float s = sinf(m);        // ggml_sin
-    const float p = s * s;          // ggml_sqr
+    const float p = sin_sq(m);      // ggml_sin, ggml_sqr
     const float d = div_by(p, q.beta, q.rbeta);  // ggml_div(periodic, beta)
     return x + d;                   // ggml_add(input, .)
 }
@@ -96,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void snake_beta_vec(
         const float * x, int64_t x_stride, const P * __restrict__ alpha_log,
         const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total4,
         fast_div div_t4) {
-    __shared__ snake_param params[kMaxTileChannels];
+    extern __shared__ snake_param params[];  // sized by tile_param_bytes
     constexpr uint32_t tile = kThreads * VPT;
     const uint32_t first = blockIdx.x * tile;
     const uint32_t last = min(first + tile, total4) - 1;
@@ -140,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void snake_beta_scalar(
         const float * x, int64_t x_stride, const P * __restrict__ alpha_log,
         const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total,
         fast_div div_t) {
-    __shared__ snake_param params[kMaxTileChannels];
+    extern __shared__ snake_param params[];  // sized by tile_param_bytes
     constexpr uint32_t tile = kThreads * 4;
     const uint32_t first = blockIdx.x * tile;
     const uint32_t last = min(first + tile, total) - 1;
@@ -160,6 +206,20 @@ __global__ __launch_bounds__(kThreads) void snake_beta_scalar(
     }
 }
 
+size_t tile_param_bytes(int64_t items, int64_t row, int64_t channels) {
+    const int64_t span = (items - 1) / row + 2;
+    return static_cast<size_t>(span < channels ? span : channels) * sizeof(snake_param);
+}
+
+template <typename P, int VPT>
+void launch_vec(const float * x, int64_t x_stride, const P * a, const P * b, float * y, int64_t y_stride,
+                int64_t channels, uint32_t total4, uint32_t t4, hipStream_t stream) {
+    const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads * VPT));
+    const size_t lds = tile_param_bytes(kThreads * VPT, t4, channels);
+    snake_beta_vec<P, VPT><<<grid, kThreads, lds, stream>>>(x, x_stride, a, b, y, y_stride, total4,
+                                                            make_fast_div(t4));
+}
+
 template <typename P>
 int launch_snake(const float * x, int64_t x_stride, const P * a, const P * b, float * y,
                  int64_t y_stride, int64_t channels, int64_t time, hipStream_t stream) {
@@ -168,23 +228,19 @@ int launch_snake(const float * x, int64_t x_stride, const P * a, const P * b, fl
                      aligned16(x) && aligned16(y);
     if (vec) {
         const uint32_t total4 = static_cast<uint32_t>(total / 4);
-        const fast_div d = make_fast_div(static_cast<uint32_t>(time / 4));
-        // Fill the chip: keep >= ~4096 workgroups before widening the tile.
-        if (total4 >= 4096u * kThreads * 4u) {
-            const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads * 4));
-            snake_beta_vec<P, 4><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride, total4, d);
-        } else if (total4 >= 4096u * kThreads * 2u) {
-            const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads * 2));
-            snake_beta_vec<P, 2><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride, total4, d);
-        } else {
-            const uint32_t grid = static_cast<uint32_t>(ceil_div(total4, kThreads));
-            snake_beta_vec<P, 1><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride, total4, d);
-        }
+        const uint32_t t4 = static_cast<uint32_t>(time / 4);
+        // Vectors per thread by size, as measured on MI355X: one for small
+        // tensors (most workgroups in flight), four in the mid range, two
+        // for the largest (fewest parameter set-ups without a long tail).
+        if (total4 < (1u << 20)) launch_vec<P, 1>(x, x_stride, a, b, y, y_stride, channels, total4, t4, stream);
+        else if (total4 < (1u << 23)) launch_vec<P, 4>(x, x_stride, a, b, y, y_stride, channels, total4, t4, stream);
+        else launch_vec<P, 2>(x, x_stride, a, b, y, y_stride, channels, total4, t4, stream);
     } else {
-        const fast_div d = make_fast_div(static_cast<uint32_t>(time));
         const uint32_t grid = static_cast<uint32_t>(ceil_div(total, kThreads * 4));
-        snake_beta_scalar<P><<<grid, kThreads, 0, stream>>>(x, x_stride, a, b, y, y_stride,
-                                                           static_cast<uint32_t>(total), d);
+        const size_t lds = tile_param_bytes(kThreads * 4, time, channels);
+        snake_beta_scalar<P><<<grid, kThreads, lds, stream>>>(x, x_stride, a, b, y, y_stride,
+                                                             static_cast<uint32_t>(total),
+                                                             make_fast_div(static_cast<uint32_t>(time)));
     }
     return launch_status("levo_hip_snake_beta");
 }
