@@ -1,11 +1,11 @@
-// Fused residual add + RMSNorm / LayerNorm, one wave64 per row.
+// Fused residual add + RMSNorm / LayerNorm, one 4-wave workgroup per row.
 //
-// Each row (dim contiguous elements) is owned by one wavefront: every load
-// of the row (x, delta, weight, bias) is issued up front with dwordx4
-// accesses, the row stays in registers, is reduced with cross-lane shuffles
-// (no LDS, no barrier), normalised and written once. The reduction
-// accumulates in double like ggml-cpu's ggml_float row sums, so the F32 mean
-// / variance (and hence every rounding point after it) matches the CPU chain.
+// Every load of the row (x, delta, weight, bias) is issued up front with
+// dwordx4 accesses, the row stays in registers, is reduced with cross-lane
+// shuffles and one LDS exchange between the four waves, normalised and
+// written once. The reduction accumulates in double like ggml-cpu's ggml_float
+// row sums, so the F32 mean / variance (and hence every rounding point after
+// it) matches the CPU chain.
 //
 //   RMSNorm F16 (src/levo-kv.cpp:153-160, residual :462/:507):
 //     h = f16(x + d); n = f16(h * 1/sqrtf(mean(h^2) + eps)); y = f16(n * w)
@@ -14,8 +14,9 @@
 //     h = x + d; v = h - mean; scale = 1/sqrtf(mean(v^2) + eps);
 //     y = ((v * scale) * gamma) + beta   (F16 storage: h and y rounded to F16)
 //
-// Rows whose length is not a multiple of 8 (or unaligned buffers) take a
-// loop kernel that reads the row from L2 again per pass.
+// Rows whose length is not a multiple of 8, longer than 8192, or unaligned
+// buffers take a loop kernel (one wave per row) that reads the row from L2
+// again per pass.
 #include "common.hpp"
 
 #include <type_traits>
@@ -26,6 +27,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kVec = 8;  // elements per lane per group (16 B of F16, 32 B of F32)
+constexpr int kRowWaves = 4;  // waves sharing one row in the vector kernel
 
 template <typename T>
 __device__ __forceinline__ void load8(const T * p, float (&o)[kVec]);
@@ -85,28 +87,29 @@ __device__ __forceinline__ float norm_out(float n, float w, float b) {
 }
 
 // T: activation storage (uint16_t = F16, float); P: parameter storage.
-// NV groups of 8 elements per lane (dim <= 512 * NV).
-// x / d may alias h_out or y (in-place residual): every load precedes every
-// store of the row in program order, so no __restrict__ on them.
-template <typename T, typename P, bool kLayer, int NV>
-__global__ __launch_bounds__(kThreads) void norm_kernel(const T * x, const T * d, const P * __restrict__ w,
-                                                        const P * __restrict__ b, T * h_out, T * y,
-                                                        int64_t rows, int dim, float eps) {
+// One row per workgroup of W waves; lane groups g = tid + 64*W*j, NV groups of
+// 8 elements per lane (dim <= 512 * W * NV). The wave sums meet in LDS and are
+// added in wave order.
+// x / d may alias h_out or y (in-place residual): each element is loaded and
+// stored by the same lane, loads first, so no __restrict__ on them.
+template <typename T, typename P, bool kLayer, int NV, int W>
+__global__ __launch_bounds__(64 * W) void norm_kernel_wg(const T * x, const T * d, const P * __restrict__ w,
+                                                         const P * __restrict__ b, T * h_out, T * y,
+                                                         int64_t rows, int dim, float eps) {
     constexpr bool kF16 = std::is_same<T, uint16_t>::value;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-    if (row >= rows) return;  // whole wavefront leaves; no block barrier follows
+    __shared__ double part[2][W];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int64_t row = blockIdx.x;
     const T * xr = x + row * dim;
     const T * dr = d ? d + row * dim : nullptr;
     T * hr = h_out ? h_out + row * dim : nullptr;
     T * yr = y + row * dim;
-
-    // ---- every load first: groups past dim read a clamped, valid address ----
     bool in[NV];
     int off[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = (lane + 64 * j) * kVec;
+        const int e = (tid + 64 * W * j) * kVec;
         in[j] = e < dim;
         off[j] = in[j] ? e : 0;
     }
@@ -132,8 +135,6 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const T * x, const T * d
         load8(w + off[j], wv[j]);
         if constexpr (kLayer) load8(b + off[j], bv[j]);
     }
-
-    // ---- residual, statistics ---------------------------------------------------
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -160,7 +161,11 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const T * x, const T * d
         }
     }
     acc = wave_sum_f64(acc);
-
+    if ((tid & 63) == 0) part[0][wave] = acc;
+    __syncthreads();
+    acc = part[0][0];
+#pragma unroll
+    for (int i = 1; i < W; ++i) acc += part[0][i];
     float scale;
     if constexpr (kLayer) {
         const float mean = static_cast<float>(acc / static_cast<double>(dim));
@@ -175,14 +180,17 @@ __global__ __launch_bounds__(kThreads) void norm_kernel(const T * x, const T * d
             }
         }
         acc2 = wave_sum_f64(acc2);
+        if ((tid & 63) == 0) part[1][wave] = acc2;
+        __syncthreads();
+        acc2 = part[1][0];
+#pragma unroll
+        for (int i = 1; i < W; ++i) acc2 += part[1][i];
         const float variance = static_cast<float>(acc2 / static_cast<double>(dim));
         scale = 1.0f / sqrtf(variance + eps);
     } else {
         const float ms = static_cast<float>(acc / static_cast<double>(dim));
         scale = 1.0f / sqrtf(ms + eps);
     }
-
-    // ---- normalise and store ---------------------------------------------------------
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         if (in[j]) {
@@ -260,20 +268,17 @@ int launch_norm(const void * xv, const void * dv, const void * wv, const void * 
     const int64_t grid = ceil_div(rows, kWaves);
     const bool vec = dim % kVec == 0 && aligned16(x) && (d == nullptr || aligned16(d)) && aligned16(w) &&
                      (b == nullptr || aligned16(b)) && (h == nullptr || aligned16(h)) && aligned16(y) &&
-                     dim <= 64 * kVec * 16;
+                     dim <= 64 * kRowWaves * kVec * 4;
     if (vec) {
-        const int groups = static_cast<int>(ceil_div(dim, 64 * kVec));
-#define LEVO_NORM_CASE(NVV)                                                                                 \
-        if (groups <= NVV) {                                                                                \
-            norm_kernel<T, P, kLayer, NVV><<<grid, kThreads, 0, stream>>>(x, d, w, b, h, y, rows, dim, eps); \
-            return launch_status("levo_hip_residual_norm");                                                 \
-        }
-        LEVO_NORM_CASE(1)
-        LEVO_NORM_CASE(2)
-        LEVO_NORM_CASE(4)
-        LEVO_NORM_CASE(8)
-        LEVO_NORM_CASE(16)
-#undef LEVO_NORM_CASE
+        // One row per 4-wave workgroup: 8 values per lane at dim 2048, so the
+        // per-lane chain load -> reduce -> store is short and every CU gets rows.
+        constexpr int W = kRowWaves;
+        const int groups = static_cast<int>(ceil_div(dim, 64 * W * kVec));
+        const hipStream_t s = stream;
+        if (groups <= 1) norm_kernel_wg<T, P, kLayer, 1, W><<<rows, 64 * W, 0, s>>>(x, d, w, b, h, y, rows, dim, eps);
+        else if (groups <= 2) norm_kernel_wg<T, P, kLayer, 2, W><<<rows, 64 * W, 0, s>>>(x, d, w, b, h, y, rows, dim, eps);
+        else norm_kernel_wg<T, P, kLayer, 4, W><<<rows, 64 * W, 0, s>>>(x, d, w, b, h, y, rows, dim, eps);
+        return launch_status("levo_hip_residual_norm");
     }
     norm_kernel_loop<T, P, kLayer><<<grid, kThreads, 0, stream>>>(x, d, w, b, h, y, rows, dim, eps);
     return launch_status("levo_hip_residual_norm");
