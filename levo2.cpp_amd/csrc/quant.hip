@@ -6,13 +6,12 @@
 //   Q4_0: max = first value of largest |x|; d = max/-8; id = d ? 1/d : 0;
 //         q = min(15, (int8)(x*id + 8.5)); qs[j] = q[j] | q[j+16] << 4
 // with d stored as IEEE F16 (RNE). Blocks are 34 / 18 bytes and therefore not
-// naturally aligned; each wave quantizes a group of 8 or 16 consecutive blocks
-// (a 16-byte-aligned byte range), assembles them in LDS and writes the group
-// with dwordx4 stores, so every HBM access is coalesced and aligned.
+// naturally aligned.
 //
-// Source layout: lanes own 16 contiguous source bytes each (8 F16 or 4 F32
-// values); 4 (F16) or 8 (F32) lanes form one block and reduce its max with
-// cross-lane shuffles.
+// Quantize: one lane per block; the wave's 64 consecutive blocks (a
+// 16-byte-aligned byte range) are assembled in LDS and written with dwordx4
+// stores. Dequantize: a wave stages 32 blocks in LDS and writes their values
+// as contiguous 16-byte chunks.
 #include "common.hpp"
 
 #include <type_traits>
@@ -25,13 +24,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kQ8Bytes = 34;
 constexpr int kQ4Bytes = 18;
 
-// (int8_t)f as x86-64 computes it for the reference: truncation, with the
-// invalid (non-finite / out-of-int32) case giving 0x80000000 -> low byte 0.
-__device__ __forceinline__ int trunc_i8(float f) {
-    if (!(fabsf(f) < 2147483648.0f)) return 0;
-    return static_cast<int8_t>(static_cast<int32_t>(f));
-}
-
 template <int QT>
 struct qtraits;
 template <>
@@ -43,30 +35,38 @@ struct qtraits<LEVO_HIP_TYPE_Q4_0> {
     static constexpr int bytes = kQ4Bytes;
 };
 
-// Loads this lane's N source values (N = 8 for F16, 4 for F32) of column
-// col0.. of one row, zero beyond src_cols (row padding, write_tensor :375-384).
-template <typename S, int N, bool kVec>
-__device__ __forceinline__ void load_src(const S * row, int64_t col0, int64_t src_cols, float (&x)[N]) {
-    if constexpr (kVec) {
-        if (col0 < src_cols) {
-            if constexpr (std::is_same<S, uint16_t>::value) {
-                const u16x8 v = *reinterpret_cast<const u16x8 *>(row + col0);
+// Loads one 32-value block starting at column col0 of a source row, zero
+// beyond src_cols (row padding, write_tensor :375-384). kVec: the row start is
+// 16-byte aligned, so a block that lies wholly inside the row takes dwordx4
+// loads (4 for F16, 8 for F32).
+template <typename S, bool kVec>
+__device__ __forceinline__ void load_block(const S * row, int64_t col0, int64_t src_cols, float (&x)[32]) {
+    if (kVec && col0 + 32 <= src_cols) {
+        if constexpr (std::is_same<S, uint16_t>::value) {
+            const u16x8 * p = reinterpret_cast<const u16x8 *>(row + col0);
+            u16x8 v[4];
 #pragma unroll
-                for (int k = 0; k < N; ++k) x[k] = h2f(v[k]);
-            } else {
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(row + col0);
-                x[0] = v.x;
-                x[1] = v.y;
-                x[2] = v.z;
-                x[3] = v.w;
-            }
+            for (int i = 0; i < 4; ++i) v[i] = __builtin_nontemporal_load(p + i);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) x[i * 8 + k] = h2f(v[i][k]);
         } else {
+            const f32x4 * p = reinterpret_cast<const f32x4 *>(row + col0);
+            f32x4 v[8];
 #pragma unroll
-            for (int k = 0; k < N; ++k) x[k] = 0.0f;
+            for (int i = 0; i < 8; ++i) v[i] = __builtin_nontemporal_load(p + i);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                x[i * 4 + 0] = v[i].x;
+                x[i * 4 + 1] = v[i].y;
+                x[i * 4 + 2] = v[i].z;
+                x[i * 4 + 3] = v[i].w;
+            }
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
+        for (int k = 0; k < 32; ++k) {
             const int64_t c = col0 + k;
             if (c < src_cols) {
                 if constexpr (std::is_same<S, uint16_t>::value) x[k] = h2f(row[c]);
@@ -78,187 +78,318 @@ __device__ __forceinline__ void load_src(const S * row, int64_t col0, int64_t sr
     }
 }
 
-__device__ __forceinline__ void lds_put16(uint8_t * lds, int off, uint32_t v16) {
-    *reinterpret_cast<uint16_t *>(lds + off) = static_cast<uint16_t>(v16);
+// roundf (half away from zero) is trunc(v + copysign(0.5 - 2^-25, v)): the
+// two agree for every non-NaN float (checked exhaustively), and NaN stays NaN.
+// low_byte_i8 truncates toward zero itself, so callers pass the sum and the
+// trunc is left to the conversion.
+__device__ __forceinline__ float half_away_offset(float v) {
+    return v + __builtin_copysignf(0x1.fffffep-2f, v);
 }
 
-// QT block type; S source element; kVec = dwordx4 source path.
-template <int QT, typename S, bool kVec>
-__global__ __launch_bounds__(kThreads) void quantize_kernel(const S * __restrict__ src, int64_t src_cols,
-                                                            int64_t src_stride, uint8_t * __restrict__ dst,
-                                                            int64_t nblocks_row, int64_t nblocks, bool dst_vec) {
-    constexpr bool kF16 = std::is_same<S, uint16_t>::value;
-    constexpr int N = kF16 ? 8 : 4;           // values per lane
-    constexpr int LPB = 32 / N;               // lanes per block
-    constexpr int BPW = 64 / LPB;             // blocks per wave group
-    constexpr int QB = qtraits<QT>::bytes;
-    constexpr int GB = BPW * QB;              // group bytes (multiple of 16)
-    __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][GB];
+// (int8_t)v as the reference's x86-64 build computes it: truncation to int32
+// (cvttss2si), low byte kept. v_cvt_i32_f32 truncates too and gives 0 for NaN
+// where cvttss2si gives 0x80000000 (low byte 0 as well); the two differ only
+// beyond +-2^31, which the callers exclude (x * id stays within +-128 while id
+// is finite; an id of +inf is replaced by NaN first). Inline asm because a
+// C++ float -> int conversion of NaN is undefined.
+__device__ __forceinline__ uint32_t low_byte_i8(float v) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return static_cast<uint32_t>(r) & 0xffu;
+}
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int64_t group = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
-    const int64_t b0 = group * BPW;
-    const int part = lane % LPB;
-    const int64_t blk = b0 + lane / LPB;
-    const bool valid = blk < nblocks;
-    uint8_t * lds = stage[wave];
+// id = 1/d is +inf only when d underflows; then every x * id is +-inf or NaN
+// and the reference's (int8_t) conversion yields 0 for each (cvttss2si gives
+// 0x80000000). Replacing such an id by NaN makes every product NaN, which
+// low_byte_i8 maps to 0 as well, so the per-value code needs no special case.
+__device__ __forceinline__ float nan_if_inf(float id) {
+    return __builtin_isinf(id) ? __builtin_nanf("") : id;
+}
 
-    float x[N];
-    if (valid) {
-        const int64_t r = blk / nblocks_row;
-        const int64_t cb = blk - r * nblocks_row;
-        load_src<S, N, kVec>(src + r * src_stride, cb * 32 + part * N, src_cols, x);
-    } else {
+__device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return a | (b << 8) | (c << 16) | (d << 24);
+}
+
+// Writes one block (F16 scale d16, then NW little-endian dwords of packed
+// quants) to LDS at byte offset base = lane * (2 + 4 * NW) with 4-byte aligned
+// stores only: base is 4-aligned for even lanes and 2 mod 4 for odd ones, so
+// odd lanes store d16 and then the dwords as they are, even lanes store
+// dwords shifted by 16 bits (d16 first) and the last half-word on its own.
+template <int NW>
+__device__ __forceinline__ void stage_block(uint8_t * lds, int lane, uint32_t d16, const uint32_t (&pk)[NW]) {
+    constexpr int QB = 2 + 4 * NW;
+    const int base = lane * QB;
+    const bool odd = lane & 1;
+    uint32_t * words = reinterpret_cast<uint32_t *>(lds + base + (odd ? 2 : 0));
 #pragma unroll
-        for (int k = 0; k < N; ++k) x[k] = 0.0f;
+    for (int i = 0; i < NW; ++i) {
+        const uint32_t shifted = i == 0 ? (d16 | (pk[0] << 16)) : __builtin_amdgcn_alignbit(pk[i], pk[i - 1], 16);
+        words[i] = odd ? pk[i] : shifted;
     }
-    const int lb = (lane / LPB) * QB;  // block offset in the group
+    *reinterpret_cast<uint16_t *>(lds + base + (odd ? 0 : QB - 2)) =
+            static_cast<uint16_t>(odd ? d16 : (pk[NW - 1] >> 16));
+}
 
+// Quantizes one block of 32 values in ggml's reference order and stages it
+// in LDS (stage_block) for lane `lane`.
+template <int QT>
+__device__ __forceinline__ void quantize_block(const float (&x)[32], uint8_t * lds, int lane) {
     if constexpr (QT == LEVO_HIP_TYPE_Q8_0) {
         float amax = 0.0f;
 #pragma unroll
-        for (int k = 0; k < N; ++k) amax = amax > fabsf(x[k]) ? amax : fabsf(x[k]);
-#pragma unroll
-        for (int o = 1; o < LPB; o <<= 1) {
-            const float t = __shfl_xor(amax, o, 64);
-            amax = amax > t ? amax : t;
+        for (int k = 0; k < 32; ++k) {
+            const float v = fabsf(x[k]);
+            amax = amax > v ? amax : v;  // MAX(amax, fabsf(v))
         }
         const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        if (part == 0) lds_put16(lds, lb, f2h(d));
-        uint32_t q[N];
+        const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
+        uint32_t pk[8];
 #pragma unroll
-        for (int k = 0; k < N; ++k) q[k] = static_cast<uint8_t>(trunc_i8(roundf(x[k] * id)));
+        for (int w = 0; w < 8; ++w) {
+            uint32_t q[4];
 #pragma unroll
-        for (int k = 0; k < N; k += 2) lds_put16(lds, lb + 2 + part * N + k, q[k] | (q[k + 1] << 8));
+            for (int k = 0; k < 4; ++k) q[k] = low_byte_i8(half_away_offset(x[4 * w + k] * id));  // (int8_t)roundf(x * id)
+            pk[w] = pack4(q[0], q[1], q[2], q[3]);
+        }
+        stage_block<8>(lds, lane, f2h(d), pk);
     } else {
-        // signed value of the first largest |x| (strictly greater replaces)
         float amax = 0.0f, vmax = 0.0f;
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
+        for (int k = 0; k < 32; ++k) {
             if (amax < fabsf(x[k])) {
                 amax = fabsf(x[k]);
                 vmax = x[k];
             }
         }
-        int owner = part;
-#pragma unroll
-        for (int o = 1; o < LPB; o <<= 1) {
-            const float ta = __shfl_xor(amax, o, 64);
-            const float tv = __shfl_xor(vmax, o, 64);
-            const int to = __shfl_xor(owner, o, 64);
-            if (ta > amax || (ta == amax && to < owner)) {
-                amax = ta;
-                vmax = tv;
-                owner = to;
-            }
-        }
         const float d = vmax / -8.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        if (part == 0) lds_put16(lds, lb, f2h(d));
-        uint32_t nib = 0;  // this lane's N nibbles, value k at bits 4k
+        const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
+        uint32_t pk[4];
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
-            int qi = trunc_i8(x[k] * id + 8.5f);
-            qi = qi < 15 ? qi : 15;
-            nib |= (static_cast<uint32_t>(qi) & 0xfu) << (4 * k);
-        }
-        // values j (parts < LPB/2) pair with j + 16 (parts >= LPB/2)
-        const uint32_t hi = __shfl_down(nib, LPB / 2, 64);
-        if (part < LPB / 2) {
+        for (int w = 0; w < 4; ++w) {
+            uint32_t b[4];
 #pragma unroll
-            for (int k = 0; k < N; k += 2) {
-                const uint32_t b_lo = ((nib >> (4 * k)) & 0xfu) | (((hi >> (4 * k)) & 0xfu) << 4);
-                const uint32_t b_hi = ((nib >> (4 * k + 4)) & 0xfu) | (((hi >> (4 * k + 4)) & 0xfu) << 4);
-                lds_put16(lds, lb + 2 + part * N + k, b_lo | (b_hi << 8));
+            for (int k = 0; k < 4; ++k) {
+                const int j = 4 * w + k;
+                const uint32_t c0 = low_byte_i8(x[j] * id + 8.5f);
+                const uint32_t c1 = low_byte_i8(x[j + 16] * id + 8.5f);
+                const uint32_t q0 = c0 < 15u ? c0 : 15u;
+                const uint32_t q1 = c1 < 15u ? c1 : 15u;
+                b[k] = q0 | (q1 << 4);
             }
+            pk[w] = pack4(b[0], b[1], b[2], b[3]);
+        }
+        stage_block<4>(lds, lane, f2h(d), pk);
+    }
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+    // Only this wave touches its LDS region, and one wave's LDS operations
+    // complete in issue order: a wavefront-scope fence is enough.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Packed rows (source value i of block b is src[32 b + i]), 16-byte aligned
+// source. The wave's 64 blocks are read with coalesced dwordx4 loads (lane l
+// takes 16-byte chunks l, l + 64, ...), transposed through LDS (each block in
+// its own 16-byte-padded slot, so the per-lane reads of one block spread over
+// distinct bank groups), and each lane then quantizes one block.
+template <int QT, typename S>
+__global__ __launch_bounds__(kThreads) void quantize_dense_kernel(const S * __restrict__ src,
+                                                                  uint8_t * __restrict__ dst, int64_t nblocks,
+                                                                  bool dst_vec) {
+    constexpr int QB = qtraits<QT>::bytes;
+    constexpr int CPB = 32 * static_cast<int>(sizeof(S)) / 16;  // 16-byte chunks per block: 4 (F16) or 8 (F32)
+    constexpr int SLOT = (CPB + 1) * 16;                        // padded block slot in LDS
+    constexpr int STAGE = 64 * SLOT;                            // >= 64 * QB output bytes
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][STAGE];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * 64;
+    uint8_t * lds = stage[wave];
+    const u32x4 * in = reinterpret_cast<const u32x4 *>(src);
+    const int64_t last = nblocks * CPB - 1;  // last valid chunk of the source
+
+    // Every load is issued before any is used: chunks past the end read the
+    // last valid chunk (no branch around a load) and are zeroed afterwards.
+    u32x4 v[CPB];
+#pragma unroll
+    for (int j = 0; j < CPB; ++j) {
+        const int64_t g = b0 * CPB + lane + 64 * j;
+        v[j] = __builtin_nontemporal_load(in + (g < last ? g : last));
+    }
+#pragma unroll
+    for (int j = 0; j < CPB; ++j) {
+        if (b0 * CPB + lane + 64 * j > last) v[j] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < CPB; ++j) {
+        const int c = lane + 64 * j;
+        *reinterpret_cast<u32x4 *>(lds + (c / CPB) * SLOT + (c % CPB) * 16) = v[j];
+    }
+    wave_lds_fence();
+    float x[32];
+#pragma unroll
+    for (int j = 0; j < CPB; ++j) {
+        const u32x4 w = *reinterpret_cast<const u32x4 *>(lds + lane * SLOT + j * 16);
+        if constexpr (std::is_same<S, uint16_t>::value) {
+            const u16x8 h = __builtin_bit_cast(u16x8, w);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[j * 8 + k] = h2f(h[k]);
+        } else {
+            // Cast the whole vector: ROCm 7.2's clang lowers a bit_cast of a
+            // single ext_vector element (w.y, ...) as a cast of element 0.
+            const f32x4 f = __builtin_bit_cast(f32x4, w);
+            x[j * 4 + 0] = f.x;
+            x[j * 4 + 1] = f.y;
+            x[j * 4 + 2] = f.z;
+            x[j * 4 + 3] = f.w;
         }
     }
-    __syncthreads();
+    // The output reuses the stage: the fence keeps every read above ahead of
+    // the writes below, and the wave's LDS operations execute in that order.
+    wave_lds_fence();
+    quantize_block<QT>(x, lds, lane);
+    wave_lds_fence();
 
-    // write the group: dwordx4 when the whole group is valid and dst is
-    // 16-byte aligned (groups start at multiples of 16 bytes), u16 otherwise
     uint8_t * out = dst + b0 * QB;
     const int64_t nvalid = nblocks - b0;
-    if (nvalid >= BPW && dst_vec) {
-        if (lane < GB / 16)
-            reinterpret_cast<u32x4 *>(out)[lane] = reinterpret_cast<const u32x4 *>(lds)[lane];
+    if (nvalid >= 64 && dst_vec) {
+        for (int i = lane; i < 64 * QB / 16; i += 64)
+            reinterpret_cast<u32x4 *>(out)[i] = reinterpret_cast<const u32x4 *>(lds)[i];
     } else if (nvalid > 0) {
-        const int nbytes = static_cast<int>(nvalid < BPW ? nvalid : BPW) * QB;
+        const int nbytes = static_cast<int>(nvalid < 64 ? nvalid : 64) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)
             reinterpret_cast<uint16_t *>(out)[i] = reinterpret_cast<const uint16_t *>(lds)[i];
     }
 }
 
-// Dequantize: each wave reads a group of 16 blocks (16-byte aligned range),
-// stages it in LDS, and each lane expands 8 values of one block.
+// QT block type; S source element; kVec: dwordx4 source loads.
+// One lane quantizes one 32-value block, scanning it in index order exactly as
+// ggml's reference quantizer (so the max, its first occurrence and NaN
+// handling match); the wave's 64 blocks are assembled in LDS and written as
+// 16-byte stores (64 * 34 and 64 * 18 bytes are multiples of 16).
+template <int QT, typename S, bool kVec>
+__global__ __launch_bounds__(kThreads) void quantize_kernel(const S * __restrict__ src, int64_t src_cols,
+                                                            int64_t src_stride, uint8_t * __restrict__ dst,
+                                                            int64_t nblocks_row, int64_t nblocks, bool dense,
+                                                            bool dst_vec) {
+    constexpr int QB = qtraits<QT>::bytes;
+    constexpr int GB = 64 * QB;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][GB];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * 64;
+    const int64_t blk = b0 + lane;
+
+    float x[32];
+    if (blk < nblocks) {
+        if (dense) {
+            load_block<S, kVec>(src + blk * 32, 0, 32, x);
+        } else {
+            const int64_t r = blk / nblocks_row;
+            const int64_t cb = blk - r * nblocks_row;
+            load_block<S, kVec>(src + r * src_stride, cb * 32, src_cols, x);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) x[k] = 0.0f;
+    }
+
+    quantize_block<QT>(x, stage[wave], lane);
+    wave_lds_fence();
+
+    uint8_t * out = dst + b0 * QB;
+    const uint8_t * lds = stage[wave];
+    const int64_t nvalid = nblocks - b0;
+    if (nvalid >= 64 && dst_vec) {
+        for (int i = lane; i < GB / 16; i += 64)
+            reinterpret_cast<u32x4 *>(out)[i] = reinterpret_cast<const u32x4 *>(lds)[i];
+    } else if (nvalid > 0) {
+        const int nbytes = static_cast<int>(nvalid < 64 ? nvalid : 64) * QB;
+        for (int i = lane; i < nbytes / 2; i += 64)
+            reinterpret_cast<uint16_t *>(out)[i] = reinterpret_cast<const uint16_t *>(lds)[i];
+    }
+}
+
+// Dequantize: a wave expands 32 consecutive blocks. Their 32 * QB bytes (a
+// 16-byte-aligned range) are staged in LDS; the output is written as 16-byte
+// chunks with lane l taking chunks l, l + 64, ..., so every store instruction
+// covers one contiguous 1 KiB span. Chunk c holds values (c % CPB) * VPC ..
+// of block c / CPB.
 template <int QT, typename D>
 __global__ __launch_bounds__(kThreads) void dequantize_kernel(const uint8_t * __restrict__ src, D * __restrict__ dst,
                                                               int64_t nblocks, bool src_vec, bool dst_vec) {
     constexpr int QB = qtraits<QT>::bytes;
-    constexpr int BPW = 16;
+    constexpr int BPW = 32;
     constexpr int GB = BPW * QB;
+    constexpr int VPC = 16 / static_cast<int>(sizeof(D));  // values per 16-byte chunk: 4 (F32) or 8 (F16)
+    constexpr int CPB = 32 / VPC;                          // chunks per block
+    constexpr int CPL = BPW * CPB / 64;                    // chunks per lane
     __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][GB];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t group = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
-    const int64_t b0 = group * BPW;
+    const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * BPW;
     const int64_t nvalid = nblocks - b0;
+    if (nvalid <= 0) return;  // whole wave; no barrier follows
     uint8_t * lds = stage[wave];
     const uint8_t * in = src + b0 * QB;
     if (nvalid >= BPW && src_vec) {
-        if (lane < GB / 16)
-            reinterpret_cast<u32x4 *>(lds)[lane] = reinterpret_cast<const u32x4 *>(in)[lane];
-    } else if (nvalid > 0) {
+        for (int i = lane; i < GB / 16; i += 64)
+            reinterpret_cast<u32x4 *>(lds)[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(in) + i);
+    } else {
         const int nbytes = static_cast<int>(nvalid < BPW ? nvalid : BPW) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)
             reinterpret_cast<uint16_t *>(lds)[i] = reinterpret_cast<const uint16_t *>(in)[i];
     }
-    __syncthreads();
-    const int bi = lane >> 2;
-    const int part = lane & 3;
-    if (bi >= nvalid) return;
-    const uint8_t * blk = lds + bi * QB;
-    const float d = h2f(*reinterpret_cast<const uint16_t *>(blk));
-    float y[8];
-    if constexpr (QT == LEVO_HIP_TYPE_Q8_0) {
+    wave_lds_fence();
 #pragma unroll
-        for (int k = 0; k < 8; k += 2) {
-            const uint16_t two = *reinterpret_cast<const uint16_t *>(blk + 2 + part * 8 + k);
-            y[k] = static_cast<float>(static_cast<int8_t>(two & 0xffu)) * d;
-            y[k + 1] = static_cast<float>(static_cast<int8_t>(two >> 8)) * d;
+    for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        const int bi = c / CPB;
+        const int part = c % CPB;
+        if (bi >= nvalid) break;
+        const uint8_t * blk = lds + bi * QB;
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(blk));
+        float y[VPC];
+#pragma unroll
+        for (int k = 0; k < VPC; k += 2) {
+            const int v = part * VPC + k;  // first of the two values
+            if constexpr (QT == LEVO_HIP_TYPE_Q8_0) {
+                const uint16_t two = *reinterpret_cast<const uint16_t *>(blk + 2 + v);
+                y[k] = static_cast<float>(static_cast<int8_t>(two & 0xffu)) * d;
+                y[k + 1] = static_cast<float>(static_cast<int8_t>(two >> 8)) * d;
+            } else {
+                // values 0..15: low nibbles of qs[0..15]; 16..31: high nibbles
+                const uint16_t two = *reinterpret_cast<const uint16_t *>(blk + 2 + (v & 15));
+                const int shift = (v >> 4) * 4;
+                y[k] = static_cast<float>(static_cast<int>((two >> shift) & 0xfu) - 8) * d;
+                y[k + 1] = static_cast<float>(static_cast<int>((two >> (8 + shift)) & 0xfu) - 8) * d;
+            }
         }
-    } else {
-        const int j0 = (part & 1) * 8;     // qs byte index
-        const int shift = (part >> 1) * 4;  // low nibbles: values 0..15, high: 16..31
+        const int64_t e0 = (b0 + bi) * 32 + part * VPC;
+        if (dst_vec) {
+            if constexpr (std::is_same<D, float>::value) {
+                f32x4 o;
+                o.x = y[0];
+                o.y = y[1];
+                o.z = y[2];
+                o.w = y[3];
+                __builtin_nontemporal_store(o, reinterpret_cast<f32x4 *>(dst + e0));
+            } else {
+                u16x8 h;
 #pragma unroll
-        for (int k = 0; k < 8; k += 2) {
-            const uint16_t two = *reinterpret_cast<const uint16_t *>(blk + 2 + j0 + k);
-            y[k] = static_cast<float>(static_cast<int>((two >> shift) & 0xfu) - 8) * d;
-            y[k + 1] = static_cast<float>(static_cast<int>((two >> (8 + shift)) & 0xfu) - 8) * d;
+                for (int k = 0; k < 8; ++k) h[k] = f2h(y[k]);
+                __builtin_nontemporal_store(h, reinterpret_cast<u16x8 *>(dst + e0));
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < VPC; ++k) {
+                if constexpr (std::is_same<D, float>::value) dst[e0 + k] = y[k];
+                else dst[e0 + k] = f2h(y[k]);
+            }
         }
-    }
-    // output values of this lane: block (b0+bi), values part*8 .. part*8+7
-    // (Q4_0 part p holds values 8p..8p+7 too: parts 0,1 low nibbles, 2,3 high)
-    const int64_t e0 = (b0 + bi) * 32 + part * 8;
-    if (!dst_vec) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if constexpr (std::is_same<D, float>::value) dst[e0 + k] = y[k];
-            else dst[e0 + k] = f2h(y[k]);
-        }
-    } else if constexpr (std::is_same<D, float>::value) {
-        f32x4 a, b;
-        a.x = y[0]; a.y = y[1]; a.z = y[2]; a.w = y[3];
-        b.x = y[4]; b.y = y[5]; b.z = y[6]; b.w = y[7];
-        reinterpret_cast<f32x4 *>(dst + e0)[0] = a;
-        reinterpret_cast<f32x4 *>(dst + e0)[1] = b;
-    } else {
-        u16x8 h;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) h[k] = f2h(y[k]);
-        *reinterpret_cast<u16x8 *>(dst + e0) = h;
     }
 }
 
@@ -271,20 +402,22 @@ int64_t block_bytes(levo_hip_type t) {
 template <int QT, typename S>
 int launch_quant(const void * src, int64_t src_cols, int64_t src_stride, void * dst, int64_t nrows,
                  int64_t dst_cols, hipStream_t stream) {
-    constexpr int N = std::is_same<S, uint16_t>::value ? 8 : 4;
-    constexpr int BPW = 64 / (32 / N);
     const int64_t nb_row = dst_cols / 32;
     const int64_t nblocks = nrows * nb_row;
-    const int64_t groups = ceil_div(nblocks, BPW);
-    const int64_t grid = ceil_div(groups, kWaves);
-    const bool vec = src_cols % N == 0 && src_stride % N == 0 && aligned16(src);
+    const int64_t grid = ceil_div(nblocks, 64 * kWaves);
+    // dwordx4 loads need every row start 16-byte aligned
+    const bool vec = aligned16(src) && (src_stride * static_cast<int64_t>(sizeof(S))) % 16 == 0;
+    // rows packed back to back with no padding: block b is source values 32b..32b+31
+    const bool dense = src_cols == dst_cols && src_stride == src_cols;
     const S * s = static_cast<const S *>(src);
     uint8_t * d = static_cast<uint8_t *>(dst);
     const bool dst_vec = aligned16(dst);
-    if (vec)
-        quantize_kernel<QT, S, true><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dst_vec);
+    if (vec && dense)
+        quantize_dense_kernel<QT, S><<<grid, kThreads, 0, stream>>>(s, d, nblocks, dst_vec);
+    else if (vec)
+        quantize_kernel<QT, S, true><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dense, dst_vec);
     else
-        quantize_kernel<QT, S, false><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dst_vec);
+        quantize_kernel<QT, S, false><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dense, dst_vec);
     return launch_status("levo_hip_quantize");
 }
 
@@ -361,7 +494,7 @@ extern "C" int levo_hip_dequantize(levo_hip_type type, const void * src, void * 
     const bool src_vec = aligned16(src);
     const bool dst_vec = aligned16(dst);
     const int64_t nblocks = k / 32;
-    const int64_t grid = ceil_div(ceil_div(nblocks, 16), kWaves);
+    const int64_t grid = ceil_div(ceil_div(nblocks, 32), kWaves);
     const hipStream_t st = as_hip(stream);
     const uint8_t * s = static_cast<const uint8_t *>(src);
     if (type == LEVO_HIP_TYPE_Q8_0) {
