@@ -89,9 +89,8 @@ __device__ __forceinline__ float half_away_offset(float v) {
 // (int8_t)v as the reference's x86-64 build computes it: truncation to int32
 // (cvttss2si), low byte kept. v_cvt_i32_f32 truncates too and gives 0 for NaN
 // where cvttss2si gives 0x80000000 (low byte 0 as well); the two differ only
-// beyond +-2^31, which the callers exclude (x * id stays within +-128 while id
-// is finite; an id of +inf is replaced by NaN first). Inline asm because a
-// C++ float -> int conversion of NaN is undefined.
+// beyond +-2^31, which the callers exclude or handle (see quantize_block).
+// Inline asm because a C++ float -> int conversion of NaN is undefined.
 __device__ __forceinline__ uint32_t low_byte_i8(float v) {
     int32_t r;
     asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
@@ -135,21 +134,40 @@ __device__ __forceinline__ void stage_block(uint8_t * lds, int lane, uint32_t d1
 template <int QT>
 __device__ __forceinline__ void quantize_block(const float (&x)[32], uint8_t * lds, int lane) {
     if constexpr (QT == LEVO_HIP_TYPE_Q8_0) {
-        float amax = 0.0f;
+        float amax = 0.0f;  // ggml's MAX(amax, fabsf(v)) in index order
+        float m = 0.0f;     // max of the non-NaN |x|
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
             const float v = fabsf(x[k]);
-            amax = amax > v ? amax : v;  // MAX(amax, fabsf(v))
+            amax = amax > v ? amax : v;
+            m = __builtin_fmaxf(m, v);
         }
         const float d = amax / 127.0f;
         const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
         uint32_t pk[8];
+        if (m == amax) {
+            // every |x| <= amax: |x * id| stays within 128 (or is NaN)
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            uint32_t q[4];
+            for (int w = 0; w < 8; ++w) {
+                uint32_t q[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) q[k] = low_byte_i8(half_away_offset(x[4 * w + k] * id));  // (int8_t)roundf(x * id)
-            pk[w] = pack4(q[0], q[1], q[2], q[3]);
+                for (int k = 0; k < 4; ++k) q[k] = low_byte_i8(half_away_offset(x[4 * w + k] * id));
+                pk[w] = pack4(q[0], q[1], q[2], q[3]);
+            }
+        } else {
+            // A NaN reset the running MAX, so earlier values may exceed amax
+            // and x * id may leave the int32 range: there cvttss2si gives
+            // 0x80000000 (low byte 0).
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                uint32_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float v = half_away_offset(x[4 * w + k] * id);
+                    q[k] = __builtin_fabsf(v) < 0x1p31f ? low_byte_i8(v) : 0u;
+                }
+                pk[w] = pack4(q[0], q[1], q[2], q[3]);
+            }
         }
         stage_block<8>(lds, lane, f2h(d), pk);
     } else {

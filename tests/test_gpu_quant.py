@@ -148,3 +148,42 @@ def test_unaligned_buffers(hip, dev, oracle, qt):
     yd = from_dev(y)
     assert np.array_equal(yd[1: 1 + nblocks * 32], oracle.dequantize(qt, want, nblocks * 32))
     assert yd[0] == 5.0 and np.all(yd[1 + nblocks * 32:] == 5.0)
+
+
+@pytest.mark.parametrize("qt", [Q8, Q4], ids=["q8_0", "q4_0"])
+@pytest.mark.parametrize("dense", [True, False], ids=["packed", "padded"])
+def test_non_finite_blocks_follow_the_reference_scan(hip, dev, oracle, qt, dense):
+    """NaN and +-inf inside blocks. ggml's Q8_0 max is MAX(amax, fabsf(v))
+    applied in index order, so a NaN forgets every earlier value and a NaN in
+    the last slot makes d NaN; Q4_0's `amax < fabsf(v)` never picks a NaN.
+    The oracle restates that order; both the packed-row kernel and the padded
+    (strided) kernel must reproduce it byte for byte."""
+    import torch
+    nb = 40
+    x = (oracle.gaussian(nb * 32, 2100) * 0.5).reshape(nb, 32)
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    x[0, 0] = nan                       # NaN first
+    x[1, 17] = nan                      # NaN in the middle: earlier maxima forgotten
+    x[2, 31] = nan                      # NaN last: d = NaN
+    x[3, :] = nan                       # all NaN
+    x[4, 9] = inf                       # +inf: d = inf, id = 0
+    x[5, 3] = -inf
+    x[6, 4], x[6, 20] = nan, inf
+    x[7, 12], x[7, 30] = inf, nan
+    x[8, :16] = nan                     # NaN run then finite values
+    x[9, 5], x[9, 6] = -inf, inf
+    want = oracle.quantize(qt, x)
+    if dense:
+        out = torch.empty(nb * BB[qt], dtype=torch.uint8, device=dev)
+        hip.quantize_chunk(qt, to_dev(x, dev), out, 0, nb, 32)
+        got = from_dev(out)
+    else:
+        # the same blocks as rows of 32 values stored 40 floats apart
+        src = np.zeros((nb, 40), np.float32)
+        src[:, :32] = x
+        out = torch.empty(nb * BB[qt], dtype=torch.uint8, device=dev)
+        n = hip.quantize_rows(qt, to_dev(src, dev), 0, 32, 40, out, nb, 32)
+        assert n == out.numel()
+        got = from_dev(out)
+    bad = np.nonzero((got != want).reshape(nb, BB[qt]).any(axis=1))[0]
+    assert bad.size == 0, bad
