@@ -121,6 +121,39 @@ def op_entry(bytes_per_launch, ms, **extra):
     return e
 
 
+_COPY_CACHE = {}
+
+
+def copy_ceiling(torch, head, dev, nbytes, warmup, steps):
+    """GB/s of a plain device copy moving the same bytes (half read, half
+    written), timed like the ops with >= 512 MB of rotation: what any single
+    streaming launch of this size reaches on this GPU."""
+    key = int(nbytes)
+    if key in _COPY_CACHE:
+        return _COPY_CACHE[key]
+    half = max(16, key // 2 // 16 * 16)
+    n = math.ceil(ROTATE_BYTES / (2 * half)) + 1
+    src = [torch.empty(half // 4, dtype=torch.float32, device=dev).fill_(1.0) for _ in range(n)]
+    dst = [torch.empty(half // 4, dtype=torch.float32, device=dev) for _ in range(n)]
+    ms = time_op(torch, head, lambda i: dst[i].copy_(src[i]), n, warmup, steps)
+    gbps = round(2 * half / (ms * 1e-3) / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    _COPY_CACHE[key] = gbps
+    return gbps
+
+
+def add_ceilings(torch, head, dev, ops, warmup, steps):
+    """Annotate every op entry with the copy ceiling at its byte count."""
+    for entry in ops.values():
+        entries = entry.values() if "bytes_per_launch" not in entry else [entry]
+        for e in entries:
+            if isinstance(e, dict) and "bytes_per_launch" in e:
+                c = copy_ceiling(torch, head, dev, e["bytes_per_launch"], warmup, steps)
+                e["copy_GB/s"] = c
+                e["of_copy"] = round(e["GB/s"] / c, 3)
+
+
 def cpu_threads():
     try:
         return max(1, min(16, len(os.sched_getaffinity(0))))
@@ -455,6 +488,8 @@ def main() -> int:
     p.add_argument("--only", default="",
                    help="comma-separated op groups to run alone (snake,flow,norm,sample,quant); "
                         "prints the op table without the headline ladder")
+    p.add_argument("--copy-ceiling", action="store_true",
+                   help="with --only: annotate each op with a plain device copy of the same bytes")
     p.add_argument("--traffic-probe", action="store_true",
                    help="one launch per kernel + a 256 MiB copy, for rocprofv3 --pmc runs")
     args = p.parse_args()
@@ -494,6 +529,8 @@ def main() -> int:
                                                                 args.steps)
         if "quant" in groups:
             ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
+        if args.copy_ceiling:
+            add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
         print(json.dumps({"ops": ops}))
         return 0
     log("ladder: start")
@@ -504,7 +541,7 @@ def main() -> int:
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBPS, 4), "traffic": None,
-                "kernel": "snake_beta_vec<float,4>", "shape": [C, T], "algorithmic_bytes_per_launch": dom_bytes,
+                "kernel": "snake_beta_vec<float, 2>", "shape": [C, T], "algorithmic_bytes_per_launch": dom_bytes,
                 "us_per_launch": round(dom_ms * 1e3, 3)}
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(traffic_file):
@@ -530,6 +567,8 @@ def main() -> int:
         ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup, args.steps)
         log("ops: quant")
         ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
+        log("ops: plain-copy ceilings")
+        add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 
     cpu = None
     if not args.no_cpu:
