@@ -180,6 +180,33 @@ __global__ __launch_bounds__(kThreads) void snake_beta_vec(
     }
 }
 
+// Small tensors (latency-bound launches): one vector per thread with the
+// channel's parameters computed by the thread itself (two exps per four
+// elements), so no LDS round trip or barrier sits on the critical path.
+template <typename P>
+__global__ __launch_bounds__(kThreads) void snake_beta_vec_direct(
+        const float * x, int64_t x_stride, const P * __restrict__ alpha_log,
+        const P * __restrict__ beta_log, float * y, int64_t y_stride, uint32_t total4,
+        fast_div div_t4) {
+    const uint32_t f = blockIdx.x * kThreads + threadIdx.x;
+    if (f >= total4) return;
+    const uint32_t ch = div_of(f, div_t4);
+    const uint32_t t4 = f - ch * div_t4.d;
+    const f32x4 v =
+            __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(x + static_cast<int64_t>(ch) * x_stride) + t4);
+    snake_param q;
+    q.alpha = expf(param_f32(alpha_log, ch));
+    const float e = expf(param_f32(beta_log, ch));
+    q.beta = e * 1.0f + 1.0e-9f;  // ggml_scale_bias(exp(beta_log), 1, 1e-9)
+    q.rbeta = 1.0f / q.beta;
+    f32x4 r;
+    r.x = snake(v.x, q);
+    r.y = snake(v.y, q);
+    r.z = snake(v.z, q);
+    r.w = snake(v.w, q);
+    __builtin_nontemporal_store(r, reinterpret_cast<f32x4 *>(y + static_cast<int64_t>(ch) * y_stride) + t4);
+}
+
 // Scalar path for any time / stride / alignment.
 template <typename P>
 __global__ __launch_bounds__(kThreads) void snake_beta_scalar(
@@ -229,10 +256,13 @@ int launch_snake(const float * x, int64_t x_stride, const P * a, const P * b, fl
     if (vec) {
         const uint32_t total4 = static_cast<uint32_t>(total / 4);
         const uint32_t t4 = static_cast<uint32_t>(time / 4);
-        // Vectors per thread by size, as measured on MI355X: one for small
-        // tensors (most workgroups in flight), four in the mid range, two
-        // for the largest (fewest parameter set-ups without a long tail).
-        if (total4 < (1u << 20)) launch_vec<P, 1>(x, x_stride, a, b, y, y_stride, channels, total4, t4, stream);
+        // By size, as measured on MI355X: below 4 M elements one vector per
+        // thread with per-thread parameters; four vectors per thread in the
+        // mid range; two for the largest (fewest parameter set-ups without a
+        // long tail).
+        if (total4 < (1u << 20))
+            snake_beta_vec_direct<P><<<static_cast<uint32_t>(ceil_div(total4, kThreads)), kThreads, 0, stream>>>(
+                    x, x_stride, a, b, y, y_stride, total4, make_fast_div(t4));
         else if (total4 < (1u << 23)) launch_vec<P, 4>(x, x_stride, a, b, y, y_stride, channels, total4, t4, stream);
         else launch_vec<P, 2>(x, x_stride, a, b, y, y_stride, channels, total4, t4, stream);
     } else {
