@@ -326,6 +326,73 @@ def bench_sample(torch, hip, binding, head, dev, warmup, steps):
     return op_entry(per, ms, shape=[P, 2, S, V], dtype="f32", top_k=50, temperature=0.9)
 
 
+def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
+    """Sampling of one LeLM decode step on the device: 1 position x 3 streams
+    x 16385 ids, CFG s = 1.5, penalty window 50, a 3-id ignore list, top-k
+    50/1/1, T = 0.9; levo_hip_cfg_sample + levo_hip_sample_draw. Latency-bound
+    (393 KB per step). `device_us`: both launches back to back; `roundtrip_us`:
+    median wall time from the first launch until the 3 ids and draw counts
+    are in pinned host memory (Python launch overhead included)."""
+    S, V, cap = 3, 16385, 64
+    n = 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(V)
+    sets = [(torch.randn((S, V), generator=g, device=dev) * 3, torch.randn((S, V), generator=g, device=dev) * 3)
+            for _ in range(n)]
+    recent = torch.randint(0, V - 1, (S, 50), generator=g, device=dev, dtype=torch.int64)
+    ignore = torch.tensor([0, 1, 2], dtype=torch.int64, device=dev)
+    bits = torch.randint(-2 ** 62, 2 ** 62, (S,), generator=g, device=dev, dtype=torch.int64)
+    best = torch.empty(S, dtype=torch.int32, device=dev)
+    count = torch.empty(S, dtype=torch.int32, device=dev)
+    ids = torch.empty((S, cap), dtype=torch.int32, device=dev)
+    lg = torch.empty((S, cap), dtype=torch.float32, device=dev)
+    mx = torch.empty(S, dtype=torch.float32, device=dev)
+    tokens = torch.empty(S, dtype=torch.int64, device=dev)
+    draws = torch.empty(S, dtype=torch.int32, device=dev)
+    sargs = []
+    for c, u in sets:
+        a = binding.SampleArgs()
+        a.cond, a.uncond, a.rows, a.vocab, a.row_pitch = c.data_ptr(), u.data_ptr(), S, V, V
+        a.cfg_scale, a.temperature, a.n_streams = 1.5, 0.9, S
+        a.top_k[0], a.top_k[1], a.top_k[2] = 50, 1, 1
+        a.recent, a.n_recent, a.repetition_penalty, a.penalty_limit = recent.data_ptr(), 50, 1.1, V - 1
+        a.ignore, a.n_ignore = ignore.data_ptr(), 3
+        a.best, a.count, a.cand_ids, a.cand_logits = best.data_ptr(), count.data_ptr(), ids.data_ptr(), lg.data_ptr()
+        a.row_max, a.capacity = mx.data_ptr(), cap
+        sargs.append(a)
+    d = binding.DrawArgs()
+    d.best, d.count, d.cand_ids, d.cand_logits, d.row_max = (best.data_ptr(), count.data_ptr(), ids.data_ptr(),
+                                                             lg.data_ptr(), mx.data_ptr())
+    d.rows, d.capacity, d.temperature, d.use_sampling = S, cap, 0.9, 1
+    d.bits, d.tokens, d.draws = bits.data_ptr(), tokens.data_ptr(), draws.data_ptr()
+
+    def step(i):
+        hip.cfg_sample(sargs[i])
+        hip.sample_draw(d)
+
+    device_ms = time_op(torch, head, step, n, warmup, max(steps, 200))
+    sample_ms = time_op(torch, head, lambda i: hip.cfg_sample(sargs[i]), n, warmup, max(steps, 200))
+    h_tok = torch.empty(S, dtype=torch.int64, pin_memory=True)
+    h_draws = torch.empty(S, dtype=torch.int32, pin_memory=True)
+    stream = torch.cuda.current_stream()
+    walls = []
+    for i in range(warmup + 200):
+        stream.synchronize()
+        t0 = time.perf_counter()
+        step(i % n)
+        h_tok.copy_(tokens, non_blocking=True)
+        h_draws.copy_(draws, non_blocking=True)
+        stream.synchronize()
+        walls.append(time.perf_counter() - t0)
+    roundtrip_ms = float(np.median(walls[warmup:])) * 1e3
+    per = 2 * S * V * 4 + S * 50 * 8 + 3 * 8 + S * (4 + 4 + 4 + cap * 8 + 8 + 8 + 4)
+    return op_entry(per, device_ms, shape=[1, 2, S, V], dtype="f32 logits / f64 weights", top_k=[50, 1, 1],
+                    temperature=0.9, cfg_sample_us=round(sample_ms * 1e3, 3),
+                    sample_draw_us=round((device_ms - sample_ms) * 1e3, 3),
+                    roundtrip_us=round(roundtrip_ms * 1e3, 2), bytes_to_host=S * (8 + 4),
+                    bound="latency")
+
+
 def bench_quant(torch, hip, head, dev, warmup, steps):
     R, Cc = 4096, 1536
     out = {}
@@ -415,6 +482,20 @@ def cpu_ops_baselines():
         res["cfg_sample_top50"] = {"GB/s": round(60 * 2 * V * 4 / secs / 1e9, 3), "rows_per_s": round(60 / secs, 1),
                                    "cores": 1, "kind": "reference",
                                    "sample": "60 rows of 16384: levo::apply_cfg + Sampler::sample(top-50, T=0.9)"}
+        V2 = 16385
+        streams = (orc.gaussian(3 * V2, 10) * 3).reshape(3, V2)
+        recent = (np.arange(150, dtype=np.int64) * 97 % (V2 - 1)).reshape(3, 50)
+        s2 = ref.sampler(2)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 1.0:
+            s2.sample_streams(streams, use_sampling=True, temperature=0.9, top_k_mixed=50, top_k_detail=1,
+                              repetition_penalty=1.1, recent=recent, ignore=(0, 1, 2))
+            reps += 1
+        res["decode_step_sample"] = {
+            "us_per_step": round((time.perf_counter() - t0) / reps * 1e6, 1), "cores": 1, "kind": "reference",
+            "sample": "Sampler::sample_streams over 3 host rows of 16385 (penalty window 50, 3 ignored ids, "
+                      "top-k 50/1/1, T = 0.9); the reference first copies 2 x 196 KB of logits to the host"}
     return res
 
 
@@ -527,6 +608,8 @@ def main() -> int:
         if "sample" in groups:
             ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup,
                                                                 args.steps)
+            ops["decode_step_sample_1x3x16385"] = bench_decode_step(torch, hip, binding, head, dev, args.warmup,
+                                                                    args.steps)
         if "quant" in groups:
             ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
         if args.copy_ceiling:
@@ -565,6 +648,9 @@ def main() -> int:
                                                                     layer, rows, D)
         log("ops: cfg sample")
         ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup, args.steps)
+        log("ops: decode-step sampling")
+        ops["decode_step_sample_1x3x16385"] = bench_decode_step(torch, hip, binding, head, dev, args.warmup,
+                                                                args.steps)
         log("ops: quant")
         ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
         log("ops: plain-copy ceilings")

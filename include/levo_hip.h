@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LEVO_HIP_ABI_VERSION 2
+#define LEVO_HIP_ABI_VERSION 3
 
 /* Same tag as HIP's hipStream_t, so a hipStream_t converts without a cast. */
 typedef struct ihipStream_t * levo_hip_stream_t;
@@ -155,6 +155,42 @@ int levo_hip_repetition_penalty(float * logits, int64_t vocab, const int64_t * r
  * temperature softmax over it. The single uniform draw of a sampled token
  * stays on the host so the mt19937_64 cursor is unchanged. */
 int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_stream_t stream);
+
+/* Token codes of levo_hip_sample_draw besides ids >= 0. */
+#define LEVO_HIP_TOKEN_NAN (-1)      /* the row holds a NaN: the reference throws "logits contain NaN" */
+#define LEVO_HIP_TOKEN_OVERFLOW (-2) /* more candidates than `capacity`: run levo_hip_cfg_sample again
+                                      * with a larger capacity and draw again with the same bits */
+#define LEVO_HIP_TOKEN_RECHECK (-3)  /* the target lies within the double-rounding bound of a cumulative
+                                      * boundary: draw this row on the host from its candidates with
+                                      * the raw value bits[draws[r] - 1] */
+
+/* Arguments of levo_hip_sample_draw. The candidate inputs are the outputs of
+ * levo_hip_cfg_sample for the same rows (cand_logits and row_max required). */
+typedef struct levo_hip_draw_args {
+    const int32_t * best;        /* [rows] */
+    const int32_t * count;       /* [rows] */
+    const int32_t * cand_ids;    /* [rows][capacity] */
+    const float * cand_logits;   /* [rows][capacity] */
+    const float * row_max;       /* [rows] */
+    int64_t rows;
+    int32_t capacity;
+    float temperature;           /* finite, >= 0; 0 = greedy */
+    int32_t use_sampling;        /* 0 = greedy: tokens = best, no draws */
+    const uint64_t * bits;       /* [rows] the next raw outputs of the caller's mt19937_64 */
+    int64_t * tokens;            /* [rows] out: sampled id or LEVO_HIP_TOKEN_* */
+    int32_t * draws;             /* [rows] out: raw values consumed by rows 0..r */
+} levo_hip_draw_args;
+
+/* The sampled branch of sample_top_k_counted (src/levo-sampling.cpp:97-115;
+ * Sampler::sample_streams :129-152 for consecutive rows) on the device: the
+ * double weights exp((double)((v - max) / T)) of the candidates in id order,
+ * their sequential sum, the uniform (bits >> 11 + 0.5) / 2^53 and the
+ * cumulative search. Row r draws, taking the next unused entry of `bits`,
+ * exactly when the reference's row would consume one mt19937_64 value
+ * (sampling, T != 0, no NaN, finite maximum); greedy rows return `best`.
+ * The caller advances its engine by draws[rows - 1]. One small launch; only
+ * `tokens` and `draws` need to reach the host. */
+int levo_hip_sample_draw(const levo_hip_draw_args * args, levo_hip_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Flow Euler / CFG latent update                                            */

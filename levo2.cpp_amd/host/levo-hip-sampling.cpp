@@ -21,14 +21,45 @@ struct sample_workspace {
     device_buffer<int32_t> count;
     device_buffer<int32_t> cand_ids;
     device_buffer<float> cand_logits;
+    device_buffer<float> row_max;
+    device_buffer<uint64_t> bits;     // next raw engine values for the device draw
+    device_buffer<int64_t> tokens;
+    device_buffer<int32_t> draws;
     pinned_buffer<float> stage;       // host rows staged for upload
     pinned_buffer<int64_t> stage_ids; // recent windows + ignore list staged for upload
     pinned_buffer<int32_t> h_best;
     pinned_buffer<int32_t> h_count;
     pinned_buffer<int32_t> h_ids;
     pinned_buffer<float> h_logits;
+    pinned_buffer<uint64_t> h_bits;
+    pinned_buffer<int64_t> h_tokens;
+    pinned_buffer<int32_t> h_draws;
     std::size_t capacity = 64;        // candidate slots per row; grows on demand
 };
+
+int64_t pick_candidate(const int32_t * ids, const float * values, std::size_t n, int32_t best, float temperature,
+                       uint64_t raw) {
+    thread_local std::vector<double> weights;
+    float max_logit = -std::numeric_limits<float>::infinity();
+    for (std::size_t i = 0; i < n; ++i) max_logit = std::max(max_logit, values[i]);
+    weights.resize(n);
+    double total = 0.0;
+    for (std::size_t i = 0; i < n; ++i) {
+        const float v = values[i];
+        weights[i] = (std::isinf(v) && v < 0.0F)
+                         ? 0.0
+                         : std::exp(static_cast<double>((v - max_logit) / temperature));
+        total += weights[i];
+    }
+    if (!(total > 0.0) || !std::isfinite(total)) return best;
+    const double target = (static_cast<double>(raw >> 11) + 0.5) / 9007199254740992.0 * total;
+    double cumulative = 0.0;
+    for (std::size_t i = 0; i < n; ++i) {
+        cumulative += weights[i];
+        if (target < cumulative) return ids[i];
+    }
+    return ids[n - 1];
+}
 
 } // namespace detail
 
@@ -65,74 +96,136 @@ int32_t kernel_top_k(std::size_t top_k, std::size_t vocab) {
     return static_cast<int32_t>(top_k);
 }
 
-// The sampled branch of sample_top_k_counted (src/levo-sampling.cpp:97-115)
-// over the candidate set the kernel produced: weights in double from the
-// exact F32 candidate logits, one draw, a sequential cumulative search.
-int64_t draw_candidate(const int32_t * ids, const float * values, std::size_t n, int32_t best,
-                       float temperature, std::mt19937_64 & rng, uint64_t * draws) {
-    thread_local std::vector<double> weights;
-    float max_logit = -std::numeric_limits<float>::infinity();
-    for (std::size_t i = 0; i < n; ++i) max_logit = std::max(max_logit, values[i]);
-    weights.resize(n);
-    double total = 0.0;
-    for (std::size_t i = 0; i < n; ++i) {
-        const float v = values[i];
-        weights[i] = (std::isinf(v) && v < 0.0F)
-                         ? 0.0
-                         : std::exp(static_cast<double>((v - max_logit) / temperature));
-        total += weights[i];
-    }
-    if (!(total > 0.0) || !std::isfinite(total)) return best;
-    const double target = manual_uniform(rng, draws) * total;
-    double cumulative = 0.0;
-    for (std::size_t i = 0; i < n; ++i) {
-        cumulative += weights[i];
-        if (target < cumulative) return ids[i];
-    }
-    return ids[n - 1];
+// Advances the engine past the `n` raw values the rows consumed.
+void advance(std::mt19937_64 & rng, uint64_t * draws, uint64_t n) {
+    rng.discard(n);
+    if (draws) *draws += n;
 }
 
-// Runs levo_hip_cfg_sample over args.rows rows and brings best, count and
-// (when `candidates`) the candidate ids/logits to the pinned host mirrors,
-// growing the candidate capacity until every row's set fits.
-void run_rows(sample_workspace & ws, levo_hip_sample_args args, bool candidates, stream_t stream) {
+// Host draw of one row whose device pick was flagged LEVO_HIP_TOKEN_RECHECK:
+// its candidates come back and pick_candidate (the reference's libm exp)
+// decides with the same raw value.
+int64_t recheck_row(sample_workspace & ws, std::size_t r, std::size_t cap, float temperature, uint64_t raw,
+                    stream_t stream) {
+    ws.h_best.reserve_discard(1);
+    ws.h_count.reserve_discard(1);
+    ws.h_ids.reserve_discard(cap);
+    ws.h_logits.reserve_discard(cap);
+    check_hip(hipMemcpyAsync(ws.h_best.data(), ws.best.data() + r, sizeof(int32_t), hipMemcpyDeviceToHost, stream),
+              "device-to-host copy");
+    check_hip(hipMemcpyAsync(ws.h_count.data(), ws.count.data() + r, sizeof(int32_t), hipMemcpyDeviceToHost,
+                             stream),
+              "device-to-host copy");
+    check_hip(hipMemcpyAsync(ws.h_ids.data(), ws.cand_ids.data() + r * cap, cap * sizeof(int32_t),
+                             hipMemcpyDeviceToHost, stream),
+              "device-to-host copy");
+    check_hip(hipMemcpyAsync(ws.h_logits.data(), ws.cand_logits.data() + r * cap, cap * sizeof(float),
+                             hipMemcpyDeviceToHost, stream),
+              "device-to-host copy");
+    synchronize(stream);
+    return detail::pick_candidate(ws.h_ids.data(), ws.h_logits.data(), static_cast<std::size_t>(ws.h_count[0]),
+                                  ws.h_best[0], temperature, raw);
+}
+
+// The ids sample_top_k_counted returns (src/levo-sampling.cpp:75-116) for
+// args.rows consecutive rows, in row order as sample_streams takes them
+// (:135-150). One levo_hip_cfg_sample launch; for sampled rows a
+// levo_hip_sample_draw launch fed with the engine's next raw values (read
+// from a copy, so nothing is consumed yet). Only the ids and the draw counts
+// come back; the engine then advances by exactly the values the reference's
+// rows would have consumed, also when a NaN row ends the batch.
+std::vector<int64_t> sample_rows(sample_workspace & ws, levo_hip_sample_args args, bool greedy, float temperature,
+                                 std::mt19937_64 & rng, uint64_t * draws, stream_t stream) {
     const std::size_t rows = static_cast<std::size_t>(args.rows);
+    std::vector<int64_t> out(rows);
     ws.best.reserve_discard(rows);
     ws.count.reserve_discard(rows);
-    ws.h_best.reserve_discard(rows);
-    ws.h_count.reserve_discard(rows);
-    for (;;) {
-        const std::size_t cap = candidates ? ws.capacity : 1;
-        ws.cand_ids.reserve_discard(rows * cap);
-        if (candidates) {
-            ws.cand_logits.reserve_discard(rows * cap);
-            ws.h_ids.reserve_discard(rows * cap);
-            ws.h_logits.reserve_discard(rows * cap);
-        }
-        args.best = ws.best.data();
-        args.count = ws.count.data();
+    args.best = ws.best.data();
+    args.count = ws.count.data();
+    args.cand_probs = nullptr;
+    args.row_lse = nullptr;
+    if (greedy) {
+        ws.cand_ids.reserve_discard(rows);
+        ws.h_best.reserve_discard(rows);
         args.cand_ids = ws.cand_ids.data();
-        args.cand_logits = candidates ? ws.cand_logits.data() : nullptr;
-        args.cand_probs = nullptr;
+        args.cand_logits = nullptr;
         args.row_max = nullptr;
-        args.row_lse = nullptr;
-        args.capacity = static_cast<int32_t>(cap);
+        args.capacity = 1;
         check_status(levo_hip_cfg_sample(&args, stream));
         ws.best.download(ws.h_best.data(), rows, stream);
-        ws.count.download(ws.h_count.data(), rows, stream);
-        if (candidates) {
-            ws.cand_ids.download(ws.h_ids.data(), rows * cap, stream);
-            ws.cand_logits.download(ws.h_logits.data(), rows * cap, stream);
-        }
         synchronize(stream);
-        if (!candidates) return;
-        std::size_t needed = 0;
         for (std::size_t r = 0; r < rows; ++r) {
-            if (ws.h_count[r] > 0) needed = std::max(needed, static_cast<std::size_t>(ws.h_count[r]));
+            if (ws.h_best[r] < 0) throw std::invalid_argument("logits contain NaN");
+            out[r] = ws.h_best[r];
         }
-        if (needed <= cap) return;
+        return out;
+    }
+
+    ws.h_bits.reserve_discard(rows);
+    ws.bits.reserve_discard(rows);
+    {
+        std::mt19937_64 peek = rng;
+        for (std::size_t r = 0; r < rows; ++r) ws.h_bits[r] = peek();
+    }
+    ws.bits.upload(ws.h_bits.data(), rows, stream);
+    ws.row_max.reserve_discard(rows);
+    ws.tokens.reserve_discard(rows);
+    ws.draws.reserve_discard(rows);
+    ws.h_tokens.reserve_discard(rows);
+    ws.h_draws.reserve_discard(rows);
+    for (;;) {
+        const std::size_t cap = ws.capacity;
+        ws.cand_ids.reserve_discard(rows * cap);
+        ws.cand_logits.reserve_discard(rows * cap);
+        args.cand_ids = ws.cand_ids.data();
+        args.cand_logits = ws.cand_logits.data();
+        args.row_max = ws.row_max.data();
+        args.capacity = static_cast<int32_t>(cap);
+        check_status(levo_hip_cfg_sample(&args, stream));
+        levo_hip_draw_args d;
+        std::memset(&d, 0, sizeof(d));
+        d.best = ws.best.data();
+        d.count = ws.count.data();
+        d.cand_ids = ws.cand_ids.data();
+        d.cand_logits = ws.cand_logits.data();
+        d.row_max = ws.row_max.data();
+        d.rows = args.rows;
+        d.capacity = args.capacity;
+        d.temperature = temperature;
+        d.use_sampling = 1;
+        d.bits = ws.bits.data();
+        d.tokens = ws.tokens.data();
+        d.draws = ws.draws.data();
+        check_status(levo_hip_sample_draw(&d, stream));
+        ws.tokens.download(ws.h_tokens.data(), rows, stream);
+        ws.draws.download(ws.h_draws.data(), rows, stream);
+        synchronize(stream);
+        std::size_t r = 0;
+        while (r < rows && ws.h_tokens[r] != LEVO_HIP_TOKEN_NAN && ws.h_tokens[r] != LEVO_HIP_TOKEN_OVERFLOW) ++r;
+        if (r == rows || ws.h_tokens[r] == LEVO_HIP_TOKEN_NAN) break;
+        // A candidate set outgrew the slots: size them for the largest set and
+        // run again with the same raw values (none has been consumed).
+        ws.h_count.reserve_discard(rows);
+        ws.count.download(ws.h_count.data(), rows, stream);
+        synchronize(stream);
+        std::size_t needed = cap;
+        for (std::size_t q = 0; q < rows; ++q) {
+            if (ws.h_count[q] > 0) needed = std::max(needed, static_cast<std::size_t>(ws.h_count[q]));
+        }
         ws.capacity = (needed + 63) / 64 * 64;
     }
+    for (std::size_t r = 0; r < rows; ++r) {
+        const int64_t t = ws.h_tokens[r];
+        if (t == LEVO_HIP_TOKEN_NAN) {
+            advance(rng, draws, r == 0 ? 0 : static_cast<uint64_t>(ws.h_draws[r - 1]));
+            throw std::invalid_argument("logits contain NaN");
+        }
+        out[r] = t == LEVO_HIP_TOKEN_RECHECK
+                     ? recheck_row(ws, r, ws.capacity, temperature, ws.h_bits[ws.h_draws[r] - 1], stream)
+                     : t;
+    }
+    advance(rng, draws, static_cast<uint64_t>(ws.h_draws[rows - 1]));
+    return out;
 }
 
 // Uploads penalty windows ([rows][width], -1 padded) and the ignore list.
@@ -190,17 +283,7 @@ levo_hip_sample_args base_args() {
     return a;
 }
 
-// Samples rows r of the workspace mirrors in order, as sample_top_k_counted.
-int64_t finish_row(const sample_workspace & ws, std::size_t r, std::size_t capacity, bool greedy,
-                   float temperature, std::mt19937_64 & rng, uint64_t * draws) {
-    const int32_t best = ws.h_best[r];
-    if (best < 0) throw std::invalid_argument("logits contain NaN");
-    if (greedy) return best;
-    return draw_candidate(ws.h_ids.data() + r * capacity, ws.h_logits.data() + r * capacity,
-                          static_cast<std::size_t>(ws.h_count[r]), best, temperature, rng, draws);
-}
-
-// One host row through the kernel (uploading it first), then the host draw.
+// One host row through the kernels (uploading it first).
 int64_t sample_host_row(sample_workspace & ws, const logits & input, std::size_t top_k, float temperature,
                         bool use_sampling, std::mt19937_64 & rng, uint64_t * draws, stream_t stream,
                         const std::vector<int64_t> * window, float penalty,
@@ -223,8 +306,7 @@ int64_t sample_host_row(sample_workspace & ws, const logits & input, std::size_t
     if (window) windows.push_back(*window);
     args.penalty_limit = static_cast<int64_t>(V - 1);
     stage_lists(ws, args, windows, ignore ? *ignore : std::vector<int64_t>{}, penalty, stream);
-    run_rows(ws, args, !greedy, stream);
-    return finish_row(ws, 0, ws.capacity, greedy, temperature, rng, draws);
+    return sample_rows(ws, args, greedy, temperature, rng, draws, stream)[0];
 }
 
 } // namespace
@@ -363,11 +445,7 @@ std::vector<int64_t> Sampler::sample_streams(const std::vector<logits> & streams
     for (const auto & history : recent) windows.push_back(trailing(history, config.repetition_window));
     args.penalty_limit = static_cast<int64_t>(V - 1);  // upstream code_size includes EOS; exclude it
     stage_lists(ws, args, windows, config.ignore_tokens, config.repetition_penalty, stream_);
-    run_rows(ws, args, !greedy, stream_);
-    for (std::size_t q = 0; q < rows; ++q) {
-        out.push_back(finish_row(ws, q, ws.capacity, greedy, config.temperature, engine_, &draws_));
-    }
-    return out;
+    return sample_rows(ws, args, greedy, config.temperature, engine_, &draws_, stream_);
 }
 
 std::vector<int64_t> Sampler::sample_device(const device_logits & batch, const sampling_config & config,
@@ -403,12 +481,7 @@ std::vector<int64_t> Sampler::sample_device(const device_logits & batch, const s
     for (const auto & history : recent) windows.push_back(trailing(history, config.repetition_window));
     args.penalty_limit = static_cast<int64_t>(batch.vocab - 1);
     stage_lists(ws, args, windows, config.ignore_tokens, config.repetition_penalty, stream_);
-    run_rows(ws, args, !greedy, stream_);
-    out.reserve(batch.rows);
-    for (std::size_t r = 0; r < batch.rows; ++r) {
-        out.push_back(finish_row(ws, r, ws.capacity, greedy, config.temperature, engine_, &draws_));
-    }
-    return out;
+    return sample_rows(ws, args, greedy, config.temperature, engine_, &draws_, stream_);
 }
 
 int64_t sample_top_k(const logits & input, std::size_t top_k, float temperature, bool use_sampling,

@@ -10,10 +10,13 @@
 // What runs where: CFG, the repetition penalty, the ignore list, the NaN
 // check, the first-maximum argmax and the top-k candidate set (all ties with
 // the k-th value kept, ascending id order) run in one levo_hip_cfg_sample
-// launch. The host keeps the mt19937_64 engine and its draw cursor, and turns
-// the k candidate logits into the reference's double weights
-// exp((double)((v - max) / T)) before its single uniform draw, so the sampled
-// id is the reference's for the same seed and cursor.
+// launch; a levo_hip_sample_draw launch turns the candidates into the
+// reference's double weights exp((double)((v - max) / T)) and makes the
+// uniform draw. The host keeps the mt19937_64 engine and its draw cursor: it
+// hands the device the engine's next raw values and afterwards advances the
+// engine by the number the rows consumed, so the sampled ids and the cursor
+// are the reference's for the same seed. Per call only the ids and draw
+// counts come back from the device.
 //
 // Limit: at most 32768 logits per row (LeVo's vocabulary is 16385).
 #pragma once
@@ -73,6 +76,14 @@ struct device_logits {
 
 namespace detail {
 struct sample_workspace;
+
+// The sampled branch of sample_top_k_counted (src/levo-sampling.cpp:97-115)
+// over a candidate set (ids ascending, their logits) with the uniform taken
+// from one raw mt19937_64 value: the host's draw for a row the device marks
+// LEVO_HIP_TOKEN_RECHECK. Returns `best` when the weight total is not a
+// positive finite number, as the reference does.
+int64_t pick_candidate(const int32_t * ids, const float * values, std::size_t n, int32_t best, float temperature,
+                       uint64_t raw);
 }
 
 class Sampler {

@@ -43,6 +43,19 @@ class SampleArgs(ctypes.Structure):
     ]
 
 
+class DrawArgs(ctypes.Structure):
+    """levo_hip_draw_args (include/levo_hip.h)."""
+
+    _fields_ = [
+        ("best", _P), ("count", _P), ("cand_ids", _P), ("cand_logits", _P), ("row_max", _P),
+        ("rows", _I64), ("capacity", _I32), ("temperature", _F), ("use_sampling", _I32),
+        ("bits", _P), ("tokens", _P), ("draws", _P),
+    ]
+
+
+TOKEN_NAN, TOKEN_OVERFLOW, TOKEN_RECHECK = -1, -2, -3
+
+
 def header_abi_version(header: str = HEADER) -> int:
     """LEVO_HIP_ABI_VERSION as declared in include/levo_hip.h."""
     m = re.search(r"#define\s+LEVO_HIP_ABI_VERSION\s+(\d+)", open(header).read())
@@ -90,6 +103,7 @@ class LevoHip:
                                                             _I64, _I64, _F, _P]),
             "levo_hip_cfg_combine": (ctypes.c_int, [_P, _P, _P, _I64, _F, _P]),
             "levo_hip_cfg_sample": (ctypes.c_int, [ctypes.POINTER(SampleArgs), _P]),
+            "levo_hip_sample_draw": (ctypes.c_int, [ctypes.POINTER(DrawArgs), _P]),
             "levo_hip_flow_cfg_euler": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
             "levo_hip_flow_cfg_euler_checked": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P, _P]),
             "levo_hip_check_finite": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _P]),
@@ -141,6 +155,9 @@ class LevoHip:
 
     def cfg_sample(self, args: SampleArgs, stream=None):
         return self._check(self.lib.levo_hip_cfg_sample(ctypes.byref(args), _stream(stream)))
+
+    def sample_draw(self, args: DrawArgs, stream=None):
+        return self._check(self.lib.levo_hip_sample_draw(ctypes.byref(args), _stream(stream)))
 
     def flow_cfg_euler(self, state, v_uncond, v_cond, n, guidance, dt, stream=None):
         return self._check(self.lib.levo_hip_flow_cfg_euler(_addr(state), _addr(v_uncond), _addr(v_cond), n,

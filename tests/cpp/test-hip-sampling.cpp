@@ -129,6 +129,36 @@ void sample_parity() {
     }
 }
 
+// detail::pick_candidate (the host draw for rows the device flags) against
+// the oracle's sample_top_k_counted with top_k = 0 over the same candidate
+// values and the same next raw engine value: ties, -inf entries, one
+// candidate, all -inf (no draw: the first maximum).
+void pick_candidate_parity() {
+    lo_mt19937_64 rng;
+    lo_mt_seed(&rng, 4242);
+    uint64_t draws = 0;
+    const float ninf = -std::numeric_limits<float>::infinity();
+    for (int set = 0; set < 300; ++set) {
+        const std::size_t n = 1 + static_cast<std::size_t>(set * 37) % 300;
+        std::vector<float> v = gaussian(n, 5000 + static_cast<uint64_t>(set), 2.0F);
+        if (set % 3 == 0) for (std::size_t i = 0; i < n; i += 7) v[i] = v[0];
+        if (set % 5 == 0) for (std::size_t i = 1; i < n; i += 4) v[i] = ninf;
+        if (set == 7) std::fill(v.begin(), v.end(), ninf);
+        std::vector<int32_t> ids(n);
+        for (std::size_t i = 0; i < n; ++i) ids[i] = static_cast<int32_t>(3 * i + 1);
+        std::size_t first_max = 0;
+        for (std::size_t i = 1; i < n; ++i) if (v[i] > v[first_max]) first_max = i;
+        const float t = set % 4 == 0 ? 0.25F : set % 4 == 1 ? 0.9F : 2.0F;
+        lo_mt19937_64 peek = rng;
+        const uint64_t raw = lo_mt_next(&peek);
+        int64_t want = -1;
+        CHECK(lo_sample_top_k(v.data(), static_cast<int64_t>(n), 0, t, 1, &rng, &draws, &want) == 0);
+        const int64_t got = detail::pick_candidate(ids.data(), v.data(), n, ids[first_max], t, raw);
+        CHECK(got == ids[static_cast<std::size_t>(want)]);
+    }
+    CHECK(draws == 299);  // every set draws except the all -inf one
+}
+
 // A 40-step generation loop at LeVo's shape: CFG on the host, the penalty
 // window fed back from the sampled ids, the prompt ignore list on stream 0.
 void streams_parity() {
@@ -248,6 +278,7 @@ int main() {
         reference_assertions();
         error_behaviour();
         sample_parity();
+        pick_candidate_parity();
         streams_parity();
         device_parity();
         ragged_streams();

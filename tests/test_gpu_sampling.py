@@ -3,8 +3,9 @@ the compiled reference sampler (src/levo-sampling.cpp).
 
 Bars: argmax ids, candidate ids (top-k with ties) and candidate logits are
 bit-exact; probabilities and the log-sum-exp are F32 outputs (<= 1e-5);
-sampled tokens drawn on the host from the GPU candidates equal the
-reference Sampler's tokens and its draw cursor.
+sampled tokens drawn on the host from the GPU candidates, and those drawn
+on the GPU by levo_hip_sample_draw, equal the reference Sampler's tokens
+and its draw cursor.
 """
 from __future__ import annotations
 
@@ -56,7 +57,8 @@ def run_sample(hip, binding, dev, cond, uncond, *, top_k, n_streams, temperature
     a.capacity = capacity
     hip.cfg_sample(a)
     out = dict(best=from_dev(best), count=from_dev(count), ids=from_dev(ids), logits=from_dev(lg),
-               probs=from_dev(pr), max=from_dev(mx))
+               probs=from_dev(pr), max=from_dev(mx),
+               dev=dict(best=best, count=count, ids=ids, logits=lg, max=mx, capacity=capacity))
     if lse:
         out["lse"] = from_dev(ls)
     return out
@@ -290,3 +292,125 @@ def test_standalone_repetition_penalty_reference_kat(hip, dev, binding):
     assert from_dev(d).tolist() == [5.0, 4.0, 6.0]
     with pytest.raises(binding.LevoHipError, match="repetition penalty must be finite and positive"):
         hip.repetition_penalty(d, 3, r, 3, 0.0)
+
+
+# ---- levo_hip_sample_draw -------------------------------------------------------
+
+def run_draw(hip, binding, dev, out, bits, *, temperature, use_sampling=True):
+    """levo_hip_sample_draw over the device outputs of run_sample; bits are
+    the raw engine values handed to the rows in order."""
+    import torch
+    d = out["dev"]
+    rows = d["best"].numel()
+    b = torch.tensor(np.asarray(bits, np.uint64).view(np.int64), dtype=torch.int64, device=dev)
+    tokens = torch.full((rows,), -99, dtype=torch.int64, device=dev)
+    draws = torch.full((rows,), -99, dtype=torch.int32, device=dev)
+    a = binding.DrawArgs()
+    a.best, a.count, a.cand_ids = d["best"].data_ptr(), d["count"].data_ptr(), d["ids"].data_ptr()
+    a.cand_logits, a.row_max = d["logits"].data_ptr(), d["max"].data_ptr()
+    a.rows, a.capacity, a.temperature, a.use_sampling = rows, d["capacity"], temperature, int(use_sampling)
+    a.bits, a.tokens, a.draws = b.data_ptr(), tokens.data_ptr(), draws.data_ptr()
+    hip.sample_draw(a)
+    return from_dev(tokens), from_dev(draws)
+
+
+def peek_bits(oracle, seed, consumed, n):
+    """The next n raw mt19937_64 values after `consumed` draws from `seed`."""
+    rng = oracle.mt(seed)
+    oracle.lib.lo_mt_discard(__import__("ctypes").byref(rng), consumed)
+    return np.array([oracle.mt_next(rng) for _ in range(n)], np.uint64)
+
+
+def test_device_draw_matches_reference_sampler(hip, binding, dev, oracle, ref):
+    """Sampler::sample_streams (src/levo-sampling.cpp:129-152) over 60
+    positions of 3 streams with CFG, penalty windows and the ignore list: the
+    ids drawn on the GPU and the engine cursor equal the reference's."""
+    P, S, V = 60, 3, 16385
+    cond = _f16_logits(oracle, P * S, V, 1400)
+    uncond = _f16_logits(oracle, P * S, V, 1401)
+    adjusted = oracle.apply_cfg(cond, uncond, 1.5)
+    for seed, temp in ((21, 0.9), (22, 0.25), (23, 2.0)):
+        s = ref.sampler(seed)
+        consumed = 0
+        recent = np.full((S, 50), -1, np.int64)
+        for pos in range(P):
+            rows = slice(pos * S, pos * S + S)
+            want = s.sample_streams(adjusted[rows], use_sampling=True, temperature=temp, top_k_mixed=50,
+                                    top_k_detail=1, repetition_penalty=1.1, recent=recent, ignore=(3, 9))
+            out = run_sample(hip, binding, dev, cond[rows], uncond[rows], top_k=[50, 1, 1], n_streams=3,
+                             temperature=temp, capacity=64, recent=recent, penalty=1.1, penalty_limit=V - 1,
+                             ignore=(3, 9), lse=False)
+            tokens, draws = run_draw(hip, binding, dev, out, peek_bits(oracle, seed, consumed, S), temperature=temp)
+            assert tokens.tolist() == want.tolist(), (seed, pos)
+            assert draws.tolist() == [1, 2, 3]
+            consumed += int(draws[-1])
+            recent = np.concatenate([recent[:, 1:], tokens[:, None]], axis=1)
+        assert consumed == s.draw_count
+
+
+def test_device_draw_batch_750_positions(hip, binding, dev, oracle):
+    """The [750][3][16384] batch, top-50, T = 0.9: row r draws bits[r]; every
+    id equals the host draw of sample_top_k_counted over the same candidates."""
+    P, S, V = 750, 3, 16384
+    cond = (oracle.gaussian(P * S * V, 511) * 3).reshape(P * S, V)
+    uncond = (oracle.gaussian(P * S * V, 512) * 3).reshape(P * S, V)
+    out = run_sample(hip, binding, dev, cond, uncond, top_k=[50, 50, 50], n_streams=3, lse=False)
+    bits = peek_bits(oracle, 77, 0, P * S)
+    tokens, draws = run_draw(hip, binding, dev, out, bits, temperature=0.9)
+    assert np.array_equal(draws, np.arange(1, P * S + 1))
+    rng, consumed = oracle.mt(77), 0
+    want = []
+    for r in range(P * S):
+        tok, consumed = host_draw(oracle, rng, consumed, out["ids"][r], out["logits"][r], int(out["best"][r]),
+                                  int(out["count"][r]), 0.9, True)
+        want.append(tok)
+    assert tokens.tolist() == want
+
+
+def test_device_draw_special_rows(hip, binding, dev, oracle):
+    """Rows that do not draw: NaN (token -1, the reference throws), all -inf
+    and +inf maxima (the first maximum, no draw, :108), greedy and T = 0;
+    an overflowing candidate set reports -2 but still counts its draw."""
+    V = 4096
+    cond = _f16_logits(oracle, 6, V, 1500)
+    cond[1, 17] = np.nan
+    cond[2, :] = -np.inf
+    cond[3, 10] = np.inf
+    cond[5, :] = 1.0                      # 4096 tied candidates, capacity 64
+    out = run_sample(hip, binding, dev, cond, None, top_k=[50], n_streams=1, capacity=64, lse=False)
+    bits = peek_bits(oracle, 5, 0, 6)
+    tokens, draws = run_draw(hip, binding, dev, out, bits, temperature=0.9)
+    rng, consumed = oracle.mt(5), 0
+    t0, consumed = host_draw(oracle, rng, consumed, out["ids"][0], out["logits"][0], int(out["best"][0]),
+                             int(out["count"][0]), 0.9, True)
+    assert tokens[0] == t0 and draws[0] == 1
+    assert tokens[1] == binding.TOKEN_NAN and draws[1] == 1
+    assert tokens[2] == out["best"][2] == 0 and draws[2] == 1
+    assert tokens[3] == out["best"][3] == 10 and draws[3] == 1
+    t4, consumed = host_draw(oracle, rng, consumed, out["ids"][4], out["logits"][4], int(out["best"][4]),
+                             int(out["count"][4]), 0.9, True)
+    assert tokens[4] == t4 and draws[4] == 2
+    assert tokens[5] == binding.TOKEN_OVERFLOW and draws[5] == 3
+    for temp, use in ((0.9, False), (0.0, True)):
+        tokens, draws = run_draw(hip, binding, dev, out, bits, temperature=temp, use_sampling=use)
+        assert tokens[[0, 2, 3, 4, 5]].tolist() == out["best"][[0, 2, 3, 4, 5]].tolist()
+        assert tokens[1] == binding.TOKEN_NAN and np.all(draws == 0)
+
+
+def test_device_draw_flags_targets_at_a_boundary(hip, binding, dev, oracle):
+    """Two equal candidates: weights 1, 1, total 2. The raw value 2^52 << 11
+    gives u = (2^52 + 0.5) / 2^53, which rounds to 0.5, so the target is 1.0,
+    exactly the first cumulative boundary, where a last-bit difference
+    between device and host exp could flip the pick: the row is flagged -3
+    (draw on the host). 2^30 raw steps to either side the pick is made on the
+    device: candidate 40 above the boundary, 7 below."""
+    V = 64
+    cond = np.full((1, V), -50.0, np.float32)
+    cond[0, 7] = cond[0, 40] = 2.5
+    out = run_sample(hip, binding, dev, cond, None, top_k=[2], n_streams=1, capacity=64, lse=False)
+    assert out["count"][0] == 2
+    tokens, draws = run_draw(hip, binding, dev, out, np.array([(1 << 52) << 11], np.uint64), temperature=0.9)
+    assert tokens[0] == binding.TOKEN_RECHECK and draws[0] == 1
+    for raw, want in ((((1 << 52) + (1 << 30)) << 11, 40), (((1 << 52) - (1 << 30)) << 11, 7)):
+        tokens, draws = run_draw(hip, binding, dev, out, np.array([raw], np.uint64), temperature=0.9)
+        assert tokens[0] == want and draws[0] == 1
