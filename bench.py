@@ -278,6 +278,70 @@ def bench_flow(torch, hip, head, dev, warmup, steps):
     return e
 
 
+def bench_flow_window(torch, hip, binding, head, dev, warmup, steps):
+    """Device-resident Flow step at LeVo's window: estimator rows of
+    24 | 64 | 2048 | 64 = 2200 floats, 1000 frames, 250 in-context frames,
+    batch 2 (CFG 1.5). `us_per_launch`: levo_hip_flow_step (a middle step:
+    velocity slice + CFG + Euler + next state columns), buffers rotated over
+    >= 512 MB. `assemble_us`: levo_hip_flow_assemble_input, once per window.
+    `replaced_copies_us`: the 17.6 MB host-to-device + 17.6 MB device-to-host
+    pinned copies the reference makes per step instead."""
+    F, L, M, C, P = 1000, 64, 24, 2048, 250
+    H = M + 2 * L + C
+    step_bytes = 4 * L * (2 * F + (F - P) + 2 * P + F + 2 * F)
+    n_step = math.ceil(ROTATE_BYTES / step_bytes) + 1
+    big = torch.empty((n_step, 2, 2, F, H), dtype=torch.float32, device=dev)  # [set][mi|out][batch][frame][col]
+    big[:, :, :, :, H - L:].normal_()
+    g = torch.Generator(device=dev)
+    g.manual_seed(2200)
+    mk = lambda *shape: torch.randn(shape, generator=g, device=dev)
+    noise, ctx, mask, cond = mk(F, L), mk(F, L), mk(F, M), mk(F, C)
+    states = [mk(F, L) for _ in range(n_step)]
+    args = []
+    for i in range(n_step):
+        a = binding.FlowStepArgs()
+        a.state, a.output, a.out_pitch, a.vel_col = states[i].data_ptr(), big[i, 1].data_ptr(), H, H - L
+        a.batch, a.guidance, a.frames, a.latent, a.step, a.steps = 2, 1.5, F, L, 20, 50
+        a.noise, a.context, a.prefix_frames, a.sigma_min = noise.data_ptr(), ctx.data_ptr(), P, 1e-4
+        a.next_input, a.in_pitch, a.state_col = big[i, 0].data_ptr(), H, H - L
+        args.append(a)
+    step_ms = time_op(torch, head, lambda i: hip.flow_step(args[i]), n_step, warmup, max(steps, 100))
+
+    asm_bytes = 4 * (2 * F * H + F * M + 2 * F * L + F * C + F * L + 2 * P * L)
+    n_asm = math.ceil(ROTATE_BYTES / asm_bytes) + 1
+    mis = torch.empty((n_asm, 2, F, H), dtype=torch.float32, device=dev)
+    asm = []
+    for i in range(n_asm):
+        a = binding.FlowInputArgs()
+        a.model_input, a.batch, a.frames = mis[i].data_ptr(), 2, F
+        a.mask_embedding, a.mask_dim, a.context, a.latent = mask.data_ptr(), M, ctx.data_ptr(), L
+        a.conditioning, a.condition_width = cond.data_ptr(), C
+        a.state, a.noise, a.prefix_frames = states[i % n_step].data_ptr(), noise.data_ptr(), P
+        a.step, a.steps, a.sigma_min = 0, 50, 1e-4
+        asm.append(a)
+    asm_ms = time_op(torch, head, lambda i: hip.flow_assemble_input(asm[i]), n_asm, warmup, max(steps, 50))
+    del mis
+
+    host = torch.empty((2, F, H), dtype=torch.float32).pin_memory()
+    dbuf = big[0, 0]
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    a.record()
+    for _ in range(reps):
+        dbuf.copy_(host, non_blocking=True)
+        host.copy_(big[0, 1], non_blocking=True)
+    b.record()
+    torch.cuda.synchronize()
+    copies_ms = a.elapsed_time(b) / reps
+    del big
+    return op_entry(step_bytes, step_ms, shape=[2, F, H], dtype="f32", prefix_frames=P, guidance=1.5,
+                    assemble_us=round(asm_ms * 1e3, 3),
+                    assemble_GBps=round(asm_bytes / (asm_ms * 1e-3) / 1e9, 1), assemble_bytes=asm_bytes,
+                    window_50_steps_us=round((asm_ms + 50 * step_ms) * 1e3, 2),
+                    replaced_copies_us=round(copies_ms * 1e3, 1), bound="latency")
+
+
 def bench_norm(torch, hip, head, dev, warmup, steps, layer, rows, D):
     per = 8 * rows * D + (4 * D if layer else 2 * D)
     n = max(2, math.ceil(ROTATE_BYTES / per) + 1) if rows > 2 else 64
@@ -600,6 +664,8 @@ def main() -> int:
             ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
         if "flow" in groups:
             ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, args.warmup, args.steps)
+            ops["flow_window_step_1000x64_rows2200"] = bench_flow_window(torch, hip, binding, head, dev,
+                                                                         args.warmup, args.steps)
         if "norm" in groups:
             for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
                 for rows, D in ((756, 2048), (1, 2048)):
@@ -641,6 +707,9 @@ def main() -> int:
         ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: flow")
         ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, args.warmup, args.steps)
+        log("ops: flow window step")
+        ops["flow_window_step_1000x64_rows2200"] = bench_flow_window(torch, hip, binding, head, dev, args.warmup,
+                                                                     args.steps)
         for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
             for rows, D in ((756, 2048), (756, 1536), (1, 2048), (2, 2048)):
                 log(f"ops: {name} {rows}x{D}")

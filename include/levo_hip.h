@@ -229,6 +229,80 @@ int levo_hip_flow_incontext(float * state, const float * noise, const float * co
                             int64_t n_prefix, float time, float sigma_min,
                             levo_hip_stream_t stream);
 
+/* ---- Device-resident Flow step (estimator tensors left in HBM) ---------- */
+
+/* Arguments of levo_hip_flow_assemble_input: the estimator input rows
+ * [batch][frames][mask_dim + latent + condition_width + latent] that
+ * append_model_row builds on the host for every step
+ * (src/levo-flow-renderer.cpp:35-53, :287-295). */
+typedef struct levo_hip_flow_input_args {
+    float * model_input;           /* out: [batch][frames][hidden] */
+    int32_t batch;                 /* 1, or 2 with row 0 unconditional (conditioning zeroed) */
+    int64_t frames;
+    const float * mask_embedding;  /* [frames][mask_dim] */
+    int64_t mask_dim;
+    const float * context;         /* normalized in-context latent [frames][latent] */
+    int64_t latent;
+    const float * conditioning;    /* [frames][condition_width] (2 * condition_dim) */
+    int64_t condition_width;
+    const float * state;           /* Euler state [frames][latent] before step `step` */
+    const float * noise;           /* initial noise [frames][latent] (prefix rows) */
+    int64_t prefix_frames;         /* in-context frames */
+    int64_t step, steps;           /* the state columns carry step `step`'s prefix interpolation */
+    float sigma_min;
+} levo_hip_flow_input_args;
+
+/* Writes every estimator input row: mask embedding | in-context latent |
+ * conditioning (zeros for the unconditional row) | state, the state's
+ * prefix rows interpolated as at the start of step `step` (:93-101). One
+ * launch per window; levo_hip_flow_step keeps the state columns current. */
+int levo_hip_flow_assemble_input(const levo_hip_flow_input_args * args, levo_hip_stream_t stream);
+
+/* Arguments of levo_hip_flow_step. */
+typedef struct levo_hip_flow_step_args {
+    float * state;                 /* [frames][latent] the reference's Euler `state`, in place */
+    const float * output;          /* estimator output [batch][frames][out_pitch] */
+    int64_t out_pitch;             /* floats per output row (hidden) */
+    int64_t vel_col;               /* first velocity column (hidden - latent) */
+    int32_t batch;                 /* 1: v = output; 2: row 0 unconditional, row 1 conditional */
+    float guidance;                /* v = u + guidance * (c - u) when batch == 2 */
+    int64_t frames, latent;
+    int64_t step, steps;           /* performs step `step` of `steps` (dt = 1 / steps) */
+    const float * noise;           /* [frames][latent] */
+    const float * context;         /* [frames][latent] normalized in-context latent */
+    int64_t prefix_frames;
+    float sigma_min;
+    float * next_input;            /* estimator input [batch][frames][in_pitch] or NULL */
+    int64_t in_pitch, state_col;   /* where the state columns of next_input start */
+    const float * mean, * stddev;  /* [latent], used with denormalized */
+    float * denormalized;          /* [frames][latent] after the last step, or NULL */
+    int32_t * nonfinite;           /* device flag word: LEVO_HIP_NONFINITE_* ORed in, or NULL */
+} levo_hip_flow_step_args;
+
+/* One Euler step of solve_flow_euler (src/levo-flow-renderer.cpp:89-117) fed
+ * straight from the estimator output: the velocity slice of
+ * estimator::velocity (src/levo-flow-estimator.cpp:390-399), the CFG lambda
+ * (src/levo-flow-renderer.cpp:301-309), the step's prefix interpolation
+ * (:93-101) and update (:105) with its finiteness checks (:104, :106). The
+ * next step's state columns (prefix interpolated for step + 1) go into
+ * next_input; after the last step the prefix is restored (:112-113) and
+ * denormalize_latents (src/levo-flow-conditioning.cpp:124-133) writes
+ * state * stddev + mean. Replaces the 17.6 MB host-to-device and 17.6 MB
+ * device-to-host copies per step at LeVo's window (2 x 1000 x 2200 F32,
+ * src/levo-flow-estimator.cpp:368, :382). */
+int levo_hip_flow_step(const levo_hip_flow_step_args * args, levo_hip_stream_t stream);
+
+/* conditioning::normalize_latents (src/levo-flow-conditioning.cpp:113-121):
+ * normalized[f][c] = (raw[f][c] - mean[c]) / stddev[c]; and
+ * denormalize_latents (:124-133): raw = normalized * stddev + mean. Two F32
+ * roundings each. ORs LEVO_HIP_NONFINITE_STATE into *nonfinite (device
+ * int32, or NULL) when an input value is not finite (the reference's
+ * require_finite on the input, :116, :128). */
+int levo_hip_flow_normalize(const float * raw, const float * mean, const float * stddev, float * normalized,
+                            int64_t frames, int64_t latent, int32_t * nonfinite, levo_hip_stream_t stream);
+int levo_hip_flow_denormalize(const float * normalized, const float * mean, const float * stddev, float * raw,
+                              int64_t frames, int64_t latent, int32_t * nonfinite, levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Q8_0 / Q4_0 block quantization (ggml block layouts, little-endian)        */
 /*   block_q8_0 = { f16 d; int8 qs[32]; }  34 bytes                          */

@@ -1,7 +1,9 @@
 // Euler solver of src/levo-flow-renderer.cpp:57-120 with the state on the GPU:
 // levo_hip_flow_incontext for the prefix interpolation, levo_hip_check_finite
 // for the entry checks and levo_hip_flow_cfg_euler_checked for the update and
-// its per-step finiteness checks.
+// its per-step finiteness checks; for a whole window with the estimator's
+// tensors in HBM, levo_hip_flow_assemble_input once and levo_hip_flow_step
+// after every estimator call.
 #include "levo-hip-flow-renderer.h"
 
 #include <cmath>
@@ -216,6 +218,128 @@ void solve_flow_euler_device(const device_euler_input & input, std::size_t steps
                              stream),
               "device-to-device copy");
     save(checkpoint, steps, state, n, stream);
+    synchronize(stream);
+}
+
+void solve_flow_window_device(const device_euler_input & input, const device_window_conditioning & conditioning,
+                              std::size_t steps, float guidance_scale, const device_estimator_tensors & estimator_io,
+                              const device_estimator_callback & estimator, float * state, float * denormalized,
+                              const euler_progress_callback & progress, const cancellation_callback & cancelled,
+                              const euler_resume_state * resume, euler_resume_state * checkpoint, stream_t stream) {
+    validate_common(steps, static_cast<bool>(estimator));
+    const std::size_t n = element_count(input.frames, input.latent_dim);
+    if (!input.initial_noise || !input.normalized_incontext || !state) {
+        fail("Euler tensors must have shape [frames, latent_dim]");
+    }
+    validate_prefix(input.frames, input.incontext_frames, input.sigma_min);
+    if (!estimator_io.model_input || !estimator_io.output) fail("estimator tensors are required");
+    if (estimator_io.hidden != conditioning.mask_dim + 2 * input.latent_dim + conditioning.condition_width) {
+        fail("estimator rows must hold mask embedding, in-context latent, conditioning and state");
+    }
+    if ((conditioning.mask_dim && !conditioning.mask_embedding) ||
+        (conditioning.condition_width && !conditioning.conditioning)) {
+        fail("conditioning tensors are required");
+    }
+    if (denormalized && (!conditioning.latent_mean || !conditioning.latent_stddev)) {
+        fail("denormalization needs the latent mean and standard deviation");
+    }
+    if (steps > static_cast<std::size_t>(std::numeric_limits<int64_t>::max())) fail("Euler step count is too large");
+
+    flag_word flags;
+    check_inputs_finite(flags, input.initial_noise, input.normalized_incontext, n, stream);
+
+    std::size_t completed_steps = 0;
+    if (resume) {
+        if (resume->completed_steps > steps) fail("Euler resume step exceeds total steps");
+        if (resume->normalized_state.size() != n) fail("Euler resume state has an unexpected shape");
+        check_hip(hipMemcpyAsync(state, resume->normalized_state.data(), n * sizeof(float), hipMemcpyHostToDevice,
+                                 stream),
+                  "host-to-device copy");
+        check_resume_finite(flags, state, n, stream);
+        completed_steps = resume->completed_steps;
+    } else {
+        check_hip(hipMemcpyAsync(state, input.initial_noise, n * sizeof(float), hipMemcpyDeviceToDevice, stream),
+                  "device-to-device copy");
+    }
+    save(checkpoint, completed_steps, state, n, stream);
+
+    const int32_t batch = guidance_scale > 1.0F ? 2 : 1;
+    const auto frames = static_cast<int64_t>(input.frames);
+    const auto latent = static_cast<int64_t>(input.latent_dim);
+    const auto hidden = static_cast<int64_t>(estimator_io.hidden);
+    const std::size_t prefix = input.incontext_frames * input.latent_dim;
+    if (completed_steps == steps) {
+        // Nothing left to integrate: restore the prefix and denormalize.
+        check_hip(hipMemcpyAsync(state, input.normalized_incontext, prefix * sizeof(float), hipMemcpyDeviceToDevice,
+                                 stream),
+                  "device-to-device copy");
+        save(checkpoint, steps, state, n, stream);
+        if (denormalized) {
+            flags.clear(stream);
+            check_status(levo_hip_flow_denormalize(state, conditioning.latent_mean, conditioning.latent_stddev,
+                                                   denormalized, frames, latent, flags.device(), stream),
+                         error_kind::runtime_error);
+            if (flags.read(stream)) {
+                throw std::runtime_error("LeVo Flow conditioning: normalized latent contains a non-finite value");
+            }
+        }
+        synchronize(stream);
+        return;
+    }
+
+    levo_hip_flow_input_args in{};
+    in.model_input = estimator_io.model_input;
+    in.batch = batch;
+    in.frames = frames;
+    in.mask_embedding = conditioning.mask_embedding;
+    in.mask_dim = static_cast<int64_t>(conditioning.mask_dim);
+    in.context = input.normalized_incontext;
+    in.latent = latent;
+    in.conditioning = conditioning.conditioning;
+    in.condition_width = static_cast<int64_t>(conditioning.condition_width);
+    in.state = state;
+    in.noise = input.initial_noise;
+    in.prefix_frames = static_cast<int64_t>(input.incontext_frames);
+    in.step = static_cast<int64_t>(completed_steps);
+    in.steps = static_cast<int64_t>(steps);
+    in.sigma_min = input.sigma_min;
+    check_status(levo_hip_flow_assemble_input(&in, stream), error_kind::runtime_error);
+
+    levo_hip_flow_step_args st{};
+    st.state = state;
+    st.output = estimator_io.output;
+    st.out_pitch = hidden;
+    st.vel_col = hidden - latent;
+    st.batch = batch;
+    st.guidance = guidance_scale;
+    st.frames = frames;
+    st.latent = latent;
+    st.steps = static_cast<int64_t>(steps);
+    st.noise = input.initial_noise;
+    st.context = input.normalized_incontext;
+    st.prefix_frames = static_cast<int64_t>(input.incontext_frames);
+    st.sigma_min = input.sigma_min;
+    st.next_input = estimator_io.model_input;
+    st.in_pitch = hidden;
+    st.state_col = hidden - latent;
+    st.mean = conditioning.latent_mean;
+    st.stddev = conditioning.latent_stddev;
+    st.denormalized = denormalized;
+    const float dt = 1.0F / static_cast<float>(steps);
+    for (std::size_t step = completed_steps; step < steps; ++step) {
+        if (cancelled && cancelled()) throw operation_cancelled();
+        const float time = static_cast<float>(step) * dt;
+        estimator(time, stream);
+        flags.clear(stream);
+        st.step = static_cast<int64_t>(step);
+        st.nonfinite = flags.device();
+        check_status(levo_hip_flow_step(&st, stream), error_kind::runtime_error);
+        const int32_t f = flags.read(stream);
+        if (f & LEVO_HIP_NONFINITE_VELOCITY) fail("Euler velocity contains a non-finite value");
+        if (f & LEVO_HIP_NONFINITE_STATE) fail("Euler state contains a non-finite value");
+        save(checkpoint, step + 1U, state, n, stream);
+        if (progress) progress(step + 1U, steps);
+    }
     synchronize(stream);
 }
 

@@ -97,5 +97,64 @@ void solve_flow_euler_device(
         euler_resume_state * checkpoint = nullptr,
         stream_t stream = nullptr);
 
+// ---- One Flow window with the estimator's tensors in HBM ---------------------
+
+// The estimator's input and output as estimator::velocity lays them out
+// (src/levo-flow-estimator.cpp:343-399), in device memory:
+// model_input [batch][frames][hidden] with rows
+//   mask_embedding | normalized_incontext | conditioning (zeros in the
+//   unconditional row) | state       (append_model_row, src/levo-flow-renderer.cpp:35-53)
+// and output [batch][frames][hidden] whose last latent_dim columns are the
+// velocity. batch is 2 (row 0 unconditional, row 1 conditional) when
+// guidance_scale > 1, else 1, as the renderer decides (:283-285).
+struct device_estimator_tensors {
+    float * model_input = nullptr;
+    const float * output = nullptr;
+    std::size_t hidden = 0;
+};
+
+// The window's conditioning_output in device memory
+// (src/levo-flow-conditioning.h): the parts of the estimator rows that stay
+// fixed over the steps, and the latent statistics for denormalize_latents.
+struct device_window_conditioning {
+    const float * mask_embedding = nullptr;  // [frames][mask_dim]
+    std::size_t mask_dim = 0;
+    const float * conditioning = nullptr;    // [frames][condition_width] (2 * condition_dim)
+    std::size_t condition_width = 0;
+    const float * latent_mean = nullptr;     // [latent_dim]; with latent_stddev, or both null
+    const float * latent_stddev = nullptr;
+};
+
+// Runs the estimator graph for `timestep` (every batch row) on `stream`:
+// reads model_input, writes output.
+using device_estimator_callback = std::function<void(float timestep, stream_t stream)>;
+
+// solve_flow_euler for one window as the renderer drives it
+// (src/levo-flow-renderer.cpp:283-331): the estimator input rows are built
+// once (levo_hip_flow_assemble_input), and after every estimator call one
+// levo_hip_flow_step launch reads the velocity slice, applies the CFG lambda,
+// the prefix interpolation and the Euler update with the reference's
+// finiteness checks, and writes the next step's state columns. After the
+// last step the prefix is restored and, when the statistics are given,
+// `denormalized` receives denormalize_latents (state * stddev + mean).
+// Per step only the 4-byte flag word comes back to the host. `state` (device,
+// frames * latent_dim floats) holds the reference's state after every step,
+// so a checkpoint or a resume matches bit for bit. Errors, progress,
+// cancellation, resume and checkpoint behave as in solve_flow_euler.
+void solve_flow_window_device(
+        const device_euler_input & input,
+        const device_window_conditioning & conditioning,
+        std::size_t steps,
+        float guidance_scale,
+        const device_estimator_tensors & estimator_io,
+        const device_estimator_callback & estimator,
+        float * state,
+        float * denormalized = nullptr,
+        const euler_progress_callback & progress = {},
+        const cancellation_callback & cancelled = {},
+        const euler_resume_state * resume = nullptr,
+        euler_resume_state * checkpoint = nullptr,
+        stream_t stream = nullptr);
+
 } // namespace flow
 } // namespace levo::hip

@@ -56,6 +56,29 @@ class DrawArgs(ctypes.Structure):
 TOKEN_NAN, TOKEN_OVERFLOW, TOKEN_RECHECK = -1, -2, -3
 
 
+class FlowInputArgs(ctypes.Structure):
+    """levo_hip_flow_input_args (include/levo_hip.h)."""
+
+    _fields_ = [
+        ("model_input", _P), ("batch", _I32), ("frames", _I64), ("mask_embedding", _P), ("mask_dim", _I64),
+        ("context", _P), ("latent", _I64), ("conditioning", _P), ("condition_width", _I64),
+        ("state", _P), ("noise", _P), ("prefix_frames", _I64), ("step", _I64), ("steps", _I64),
+        ("sigma_min", _F),
+    ]
+
+
+class FlowStepArgs(ctypes.Structure):
+    """levo_hip_flow_step_args (include/levo_hip.h)."""
+
+    _fields_ = [
+        ("state", _P), ("output", _P), ("out_pitch", _I64), ("vel_col", _I64), ("batch", _I32),
+        ("guidance", _F), ("frames", _I64), ("latent", _I64), ("step", _I64), ("steps", _I64),
+        ("noise", _P), ("context", _P), ("prefix_frames", _I64), ("sigma_min", _F),
+        ("next_input", _P), ("in_pitch", _I64), ("state_col", _I64),
+        ("mean", _P), ("stddev", _P), ("denormalized", _P), ("nonfinite", _P),
+    ]
+
+
 def header_abi_version(header: str = HEADER) -> int:
     """LEVO_HIP_ABI_VERSION as declared in include/levo_hip.h."""
     m = re.search(r"#define\s+LEVO_HIP_ABI_VERSION\s+(\d+)", open(header).read())
@@ -109,6 +132,10 @@ class LevoHip:
             "levo_hip_check_finite": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _P]),
             "levo_hip_repetition_penalty": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _F, _I64, _P]),
             "levo_hip_flow_incontext": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
+            "levo_hip_flow_assemble_input": (ctypes.c_int, [ctypes.POINTER(FlowInputArgs), _P]),
+            "levo_hip_flow_step": (ctypes.c_int, [ctypes.POINTER(FlowStepArgs), _P]),
+            "levo_hip_flow_normalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
+            "levo_hip_flow_denormalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
             "levo_hip_quantize_chunk": (_I64, [ctypes.c_int, _P, _P, _I64, _I64, _I64, _P, _P]),
             "levo_hip_quantize_rows": (_I64, [ctypes.c_int, _P, ctypes.c_int, _I64, _I64, _P, _I64, _I64, _P]),
@@ -177,6 +204,20 @@ class LevoHip:
     def flow_incontext(self, state, noise, context, n_prefix, time, sigma_min, stream=None):
         return self._check(self.lib.levo_hip_flow_incontext(_addr(state), _addr(noise), _addr(context), n_prefix,
                                                             time, sigma_min, _stream(stream)))
+
+    def flow_assemble_input(self, args: FlowInputArgs, stream=None):
+        return self._check(self.lib.levo_hip_flow_assemble_input(ctypes.byref(args), _stream(stream)))
+
+    def flow_step(self, args: FlowStepArgs, stream=None):
+        return self._check(self.lib.levo_hip_flow_step(ctypes.byref(args), _stream(stream)))
+
+    def flow_normalize(self, raw, mean, stddev, out, frames, latent, flags=None, stream=None):
+        return self._check(self.lib.levo_hip_flow_normalize(_addr(raw), _addr(mean), _addr(stddev), _addr(out),
+                                                             frames, latent, _addr(flags), _stream(stream)))
+
+    def flow_denormalize(self, x, mean, stddev, out, frames, latent, flags=None, stream=None):
+        return self._check(self.lib.levo_hip_flow_denormalize(_addr(x), _addr(mean), _addr(stddev), _addr(out),
+                                                               frames, latent, _addr(flags), _stream(stream)))
 
     def row_size(self, qtype, n):
         return self._check(self.lib.levo_hip_row_size(qtype, n))

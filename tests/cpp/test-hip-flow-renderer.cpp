@@ -2,7 +2,8 @@
 // (KAT, pause/resume bit-exactness, invalid resumes, cancellation) restated
 // against levo::hip::flow, the error messages of src/levo-flow-renderer.cpp,
 // and seeded parity of both solvers with the oracle's Euler restatement at the
-// renderer's per-window shape.
+// renderer's per-window shape, and the window solver that leaves the
+// estimator's tensors in device memory.
 #include "check.h"
 #include "levo-hip-flow-renderer.h"
 #include "levo_oracle.h"
@@ -251,6 +252,175 @@ void solver_parity() {
     CHECK(checkpoint.completed_steps == steps && checkpoint.normalized_state == dev);
 }
 
+// solve_flow_window_device at LeVo's window (1000 x 64, estimator rows
+// 24 | 64 | 2048 | 64, 250 in-context frames, CFG 1.5) against the oracle's
+// solver loop with the same stand-in estimator, computed on the host from
+// the device input rows: velocity = (state column * 0.5 - t) +
+// conditioning column * 0.25. The output columns outside the velocity slice
+// hold NaN. Also: cancellation + resume from the checkpoint, a resume that
+// has no step left, progress, and the errors.
+void window_parity() {
+    const std::size_t F = 1000, L = 64, M = 24, C = 2048, H = M + 2 * L + C, P = 250, n = F * L, steps = 12;
+    const float g = 1.5F, sigma = 1.0e-4F;
+    const auto gauss = [](std::size_t count, uint64_t seed) {
+        std::vector<float> v(count);
+        lo_gaussian_noise(v.data(), static_cast<int64_t>(count), seed);
+        return v;
+    };
+    const std::vector<float> mask = gauss(F * M, 31), ctx = gauss(n, 32), cond = gauss(F * C, 33),
+                             noise = gauss(n, 34);
+    std::vector<float> mean = gauss(L, 35), sd = gauss(L, 36);
+    for (auto & x : mean) x *= 0.1F;
+    for (auto & x : sd) x = std::fabs(x) * 0.5F + 0.5F;
+    const auto rows = [&](const std::vector<float> & state) {
+        std::vector<float> mi(2 * F * H);
+        for (std::size_t b = 0; b < 2; ++b) {
+            for (std::size_t f = 0; f < F; ++f) {
+                float * row = mi.data() + (b * F + f) * H;
+                std::copy_n(mask.data() + f * M, M, row);
+                std::copy_n(ctx.data() + f * L, L, row + M);
+                if (b == 0) std::fill_n(row + M + L, C, 0.0F);
+                else std::copy_n(cond.data() + f * C, C, row + M + L);
+                std::copy_n(state.data() + f * L, L, row + M + L + C);
+            }
+        }
+        return mi;
+    };
+    const auto velocity = [&](const float * mi, float t, std::size_t b, std::size_t f, std::size_t c) {
+        const float * row = mi + (b * F + f) * H;
+        return (row[H - L + c] * 0.5F - t) + row[M + L + c] * 0.25F;
+    };
+
+    // Oracle loop (src/levo-flow-renderer.cpp:89-117 + the CFG lambda).
+    const float dt = 1.0F / static_cast<float>(steps);
+    std::vector<float> want = noise, vu(n), vc(n);
+    std::vector<std::vector<float>> after;
+    for (std::size_t k = 0; k < steps; ++k) {
+        const float t = static_cast<float>(k) * dt;
+        lo_flow_incontext(want.data(), noise.data(), ctx.data(), static_cast<int64_t>(P * L), t, sigma);
+        const std::vector<float> mi = rows(want);
+        for (std::size_t f = 0; f < F; ++f) {
+            for (std::size_t c = 0; c < L; ++c) {
+                vu[f * L + c] = velocity(mi.data(), t, 0, f, c);
+                vc[f * L + c] = velocity(mi.data(), t, 1, f, c);
+            }
+        }
+        lo_flow_cfg_euler(want.data(), vu.data(), vc.data(), static_cast<int64_t>(n), g, dt);
+        after.push_back(want);
+    }
+    std::copy_n(ctx.begin(), P * L, want.begin());
+    std::vector<float> want_raw(n);
+    for (std::size_t e = 0; e < n; ++e) want_raw[e] = want[e] * sd[e % L] + mean[e % L];
+
+    device_buffer<float> d_mask(F * M), d_ctx(n), d_cond(F * C), d_noise(n), d_mean(L), d_sd(L), d_mi(2 * F * H),
+            d_out(2 * F * H), d_state(n), d_raw(n);
+    d_mask.upload(mask.data(), F * M, nullptr);
+    d_ctx.upload(ctx.data(), n, nullptr);
+    d_cond.upload(cond.data(), F * C, nullptr);
+    d_noise.upload(noise.data(), n, nullptr);
+    d_mean.upload(mean.data(), L, nullptr);
+    d_sd.upload(sd.data(), L, nullptr);
+    std::vector<float> host_out(2 * F * H, std::numeric_limits<float>::quiet_NaN()), host_mi(2 * F * H);
+    device_euler_input din;
+    din.initial_noise = d_noise.data();
+    din.normalized_incontext = d_ctx.data();
+    din.frames = F;
+    din.latent_dim = L;
+    din.incontext_frames = P;
+    din.sigma_min = sigma;
+    device_window_conditioning wc;
+    wc.mask_embedding = d_mask.data();
+    wc.mask_dim = M;
+    wc.conditioning = d_cond.data();
+    wc.condition_width = C;
+    wc.latent_mean = d_mean.data();
+    wc.latent_stddev = d_sd.data();
+    device_estimator_tensors io;
+    io.model_input = d_mi.data();
+    io.output = d_out.data();
+    io.hidden = H;
+    std::vector<float> times;
+    bool poison = false;
+    const device_estimator_callback estimator = [&](float t, stream_t stream) {
+        times.push_back(t);
+        d_mi.download(host_mi.data(), 2 * F * H, stream);
+        levo::hip::synchronize(stream);
+        for (std::size_t b = 0; b < 2; ++b) {
+            for (std::size_t f = 0; f < F; ++f) {
+                for (std::size_t c = 0; c < L; ++c) host_out[(b * F + f) * H + H - L + c] = velocity(host_mi.data(), t, b, f, c);
+            }
+        }
+        if (poison) host_out[(1 * F + 3) * H + H - 1] = std::numeric_limits<float>::quiet_NaN();
+        d_out.upload(host_out.data(), 2 * F * H, stream);
+    };
+    const auto download = [&](const device_buffer<float> & d) {
+        std::vector<float> h(n);
+        d.download(h.data(), n, nullptr);
+        levo::hip::synchronize(nullptr);
+        return h;
+    };
+
+    // Whole window, checkpoint after every step.
+    std::vector<std::size_t> progress;
+    euler_resume_state checkpoint;
+    solve_flow_window_device(din, wc, steps, g, io, estimator, d_state.data(), d_raw.data(),
+                             [&](std::size_t done, std::size_t total) {
+                                 CHECK(total == steps);
+                                 progress.push_back(done);
+                             },
+                             {}, nullptr, &checkpoint);
+    CHECK(progress.size() == steps && progress.back() == steps);
+    CHECK(times.size() == steps && times[3] == 3.0F * dt);
+    CHECK(bit_equal(download(d_state).data(), want.data(), n));
+    CHECK(bit_equal(download(d_raw).data(), want_raw.data(), n));
+    CHECK(checkpoint.completed_steps == steps && bit_equal(checkpoint.normalized_state.data(), want.data(), n));
+
+    // Cancel after 5 steps: the checkpoint is the reference's state after
+    // step 5; resuming from it finishes bit for bit.
+    std::size_t polls = 0;
+    euler_resume_state paused;
+    expect_throw<levo::hip::operation_cancelled>("cancelled", [&] {
+        solve_flow_window_device(din, wc, steps, g, io, estimator, d_state.data(), d_raw.data(), {},
+                                 [&] { return polls++ == 5; }, nullptr, &paused);
+    });
+    CHECK(paused.completed_steps == 5 && bit_equal(paused.normalized_state.data(), after[4].data(), n));
+    times.clear();
+    solve_flow_window_device(din, wc, steps, g, io, estimator, d_state.data(), d_raw.data(), {}, {}, &paused);
+    CHECK(times.size() == steps - 5 && times[0] == 5.0F * dt);
+    CHECK(bit_equal(download(d_state).data(), want.data(), n));
+    CHECK(bit_equal(download(d_raw).data(), want_raw.data(), n));
+
+    // A resume with every step done: prefix restore and denormalization only.
+    euler_resume_state done;
+    done.completed_steps = steps;
+    done.normalized_state = after.back();
+    times.clear();
+    solve_flow_window_device(din, wc, steps, g, io, estimator, d_state.data(), d_raw.data(), {}, {}, &done);
+    CHECK(times.empty());
+    CHECK(bit_equal(download(d_state).data(), want.data(), n));
+    CHECK(bit_equal(download(d_raw).data(), want_raw.data(), n));
+
+    // Errors.
+    poison = true;
+    expect_throw<std::runtime_error>("LeVo Flow renderer: Euler velocity contains a non-finite value", [&] {
+        solve_flow_window_device(din, wc, steps, g, io, estimator, d_state.data());
+    });
+    poison = false;
+    device_estimator_tensors bad = io;
+    bad.hidden = H + 4;
+    expect_throw<std::runtime_error>("estimator rows must hold", [&] {
+        solve_flow_window_device(din, wc, steps, g, bad, estimator, d_state.data());
+    });
+    device_window_conditioning no_stats = wc;
+    no_stats.latent_stddev = nullptr;
+    expect_throw<std::runtime_error>("denormalization needs", [&] {
+        solve_flow_window_device(din, no_stats, steps, g, io, estimator, d_state.data(), d_raw.data());
+    });
+    expect_throw<std::runtime_error>("Euler step count must be positive", [&] {
+        solve_flow_window_device(din, wc, 0, g, io, estimator, d_state.data());
+    });
+}
+
 } // namespace
 
 int main() {
@@ -258,6 +428,7 @@ int main() {
         reference_assertions();
         error_behaviour();
         solver_parity();
+        window_parity();
     } catch (const std::exception & e) {
         std::cerr << "unexpected exception: " << e.what() << '\n';
         return 1;
