@@ -457,6 +457,77 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
                     bound="latency")
 
 
+def bench_mul_mat(torch, hip, head, dev, warmup, steps):
+    """Q8_0 decode mat-vec at LeLM medium's matrices (hidden 1536, FFN 8960,
+    codebook head 16385) with the CFG pair of activation columns, already
+    quantized to Q8_0; weights rotated over >= 512 MB. `layer`: one decoder
+    layer's decode step as it runs: the 4 activation quantizations
+    (levo_hip_quantize_chunk: attention input, attention output, FFN input,
+    FFN hidden) and the 7 matrices (q, k, v, o, gate, up, down)."""
+    shapes = {"attn_1536x1536": (1536, 1536), "ffn_up_8960x1536": (8960, 1536),
+              "ffn_down_1536x8960": (1536, 8960), "head_16385x1536": (16385, 1536)}
+    n_vec = 2
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(34)
+
+    def mk(rows, k, n):
+        nbytes = rows * (k // 32) * 34
+        stride = (nbytes + 255) // 256 * 256
+        w = torch.randint(-127, 128, (n, stride), generator=g, device=dev, dtype=torch.int8).view(torch.uint8)
+        scale = torch.full((rows * (k // 32),), 0x2000, dtype=torch.int16, device=dev)  # F16 2^-7 scales
+        for i in range(n):
+            w[i, :nbytes].view(rows * (k // 32), 34)[:, :2] = scale.view(torch.uint8).view(-1, 2)
+        return w
+
+    def quantized(k):
+        x = torch.randn((n_vec, k), generator=g, device=dev)
+        xb = torch.empty(n_vec * (k // 32) * 34 + 16, dtype=torch.uint8, device=dev)
+        hip.quantize_chunk(8, x, xb, 0, n_vec, k)
+        return x, xb
+
+    for name, (rows, k) in shapes.items():
+        nbytes = rows * (k // 32) * 34
+        per = nbytes + n_vec * (k // 32) * 34 + n_vec * rows * 4
+        n = math.ceil(ROTATE_BYTES / nbytes) + 1
+        w = mk(rows, k, n)
+        _, xb = quantized(k)
+        y = torch.empty((n_vec, rows), device=dev)
+        ms = time_op(torch, head, lambda i: hip.mul_mat_q8_0(w[i].data_ptr(), xb, y, rows, rows, k, n_vec),
+                     n, warmup, max(steps, 50))
+        out[name] = op_entry(per, ms, shape=[rows, k], n_vec=n_vec, dtype="q8_0 weights / q8_0 activations")
+        del w
+    layer = [(1536, 1536)] * 4 + [(8960, 1536)] * 2 + [(1536, 8960)]
+    layer_bytes = sum(r * (k // 32) * 34 + n_vec * (k // 32) * 34 + n_vec * r * 4 for r, k in layer)
+    layer_bytes += 3 * n_vec * 1536 * (4 + 34 / 32) + n_vec * 8960 * (4 + 34 / 32)
+    n = math.ceil(ROTATE_BYTES / layer_bytes) + 1
+    mats = [[mk(r, k, 1)[0] for r, k in layer] for _ in range(n)]
+    x_attn, xb_attn = quantized(1536)
+    x_out, xb_out = quantized(1536)
+    x_ffn, xb_ffn = quantized(1536)
+    x_hid, xb_hid = quantized(8960)
+    ys = {r: torch.empty((n_vec, r), device=dev) for r in (1536, 8960)}
+    plan = [(xb_attn, 1536, 1536)] * 3 + [(xb_out, 1536, 1536)] + [(xb_ffn, 8960, 1536)] * 2 + [(xb_hid, 1536, 8960)]
+
+    def run_layer(i):
+        hip.quantize_chunk(8, x_attn, xb_attn, 0, n_vec, 1536)
+        for j in range(3):
+            hip.mul_mat_q8_0(mats[i][j].data_ptr(), xb_attn, ys[1536], 1536, 1536, 1536, n_vec)
+        hip.quantize_chunk(8, x_out, xb_out, 0, n_vec, 1536)
+        hip.mul_mat_q8_0(mats[i][3].data_ptr(), xb_out, ys[1536], 1536, 1536, 1536, n_vec)
+        hip.quantize_chunk(8, x_ffn, xb_ffn, 0, n_vec, 1536)
+        for j in (4, 5):
+            hip.mul_mat_q8_0(mats[i][j].data_ptr(), xb_ffn, ys[8960], 8960, 8960, 1536, n_vec)
+        hip.quantize_chunk(8, x_hid, xb_hid, 0, n_vec, 8960)
+        hip.mul_mat_q8_0(mats[i][6].data_ptr(), xb_hid, ys[1536], 1536, 1536, 8960, n_vec)
+
+    ms = time_op(torch, head, run_layer, n, warmup, max(steps, 20))
+    out["layer_4_quantize_7_matrices"] = op_entry(layer_bytes, ms, n_vec=n_vec,
+                                                  dtype="q8_0 weights / q8_0 activations",
+                                                  us_per_token_28_layers=round(28 * ms * 1e3, 1))
+    return out
+
+
 def bench_quant(torch, hip, head, dev, warmup, steps):
     R, Cc = 4096, 1536
     out = {}
@@ -631,7 +702,7 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-ops", action="store_true", help="only the headline ladder")
     p.add_argument("--only", default="",
-                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant); "
+                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant,gemv); "
                         "prints the op table without the headline ladder")
     p.add_argument("--copy-ceiling", action="store_true",
                    help="with --only: annotate each op with a plain device copy of the same bytes")
@@ -678,6 +749,8 @@ def main() -> int:
                                                                     args.steps)
         if "quant" in groups:
             ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
+        if "gemv" in groups:
+            ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
         if args.copy_ceiling:
             add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
         print(json.dumps({"ops": ops}))
@@ -722,6 +795,8 @@ def main() -> int:
                                                                 args.steps)
         log("ops: quant")
         ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
+        log("ops: q8_0 mat-vec")
+        ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: plain-copy ceilings")
         add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 

@@ -335,6 +335,21 @@ int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, levo_hip_ty
 int levo_hip_dequantize(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type,
                         int64_t k, levo_hip_stream_t stream);
 
+/* Decode mat-vec with Q8_0 weights and Q8_0 activations: the
+ * ggml_vec_dot_q8_0_q8_0 rows of ggml_mul_mat(W, x) on ggml's CPU backend
+ * for the quantized LeLM / Flow matrices (src/levo-quantization.h:96-118).
+ * weight: [rows][k/32] block_q8_0; x_blocks: [n_vec][k/32] block_q8_0, the
+ * activation columns quantized once with levo_hip_quantize_chunk (ggml's
+ * vec_dot_type for Q8_0 is Q8_0), shared by every matrix with that input;
+ * both 16-byte aligned. y: [n_vec][y_pitch] F32, y[v][r] = sum over blocks of
+ * (float)sumi * (d_w * d_x), sumi the exact int32 dot of the quants. The F32
+ * terms are summed in a tree, so y agrees with ggml's sequential loop to F32
+ * rounding. k a multiple of 32 (pad rows as padded_input_columns does,
+ * :120-130), k <= 32768; 1 <= n_vec <= 8, n_vec * k <= 26000 or so (the
+ * activations live in the workgroup's LDS; k = 11008 at n_vec = 2 fits). */
+int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks, float * y, int64_t y_pitch,
+                          int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream);
+
 /* ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row (tools/levo-quantize.cpp:
  * 358, 369): IEEE round-to-nearest-even narrowing, exact widening. */
 int levo_hip_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, levo_hip_stream_t stream);

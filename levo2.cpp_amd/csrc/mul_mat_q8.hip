@@ -1,0 +1,295 @@
+// Decode mat-vec with Q8_0 weights and Q8_0 activations:
+// y[v][r] = sum_b (float)sumi(W[r][b], X[v][b]) * (d_w * d_x), the
+// ggml_vec_dot_q8_0_q8_0 that ggml's CPU mul_mat runs for a Q8_0 weight once
+// the activation columns are quantized to Q8_0 (its vec_dot_type); the
+// quantized LeLM / Flow matrices (src/levo-quantization.h:96-118) take it at
+// every decode step. sumi is the exact int32 dot of the two blocks' quants;
+// the F32 terms are summed in a different order than ggml's loop, so outputs
+// agree to F32 rounding. The activations come quantized (for example by
+// levo_hip_quantize_chunk), once per input vector, so the GEMVs that share an
+// input (q / k / v, gate / up) share the quantization too.
+//
+// One 256-thread workgroup (4 waves) per group of rows, all launched at
+// once so that the whole matrix is requested up front; per workgroup:
+//   1. each wave issues coalesced dwordx4 loads of its span of weight blocks
+//      (contiguous bytes, at most 256 blocks = 8704 B);
+//   2. while they are in flight the workgroup stages the activation blocks
+//      and unpacks them in LDS (quants as aligned dwords, scales as F32);
+//   3. the wave stores its span in LDS and computes: a group of LPR lanes
+//      per row, each lane a strided subset of the row's blocks, v_dot4 for
+//      sumi, then the F32 term; a shuffle reduction over the group gives y.
+// Geometry by blocks per row nb: nb <= 64: 16 lanes per row (16 rows per
+// workgroup); nb <= 128: 32 lanes (8 rows); nb <= 256: 64 lanes (4 rows);
+// nb <= 512 / 1024: a row is split over 2 / 4 waves (2 / 1 rows per
+// workgroup), whose partial sums meet in LDS in wave order (LeLM's
+// ffn_down, K = 8960 / 11008).
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace levo_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kQ8Bytes = 34;
+constexpr int kSpanBlocks = 256;
+constexpr int kChunksPerLane = (kSpanBlocks * kQ8Bytes + 15 + 15) / 16 / 64 + 1;
+constexpr int kMaxVectors = 8;
+constexpr int kMaxBlocksPerRow = 1024;
+
+struct mm_params {
+    const uint8_t * w;    // [rows][nb] weight blocks, 16-byte aligned
+    const uint8_t * x;    // [n_vec][nb] activation blocks, 16-byte aligned
+    float * y;            // [n_vec][y_pitch]
+    int64_t rows;
+    int64_t w_bytes;      // rows * nb * 34
+    int64_t y_pitch;
+    int32_t nb;           // blocks per row (K / 32)
+    int32_t n_vec;
+    int32_t stage_bytes;  // LDS bytes per wave for its weight span
+};
+
+// Coalesced loads of the 16-byte chunks covering bytes [a0, b1) of `base`
+// (a0 16-byte aligned): lane l takes chunks l, l + 64, ... A chunk that
+// would cross `limit` is read as half-words.
+__device__ __forceinline__ void load_span(const uint8_t * base, int64_t limit, int64_t a0, int64_t b1, int lane,
+                                          u32x4 (&r)[kChunksPerLane]) {
+    const int nchunks = static_cast<int>((b1 - a0 + 15) >> 4);
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+        const int c = lane + 64 * i;
+        const int64_t at = a0 + 16 * static_cast<int64_t>(c);
+        if (c < nchunks) {
+            if (at + 16 <= limit) {
+                r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + at));
+            } else {
+                uint32_t h[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    h[k] = at + 2 * k + 2 <= limit ? *reinterpret_cast<const uint16_t *>(base + at + 2 * k) : 0u;
+                }
+                r[i] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void store_span(uint8_t * stage, int64_t a0, int64_t b1, int lane,
+                                           const u32x4 (&r)[kChunksPerLane]) {
+    const int nchunks = static_cast<int>((b1 - a0 + 15) >> 4);
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nchunks) reinterpret_cast<u32x4 *>(stage)[c] = r[i];
+    }
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Block at LDS byte offset `off` (even): its F16 scale and 8 quant dwords.
+// The quants start at off + 2; the dwords read from (off + 2) & ~3 hold them
+// shifted by 0 (off = 2 mod 4) or 16 bits (off = 0 mod 4).
+__device__ __forceinline__ float read_block(const uint8_t * stage, int off, uint32_t (&q)[8]) {
+    const int qa = (off + 2) & ~3;
+    const uint32_t * wd = reinterpret_cast<const uint32_t *>(stage + qa);
+    uint32_t w[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w[i] = wd[i];
+    const uint32_t shift = (off & 2) ? 0u : 16u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], shift);
+    return h2f(*reinterpret_cast<const uint16_t *>(stage + off));
+}
+
+// Rows and blocks of wave `wave` in workgroup `grp`: WPR waves share a row
+// (each a contiguous part of its blocks), a wave of a WPR = 1 geometry takes
+// 64 / LPR whole rows. Returns false when the wave has nothing to do.
+template <int LPR, int WPR>
+__device__ __forceinline__ bool wave_span(const mm_params & p, int64_t grp, int wave, int64_t & row0, int & nrows,
+                                          int & kb0, int & kb1) {
+    if constexpr (WPR > 1) {
+        row0 = grp * (kWaves / WPR) + wave / WPR;
+        nrows = 1;
+        const int q = (p.nb + WPR - 1) / WPR;
+        kb0 = (wave % WPR) * q;
+        kb1 = kb0 + q < p.nb ? kb0 + q : p.nb;
+        return row0 < p.rows && kb0 < kb1;
+    } else {
+        constexpr int RPW = 64 / LPR;
+        row0 = (grp * kWaves + wave) * RPW;
+        const int64_t left = p.rows - row0;
+        nrows = left < RPW ? (left > 0 ? static_cast<int>(left) : 0) : RPW;
+        kb0 = 0;
+        kb1 = p.nb;
+        return nrows > 0;
+    }
+}
+
+template <int LPR, int WPR>
+__global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int nvb = p.n_vec * p.nb;
+    uint32_t * xq = reinterpret_cast<uint32_t *>(smem);                   // [n_vec][nb][8]
+    float * dx = reinterpret_cast<float *>(smem + nvb * 32);               // [n_vec][nb]
+    float * part = dx + nvb;                                               // [kWaves][kMaxVectors]
+    uint8_t * stages = smem + ((nvb * 36 + kWaves * kMaxVectors * 4 + 15) & ~15);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    uint8_t * stage = stages + wave * p.stage_bytes;
+
+    // 1. this wave's weight loads
+    int64_t row0;
+    int nrows, kb0, kb1;
+    const bool have = wave_span<LPR, WPR>(p, blockIdx.x, wave, row0, nrows, kb0, kb1);
+    u32x4 regs[kChunksPerLane];
+    const int64_t sb0 = (row0 * p.nb + kb0) * kQ8Bytes;
+    const int64_t sb1 = (row0 * p.nb + (WPR > 1 ? kb1 : static_cast<int64_t>(nrows) * p.nb)) * kQ8Bytes;
+    if (have) load_span(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, lane, regs);
+
+    // 2. activation blocks -> LDS (raw, through the stage area), then
+    //    unpacked to aligned quant dwords and F32 scales
+    {
+        const int64_t xbytes = static_cast<int64_t>(nvb) * kQ8Bytes;
+        const int nchunks = static_cast<int>((xbytes + 15) >> 4);
+        for (int c = threadIdx.x; c < nchunks; c += kThreads) {
+            const int64_t at = 16 * static_cast<int64_t>(c);
+            u32x4 v;
+            if (at + 16 <= xbytes) {
+                v = *reinterpret_cast<const u32x4 *>(p.x + at);
+            } else {
+                uint32_t h[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    h[k] = at + 2 * k + 2 <= xbytes ? *reinterpret_cast<const uint16_t *>(p.x + at + 2 * k) : 0u;
+                }
+                v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+            }
+            reinterpret_cast<u32x4 *>(stages)[c] = v;
+        }
+        __syncthreads();
+        for (int t = threadIdx.x; t < nvb; t += kThreads) {
+            uint32_t q[8];
+            dx[t] = read_block(stages, t * kQ8Bytes, q);
+            u32x4 * dst = reinterpret_cast<u32x4 *>(xq + t * 8);
+            dst[0] = u32x4{q[0], q[1], q[2], q[3]};
+            dst[1] = u32x4{q[4], q[5], q[6], q[7]};
+        }
+        __syncthreads();
+    }
+
+    // 3. the wave's blocks: lane li of row group g takes kb = kb0 + li + LPR * i
+    const int g = lane / LPR;
+    const int li = lane % LPR;
+    const int lead = static_cast<int>(sb0 & 15);
+    if (have) store_span(stage, sb0 & ~int64_t{15}, sb1, lane, regs);
+    wave_lds_fence();
+    float acc[kMaxVectors];
+#pragma unroll
+    for (int v = 0; v < kMaxVectors; ++v) acc[v] = 0.0f;
+    if (have && g < nrows) {
+        const int row_base = WPR > 1 ? 0 : g * p.nb;  // LDS block index of (row g, kb0)
+        for (int kb = kb0 + li; kb < kb1; kb += LPR) {
+            uint32_t q[8];
+            const float dw = read_block(stage, lead + (row_base + kb - kb0) * kQ8Bytes, q);
+#pragma unroll
+            for (int v = 0; v < kMaxVectors; ++v) {
+                if (v >= p.n_vec) break;
+                const u32x4 * xb = reinterpret_cast<const u32x4 *>(xq + (v * p.nb + kb) * 8);
+                const u32x4 x0 = xb[0];
+                const u32x4 x1 = xb[1];
+                int s = 0;
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[0]), static_cast<int>(x0.x), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[1]), static_cast<int>(x0.y), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[2]), static_cast<int>(x0.z), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[3]), static_cast<int>(x0.w), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[4]), static_cast<int>(x1.x), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[5]), static_cast<int>(x1.y), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[6]), static_cast<int>(x1.z), s, false);
+                s = __builtin_amdgcn_sdot4(static_cast<int>(q[7]), static_cast<int>(x1.w), s, false);
+                acc[v] += static_cast<float>(s) * (dw * dx[v * p.nb + kb]);
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < kMaxVectors; ++v) {
+        if (v >= p.n_vec) break;
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) acc[v] += __shfl_xor(acc[v], o, 64);
+    }
+    if constexpr (WPR > 1) {
+        // the row's parts meet in LDS, summed in wave order
+        if (lane == 0) {
+#pragma unroll
+            for (int v = 0; v < kMaxVectors; ++v) part[wave * kMaxVectors + v] = acc[v];
+        }
+        __syncthreads();
+        if (wave % WPR == 0 && lane < p.n_vec && row0 < p.rows) {
+            float s = part[wave * kMaxVectors + lane];
+#pragma unroll
+            for (int w = 1; w < WPR; ++w) s += part[(wave + w) * kMaxVectors + lane];
+            p.y[lane * p.y_pitch + row0] = s;
+        }
+    } else if (have && g < nrows && li == 0) {
+#pragma unroll
+        for (int v = 0; v < kMaxVectors; ++v) {
+            if (v >= p.n_vec) break;
+            p.y[v * p.y_pitch + row0 + g] = acc[v];
+        }
+    }
+}
+
+template <int LPR, int WPR>
+int launch_mm(mm_params p, hipStream_t st) {
+    constexpr int rows_per_block = WPR > 1 ? kWaves / WPR : kWaves * (64 / LPR);
+    const int span_blocks = WPR > 1 ? (p.nb + WPR - 1) / WPR : (64 / LPR) * p.nb;
+    p.stage_bytes = (span_blocks * kQ8Bytes + 32 + 15) & ~15;
+    const int64_t nvb = static_cast<int64_t>(p.n_vec) * p.nb;
+    // The raw activation blocks pass through the stage area before unpacking
+    // (unpacking the last one reads 4 bytes past it), so it holds both.
+    const int64_t stages = std::max<int64_t>(int64_t{kWaves} * p.stage_bytes, (nvb * kQ8Bytes + 16 + 15) & ~int64_t{15});
+    const size_t lds = ((static_cast<size_t>(nvb) * 36 + kWaves * kMaxVectors * 4 + 15) & ~size_t{15}) +
+                       static_cast<size_t>(stages);
+    LEVO_REQUIRE(lds <= 64 * 1024, "mul_mat_q8_0: n_vec * K too large for the workgroup's LDS");
+    const uint32_t blocks = static_cast<uint32_t>(ceil_div(p.rows, rows_per_block));
+    mul_mat_q8_0_kernel<LPR, WPR><<<blocks, kThreads, lds, st>>>(p);
+    return launch_status("levo_hip_mul_mat_q8_0");
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+using namespace levo_hip;
+
+extern "C" int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks, float * y, int64_t y_pitch,
+                                     int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(rows >= 0 && n_vec >= 0, "mul_mat_q8_0: negative size");
+    if (rows == 0 || n_vec == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(k > 0 && k % 32 == 0, "mul_mat_q8_0: K must be a positive multiple of 32 (pad the rows)");
+    LEVO_REQUIRE(k / 32 <= kMaxBlocksPerRow, "mul_mat_q8_0: K exceeds %d", kMaxBlocksPerRow * 32);
+    LEVO_REQUIRE(n_vec <= kMaxVectors, "mul_mat_q8_0: at most %d activation columns", kMaxVectors);
+    LEVO_REQUIRE(rows < (int64_t{1} << 31) / 4, "mul_mat_q8_0: too many rows");
+    LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "mul_mat_q8_0: null tensor");
+    LEVO_REQUIRE(aligned16(weight) && aligned16(x_blocks), "mul_mat_q8_0: block buffers must be 16-byte aligned");
+    LEVO_REQUIRE(y_pitch >= rows, "mul_mat_q8_0: y pitch smaller than the row count");
+    mm_params p;
+    p.w = static_cast<const uint8_t *>(weight);
+    p.x = static_cast<const uint8_t *>(x_blocks);
+    p.y = y;
+    p.rows = rows;
+    p.nb = static_cast<int32_t>(k / 32);
+    p.w_bytes = rows * p.nb * kQ8Bytes;
+    p.y_pitch = y_pitch;
+    p.n_vec = static_cast<int32_t>(n_vec);
+    p.stage_bytes = 0;
+    const hipStream_t st = as_hip(stream);
+    if (p.nb <= 64) return launch_mm<16, 1>(p, st);
+    if (p.nb <= 128) return launch_mm<32, 1>(p, st);
+    if (p.nb <= 256) return launch_mm<64, 1>(p, st);
+    if (p.nb <= 512) return launch_mm<64, 2>(p, st);
+    return launch_mm<64, 4>(p, st);
+}

@@ -25,6 +25,18 @@ std::size_t quantize_rows(levo_hip_type type, const void * src, levo_hip_type sr
             levo_hip_quantize_rows(type, src, src_type, src_cols, src_row_stride, dst, nrows, dst_cols, stream)));
 }
 
+void mul_mat_q8_0(const void * weight, const float * x, void * x_blocks, float * y, int64_t rows, int64_t k,
+                  int64_t n_vec, stream_t stream) {
+    if (rows == 0 || n_vec == 0) return;
+    check_status(levo_hip_quantize_chunk(LEVO_HIP_TYPE_Q8_0, x, x_blocks, 0, n_vec, k, nullptr, stream));
+    mul_mat_q8_0_quantized(weight, x_blocks, y, rows, k, n_vec, stream);
+}
+
+void mul_mat_q8_0_quantized(const void * weight, const void * x_blocks, float * y, int64_t rows, int64_t k,
+                            int64_t n_vec, stream_t stream) {
+    check_status(levo_hip_mul_mat_q8_0(weight, x_blocks, y, rows, rows, k, n_vec, stream));
+}
+
 void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream) {
     check_status(levo_hip_dequantize(type, src, dst, LEVO_HIP_TYPE_F32, k, stream));
 }

@@ -2,8 +2,10 @@
 // ggml_quantize_chunk / ggml_row_size (tools/levo-quantize.cpp:386-388),
 // padded_input_columns (src/levo-quantization.h:120-125), write_tensor's
 // widen -> pad -> quantize chunk (tools/levo-quantize.cpp:355-388), the
-// dequantizers and the F16 row converters (:358, :369). Q8_0 and Q4_0 blocks
-// are ggml's byte layouts. Errors are std::invalid_argument.
+// dequantizers and the F16 row converters (:358, :369), and the decode
+// mat-vec of a Q8_0 matrix (ggml_mul_mat on the quantized LeLM / Flow
+// weights, src/levo-quantization.h:96-118). Q8_0 and Q4_0 blocks are ggml's
+// byte layouts. Errors are std::invalid_argument.
 #pragma once
 
 #include "levo-hip-device.h"
@@ -34,6 +36,18 @@ std::size_t quantize_rows(levo_hip_type type, const void * src, levo_hip_type sr
 
 // ggml's to_float for Q8_0 / Q4_0: k values (a multiple of 32).
 void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream = nullptr);
+
+// ggml_mul_mat(W, x) for a Q8_0 weight at decode, as ggml's CPU backend
+// computes it: x [n_vec][k] F32 is quantized to Q8_0 (ggml's vec_dot_type for
+// Q8_0) into x_blocks (n_vec * row_size(Q8_0, k) bytes, 16-byte aligned), then
+// y [n_vec][rows] = sum over blocks of sumi * (d_w * d_x). weight is
+// [rows][k / 32] block_q8_0, 16-byte aligned; every pointer is device memory.
+// For further matrices with the same input, mul_mat_q8_0_quantized reuses
+// x_blocks. k a multiple of 32, 1 <= n_vec <= 8.
+void mul_mat_q8_0(const void * weight, const float * x, void * x_blocks, float * y, int64_t rows, int64_t k,
+                  int64_t n_vec, stream_t stream = nullptr);
+void mul_mat_q8_0_quantized(const void * weight, const void * x_blocks, float * y, int64_t rows, int64_t k,
+                            int64_t n_vec, stream_t stream = nullptr);
 
 void fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, stream_t stream = nullptr);
 void fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n, stream_t stream = nullptr);

@@ -136,6 +136,7 @@ class LevoHip:
             "levo_hip_flow_step": (ctypes.c_int, [ctypes.POINTER(FlowStepArgs), _P]),
             "levo_hip_flow_normalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_flow_denormalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
+            "levo_hip_mul_mat_q8_0": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
             "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
             "levo_hip_quantize_chunk": (_I64, [ctypes.c_int, _P, _P, _I64, _I64, _I64, _P, _P]),
             "levo_hip_quantize_rows": (_I64, [ctypes.c_int, _P, ctypes.c_int, _I64, _I64, _P, _I64, _I64, _P]),
@@ -218,6 +219,10 @@ class LevoHip:
     def flow_denormalize(self, x, mean, stddev, out, frames, latent, flags=None, stream=None):
         return self._check(self.lib.levo_hip_flow_denormalize(_addr(x), _addr(mean), _addr(stddev), _addr(out),
                                                                frames, latent, _addr(flags), _stream(stream)))
+
+    def mul_mat_q8_0(self, weight, x_blocks, y, y_pitch, rows, k, n_vec, stream=None):
+        return self._check(self.lib.levo_hip_mul_mat_q8_0(_addr(weight), _addr(x_blocks), _addr(y), y_pitch,
+                                                          rows, k, n_vec, _stream(stream)))
 
     def row_size(self, qtype, n):
         return self._check(self.lib.levo_hip_row_size(qtype, n))

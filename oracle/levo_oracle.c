@@ -700,3 +700,31 @@ void lo_gaussian_noise(float * out, int64_t count, uint64_t seed) {
         if (i + 1 < count) out[i + 1] = (float)(radius * sin(angle));
     }
 }
+
+/* ------------------------------------------------------------------------- */
+/* Q8_0 x Q8_0 matrix-vector product (ggml CPU mul_mat, generic vec_dot)      */
+/* ------------------------------------------------------------------------- */
+
+void lo_mul_mat_q8_0(const void * w, const float * x, float * y, int64_t rows, int64_t k, int64_t n_vec) {
+    const int64_t nb = k / 32;
+    unsigned char * xq = (unsigned char *)malloc((size_t)(nb * 34));
+    if (!xq) return;
+    for (int64_t v = 0; v < n_vec; ++v) {
+        lo_quantize_row_q8_0(x + v * k, xq, k);
+        for (int64_t r = 0; r < rows; ++r) {
+            const unsigned char * wr = (const unsigned char *)w + r * nb * 34;
+            float sumf = 0.0f;
+            for (int64_t ib = 0; ib < nb; ++ib) {
+                const unsigned char * bw = wr + ib * 34;
+                const unsigned char * bx = xq + ib * 34;
+                int sumi = 0;
+                for (int j = 0; j < 32; ++j) sumi += (int)(int8_t)bw[2 + j] * (int)(int8_t)bx[2 + j];
+                const float dw = lo_fp16_to_fp32((uint16_t)(bw[0] | (bw[1] << 8)));
+                const float dx = lo_fp16_to_fp32((uint16_t)(bx[0] | (bx[1] << 8)));
+                sumf += (float)sumi * (dw * dx);
+            }
+            y[v * rows + r] = sumf;
+        }
+    }
+    free(xq);
+}

@@ -32,6 +32,9 @@
  *   lo_quantize_row_q8_0 / q4_0 .......... reference KAT (tests/test-quantization.cpp:32-81),
  *                                          block invariants, numpy restatement of ggml's
  *                                          published reference quantizer
+ *   lo_mul_mat_q8_0 ...................... float64 sum of the same block terms within the
+ *                                          sequential-sum error bound; integer-valued
+ *                                          blocks (d = 1) equal the exact integer product
  */
 #ifndef LEVO_ORACLE_H
 #define LEVO_ORACLE_H
@@ -148,6 +151,15 @@ void lo_quantize_row_q8_0(const float * x, void * y, int64_t k);
 void lo_quantize_row_q4_0(const float * x, void * y, int64_t k);
 void lo_dequantize_row_q8_0(const void * x, float * y, int64_t k);
 void lo_dequantize_row_q4_0(const void * x, float * y, int64_t k);
+/* ggml_mul_mat(W, x) on ggml's CPU backend for a Q8_0 weight (the quantized
+ * LeLM / Flow matrices, src/levo-quantization.h:96-118): W is [rows][k/32]
+ * Q8_0 blocks, x [n_vec][k] F32, y [n_vec][rows]. Each activation column is
+ * quantized with lo_quantize_row_q8_0 (Q8_0's vec_dot_type is Q8_0), then
+ * every row takes ggml_vec_dot_q8_0_q8_0's generic loop: per block the exact
+ * int32 dot sumi of the quants, sumf += sumi * (d_w * d_x) in block order,
+ * F32. (ggml's SIMD variants sum the same terms in another order.) */
+void lo_mul_mat_q8_0(const void * w, const float * x, float * y, int64_t rows, int64_t k, int64_t n_vec);
+
 /* ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, NULL).
  * Returns bytes written or 0 for an unsupported type. */
 size_t lo_quantize_chunk(int type, const float * src, void * dst, int64_t start, int64_t nrows,

@@ -70,6 +70,7 @@ class Oracle:
             "lo_quantize_chunk": (ctypes.c_size_t, [ctypes.c_int, _P, _P, _I64, _I64, _I64]),
             "lo_quantize_f16_rows_padded": (ctypes.c_size_t, [ctypes.c_int, _P, _I64, _I64, _I64, _P]),
             "lo_dequantize_row_q8_0": (None, [_P, _P, _I64]),
+            "lo_mul_mat_q8_0": (None, [_P, _P, _P, _I64, _I64, _I64]),
             "lo_dequantize_row_q4_0": (None, [_P, _P, _I64]),
             "lo_gaussian_noise": (None, [_P, _I64, ctypes.c_uint64]),
         }
@@ -211,6 +212,14 @@ class Oracle:
         n = self.lib.lo_quantize_f16_rows_padded(qtype, _ptr(x), rows, cols, dst_cols, _ptr(out))
         assert n == out.size
         return out
+
+    def mul_mat_q8_0(self, w_blocks: np.ndarray, x: np.ndarray, rows: int, k: int) -> np.ndarray:
+        """ggml CPU mul_mat of Q8_0 rows [rows][k/32] by x [n_vec][k] -> [n_vec][rows]."""
+        w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+        y = np.empty((x.shape[0], rows), dtype=np.float32)
+        self.lib.lo_mul_mat_q8_0(_ptr(w_blocks), _ptr(x), _ptr(y), rows, k, x.shape[0])
+        return y
 
     def dequantize(self, qtype, blocks: np.ndarray, count: int) -> np.ndarray:
         blocks = np.ascontiguousarray(blocks, dtype=np.uint8)

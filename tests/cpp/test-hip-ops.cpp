@@ -254,6 +254,50 @@ void quantize_surface() {
     CHECK(bit_equal(got_back.data(), want_back.data(), 4099));
 }
 
+// The Q8_0 decode mat-vec against the oracle's ggml CPU restatement: the
+// CFG pair at LeLM's ffn_down shape (1536 x 8960) within F32 rounding, and an
+// integer-valued case (d = 1 blocks) exactly.
+void mul_mat_surface() {
+    const int64_t rows = 1536, k = 8960, n_vec = 2;
+    std::vector<float> w = gaussian(static_cast<std::size_t>(rows * k), 51, 0.02F);
+    const std::vector<float> x = gaussian(static_cast<std::size_t>(n_vec * k), 52, 1.0F);
+    std::vector<uint8_t> wb(row_size(LEVO_HIP_TYPE_Q8_0, k) * static_cast<std::size_t>(rows));
+    CHECK(lo_quantize_chunk(LEVO_HIP_TYPE_Q8_0, w.data(), wb.data(), 0, rows, k) == wb.size());
+    std::vector<float> want(static_cast<std::size_t>(n_vec * rows));
+    lo_mul_mat_q8_0(wb.data(), x.data(), want.data(), rows, k, n_vec);
+    device_vec<uint8_t> dw(wb), dxb(row_size(LEVO_HIP_TYPE_Q8_0, k) * static_cast<std::size_t>(n_vec) + 16);
+    device_vec<float> dx(x), dy(static_cast<std::size_t>(n_vec * rows));
+    mul_mat_q8_0(dw.data(), dx.data(), dxb.data(), dy.data(), rows, k, n_vec);
+    const std::vector<float> got = dy.get();
+    for (std::size_t i = 0; i < got.size(); ++i) {
+        CHECK(std::fabs(got[i] - want[i]) <= 1e-5F * std::max(1.0F, std::fabs(want[i])));
+    }
+
+    const int64_t ir = 40, ik = 640;
+    std::vector<float> iw(static_cast<std::size_t>(ir * ik)), ix(static_cast<std::size_t>(2 * ik));
+    for (std::size_t i = 0; i < iw.size(); ++i) iw[i] = i % 32 == 0 ? 127.0F : static_cast<float>(static_cast<int>(i * 7919 % 255) - 127);
+    for (std::size_t i = 0; i < ix.size(); ++i) ix[i] = i % 32 == 3 ? -127.0F : static_cast<float>(static_cast<int>(i * 104729 % 255) - 127);
+    std::vector<uint8_t> iwb(row_size(LEVO_HIP_TYPE_Q8_0, ik) * static_cast<std::size_t>(ir));
+    CHECK(lo_quantize_chunk(LEVO_HIP_TYPE_Q8_0, iw.data(), iwb.data(), 0, ir, ik) == iwb.size());
+    device_vec<uint8_t> diw(iwb), dixb(row_size(LEVO_HIP_TYPE_Q8_0, ik) * 2 + 16);
+    device_vec<float> dix(ix), diy(static_cast<std::size_t>(2 * ir));
+    mul_mat_q8_0(diw.data(), dix.data(), dixb.data(), diy.data(), ir, ik, 2);
+    const std::vector<float> igot = diy.get();
+    for (int64_t v = 0; v < 2; ++v) {
+        for (int64_t r = 0; r < ir; ++r) {
+            int64_t exact = 0;
+            for (int64_t c = 0; c < ik; ++c) {
+                exact += static_cast<int64_t>(iw[static_cast<std::size_t>(r * ik + c)]) *
+                         static_cast<int64_t>(ix[static_cast<std::size_t>(v * ik + c)]);
+            }
+            CHECK(igot[static_cast<std::size_t>(v * ir + r)] == static_cast<float>(exact));
+        }
+    }
+    expect_throw<std::invalid_argument>("multiple of 32", [&] {
+        mul_mat_q8_0_quantized(dw.data(), dxb.data(), dy.data(), rows, 100, n_vec);
+    });
+}
+
 } // namespace
 
 int main() {
@@ -262,6 +306,7 @@ int main() {
         snake_parity();
         norm_parity();
         quantize_surface();
+        mul_mat_surface();
     } catch (const std::exception & e) {
         std::cerr << "unexpected exception: " << e.what() << '\n';
         return 1;

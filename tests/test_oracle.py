@@ -495,3 +495,51 @@ def test_quantize_padding_matches_chunk_of_padded_rows(oracle):
         padded = np.zeros((rows, dst_cols), np.float32)
         padded[:, :src_cols] = oracle.f16_to_f32(xh)
         assert np.array_equal(oracle.quantize_f16_padded(qt, xh, dst_cols), oracle.quantize(qt, padded))
+
+
+# ---------------------------------------------------------------- Q8_0 mat-vec
+
+def _q8_parts(blocks, nblocks):
+    """(d as float32, quants as int32 [nblocks][32]) of packed Q8_0 blocks."""
+    b = np.ascontiguousarray(blocks, np.uint8).reshape(nblocks, 34)
+    d = b[:, :2].copy().view(np.float16).astype(np.float32).reshape(nblocks)
+    q = b[:, 2:].view(np.int8).astype(np.int32)
+    return d, q
+
+
+@pytest.mark.parametrize("rows,k,n_vec", [(64, 1536, 2), (7, 8960, 1), (33, 32, 3)])
+def test_mul_mat_q8_0_matches_block_terms(oracle, rows, k, n_vec):
+    """ggml_vec_dot_q8_0_q8_0 semantics: y = sum_b sumi_b * (d_w * d_x) with
+    the activation quantized by the reference quantizer. Checked against the
+    float64 sum of independently built block terms, within the error bound of
+    a sequential F32 sum ((nb - 1) * 2^-24 * sum |term|). A dropped or
+    transposed term, a wrong scale or an unquantized activation fails it."""
+    nb = k // 32
+    w = (oracle.gaussian(rows * k, 1000 + k) * np.float32(0.02)).reshape(rows, k)
+    x = oracle.gaussian(n_vec * k, 2000 + k).reshape(n_vec, k)
+    wb = oracle.quantize(8, w)
+    y = oracle.mul_mat_q8_0(wb, x, rows, k)
+    dw, qw = _q8_parts(wb, rows * nb)
+    for v in range(n_vec):
+        dx, qx = _q8_parts(oracle.quantize(8, x[v].reshape(1, k)), nb)
+        sumi = (qw.reshape(rows, nb, 32) * qx.reshape(1, nb, 32)).sum(axis=2)
+        terms = sumi.astype(np.float32) * (dw.reshape(rows, nb) * dx.reshape(1, nb)).astype(np.float32)
+        exact = terms.astype(np.float64).sum(axis=1)
+        bound = (nb - 1) * 2.0 ** -24 * np.abs(terms).astype(np.float64).sum(axis=1) + 1e-30
+        assert np.all(np.abs(y[v].astype(np.float64) - exact) <= bound)
+        # and close to the unquantized product (quantization error only)
+        assert np.max(np.abs(y[v] - w @ x[v])) < 0.05 * np.sqrt(k) * 0.02
+
+
+def test_mul_mat_q8_0_integer_blocks_exact(oracle):
+    """Blocks whose largest |value| is 127 quantize with d = 1 and q = value:
+    the product is the exact integer product (every partial sum < 2^24)."""
+    rng = np.random.default_rng(5)
+    rows, k, n_vec = 40, 640, 2
+    w = rng.integers(-127, 128, (rows, k)).astype(np.float32)
+    x = rng.integers(-127, 128, (n_vec, k)).astype(np.float32)
+    w[:, ::32] = 127.0
+    x[:, 5::32] = -127.0
+    y = oracle.mul_mat_q8_0(oracle.quantize(8, w), x, rows, k)
+    want = (w.astype(np.int64) @ x.astype(np.int64).T).T
+    assert np.array_equal(y, want.astype(np.float32))
