@@ -528,6 +528,45 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
     return out
 
 
+PEAK_F32_MFMA_TFLOPS = 157.3
+
+
+def bench_snake_conv(torch, hip, head, dev, warmup, steps):
+    """Fused SnakeBeta + Conv1d (+ bias, + residual) of the VAE decoder's
+    residual units at a 10.08 s window's real stage lengths: stage 5
+    (128 channels x 483840 samples; k = 7 at dilation 1 / 3 / 9, k = 1 with
+    the residual add), stage 3 (256 x 60480) and stage 1 (1024 x 2520).
+    Matrix-core bound: `TFLOP/s` is 2 * C_out * C_in * k * T_out per launch
+    over the launch time, against the F32 MFMA peak; bytes are x, y (and the
+    residual) once."""
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    cases = [("stage5_k7_d1", 128, 483840, 7, 1), ("stage5_k7_d9", 128, 483840, 7, 9),
+             ("stage5_k1_residual", 128, 483840, 1, 1), ("stage3_k7_d3", 256, 60480, 7, 3),
+             ("stage1_k7_d9", 1024, 2520, 7, 9)]
+    for name, c, t, kw, dil in cases:
+        pad = 3 * dil if kw == 7 else 0
+        x = torch.randn((c, t), generator=g, device=dev)
+        w = torch.randn((c, c, kw), generator=g, device=dev) / math.sqrt(c * kw)
+        b = torch.randn(c, generator=g, device=dev) * 0.1
+        a = torch.randn(c, generator=g, device=dev) * 0.5
+        bl = torch.randn(c, generator=g, device=dev) * 0.5
+        r = torch.randn((c, t), generator=g, device=dev) if kw == 1 else None
+        y = torch.empty((c, t), device=dev)
+        fn = lambda i: hip.snake_conv1d(x, c, t, w, c, kw, alpha_log=a, beta_log=bl, bias=b, padding=pad,
+                                        dilation=dil, residual=r, y=y)
+        ms = time_op(torch, head, fn, 1, warmup, max(steps // 4, 5))
+        flops = 2.0 * c * c * kw * t
+        tflops = flops / (ms * 1e-3) / 1e12
+        nbytes = 4 * c * t * (3 if r is not None else 2)
+        out[name] = {"shape": [c, t, kw, dil], "us_per_launch": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
+                     "frac_f32_mfma": round(tflops / PEAK_F32_MFMA_TFLOPS, 4), "bytes_per_launch": nbytes,
+                     "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": "mfma"}
+        del x, w, y, r
+    return out
+
+
 def bench_quant(torch, hip, head, dev, warmup, steps):
     R, Cc = 4096, 1536
     out = {}
@@ -702,7 +741,7 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-ops", action="store_true", help="only the headline ladder")
     p.add_argument("--only", default="",
-                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant,gemv); "
+                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant,gemv,conv); "
                         "prints the op table without the headline ladder")
     p.add_argument("--copy-ceiling", action="store_true",
                    help="with --only: annotate each op with a plain device copy of the same bytes")
@@ -751,6 +790,8 @@ def main() -> int:
             ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
         if "gemv" in groups:
             ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
+        if "conv" in groups:
+            ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
         if args.copy_ceiling:
             add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
         print(json.dumps({"ops": ops}))
@@ -797,6 +838,8 @@ def main() -> int:
         ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
         log("ops: q8_0 mat-vec")
         ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
+        log("ops: snake conv1d")
+        ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: plain-copy ceilings")
         add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 

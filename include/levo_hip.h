@@ -67,6 +67,26 @@ int levo_hip_snake_beta(const float * x, int64_t x_stride,
                         float * y, int64_t y_stride,
                         int64_t channels, int64_t time, levo_hip_stream_t stream);
 
+/* SnakeBeta + Conv1d (stride 1) + bias + residual in one pass: the Oobleck
+ * decoder's conv_1d_f32 calls (ggml_im2col + ggml_mul_mat + bias,
+ * src/levo-audio-ops.cpp:56-87) with the SnakeBeta that feeds them
+ * (run_residual src/levo-vae.cpp:91-100; decode :219-221, :260-262):
+ *   y[co][t] = (sum_{ci,k} weight[co][ci][k] * s(x)[ci][t + k*dilation - padding])
+ *              + bias[co] (+ residual[co][t])
+ * x: F32 [c_in][x_stride], t_in samples, zero outside [0, t_in). s: SnakeBeta
+ * with alpha_log / beta_log [c_in] of param_type (F32 or F16), as
+ * levo_hip_snake_beta computes it; both NULL: s is the identity. weight: F32
+ * [c_out][c_in][kernel] (ggml ne = [kernel, c_in, c_out]), kernel 1, 3, 5 or
+ * 7. bias [c_out] or NULL. residual [c_out][residual_stride] or NULL.
+ * y: F32 [c_out][y_stride], t_out = t_in + 2*padding - dilation*(kernel-1).
+ * y may be the residual, never x. Accumulation on the F32 matrix cores, so
+ * y agrees with the reference to F32 rounding. */
+int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                          const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                          const float * weight, int64_t c_out, int64_t kernel, const float * bias,
+                          int64_t padding, int64_t dilation, const float * residual, int64_t residual_stride,
+                          float * y, int64_t y_stride, levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Residual add + RMSNorm / LayerNorm (rows of `dim` contiguous elements)    */
 /* ------------------------------------------------------------------------ */

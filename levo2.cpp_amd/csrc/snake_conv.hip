@@ -1,0 +1,421 @@
+// Conv1d (stride 1) with SnakeBeta applied to its input and the bias and a
+// residual add applied to its output, as one implicit GEMM on the F32 matrix
+// cores. It is the Oobleck VAE decoder's residual unit written as two calls
+// (src/levo-vae.cpp:91-100):
+//   h = conv_1d_f32(snake(x, pre), W0, b0, pad 3d, dilation d)
+//   y = x + conv_1d_f32(snake(h, post), W1, b1, 0, 1)
+// and also its input / output convolutions (:219-221, :260-262). conv_1d_f32
+// is ggml_im2col + ggml_mul_mat + the bias add (src/levo-audio-ops.cpp:56-87);
+// here the im2col matrix is never formed and the activated input is never
+// written to HBM:
+//   y[co][t] = (sum_{ci,k} W[co][ci][k] * s(x)[ci][t + k * dil - pad]) + b[co]
+//              (+ r[co][t])
+// with s the SnakeBeta of snake_math.hpp (or the identity) and zero outside
+// [0, T_in), the same arithmetic as the standalone SnakeBeta kernel. The sum
+// is accumulated by the F32 MFMA in another order than ggml's dot, so y
+// agrees with the reference to F32 rounding.
+//
+// Workgroup tile: 128 output channels x 128 samples, 4 waves of 64 x 64, each
+// 4 x 4 tiles of v_mfma_f32_16x16x4f32. K runs over chunks of CI input
+// channels x KW taps: the weight chunk is staged in LDS k-major with the rows
+// permuted so that a lane's four A fragments are one 16-byte read; the input
+// chunk (CI rows of 128 + (KW - 1) * dil samples, the halo included) is staged
+// with SnakeBeta applied once per element, from per-channel parameters the
+// workgroup computes up front.
+#include "common.hpp"
+#include "snake_math.hpp"
+
+#include <algorithm>
+
+namespace levo_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMT = 128;  // output channels per workgroup
+constexpr int kNT = 128;  // output samples per workgroup
+constexpr int kMaxSnakeChannels = 2048;
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <int KW>
+struct conv_chunk {
+    static constexpr int CI = KW == 1 ? 32 : 8;  // input channels per K chunk
+    static constexpr int KC = CI * KW;           // K values per chunk (a multiple of 4)
+};
+
+struct conv_params {
+    const float * x;
+    int64_t x_pitch;
+    int64_t t_in;
+    const void * alpha_log;
+    const void * beta_log;
+    int32_t param_f16;
+    int32_t snake;
+    const float * w;          // [c_out][c_in][KW]
+    const float * bias;       // [c_out] or null
+    const float * residual;   // [c_out][r_pitch] or null
+    int64_t r_pitch;
+    float * y;
+    int64_t y_pitch;
+    int64_t t_out;
+    int32_t c_in, c_out;
+    int32_t pad, dil;
+    int32_t b_width;          // staged samples per input row: kNT + (KW - 1) * dil, rounded up to 4
+    int32_t w_vec;            // weight rows 16-byte aligned with KW * c_in % 4 == 0
+    int32_t y_vec;            // y (and residual) rows 16-byte aligned: float4 epilogue
+};
+
+// LDS float index of weight (kk, r) in the A chunk: rows r = 64 h + 16 i + m
+// are stored as [kk][h][m][i] so lane m of a wave on row half h reads
+// its four fragments i = 0..3 with one ds_read_b128. Rows of kk are kAStride
+// floats apart, which puts the four lane groups (four kk) of one read on
+// different banks.
+constexpr int kAStride = kMT + 4;
+
+__device__ __forceinline__ int a_index(int kk, int r) {
+    const int h = r >> 6;
+    const int i = (r >> 4) & 3;
+    const int m = r & 15;
+    return kk * kAStride + h * 64 + m * 4 + i;
+}
+
+// Register slots of one K chunk, loaded while the previous chunk's MFMAs run.
+// A: NA float4s per thread, slot u = element e = tid + 256 u of the
+// [q][r] = [KC / 4][kMT] chunk (row r = e % kMT, weights 4q .. 4q + 3).
+// B: NB input samples per thread: for KW = 1 (128-sample rows) slot s is row
+// 2 s + tid / 128, sample tid % 128; otherwise row s % CI, sample
+// tid + 256 (s / CI) (b_width <= 512). Threads past a row's end idle; the
+// waves that stage less reach their MFMAs first, which measured faster than
+// spreading the samples evenly.
+template <int KW>
+struct conv_slots {
+    static constexpr int CI = conv_chunk<KW>::CI;
+    static constexpr int KC = conv_chunk<KW>::KC;
+    static constexpr int NA = KC / 4 * kMT / kThreads;
+    static constexpr int NB = KW == 1 ? CI / 2 : 2 * CI;
+};
+
+template <int KW>
+__device__ __forceinline__ void b_slot(int s, int tid, int & c, int & j) {
+    c = KW == 1 ? 2 * s + (tid >> 7) : s % conv_chunk<KW>::CI;
+    j = KW == 1 ? (tid & 127) : tid + kThreads * (s / conv_chunk<KW>::CI);
+}
+
+template <int KW>
+__device__ __forceinline__ void load_chunk(const conv_params & p, int ci0, int co0, int64_t t0, int tid,
+                                           f32x4v (&ra)[conv_slots<KW>::NA], float (&rb)[conv_slots<KW>::NB]) {
+    constexpr int CI = conv_slots<KW>::CI;
+    const int64_t w_row = static_cast<int64_t>(p.c_in) * KW;
+    const bool a_inside = p.w_vec && co0 + kMT <= p.c_out && ci0 + CI <= p.c_in;
+#pragma unroll
+    for (int u = 0; u < conv_slots<KW>::NA; ++u) {
+        const int e = tid + kThreads * u;
+        const int r = e % kMT;
+        const int kk = 4 * (e / kMT);
+        const int co = co0 + r;
+        const float * src = p.w + co * w_row + static_cast<int64_t>(ci0) * KW + kk;
+        f32x4v v = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+        if (a_inside) {
+            v = *reinterpret_cast<const f32x4v *>(src);
+        } else if (co < p.c_out) {
+            if (p.w_vec && ci0 + (kk + 3) / KW < p.c_in) {
+                v = *reinterpret_cast<const f32x4v *>(src);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (ci0 + (kk + q) / KW < p.c_in) v[q] = src[q];
+                }
+            }
+        }
+        ra[u] = v;
+    }
+    const int64_t tb = t0 - p.pad;
+    const bool b_inside = tb >= 0 && tb + p.b_width <= p.t_in && ci0 + CI <= p.c_in;
+    const float * xb = p.x + static_cast<int64_t>(ci0) * p.x_pitch + tb;
+#pragma unroll
+    for (int s = 0; s < conv_slots<KW>::NB; ++s) {
+        int c, j;
+        b_slot<KW>(s, tid, c, j);
+        float v = 0.0f;
+        if (j < p.b_width) {
+            if (b_inside) {
+                v = xb[c * p.x_pitch + j];
+            } else if (ci0 + c < p.c_in && tb + j >= 0 && tb + j < p.t_in) {
+                v = xb[c * p.x_pitch + j];
+            }
+        }
+        rb[s] = v;
+    }
+}
+
+template <int KW>
+__device__ __forceinline__ void store_chunk(const conv_params & p, int ci0, int tid, float * As, float * Bs,
+                                            const snake_param * sp, const f32x4v (&ra)[conv_slots<KW>::NA],
+                                            const float (&rb)[conv_slots<KW>::NB]) {
+#pragma unroll
+    for (int u = 0; u < conv_slots<KW>::NA; ++u) {
+        const int e = tid + kThreads * u;
+        const int r = e % kMT;
+        const int kk = 4 * (e / kMT);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) As[a_index(kk + q, r)] = ra[u][q];
+    }
+#pragma unroll
+    for (int s = 0; s < conv_slots<KW>::NB; ++s) {
+        int c, j;
+        b_slot<KW>(s, tid, c, j);
+        if (j < p.b_width) {
+            float v = rb[s];
+            // zero padding stays zero: s(0) = 0 + sin^2(0) / beta = 0 exactly
+            if (p.snake && ci0 + c < p.c_in) v = snake(v, sp[ci0 + c]);
+            Bs[c * p.b_width + j] = v;
+        }
+    }
+}
+
+// LDS floats of one A buffer.
+template <int KW>
+__host__ __device__ constexpr int a_floats() {
+    return conv_chunk<KW>::KC * kAStride;
+}
+
+constexpr int kOutStride = kNT + 4;  // floats per row of the staged output tile
+
+// A fragments (rows 16 i + m of the wave's row half, i = 0..3) and B
+// fragments (columns 16 j + m of its column half) of K step ks for lane
+// group g: K index kk = 4 ks + g is input channel kk / KW, tap kk % KW.
+template <int KW>
+__device__ __forceinline__ void read_operands(const float * As, const float * Bs, const conv_params & p, int ks,
+                                              int g, int h, int vh, int m, f32x4v & a, float (&b)[4]) {
+    const int kk = 4 * ks + g;
+    const int c = kk / KW;
+    const int k = kk - c * KW;
+    a = *reinterpret_cast<const f32x4v *>(As + kk * kAStride + h * 64 + m * 4);
+    const float * brow = Bs + c * p.b_width + vh * 64 + m + k * p.dil;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = brow[16 * j];
+}
+
+template <int KW>
+__global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_params p) {
+    constexpr int CI = conv_chunk<KW>::CI;
+    constexpr int KC = conv_chunk<KW>::KC;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    // two buffers of [A: KC x kAStride][B: CI x b_width], then the SnakeBeta
+    // parameters; the output tile reuses the buffers at the end
+    const int buf_floats = a_floats<KW>() + CI * p.b_width;
+    snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);  // [c_in] when p.snake
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = wave >> 1;      // row half of the tile
+    const int vh = wave & 1;      // column half
+    const int m = lane & 15;
+    const int g = lane >> 4;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kNT;
+    const int co0 = blockIdx.y * kMT;
+
+    f32x4v ra[conv_slots<KW>::NA];
+    float rb[conv_slots<KW>::NB];
+    load_chunk<KW>(p, 0, co0, t0, tid, ra, rb);
+
+    if (p.snake) {
+        for (int c = tid; c < p.c_in; c += kThreads) {
+            const float al = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.alpha_log)[c])
+                                         : static_cast<const float *>(p.alpha_log)[c];
+            const float bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.beta_log)[c])
+                                         : static_cast<const float *>(p.beta_log)[c];
+            sp[c] = make_snake_param(al, bl);
+        }
+        __syncthreads();
+    }
+    store_chunk<KW>(p, 0, tid, lds, lds + a_floats<KW>(), sp, ra, rb);
+    __syncthreads();
+
+    f32x4v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    int buf = 0;
+    for (int ci0 = 0; ci0 < p.c_in; ci0 += CI) {
+        const bool more = ci0 + CI < p.c_in;
+        if (more) load_chunk<KW>(p, ci0 + CI, co0, t0, tid, ra, rb);  // in flight during the MFMAs
+        const float * As = lds + buf * buf_floats;
+        const float * Bs = As + a_floats<KW>();
+        // Operands of step ks + 1 are read while step ks's 16 MFMAs issue.
+        f32x4v a;
+        float b[4];
+        read_operands<KW>(As, Bs, p, 0, g, h, vh, m, a, b);
+#pragma unroll 2
+        for (int ks = 0; ks < KC / 4; ++ks) {
+            f32x4v an = a;
+            float bn[4] = {b[0], b[1], b[2], b[3]};
+            if (ks + 1 < KC / 4) read_operands<KW>(As, Bs, p, ks + 1, g, h, vh, m, an, bn);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            a = an;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = bn[j];
+        }
+        if (more) {
+            // the other buffer was last read before the previous barrier
+            float * An = lds + (buf ^ 1) * buf_floats;
+            store_chunk<KW>(p, ci0 + CI, tid, An, An + a_floats<KW>(), sp, ra, rb);
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    // The output tile goes through LDS (the A / B buffers, free after the
+    // last barrier) so that bias, residual and y move as whole rows.
+    // D[row][col] of a 16 x 16 tile is in lane col + 16 * (row / 4), item row % 4.
+    float * out = lds;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                out[(h * 64 + 16 * i + 4 * g + u) * kOutStride + vh * 64 + 16 * j + m] = acc[i][j][u];
+    __syncthreads();
+    const bool vec = p.y_vec && t0 + kNT <= p.t_out;
+    constexpr int kOutIters = kMT * (kNT / 4) / kThreads;  // float4s of the tile per thread
+    if (vec && co0 + kMT <= p.c_out) {
+        // Whole tile inside y: the thread's residual float4s are loaded
+        // before any store (y may be the residual, so the loads cannot move
+        // past the stores on their own), then each row is finished.
+        f32x4v res[kOutIters];
+        if (p.residual) {
+#pragma unroll
+            for (int it = 0; it < kOutIters; ++it) {
+                const int e = tid + kThreads * it;
+                const int r = e / (kNT / 4);
+                const int c4 = 4 * (e % (kNT / 4));
+                res[it] = *reinterpret_cast<const f32x4v *>(p.residual + (co0 + r) * p.r_pitch + t0 + c4);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kOutIters; ++it) {
+            const int e = tid + kThreads * it;
+            const int r = e / (kNT / 4);
+            const int c4 = 4 * (e % (kNT / 4));
+            const int co = co0 + r;
+            f32x4v v = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
+            if (p.bias) v = v + p.bias[co];
+            if (p.residual) v = res[it] + v;
+            *reinterpret_cast<f32x4v *>(p.y + co * p.y_pitch + t0 + c4) = v;
+        }
+        return;
+    }
+    for (int e = tid; e < kMT * (kNT / 4); e += kThreads) {
+        const int r = e / (kNT / 4);
+        const int c4 = 4 * (e % (kNT / 4));
+        const int co = co0 + r;
+        if (co >= p.c_out) break;  // rows only grow with e
+        const float bv = p.bias ? p.bias[co] : 0.0f;
+        const f32x4v o = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
+        const int64_t t = t0 + c4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (t + q >= p.t_out) break;
+            float v = o[q];
+            if (p.bias) v = v + bv;
+            if (p.residual) v = p.residual[co * p.r_pitch + t + q] + v;
+            p.y[co * p.y_pitch + t + q] = v;
+        }
+    }
+}
+
+template <int KW>
+int launch_conv(conv_params p, hipStream_t st) {
+    constexpr int CI = conv_chunk<KW>::CI;
+    p.b_width = (kNT + (KW - 1) * p.dil + 3) & ~3;
+    // each thread stages at most two samples of an input row
+    LEVO_REQUIRE(KW == 1 || p.b_width <= 2 * kThreads, "snake_conv1d: dilation too large");
+    p.w_vec = aligned16(p.w) && (static_cast<int64_t>(p.c_in) * KW) % 4 == 0;
+    p.y_vec = aligned16(p.y) && p.y_pitch % 4 == 0 &&
+              (p.residual == nullptr || (aligned16(p.residual) && p.r_pitch % 4 == 0));
+    const size_t buf = static_cast<size_t>(a_floats<KW>() + CI * p.b_width);
+    const size_t lds = std::max(2 * buf, static_cast<size_t>(kMT) * kOutStride) * sizeof(float) +
+                       (p.snake ? static_cast<size_t>(p.c_in) * sizeof(snake_param) : 0);
+    LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
+    static bool attribute_set = false;
+    if (!attribute_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&snake_conv1d_kernel<KW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024) != hipSuccess) {
+            set_error("snake_conv1d: cannot raise the LDS limit");
+            return LEVO_HIP_ERR_RUNTIME;
+        }
+        attribute_set = true;
+    }
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)));
+    snake_conv1d_kernel<KW><<<grid, kThreads, lds, st>>>(p);
+    return launch_status("levo_hip_snake_conv1d");
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+using namespace levo_hip;
+
+extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                     const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                                     const float * weight, int64_t c_out, int64_t kernel, const float * bias,
+                                     int64_t padding, int64_t dilation, const float * residual,
+                                     int64_t residual_stride, float * y, int64_t y_stride,
+                                     levo_hip_stream_t stream) {
+    LEVO_REQUIRE(c_in > 0 && c_out > 0 && t_in > 0, "LeVo audio graph: incompatible Conv1d weight/input shapes");
+    LEVO_REQUIRE(padding >= 0 && dilation > 0, "LeVo audio graph: invalid Conv1d stride, padding, or dilation");
+    LEVO_REQUIRE(kernel == 1 || kernel == 3 || kernel == 5 || kernel == 7, "snake_conv1d: kernel size must be 1, 3, 5 or 7");
+    LEVO_REQUIRE(c_in <= (1 << 20) && c_out <= (1 << 20) && t_in < (int64_t{1} << 40) && padding < (1 << 20) &&
+                     dilation < (1 << 16),
+                 "snake_conv1d: dimensions too large");
+    const int64_t t_out = t_in + 2 * padding - dilation * (kernel - 1);
+    LEVO_REQUIRE(t_out > 0, "snake_conv1d: the kernel is wider than the padded input");
+    LEVO_REQUIRE(ceil_div(t_out, kNT) < (int64_t{1} << 31) && ceil_div(c_out, kMT) < 65536, "snake_conv1d: grid too large");
+    LEVO_REQUIRE(x != nullptr && weight != nullptr && y != nullptr, "snake_conv1d: null tensor");
+    LEVO_REQUIRE(x_stride >= t_in && y_stride >= t_out && (residual == nullptr || residual_stride >= t_out),
+                 "snake_conv1d: row stride smaller than the row");
+    const bool snake = alpha_log != nullptr || beta_log != nullptr;
+    LEVO_REQUIRE(!snake || (alpha_log != nullptr && beta_log != nullptr),
+                 "snake_conv1d: SnakeBeta needs both alpha_log and beta_log");
+    LEVO_REQUIRE(!snake || param_type == LEVO_HIP_TYPE_F32 || param_type == LEVO_HIP_TYPE_F16,
+                 "LeVo audio graph: SnakeBeta alpha_log must be F32 or F16");
+    LEVO_REQUIRE(!snake || c_in <= kMaxSnakeChannels, "snake_conv1d: at most %d input channels with SnakeBeta",
+                 kMaxSnakeChannels);
+    conv_params p;
+    p.x = x;
+    p.x_pitch = x_stride;
+    p.t_in = t_in;
+    p.alpha_log = alpha_log;
+    p.beta_log = beta_log;
+    p.param_f16 = param_type == LEVO_HIP_TYPE_F16;
+    p.snake = snake;
+    p.w = weight;
+    p.bias = bias;
+    p.residual = residual;
+    p.r_pitch = residual_stride;
+    p.y = y;
+    p.y_pitch = y_stride;
+    p.t_out = t_out;
+    p.c_in = static_cast<int32_t>(c_in);
+    p.c_out = static_cast<int32_t>(c_out);
+    p.pad = static_cast<int32_t>(padding);
+    p.dil = static_cast<int32_t>(dilation);
+    p.b_width = 0;
+    p.w_vec = 0;
+    p.y_vec = 0;
+    const hipStream_t st = as_hip(stream);
+    switch (kernel) {
+        case 1: return launch_conv<1>(p, st);
+        case 3: return launch_conv<3>(p, st);
+        case 5: return launch_conv<5>(p, st);
+        default: return launch_conv<7>(p, st);
+    }
+}

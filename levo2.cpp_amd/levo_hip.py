@@ -120,6 +120,8 @@ class LevoHip:
             "levo_hip_last_error": (ctypes.c_char_p, []),
             "levo_hip_abi_version": (ctypes.c_int, []),
             "levo_hip_snake_beta": (ctypes.c_int, [_P, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _I64, _P]),
+            "levo_hip_snake_conv1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _P,
+                                                     _I64, _I64, _P, _I64, _P, _I64, _P]),
             "levo_hip_residual_rms_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P,
                                                           _I64, _I64, _F, _P]),
             "levo_hip_residual_layer_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P,
@@ -166,6 +168,15 @@ class LevoHip:
         ys = y_stride if y_stride is not None else (y.stride(0) if hasattr(y, "stride") else T)
         return self._check(self.lib.levo_hip_snake_beta(_addr(x), xs, _addr(alpha_log), _addr(beta_log), param_type,
                                                         _addr(y), ys, C, T, _stream(stream)))
+
+    def snake_conv1d(self, x, c_in, t_in, weight, c_out, kernel, *, alpha_log=None, beta_log=None, param_type=F32,
+                     bias=None, padding=0, dilation=1, residual=None, y=None, x_stride=None, residual_stride=None,
+                     y_stride=None, stream=None):
+        t_out = t_in + 2 * padding - dilation * (kernel - 1)
+        return self._check(self.lib.levo_hip_snake_conv1d(
+            _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
+            _addr(weight), c_out, kernel, _addr(bias), padding, dilation, _addr(residual),
+            residual_stride or t_out, _addr(y), y_stride or t_out, _stream(stream)))
 
     def rms_norm(self, act_type, x, delta, weight, weight_type, h_out, y, rows, dim, eps, stream=None):
         return self._check(self.lib.levo_hip_residual_rms_norm(act_type, _addr(x), _addr(delta), _addr(weight),

@@ -728,3 +728,68 @@ void lo_mul_mat_q8_0(const void * w, const float * x, float * y, int64_t rows, i
     }
     free(xq);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Conv1d (im2col + F32 mul_mat + bias), stride 1                            */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    const float * x;
+    int64_t c_in, t_in;
+    const float * w;
+    int64_t c_out, kernel;
+    const float * bias;
+    int64_t padding, dilation, t_out;
+    float * y;
+    int64_t co0, co1;
+} lo_conv_job;
+
+static void * lo_conv_rows(void * arg) {
+    const lo_conv_job * j = (const lo_conv_job *)arg;
+    const int64_t kk = j->c_in * j->kernel;
+    float * col = (float *)malloc((size_t)kk * sizeof(float));
+    if (!col) return NULL;
+    for (int64_t t = 0; t < j->t_out; ++t) {
+        /* the im2col column of output t */
+        for (int64_t ci = 0; ci < j->c_in; ++ci) {
+            for (int64_t k = 0; k < j->kernel; ++k) {
+                const int64_t ti = t + k * j->dilation - j->padding;
+                col[ci * j->kernel + k] = (ti >= 0 && ti < j->t_in) ? j->x[ci * j->t_in + ti] : 0.0f;
+            }
+        }
+        for (int64_t co = j->co0; co < j->co1; ++co) {
+            const float * wr = j->w + co * kk;
+            float sum = 0.0f;
+            for (int64_t e = 0; e < kk; ++e) sum += wr[e] * col[e];
+            j->y[co * j->t_out + t] = j->bias ? sum + j->bias[co] : sum;
+        }
+    }
+    free(col);
+    return NULL;
+}
+
+void lo_conv1d_f32(const float * x, int64_t c_in, int64_t t_in, const float * w, int64_t c_out, int64_t kernel,
+                   const float * bias, int64_t padding, int64_t dilation, float * y, int threads) {
+    const int64_t t_out = t_in + 2 * padding - dilation * (kernel - 1);
+    if (t_out <= 0) return;
+    if (threads < 1) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t tid[64];
+    lo_conv_job jobs[64];
+    const int64_t per = (c_out + threads - 1) / threads;
+    int started = 0;
+    for (int i = 0; i < threads; ++i) {
+        lo_conv_job * j = &jobs[i];
+        j->x = x; j->c_in = c_in; j->t_in = t_in; j->w = w; j->c_out = c_out; j->kernel = kernel;
+        j->bias = bias; j->padding = padding; j->dilation = dilation; j->t_out = t_out; j->y = y;
+        j->co0 = i * per;
+        j->co1 = (i + 1) * per < c_out ? (i + 1) * per : c_out;
+        if (j->co0 >= j->co1) break;
+        if (threads == 1 || pthread_create(&tid[i], NULL, lo_conv_rows, j) != 0) {
+            lo_conv_rows(j);
+            tid[i] = 0;
+        }
+        started = i + 1;
+    }
+    for (int i = 0; i < started; ++i) if (threads > 1 && tid[i]) pthread_join(tid[i], NULL);
+}

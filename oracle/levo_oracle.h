@@ -32,6 +32,8 @@
  *   lo_quantize_row_q8_0 / q4_0 .......... reference KAT (tests/test-quantization.cpp:32-81),
  *                                          block invariants, numpy restatement of ggml's
  *                                          published reference quantizer
+ *   lo_conv1d_f32 ........................ float64 direct convolution within the sequential-sum
+ *                                          error bound; identity / shift kernels exactly
  *   lo_mul_mat_q8_0 ...................... float64 sum of the same block terms within the
  *                                          sequential-sum error bound; integer-valued
  *                                          blocks (d = 1) equal the exact integer product
@@ -151,6 +153,16 @@ void lo_quantize_row_q8_0(const float * x, void * y, int64_t k);
 void lo_quantize_row_q4_0(const float * x, void * y, int64_t k);
 void lo_dequantize_row_q8_0(const void * x, float * y, int64_t k);
 void lo_dequantize_row_q4_0(const void * x, float * y, int64_t k);
+/* conv_1d_f32 (src/levo-audio-ops.cpp:56-87), stride 1: ggml_im2col (input
+ * index t + k * dilation - padding, zero outside [0, t_in)), ggml_mul_mat of
+ * the columns with the [c_out][c_in * kernel] weight (the dot over
+ * ci * kernel + k in that order, F32, generic loop), then the bias add
+ * (add_channel_bias, :42-54) as its own rounding. x [c_in][t_in],
+ * w [c_out][c_in][kernel] (ggml ne = [kernel, c_in, c_out]), bias [c_out] or
+ * NULL, y [c_out][t_out], t_out = t_in + 2 * padding - dilation * (kernel - 1). */
+void lo_conv1d_f32(const float * x, int64_t c_in, int64_t t_in, const float * w, int64_t c_out, int64_t kernel,
+                   const float * bias, int64_t padding, int64_t dilation, float * y, int threads);
+
 /* ggml_mul_mat(W, x) on ggml's CPU backend for a Q8_0 weight (the quantized
  * LeLM / Flow matrices, src/levo-quantization.h:96-118): W is [rows][k/32]
  * Q8_0 blocks, x [n_vec][k] F32, y [n_vec][rows]. Each activation column is

@@ -71,6 +71,7 @@ class Oracle:
             "lo_quantize_f16_rows_padded": (ctypes.c_size_t, [ctypes.c_int, _P, _I64, _I64, _I64, _P]),
             "lo_dequantize_row_q8_0": (None, [_P, _P, _I64]),
             "lo_mul_mat_q8_0": (None, [_P, _P, _P, _I64, _I64, _I64]),
+            "lo_conv1d_f32": (None, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, ctypes.c_int]),
             "lo_dequantize_row_q4_0": (None, [_P, _P, _I64]),
             "lo_gaussian_noise": (None, [_P, _I64, ctypes.c_uint64]),
         }
@@ -212,6 +213,19 @@ class Oracle:
         n = self.lib.lo_quantize_f16_rows_padded(qtype, _ptr(x), rows, cols, dst_cols, _ptr(out))
         assert n == out.size
         return out
+
+    def conv1d(self, x, w, bias, padding, dilation, threads=1):
+        """conv_1d_f32 (stride 1): x [c_in][t_in], w [c_out][c_in][kernel] -> [c_out][t_out]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        c_in, t_in = x.shape
+        c_out, _, kernel = w.shape
+        t_out = t_in + 2 * padding - dilation * (kernel - 1)
+        y = np.empty((c_out, t_out), dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self.lib.lo_conv1d_f32(_ptr(x), c_in, t_in, _ptr(w), c_out, kernel, _ptr(b), padding, dilation, _ptr(y),
+                               threads)
+        return y
 
     def mul_mat_q8_0(self, w_blocks: np.ndarray, x: np.ndarray, rows: int, k: int) -> np.ndarray:
         """ggml CPU mul_mat of Q8_0 rows [rows][k/32] by x [n_vec][k] -> [n_vec][rows]."""

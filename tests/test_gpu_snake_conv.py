@@ -1,0 +1,153 @@
+"""Fused SnakeBeta + Conv1d + bias + residual (levo_hip_snake_conv1d)
+against the oracle's chain: lo_snake_beta_f32 (the reference's ggml chain)
+then lo_conv1d_f32 (ggml_im2col + F32 mul_mat + bias,
+src/levo-audio-ops.cpp:56-87), then the residual add (src/levo-vae.cpp:100).
+
+Bar: F32 max|a - b| / max(|b|, 1) <= 1e-5 (the matrix cores sum in another
+order than ggml's dot); bit-exact for delta kernels without SnakeBeta,
+where every output is one product (KAT-style identity / shift / dilation).
+Shapes: the decoder's residual units (k = 7 at dilation 1, 3, 9 with
+padding 3d; k = 1) at the last stage's 128 channels and at 1024 channels,
+the input conv 64 -> 2048 without SnakeBeta, the output conv 128 -> 2, odd
+channel counts and lengths, F16 SnakeBeta parameters, strides, and y
+written over the residual.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import f32_err, from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(oracle, c, seed):
+    a = (oracle.gaussian(c, seed) * np.float32(0.5)).astype(np.float32)
+    b = (oracle.gaussian(c, seed + 1) * np.float32(0.5)).astype(np.float32)
+    return a, b
+
+
+def _want(oracle, x, w, b, pad, dil, a=None, bl=None, residual=None):
+    xs = oracle.snake_beta(x, a, bl, threads=8) if a is not None else x
+    y = oracle.conv1d(xs, w, b, pad, dil, threads=8)
+    if residual is not None:
+        y = (residual + y).astype(np.float32)
+    return y
+
+
+def _run(hip, dev, x, w, b, pad, dil, a=None, bl=None, residual=None, param_type=0):
+    import torch
+    c_in, t_in = x.shape
+    c_out, _, kw = w.shape
+    t_out = t_in + 2 * pad - dil * (kw - 1)
+    y = torch.full((c_out, t_out), float("nan"), dtype=torch.float32, device=dev)
+    keep = [to_dev(x, dev), to_dev(w, dev)]
+    bd = to_dev(b, dev) if b is not None else None
+    ad = to_dev(a, dev) if a is not None else None
+    bld = to_dev(bl, dev) if bl is not None else None
+    rd = to_dev(residual, dev) if residual is not None else None
+    hip.snake_conv1d(keep[0], c_in, t_in, keep[1], c_out, kw, alpha_log=ad, beta_log=bld, param_type=param_type,
+                     bias=bd, padding=pad, dilation=dil, residual=rd, y=y)
+    return from_dev(y)
+
+
+@pytest.mark.parametrize("c,t,kw,dil", [(128, 48384, 7, 1), (128, 48384, 7, 3), (128, 48384, 7, 9),
+                                        (128, 48384, 1, 1), (1024, 2520, 7, 9), (512, 3000, 1, 1)])
+def test_residual_unit_convs(hip, dev, oracle, c, t, kw, dil):
+    """snake -> conv (k = 7, padding 3d, dilation d) and snake -> conv (k = 1)
+    + residual, as run_residual builds them (src/levo-vae.cpp:91-100)."""
+    pad = 3 * dil if kw == 7 else 0
+    x = oracle.gaussian(c * t, c + kw + dil).reshape(c, t)
+    w = (oracle.gaussian(c * c * kw, 2 * c + dil) * np.float32(1.0 / np.sqrt(c * kw))).reshape(c, c, kw)
+    b = (oracle.gaussian(c, 3 * c) * np.float32(0.1)).astype(np.float32)
+    a, bl = _params(oracle, c, 4 * c + dil)
+    residual = oracle.gaussian(c * t, 5 * c).reshape(c, t) if kw == 1 else None
+    got = _run(hip, dev, x, w, b, pad, dil, a, bl, residual)
+    want = _want(oracle, x, w, b, pad, dil, a, bl, residual)
+    assert f32_err(got, want) <= 1e-5
+
+
+def test_input_and_output_convs(hip, dev, oracle):
+    """The decoder's input conv (64 -> 2048, k = 7, padding 3, no SnakeBeta)
+    and output conv (SnakeBeta, 128 -> 2, k = 7, no bias)."""
+    x = oracle.gaussian(64 * 252, 11).reshape(64, 252)
+    w = (oracle.gaussian(2048 * 64 * 7, 12) * np.float32(0.05)).reshape(2048, 64, 7)
+    b = oracle.gaussian(2048, 13)
+    assert f32_err(_run(hip, dev, x, w, b, 3, 1), _want(oracle, x, w, b, 3, 1)) <= 1e-5
+    x = oracle.gaussian(128 * 20000, 14).reshape(128, 20000)
+    w = (oracle.gaussian(2 * 128 * 7, 15) * np.float32(0.03)).reshape(2, 128, 7)
+    a, bl = _params(oracle, 128, 16)
+    assert f32_err(_run(hip, dev, x, w, None, 3, 1, a, bl), _want(oracle, x, w, None, 3, 1, a, bl)) <= 1e-5
+
+
+@pytest.mark.parametrize("c_in,c_out,t,kw,pad,dil", [(13, 7, 300, 3, 1, 2), (5, 3, 9, 5, 0, 1), (1, 1, 1, 1, 0, 1),
+                                                    (200, 130, 129, 7, 3, 1), (33, 257, 1000, 1, 0, 1),
+                                                    (9, 4, 70, 7, 27, 9)])
+def test_odd_shapes(hip, dev, oracle, c_in, c_out, t, kw, pad, dil):
+    """Partial K chunks, partial channel and time tiles, scalar weight loads."""
+    x = oracle.gaussian(c_in * t, c_in + t).reshape(c_in, t)
+    w = (oracle.gaussian(c_out * c_in * kw, c_out + t) * np.float32(0.2)).reshape(c_out, c_in, kw)
+    b = oracle.gaussian(c_out, 7)
+    a, bl = _params(oracle, c_in, 8)
+    assert f32_err(_run(hip, dev, x, w, b, pad, dil, a, bl), _want(oracle, x, w, b, pad, dil, a, bl)) <= 1e-5
+
+
+def test_delta_kernels_bit_exact(hip, dev, oracle):
+    """Identity, one-sample delay and dilated advance: each output is one
+    product with 1.0 (exact), plus the bias in its own rounding."""
+    c, t = 130, 1000
+    x = oracle.gaussian(c * t, 90).reshape(c, t)
+    b = oracle.gaussian(c, 91)
+    eye = np.eye(c, dtype=np.float32)
+    for tap, pad, dil in ((3, 3, 1), (0, 3, 1), (6, 27, 9)):
+        w = np.zeros((c, c, 7), np.float32)
+        w[:, :, tap] = eye
+        got = _run(hip, dev, x, w, b, pad, dil)
+        want = _want(oracle, x, w, b, pad, dil)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (tap, pad, dil)
+
+
+def test_f16_snake_parameters(hip, dev, oracle):
+    """F16 alpha_log / beta_log are widened exactly (src/levo-audio-ops.cpp:143-144)."""
+    c, t = 64, 5000
+    x = oracle.gaussian(c * t, 100).reshape(c, t)
+    w = (oracle.gaussian(c * c * 7, 101) * np.float32(0.05)).reshape(c, c, 7)
+    a16 = oracle.f32_to_f16(_params(oracle, c, 102)[0])
+    b16 = oracle.f32_to_f16(_params(oracle, c, 102)[1])
+    got = _run(hip, dev, x, w, None, 3, 1, a16, b16, param_type=1)
+    want = _want(oracle, x, w, None, 3, 1, oracle.f16_to_f32(a16), oracle.f16_to_f32(b16))
+    assert f32_err(got, want) <= 1e-5
+
+
+def test_strides_and_in_place_residual(hip, dev, oracle):
+    """Row strides on x and y, and y written over the residual (the unit's
+    second conv adds its input in place)."""
+    import torch
+    c, t = 128, 3000
+    x = oracle.gaussian(c * t, 110).reshape(c, t)
+    w = (oracle.gaussian(c * c, 111) * np.float32(0.1)).reshape(c, c, 1)
+    b = oracle.gaussian(c, 112)
+    r = oracle.gaussian(c * t, 113).reshape(c, t)
+    a, bl = _params(oracle, c, 114)
+    want = _want(oracle, x, w, b, 0, 1, a, bl, r)
+    xs = torch.zeros((c, t + 5), dtype=torch.float32, device=dev)
+    xs[:, :t] = torch.from_numpy(x).to(dev)
+    rs = torch.zeros((c, t + 3), dtype=torch.float32, device=dev)
+    rs[:, :t] = torch.from_numpy(r).to(dev)
+    hip.snake_conv1d(xs, c, t, to_dev(w, dev), c, 1, alpha_log=to_dev(a, dev), beta_log=to_dev(bl, dev),
+                     bias=to_dev(b, dev), residual=rs, y=rs, x_stride=t + 5, residual_stride=t + 3, y_stride=t + 3)
+    assert f32_err(from_dev(rs)[:, :t], want) <= 1e-5
+
+
+def test_rejects_bad_arguments(hip, dev, binding):
+    import torch
+    x = torch.zeros((4, 10), device=dev)
+    w = torch.zeros((4, 4, 7), device=dev)
+    y = torch.zeros((4, 10), device=dev)
+    with pytest.raises(binding.LevoHipError, match="kernel size"):
+        hip.snake_conv1d(x, 4, 10, w, 4, 9, padding=4, y=y)
+    with pytest.raises(binding.LevoHipError, match="wider than the padded input"):
+        hip.snake_conv1d(x, 4, 10, w, 4, 7, padding=0, dilation=2, y=y)
+    with pytest.raises(binding.LevoHipError, match="needs both"):
+        hip.snake_conv1d(x, 4, 10, w, 4, 7, padding=3, alpha_log=torch.zeros(4, device=dev), y=y)

@@ -543,3 +543,59 @@ def test_mul_mat_q8_0_integer_blocks_exact(oracle):
     y = oracle.mul_mat_q8_0(oracle.quantize(8, w), x, rows, k)
     want = (w.astype(np.int64) @ x.astype(np.int64).T).T
     assert np.array_equal(y, want.astype(np.float32))
+
+
+# ---------------------------------------------------------------- Conv1d
+
+def _conv64(x, w, bias, pad, dil):
+    c_in, t_in = x.shape
+    c_out, _, kw = w.shape
+    t_out = t_in + 2 * pad - dil * (kw - 1)
+    xp = np.zeros((c_in, t_in + 2 * pad + dil * kw), np.float64)
+    xp[:, pad:pad + t_in] = x
+    y = np.zeros((c_out, t_out), np.float64)
+    absum = np.zeros((c_out, t_out), np.float64)
+    for k in range(kw):
+        win = xp[:, k * dil:k * dil + t_out]
+        y += w[:, :, k].astype(np.float64) @ win
+        absum += np.abs(w[:, :, k]).astype(np.float64) @ np.abs(win)
+    return y, absum
+
+
+@pytest.mark.parametrize("c_in,c_out,t_in,kw,pad,dil", [(16, 24, 300, 7, 3, 1), (8, 8, 200, 7, 27, 9),
+                                                       (32, 16, 100, 1, 0, 1), (5, 3, 40, 3, 2, 2)])
+def test_conv1d_matches_float64(oracle, c_in, c_out, t_in, kw, pad, dil):
+    """conv_1d_f32's im2col + dot + bias against a float64 direct convolution:
+    within the error bound of a sequential F32 sum plus the bias rounding.
+    A wrong tap offset, padding side or dilation fails it."""
+    x = oracle.gaussian(c_in * t_in, 70 + kw).reshape(c_in, t_in)
+    w = (oracle.gaussian(c_out * c_in * kw, 71 + kw) * np.float32(0.3)).reshape(c_out, c_in, kw)
+    b = oracle.gaussian(c_out, 72)
+    y = oracle.conv1d(x, w, b, pad, dil, threads=2)
+    exact, absum = _conv64(x, w, None, pad, dil)
+    exact += b[:, None]
+    bound = c_in * kw * 2.0 ** -24 * absum + 2.0 ** -24 * np.abs(exact) + 1e-30
+    assert y.shape == exact.shape
+    assert np.all(np.abs(y - exact) <= bound)
+
+
+def test_conv1d_identity_shift_and_dilation_kernels(oracle):
+    """Delta kernels move samples exactly: the centre tap is the identity,
+    tap 0 with padding 1 delays by one, tap 2 at dilation 2 with padding 2
+    advances by two; zeros come in from the padding."""
+    c, t = 6, 50
+    x = oracle.gaussian(c * t, 80).reshape(c, t)
+    eye = np.eye(c, dtype=np.float32)
+    for tap, pad, dil, shift in ((1, 1, 1, 0), (0, 1, 1, -1), (2, 2, 2, 2)):
+        w = np.zeros((c, c, 3), np.float32)
+        w[:, :, tap] = eye
+        y = oracle.conv1d(x, w, None, pad, dil)
+        want = np.zeros_like(y)
+        for i in range(y.shape[1]):
+            if 0 <= i + shift < t:
+                want[:, i] = x[:, i + shift]
+        assert np.array_equal(y, want), (tap, pad, dil)
+    b = oracle.gaussian(c, 81)
+    w = np.zeros((c, c, 3), np.float32)
+    w[:, :, 1] = eye
+    assert np.array_equal(oracle.conv1d(x, w, b, 1, 1), (x + b[:, None]).astype(np.float32))
