@@ -148,7 +148,7 @@ def add_ceilings(torch, head, dev, ops, warmup, steps):
     for entry in ops.values():
         entries = entry.values() if "bytes_per_launch" not in entry else [entry]
         for e in entries:
-            if isinstance(e, dict) and "bytes_per_launch" in e:
+            if isinstance(e, dict) and "bytes_per_launch" in e and e.get("bound") != "mfma":
                 c = copy_ceiling(torch, head, dev, e["bytes_per_launch"], warmup, steps)
                 e["copy_GB/s"] = c
                 e["of_copy"] = round(e["GB/s"] / c, 3)
