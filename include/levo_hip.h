@@ -87,6 +87,33 @@ int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t c_in, int64
                           int64_t padding, int64_t dilation, const float * residual, int64_t residual_stride,
                           float * y, int64_t y_stride, levo_hip_stream_t stream);
 
+/* Weights of a ConvTranspose1d with kernel 2 * stride (the decoder's
+ * upsamplers) rearranged for levo_hip_snake_conv_transpose1d: weight is
+ * ggml's [c_in][c_out][2 * stride] (ne = [kernel, c_out, c_in]); packed
+ * (stride * c_out * c_in * 2 floats) holds, for every phase r < stride,
+ * [c_out][c_in][2] = (weight[..][..][r + stride], weight[..][..][r]). Done once
+ * per model; packed must be 16-byte aligned for the fast weight loads. */
+int levo_hip_conv_transpose1d_pack_weights(const float * weight, float * packed, int64_t c_in, int64_t c_out,
+                                           int64_t stride, levo_hip_stream_t stream);
+
+/* SnakeBeta + ConvTranspose1d (kernel 2 * stride) + crop + bias: the
+ * decoder's upsample step, run_snake then conv_transpose_1d_f32
+ * (src/levo-vae.cpp:223-228; src/levo-audio-ops.cpp:89-123:
+ * ggml_conv_transpose_1d, the crop of `padding` samples on both sides, the
+ * bias). Output sample t = q * stride + r - padding of phase r is
+ * sum_ci (w[ci][co][r] * s(x)[ci][q] + w[ci][co][r + stride] * s(x)[ci][q - 1]),
+ * so each phase is a 2-tap convolution on the matrix cores (one launch, the
+ * phase on the grid's z axis). x: F32 [c_in][x_stride] with t_in samples;
+ * SnakeBeta parameters as in levo_hip_snake_conv1d (NULL: none);
+ * packed_weight from levo_hip_conv_transpose1d_pack_weights; bias [c_out] or
+ * NULL; y: F32 [c_out][y_stride] with (t_in + 1) * stride - 2 * padding
+ * samples. The sum is accumulated on the F32 matrix cores in another order
+ * than ggml's, so y agrees with the reference to F32 rounding. */
+int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                    const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                                    const float * packed_weight, int64_t c_out, int64_t stride, const float * bias,
+                                    int64_t padding, float * y, int64_t y_stride, levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Residual add + RMSNorm / LayerNorm (rows of `dim` contiguous elements)    */
 /* ------------------------------------------------------------------------ */

@@ -39,8 +39,8 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 template <int KW>
 struct conv_chunk {
-    static constexpr int CI = KW == 1 ? 32 : 8;  // input channels per K chunk
-    static constexpr int KC = CI * KW;           // K values per chunk (a multiple of 4)
+    static constexpr int CI = KW == 1 ? 32 : KW == 2 ? 16 : 8;  // input channels per K chunk
+    static constexpr int KC = CI * KW;                          // K values per chunk (a multiple of 4)
 };
 
 struct conv_params {
@@ -63,6 +63,15 @@ struct conv_params {
     int32_t b_width;          // staged samples per input row: kNT + (KW - 1) * dil, rounded up to 4
     int32_t w_vec;            // weight rows 16-byte aligned with KW * c_in % 4 == 0
     int32_t y_vec;            // y (and residual) rows 16-byte aligned: float4 epilogue
+    // Output placement: column q of phase z = blockIdx.z goes to sample
+    // q * o_stride + o_base + z of y (kept when in [0, y_len)); the phase's
+    // weights start w_phase floats after p.w. A plain convolution has one
+    // phase, o_stride 1, o_base 0, y_len t_out.
+    int32_t o_stride;
+    int32_t o_base;
+    int64_t y_len;
+    int64_t w_phase;
+    int32_t scatter;          // transposed convolution: the strided epilogue
 };
 
 // LDS float index of weight (kk, r) in the A chunk: rows r = 64 h + 16 i + m
@@ -92,7 +101,7 @@ struct conv_slots {
     static constexpr int CI = conv_chunk<KW>::CI;
     static constexpr int KC = conv_chunk<KW>::KC;
     static constexpr int NA = KC / 4 * kMT / kThreads;
-    static constexpr int NB = KW == 1 ? CI / 2 : 2 * CI;
+    static constexpr int NB = KW == 1 ? CI / 2 : KW == 2 ? CI : 2 * CI;
 };
 
 template <int KW>
@@ -197,7 +206,9 @@ __device__ __forceinline__ void read_operands(const float * As, const float * Bs
 }
 
 template <int KW>
-__global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_params p) {
+__global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_params p0) {
+    conv_params p = p0;
+    p.w += static_cast<int64_t>(blockIdx.z) * p.w_phase;  // this phase's weights
     constexpr int CI = conv_chunk<KW>::CI;
     constexpr int KC = conv_chunk<KW>::KC;
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -284,6 +295,23 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
             for (int u = 0; u < 4; ++u)
                 out[(h * 64 + 16 * i + 4 * g + u) * kOutStride + vh * 64 + 16 * j + m] = acc[i][j][u];
     __syncthreads();
+    if (p.scatter) {
+        // transposed convolution: phase z's columns land every o_stride samples
+        const int64_t base = p.o_base + static_cast<int64_t>(blockIdx.z);
+        for (int e = tid; e < kMT * kNT; e += kThreads) {
+            const int r = e / kNT;
+            const int c = e % kNT;
+            const int co = co0 + r;
+            if (co >= p.c_out) break;  // rows only grow with e
+            const int64_t q = t0 + c;
+            const int64_t t = q * p.o_stride + base;
+            if (q >= p.t_out || t < 0 || t >= p.y_len) continue;
+            float v = out[r * kOutStride + c];
+            if (p.bias) v = v + p.bias[co];
+            p.y[co * p.y_pitch + t] = v;
+        }
+        return;
+    }
     const bool vec = p.y_vec && t0 + kNT <= p.t_out;
     constexpr int kOutIters = kMT * (kNT / 4) / kThreads;  // float4s of the tile per thread
     if (vec && co0 + kMT <= p.c_out) {
@@ -333,13 +361,13 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
 }
 
 template <int KW>
-int launch_conv(conv_params p, hipStream_t st) {
+int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
     constexpr int CI = conv_chunk<KW>::CI;
     p.b_width = (kNT + (KW - 1) * p.dil + 3) & ~3;
-    // each thread stages at most two samples of an input row
-    LEVO_REQUIRE(KW == 1 || p.b_width <= 2 * kThreads, "snake_conv1d: dilation too large");
-    p.w_vec = aligned16(p.w) && (static_cast<int64_t>(p.c_in) * KW) % 4 == 0;
-    p.y_vec = aligned16(p.y) && p.y_pitch % 4 == 0 &&
+    // each thread stages at most two samples of an input row (one for KW = 2)
+    LEVO_REQUIRE(KW == 1 || p.b_width <= (KW == 2 ? 1 : 2) * kThreads, "snake_conv1d: dilation too large");
+    p.w_vec = aligned16(p.w) && (static_cast<int64_t>(p.c_in) * KW) % 4 == 0 && p.w_phase % 4 == 0;
+    p.y_vec = !p.scatter && aligned16(p.y) && p.y_pitch % 4 == 0 &&
               (p.residual == nullptr || (aligned16(p.residual) && p.r_pitch % 4 == 0));
     const size_t buf = static_cast<size_t>(a_floats<KW>() + CI * p.b_width);
     const size_t lds = std::max(2 * buf, static_cast<size_t>(kMT) * kOutStride) * sizeof(float) +
@@ -354,9 +382,10 @@ int launch_conv(conv_params p, hipStream_t st) {
         }
         attribute_set = true;
     }
-    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)));
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
+                    static_cast<uint32_t>(phases));
     snake_conv1d_kernel<KW><<<grid, kThreads, lds, st>>>(p);
-    return launch_status("levo_hip_snake_conv1d");
+    return launch_status(what);
 }
 
 }  // namespace
@@ -411,11 +440,103 @@ extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t 
     p.b_width = 0;
     p.w_vec = 0;
     p.y_vec = 0;
+    p.o_stride = 1;
+    p.o_base = 0;
+    p.y_len = t_out;
+    p.w_phase = 0;
+    p.scatter = 0;
     const hipStream_t st = as_hip(stream);
+    const char * what = "levo_hip_snake_conv1d";
     switch (kernel) {
-        case 1: return launch_conv<1>(p, st);
-        case 3: return launch_conv<3>(p, st);
-        case 5: return launch_conv<5>(p, st);
-        default: return launch_conv<7>(p, st);
+        case 1: return launch_conv<1>(p, 1, st, what);
+        case 3: return launch_conv<3>(p, 1, st, what);
+        case 5: return launch_conv<5>(p, 1, st, what);
+        default: return launch_conv<7>(p, 1, st, what);
     }
+}
+
+namespace levo_hip {
+namespace {
+
+// packed[r][co][ci][0] = w[ci][co][r + stride], packed[r][co][ci][1] = w[ci][co][r]:
+// phase r of the transposed convolution as a 2-tap convolution over
+// x[q - 1], x[q].
+__global__ __launch_bounds__(kThreads) void pack_transpose_kernel(const float * __restrict__ w, float * packed,
+                                                                  int64_t c_in, int64_t c_out, int32_t stride) {
+    const int64_t n = static_cast<int64_t>(stride) * c_out * c_in;
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e >= n) return;
+    const int64_t ci = e % c_in;
+    const int64_t co = (e / c_in) % c_out;
+    const int64_t r = e / (c_in * c_out);
+    const int64_t k = 2 * static_cast<int64_t>(stride);
+    const float * src = w + (ci * c_out + co) * k;
+    packed[2 * e] = src[r + stride];
+    packed[2 * e + 1] = src[r];
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+extern "C" int levo_hip_conv_transpose1d_pack_weights(const float * weight, float * packed, int64_t c_in,
+                                                      int64_t c_out, int64_t stride, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(c_in > 0 && c_out > 0 && stride > 0, "LeVo audio graph: incompatible ConvTranspose1d weight/input shapes");
+    LEVO_REQUIRE(c_in <= (1 << 20) && c_out <= (1 << 20) && stride <= 64, "conv_transpose1d: dimensions too large");
+    LEVO_REQUIRE(weight != nullptr && packed != nullptr, "conv_transpose1d: null tensor");
+    const int64_t n = stride * c_out * c_in;
+    pack_transpose_kernel<<<static_cast<uint32_t>(ceil_div(n, kThreads)), kThreads, 0, as_hip(stream)>>>(
+            weight, packed, c_in, c_out, static_cast<int32_t>(stride));
+    return launch_status("levo_hip_conv_transpose1d_pack_weights");
+}
+
+extern "C" int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                               const void * alpha_log, const void * beta_log,
+                                               levo_hip_type param_type, const float * packed_weight,
+                                               int64_t c_out, int64_t stride, const float * bias, int64_t padding,
+                                               float * y, int64_t y_stride, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(c_in > 0 && c_out > 0 && t_in > 0, "LeVo audio graph: incompatible ConvTranspose1d weight/input shapes");
+    LEVO_REQUIRE(stride > 0 && padding >= 0, "LeVo audio graph: invalid ConvTranspose1d stride or padding");
+    LEVO_REQUIRE(stride <= 64 && c_in <= (1 << 20) && c_out <= (1 << 20) && t_in < (int64_t{1} << 36),
+                 "conv_transpose1d: dimensions too large");
+    const int64_t y_len = (t_in + 1) * stride - 2 * padding;
+    LEVO_REQUIRE(y_len > 0, "LeVo audio graph: ConvTranspose1d padding removes the entire output");
+    LEVO_REQUIRE(x != nullptr && packed_weight != nullptr && y != nullptr, "conv_transpose1d: null tensor");
+    LEVO_REQUIRE(x_stride >= t_in && y_stride >= y_len, "conv_transpose1d: row stride smaller than the row");
+    const bool snake = alpha_log != nullptr || beta_log != nullptr;
+    LEVO_REQUIRE(!snake || (alpha_log != nullptr && beta_log != nullptr),
+                 "snake_conv1d: SnakeBeta needs both alpha_log and beta_log");
+    LEVO_REQUIRE(!snake || param_type == LEVO_HIP_TYPE_F32 || param_type == LEVO_HIP_TYPE_F16,
+                 "LeVo audio graph: SnakeBeta alpha_log must be F32 or F16");
+    LEVO_REQUIRE(!snake || c_in <= kMaxSnakeChannels, "snake_conv1d: at most %d input channels with SnakeBeta",
+                 kMaxSnakeChannels);
+    LEVO_REQUIRE(ceil_div(t_in + 1, kNT) < (int64_t{1} << 31) && ceil_div(c_out, kMT) < 65536,
+                 "conv_transpose1d: grid too large");
+    conv_params p;
+    p.x = x;
+    p.x_pitch = x_stride;
+    p.t_in = t_in;
+    p.alpha_log = alpha_log;
+    p.beta_log = beta_log;
+    p.param_f16 = param_type == LEVO_HIP_TYPE_F16;
+    p.snake = snake;
+    p.w = packed_weight;
+    p.bias = bias;
+    p.residual = nullptr;
+    p.r_pitch = 0;
+    p.y = y;
+    p.y_pitch = y_stride;
+    p.t_out = t_in + 1;  // columns q = 0 .. t_in of every phase
+    p.c_in = static_cast<int32_t>(c_in);
+    p.c_out = static_cast<int32_t>(c_out);
+    p.pad = 1;
+    p.dil = 1;
+    p.b_width = 0;
+    p.w_vec = 0;
+    p.y_vec = 0;
+    p.o_stride = static_cast<int32_t>(stride);
+    p.o_base = static_cast<int32_t>(-padding);
+    p.y_len = y_len;
+    p.w_phase = c_out * c_in * 2;
+    p.scatter = 1;
+    return launch_conv<2>(p, static_cast<int>(stride), as_hip(stream), "levo_hip_snake_conv_transpose1d");
 }

@@ -122,6 +122,9 @@ class LevoHip:
             "levo_hip_snake_beta": (ctypes.c_int, [_P, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _I64, _P]),
             "levo_hip_snake_conv1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _P,
                                                      _I64, _I64, _P, _I64, _P, _I64, _P]),
+            "levo_hip_conv_transpose1d_pack_weights": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P]),
+            "levo_hip_snake_conv_transpose1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64,
+                                                               _I64, _P, _I64, _P, _I64, _P]),
             "levo_hip_residual_rms_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P,
                                                           _I64, _I64, _F, _P]),
             "levo_hip_residual_layer_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P,
@@ -177,6 +180,19 @@ class LevoHip:
             _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
             _addr(weight), c_out, kernel, _addr(bias), padding, dilation, _addr(residual),
             residual_stride or t_out, _addr(y), y_stride or t_out, _stream(stream)))
+
+    def conv_transpose1d_pack_weights(self, weight, packed, c_in, c_out, stride, stream=None):
+        return self._check(self.lib.levo_hip_conv_transpose1d_pack_weights(_addr(weight), _addr(packed), c_in, c_out,
+                                                                           stride, _stream(stream)))
+
+    def snake_conv_transpose1d(self, x, c_in, t_in, packed_weight, c_out, stride, *, alpha_log=None, beta_log=None,
+                               param_type=F32, bias=None, padding=0, y=None, x_stride=None, y_stride=None,
+                               stream=None):
+        t_out = (t_in + 1) * stride - 2 * padding
+        return self._check(self.lib.levo_hip_snake_conv_transpose1d(
+            _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
+            _addr(packed_weight), c_out, stride, _addr(bias), padding, _addr(y), y_stride or t_out,
+            _stream(stream)))
 
     def rms_norm(self, act_type, x, delta, weight, weight_type, h_out, y, rows, dim, eps, stream=None):
         return self._check(self.lib.levo_hip_residual_rms_norm(act_type, _addr(x), _addr(delta), _addr(weight),

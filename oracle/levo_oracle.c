@@ -793,3 +793,37 @@ void lo_conv1d_f32(const float * x, int64_t c_in, int64_t t_in, const float * w,
     }
     for (int i = 0; i < started; ++i) if (threads > 1 && tid[i]) pthread_join(tid[i], NULL);
 }
+
+/* ------------------------------------------------------------------------- */
+/* ConvTranspose1d (ggml_conv_transpose_1d + crop + bias)                     */
+/* ------------------------------------------------------------------------- */
+
+void lo_conv_transpose1d_f32(const float * x, int64_t c_in, int64_t t_in, const float * w, int64_t c_out,
+                             int64_t kernel, int64_t stride, int64_t padding, const float * bias, float * y) {
+    const int64_t t_full = (t_in - 1) * stride + kernel;
+    const int64_t t_out = t_full - 2 * padding;
+    if (t_out <= 0) return;
+    float * full = (float *)calloc((size_t)t_full, sizeof(float));
+    float * col = (float *)malloc((size_t)c_in * sizeof(float));
+    if (!full || !col) {
+        free(full);
+        free(col);
+        return;
+    }
+    for (int64_t co = 0; co < c_out; ++co) {
+        memset(full, 0, (size_t)t_full * sizeof(float));
+        for (int64_t i = 0; i < t_in; ++i) {
+            for (int64_t ci = 0; ci < c_in; ++ci) col[ci] = x[ci * t_in + i];
+            for (int64_t k = 0; k < kernel; ++k) {
+                float v = 0.0f;
+                for (int64_t ci = 0; ci < c_in; ++ci) v += w[(ci * c_out + co) * kernel + k] * col[ci];
+                full[i * stride + k] += v;
+            }
+        }
+        for (int64_t t = 0; t < t_out; ++t) {
+            y[co * t_out + t] = bias ? full[t + padding] + bias[co] : full[t + padding];
+        }
+    }
+    free(full);
+    free(col);
+}

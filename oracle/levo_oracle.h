@@ -34,6 +34,8 @@
  *                                          published reference quantizer
  *   lo_conv1d_f32 ........................ float64 direct convolution within the sequential-sum
  *                                          error bound; identity / shift kernels exactly
+ *   lo_conv_transpose1d_f32 .............. float64 scatter form within the error bound; delta
+ *                                          kernels upsample exactly
  *   lo_mul_mat_q8_0 ...................... float64 sum of the same block terms within the
  *                                          sequential-sum error bound; integer-valued
  *                                          blocks (d = 1) equal the exact integer product
@@ -162,6 +164,16 @@ void lo_dequantize_row_q4_0(const void * x, float * y, int64_t k);
  * NULL, y [c_out][t_out], t_out = t_in + 2 * padding - dilation * (kernel - 1). */
 void lo_conv1d_f32(const float * x, int64_t c_in, int64_t t_in, const float * w, int64_t c_out, int64_t kernel,
                    const float * bias, int64_t padding, int64_t dilation, float * y, int threads);
+
+/* conv_transpose_1d_f32 (src/levo-audio-ops.cpp:89-123): ggml_conv_transpose_1d
+ * (stride, no padding, dilation 1), then the crop of `padding` samples on
+ * both sides and the bias add. ggml-cpu's loop: for every output channel,
+ * input position i and tap k, v = dot over ci of w[ci][co][k] * x[ci][i]
+ * (F32, generic order), then full[co][i * stride + k] += v in order of i.
+ * x [c_in][t_in], w [c_in][c_out][kernel] (ggml ne = [kernel, c_out, c_in]),
+ * y [c_out][t_out], t_out = (t_in - 1) * stride + kernel - 2 * padding. */
+void lo_conv_transpose1d_f32(const float * x, int64_t c_in, int64_t t_in, const float * w, int64_t c_out,
+                             int64_t kernel, int64_t stride, int64_t padding, const float * bias, float * y);
 
 /* ggml_mul_mat(W, x) on ggml's CPU backend for a Q8_0 weight (the quantized
  * LeLM / Flow matrices, src/levo-quantization.h:96-118): W is [rows][k/32]

@@ -72,6 +72,7 @@ class Oracle:
             "lo_dequantize_row_q8_0": (None, [_P, _P, _I64]),
             "lo_mul_mat_q8_0": (None, [_P, _P, _P, _I64, _I64, _I64]),
             "lo_conv1d_f32": (None, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, ctypes.c_int]),
+            "lo_conv_transpose1d_f32": (None, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P]),
             "lo_dequantize_row_q4_0": (None, [_P, _P, _I64]),
             "lo_gaussian_noise": (None, [_P, _I64, ctypes.c_uint64]),
         }
@@ -225,6 +226,19 @@ class Oracle:
         b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
         self.lib.lo_conv1d_f32(_ptr(x), c_in, t_in, _ptr(w), c_out, kernel, _ptr(b), padding, dilation, _ptr(y),
                                threads)
+        return y
+
+    def conv_transpose1d(self, x, w, bias, stride, padding):
+        """conv_transpose_1d_f32: x [c_in][t_in], w [c_in][c_out][kernel] -> [c_out][t_out]."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        c_in, t_in = x.shape
+        _, c_out, kernel = w.shape
+        t_out = (t_in - 1) * stride + kernel - 2 * padding
+        y = np.empty((c_out, t_out), dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        self.lib.lo_conv_transpose1d_f32(_ptr(x), c_in, t_in, _ptr(w), c_out, kernel, stride, padding, _ptr(b),
+                                         _ptr(y))
         return y
 
     def mul_mat_q8_0(self, w_blocks: np.ndarray, x: np.ndarray, rows: int, k: int) -> np.ndarray:

@@ -151,3 +151,85 @@ def test_rejects_bad_arguments(hip, dev, binding):
         hip.snake_conv1d(x, 4, 10, w, 4, 7, padding=0, dilation=2, y=y)
     with pytest.raises(binding.LevoHipError, match="needs both"):
         hip.snake_conv1d(x, 4, 10, w, 4, 7, padding=3, alpha_log=torch.zeros(4, device=dev), y=y)
+
+
+# ---- SnakeBeta + ConvTranspose1d (the decoder's upsamplers) ----------------------
+
+def _run_transpose(hip, dev, x, w, b, stride, pad, a=None, bl=None, param_type=0):
+    import torch
+    c_in, t_in = x.shape
+    _, c_out, k = w.shape
+    assert k == 2 * stride
+    t_out = (t_in + 1) * stride - 2 * pad
+    packed = torch.empty(stride * c_out * c_in * 2, dtype=torch.float32, device=dev)
+    wd = to_dev(w, dev)
+    hip.conv_transpose1d_pack_weights(wd, packed, c_in, c_out, stride)
+    y = torch.full((c_out, t_out), float("nan"), dtype=torch.float32, device=dev)
+    hip.snake_conv_transpose1d(to_dev(x, dev), c_in, t_in, packed, c_out, stride,
+                               alpha_log=to_dev(a, dev) if a is not None else None,
+                               beta_log=to_dev(bl, dev) if bl is not None else None, param_type=param_type,
+                               bias=to_dev(b, dev) if b is not None else None, padding=pad, y=y)
+    return from_dev(y)
+
+
+def _want_transpose(oracle, x, w, b, stride, pad, a=None, bl=None):
+    xs = oracle.snake_beta(x, a, bl, threads=8) if a is not None else x
+    return oracle.conv_transpose1d(xs, w, b, stride, pad)
+
+
+@pytest.mark.parametrize("c_in,c_out,t_in,stride", [(2048, 1024, 40, 10), (1024, 512, 250, 6), (512, 256, 600, 4),
+                                                    (256, 128, 2000, 4), (128, 128, 9000, 2)])
+def test_upsample_stages(hip, dev, oracle, c_in, c_out, t_in, stride):
+    """The five upsample steps of decode (strides 10, 6, 4, 4, 2, kernel
+    2 * stride, padding (stride + 1) / 2; src/levo-vae.cpp:215-228) with
+    SnakeBeta in front, at shortened lengths."""
+    pad = (stride + 1) // 2
+    x = oracle.gaussian(c_in * t_in, c_in + stride).reshape(c_in, t_in)
+    w = (oracle.gaussian(c_in * c_out * 2 * stride, c_out + t_in) *
+         np.float32(1.0 / np.sqrt(2 * c_in))).reshape(c_in, c_out, 2 * stride)
+    b = (oracle.gaussian(c_out, 7 + stride) * np.float32(0.1)).astype(np.float32)
+    a, bl = _params(oracle, c_in, 8 + stride)
+    got = _run_transpose(hip, dev, x, w, b, stride, pad, a, bl)
+    want = _want_transpose(oracle, x, w, b, stride, pad, a, bl)
+    assert got.shape == want.shape
+    assert f32_err(got, want) <= 1e-5
+
+
+@pytest.mark.parametrize("c_in,c_out,t_in,stride,pad", [(3, 5, 7, 3, 2), (17, 9, 130, 5, 0), (1, 1, 1, 1, 0),
+                                                        (33, 130, 255, 2, 1), (6, 4, 20, 4, 3)])
+def test_transpose_odd_shapes(hip, dev, oracle, c_in, c_out, t_in, stride, pad):
+    """Partial channel and time tiles, odd channel counts (scalar weight
+    loads), stride 1, paddings other than the decoder's."""
+    x = oracle.gaussian(c_in * t_in, 40 + c_in).reshape(c_in, t_in)
+    w = (oracle.gaussian(c_in * c_out * 2 * stride, 41 + c_out) * np.float32(0.3)).reshape(c_in, c_out, 2 * stride)
+    b = oracle.gaussian(c_out, 42)
+    a, bl = _params(oracle, c_in, 43)
+    got = _run_transpose(hip, dev, x, w, b, stride, pad, a, bl)
+    want = _want_transpose(oracle, x, w, b, stride, pad, a, bl)
+    assert f32_err(got, want) <= 1e-5
+
+
+def test_transpose_delta_kernel_bit_exact(hip, dev, oracle):
+    """A delta tap with no SnakeBeta and no bias is zero-insertion
+    upsampling: every output is one product with 1.0 (exact)."""
+    c, t, s = 64, 300, 4
+    x = oracle.gaussian(c * t, 50).reshape(c, t)
+    for tap in (0, 2, 5, 7):
+        w = np.zeros((c, c, 2 * s), np.float32)
+        w[:, :, tap] = np.eye(c, dtype=np.float32)
+        got = _run_transpose(hip, dev, x, w, None, s, 2)
+        want = _want_transpose(oracle, x, w, None, s, 2)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), tap
+
+
+def test_transpose_f16_params_and_no_snake(hip, dev, oracle):
+    c_in, c_out, t, s = 64, 32, 500, 6
+    x = oracle.gaussian(c_in * t, 60).reshape(c_in, t)
+    w = (oracle.gaussian(c_in * c_out * 2 * s, 61) * np.float32(0.1)).reshape(c_in, c_out, 2 * s)
+    a16 = oracle.f32_to_f16(_params(oracle, c_in, 62)[0])
+    b16 = oracle.f32_to_f16(_params(oracle, c_in, 62)[1])
+    got = _run_transpose(hip, dev, x, w, None, s, 3, a16, b16, param_type=1)
+    want = _want_transpose(oracle, x, w, None, s, 3, oracle.f16_to_f32(a16), oracle.f16_to_f32(b16))
+    assert f32_err(got, want) <= 1e-5
+    got = _run_transpose(hip, dev, x, w, None, s, 3)
+    assert f32_err(got, _want_transpose(oracle, x, w, None, s, 3)) <= 1e-5

@@ -599,3 +599,46 @@ def test_conv1d_identity_shift_and_dilation_kernels(oracle):
     w = np.zeros((c, c, 3), np.float32)
     w[:, :, 1] = eye
     assert np.array_equal(oracle.conv1d(x, w, b, 1, 1), (x + b[:, None]).astype(np.float32))
+
+
+@pytest.mark.parametrize("c_in,c_out,t_in,stride", [(16, 8, 30, 10), (8, 16, 50, 6), (12, 12, 40, 4),
+                                                    (6, 5, 90, 2), (3, 2, 7, 3)])
+def test_conv_transpose1d_matches_float64(oracle, c_in, c_out, t_in, stride):
+    """ggml_conv_transpose_1d (kernel 2 * stride) + crop (stride + 1) / 2 +
+    bias against a float64 scatter-form transposed convolution, within the
+    error bound of the per-tap F32 dots and the two F32 additions."""
+    k = 2 * stride
+    pad = (stride + 1) // 2
+    x = oracle.gaussian(c_in * t_in, 300 + stride).reshape(c_in, t_in)
+    w = (oracle.gaussian(c_in * c_out * k, 301 + stride) * np.float32(0.3)).reshape(c_in, c_out, k)
+    b = oracle.gaussian(c_out, 302)
+    y = oracle.conv_transpose1d(x, w, b, stride, pad)
+    t_full = (t_in - 1) * stride + k
+    full = np.zeros((c_out, t_full))
+    absf = np.zeros((c_out, t_full))
+    for i in range(t_in):
+        for kk in range(k):
+            full[:, i * stride + kk] += w[:, :, kk].astype(np.float64).T @ x[:, i].astype(np.float64)
+            absf[:, i * stride + kk] += np.abs(w[:, :, kk]).astype(np.float64).T @ np.abs(x[:, i]).astype(np.float64)
+    exact = full[:, pad:t_full - pad] + b[:, None]
+    bound = (c_in + 2) * 2.0 ** -24 * absf[:, pad:t_full - pad] + 2.0 ** -24 * np.abs(exact) + 1e-30
+    assert y.shape == exact.shape
+    assert np.all(np.abs(y - exact) <= bound)
+
+
+def test_conv_transpose1d_delta_kernel_upsamples(oracle):
+    """A delta at tap k of a stride-s kernel places x[ci][i] at output
+    i * s + k - padding: zero-insertion upsampling, exactly."""
+    c, t, s = 4, 20, 4
+    x = oracle.gaussian(c * t, 310).reshape(c, t)
+    for tap in (0, 3, 5, 7):
+        w = np.zeros((c, c, 2 * s), np.float32)
+        w[:, :, tap] = np.eye(c, dtype=np.float32)
+        pad = (s + 1) // 2
+        y = oracle.conv_transpose1d(x, w, None, s, pad)
+        want = np.zeros_like(y)
+        for i in range(t):
+            o = i * s + tap - pad
+            if 0 <= o < y.shape[1]:
+                want[:, o] = x[:, i]
+        assert np.array_equal(y, want), tap
