@@ -567,6 +567,67 @@ def bench_snake_conv(torch, hip, head, dev, warmup, steps):
     return out
 
 
+def vae_decode_flops(frames):
+    """2 * C_out * C_in * taps * T_out summed over the decoder's 37 convolutions
+    (each transposed-conv output sample takes 2 taps per input channel)."""
+    f = 2.0 * 2048 * 64 * 7 * frames
+    t = frames
+    for s, (ci, co) in enumerate(zip((2048, 1024, 512, 256, 128), (1024, 512, 256, 128, 128))):
+        t *= (10, 6, 4, 4, 2)[s]
+        f += 2.0 * ci * co * 2 * t + 3 * (2.0 * co * co * 7 * t + 2.0 * co * co * t)
+    return f + 2.0 * 2 * 128 * 7 * t
+
+
+def bench_vae_decode(torch, hip, binding, head, dev, warmup, steps, frames=252):
+    """The whole Oobleck VAE decoder (levo_hip_vae_decode, 37 fused SnakeBeta +
+    convolution launches) on one 10.08 s window: latent [64][252] to stereo
+    audio [2][483840], random weights of the decoder's shapes."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    keep = []
+
+    def put(*shape, scale):
+        t = torch.randn(shape, generator=g, device=dev) * scale
+        keep.append(t)
+        return t.data_ptr()
+
+    w = binding.VaeDecoderWeights()
+    w.input.weight, w.input.bias = put(2048, 64, 7, scale=0.5 / math.sqrt(64 * 7)), put(2048, scale=0.05)
+    for s in range(5):
+        ci, co, st = binding.VAE_IN_WIDTH[s], binding.VAE_OUT_WIDTH[s], binding.VAE_STRIDES[s]
+        sg = w.stage[s]
+        sg.activation.alpha_log, sg.activation.beta_log = put(ci, scale=0.3), put(ci, scale=0.3)
+        raw = torch.randn((ci, co, 2 * st), generator=g, device=dev) * (0.5 / math.sqrt(2 * ci))
+        packed = torch.empty(st * co * ci * 2, device=dev)
+        hip.conv_transpose1d_pack_weights(raw, packed, ci, co, st)
+        keep.append(packed)
+        sg.upsample.weight, sg.upsample.bias = packed.data_ptr(), put(co, scale=0.05)
+        for r in range(3):
+            ru = sg.residual[r]
+            ru.pre.alpha_log, ru.pre.beta_log = put(co, scale=0.3), put(co, scale=0.3)
+            ru.conv_0.weight, ru.conv_0.bias = put(co, co, 7, scale=0.5 / math.sqrt(co * 7)), put(co, scale=0.05)
+            ru.post.alpha_log, ru.post.beta_log = put(co, scale=0.3), put(co, scale=0.3)
+            ru.conv_1.weight, ru.conv_1.bias = put(co, co, 1, scale=0.3 / math.sqrt(co)), put(co, scale=0.05)
+    w.output_activation.alpha_log, w.output_activation.beta_log = put(128, scale=0.3), put(128, scale=0.3)
+    w.output_weight = put(2, 128, 7, scale=0.5 / math.sqrt(128 * 7))
+    w.param_type = 0
+    latent = torch.randn((64, frames), generator=g, device=dev)
+    audio = torch.empty((2, frames * 1920), device=dev)
+    nbytes = hip.vae_decode_workspace_bytes(frames)
+    ws = torch.empty(nbytes // 4, device=dev)
+    ms = time_op(torch, head, lambda i: hip.vae_decode(w, latent, frames, audio, ws, nbytes), 1,
+                 max(warmup // 10, 2), max(steps // 10, 5))
+    assert bool(torch.isfinite(audio).all())
+    flops = vae_decode_flops(frames)
+    tflops = flops / (ms * 1e-3) / 1e12
+    seconds = frames * 1920 / 48000
+    del keep, ws
+    torch.cuda.empty_cache()
+    return {"frames": frames, "audio_seconds": seconds, "ms_per_window": round(ms, 3),
+            "realtime_factor": round(seconds / (ms * 1e-3), 1), "launches": 37, "flops_per_window": flops,
+            "TFLOP/s": round(tflops, 1), "frac_f32_mfma": round(tflops / PEAK_F32_MFMA_TFLOPS, 4), "bound": "mfma"}
+
+
 def bench_quant(torch, hip, head, dev, warmup, steps):
     R, Cc = 4096, 1536
     out = {}
@@ -741,7 +802,7 @@ def main() -> int:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-ops", action="store_true", help="only the headline ladder")
     p.add_argument("--only", default="",
-                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant,gemv,conv); "
+                   help="comma-separated op groups to run alone (snake,flow,norm,sample,quant,gemv,conv,vae); "
                         "prints the op table without the headline ladder")
     p.add_argument("--copy-ceiling", action="store_true",
                    help="with --only: annotate each op with a plain device copy of the same bytes")
@@ -792,6 +853,8 @@ def main() -> int:
             ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
         if "conv" in groups:
             ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
+        if "vae" in groups:
+            ops["vae_decode_252_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup, args.steps)
         if args.copy_ceiling:
             add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
         print(json.dumps({"ops": ops}))
@@ -840,6 +903,8 @@ def main() -> int:
         ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: snake conv1d")
         ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
+        log("ops: vae decoder window")
+        ops["vae_decode_252_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup, args.steps)
         log("ops: plain-copy ceilings")
         add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 

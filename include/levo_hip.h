@@ -114,6 +114,68 @@ int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride, int64_t c
                                     const float * packed_weight, int64_t c_out, int64_t stride, const float * bias,
                                     int64_t padding, float * y, int64_t y_stride, levo_hip_stream_t stream);
 
+/* The VAE decoder's weights in device memory, the fields of
+ * vae_decoder_weights (src/levo-vae-model.h:39-66). Convolution weights are
+ * F32 in ggml order ([k][c_in][c_out] ne = W[c_out][c_in][k] in memory);
+ * each upsample weight is the packed form of
+ * levo_hip_conv_transpose1d_pack_weights. The reference promotes F16
+ * artifacts' convolution weights to F32 before every operator; widen them
+ * once at load with levo_hip_fp16_to_fp32_row (exact). SnakeBeta parameters
+ * are of param_type (F32 or F16). */
+typedef struct levo_hip_vae_snake {
+    const void * alpha_log;
+    const void * beta_log;
+} levo_hip_vae_snake;
+typedef struct levo_hip_vae_conv {
+    const float * weight;
+    const float * bias;
+} levo_hip_vae_conv;
+typedef struct levo_hip_vae_residual {
+    levo_hip_vae_snake pre;
+    levo_hip_vae_conv conv_0;     /* k 7, dilation 1 / 3 / 9 */
+    levo_hip_vae_snake post;
+    levo_hip_vae_conv conv_1;     /* k 1 */
+} levo_hip_vae_residual;
+typedef struct levo_hip_vae_stage {
+    levo_hip_vae_snake activation;
+    levo_hip_vae_conv upsample;   /* packed ConvTranspose1d weight */
+    levo_hip_vae_residual residual[3];
+} levo_hip_vae_stage;
+typedef struct levo_hip_vae_decoder_weights {
+    levo_hip_vae_conv input;      /* [2048][64][7] */
+    levo_hip_vae_stage stage[5];  /* decode order: strides 10, 6, 4, 4, 2 */
+    levo_hip_vae_snake output_activation;
+    const float * output_weight;  /* [2][128][7], no bias */
+    levo_hip_type param_type;
+} levo_hip_vae_decoder_weights;
+
+/* validate_weights (src/levo-vae.cpp:56-78): LEVO_HIP_OK when every weight
+ * levo_hip_vae_decode reads is non-null and param_type is F32 or F16, else
+ * LEVO_HIP_ERR_INVALID naming the first missing one in the reference's order. */
+int levo_hip_vae_validate_weights(const levo_hip_vae_decoder_weights * weights);
+
+/* Workspace bytes levo_hip_vae_decode needs for `frames` latent frames
+ * (three activation buffers of 128 x 1920 x frames floats); < 0 if invalid. */
+int64_t levo_hip_vae_decode_workspace_bytes(int64_t frames);
+
+/* vae_decoder::decode (src/levo-vae.cpp:172-276) on the device: latent
+ * [64][frames] F32 to audio [2][frames * 1920] F32, with the reference's
+ * hyper-parameters (latent 64, widths 2048 -> 1024 -> 512 -> 256 -> 128 ->
+ * 128, strides 10, 6, 4, 4, 2, dilations 1, 3, 9). 37 fused SnakeBeta +
+ * convolution launches (input conv, 7 per stage, output conv); none of the
+ * activations leaves the device, the caller's workspace (16-byte aligned,
+ * levo_hip_vae_decode_workspace_bytes) holds them. Every weight the
+ * reference's validate_weights requires (src/levo-vae.cpp:56-78) must be
+ * non-null. stage_outputs, when non-null, holds 5 device pointers (each may
+ * be null): stage s's output [width_s][frames * prod(strides[0..s])] is
+ * copied there, the reference's capture_stages tensors. Every convolution
+ * agrees with the reference to F32 rounding; so does the composition. The
+ * reference's host-side latent checks (shape, finite values) belong to the
+ * caller, which holds the latent on the host. */
+int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * weights, const float * latent, int64_t frames,
+                        float * audio, float * const * stage_outputs, void * workspace, int64_t workspace_bytes,
+                        levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Residual add + RMSNorm / LayerNorm (rows of `dim` contiguous elements)    */
 /* ------------------------------------------------------------------------ */

@@ -360,8 +360,150 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     }
 }
 
+// ---- narrow output (c_out <= 4): the decoder's 128 -> 2 output conv -------
+//
+// A 128-row matrix-core tile would compute 2 useful rows, so narrow outputs
+// take a VALU kernel instead: a workgroup owns kNarrowT output samples (thread
+// tid the samples tid + 256 j, j < 4) and walks the input channels in chunks
+// of kNarrowCI. A chunk's raw input rows (halo included) and weights are
+// loaded into registers while the previous chunk is summed, then SnakeBeta is
+// applied once per element on the way into LDS; the weights sit in LDS
+// (zero past c_out) and are read at wave-uniform addresses. Every output
+// channel is summed with FMAs over (ci, k) in ascending order.
+constexpr int kNarrowT = 1024;
+constexpr int kNarrowCI = 8;
+constexpr int kNarrowJ = kNarrowT / kThreads;
+constexpr int kNarrowMaxSpan = 512;                                   // (kernel - 1) * dilation
+constexpr int kNarrowRowLoads = (kNarrowT + kNarrowMaxSpan + kThreads - 1) / kThreads;  // per row and thread
+
+template <int KW, int NCO>
+struct narrow_regs {
+    float x[kNarrowCI][kNarrowRowLoads];
+    float w;  // weight tid of the chunk's [NCO][kNarrowCI][KW] (tid < NCO * kNarrowCI * KW)
+};
+
+template <int KW, int NCO>
+__device__ __forceinline__ void narrow_load(const conv_params & p, int ci0, int64_t tb, bool inside, int tid,
+                                            narrow_regs<KW, NCO> & r) {
+#pragma unroll
+    for (int c = 0; c < kNarrowCI; ++c) {
+        const bool row = ci0 + c < p.c_in;
+        const float * xr = p.x + static_cast<int64_t>(ci0 + c) * p.x_pitch + tb;
+#pragma unroll
+        for (int i = 0; i < kNarrowRowLoads; ++i) {
+            const int j = tid + kThreads * i;
+            float v = 0.0f;
+            if (row && j < p.b_width && (inside || (tb + j >= 0 && tb + j < p.t_in))) v = xr[j];
+            r.x[c][i] = v;
+        }
+    }
+    r.w = 0.0f;
+    if (tid < NCO * kNarrowCI * KW) {
+        const int co = tid / (kNarrowCI * KW);
+        const int rem = tid - co * (kNarrowCI * KW);  // c * KW + k
+        const int c = rem / KW;
+        if (co < p.c_out && ci0 + c < p.c_in) r.w = p.w[(static_cast<int64_t>(co) * p.c_in + ci0) * KW + rem];
+    }
+}
+
+template <int KW, int NCO>
+__global__ __launch_bounds__(kThreads) void snake_conv_narrow_kernel(const conv_params p) {
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int width = p.b_width;                                     // kNarrowT + (KW - 1) * dil, rounded to 4
+    float * xs = lds;                                                // [kNarrowCI][width]
+    float * ws = xs + kNarrowCI * width;                             // [NCO][kNarrowCI][KW]
+    snake_param * sp = reinterpret_cast<snake_param *>(ws + NCO * kNarrowCI * KW);  // [c_in] when p.snake
+    const int tid = threadIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kNarrowT;
+    const int64_t tb = t0 - p.pad;
+    const bool inside = tb >= 0 && tb + width <= p.t_in;
+    narrow_regs<KW, NCO> r;
+    narrow_load<KW, NCO>(p, 0, tb, inside, tid, r);
+    if (p.snake) {
+        for (int c = tid; c < p.c_in; c += kThreads) {
+            const float al = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.alpha_log)[c])
+                                         : static_cast<const float *>(p.alpha_log)[c];
+            const float bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.beta_log)[c])
+                                         : static_cast<const float *>(p.beta_log)[c];
+            sp[c] = make_snake_param(al, bl);
+        }
+    }
+    float acc[NCO][kNarrowJ];
+#pragma unroll
+    for (int co = 0; co < NCO; ++co)
+#pragma unroll
+        for (int j = 0; j < kNarrowJ; ++j) acc[co][j] = 0.0f;
+    for (int ci0 = 0; ci0 < p.c_in; ci0 += kNarrowCI) {
+        __syncthreads();  // the previous chunk's reads are done (and sp is ready)
+#pragma unroll
+        for (int c = 0; c < kNarrowCI; ++c) {
+#pragma unroll
+            for (int i = 0; i < kNarrowRowLoads; ++i) {
+                const int j = tid + kThreads * i;
+                if (j < width) {
+                    float v = r.x[c][i];
+                    // zero padding stays zero: s(0) = 0 + sin^2(0) / beta = 0 exactly
+                    if (p.snake && ci0 + c < p.c_in) v = snake(v, sp[ci0 + c]);
+                    xs[c * width + j] = v;
+                }
+            }
+        }
+        if (tid < NCO * kNarrowCI * KW) ws[tid] = r.w;
+        __syncthreads();
+        if (ci0 + kNarrowCI < p.c_in) narrow_load<KW, NCO>(p, ci0 + kNarrowCI, tb, inside, tid, r);  // in flight
+        const int nc = min(kNarrowCI, p.c_in - ci0);
+        for (int c = 0; c < nc; ++c) {
+            const float * row = xs + c * width + tid;
+#pragma unroll
+            for (int k = 0; k < KW; ++k) {
+                float xv[kNarrowJ];
+#pragma unroll
+                for (int j = 0; j < kNarrowJ; ++j) xv[j] = row[kThreads * j + k * p.dil];
+#pragma unroll
+                for (int co = 0; co < NCO; ++co) {
+                    const float w = ws[(co * kNarrowCI + c) * KW + k];
+#pragma unroll
+                    for (int j = 0; j < kNarrowJ; ++j) acc[co][j] = __builtin_fmaf(w, xv[j], acc[co][j]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int co = 0; co < NCO; ++co) {
+        if (co >= p.c_out) break;
+        const float bv = p.bias ? p.bias[co] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kNarrowJ; ++j) {
+            const int64_t t = t0 + tid + kThreads * j;
+            if (t >= p.t_out) break;
+            float v = acc[co][j];
+            if (p.bias) v = v + bv;
+            if (p.residual) v = p.residual[co * p.r_pitch + t] + v;
+            p.y[co * p.y_pitch + t] = v;
+        }
+    }
+}
+
+template <int KW>
+int launch_narrow(conv_params p, hipStream_t st, const char * what) {
+    p.b_width = (kNarrowT + (KW - 1) * p.dil + 3) & ~3;
+    const int nco = p.c_out <= 2 ? 2 : 4;
+    const size_t lds = (static_cast<size_t>(kNarrowCI) * p.b_width + nco * kNarrowCI * KW) * sizeof(float) +
+                       (p.snake ? static_cast<size_t>(p.c_in) * sizeof(snake_param) : 0);
+    LEVO_REQUIRE(p.b_width <= kThreads * kNarrowRowLoads, "snake_conv1d: dilation too large");
+    LEVO_REQUIRE(lds <= 64 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNarrowT)));
+    if (nco == 2) {
+        snake_conv_narrow_kernel<KW, 2><<<grid, kThreads, lds, st>>>(p);
+    } else {
+        snake_conv_narrow_kernel<KW, 4><<<grid, kThreads, lds, st>>>(p);
+    }
+    return launch_status(what);
+}
+
 template <int KW>
 int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
+    if (!p.scatter && p.c_out <= 4 && (KW - 1) * p.dil <= kNarrowMaxSpan) return launch_narrow<KW>(p, st, what);
     constexpr int CI = conv_chunk<KW>::CI;
     p.b_width = (kNT + (KW - 1) * p.dil + 3) & ~3;
     // each thread stages at most two samples of an input row (one for KW = 2)

@@ -1,0 +1,145 @@
+// The Oobleck VAE decoder of vae_decoder::decode (src/levo-vae.cpp:172-276)
+// as a sequence of fused launches on one stream, every activation in HBM:
+//   input conv (64 -> 2048, k 7, padding 3)
+//   5 x [SnakeBeta + ConvTranspose1d upsample (stride s, kernel 2s,
+//        padding (s + 1) / 2) + 3 residual units (SnakeBeta + conv k 7 at
+//        dilation 1 / 3 / 9, SnakeBeta + conv k 1, + input)]
+//   SnakeBeta + output conv (128 -> 2, k 7, padding 3, no bias)
+// with the reference's fixed hyper-parameters (src/levo-vae-model.h:18-33,
+// decode order: strides 10, 6, 4, 4, 2; widths 2048 -> 1024 -> 512 -> 256
+// -> 128 -> 128). Host code only: it orders levo_hip_snake_conv1d and
+// levo_hip_snake_conv_transpose1d launches over three workspace buffers.
+#include "common.hpp"
+
+#include <algorithm>
+#include <utility>
+
+namespace levo_hip {
+namespace {
+
+constexpr int64_t kLatent = 64;
+constexpr int64_t kAudio = 2;
+constexpr int64_t kStrides[5] = {10, 6, 4, 4, 2};
+constexpr int64_t kInWidth[5] = {2048, 1024, 512, 256, 128};
+constexpr int64_t kOutWidth[5] = {1024, 512, 256, 128, 128};
+constexpr int64_t kDilations[3] = {1, 3, 9};
+
+// Largest channels x samples of any activation: the last stage's 128 x 1920 T.
+int64_t buffer_floats(int64_t frames) {
+    int64_t n = kInWidth[0] * frames;
+    int64_t len = frames;
+    for (int i = 0; i < 5; ++i) {
+        len *= kStrides[i];
+        n = std::max(n, kOutWidth[i] * len);
+    }
+    return (n + 63) / 64 * 64;  // 256-byte aligned thirds
+}
+
+// The first weight validate_weights (src/levo-vae.cpp:56-78) would reject as
+// absent, in its order, or nullptr when every one is present.
+const char * missing_weight(const levo_hip_vae_decoder_weights & w) {
+    const auto snake = [](const levo_hip_vae_snake & v) -> const char * {
+        if (v.alpha_log == nullptr) return "SnakeBeta alpha";
+        if (v.beta_log == nullptr) return "SnakeBeta beta";
+        return nullptr;
+    };
+    const auto conv = [](const levo_hip_vae_conv & v) -> const char * {
+        if (v.weight == nullptr) return "convolution weight";
+        if (v.bias == nullptr) return "convolution bias";
+        return nullptr;
+    };
+    const char * m = conv(w.input);
+    for (int s = 0; m == nullptr && s < 5; ++s) {
+        const levo_hip_vae_stage & sg = w.stage[s];
+        if ((m = snake(sg.activation)) || (m = conv(sg.upsample))) break;
+        for (int r = 0; m == nullptr && r < 3; ++r) {
+            const levo_hip_vae_residual & ru = sg.residual[r];
+            if (!(m = snake(ru.pre)) && !(m = conv(ru.conv_0)) && !(m = snake(ru.post))) m = conv(ru.conv_1);
+        }
+    }
+    if (m == nullptr) m = snake(w.output_activation);
+    if (m == nullptr && w.output_weight == nullptr) m = "output convolution weight";
+    return m;
+}
+
+bool weights_present(const levo_hip_vae_decoder_weights & w) { return missing_weight(w) == nullptr; }
+
+}  // namespace
+}  // namespace levo_hip
+
+using namespace levo_hip;
+
+extern "C" int64_t levo_hip_vae_decode_workspace_bytes(int64_t frames) {
+    if (frames <= 0 || frames > (int64_t{1} << 24)) return -1;
+    return 3 * buffer_floats(frames) * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int levo_hip_vae_validate_weights(const levo_hip_vae_decoder_weights * w) {
+    clear_error();
+    LEVO_REQUIRE(w != nullptr, "vae_decode: null weights");
+    LEVO_REQUIRE(w->param_type == LEVO_HIP_TYPE_F32 || w->param_type == LEVO_HIP_TYPE_F16,
+                 "vae_decode: SnakeBeta parameters must be F32 or F16");
+    LEVO_REQUIRE(weights_present(*w), "vae_decode: %s must be present", missing_weight(*w));
+    return LEVO_HIP_OK;
+}
+
+extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const float * latent, int64_t frames,
+                                   float * audio, float * const * stage_outputs, void * workspace,
+                                   int64_t workspace_bytes, levo_hip_stream_t stream) {
+    const int valid = levo_hip_vae_validate_weights(w);
+    if (valid != LEVO_HIP_OK) return valid;
+    LEVO_REQUIRE(frames > 0 && frames <= (int64_t{1} << 24), "latent frame count must be positive and representable");
+    LEVO_REQUIRE(latent != nullptr && audio != nullptr && workspace != nullptr, "vae_decode: null tensor");
+    LEVO_REQUIRE(aligned16(workspace), "vae_decode: workspace must be 16-byte aligned");
+    LEVO_REQUIRE(workspace_bytes >= levo_hip_vae_decode_workspace_bytes(frames),
+                 "vae_decode: workspace smaller than levo_hip_vae_decode_workspace_bytes");
+    const int64_t n = buffer_floats(frames);
+    float * a = static_cast<float *>(workspace);
+    float * b = a + n;
+    float * h = b + n;
+    const levo_hip_type pt = w->param_type;
+    int st;
+#define LEVO_STEP(call)                   \
+    do {                                  \
+        st = (call);                      \
+        if (st != LEVO_HIP_OK) return st; \
+    } while (0)
+    // input projection: no SnakeBeta in front (src/levo-vae.cpp:219-221)
+    LEVO_STEP(levo_hip_snake_conv1d(latent, frames, kLatent, frames, nullptr, nullptr, pt, w->input.weight,
+                                    kInWidth[0], 7, w->input.bias, 3, 1, nullptr, 0, a, frames, stream));
+    int64_t len = frames;
+    for (int s = 0; s < 5; ++s) {
+        const levo_hip_vae_stage & sg = w->stage[s];
+        const int64_t stride = kStrides[s];
+        const int64_t out_len = len * stride;  // (len + 1) s - 2 ((s + 1) / 2) for even s
+        LEVO_STEP(levo_hip_snake_conv_transpose1d(a, len, kInWidth[s], len, sg.activation.alpha_log,
+                                                  sg.activation.beta_log, pt, sg.upsample.weight, kOutWidth[s],
+                                                  stride, sg.upsample.bias, (stride + 1) / 2, b, out_len, stream));
+        len = out_len;
+        const int64_t c = kOutWidth[s];
+        for (int r = 0; r < 3; ++r) {
+            const levo_hip_vae_residual & ru = sg.residual[r];
+            const int64_t d = kDilations[r];
+            LEVO_STEP(levo_hip_snake_conv1d(b, len, c, len, ru.pre.alpha_log, ru.pre.beta_log, pt, ru.conv_0.weight,
+                                            c, 7, ru.conv_0.bias, 3 * d, d, nullptr, 0, h, len, stream));
+            // y = x + conv(snake(h)), written over x (src/levo-vae.cpp:96-100)
+            LEVO_STEP(levo_hip_snake_conv1d(h, len, c, len, ru.post.alpha_log, ru.post.beta_log, pt,
+                                            ru.conv_1.weight, c, 1, ru.conv_1.bias, 0, 1, b, len, b, len, stream));
+        }
+        if (stage_outputs != nullptr && stage_outputs[s] != nullptr) {
+            const hipError_t e = hipMemcpyAsync(stage_outputs[s], b, sizeof(float) * c * len,
+                                                hipMemcpyDeviceToDevice, as_hip(stream));
+            if (e != hipSuccess) {
+                set_error("vae_decode: stage %d copy: %s", s, hipGetErrorString(e));
+                return LEVO_HIP_ERR_RUNTIME;
+            }
+        }
+        std::swap(a, b);
+    }
+    // output: SnakeBeta + conv 128 -> 2, no bias (src/levo-vae.cpp:258-262)
+    LEVO_STEP(levo_hip_snake_conv1d(a, len, kOutWidth[4], len, w->output_activation.alpha_log,
+                                    w->output_activation.beta_log, pt, w->output_weight, kAudio, 7, nullptr, 3, 1,
+                                    nullptr, 0, audio, len, stream));
+#undef LEVO_STEP
+    return LEVO_HIP_OK;
+}

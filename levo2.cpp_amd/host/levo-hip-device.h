@@ -12,6 +12,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -19,6 +20,14 @@
 namespace levo::hip {
 
 using stream_t = hipStream_t;
+
+// Thrown when the cancellation callback returns true (include/levo.h:21-26).
+class operation_cancelled : public std::runtime_error {
+public:
+    operation_cancelled() : std::runtime_error("LeVo operation cancelled") {}
+};
+
+using cancellation_callback = std::function<bool()>;
 
 // Throws std::runtime_error("LeVo HIP: <what>: <HIP error>") if status is not hipSuccess.
 void check_hip(hipError_t status, const char * what);

@@ -19,14 +19,6 @@
 
 namespace levo::hip {
 
-// Thrown when the cancellation callback returns true (include/levo.h:21-26).
-class operation_cancelled : public std::runtime_error {
-public:
-    operation_cancelled() : std::runtime_error("LeVo operation cancelled") {}
-};
-
-using cancellation_callback = std::function<bool()>;
-
 namespace flow {
 
 // Same fields as levo::flow::euler_input: C-order [frames, latent_dim] state.

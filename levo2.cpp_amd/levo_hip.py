@@ -79,6 +79,35 @@ class FlowStepArgs(ctypes.Structure):
     ]
 
 
+class VaeSnake(ctypes.Structure):
+    _fields_ = [("alpha_log", _P), ("beta_log", _P)]
+
+
+class VaeConv(ctypes.Structure):
+    _fields_ = [("weight", _P), ("bias", _P)]
+
+
+class VaeResidual(ctypes.Structure):
+    _fields_ = [("pre", VaeSnake), ("conv_0", VaeConv), ("post", VaeSnake), ("conv_1", VaeConv)]
+
+
+class VaeStage(ctypes.Structure):
+    _fields_ = [("activation", VaeSnake), ("upsample", VaeConv), ("residual", VaeResidual * 3)]
+
+
+class VaeDecoderWeights(ctypes.Structure):
+    """levo_hip_vae_decoder_weights (include/levo_hip.h)."""
+
+    _fields_ = [("input", VaeConv), ("stage", VaeStage * 5), ("output_activation", VaeSnake),
+                ("output_weight", _P), ("param_type", ctypes.c_int)]
+
+
+VAE_STRIDES = (10, 6, 4, 4, 2)
+VAE_IN_WIDTH = (2048, 1024, 512, 256, 128)
+VAE_OUT_WIDTH = (1024, 512, 256, 128, 128)
+VAE_DILATIONS = (1, 3, 9)
+
+
 def header_abi_version(header: str = HEADER) -> int:
     """LEVO_HIP_ABI_VERSION as declared in include/levo_hip.h."""
     m = re.search(r"#define\s+LEVO_HIP_ABI_VERSION\s+(\d+)", open(header).read())
@@ -125,6 +154,10 @@ class LevoHip:
             "levo_hip_conv_transpose1d_pack_weights": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_snake_conv_transpose1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64,
                                                                _I64, _P, _I64, _P, _I64, _P]),
+            "levo_hip_vae_decode_workspace_bytes": (_I64, [_I64]),
+            "levo_hip_vae_validate_weights": (ctypes.c_int, [ctypes.POINTER(VaeDecoderWeights)]),
+            "levo_hip_vae_decode": (ctypes.c_int, [ctypes.POINTER(VaeDecoderWeights), _P, _I64, _P, _P, _P, _I64,
+                                                    _P]),
             "levo_hip_residual_rms_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P,
                                                           _I64, _I64, _F, _P]),
             "levo_hip_residual_layer_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P,
@@ -193,6 +226,23 @@ class LevoHip:
             _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
             _addr(packed_weight), c_out, stride, _addr(bias), padding, _addr(y), y_stride or t_out,
             _stream(stream)))
+
+    def vae_validate_weights(self, weights: VaeDecoderWeights):
+        return self._check(self.lib.levo_hip_vae_validate_weights(ctypes.byref(weights)))
+
+    def vae_decode_workspace_bytes(self, frames):
+        return int(self.lib.levo_hip_vae_decode_workspace_bytes(frames))
+
+    def vae_decode(self, weights: VaeDecoderWeights, latent, frames, audio, workspace, workspace_bytes, *,
+                   stage_outputs=None, stream=None):
+        """stage_outputs: None or 5 device tensors (or None) receiving each stage's output."""
+        stages = None
+        if stage_outputs is not None:
+            if len(stage_outputs) != 5:
+                raise ValueError("stage_outputs holds one tensor (or None) per stage")
+            stages = (ctypes.c_void_p * 5)(*[_addr(t) for t in stage_outputs])
+        return self._check(self.lib.levo_hip_vae_decode(ctypes.byref(weights), _addr(latent), frames, _addr(audio),
+                                                        stages, _addr(workspace), workspace_bytes, _stream(stream)))
 
     def rms_norm(self, act_type, x, delta, weight, weight_type, h_out, y, rows, dim, eps, stream=None):
         return self._check(self.lib.levo_hip_residual_rms_norm(act_type, _addr(x), _addr(delta), _addr(weight),

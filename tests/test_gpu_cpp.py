@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 BIN = os.path.join(HERE, "cpp", "bin")
-NAMES = ["test-hip-sampling", "test-hip-flow-renderer", "test-hip-ops"]
+NAMES = ["test-hip-sampling", "test-hip-flow-renderer", "test-hip-ops", "test-hip-vae-decoder"]
 
 
 @pytest.mark.parametrize("name", NAMES)

@@ -140,6 +140,50 @@ def test_strides_and_in_place_residual(hip, dev, oracle):
     assert f32_err(from_dev(rs)[:, :t], want) <= 1e-5
 
 
+@pytest.mark.parametrize("c_in,c_out,t,kw,pad,dil", [(128, 2, 483840, 7, 3, 1), (128, 1, 5000, 7, 3, 1),
+                                                    (37, 3, 2049, 5, 2, 4), (8, 4, 1024, 3, 1, 1),
+                                                    (17, 4, 3001, 7, 255, 85), (300, 2, 777, 1, 0, 1),
+                                                    (2, 3, 40, 7, 0, 5)])
+def test_narrow_outputs(hip, dev, oracle, c_in, c_out, t, kw, pad, dil):
+    """c_out <= 4 (the decoder's 128 -> 2 output conv at a 10.08 s window's
+    483840 samples, and ragged ones): the VAE output path. Partial channel
+    chunks, tiles past t_out, padding wider than a tile's halo, the largest
+    span (kernel - 1) * dilation = 510 of that path."""
+    x = oracle.gaussian(c_in * t, c_in + t + kw).reshape(c_in, t)
+    w = (oracle.gaussian(c_out * c_in * kw, c_out + t) * np.float32(1.0 / np.sqrt(c_in * kw))).reshape(c_out, c_in, kw)
+    b = oracle.gaussian(c_out, 9) if c_out != 1 else None
+    a, bl = _params(oracle, c_in, 10 + c_in)
+    got = _run(hip, dev, x, w, b, pad, dil, a, bl)
+    want = _want(oracle, x, w, b, pad, dil, a, bl)
+    assert got.shape == want.shape
+    assert f32_err(got, want) <= 1e-5
+
+
+def test_narrow_delta_residual_f16(hip, dev, oracle):
+    """c_out <= 4: a one-tap selector is exact (each output one product with
+    1.0 plus the bias), y written over the residual, F16 SnakeBeta parameters."""
+    import torch
+    c_in, c_out, t = 19, 4, 3000
+    x = oracle.gaussian(c_in * t, 120).reshape(c_in, t)
+    b = oracle.gaussian(c_out, 121)
+    w = np.zeros((c_out, c_in, 7), np.float32)
+    for co, (ci, tap) in enumerate(((0, 3), (7, 0), (18, 6), (11, 2))):
+        w[co, ci, tap] = 1.0
+    got = _run(hip, dev, x, w, b, 9, 3)
+    want = _want(oracle, x, w, b, 9, 3)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    r = oracle.gaussian(c_out * t, 122).reshape(c_out, t)
+    w = (oracle.gaussian(c_out * c_in * 7, 123) * np.float32(0.1)).reshape(c_out, c_in, 7)
+    a16 = oracle.f32_to_f16(_params(oracle, c_in, 124)[0])
+    b16 = oracle.f32_to_f16(_params(oracle, c_in, 124)[1])
+    want = _want(oracle, x, w, b, 3, 1, oracle.f16_to_f32(a16), oracle.f16_to_f32(b16), r)
+    rs = to_dev(r, dev)
+    hip.snake_conv1d(to_dev(x, dev), c_in, t, to_dev(w, dev), c_out, 7, alpha_log=to_dev(a16, dev),
+                     beta_log=to_dev(b16, dev), param_type=1, bias=to_dev(b, dev), padding=3, residual=rs, y=rs)
+    torch.cuda.synchronize()
+    assert f32_err(from_dev(rs), want) <= 1e-5
+
+
 def test_rejects_bad_arguments(hip, dev, binding):
     import torch
     x = torch.zeros((4, 10), device=dev)

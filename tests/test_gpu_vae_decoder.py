@@ -1,0 +1,203 @@
+"""The whole VAE decoder (levo_hip_vae_decode) against the oracle's chain of
+the same operations in the reference's order (vae_decoder::decode,
+src/levo-vae.cpp:172-276): input conv, five stages of SnakeBeta +
+ConvTranspose1d upsample and three residual units, SnakeBeta + output conv.
+
+Random weights of the reference's shapes (no checkpoint is available); one
+and two latent frames, as the reference's own first VAE fixtures use
+(docs/renderer-parity.md). Every convolution agrees with the oracle to F32
+rounding (tests/test_gpu_snake_conv.py); through the ~35 convolutions of the
+decoder that rounding compounds, so the end-to-end bar is 1e-4 of max(|y|, 1)
+(measured values are printed).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import f32_err, from_dev, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+class Weights:
+    """Host copies of one decoder's weights, drawn from a seeded generator."""
+
+    def __init__(self, binding, seed):
+        rng = np.random.default_rng(seed)
+        f32 = lambda a: np.ascontiguousarray(a, np.float32)
+
+        def conv(c_out, c_in, k, bias=True, gain=0.5):
+            w = f32(rng.standard_normal((c_out, c_in, k)) * (gain / np.sqrt(c_in * k)))
+            b = f32(rng.standard_normal(c_out) * 0.05) if bias else None
+            return w, b
+
+        def snake(c):
+            return f32(rng.standard_normal(c) * 0.3), f32(rng.standard_normal(c) * 0.3)
+
+        self.input = conv(2048, 64, 7)
+        self.stages = []
+        for s, (ci, co) in enumerate(zip(binding.VAE_IN_WIDTH, binding.VAE_OUT_WIDTH)):
+            st = binding.VAE_STRIDES[s]
+            up_w = f32(rng.standard_normal((ci, co, 2 * st)) * (0.5 / np.sqrt(2 * ci)))
+            up_b = f32(rng.standard_normal(co) * 0.05)
+            res = [dict(pre=snake(co), conv0=conv(co, co, 7), post=snake(co), conv1=conv(co, co, 1, gain=0.3))
+                   for _ in range(3)]
+            self.stages.append(dict(act=snake(ci), up=(up_w, up_b), res=res))
+        self.out_act = snake(128)
+        self.out_w = conv(2, 128, 7, bias=False)[0]
+
+
+def oracle_decode(oracle, w, latent):
+    """vae_decoder::decode's graph with the oracle's operations."""
+    h = oracle.conv1d(latent, w.input[0], w.input[1], 3, 1, threads=8)
+    for s, sg in enumerate(w.stages):
+        st = (10, 6, 4, 4, 2)[s]
+        x = oracle.snake_beta(h, *sg["act"], threads=8)
+        y = oracle.conv_transpose1d(x, sg["up"][0], sg["up"][1], st, (st + 1) // 2)
+        for r, d in enumerate((1, 3, 9)):
+            ru = sg["res"][r]
+            t = oracle.conv1d(oracle.snake_beta(y, *ru["pre"], threads=8), ru["conv0"][0], ru["conv0"][1], 3 * d, d,
+                              threads=8)
+            t = oracle.conv1d(oracle.snake_beta(t, *ru["post"], threads=8), ru["conv1"][0], ru["conv1"][1], 0, 1,
+                              threads=8)
+            y = (y + t).astype(np.float32)
+        h = y
+    return oracle.conv1d(oracle.snake_beta(h, *w.out_act, threads=8), w.out_w, None, 3, 1, threads=8)
+
+
+def device_weights(hip, binding, dev, w):
+    import torch
+    keep = []
+
+    def put(a):
+        if a is None:
+            return None
+        t = to_dev(a, dev)
+        keep.append(t)
+        return t.data_ptr()
+
+    dw = binding.VaeDecoderWeights()
+    dw.input.weight, dw.input.bias = put(w.input[0]), put(w.input[1])
+    for s, sg in enumerate(w.stages):
+        st = binding.VAE_STRIDES[s]
+        ci, co = binding.VAE_IN_WIDTH[s], binding.VAE_OUT_WIDTH[s]
+        stage = dw.stage[s]
+        stage.activation.alpha_log, stage.activation.beta_log = put(sg["act"][0]), put(sg["act"][1])
+        packed = torch.empty(st * co * ci * 2, dtype=torch.float32, device=dev)
+        keep.append(packed)
+        raw = to_dev(sg["up"][0], dev)
+        hip.conv_transpose1d_pack_weights(raw, packed, ci, co, st)
+        keep.append(raw)
+        stage.upsample.weight, stage.upsample.bias = packed.data_ptr(), put(sg["up"][1])
+        for r in range(3):
+            ru, dr = sg["res"][r], stage.residual[r]
+            dr.pre.alpha_log, dr.pre.beta_log = put(ru["pre"][0]), put(ru["pre"][1])
+            dr.conv_0.weight, dr.conv_0.bias = put(ru["conv0"][0]), put(ru["conv0"][1])
+            dr.post.alpha_log, dr.post.beta_log = put(ru["post"][0]), put(ru["post"][1])
+            dr.conv_1.weight, dr.conv_1.bias = put(ru["conv1"][0]), put(ru["conv1"][1])
+    dw.output_activation.alpha_log, dw.output_activation.beta_log = put(w.out_act[0]), put(w.out_act[1])
+    dw.output_weight = put(w.out_w)
+    dw.param_type = 0
+    return dw, keep
+
+
+@pytest.mark.parametrize("frames", [1, 2])
+def test_decoder_matches_oracle_chain(hip, binding, dev, oracle, frames):
+    import torch
+    w = Weights(binding, 1234 + frames)
+    latent = oracle.gaussian(64 * frames, 99 + frames).reshape(64, frames)
+    want = oracle_decode(oracle, w, latent)
+    dw, keep = device_weights(hip, binding, dev, w)
+    nbytes = hip.vae_decode_workspace_bytes(frames)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    audio = torch.full((2, frames * 1920), float("nan"), dtype=torch.float32, device=dev)
+    hip.vae_decode(dw, to_dev(latent, dev), frames, audio, ws, nbytes)
+    got = from_dev(audio)
+    err = f32_err(got, want)
+    print(f"frames {frames}: max|y| {np.abs(want).max():.3g}, err {err:.3g}")
+    assert got.shape == (2, frames * 1920)
+    assert np.isfinite(got).all()
+    assert err <= 1e-4
+
+
+def fill_pointers(struct, address):
+    """Every pointer field of a VaeDecoderWeights (nested) set to address."""
+    import ctypes
+    for name, kind in struct._fields_:
+        value = getattr(struct, name)
+        if isinstance(value, ctypes.Array):
+            for item in value:
+                fill_pointers(item, address)
+        elif isinstance(value, ctypes.Structure):
+            fill_pointers(value, address)
+        elif kind is ctypes.c_void_p:
+            setattr(struct, name, address)
+
+
+def test_decoder_rejects_bad_arguments(hip, binding, dev):
+    """validate_weights (src/levo-vae.cpp:56-78) and the frame / workspace
+    checks, each before any launch."""
+    import torch
+    dw = binding.VaeDecoderWeights()
+    ws = torch.empty(16, dtype=torch.float32, device=dev)
+    lat = torch.zeros(64, device=dev)
+    audio = torch.zeros(2 * 1920, device=dev)
+    with pytest.raises(binding.LevoHipError, match="convolution weight must be present"):
+        hip.vae_decode(dw, lat, 1, audio, ws, hip.vae_decode_workspace_bytes(1))
+    fill_pointers(dw, ws.data_ptr())
+    hip.vae_validate_weights(dw)
+    dw.stage[3].residual[2].pre.alpha_log = None
+    with pytest.raises(binding.LevoHipError, match="SnakeBeta alpha must be present"):
+        hip.vae_validate_weights(dw)
+    dw.stage[3].residual[2].pre.alpha_log = ws.data_ptr()
+    dw.param_type = 8
+    with pytest.raises(binding.LevoHipError, match="F32 or F16"):
+        hip.vae_validate_weights(dw)
+    dw.param_type = 0
+    with pytest.raises(binding.LevoHipError, match="workspace smaller"):
+        hip.vae_decode(dw, lat, 1, audio, ws, 64)
+    with pytest.raises(binding.LevoHipError, match="frame count"):
+        hip.vae_decode(dw, lat, 0, audio, ws, 64)
+    assert hip.vae_decode_workspace_bytes(1) == 3 * 128 * 1920 * 4
+    assert hip.vae_decode_workspace_bytes(0) < 0
+
+
+def test_decoder_stage_outputs(hip, binding, dev, oracle):
+    """Stage capture: stage s's output equals the oracle chain's, and the
+    audio is bit-identical to a decode without capture."""
+    import torch
+    frames = 1
+    w = Weights(binding, 77)
+    latent = oracle.gaussian(64 * frames, 5).reshape(64, frames)
+    dw, keep = device_weights(hip, binding, dev, w)
+    nbytes = hip.vae_decode_workspace_bytes(frames)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    lat = to_dev(latent, dev)
+    plain = torch.empty(2, 1920 * frames, device=dev)
+    hip.vae_decode(dw, lat, frames, plain, ws, nbytes)
+    lens = np.cumprod(binding.VAE_STRIDES) * frames
+    stages = [torch.full((c, n), float("nan"), device=dev) for c, n in zip(binding.VAE_OUT_WIDTH, lens)]
+    stages[2] = None
+    audio = torch.empty_like(plain)
+    hip.vae_decode(dw, lat, frames, audio, ws, nbytes, stage_outputs=stages)
+    torch.cuda.synchronize()
+    assert torch.equal(audio, plain)
+    # the oracle's stage outputs, recomputed stage by stage
+    h = oracle.conv1d(latent, w.input[0], w.input[1], 3, 1, threads=8)
+    for s, sg in enumerate(w.stages):
+        st = binding.VAE_STRIDES[s]
+        y = oracle.conv_transpose1d(oracle.snake_beta(h, *sg["act"], threads=8), sg["up"][0], sg["up"][1], st,
+                                    (st + 1) // 2)
+        for r, d in enumerate(binding.VAE_DILATIONS):
+            ru = sg["res"][r]
+            t = oracle.conv1d(oracle.snake_beta(y, *ru["pre"], threads=8), ru["conv0"][0], ru["conv0"][1], 3 * d, d,
+                              threads=8)
+            t = oracle.conv1d(oracle.snake_beta(t, *ru["post"], threads=8), ru["conv1"][0], ru["conv1"][1], 0, 1,
+                              threads=8)
+            y = (y + t).astype(np.float32)
+        h = y
+        if stages[s] is not None:
+            err = f32_err(from_dev(stages[s]), y)
+            print(f"stage {s}: err {err:.3g}")
+            assert err <= 1e-4
