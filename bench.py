@@ -580,8 +580,10 @@ def vae_decode_flops(frames):
 
 def bench_vae_decode(torch, hip, binding, head, dev, warmup, steps, frames=252):
     """The whole Oobleck VAE decoder (levo_hip_vae_decode, 37 fused SnakeBeta +
-    convolution launches) on one 10.08 s window: latent [64][252] to stereo
-    audio [2][483840], random weights of the decoder's shapes."""
+    convolution launches) on one window: latent [64][frames] to stereo audio
+    [2][frames * 1920], random weights of the decoder's shapes. 252 frames is
+    10.08 s of audio; 1000 frames is the renderer's decode window
+    (renderer_window_frames, src/levo-renderer-pattern.h:11)."""
     g = torch.Generator(device=dev)
     g.manual_seed(11)
     keep = []
@@ -854,7 +856,9 @@ def main() -> int:
         if "conv" in groups:
             ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
         if "vae" in groups:
-            ops["vae_decode_252_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup, args.steps)
+            for frames in (252, 1000):
+                ops[f"vae_decode_{frames}_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup,
+                                                                      args.steps, frames)
         if args.copy_ceiling:
             add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
         print(json.dumps({"ops": ops}))
@@ -903,8 +907,10 @@ def main() -> int:
         ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: snake conv1d")
         ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
-        log("ops: vae decoder window")
-        ops["vae_decode_252_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup, args.steps)
+        for frames in (252, 1000):
+            log(f"ops: vae decoder window of {frames} frames")
+            ops[f"vae_decode_{frames}_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup,
+                                                                  args.steps, frames)
         log("ops: plain-copy ceilings")
         add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 

@@ -72,6 +72,10 @@ struct conv_params {
     int64_t y_len;
     int64_t w_phase;
     int32_t scatter;          // transposed convolution: the strided epilogue
+    // SnakeBeta parameters in LDS: 0 = all c_in channels, computed up front;
+    // 1 = two slots of CI channels, each chunk's computed one chunk ahead (for
+    // wide inputs, where the full table would cost a workgroup per CU)
+    int32_t param_ring;
 };
 
 // LDS float index of weight (kk, r) in the A chunk: rows r = 64 h + 16 i + m
@@ -157,9 +161,10 @@ __device__ __forceinline__ void load_chunk(const conv_params & p, int ci0, int c
     }
 }
 
+// spc: the SnakeBeta parameters of this chunk's channels ci0 .. ci0 + CI - 1.
 template <int KW>
 __device__ __forceinline__ void store_chunk(const conv_params & p, int ci0, int tid, float * As, float * Bs,
-                                            const snake_param * sp, const f32x4v (&ra)[conv_slots<KW>::NA],
+                                            const snake_param * spc, const f32x4v (&ra)[conv_slots<KW>::NA],
                                             const float (&rb)[conv_slots<KW>::NB]) {
 #pragma unroll
     for (int u = 0; u < conv_slots<KW>::NA; ++u) {
@@ -176,7 +181,7 @@ __device__ __forceinline__ void store_chunk(const conv_params & p, int ci0, int 
         if (j < p.b_width) {
             float v = rb[s];
             // zero padding stays zero: s(0) = 0 + sin^2(0) / beta = 0 exactly
-            if (p.snake && ci0 + c < p.c_in) v = snake(v, sp[ci0 + c]);
+            if (p.snake && ci0 + c < p.c_in) v = snake(v, spc[c]);
             Bs[c * p.b_width + j] = v;
         }
     }
@@ -205,7 +210,17 @@ __device__ __forceinline__ void read_operands(const float * As, const float * Bs
     for (int j = 0; j < 4; ++j) b[j] = brow[16 * j];
 }
 
-template <int KW>
+// Raw alpha_log / beta_log of channel c (zero past c_in).
+__device__ __forceinline__ void load_snake_logs(const conv_params & p, int c, float & al, float & bl) {
+    al = 0.0f;
+    bl = 0.0f;
+    if (c < p.c_in) {
+        al = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.alpha_log)[c]) : static_cast<const float *>(p.alpha_log)[c];
+        bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.beta_log)[c]) : static_cast<const float *>(p.beta_log)[c];
+    }
+}
+
+template <int KW, bool RING>
 __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_params p0) {
     conv_params p = p0;
     p.w += static_cast<int64_t>(blockIdx.z) * p.w_phase;  // this phase's weights
@@ -213,9 +228,11 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     constexpr int KC = conv_chunk<KW>::KC;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     // two buffers of [A: KC x kAStride][B: CI x b_width], then the SnakeBeta
-    // parameters; the output tile reuses the buffers at the end
+    // parameters: [c_in], or with param_ring [2][CI] (chunk i's in slot i % 2,
+    // computed one chunk ahead of its staging); the output tile reuses the
+    // buffers at the end
     const int buf_floats = a_floats<KW>() + CI * p.b_width;
-    snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);  // [c_in] when p.snake
+    snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -232,11 +249,10 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     load_chunk<KW>(p, 0, co0, t0, tid, ra, rb);
 
     if (p.snake) {
-        for (int c = tid; c < p.c_in; c += kThreads) {
-            const float al = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.alpha_log)[c])
-                                         : static_cast<const float *>(p.alpha_log)[c];
-            const float bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.beta_log)[c])
-                                         : static_cast<const float *>(p.beta_log)[c];
+        const int n = RING ? 2 * CI : p.c_in;  // ring: chunks 0 and 1
+        for (int c = tid; c < n; c += kThreads) {
+            float al, bl;
+            load_snake_logs(p, c, al, bl);
             sp[c] = make_snake_param(al, bl);
         }
         __syncthreads();
@@ -254,6 +270,10 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     for (int ci0 = 0; ci0 < p.c_in; ci0 += CI) {
         const bool more = ci0 + CI < p.c_in;
         if (more) load_chunk<KW>(p, ci0 + CI, co0, t0, tid, ra, rb);  // in flight during the MFMAs
+        // parameters of the chunk after next, computed in this chunk's store phase
+        const bool params = RING && p.snake && ci0 + 2 * CI < p.c_in && tid < CI;
+        float al = 0.0f, bl = 0.0f;
+        if (params) load_snake_logs(p, ci0 + 2 * CI + tid, al, bl);
         const float * As = lds + buf * buf_floats;
         const float * Bs = As + a_floats<KW>();
         // Operands of step ks + 1 are read while step ks's 16 MFMAs issue.
@@ -277,8 +297,11 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         if (more) {
             // the other buffer was last read before the previous barrier
             float * An = lds + (buf ^ 1) * buf_floats;
-            store_chunk<KW>(p, ci0 + CI, tid, An, An + a_floats<KW>(), sp, ra, rb);
+            store_chunk<KW>(p, ci0 + CI, tid, An, An + a_floats<KW>(), sp + (RING ? (buf ^ 1) * CI : ci0 + CI),
+                            ra, rb);
         }
+        // slot buf held this chunk's parameters, last read before the previous barrier
+        if (RING && params) sp[buf * CI + tid] = make_snake_param(al, bl);
         __syncthreads();
         buf ^= 1;
     }
@@ -512,21 +535,33 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
     p.y_vec = !p.scatter && aligned16(p.y) && p.y_pitch % 4 == 0 &&
               (p.residual == nullptr || (aligned16(p.residual) && p.r_pitch % 4 == 0));
     const size_t buf = static_cast<size_t>(a_floats<KW>() + CI * p.b_width);
-    const size_t lds = std::max(2 * buf, static_cast<size_t>(kMT) * kOutStride) * sizeof(float) +
-                       (p.snake ? static_cast<size_t>(p.c_in) * sizeof(snake_param) : 0);
+    const size_t tiles = std::max(2 * buf, static_cast<size_t>(kMT) * kOutStride) * sizeof(float);
+    const int64_t wgs = ceil_div(p.t_out, kNT) * ceil_div(p.c_out, kMT) * phases;
+    // the full parameter table unless it alone keeps a second workgroup off
+    // a CU (160 KB of LDS) in a grid that has more than one per CU
+    const size_t table = static_cast<size_t>(p.c_in) * sizeof(snake_param);
+    p.param_ring = p.snake && 2 * (tiles + table) > 160 * 1024 && 2 * (tiles + 2 * CI * sizeof(snake_param)) <= 160 * 1024 &&
+                   wgs > 256;
+    const size_t lds = tiles + (p.snake ? (p.param_ring ? 2 * CI * sizeof(snake_param) : table) : 0);
     LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
     static bool attribute_set = false;
     if (!attribute_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&snake_conv1d_kernel<KW>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024) != hipSuccess) {
-            set_error("snake_conv1d: cannot raise the LDS limit");
-            return LEVO_HIP_ERR_RUNTIME;
+        for (const void * f : {reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, false>),
+                               reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, true>)}) {
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024) != hipSuccess) {
+                set_error("snake_conv1d: cannot raise the LDS limit");
+                return LEVO_HIP_ERR_RUNTIME;
+            }
         }
         attribute_set = true;
     }
     const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
                     static_cast<uint32_t>(phases));
-    snake_conv1d_kernel<KW><<<grid, kThreads, lds, st>>>(p);
+    if (p.param_ring) {
+        snake_conv1d_kernel<KW, true><<<grid, kThreads, lds, st>>>(p);
+    } else {
+        snake_conv1d_kernel<KW, false><<<grid, kThreads, lds, st>>>(p);
+    }
     return launch_status(what);
 }
 
@@ -587,6 +622,7 @@ extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t 
     p.y_len = t_out;
     p.w_phase = 0;
     p.scatter = 0;
+    p.param_ring = 0;
     const hipStream_t st = as_hip(stream);
     const char * what = "levo_hip_snake_conv1d";
     switch (kernel) {
@@ -680,5 +716,6 @@ extern "C" int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride
     p.y_len = y_len;
     p.w_phase = c_out * c_in * 2;
     p.scatter = 1;
+    p.param_ring = 0;
     return launch_conv<2>(p, static_cast<int>(stride), as_hip(stream), "levo_hip_snake_conv_transpose1d");
 }

@@ -140,6 +140,22 @@ def test_strides_and_in_place_residual(hip, dev, oracle):
     assert f32_err(from_dev(rs)[:, :t], want) <= 1e-5
 
 
+@pytest.mark.parametrize("c_in,t,kw,dil", [(1024, 33000, 7, 9), (1280, 33000, 1, 1)])
+def test_wide_inputs_parameter_ring(hip, dev, oracle, c_in, t, kw, dil):
+    """Wide inputs in a grid of more than one workgroup per CU keep only two
+    chunks of SnakeBeta parameters in LDS, each computed one chunk ahead
+    (1024 channels at k = 7, dilation 9, as a 40 s window's first stage;
+    1280 channels at k = 1). 128 outputs: 258 workgroups."""
+    pad = 3 * dil if kw == 7 else 0
+    x = oracle.gaussian(c_in * t, 130 + kw).reshape(c_in, t)
+    w = (oracle.gaussian(128 * c_in * kw, 131) * np.float32(1.0 / np.sqrt(c_in * kw))).reshape(128, c_in, kw)
+    b = oracle.gaussian(128, 132)
+    a, bl = _params(oracle, c_in, 133)
+    got = _run(hip, dev, x, w, b, pad, dil, a, bl)
+    want = _want(oracle, x, w, b, pad, dil, a, bl)
+    assert f32_err(got, want) <= 1e-5
+
+
 @pytest.mark.parametrize("c_in,c_out,t,kw,pad,dil", [(128, 2, 483840, 7, 3, 1), (128, 1, 5000, 7, 3, 1),
                                                     (37, 3, 2049, 5, 2, 4), (8, 4, 1024, 3, 1, 1),
                                                     (17, 4, 3001, 7, 255, 85), (300, 2, 777, 1, 0, 1),
