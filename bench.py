@@ -531,6 +531,46 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
 PEAK_F32_MFMA_TFLOPS = 157.3
 
 
+def bench_mul_mat_kquant(torch, hip, head, dev, warmup, steps):
+    """K-quant decode mat-vec (levo_hip_mul_mat_kquant: Q4_K, Q5_K, Q6_K
+    weights, the Q4_K_M / Q5_K_M / Q6_K profiles' matrices) at LeLM medium's
+    matrices with the CFG pair of activation columns already quantized to
+    Q8_K; weights rotated over >= 512 MB. Bytes: weights + Q8_K activations + y."""
+    shapes = {"attn_1536x1536": (1536, 1536), "ffn_up_8960x1536": (8960, 1536),
+              "ffn_down_1536x8960": (1536, 8960), "head_16385x1536": (16385, 1536)}
+    n_vec = 2
+    out = {}
+    g = torch.Generator(device=dev)
+    g.manual_seed(35)
+    for qtype, tname, bb in ((12, "q4_K", 144), (13, "q5_K", 176), (14, "q6_K", 210)):
+        for name, (rows, k) in shapes.items():
+            nb = rows * (k // 256)
+            nbytes = nb * bb
+            stride = (nbytes + 255) // 256 * 256
+            n = math.ceil(ROTATE_BYTES / nbytes) + 1
+            w = torch.randint(0, 256, (n, stride), generator=g, device=dev, dtype=torch.uint8)
+            scale = torch.full((nb, 1), 0x1400, dtype=torch.int16, device=dev).view(torch.uint8)  # F16 2^-10
+            for i in range(n):
+                blocks = w[i, :nbytes].view(nb, bb)
+                if qtype == 14:
+                    blocks[:, 208:210] = scale
+                else:
+                    blocks[:, 0:2] = scale
+                    blocks[:, 2:4] = scale
+            x = torch.randn((n_vec, k), generator=g, device=dev)
+            xb = torch.empty(n_vec * (k // 256) * 292, dtype=torch.uint8, device=dev)
+            hip.quantize_q8_K(x, xb, n_vec * k)
+            y = torch.empty((n_vec, rows), device=dev)
+            per = nbytes + n_vec * (k // 256) * 292 + n_vec * rows * 4
+            ms = time_op(torch, head, lambda i: hip.mul_mat_kquant(qtype, w[i].data_ptr(), xb, y, rows, rows, k,
+                                                                    n_vec), n, warmup, max(steps, 50))
+            out[f"{tname}_{name}"] = op_entry(per, ms, shape=[rows, k], n_vec=n_vec,
+                                              dtype=f"{tname} weights / q8_K activations")
+            del w
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_snake_conv(torch, hip, head, dev, warmup, steps):
     """Fused SnakeBeta + Conv1d (+ bias, + residual) of the VAE decoder's
     residual units at a 10.08 s window's real stage lengths: stage 5
@@ -853,6 +893,7 @@ def main() -> int:
             ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
         if "gemv" in groups:
             ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
+            ops["mul_mat_kquant"] = bench_mul_mat_kquant(torch, hip, head, dev, args.warmup, args.steps)
         if "conv" in groups:
             ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
         if "vae" in groups:
@@ -905,6 +946,8 @@ def main() -> int:
         ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
         log("ops: q8_0 mat-vec")
         ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
+        log("ops: k-quant mat-vec")
+        ops["mul_mat_kquant"] = bench_mul_mat_kquant(torch, hip, head, dev, args.warmup, args.steps)
         log("ops: snake conv1d")
         ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
         for frames in (252, 1000):

@@ -44,7 +44,11 @@ typedef enum levo_hip_type {
     LEVO_HIP_TYPE_F32 = 0,
     LEVO_HIP_TYPE_F16 = 1,
     LEVO_HIP_TYPE_Q4_0 = 2,
-    LEVO_HIP_TYPE_Q8_0 = 8
+    LEVO_HIP_TYPE_Q8_0 = 8,
+    LEVO_HIP_TYPE_Q4_K = 12,
+    LEVO_HIP_TYPE_Q5_K = 13,
+    LEVO_HIP_TYPE_Q6_K = 14,
+    LEVO_HIP_TYPE_Q8_K = 15
 } levo_hip_type;
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -418,7 +422,8 @@ int levo_hip_flow_denormalize(const float * normalized, const float * mean, cons
 /*   block_q4_0 = { f16 d; uint8 qs[16]; } 18 bytes                          */
 /* ------------------------------------------------------------------------ */
 
-/* ggml_row_size(type, n_per_row) for the supported types; < 0 on error. */
+/* ggml_row_size(type, n_per_row) for Q8_0 / Q4_0 (n_per_row a multiple of 32)
+ * and the K-quants Q4_K / Q5_K / Q6_K / Q8_K (a multiple of 256); < 0 on error. */
 int64_t levo_hip_row_size(levo_hip_type type, int64_t n_per_row);
 
 /* Replaces ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row,
@@ -440,7 +445,11 @@ int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, levo_hip_ty
                                int64_t nrows, int64_t dst_cols, levo_hip_stream_t stream);
 
 /* dequantize_row_q8_0 / dequantize_row_q4_0 (ggml to_float): k values
- * (multiple of 32) to dst_type F32, or F16 (exact products rounded RNE). */
+ * (multiple of 32) to dst_type F32, or F16 (exact products rounded RNE).
+ * Also dequantize_row_q4_K / q5_K / q6_K (k a multiple of 256, src 16-byte
+ * aligned): Q4_K / Q5_K y = d1 * q - m1 with d1 = d * sc and m1 = dmin * m
+ * each rounded and the last step in one rounding (as ggml's backends are
+ * compiled, contraction on); Q6_K y = (d * sc) * (q - 32), two roundings. */
 int levo_hip_dequantize(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type,
                         int64_t k, levo_hip_stream_t stream);
 
@@ -458,6 +467,39 @@ int levo_hip_dequantize(levo_hip_type type, const void * src, void * dst, levo_h
  * activations live in the workgroup's LDS; k = 11008 at n_vec = 2 fits). */
 int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks, float * y, int64_t y_pitch,
                           int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* K-quants on the decode path (ggml block layouts, QK_K = 256):              */
+/*   block_q4_K {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}            144 B */
+/*   block_q5_K {f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]} 176 B */
+/*   block_q6_K {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}           210 B */
+/*   block_q8_K {f32 d; i8 qs[256]; i16 bsums[16]}                      292 B */
+/* the matrices of the Q6_K / Q5_K_M / Q4_K_M profiles                       */
+/* (src/levo-quantization.h:47-55, 96-118).                                   */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_row_q8_K_ref, ggml's vec_dot_type for Q4_K / Q5_K / Q6_K (the
+ * activation side of ggml_mul_mat on the CPU backend): k values (a multiple
+ * of 256; x 16-byte aligned) to k / 256 blocks of 292 bytes (y 4-byte
+ * aligned). Per block d = 1 / (-127 / max) with max the first value of
+ * largest magnitude, q = min(127, nearest_int(-127 / max * x)), bsums the
+ * sums of 16 quants. A block of zeros gets zero bsums (ggml leaves them as
+ * they were). */
+int levo_hip_quantize_q8_K(const float * x, void * y, int64_t k, levo_hip_stream_t stream);
+
+/* Decode mat-vec with K-quant weights: the ggml_vec_dot_q4_K_q8_K /
+ * q5_K_q8_K / q6_K_q8_K rows of ggml_mul_mat(W, x). weight: [rows][k / 256]
+ * blocks of `type` (16-byte aligned); x_blocks: [n_vec][k / 256] block_q8_K
+ * from levo_hip_quantize_q8_K (4-byte aligned), shared by every matrix with
+ * that input. y: [n_vec][y_pitch] F32, y[v][r] = sum over blocks of
+ * (d_w * d_x) * sumi - (dmin_w * d_x) * summ (Q6_K: no min term), sumi and
+ * summ the exact integer sums of the reference's loop; the F32 terms are
+ * summed in a tree, so y agrees with ggml's loop to F32 rounding. k a
+ * multiple of 256 (pad rows as padded_input_columns does,
+ * src/levo-quantization.h:120-125); 1 <= n_vec <= 8, n_vec * k * 1.14 bytes
+ * of activations in LDS (<= 160 KB). */
+int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
+                            int64_t y_pitch, int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream);
 
 /* ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row (tools/levo-quantize.cpp:
  * 358, 369): IEEE round-to-nearest-even narrowing, exact widening. */

@@ -30,6 +30,12 @@ int launch_status(const char * what);
 
 inline hipStream_t as_hip(levo_hip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// K-quant helpers shared by the quantizer entry points (kquant.hip).
+bool is_kquant(levo_hip_type type);
+int64_t kquant_block_bytes(levo_hip_type type);  // Q4_K / Q5_K / Q6_K / Q8_K per 256 values; 0 otherwise
+int dequantize_kquant(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type, int64_t k,
+                      hipStream_t stream);
+
 inline bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -1,0 +1,518 @@
+// K-quant super-blocks (ggml's Q4_K / Q5_K / Q6_K, QK_K = 256) on the decode
+// path: the Q8_K activation quantizer (ggml's vec_dot_type for the K-quants,
+// quantize_row_q8_K_ref), the dequantizers (dequantize_row_q{4,5,6}_K) and
+// the mat-vec of ggml_mul_mat(W, x) with K-quant weights
+// (ggml_vec_dot_q{4,5,6}_K_q8_K). These are the matrices the Q6_K, Q5_K_M
+// and Q4_K_M profiles write (src/levo-quantization.h:47-55, 96-118).
+//
+// Block layouts (ggml, little-endian):
+//   block_q4_K {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}            144 B
+//   block_q5_K {f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]} 176 B
+//   block_q6_K {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}           210 B
+//   block_q8_K {f32 d; i8 qs[256]; i16 bsums[16]}                      292 B
+// Q4_K / Q5_K: eight sub-blocks of 32 with 6-bit scale and min (packed in
+// 12 bytes); value = d * sc * q - dmin * m. Q6_K: sixteen sub-blocks of 16
+// with int8 scales; value = d * sc * (q - 32).
+#include "common.hpp"
+
+namespace levo_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kQK = 256;
+
+// ggml's nearest_int: fval + 1.5 * 2^23 leaves the integer (ties to even) in
+// the mantissa for |fval| < 2^22.
+__device__ __forceinline__ int nearest_int(float fval) {
+    const float val = fval + 12582912.0f;
+    return static_cast<int>(__builtin_bit_cast(uint32_t, val) & 0x007fffffu) - 0x00400000;
+}
+
+// Byte s (0..11) of the packed scales held in three dwords.
+__device__ __forceinline__ int scale_byte(uint32_t s0, uint32_t s1, uint32_t s2, int s) {
+    const uint32_t w = s < 4 ? s0 : s < 8 ? s1 : s2;
+    return static_cast<int>((w >> (8 * (s & 3))) & 0xffu);
+}
+
+// get_scale_min_k4: sub-block j's 6-bit scale and min.
+__device__ __forceinline__ void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t s2, int j, int & sc, int & m) {
+    if (j < 4) {
+        sc = scale_byte(s0, s1, s2, j) & 63;
+        m = scale_byte(s0, s1, s2, j + 4) & 63;
+    } else {
+        const int b = scale_byte(s0, s1, s2, j + 4);
+        sc = (b & 0xF) | ((scale_byte(s0, s1, s2, j - 4) >> 6) << 4);
+        m = (b >> 4) | ((scale_byte(s0, s1, s2, j) >> 6) << 4);
+    }
+}
+
+// Two dwords at byte offset `off` of a block whose start is 2 mod 4 when
+// `odd` (Q6_K's 210-byte blocks): aligned dword loads and a 16-bit funnel
+// shift. off is a multiple of 4 and off + 10 <= 210; for odd blocks the two
+// bytes before the block (the previous block's tail: the buffer itself is
+// 16-byte aligned, so its first block is never odd) are read and discarded.
+__device__ __forceinline__ void load_u32x2(const uint8_t * blk, int off, bool odd, uint32_t & a, uint32_t & b) {
+    const uint32_t * p = reinterpret_cast<const uint32_t *>(blk + off - (odd ? 2 : 0));
+    if (!odd) {
+        a = p[0];
+        b = p[1];
+    } else {
+        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+        a = __builtin_amdgcn_alignbit(w1, w0, 16);
+        b = __builtin_amdgcn_alignbit(w2, w1, 16);
+    }
+}
+
+__device__ __forceinline__ uint32_t load_u32(const uint8_t * blk, int off, bool odd) {
+    const uint32_t * p = reinterpret_cast<const uint32_t *>(blk + off - (odd ? 2 : 0));
+    return odd ? __builtin_amdgcn_alignbit(p[1], p[0], 16) : p[0];
+}
+
+// Bytes b in [0, 63] to the signed bytes b - 32 (no borrow between bytes).
+__device__ __forceinline__ uint32_t minus32(uint32_t b) {
+    return ((b | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// ---- Q8_K quantizer: one wave per 256-value block ----------------------------
+
+__global__ __launch_bounds__(kThreads) void quantize_q8_K_kernel(const float * __restrict__ x, uint8_t * y,
+                                                                  int64_t nb) {
+    const int lane = threadIdx.x & 63;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (i >= nb) return;
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(x + i * kQK + 4 * lane);
+    // first element of largest |x| (NaN never compares larger), as the
+    // reference's `if (ax > amax)` scan: key = |x| bits, then lowest index
+    uint64_t key = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float ax = __builtin_fabsf(v[q]);
+        const uint32_t bits = ax == ax ? __builtin_bit_cast(uint32_t, ax) : 0u;
+        const uint64_t k = (static_cast<uint64_t>(bits) << 32) | static_cast<uint32_t>(255 - (4 * lane + q));
+        key = k > key ? k : key;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t other = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(key), o, 64));
+        key = other > key ? other : key;
+    }
+    uint8_t * blk = y + i * 292;
+    if ((key >> 32) == 0) {  // amax == 0: an all-zero block (bsums zero too)
+        reinterpret_cast<uint32_t *>(blk + 4)[lane] = 0u;
+        if (lane < 8) reinterpret_cast<uint32_t *>(blk + 260)[lane] = 0u;
+        if (lane == 0) *reinterpret_cast<float *>(blk) = 0.0f;
+        return;
+    }
+    const int arg = 255 - static_cast<int>(key & 0xffu);
+    const float max = __shfl(v[arg & 3], arg >> 2, 64);
+    const float iscale = -127.0f / max;
+    uint32_t packed = 0;
+    int sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        int l = nearest_int(iscale * v[q]);
+        l = l < 127 ? l : 127;
+        sum += l;
+        packed |= (static_cast<uint32_t>(l) & 0xffu) << (8 * q);
+    }
+    reinterpret_cast<uint32_t *>(blk + 4)[lane] = packed;
+    // bsums[j]: elements 16 j .. 16 j + 15 = lanes 4 j .. 4 j + 3
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    const int lo = __shfl(sum, 8 * (lane & 7), 64);
+    const int hi = __shfl(sum, 8 * (lane & 7) + 4, 64);
+    if (lane < 8) {
+        reinterpret_cast<uint32_t *>(blk + 260)[lane] =
+                (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
+    }
+    if (lane == 0) *reinterpret_cast<float *>(blk) = 1.0f / iscale;
+}
+
+// ---- dequantizers: 8 outputs per thread --------------------------------------
+
+template <int TYPE, typename Out>
+__global__ __launch_bounds__(kThreads) void dequantize_kquant_kernel(const uint8_t * __restrict__ src, Out * dst,
+                                                                      int64_t nb) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    const int64_t i = t >> 5;
+    if (i >= nb) return;
+    const int r = static_cast<int>(t & 31);
+    const int j = r >> 2;         // 32-element group of the block (Q4_K / Q5_K: the sub-block)
+    const int p = r & 3;          // 8-element part of it
+    constexpr int kBytes = TYPE == LEVO_HIP_TYPE_Q4_K ? 144 : TYPE == LEVO_HIP_TYPE_Q5_K ? 176 : 210;
+    const uint8_t * blk = src + i * kBytes;
+    float out[8];
+    if constexpr (TYPE == LEVO_HIP_TYPE_Q6_K) {
+        const bool odd = (reinterpret_cast<uintptr_t>(blk) & 3u) != 0;
+        const int n = j >> 2, quarter = j & 3, l0 = 8 * p;
+        uint32_t ql0, ql1, qh0, qh1;
+        load_u32x2(blk, 64 * n + 32 * (quarter & 1) + l0, odd, ql0, ql1);
+        load_u32x2(blk, 128 + 32 * n + l0, odd, qh0, qh1);
+        const float d = h2f(*reinterpret_cast<const uint16_t *>(blk + 208));  // 2-byte load: stays in the block
+        const int sub = 8 * n + 2 * quarter + (p >> 1);
+        const uint32_t sw = load_u32(blk, 192 + (sub & ~3), odd);
+        const int sc = static_cast<int8_t>((sw >> (8 * (sub & 3))) & 0xffu);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t qlw = l < 4 ? ql0 : ql1, qhw = l < 4 ? qh0 : qh1;
+            const int byte = static_cast<int>((qlw >> (8 * (l & 3))) & 0xffu);
+            const int nib = quarter < 2 ? (byte & 0xF) : (byte >> 4);
+            const int hi = static_cast<int>((qhw >> (8 * (l & 3) + 2 * quarter)) & 3u);
+            out[l] = d * static_cast<float>(sc) * static_cast<float>((nib | (hi << 4)) - 32);
+        }
+    } else {
+        const uint32_t * hw = reinterpret_cast<const uint32_t *>(blk);
+        const uint32_t h0 = hw[0], s0 = hw[1], s1 = hw[2], s2 = hw[3];
+        const float d = h2f(static_cast<uint16_t>(h0 & 0xffffu));
+        const float dmin = h2f(static_cast<uint16_t>(h0 >> 16));
+        int sc, m;
+        scale_min_k4(s0, s1, s2, j, sc, m);
+        const float d1 = d * static_cast<float>(sc);
+        const float m1 = dmin * static_cast<float>(m);
+        const int g = j >> 1, high = j & 1;
+        const uint8_t * qs = blk + (TYPE == LEVO_HIP_TYPE_Q5_K ? 48 : 16) + 32 * g + 8 * p;
+        const uint2 q = *reinterpret_cast<const uint2 *>(qs);
+        uint2 qh = uint2{0u, 0u};
+        if constexpr (TYPE == LEVO_HIP_TYPE_Q5_K) qh = *reinterpret_cast<const uint2 *>(blk + 16 + 8 * p);
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const uint32_t qw = l < 4 ? q.x : q.y;
+            const int byte = static_cast<int>((qw >> (8 * (l & 3))) & 0xffu);
+            int code = high ? (byte >> 4) : (byte & 0xF);
+            if constexpr (TYPE == LEVO_HIP_TYPE_Q5_K) {
+                const uint32_t hw2 = l < 4 ? qh.x : qh.y;
+                code += ((hw2 >> (8 * (l & 3) + j)) & 1u) ? 16 : 0;
+            }
+            out[l] = __builtin_fmaf(d1, static_cast<float>(code), -m1);
+        }
+    }
+    Out * o = dst + i * kQK + 32 * j + 8 * p;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        if constexpr (sizeof(Out) == 4) {
+            o[l] = out[l];
+        } else {
+            o[l] = f2h(out[l]);
+        }
+    }
+}
+
+// ---- mat-vec: one wave per row, 8 lanes per super-block ----------------------
+
+constexpr int kMaxVec = 8;
+
+struct kq_params {
+    const uint8_t * w;      // [rows][nb] blocks
+    const uint8_t * x;      // [n_vec][nb] block_q8_K
+    float * y;              // [n_vec][y_pitch]
+    int64_t y_pitch;
+    int64_t rows;
+    int64_t row_bytes;
+    int32_t nb;
+    int32_t n_vec;
+};
+
+// Raw weight registers of one unit (block ib, eighth u) of a row.
+template <int TYPE>
+struct kq_unit;
+
+template <>
+struct kq_unit<LEVO_HIP_TYPE_Q4_K> {
+    u32x4 hd, qs;  // d, dmin, scales; 16 bytes of quants (32 weights)
+    __device__ __forceinline__ void load(const uint8_t * blk, int u) {
+        hd = *reinterpret_cast<const u32x4 *>(blk);
+        qs = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * (u >> 1) + 16 * (u & 1));
+    }
+};
+
+template <>
+struct kq_unit<LEVO_HIP_TYPE_Q5_K> {
+    u32x4 hd, qh, qs;
+    __device__ __forceinline__ void load(const uint8_t * blk, int u) {
+        hd = *reinterpret_cast<const u32x4 *>(blk);
+        qh = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * (u & 1));
+        qs = *reinterpret_cast<const u32x4 *>(blk + 48 + 32 * (u >> 1) + 16 * (u & 1));
+    }
+};
+
+template <>
+struct kq_unit<LEVO_HIP_TYPE_Q6_K> {
+    uint32_t a0, a1, b0, b1, h0, h1, sw0, sw1;  // ql[l], ql[l + 32], qh[l] (8 l each), scales
+    uint16_t d;
+    __device__ __forceinline__ void load(const uint8_t * blk, int u) {
+        const bool odd = (reinterpret_cast<uintptr_t>(blk) & 3u) != 0;
+        const int n = u >> 2, l0 = 8 * (u & 3);
+        load_u32x2(blk, 64 * n + l0, odd, a0, a1);
+        load_u32x2(blk, 64 * n + 32 + l0, odd, b0, b1);
+        load_u32x2(blk, 128 + 32 * n + l0, odd, h0, h1);
+        load_u32x2(blk, 192 + 8 * n, odd, sw0, sw1);
+        d = *reinterpret_cast<const uint16_t *>(blk + 208);  // 2-byte load: stays in the block
+    }
+};
+
+// Adds one unit's terms for every activation column to acc_d / acc_m.
+// Q4_K / Q5_K unit u = (g = u / 2, h = u % 2): quants of sub-blocks 2 g (low
+// nibbles) and 2 g + 1 (high), elements 64 g + 16 h + [0, 16) and + 32.
+template <int TYPE>
+__device__ __forceinline__ void kq_compute(const kq_unit<TYPE> & w, int ib, int u, int nb, int n_vec,
+                                           const int8_t * xq, const float * xd, const int16_t * xs,
+                                           float (&acc_d)[kMaxVec], float (&acc_m)[kMaxVec]) {
+    if constexpr (TYPE == LEVO_HIP_TYPE_Q6_K) {
+        const int n = u >> 2, l0 = 8 * (u & 3);
+        const float dw = h2f(w.d);
+        // scales of sub-blocks 8 n + 2 quarter + (u & 3) / 2
+        const int sh = 8 * ((u & 3) >> 1);
+        const int sc0 = static_cast<int8_t>((w.sw0 >> sh) & 0xffu);
+        const int sc1 = static_cast<int8_t>((w.sw0 >> (sh + 16)) & 0xffu);
+        const int sc2 = static_cast<int8_t>((w.sw1 >> sh) & 0xffu);
+        const int sc3 = static_cast<int8_t>((w.sw1 >> (sh + 16)) & 0xffu);
+        const uint32_t c00 = minus32((w.a0 & 0x0F0F0F0Fu) | ((w.h0 & 0x03030303u) << 4));
+        const uint32_t c01 = minus32((w.a1 & 0x0F0F0F0Fu) | ((w.h1 & 0x03030303u) << 4));
+        const uint32_t c10 = minus32((w.b0 & 0x0F0F0F0Fu) | (((w.h0 >> 2) & 0x03030303u) << 4));
+        const uint32_t c11 = minus32((w.b1 & 0x0F0F0F0Fu) | (((w.h1 >> 2) & 0x03030303u) << 4));
+        const uint32_t c20 = minus32(((w.a0 >> 4) & 0x0F0F0F0Fu) | (((w.h0 >> 4) & 0x03030303u) << 4));
+        const uint32_t c21 = minus32(((w.a1 >> 4) & 0x0F0F0F0Fu) | (((w.h1 >> 4) & 0x03030303u) << 4));
+        const uint32_t c30 = minus32(((w.b0 >> 4) & 0x0F0F0F0Fu) | (((w.h0 >> 6) & 0x03030303u) << 4));
+        const uint32_t c31 = minus32(((w.b1 >> 4) & 0x0F0F0F0Fu) | (((w.h1 >> 6) & 0x03030303u) << 4));
+#pragma unroll
+        for (int v = 0; v < kMaxVec; ++v) {
+            if (v < n_vec) {
+                const int8_t * q8 = xq + (static_cast<int64_t>(v) * nb + ib) * kQK + 128 * n + l0;
+                const uint2 x0 = *reinterpret_cast<const uint2 *>(q8);
+                const uint2 x1 = *reinterpret_cast<const uint2 *>(q8 + 32);
+                const uint2 x2 = *reinterpret_cast<const uint2 *>(q8 + 64);
+                const uint2 x3 = *reinterpret_cast<const uint2 *>(q8 + 96);
+                const int isum = sc0 * dot4(c00, x0.x, dot4(c01, x0.y, 0)) + sc1 * dot4(c10, x1.x, dot4(c11, x1.y, 0)) +
+                                 sc2 * dot4(c20, x2.x, dot4(c21, x2.y, 0)) + sc3 * dot4(c30, x3.x, dot4(c31, x3.y, 0));
+                acc_d[v] += (dw * xd[v * nb + ib]) * static_cast<float>(isum);
+            }
+        }
+    } else {
+        const int g = u >> 1, h = u & 1;
+        u32x4 lo, hi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            lo[q] = w.qs[q] & 0x0F0F0F0Fu;
+            hi[q] = (w.qs[q] >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (TYPE == LEVO_HIP_TYPE_Q5_K) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                lo[q] |= ((w.qh[q] >> (2 * g)) & 0x01010101u) << 4;
+                hi[q] |= ((w.qh[q] >> (2 * g + 1)) & 0x01010101u) << 4;
+            }
+        }
+        int sc0, m0, sc1, m1;
+        scale_min_k4(w.hd[1], w.hd[2], w.hd[3], 2 * g, sc0, m0);
+        scale_min_k4(w.hd[1], w.hd[2], w.hd[3], 2 * g + 1, sc1, m1);
+        const float dw = h2f(static_cast<uint16_t>(w.hd[0] & 0xffffu));
+        const float dminw = h2f(static_cast<uint16_t>(w.hd[0] >> 16));
+#pragma unroll
+        for (int v = 0; v < kMaxVec; ++v) {
+            if (v < n_vec) {
+                const int64_t base = (static_cast<int64_t>(v) * nb + ib) * kQK + 64 * g + 16 * h;
+                const u32x4 x0 = *reinterpret_cast<const u32x4 *>(xq + base);
+                const u32x4 x1 = *reinterpret_cast<const u32x4 *>(xq + base + 32);
+                int dl = 0, dh = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    dl = dot4(lo[q], x0[q], dl);
+                    dh = dot4(hi[q], x1[q], dh);
+                }
+                const int16_t * bs = xs + (v * nb + ib) * 16;
+                const int isum = sc0 * dl + sc1 * dh;
+                const int msum = m0 * bs[4 * g + h] + m1 * bs[4 * g + 2 + h];
+                const float dx = xd[v * nb + ib];
+                acc_d[v] += (dw * dx) * static_cast<float>(isum);
+                acc_m[v] += (dminw * dx) * static_cast<float>(msum);
+            }
+        }
+    }
+}
+
+// LPR lanes per row, 64 / LPR rows per wave; lane li of its row's group
+// takes the units li + LPR i (i < U) of the row's 8 nb units (unit = eighth of
+// a 256-value block, 32 weights). Per workgroup (4 waves, 4 * 64 / LPR rows):
+//   1. every lane issues the loads of its units' weight bytes (all U in flight);
+//   2. meanwhile the workgroup stages the Q8_K activations in LDS, re-laid out
+//      so that each lane's quants are aligned: xq [n_vec][256 nb] int8, then
+//      xd [n_vec][nb] float, xs [n_vec][16 nb] int16 (the bsums);
+//   3. each lane adds its units' terms; a reduction over the row's LPR lanes
+//      gives y.
+template <int TYPE, int LPR, int U>
+__global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_params p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
+    const int nb = p.nb;
+    const int k = nb * kQK;
+    int8_t * xq = reinterpret_cast<int8_t *>(lds_raw);
+    float * xd = reinterpret_cast<float *>(lds_raw + static_cast<size_t>(p.n_vec) * k);
+    int16_t * xs = reinterpret_cast<int16_t *>(xd + p.n_vec * nb);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int li = lane % LPR;
+    constexpr int kRowsPerWave = 64 / LPR;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (tid >> 6)) * kRowsPerWave + lane / LPR;
+    const bool live = row < p.rows;
+    const uint8_t * wrow = p.w + (live ? row : 0) * p.row_bytes;
+    constexpr int kBytes = TYPE == LEVO_HIP_TYPE_Q4_K ? 144 : TYPE == LEVO_HIP_TYPE_Q5_K ? 176 : 210;
+    const int units = nb * 8;
+    kq_unit<TYPE> w[U];
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+        const int unit = li + LPR * i;
+        if (live && unit < units) w[i].load(wrow + static_cast<int64_t>(unit >> 3) * kBytes, unit & 7);
+    }
+    const int nblk = p.n_vec * nb;
+    for (int e = tid; e < nblk * 73; e += kThreads) {  // 73 dwords per 292-byte block
+        const int b = e / 73, wd = e - b * 73;
+        const uint32_t v = reinterpret_cast<const uint32_t *>(p.x + static_cast<int64_t>(b) * 292)[wd];
+        if (wd == 0) {
+            xd[b] = __builtin_bit_cast(float, v);
+        } else if (wd <= 64) {
+            reinterpret_cast<uint32_t *>(xq)[b * 64 + wd - 1] = v;
+        } else {
+            reinterpret_cast<uint32_t *>(xs)[b * 8 + wd - 65] = v;
+        }
+    }
+    __syncthreads();
+    float acc_d[kMaxVec], acc_m[kMaxVec];
+#pragma unroll
+    for (int v = 0; v < kMaxVec; ++v) acc_d[v] = acc_m[v] = 0.0f;
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int unit = li + LPR * i;
+            if (unit < units) kq_compute<TYPE>(w[i], unit >> 3, unit & 7, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
+        }
+    }
+    // every lane of the wave takes part in the shuffles
+#pragma unroll
+    for (int v = 0; v < kMaxVec; ++v) {
+        if (v < p.n_vec) {
+            float sd = acc_d[v], sm = acc_m[v];
+#pragma unroll
+            for (int o = LPR / 2; o > 0; o >>= 1) {
+                sd += __shfl_xor(sd, o, 64);
+                if constexpr (TYPE != LEVO_HIP_TYPE_Q6_K) sm += __shfl_xor(sm, o, 64);
+            }
+            if (live && li == 0) p.y[v * p.y_pitch + row] = sd - sm;
+        }
+    }
+}
+
+template <int TYPE, int LPR, int U>
+int launch_mul_mat_u(const kq_params & p, size_t lds, hipStream_t st) {
+    static bool attribute_set = false;
+    if (!attribute_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+            set_error("mul_mat_kquant: cannot raise the LDS limit");
+            return LEVO_HIP_ERR_RUNTIME;
+        }
+        attribute_set = true;
+    }
+    const int64_t rows_per_block = (kThreads / 64) * (64 / LPR);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.rows, rows_per_block)));
+    mul_mat_kquant_kernel<TYPE, LPR, U><<<grid, kThreads, lds, st>>>(p);
+    return launch_status("levo_hip_mul_mat_kquant");
+}
+
+// Lanes per row and units per lane by the row's 8 nb units (k <= 16384).
+template <int TYPE>
+int launch_mul_mat(const kq_params & p, size_t lds, hipStream_t st) {
+    const int units = p.nb * 8;
+    if (units <= 64) return launch_mul_mat_u<TYPE, 16, 4>(p, lds, st);
+    if (units <= 128) return launch_mul_mat_u<TYPE, 16, 8>(p, lds, st);
+    if (units <= 256) return launch_mul_mat_u<TYPE, 32, 8>(p, lds, st);
+    return launch_mul_mat_u<TYPE, 64, 8>(p, lds, st);
+}
+
+}  // namespace
+
+bool is_kquant(levo_hip_type type) {
+    return type == LEVO_HIP_TYPE_Q4_K || type == LEVO_HIP_TYPE_Q5_K || type == LEVO_HIP_TYPE_Q6_K;
+}
+
+int64_t kquant_block_bytes(levo_hip_type type) {
+    switch (type) {
+        case LEVO_HIP_TYPE_Q4_K: return 144;
+        case LEVO_HIP_TYPE_Q5_K: return 176;
+        case LEVO_HIP_TYPE_Q6_K: return 210;
+        case LEVO_HIP_TYPE_Q8_K: return 292;
+        default: return 0;
+    }
+}
+
+// Dequantize k values (a multiple of 256) of a K-quant type; arguments checked by the caller.
+int dequantize_kquant(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type, int64_t k,
+                      hipStream_t st) {
+    const int64_t nb = k / kQK;
+    if (nb == 0) return LEVO_HIP_OK;
+    const dim3 grid(static_cast<uint32_t>(ceil_div(nb * 32, kThreads)));
+    const uint8_t * s = static_cast<const uint8_t *>(src);
+    const bool f32 = dst_type == LEVO_HIP_TYPE_F32;
+#define LEVO_DEQ(T)                                                                                         \
+    if (f32) dequantize_kquant_kernel<T, float><<<grid, kThreads, 0, st>>>(s, static_cast<float *>(dst), nb); \
+    else dequantize_kquant_kernel<T, uint16_t><<<grid, kThreads, 0, st>>>(s, static_cast<uint16_t *>(dst), nb)
+    switch (type) {
+        case LEVO_HIP_TYPE_Q4_K: LEVO_DEQ(LEVO_HIP_TYPE_Q4_K); break;
+        case LEVO_HIP_TYPE_Q5_K: LEVO_DEQ(LEVO_HIP_TYPE_Q5_K); break;
+        default: LEVO_DEQ(LEVO_HIP_TYPE_Q6_K); break;
+    }
+#undef LEVO_DEQ
+    return launch_status("levo_hip_dequantize");
+}
+
+}  // namespace levo_hip
+
+using namespace levo_hip;
+
+extern "C" int levo_hip_quantize_q8_K(const float * x, void * y, int64_t k, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(k >= 0 && k % kQK == 0, "quantize_q8_K: k must be a multiple of 256");
+    LEVO_REQUIRE(k < (int64_t{1} << 40), "quantize_q8_K: k too large");
+    if (k == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(x != nullptr && y != nullptr, "quantize_q8_K: null pointer");
+    LEVO_REQUIRE(aligned16(x), "quantize_q8_K: x must be 16-byte aligned");
+    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(y) & 3u) == 0, "quantize_q8_K: y must be 4-byte aligned");
+    const int64_t nb = k / kQK;
+    quantize_q8_K_kernel<<<static_cast<uint32_t>(ceil_div(nb, kThreads / 64)), kThreads, 0, as_hip(stream)>>>(
+            x, static_cast<uint8_t *>(y), nb);
+    return launch_status("levo_hip_quantize_q8_K");
+}
+
+extern "C" int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
+                                       int64_t y_pitch, int64_t rows, int64_t k, int64_t n_vec,
+                                       levo_hip_stream_t stream) {
+    LEVO_REQUIRE(is_kquant(type), "mul_mat_kquant: weight type must be Q4_K, Q5_K or Q6_K");
+    LEVO_REQUIRE(k > 0 && k % kQK == 0, "mul_mat_kquant: k must be a positive multiple of 256");
+    LEVO_REQUIRE(k <= 16384, "mul_mat_kquant: k must be at most 16384");
+    LEVO_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "mul_mat_kquant: bad row count");
+    LEVO_REQUIRE(n_vec >= 1 && n_vec <= kMaxVec, "mul_mat_kquant: n_vec must be 1..8");
+    LEVO_REQUIRE(y_pitch >= rows, "mul_mat_kquant: y_pitch smaller than rows");
+    const int64_t nb = k / kQK;
+    const size_t lds = static_cast<size_t>(n_vec) * nb * (kQK + sizeof(float) + 16 * sizeof(int16_t));
+    LEVO_REQUIRE(lds <= 160 * 1024, "mul_mat_kquant: n_vec * k too large for the activations in LDS");
+    if (rows == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "mul_mat_kquant: null pointer");
+    LEVO_REQUIRE(aligned16(weight), "mul_mat_kquant: weight must be 16-byte aligned");
+    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(x_blocks) & 3u) == 0, "mul_mat_kquant: x_blocks must be 4-byte aligned");
+    kq_params p;
+    p.w = static_cast<const uint8_t *>(weight);
+    p.x = static_cast<const uint8_t *>(x_blocks);
+    p.y = y;
+    p.y_pitch = y_pitch;
+    p.rows = rows;
+    p.row_bytes = nb * kquant_block_bytes(type);
+    p.nb = static_cast<int32_t>(nb);
+    p.n_vec = static_cast<int32_t>(n_vec);
+    const hipStream_t st = as_hip(stream);
+    switch (type) {
+        case LEVO_HIP_TYPE_Q4_K: return launch_mul_mat<LEVO_HIP_TYPE_Q4_K>(p, lds, st);
+        case LEVO_HIP_TYPE_Q5_K: return launch_mul_mat<LEVO_HIP_TYPE_Q5_K>(p, lds, st);
+        default: return launch_mul_mat<LEVO_HIP_TYPE_Q6_K>(p, lds, st);
+    }
+}

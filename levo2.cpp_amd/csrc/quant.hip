@@ -339,6 +339,10 @@ int launch_quant(const void * src, int64_t src_cols, int64_t src_stride, void * 
 using namespace levo_hip;
 
 extern "C" int64_t levo_hip_row_size(levo_hip_type type, int64_t n_per_row) {
+    if (const int64_t kb = kquant_block_bytes(type)) {
+        LEVO_REQUIRE(n_per_row >= 0 && n_per_row % 256 == 0, "row_size: row length must be a multiple of 256");
+        return n_per_row / 256 * kb;
+    }
     const int64_t bb = block_bytes(type);
     LEVO_REQUIRE(bb > 0, "row_size: unsupported type %d", static_cast<int>(type));
     LEVO_REQUIRE(n_per_row >= 0 && n_per_row % 32 == 0, "row_size: row length must be a multiple of 32");
@@ -393,6 +397,17 @@ extern "C" int64_t levo_hip_quantize_chunk(levo_hip_type type, const float * src
 
 extern "C" int levo_hip_dequantize(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type,
                                    int64_t k, levo_hip_stream_t stream) {
+    if (is_kquant(type)) {
+        LEVO_REQUIRE(dst_type == LEVO_HIP_TYPE_F32 || dst_type == LEVO_HIP_TYPE_F16,
+                     "dequantize: destination must be F32 or F16");
+        LEVO_REQUIRE(k >= 0 && k % 256 == 0 && k < (int64_t{1} << 40), "dequantize: k must be a multiple of 256");
+        if (k == 0) return LEVO_HIP_OK;
+        LEVO_REQUIRE(src != nullptr && dst != nullptr, "dequantize: null pointer");
+        LEVO_REQUIRE(aligned16(src), "dequantize: K-quant source must be 16-byte aligned");
+        LEVO_REQUIRE((reinterpret_cast<uintptr_t>(dst) & (dst_type == LEVO_HIP_TYPE_F16 ? 1u : 3u)) == 0,
+                     "dequantize: destination is not aligned to its element size");
+        return dequantize_kquant(type, src, dst, dst_type, k, as_hip(stream));
+    }
     LEVO_REQUIRE(type == LEVO_HIP_TYPE_Q8_0 || type == LEVO_HIP_TYPE_Q4_0,
                  "dequantize: unsupported block type %d", static_cast<int>(type));
     LEVO_REQUIRE(dst_type == LEVO_HIP_TYPE_F32 || dst_type == LEVO_HIP_TYPE_F16,

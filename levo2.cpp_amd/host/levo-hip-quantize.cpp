@@ -7,8 +7,10 @@ std::size_t row_size(levo_hip_type type, int64_t n_per_row) {
 }
 
 int64_t padded_input_columns(int64_t columns, levo_hip_type type) {
-    if (type != LEVO_HIP_TYPE_Q8_0 && type != LEVO_HIP_TYPE_Q4_0) return columns;
-    constexpr int64_t block = 32;
+    int64_t block = 0;  // ggml_blck_size of the quantized types
+    if (type == LEVO_HIP_TYPE_Q8_0 || type == LEVO_HIP_TYPE_Q4_0) block = 32;
+    if (type == LEVO_HIP_TYPE_Q4_K || type == LEVO_HIP_TYPE_Q5_K || type == LEVO_HIP_TYPE_Q6_K) block = 256;
+    if (block == 0) return columns;
     if (columns <= 0) return columns;
     return (columns + block - 1) / block * block;
 }
@@ -35,6 +37,18 @@ void mul_mat_q8_0(const void * weight, const float * x, void * x_blocks, float *
 void mul_mat_q8_0_quantized(const void * weight, const void * x_blocks, float * y, int64_t rows, int64_t k,
                             int64_t n_vec, stream_t stream) {
     check_status(levo_hip_mul_mat_q8_0(weight, x_blocks, y, rows, rows, k, n_vec, stream));
+}
+
+void mul_mat_kquant(levo_hip_type type, const void * weight, const float * x, void * x_blocks, float * y,
+                    int64_t rows, int64_t k, int64_t n_vec, stream_t stream) {
+    if (rows == 0 || n_vec == 0) return;
+    check_status(levo_hip_quantize_q8_K(x, x_blocks, n_vec * k, stream));
+    mul_mat_kquant_quantized(type, weight, x_blocks, y, rows, k, n_vec, stream);
+}
+
+void mul_mat_kquant_quantized(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
+                              int64_t rows, int64_t k, int64_t n_vec, stream_t stream) {
+    check_status(levo_hip_mul_mat_kquant(type, weight, x_blocks, y, rows, rows, k, n_vec, stream));
 }
 
 void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream) {

@@ -34,7 +34,8 @@ std::size_t quantize_rows(levo_hip_type type, const void * src, levo_hip_type sr
                           int64_t src_row_stride, void * dst, int64_t nrows, int64_t dst_cols,
                           stream_t stream = nullptr);
 
-// ggml's to_float for Q8_0 / Q4_0: k values (a multiple of 32).
+// ggml's to_float for Q8_0 / Q4_0 (k a multiple of 32) and Q4_K / Q5_K / Q6_K
+// (k a multiple of 256, src 16-byte aligned).
 void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream = nullptr);
 
 // ggml_mul_mat(W, x) for a Q8_0 weight at decode, as ggml's CPU backend
@@ -48,6 +49,19 @@ void mul_mat_q8_0(const void * weight, const float * x, void * x_blocks, float *
                   int64_t n_vec, stream_t stream = nullptr);
 void mul_mat_q8_0_quantized(const void * weight, const void * x_blocks, float * y, int64_t rows, int64_t k,
                             int64_t n_vec, stream_t stream = nullptr);
+
+// ggml_mul_mat(W, x) for a Q4_K / Q5_K / Q6_K weight at decode (the Q4_K_M,
+// Q5_K_M and Q6_K profiles' matrices, src/levo-quantization.h:47-55, 96-118),
+// as ggml's CPU backend computes it: x [n_vec][k] F32 is quantized to Q8_K
+// (the K-quants' vec_dot_type) into x_blocks (n_vec * row_size(Q8_K, k)
+// bytes, 4-byte aligned), then y [n_vec][rows] = ggml_vec_dot_q*_K_q8_K per
+// row. weight is [rows][k / 256] blocks, 16-byte aligned; k a multiple of 256
+// (padded_input_columns), 1 <= n_vec <= 8. mul_mat_kquant_quantized reuses
+// x_blocks for further matrices with the same input.
+void mul_mat_kquant(levo_hip_type type, const void * weight, const float * x, void * x_blocks, float * y,
+                    int64_t rows, int64_t k, int64_t n_vec, stream_t stream = nullptr);
+void mul_mat_kquant_quantized(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
+                              int64_t rows, int64_t k, int64_t n_vec, stream_t stream = nullptr);
 
 void fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, stream_t stream = nullptr);
 void fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n, stream_t stream = nullptr);

@@ -175,6 +175,8 @@ class LevoHip:
             "levo_hip_flow_normalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_flow_denormalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_mul_mat_q8_0": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+            "levo_hip_quantize_q8_K": (ctypes.c_int, [_P, _P, _I64, _P]),
+            "levo_hip_mul_mat_kquant": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
             "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
             "levo_hip_quantize_chunk": (_I64, [ctypes.c_int, _P, _P, _I64, _I64, _I64, _P, _P]),
             "levo_hip_quantize_rows": (_I64, [ctypes.c_int, _P, ctypes.c_int, _I64, _I64, _P, _I64, _I64, _P]),
@@ -300,6 +302,13 @@ class LevoHip:
     def mul_mat_q8_0(self, weight, x_blocks, y, y_pitch, rows, k, n_vec, stream=None):
         return self._check(self.lib.levo_hip_mul_mat_q8_0(_addr(weight), _addr(x_blocks), _addr(y), y_pitch,
                                                           rows, k, n_vec, _stream(stream)))
+
+    def quantize_q8_K(self, x, y, k, stream=None):
+        return self._check(self.lib.levo_hip_quantize_q8_K(_addr(x), _addr(y), k, _stream(stream)))
+
+    def mul_mat_kquant(self, qtype, weight, x_blocks, y, y_pitch, rows, k, n_vec, stream=None):
+        return self._check(self.lib.levo_hip_mul_mat_kquant(qtype, _addr(weight), _addr(x_blocks), _addr(y), y_pitch,
+                                                            rows, k, n_vec, _stream(stream)))
 
     def row_size(self, qtype, n):
         return self._check(self.lib.levo_hip_row_size(qtype, n))

@@ -730,6 +730,230 @@ void lo_mul_mat_q8_0(const void * w, const float * x, float * y, int64_t rows, i
 }
 
 /* ------------------------------------------------------------------------- */
+/* K-quant super-blocks (ggml public layout, QK_K = 256, little-endian):      */
+/*   block_q4_K {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}            144 B */
+/*   block_q5_K {f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]} 176 B */
+/*   block_q6_K {u8 ql[128]; u8 qh[64]; i8 scales[16]; f16 d}           210 B */
+/*   block_q8_K {f32 d; i8 qs[256]; i16 bsums[16]}                      292 B */
+/* Routed to by the Q6_K / Q5_K_M / Q4_K_M profiles                          */
+/* (src/levo-quantization.h:47-55, 96-118).                                  */
+/* ------------------------------------------------------------------------- */
+
+/* ggml's nearest_int: fval + 1.5 * 2^23 rounds to an integer (ties to even)
+ * for |fval| < 2^22, read back from the mantissa bits. */
+static int lo_nearest_int(float fval) {
+    const float val = fval + 12582912.0f;
+    int32_t i;
+    memcpy(&i, &val, sizeof(i));
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+static float lo_h(const unsigned char * p) { return lo_fp16_to_fp32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* get_scale_min_k4: sub-block j's 6-bit scale and min from the 12 packed
+ * bytes (j < 4: low 6 bits of bytes j and j + 4; j >= 4: a nibble of byte
+ * j + 4 and the top 2 bits of bytes j - 4 and j). */
+static void lo_scale_min_k4(int j, const unsigned char * q, int * d, int * m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
+    }
+}
+
+void lo_quantize_row_q8_K(const float * x, void * out, int64_t k) {
+    unsigned char * y = (unsigned char *)out;
+    const int64_t nb = k / 256;
+    for (int64_t i = 0; i < nb; ++i, x += 256) {
+        unsigned char * blk = y + i * 292;
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < 256; ++j) {
+            const float ax = fabsf(x[j]);
+            if (ax > amax) {
+                amax = ax;
+                max = x[j];
+            }
+        }
+        if (!amax) {  /* the reference leaves bsums as they were; zero here */
+            memset(blk, 0, 292);
+            continue;
+        }
+        const float iscale = -127.0f / max;
+        int8_t qs[256];
+        for (int j = 0; j < 256; ++j) {
+            const int v = lo_nearest_int(iscale * x[j]);
+            qs[j] = (int8_t)(v < 127 ? v : 127);
+        }
+        const float d = 1.0f / iscale;
+        memcpy(blk, &d, 4);
+        memcpy(blk + 4, qs, 256);
+        for (int j = 0; j < 16; ++j) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ++ii) sum += qs[j * 16 + ii];
+            const int16_t s16 = (int16_t)sum;
+            memcpy(blk + 260 + 2 * j, &s16, 2);
+        }
+    }
+}
+
+/* dequantize_row_q4_K / q5_K: y = d1 * q - m1 with d1 = d * sc, m1 = dmin * m,
+ * the last step in one rounding (fmaf), as ggml's backends are compiled
+ * (floating-point contraction on). */
+void lo_dequantize_row_q4_K(const void * in, float * y, int64_t k) {
+    const unsigned char * x = (const unsigned char *)in;
+    for (int64_t i = 0; i < k / 256; ++i) {
+        const unsigned char * blk = x + i * 144;
+        const float d = lo_h(blk), min = lo_h(blk + 2);
+        const unsigned char * sc = blk + 4;
+        const unsigned char * q = blk + 16;
+        for (int j = 0; j < 4; ++j, q += 32) {
+            int s0, m0, s1, m1;
+            lo_scale_min_k4(2 * j, sc, &s0, &m0);
+            lo_scale_min_k4(2 * j + 1, sc, &s1, &m1);
+            const float d1 = d * (float)s0, mn1 = min * (float)m0;
+            const float d2 = d * (float)s1, mn2 = min * (float)m1;
+            for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float)(q[l] & 0xF), -mn1);
+            for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float)(q[l] >> 4), -mn2);
+        }
+    }
+}
+
+void lo_dequantize_row_q5_K(const void * in, float * y, int64_t k) {
+    const unsigned char * x = (const unsigned char *)in;
+    for (int64_t i = 0; i < k / 256; ++i) {
+        const unsigned char * blk = x + i * 176;
+        const float d = lo_h(blk), min = lo_h(blk + 2);
+        const unsigned char * sc = blk + 4;
+        const unsigned char * qh = blk + 16;
+        const unsigned char * ql = blk + 48;
+        unsigned u1 = 1, u2 = 2;
+        for (int j = 0; j < 4; ++j, ql += 32, u1 <<= 2, u2 <<= 2) {
+            int s0, m0, s1, m1;
+            lo_scale_min_k4(2 * j, sc, &s0, &m0);
+            lo_scale_min_k4(2 * j + 1, sc, &s1, &m1);
+            const float d1 = d * (float)s0, mn1 = min * (float)m0;
+            const float d2 = d * (float)s1, mn2 = min * (float)m1;
+            for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float)((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)), -mn1);
+            for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)), -mn2);
+        }
+    }
+}
+
+/* Q6_K element e of a block: 6-bit code (low 4 bits in ql, high 2 in qh) - 32. */
+static int lo_q6_code(const unsigned char * blk, int e) {
+    const int n = e / 128, r = e % 128, quarter = r / 32, l = r % 32;
+    const unsigned char * ql = blk + 64 * n;
+    const unsigned char * qh = blk + 128 + 32 * n;
+    const int lo = quarter & 1 ? ql[l + 32] : ql[l];
+    const int nib = quarter < 2 ? (lo & 0xF) : (lo >> 4);
+    return (nib | (((qh[l] >> (2 * quarter)) & 3) << 4)) - 32;
+}
+
+void lo_dequantize_row_q6_K(const void * in, float * y, int64_t k) {
+    const unsigned char * x = (const unsigned char *)in;
+    for (int64_t i = 0; i < k / 256; ++i) {
+        const unsigned char * blk = x + i * 210;
+        const float d = lo_h(blk + 208);
+        const int8_t * sc = (const int8_t *)(blk + 192);
+        /* y = d * sc * q, left to right (two roundings) */
+        for (int e = 0; e < 256; ++e) *y++ = d * (float)sc[e / 16] * (float)lo_q6_code(blk, e);
+    }
+}
+
+/* ggml_vec_dot_q{4,5,6}_K_q8_K, generic loops: per super-block the integer
+ * sums of scale * (q_w * q_x) in 8 lanes (element l goes to lane l % 8), then
+ * sums[lane] += (d_w * d_x) * aux32[lane]; for Q4_K / Q5_K also
+ * sumi = sum_j bsums[j] * min[j / 2] and sumf -= (dmin_w * d_x) * sumi; at
+ * the end sumf += sums[0..7] in order. */
+static float lo_vec_dot_kquant(int type, const unsigned char * w, const unsigned char * xq, int64_t nb) {
+    float sums[8] = {0};
+    float sumf = 0.0f;
+    const int wbytes = type == LO_TYPE_Q4_K ? 144 : type == LO_TYPE_Q5_K ? 176 : 210;
+    for (int64_t i = 0; i < nb; ++i) {
+        const unsigned char * blk = w + i * wbytes;
+        const unsigned char * bx = xq + i * 292;
+        float dx;
+        memcpy(&dx, bx, 4);
+        const int8_t * q8 = (const int8_t *)(bx + 4);
+        int a[256];
+        int scales[16];
+        int mins[8] = {0};
+        if (type == LO_TYPE_Q6_K) {
+            for (int e = 0; e < 256; ++e) a[e] = lo_q6_code(blk, e);
+            for (int j = 0; j < 16; ++j) scales[j] = ((const int8_t *)(blk + 192))[j];
+        } else {
+            const unsigned char * sc = blk + 4;
+            const unsigned char * qh = blk + 16;
+            const unsigned char * ql = blk + (type == LO_TYPE_Q5_K ? 48 : 16);
+            for (int j = 0; j < 4; ++j) {
+                for (int l = 0; l < 32; ++l) {
+                    a[64 * j + l] = ql[32 * j + l] & 0xF;
+                    a[64 * j + 32 + l] = ql[32 * j + l] >> 4;
+                    if (type == LO_TYPE_Q5_K) {
+                        a[64 * j + l] += (qh[l] >> (2 * j)) & 1 ? 16 : 0;
+                        a[64 * j + 32 + l] += (qh[l] >> (2 * j + 1)) & 1 ? 16 : 0;
+                    }
+                }
+            }
+            for (int j = 0; j < 8; ++j) lo_scale_min_k4(j, sc, &scales[j], &mins[j]);
+        }
+        const int sub = type == LO_TYPE_Q6_K ? 16 : 32;  /* elements per scale */
+        int32_t aux32[8] = {0};
+        for (int e = 0; e < 256; ++e) aux32[e % 8] += scales[e / sub] * (int16_t)(q8[e] * a[e]);
+        const float d = (type == LO_TYPE_Q6_K ? lo_h(blk + 208) : lo_h(blk)) * dx;
+        for (int l = 0; l < 8; ++l) sums[l] += d * (float)aux32[l];
+        if (type != LO_TYPE_Q6_K) {
+            int sumi = 0;
+            for (int j = 0; j < 16; ++j) {
+                int16_t b;
+                memcpy(&b, bx + 260 + 2 * j, 2);
+                sumi += b * mins[j / 2];
+            }
+            const float dmin = lo_h(blk + 2) * dx;
+            sumf -= dmin * (float)sumi;
+        }
+    }
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+int64_t lo_kquant_block_bytes(int type) {
+    switch (type) {
+        case LO_TYPE_Q4_K: return 144;
+        case LO_TYPE_Q5_K: return 176;
+        case LO_TYPE_Q6_K: return 210;
+        case LO_TYPE_Q8_K: return 292;
+        default: return 0;
+    }
+}
+
+void lo_dequantize_row_kquant(int type, const void * x, float * y, int64_t k) {
+    if (type == LO_TYPE_Q4_K) lo_dequantize_row_q4_K(x, y, k);
+    else if (type == LO_TYPE_Q5_K) lo_dequantize_row_q5_K(x, y, k);
+    else if (type == LO_TYPE_Q6_K) lo_dequantize_row_q6_K(x, y, k);
+}
+
+float lo_vec_dot_kquant_q8_K(int type, const void * w, const void * xq, int64_t k) {
+    return lo_vec_dot_kquant(type, (const unsigned char *)w, (const unsigned char *)xq, k / 256);
+}
+
+void lo_mul_mat_kquant(int type, const void * w, const float * x, float * y, int64_t rows, int64_t k,
+                       int64_t n_vec) {
+    const int64_t nb = k / 256;
+    const int64_t wrow = nb * lo_kquant_block_bytes(type);
+    unsigned char * xq = (unsigned char *)malloc((size_t)(nb * 292));
+    if (!xq) return;
+    for (int64_t v = 0; v < n_vec; ++v) {
+        lo_quantize_row_q8_K(x + v * k, xq, k);
+        for (int64_t r = 0; r < rows; ++r)
+            y[v * rows + r] = lo_vec_dot_kquant(type, (const unsigned char *)w + r * wrow, xq, nb);
+    }
+    free(xq);
+}
+
+/* ------------------------------------------------------------------------- */
 /* Conv1d (im2col + F32 mul_mat + bias), stride 1                            */
 /* ------------------------------------------------------------------------- */
 

@@ -39,6 +39,13 @@
  *   lo_mul_mat_q8_0 ...................... float64 sum of the same block terms within the
  *                                          sequential-sum error bound; integer-valued
  *                                          blocks (d = 1) equal the exact integer product
+ *   lo_quantize_row_q8_K ................. invariants (code range, bsums, extreme -> -127),
+ *                                          exact recovery of representable rows, zero block
+ *   lo_dequantize_row_kquant ............. blocks packed from the published layout by an
+ *                                          independent packer: every value exact
+ *   lo_vec_dot_kquant_q8_K /
+ *   lo_mul_mat_kquant .................... integer-valued blocks exactly; float64 dot of
+ *                                          the dequantized operands within the bound
  */
 #ifndef LEVO_ORACLE_H
 #define LEVO_ORACLE_H
@@ -61,7 +68,8 @@ enum {
 };
 
 /* ggml_type numbering for the block formats (ggml.h public enum). */
-enum { LO_TYPE_F32 = 0, LO_TYPE_F16 = 1, LO_TYPE_Q4_0 = 2, LO_TYPE_Q8_0 = 8 };
+enum { LO_TYPE_F32 = 0, LO_TYPE_F16 = 1, LO_TYPE_Q4_0 = 2, LO_TYPE_Q8_0 = 8,
+       LO_TYPE_Q4_K = 12, LO_TYPE_Q5_K = 13, LO_TYPE_Q6_K = 14, LO_TYPE_Q8_K = 15 };
 
 /* ---- F16 <-> F32 (ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row,
  *      tools/levo-quantize.cpp:358,369; IEEE binary16, round-to-nearest-even) */
@@ -186,6 +194,21 @@ void lo_mul_mat_q8_0(const void * w, const float * x, float * y, int64_t rows, i
 
 /* ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, NULL).
  * Returns bytes written or 0 for an unsupported type. */
+/* ---- K-quants (ggml quantize_row_q8_K_ref, dequantize_row_q{4,5,6}_K,
+ *      ggml_vec_dot_q{4,5,6}_K_q8_K generic loops; the Q6_K / Q5_K_M / Q4_K_M
+ *      profiles' matrices, src/levo-quantization.h:47-55, 96-118). k is a
+ *      multiple of 256. The Q4_K / Q5_K dequantizers round d1 * q - m1 once
+ *      (fmaf), as ggml's backends are compiled; Q8_K blocks of zeros get zero
+ *      bsums. */
+int64_t lo_kquant_block_bytes(int type);
+void lo_quantize_row_q8_K(const float * x, void * y, int64_t k);
+void lo_dequantize_row_kquant(int type, const void * x, float * y, int64_t k);
+float lo_vec_dot_kquant_q8_K(int type, const void * w, const void * xq, int64_t k);
+/* ggml CPU mul_mat of K-quant rows [rows][k / 256] by x [n_vec][k] (each
+ * vector quantized to Q8_K first) -> y [n_vec][rows]. */
+void lo_mul_mat_kquant(int type, const void * w, const float * x, float * y, int64_t rows, int64_t k,
+                       int64_t n_vec);
+
 size_t lo_quantize_chunk(int type, const float * src, void * dst, int64_t start, int64_t nrows,
                          int64_t n_per_row);
 /* write_tensor's per-chunk path (tools/levo-quantize.cpp:355-388): widen F16

@@ -21,6 +21,8 @@ _I64 = ctypes.c_int64
 _F = ctypes.c_float
 
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0 = 0, 1, 2, 8
+TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_K = 12, 13, 14, 15
+KQUANT_BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_K: 292}
 BLOCK_BYTES = {TYPE_Q8_0: 34, TYPE_Q4_0: 18}
 
 
@@ -75,6 +77,10 @@ class Oracle:
             "lo_conv_transpose1d_f32": (None, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P]),
             "lo_dequantize_row_q4_0": (None, [_P, _P, _I64]),
             "lo_gaussian_noise": (None, [_P, _I64, ctypes.c_uint64]),
+            "lo_quantize_row_q8_K": (None, [_P, _P, _I64]),
+            "lo_dequantize_row_kquant": (None, [ctypes.c_int, _P, _P, _I64]),
+            "lo_vec_dot_kquant_q8_K": (_F, [ctypes.c_int, _P, _P, _I64]),
+            "lo_mul_mat_kquant": (None, [ctypes.c_int, _P, _P, _P, _I64, _I64, _I64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -247,6 +253,32 @@ class Oracle:
         x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
         y = np.empty((x.shape[0], rows), dtype=np.float32)
         self.lib.lo_mul_mat_q8_0(_ptr(w_blocks), _ptr(x), _ptr(y), rows, k, x.shape[0])
+        return y
+
+    def quantize_q8_K(self, x: np.ndarray) -> np.ndarray:
+        """quantize_row_q8_K_ref over x (a multiple of 256 values) -> 292-byte blocks."""
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        out = np.empty(x.size // 256 * 292, dtype=np.uint8)
+        self.lib.lo_quantize_row_q8_K(_ptr(x), _ptr(out), x.size)
+        return out
+
+    def dequantize_kquant(self, qtype, blocks: np.ndarray, count: int) -> np.ndarray:
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        y = np.empty(count, dtype=np.float32)
+        self.lib.lo_dequantize_row_kquant(qtype, _ptr(blocks), _ptr(y), count)
+        return y
+
+    def vec_dot_kquant(self, qtype, w_blocks: np.ndarray, x_blocks: np.ndarray, k: int) -> float:
+        w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+        x_blocks = np.ascontiguousarray(x_blocks, dtype=np.uint8)
+        return float(self.lib.lo_vec_dot_kquant_q8_K(qtype, _ptr(w_blocks), _ptr(x_blocks), k))
+
+    def mul_mat_kquant(self, qtype, w_blocks: np.ndarray, x: np.ndarray, rows: int, k: int) -> np.ndarray:
+        """ggml CPU mul_mat of K-quant rows [rows][k/256] by x [n_vec][k] -> [n_vec][rows]."""
+        w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+        y = np.empty((x.shape[0], rows), dtype=np.float32)
+        self.lib.lo_mul_mat_kquant(qtype, _ptr(w_blocks), _ptr(x), _ptr(y), rows, k, x.shape[0])
         return y
 
     def dequantize(self, qtype, blocks: np.ndarray, count: int) -> np.ndarray:

@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstring>
 #include <iostream>
 #include <vector>
 
@@ -298,6 +299,67 @@ void mul_mat_surface() {
     });
 }
 
+// K-quant decode path: padded_input_columns for 256-value blocks
+// (src/levo-quantization.h:120-130), dequantize_row bit-exact on random
+// blocks, and mul_mat_kquant exact on integer-valued blocks (d = dmin = 1,
+// Q8_K d = 1), all against the oracle.
+void kquant_surface() {
+    CHECK(padded_input_columns(2200, LEVO_HIP_TYPE_Q4_K) == 2304);
+    CHECK(padded_input_columns(4400, LEVO_HIP_TYPE_Q6_K) == 4608);
+    CHECK(padded_input_columns(2304, LEVO_HIP_TYPE_Q5_K) == 2304);
+    const uint16_t one = 0x3C00, small = 0x1400;  // F16 1.0 and 2^-10
+    for (levo_hip_type type : {LEVO_HIP_TYPE_Q4_K, LEVO_HIP_TYPE_Q5_K, LEVO_HIP_TYPE_Q6_K}) {
+        const std::size_t bb = row_size(type, 256);
+        const int64_t rows = 24, k = 1536, nb = rows * k / 256;
+        std::vector<uint8_t> wb(bb * static_cast<std::size_t>(nb));
+        uint64_t state = 0x9E3779B97F4A7C15ULL + static_cast<uint64_t>(type);
+        for (auto & b : wb) {
+            state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+            b = static_cast<uint8_t>(state >> 56);
+        }
+        for (int64_t i = 0; i < nb; ++i) {  // finite scales
+            uint8_t * blk = wb.data() + static_cast<std::size_t>(i) * bb;
+            if (type == LEVO_HIP_TYPE_Q6_K) {
+                std::memcpy(blk + 208, &small, 2);
+            } else {
+                std::memcpy(blk, &small, 2);
+                std::memcpy(blk + 2, &small, 2);
+            }
+        }
+        std::vector<float> want(static_cast<std::size_t>(rows * k));
+        lo_dequantize_row_kquant(type, wb.data(), want.data(), rows * k);
+        device_vec<uint8_t> dw(wb);
+        device_vec<float> dq(static_cast<std::size_t>(rows * k));
+        dequantize_row(type, dw.data(), dq.data(), rows * k);
+        const std::vector<float> got = dq.get();
+        CHECK(bit_equal(got.data(), want.data(), got.size()));
+
+        for (int64_t i = 0; i < nb; ++i) {  // integer-valued blocks
+            uint8_t * blk = wb.data() + static_cast<std::size_t>(i) * bb;
+            if (type == LEVO_HIP_TYPE_Q6_K) {
+                std::memcpy(blk + 208, &one, 2);
+            } else {
+                std::memcpy(blk, &one, 2);
+                std::memcpy(blk + 2, &one, 2);
+            }
+        }
+        std::vector<float> x(static_cast<std::size_t>(2 * k));
+        for (std::size_t i = 0; i < x.size(); ++i) {
+            x[i] = i % 256 == 0 ? -127.0F : static_cast<float>(static_cast<int>(i * 104729 % 255) - 127);
+        }
+        std::vector<float> ywant(static_cast<std::size_t>(2 * rows));
+        lo_mul_mat_kquant(type, wb.data(), x.data(), ywant.data(), rows, k, 2);
+        device_vec<uint8_t> dwi(wb), dxb(row_size(LEVO_HIP_TYPE_Q8_K, k) * 2);
+        device_vec<float> dx(x), dy(static_cast<std::size_t>(2 * rows));
+        mul_mat_kquant(type, dwi.data(), dx.data(), dxb.data(), dy.data(), rows, k, 2);
+        const std::vector<float> ygot = dy.get();
+        CHECK(bit_equal(ygot.data(), ywant.data(), ygot.size()));
+    }
+    expect_throw<std::invalid_argument>("multiple of 256", [&] {
+        (void) row_size(LEVO_HIP_TYPE_Q4_K, 300);
+    });
+}
+
 } // namespace
 
 int main() {
@@ -307,6 +369,7 @@ int main() {
         norm_parity();
         quantize_surface();
         mul_mat_surface();
+        kquant_surface();
     } catch (const std::exception & e) {
         std::cerr << "unexpected exception: " << e.what() << '\n';
         return 1;

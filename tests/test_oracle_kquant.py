@@ -1,0 +1,195 @@
+"""Pins of the oracle's K-quant restatement (ggml quantize_row_q8_K_ref,
+dequantize_row_q{4,5,6}_K, ggml_vec_dot_q{4,5,6}_K_q8_K; the Q6_K, Q5_K_M and
+Q4_K_M profiles' matrices, src/levo-quantization.h:47-55, 96-118).
+
+The reference's tests hold no K-quant vectors (tests/test-quantization.cpp
+checks profile parsing and type routing only) and ggml is an un-vendored
+submodule, so the oracle is pinned by construction: blocks are packed here
+from the published block layout (an independent packer, the inverse of the
+format's unpacking) with chosen integer codes and exactly representable
+scales, so every dequantized value and every dot product has an exact
+expected value; Q8_K by its invariants and exact recovery of representable
+rows; the floating-point dot products against float64 within the
+sequential-sum error bound.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+Q4_K, Q5_K, Q6_K, Q8_K = 12, 13, 14, 15
+
+
+def f16_bytes(v):
+    return np.array([v], dtype=np.float16).view(np.uint8)
+
+
+def pack_scales_k4(sc, mn):
+    """12 bytes holding eight 6-bit scales and mins (j < 4 in the low 6 bits of
+    bytes j and j + 4; j >= 4 as nibbles of byte j + 4 plus the top 2 bits of
+    bytes j - 4 and j)."""
+    b = np.zeros(12, np.uint8)
+    for j in range(4):
+        b[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        b[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        b[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    return b
+
+
+def pack_q4_K(d, dmin, sc, mn, codes):
+    qs = np.zeros(128, np.uint8)
+    for g in range(4):
+        qs[32 * g:32 * g + 32] = codes[64 * g:64 * g + 32] | (codes[64 * g + 32:64 * g + 64] << 4)
+    return np.concatenate([f16_bytes(d), f16_bytes(dmin), pack_scales_k4(sc, mn), qs])
+
+
+def pack_q5_K(d, dmin, sc, mn, codes):
+    lo = codes & 15
+    qs = np.zeros(128, np.uint8)
+    qh = np.zeros(32, np.uint8)
+    for g in range(4):
+        qs[32 * g:32 * g + 32] = lo[64 * g:64 * g + 32] | (lo[64 * g + 32:64 * g + 64] << 4)
+        qh |= ((codes[64 * g:64 * g + 32] >> 4) << (2 * g)).astype(np.uint8)
+        qh |= ((codes[64 * g + 32:64 * g + 64] >> 4) << (2 * g + 1)).astype(np.uint8)
+    return np.concatenate([f16_bytes(d), f16_bytes(dmin), pack_scales_k4(sc, mn), qh, qs])
+
+
+def pack_q6_K(d, sc, codes):
+    """codes in [-32, 31], 16 int8 scales."""
+    c = (codes + 32).astype(np.uint8)
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for n in range(2):
+        b = c[128 * n:128 * n + 128]
+        ql[64 * n:64 * n + 32] = (b[0:32] & 15) | ((b[64:96] & 15) << 4)
+        ql[64 * n + 32:64 * n + 64] = (b[32:64] & 15) | ((b[96:128] & 15) << 4)
+        qh[32 * n:32 * n + 32] = (b[0:32] >> 4) | ((b[32:64] >> 4) << 2) | ((b[64:96] >> 4) << 4) | ((b[96:128] >> 4) << 6)
+    return np.concatenate([ql, qh, np.asarray(sc, np.int8).view(np.uint8), f16_bytes(d)])
+
+
+def random_block(qtype, rng, d=0.5, dmin=0.25):
+    """A block with exact-valued fields and its expected dequantized values (float64)."""
+    if qtype == Q6_K:
+        sc = rng.integers(-128, 128, 16)
+        codes = rng.integers(-32, 32, 256)
+        want = d * np.repeat(sc, 16) * codes
+        return pack_q6_K(d, sc, codes), want
+    top = 16 if qtype == Q4_K else 32
+    sc = rng.integers(0, 64, 8)
+    mn = rng.integers(0, 64, 8)
+    codes = rng.integers(0, top, 256).astype(np.uint8)
+    want = d * np.repeat(sc, 32) * codes - dmin * np.repeat(mn, 32)
+    pack = pack_q4_K if qtype == Q4_K else pack_q5_K
+    return pack(d, dmin, sc, mn, codes), want
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+def test_dequantize_known_blocks(oracle, qtype):
+    """Every value of blocks packed from chosen codes, 6-bit (or int8) scales
+    and mins, d = 0.5, dmin = 0.25: exact."""
+    rng = np.random.default_rng(qtype)
+    blocks, want = zip(*(random_block(qtype, rng) for _ in range(12)))
+    got = oracle.dequantize_kquant(qtype, np.concatenate(blocks), 256 * 12)
+    assert np.array_equal(got.astype(np.float64), np.concatenate(want))
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K])
+def test_scale_packing_extremes(oracle, qtype):
+    """All-63 and alternating 6-bit fields exercise every packed bit."""
+    codes = np.full(256, 1, np.uint8)
+    for sc, mn in ((np.full(8, 63), np.full(8, 63)), (np.arange(8) * 9, 63 - np.arange(8) * 9),
+                   (np.array([0, 63, 16, 47, 32, 31, 48, 15]), np.array([63, 0, 47, 16, 31, 32, 15, 48]))):
+        pack = pack_q4_K if qtype == Q4_K else pack_q5_K
+        got = oracle.dequantize_kquant(qtype, pack(1.0, 1.0, sc, mn, codes), 256)
+        assert np.array_equal(got, (np.repeat(sc, 32) - np.repeat(mn, 32)).astype(np.float32))
+
+
+def test_q8_K_invariants_and_exact_rows(oracle):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(256 * 8) * 3).astype(np.float32)
+    b = oracle.quantize_q8_K(x).reshape(8, 292)
+    for i in range(8):
+        d = b[i, :4].view(np.float32)[0]
+        qs = b[i, 4:260].view(np.int8).astype(np.int64)
+        bs = b[i, 260:292].view(np.int16)
+        xi = x[256 * i:256 * i + 256]
+        assert qs.min() >= -127 and qs.max() <= 127
+        assert np.array_equal(bs, qs.reshape(16, 16).sum(1))
+        j = np.argmax(np.abs(xi))
+        assert qs[j] == -127  # iscale = -127 / max maps the extreme value to -127
+        assert np.all(np.abs(xi.astype(np.float64) - d * qs) <= abs(d) * (0.5 + 1e-5))
+    # exactly representable rows come back exactly: x = s * n with a single
+    # extreme n = -127 (the signed max), so iscale = 1 / s, d = s, codes = n;
+    # with the extreme at +127 instead, d = -s and the codes are -n
+    n = rng.integers(-126, 127, 256)
+    for sign in (-1, 1):
+        n[17] = 127 * sign
+        for s in (0.125, 2.0 ** -10, 64.0):
+            blk = oracle.quantize_q8_K((n * s).astype(np.float32))
+            assert blk[:4].view(np.float32)[0] == -sign * s
+            assert np.array_equal(blk[4:260].view(np.int8), -sign * n)
+    zero = oracle.quantize_q8_K(np.zeros(256, np.float32))
+    assert not zero.any()
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+def test_vec_dot_integer_blocks_exact(oracle, qtype):
+    """d_w = 1 (and dmin = 1), d_x = 1: the dot product is an exact integer,
+    equal to the float64 sum over the dequantized values."""
+    rng = np.random.default_rng(20 + qtype)
+    nb = 6
+    blocks, wvals = [], []
+    for _ in range(nb):
+        blk, want = random_block(qtype, rng, d=1.0, dmin=1.0)
+        blocks.append(blk)
+        wvals.append(want)
+    w = np.concatenate(blocks)
+    xq = rng.integers(-127, 128, 256 * nb)
+    xb = np.zeros((nb, 292), np.uint8)
+    for i in range(nb):
+        xb[i, :4] = np.array([1.0], np.float32).view(np.uint8)
+        xb[i, 4:260] = xq[256 * i:256 * i + 256].astype(np.int8).view(np.uint8)
+        xb[i, 260:292] = xq[256 * i:256 * i + 256].reshape(16, 16).sum(1).astype(np.int16).view(np.uint8)
+    want = float(np.dot(np.concatenate(wvals), xq.astype(np.float64)))
+    assert abs(want) < 2 ** 24
+    assert oracle.vec_dot_kquant(qtype, w, xb.ravel(), 256 * nb) == want
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+def test_vec_dot_against_float64(oracle, qtype):
+    """Random f16 scales and real activations: within the sequential-sum bound
+    of the float64 dot product of the dequantized operands."""
+    rng = np.random.default_rng(40 + qtype)
+    nb = 8
+    blocks = []
+    for _ in range(nb):
+        blk, _ = random_block(qtype, rng)
+        blk[-2:] = f16_bytes(rng.uniform(1e-3, 2e-2)) if qtype == Q6_K else blk[-2:]
+        if qtype != Q6_K:
+            blk[0:2] = f16_bytes(rng.uniform(1e-3, 2e-2))
+            blk[2:4] = f16_bytes(rng.uniform(1e-3, 2e-2))
+        blocks.append(blk)
+    w = np.concatenate(blocks)
+    x = rng.standard_normal(256 * nb).astype(np.float32)
+    xb = oracle.quantize_q8_K(x)
+    wd = oracle.dequantize_kquant(qtype, w, 256 * nb).astype(np.float64)
+    xd = np.concatenate([xb.reshape(nb, 292)[i, :4].view(np.float32)[0] *
+                         xb.reshape(nb, 292)[i, 4:260].view(np.int8).astype(np.float64) for i in range(nb)])
+    want = float(np.dot(wd, xd))
+    got = oracle.vec_dot_kquant(qtype, w, xb, 256 * nb)
+    bound = 64 * np.finfo(np.float32).eps * float(np.abs(wd * xd).sum())
+    assert abs(got - want) <= bound, (got, want, bound)
+
+
+def test_mul_mat_kquant_is_vec_dot_per_row(oracle):
+    rng = np.random.default_rng(77)
+    rows, k = 5, 512
+    for qtype in (Q4_K, Q5_K, Q6_K):
+        w = np.concatenate([random_block(qtype, rng)[0] for _ in range(rows * k // 256)])
+        x = rng.standard_normal((2, k)).astype(np.float32)
+        y = oracle.mul_mat_kquant(qtype, w, x, rows, k)
+        nbytes = {Q4_K: 144, Q5_K: 176, Q6_K: 210}[qtype] * (k // 256)
+        for v in range(2):
+            xb = oracle.quantize_q8_K(x[v])
+            for r in range(rows):
+                assert y[v, r] == np.float32(oracle.vec_dot_kquant(qtype, w[r * nbytes:(r + 1) * nbytes], xb, k))
