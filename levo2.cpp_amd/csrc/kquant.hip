@@ -14,6 +14,7 @@
 // 12 bytes); value = d * sc * q - dmin * m. Q6_K: sixteen sub-blocks of 16
 // with int8 scales; value = d * sc * (q - 32).
 #include "common.hpp"
+#include "span_load.hpp"
 
 namespace levo_hip {
 namespace {
@@ -204,26 +205,31 @@ __global__ __launch_bounds__(kThreads) void dequantize_kquant_kernel(const uint8
 // ---- mat-vec: one wave per row, 8 lanes per super-block ----------------------
 
 constexpr int kMaxVec = 8;
+constexpr int kStageBatch = 16;  // activation dwords a thread requests at once
 
 struct kq_params {
-    const uint8_t * w;      // [rows][nb] blocks
+    const uint8_t * w;      // [rows][nb] blocks, 16-byte aligned
     const uint8_t * x;      // [n_vec][nb] block_q8_K
     float * y;              // [n_vec][y_pitch]
     int64_t y_pitch;
     int64_t rows;
     int64_t row_bytes;
+    int64_t w_bytes;        // rows * row_bytes
     int32_t nb;
     int32_t n_vec;
+    int32_t x_lds_bytes;    // staged activations, 16-byte multiple
+    int32_t stage_bytes;    // LDS bytes per wave for its weight span
 };
 
-// Raw weight registers of one unit (block ib, eighth u) of a row.
+// Registers of one unit (block ib, eighth u) of a row, read from the block's
+// bytes in the wave's LDS stage (Q6_K: `odd` when the block starts 2 mod 4).
 template <int TYPE>
 struct kq_unit;
 
 template <>
 struct kq_unit<LEVO_HIP_TYPE_Q4_K> {
     u32x4 hd, qs;  // d, dmin, scales; 16 bytes of quants (32 weights)
-    __device__ __forceinline__ void load(const uint8_t * blk, int u) {
+    __device__ __forceinline__ void load(const uint8_t * blk, int u, bool) {
         hd = *reinterpret_cast<const u32x4 *>(blk);
         qs = *reinterpret_cast<const u32x4 *>(blk + 16 + 32 * (u >> 1) + 16 * (u & 1));
     }
@@ -232,7 +238,7 @@ struct kq_unit<LEVO_HIP_TYPE_Q4_K> {
 template <>
 struct kq_unit<LEVO_HIP_TYPE_Q5_K> {
     u32x4 hd, qh, qs;
-    __device__ __forceinline__ void load(const uint8_t * blk, int u) {
+    __device__ __forceinline__ void load(const uint8_t * blk, int u, bool) {
         hd = *reinterpret_cast<const u32x4 *>(blk);
         qh = *reinterpret_cast<const u32x4 *>(blk + 16 + 16 * (u & 1));
         qs = *reinterpret_cast<const u32x4 *>(blk + 48 + 32 * (u >> 1) + 16 * (u & 1));
@@ -243,8 +249,7 @@ template <>
 struct kq_unit<LEVO_HIP_TYPE_Q6_K> {
     uint32_t a0, a1, b0, b1, h0, h1, sw0, sw1;  // ql[l], ql[l + 32], qh[l] (8 l each), scales
     uint16_t d;
-    __device__ __forceinline__ void load(const uint8_t * blk, int u) {
-        const bool odd = (reinterpret_cast<uintptr_t>(blk) & 3u) != 0;
+    __device__ __forceinline__ void load(const uint8_t * blk, int u, bool odd) {
         const int n = u >> 2, l0 = 8 * (u & 3);
         load_u32x2(blk, 64 * n + l0, odd, a0, a1);
         load_u32x2(blk, 64 * n + 32 + l0, odd, b0, b1);
@@ -337,13 +342,15 @@ __device__ __forceinline__ void kq_compute(const kq_unit<TYPE> & w, int ib, int 
 // LPR lanes per row, 64 / LPR rows per wave; lane li of its row's group
 // takes the units li + LPR i (i < U) of the row's 8 nb units (unit = eighth of
 // a 256-value block, 32 weights). Per workgroup (4 waves, 4 * 64 / LPR rows):
-//   1. every lane issues the loads of its units' weight bytes (all U in flight);
+//   1. each wave requests its rows' contiguous weight bytes with coalesced
+//      dwordx4 loads (CH chunks per lane, all in flight);
 //   2. meanwhile the workgroup stages the Q8_K activations in LDS, re-laid out
 //      so that each lane's quants are aligned: xq [n_vec][256 nb] int8, then
 //      xd [n_vec][nb] float, xs [n_vec][16 nb] int16 (the bsums);
-//   3. each lane adds its units' terms; a reduction over the row's LPR lanes
+//   3. each wave stores its span to its LDS stage area; each lane parses its
+//      units there and adds their terms; a reduction over the row's LPR lanes
 //      gives y.
-template <int TYPE, int LPR, int U>
+template <int TYPE, int LPR, int U, int CH>
 __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_params p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
     const int nb = p.nb;
@@ -353,32 +360,53 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
     int16_t * xs = reinterpret_cast<int16_t *>(xd + p.n_vec * nb);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int li = lane % LPR;
+    const int wave = tid >> 6;
+    uint8_t * stage = lds_raw + p.x_lds_bytes + wave * p.stage_bytes;
     constexpr int kRowsPerWave = 64 / LPR;
-    const int64_t row = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (tid >> 6)) * kRowsPerWave + lane / LPR;
-    const bool live = row < p.rows;
-    const uint8_t * wrow = p.w + (live ? row : 0) * p.row_bytes;
     constexpr int kBytes = TYPE == LEVO_HIP_TYPE_Q4_K ? 144 : TYPE == LEVO_HIP_TYPE_Q5_K ? 176 : 210;
-    const int units = nb * 8;
-    kq_unit<TYPE> w[U];
+    // 1. the wave's rows [row0, row0 + nrows): bytes [sb0, sb1)
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * kRowsPerWave;
+    const int64_t left = p.rows - row0;
+    const int nrows = left < kRowsPerWave ? (left > 0 ? static_cast<int>(left) : 0) : kRowsPerWave;
+    const int64_t sb0 = row0 * p.row_bytes;
+    const int64_t sb1 = sb0 + nrows * p.row_bytes;
+    u32x4 regs[CH];
+    if (nrows > 0) load_span<CH>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, lane, regs);
+    // 2. the activation blocks are dwords 0 .. 73 nblk of x (73 per 292-byte
+    //    block); kStageBatch of a thread's dwords are requested together
+    const int ndw = p.n_vec * nb * 73;
+    const uint32_t * xw = reinterpret_cast<const uint32_t *>(p.x);
+    for (int e0 = tid; e0 < ndw; e0 += kThreads * kStageBatch) {
+        uint32_t v[kStageBatch];
 #pragma unroll
-    for (int i = 0; i < U; ++i) {
-        const int unit = li + LPR * i;
-        if (live && unit < units) w[i].load(wrow + static_cast<int64_t>(unit >> 3) * kBytes, unit & 7);
-    }
-    const int nblk = p.n_vec * nb;
-    for (int e = tid; e < nblk * 73; e += kThreads) {  // 73 dwords per 292-byte block
-        const int b = e / 73, wd = e - b * 73;
-        const uint32_t v = reinterpret_cast<const uint32_t *>(p.x + static_cast<int64_t>(b) * 292)[wd];
-        if (wd == 0) {
-            xd[b] = __builtin_bit_cast(float, v);
-        } else if (wd <= 64) {
-            reinterpret_cast<uint32_t *>(xq)[b * 64 + wd - 1] = v;
-        } else {
-            reinterpret_cast<uint32_t *>(xs)[b * 8 + wd - 65] = v;
+        for (int j = 0; j < kStageBatch; ++j) {
+            const int e = e0 + kThreads * j;
+            v[j] = e < ndw ? xw[e] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kStageBatch; ++j) {
+            const int e = e0 + kThreads * j;
+            if (e < ndw) {
+                const int b = e / 73, wd = e - b * 73;
+                if (wd == 0) {
+                    xd[b] = __builtin_bit_cast(float, v[j]);
+                } else if (wd <= 64) {
+                    reinterpret_cast<uint32_t *>(xq)[b * 64 + wd - 1] = v[j];
+                } else {
+                    reinterpret_cast<uint32_t *>(xs)[b * 8 + wd - 65] = v[j];
+                }
+            }
         }
     }
     __syncthreads();
+    // 3. parse and sum
+    if (nrows > 0) store_span<CH>(stage, sb0 & ~int64_t{15}, sb1, lane, regs);
+    wave_lds_fence();
+    const int g = lane / LPR;
+    const int li = lane % LPR;
+    const bool live = g < nrows;
+    const int lead = static_cast<int>(sb0 & 15);
+    const int units = nb * 8;
     float acc_d[kMaxVec], acc_m[kMaxVec];
 #pragma unroll
     for (int v = 0; v < kMaxVec; ++v) acc_d[v] = acc_m[v] = 0.0f;
@@ -386,7 +414,12 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
 #pragma unroll
         for (int i = 0; i < U; ++i) {
             const int unit = li + LPR * i;
-            if (unit < units) kq_compute<TYPE>(w[i], unit >> 3, unit & 7, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
+            if (unit < units) {
+                const int off = lead + g * static_cast<int>(p.row_bytes) + (unit >> 3) * kBytes;
+                kq_unit<TYPE> w;
+                w.load(stage + off, unit & 7, (off & 2) != 0);
+                kq_compute<TYPE>(w, unit >> 3, unit & 7, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
+            }
         }
     }
     // every lane of the wave takes part in the shuffles
@@ -399,36 +432,43 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
                 sd += __shfl_xor(sd, o, 64);
                 if constexpr (TYPE != LEVO_HIP_TYPE_Q6_K) sm += __shfl_xor(sm, o, 64);
             }
-            if (live && li == 0) p.y[v * p.y_pitch + row] = sd - sm;
+            if (live && li == 0) p.y[v * p.y_pitch + row0 + g] = sd - sm;
         }
     }
 }
 
-template <int TYPE, int LPR, int U>
-int launch_mul_mat_u(const kq_params & p, size_t lds, hipStream_t st) {
+template <int TYPE, int LPR, int U, int CH>
+int launch_mul_mat_u(kq_params p, hipStream_t st) {
     static bool attribute_set = false;
     if (!attribute_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U, CH>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
             set_error("mul_mat_kquant: cannot raise the LDS limit");
             return LEVO_HIP_ERR_RUNTIME;
         }
         attribute_set = true;
     }
-    const int64_t rows_per_block = (kThreads / 64) * (64 / LPR);
+    constexpr int kRowsPerWave = 64 / LPR;
+    const int64_t span = kRowsPerWave * p.row_bytes;
+    LEVO_REQUIRE(span + 15 <= int64_t{CH} * 64 * 16, "mul_mat_kquant: row span exceeds the wave's registers");
+    p.stage_bytes = static_cast<int32_t>((span + 15 + 15) & ~int64_t{15});
+    const size_t lds = static_cast<size_t>(p.x_lds_bytes) + static_cast<size_t>(kThreads / 64) * p.stage_bytes;
+    LEVO_REQUIRE(lds <= 160 * 1024, "mul_mat_kquant: n_vec * k too large for the workgroup's LDS");
+    const int64_t rows_per_block = (kThreads / 64) * kRowsPerWave;
     const dim3 grid(static_cast<uint32_t>(ceil_div(p.rows, rows_per_block)));
-    mul_mat_kquant_kernel<TYPE, LPR, U><<<grid, kThreads, lds, st>>>(p);
+    mul_mat_kquant_kernel<TYPE, LPR, U, CH><<<grid, kThreads, lds, st>>>(p);
     return launch_status("levo_hip_mul_mat_kquant");
 }
 
-// Lanes per row and units per lane by the row's 8 nb units (k <= 16384).
+// Lanes per row, units per lane and span chunks per lane by the row's 8 nb
+// units (k <= 16384): a wave's span is 64 / LPR rows.
 template <int TYPE>
-int launch_mul_mat(const kq_params & p, size_t lds, hipStream_t st) {
+int launch_mul_mat(const kq_params & p, hipStream_t st) {
     const int units = p.nb * 8;
-    if (units <= 64) return launch_mul_mat_u<TYPE, 16, 4>(p, lds, st);
-    if (units <= 128) return launch_mul_mat_u<TYPE, 16, 8>(p, lds, st);
-    if (units <= 256) return launch_mul_mat_u<TYPE, 32, 8>(p, lds, st);
-    return launch_mul_mat_u<TYPE, 64, 8>(p, lds, st);
+    if (units <= 64) return launch_mul_mat_u<TYPE, 16, 4, 8>(p, st);
+    if (units <= 128) return launch_mul_mat_u<TYPE, 16, 8, 16>(p, st);
+    if (units <= 256) return launch_mul_mat_u<TYPE, 32, 8, 16>(p, st);
+    return launch_mul_mat_u<TYPE, 64, 8, 16>(p, st);
 }
 
 }  // namespace
@@ -494,8 +534,6 @@ extern "C" int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, 
     LEVO_REQUIRE(n_vec >= 1 && n_vec <= kMaxVec, "mul_mat_kquant: n_vec must be 1..8");
     LEVO_REQUIRE(y_pitch >= rows, "mul_mat_kquant: y_pitch smaller than rows");
     const int64_t nb = k / kQK;
-    const size_t lds = static_cast<size_t>(n_vec) * nb * (kQK + sizeof(float) + 16 * sizeof(int16_t));
-    LEVO_REQUIRE(lds <= 160 * 1024, "mul_mat_kquant: n_vec * k too large for the activations in LDS");
     if (rows == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "mul_mat_kquant: null pointer");
     LEVO_REQUIRE(aligned16(weight), "mul_mat_kquant: weight must be 16-byte aligned");
@@ -507,12 +545,15 @@ extern "C" int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, 
     p.y_pitch = y_pitch;
     p.rows = rows;
     p.row_bytes = nb * kquant_block_bytes(type);
+    p.w_bytes = rows * p.row_bytes;
     p.nb = static_cast<int32_t>(nb);
     p.n_vec = static_cast<int32_t>(n_vec);
+    p.x_lds_bytes = static_cast<int32_t>((n_vec * nb * (kQK + sizeof(float) + 16 * sizeof(int16_t)) + 15) & ~int64_t{15});
+    p.stage_bytes = 0;
     const hipStream_t st = as_hip(stream);
     switch (type) {
-        case LEVO_HIP_TYPE_Q4_K: return launch_mul_mat<LEVO_HIP_TYPE_Q4_K>(p, lds, st);
-        case LEVO_HIP_TYPE_Q5_K: return launch_mul_mat<LEVO_HIP_TYPE_Q5_K>(p, lds, st);
-        default: return launch_mul_mat<LEVO_HIP_TYPE_Q6_K>(p, lds, st);
+        case LEVO_HIP_TYPE_Q4_K: return launch_mul_mat<LEVO_HIP_TYPE_Q4_K>(p, st);
+        case LEVO_HIP_TYPE_Q5_K: return launch_mul_mat<LEVO_HIP_TYPE_Q5_K>(p, st);
+        default: return launch_mul_mat<LEVO_HIP_TYPE_Q6_K>(p, st);
     }
 }

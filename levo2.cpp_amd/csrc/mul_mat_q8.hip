@@ -24,6 +24,7 @@
 // workgroup), whose partial sums meet in LDS in wave order (LeLM's
 // ffn_down, K = 8960 / 11008).
 #include "common.hpp"
+#include "span_load.hpp"
 
 #include <algorithm>
 
@@ -49,47 +50,6 @@ struct mm_params {
     int32_t n_vec;
     int32_t stage_bytes;  // LDS bytes per wave for its weight span
 };
-
-// Coalesced loads of the 16-byte chunks covering bytes [a0, b1) of `base`
-// (a0 16-byte aligned): lane l takes chunks l, l + 64, ... A chunk that
-// would cross `limit` is read as half-words.
-__device__ __forceinline__ void load_span(const uint8_t * base, int64_t limit, int64_t a0, int64_t b1, int lane,
-                                          u32x4 (&r)[kChunksPerLane]) {
-    const int nchunks = static_cast<int>((b1 - a0 + 15) >> 4);
-#pragma unroll
-    for (int i = 0; i < kChunksPerLane; ++i) {
-        const int c = lane + 64 * i;
-        const int64_t at = a0 + 16 * static_cast<int64_t>(c);
-        if (c < nchunks) {
-            if (at + 16 <= limit) {
-                r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + at));
-            } else {
-                uint32_t h[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    h[k] = at + 2 * k + 2 <= limit ? *reinterpret_cast<const uint16_t *>(base + at + 2 * k) : 0u;
-                }
-                r[i] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ void store_span(uint8_t * stage, int64_t a0, int64_t b1, int lane,
-                                           const u32x4 (&r)[kChunksPerLane]) {
-    const int nchunks = static_cast<int>((b1 - a0 + 15) >> 4);
-#pragma unroll
-    for (int i = 0; i < kChunksPerLane; ++i) {
-        const int c = lane + 64 * i;
-        if (c < nchunks) reinterpret_cast<u32x4 *>(stage)[c] = r[i];
-    }
-}
-
-__device__ __forceinline__ void wave_lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Block at LDS byte offset `off` (even): its F16 scale and 8 quant dwords.
 // The quants start at off + 2; the dwords read from (off + 2) & ~3 hold them
@@ -149,7 +109,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
     u32x4 regs[kChunksPerLane];
     const int64_t sb0 = (row0 * p.nb + kb0) * kQ8Bytes;
     const int64_t sb1 = (row0 * p.nb + (WPR > 1 ? kb1 : static_cast<int64_t>(nrows) * p.nb)) * kQ8Bytes;
-    if (have) load_span(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, lane, regs);
+    if (have) load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, lane, regs);
 
     // 2. activation blocks -> LDS (raw, through the stage area), then
     //    unpacked to aligned quant dwords and F32 scales
@@ -186,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
     const int g = lane / LPR;
     const int li = lane % LPR;
     const int lead = static_cast<int>(sb0 & 15);
-    if (have) store_span(stage, sb0 & ~int64_t{15}, sb1, lane, regs);
+    if (have) store_span<kChunksPerLane>(stage, sb0 & ~int64_t{15}, sb1, lane, regs);
     wave_lds_fence();
     float acc[kMaxVectors];
 #pragma unroll
