@@ -179,25 +179,33 @@ def bench_ladder(torch, hip, head, dev, warmup, steps):
         sets.append(tensors)
     torch.cuda.synchronize()
 
-    def ladder(s):
+    def ladder_batch(s):  # the headline: one launch over the six shapes
+        hip.snake_beta_batch(sets[s])
+
+    def ladder_six(s):  # one launch per shape
         for x, a, b, y in sets[s]:
             hip.snake_beta(x, a, b, y)
 
-    t0 = time.perf_counter()
-    for i in range(warmup):
-        ladder(i % n_sets)
-    host_ms = (time.perf_counter() - t0) * 1e3 / max(warmup, 1) * steps
-    torch.cuda.synchronize()
-
-    def run():
-        for i in range(steps):
+    def timed(ladder):
+        t0 = time.perf_counter()
+        for i in range(warmup):
             ladder(i % n_sets)
+        host_ms = (time.perf_counter() - t0) * 1e3 / max(warmup, 1) * steps
+        torch.cuda.synchronize()
 
-    # timed region: K ladder steps back to back, events on the kernels' stream
+        def run():
+            for i in range(steps):
+                ladder(i % n_sets)
+
+        # timed region: K ladder steps back to back, events on the kernels' stream
+        ms, host = time_region(torch, head, run, host_ms)
+        if host > ms:
+            ms, host = time_region(torch, head, run, host)
+        return ms
+
+    ms_six = timed(ladder_six)
     wall0 = time.perf_counter()
-    ms_total, host = time_region(torch, head, run, host_ms)
-    if host > ms_total:
-        ms_total, host = time_region(torch, head, run, host)
+    ms_total = timed(ladder_batch)
     wall_ms = (time.perf_counter() - wall0) * 1e3
     host = [(t[0].cpu().numpy(), t[1].cpu().numpy(), t[2].cpu().numpy()) for t in sets[0]]
     # per-shape launch durations: each shape K times back to back over its own
@@ -215,7 +223,7 @@ def bench_ladder(torch, hip, head, dev, warmup, steps):
         del xs, ys
     del sets
     torch.cuda.empty_cache()
-    return dict(ms_per_step=ms_total / steps, wall_ms=wall_ms, per_shape=per_shape,
+    return dict(ms_per_step=ms_total / steps, ms_per_step_six=ms_six / steps, wall_ms=wall_ms, per_shape=per_shape,
                 ladder_bytes=per_set, host=host, n_sets=n_sets, dominant=(LADDER[-1], shape_ms[-1]))
 
 
@@ -794,6 +802,14 @@ def traffic_probe(torch, hip, binding, dev) -> None:
         y = torch.empty_like(x)
         hip.snake_beta(x, a, a, y)
         order.append((f"snake_beta_{C}x{T}", snake_bytes(C, T)))
+    jobs = []
+    for C, T in LADDER:
+        x = torch.randn((C, T), generator=g, device=dev)
+        a = torch.rand(C, generator=g, device=dev) - 0.5
+        jobs.append((x, a, a, torch.empty_like(x)))
+    hip.snake_beta_batch(jobs)
+    order.append(("snake_beta_batch_ladder", sum(snake_bytes(C, T) for C, T in LADDER)))
+    del jobs
     rows, D = 756, 2048
     xh = torch.randn((rows, D), generator=g, device=dev).half()
     dh = torch.randn((rows, D), generator=g, device=dev).half()
@@ -906,24 +922,29 @@ def main() -> int:
         return 0
     log("ladder: start")
     lad = bench_ladder(torch, hip, head, dev, args.warmup, args.steps)
-    log(f"ladder: {lad['ms_per_step']:.4f} ms/step")
-    (C, T), dom_ms = lad["dominant"]
-    dom_bytes = snake_bytes(C, T)
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    log(f"ladder: {lad['ms_per_step']:.4f} ms/step (six launches: {lad['ms_per_step_six']:.4f})")
+    # the headline's kernel: one levo_hip_snake_beta_batch launch moves the whole ladder
+    achieved = lad["ladder_bytes"] / (lad["ms_per_step"] * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBPS, 4), "traffic": None,
-                "kernel": "snake_beta_vec<float, 2>", "shape": [C, T], "algorithmic_bytes_per_launch": dom_bytes,
-                "us_per_launch": round(dom_ms * 1e3, 3)}
+                "kernel": "snake_beta_batch_kernel", "shape": LADDER,
+                "algorithmic_bytes_per_launch": lad["ladder_bytes"], "us_per_launch": round(lad["ms_per_step"] * 1e3, 3)}
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(traffic_file):
         try:
-            tr = json.load(open(traffic_file)).get("snake_beta_128x483840")
+            tr = json.load(open(traffic_file)).get("snake_beta_batch_ladder")
             if tr:
                 roofline["traffic"] = tr["hbm_bytes_per_launch"]
         except (ValueError, KeyError):
             pass
+    (C, T), dom_ms = lad["dominant"]
+    largest = {"kernel": "snake_beta_vec<float, 2>", "shape": [C, T], "us_per_launch": round(dom_ms * 1e3, 3),
+               "GB/s": round(snake_bytes(C, T) / (dom_ms * 1e-3) / 1e9, 1)}
 
-    ops = {"snake_beta_ladder_shapes": lad["per_shape"]}
+    ops = {"snake_beta_ladder_shapes": lad["per_shape"], "snake_beta_largest_shape_alone": largest,
+           "snake_beta_ladder_six_launches": {"ms_per_step": round(lad["ms_per_step_six"], 5),
+                                              "GB/s": round(lad["ladder_bytes"] / (lad["ms_per_step_six"] * 1e-3) / 1e9,
+                                                            1)}}
     if not args.no_ops:
         log("ops: snake 1 s")
         ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
@@ -970,7 +991,8 @@ def main() -> int:
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(lad["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "SnakeBeta ladder of one 10.08 s Oobleck VAE window, F32, one launch per shape",
+        "config": {"workload": "SnakeBeta ladder of one 10.08 s Oobleck VAE window, F32, one batched launch over "
+                               "the six shapes (levo_hip_snake_beta_batch)",
                    "shapes_CxT": LADDER, "elements_per_step": 72253440,
                    "algorithmic_bytes_per_step": lad["ladder_bytes"], "frac_of_8TBps": round(value / PEAK_GBPS, 4),
                    "rotated_buffer_sets": lad["n_sets"]},

@@ -71,6 +71,28 @@ int levo_hip_snake_beta(const float * x, int64_t x_stride,
                         float * y, int64_t y_stride,
                         int64_t channels, int64_t time, levo_hip_stream_t stream);
 
+/* One job of levo_hip_snake_beta_batch: the arguments of levo_hip_snake_beta. */
+typedef struct levo_hip_snake_job {
+    const float * x;
+    int64_t x_stride;
+    const void * alpha_log;
+    const void * beta_log;
+    levo_hip_type param_type;
+    float * y;
+    int64_t y_stride;
+    int64_t channels;
+    int64_t time;
+} levo_hip_snake_job;
+
+/* Up to 16 independent levo_hip_snake_beta jobs in one launch (the SnakeBeta
+ * instances of a decoder window, src/levo-vae.cpp:80-88, 94-97, 218-233):
+ * their tiles share one grid, so the small jobs run beside the large ones
+ * instead of each paying a launch and a ramp of its own. Each job computes
+ * exactly what levo_hip_snake_beta computes for it; jobs must not overlap
+ * (y may equal x within a job). Jobs the vector path cannot take (time or a
+ * stride not a multiple of 4, unaligned rows) run as separate launches. */
+int levo_hip_snake_beta_batch(const levo_hip_snake_job * jobs, int n_jobs, levo_hip_stream_t stream);
+
 /* SnakeBeta + Conv1d (stride 1) + bias + residual in one pass: the Oobleck
  * decoder's conv_1d_f32 calls (ggml_im2col + ggml_mul_mat + bias,
  * src/levo-audio-ops.cpp:56-87) with the SnakeBeta that feeds them

@@ -13,6 +13,8 @@
 #include "common.hpp"
 #include "snake_math.hpp"
 
+#include <algorithm>
+
 namespace levo_hip {
 namespace {
 
@@ -190,8 +192,137 @@ int launch_snake(const float * x, int64_t x_stride, const P * a, const P * b, fl
     return launch_status("levo_hip_snake_beta");
 }
 
+// ---- batch: independent SnakeBeta jobs in one launch -----------------------
+//
+// One workgroup per tile of 256 * kBatchVPT vectors of one job (the jobs'
+// tiles laid end to end on the grid), with the tile's channel parameters in
+// LDS as in snake_beta_vec: the small jobs' tiles run beside the large ones'
+// instead of each paying a launch and a ramp of its own.
+constexpr int kMaxBatchJobs = 16;
+constexpr int kBatchVPT = 2;
+
+struct batch_job {
+    const float * x;
+    float * y;
+    const void * alpha_log;
+    const void * beta_log;
+    int64_t x_stride;
+    int64_t y_stride;
+    fast_div div_t4;   // vectors per row
+    uint32_t total4;   // vectors of the job
+    uint32_t tile0;    // first workgroup of the job
+    int32_t param_f16;
+};
+
+struct batch_args {
+    batch_job job[kMaxBatchJobs];
+    int32_t n;
+};
+
+__device__ __forceinline__ float batch_param(const void * p, int f16, uint32_t i) {
+    return f16 ? param_f32(static_cast<const uint16_t *>(p), i) : param_f32(static_cast<const float *>(p), i);
+}
+
+__global__ __launch_bounds__(kThreads) void snake_beta_batch_kernel(const batch_args args) {
+    extern __shared__ snake_param params[];  // sized by the largest tile_param_bytes of the jobs
+    int j = 0;
+    for (int i = 1; i < args.n; ++i) {
+        if (args.job[i].tile0 <= blockIdx.x) j = i;  // tiles are in job order
+    }
+    const batch_job & b = args.job[j];
+    constexpr uint32_t tile = kThreads * kBatchVPT;
+    const uint32_t first = (blockIdx.x - b.tile0) * tile;
+    const uint32_t last = min(first + tile, b.total4) - 1;
+    const uint32_t c0 = div_of(first, b.div_t4);
+    const uint32_t c1 = div_of(last, b.div_t4);
+    for (uint32_t i = threadIdx.x; i <= c1 - c0; i += kThreads) {
+        params[i] = make_snake_param(batch_param(b.alpha_log, b.param_f16, c0 + i),
+                                     batch_param(b.beta_log, b.param_f16, c0 + i));
+    }
+    f32x4 v[kBatchVPT];
+    uint32_t ch[kBatchVPT];
+    uint32_t t4[kBatchVPT];
+#pragma unroll
+    for (int k = 0; k < kBatchVPT; ++k) {
+        const uint32_t f = first + threadIdx.x + k * kThreads;
+        ch[k] = div_of(f, b.div_t4);
+        t4[k] = f - ch[k] * b.div_t4.d;
+        if (f < b.total4) {
+            v[k] = __builtin_nontemporal_load(
+                    reinterpret_cast<const f32x4 *>(b.x + static_cast<int64_t>(ch[k]) * b.x_stride) + t4[k]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kBatchVPT; ++k) {
+        const uint32_t f = first + threadIdx.x + k * kThreads;
+        if (f < b.total4) {
+            const snake_param q = params[ch[k] - c0];
+            f32x4 r;
+            r.x = snake(v[k].x, q);
+            r.y = snake(v[k].y, q);
+            r.z = snake(v[k].z, q);
+            r.w = snake(v[k].w, q);
+            __builtin_nontemporal_store(
+                    r, reinterpret_cast<f32x4 *>(b.y + static_cast<int64_t>(ch[k]) * b.y_stride) + t4[k]);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace levo_hip
+
+extern "C" int levo_hip_snake_beta_batch(const levo_hip_snake_job * jobs, int n_jobs, levo_hip_stream_t stream) {
+    using namespace levo_hip;
+    LEVO_REQUIRE(n_jobs >= 0 && n_jobs <= kMaxBatchJobs, "snake_beta_batch: 0 to %d jobs", kMaxBatchJobs);
+    LEVO_REQUIRE(n_jobs == 0 || jobs != nullptr, "snake_beta_batch: null job list");
+    batch_args args{};
+    args.n = 0;
+    uint64_t tiles = 0;
+    size_t lds = 0;
+    for (int i = 0; i < n_jobs; ++i) {
+        const levo_hip_snake_job & jb = jobs[i];
+        LEVO_REQUIRE(jb.channels >= 0 && jb.time >= 0, "LeVo audio graph: SnakeBeta shape must be non-negative");
+        if (jb.channels == 0 || jb.time == 0) continue;
+        LEVO_REQUIRE(jb.x != nullptr && jb.y != nullptr, "LeVo audio graph: SnakeBeta input or output is null");
+        LEVO_REQUIRE(jb.alpha_log != nullptr && jb.beta_log != nullptr,
+                     "LeVo audio graph: SnakeBeta alpha_log or beta_log is null");
+        LEVO_REQUIRE(jb.param_type == LEVO_HIP_TYPE_F32 || jb.param_type == LEVO_HIP_TYPE_F16,
+                     "LeVo audio graph: SnakeBeta alpha_log must be F32 or F16");
+        LEVO_REQUIRE(jb.x_stride >= jb.time && jb.y_stride >= jb.time,
+                     "LeVo audio graph: SnakeBeta row stride is smaller than the time length");
+        LEVO_REQUIRE(jb.x != jb.y || jb.x_stride == jb.y_stride,
+                     "LeVo audio graph: in-place SnakeBeta needs equal input and output strides");
+        LEVO_REQUIRE(jb.channels * jb.time < (int64_t{1} << 31) && jb.channels < (int64_t{1} << 30),
+                     "LeVo audio graph: SnakeBeta tensor exceeds 2^31 elements");
+        const bool vec = jb.time % 4 == 0 && jb.x_stride % 4 == 0 && jb.y_stride % 4 == 0 && aligned16(jb.x) &&
+                         aligned16(jb.y);
+        if (!vec) {  // the single-job path's scalar kernel
+            const int st = levo_hip_snake_beta(jb.x, jb.x_stride, jb.alpha_log, jb.beta_log, jb.param_type, jb.y,
+                                               jb.y_stride, jb.channels, jb.time, stream);
+            if (st != LEVO_HIP_OK) return st;
+            continue;
+        }
+        batch_job & b = args.job[args.n++];
+        const uint32_t t4 = static_cast<uint32_t>(jb.time / 4);
+        b.x = jb.x;
+        b.y = jb.y;
+        b.alpha_log = jb.alpha_log;
+        b.beta_log = jb.beta_log;
+        b.x_stride = jb.x_stride;
+        b.y_stride = jb.y_stride;
+        b.div_t4 = make_fast_div(t4);
+        b.total4 = static_cast<uint32_t>(jb.channels * jb.time / 4);
+        b.tile0 = static_cast<uint32_t>(tiles);
+        b.param_f16 = jb.param_type == LEVO_HIP_TYPE_F16;
+        tiles += ceil_div(b.total4, kThreads * kBatchVPT);
+        lds = std::max(lds, tile_param_bytes(kThreads * kBatchVPT, t4, jb.channels));
+    }
+    LEVO_REQUIRE(tiles < (uint64_t{1} << 31), "snake_beta_batch: too many tiles");
+    if (args.n == 0) return LEVO_HIP_OK;
+    snake_beta_batch_kernel<<<static_cast<uint32_t>(tiles), kThreads, lds, as_hip(stream)>>>(args);
+    return launch_status("levo_hip_snake_beta_batch");
+}
 
 extern "C" int levo_hip_snake_beta(const float * x, int64_t x_stride, const void * alpha_log,
                                    const void * beta_log, levo_hip_type param_type, float * y,

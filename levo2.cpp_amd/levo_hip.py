@@ -79,6 +79,13 @@ class FlowStepArgs(ctypes.Structure):
     ]
 
 
+class SnakeJob(ctypes.Structure):
+    """levo_hip_snake_job (include/levo_hip.h)."""
+
+    _fields_ = [("x", _P), ("x_stride", _I64), ("alpha_log", _P), ("beta_log", _P), ("param_type", ctypes.c_int),
+                ("y", _P), ("y_stride", _I64), ("channels", _I64), ("time", _I64)]
+
+
 class VaeSnake(ctypes.Structure):
     _fields_ = [("alpha_log", _P), ("beta_log", _P)]
 
@@ -149,6 +156,7 @@ class LevoHip:
             "levo_hip_last_error": (ctypes.c_char_p, []),
             "levo_hip_abi_version": (ctypes.c_int, []),
             "levo_hip_snake_beta": (ctypes.c_int, [_P, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _I64, _P]),
+            "levo_hip_snake_beta_batch": (ctypes.c_int, [ctypes.POINTER(SnakeJob), ctypes.c_int, _P]),
             "levo_hip_snake_conv1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _P,
                                                      _I64, _I64, _P, _I64, _P, _I64, _P]),
             "levo_hip_conv_transpose1d_pack_weights": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P]),
@@ -206,6 +214,16 @@ class LevoHip:
         ys = y_stride if y_stride is not None else (y.stride(0) if hasattr(y, "stride") else T)
         return self._check(self.lib.levo_hip_snake_beta(_addr(x), xs, _addr(alpha_log), _addr(beta_log), param_type,
                                                         _addr(y), ys, C, T, _stream(stream)))
+
+    def snake_beta_batch(self, jobs, stream=None):
+        """jobs: (x, alpha_log, beta_log, y) tuples of [C][T] tensors, or (.., param_type)."""
+        arr = (SnakeJob * max(len(jobs), 1))()
+        for i, job in enumerate(jobs):
+            x, a, b, y = job[:4]
+            pt = job[4] if len(job) > 4 else F32
+            arr[i] = SnakeJob(_addr(x), x.stride(0), _addr(a), _addr(b), pt, _addr(y), y.stride(0), x.shape[0],
+                              x.shape[1])
+        return self._check(self.lib.levo_hip_snake_beta_batch(arr, len(jobs), _stream(stream)))
 
     def snake_conv1d(self, x, c_in, t_in, weight, c_out, kernel, *, alpha_log=None, beta_log=None, param_type=F32,
                      bias=None, padding=0, dilation=1, residual=None, y=None, x_stride=None, residual_stride=None,

@@ -106,3 +106,45 @@ def test_closed_form_float64(hip, dev, oracle):
         np.exp(b.astype(np.float64)) + 1e-9)[:, None]
     assert f32_err(_gpu(hip, dev, x, a, b), want) <= TOL
     assert math.isfinite(float(want.sum()))
+
+
+def test_batch_matches_single_launches(hip, dev, oracle):
+    """levo_hip_snake_beta_batch over the ladder's six shapes plus an F16
+    parameter job, an in-place job, a scalar-path job (T = 1001) and an empty
+    one: every output bit-identical to its own levo_hip_snake_beta launch (the
+    same arithmetic) and within the bar of the oracle."""
+    import torch
+    shapes = LADDER + [(96, 4000), (33, 1001), (64, 512), (0, 16)]
+    jobs, singles, want = [], [], []
+    for i, (C, T) in enumerate(shapes):
+        x = oracle.gaussian(C * T, 500 + i).reshape(C, T) if C else np.zeros((0, T), np.float32)
+        a, b = _params(max(C, 1), 900 + i)
+        pt = 1 if i == 6 else 0
+        if pt:
+            a, b = oracle.f32_to_f16(a), oracle.f32_to_f16(b)
+        xd, ad, bd = to_dev(x, dev), to_dev(a, dev), to_dev(b, dev)
+        yd = xd if i == 8 else torch.full_like(xd, float("nan"))  # job 8 in place
+        jobs.append((xd, ad, bd, yd, pt))
+        if C:
+            x2 = to_dev(x, dev)
+            y2 = torch.empty_like(x2)
+            hip.snake_beta(x2, ad, bd, y2, param_type=pt)
+            singles.append(from_dev(y2))
+            af, bf = (oracle.f16_to_f32(a), oracle.f16_to_f32(b)) if pt else (a, b)
+            want.append(oracle.snake_beta(x, af[:C], bf[:C], threads=16))
+    hip.snake_beta_batch(jobs)
+    torch.cuda.synchronize()
+    for (xd, ad, bd, yd, pt), single, w in zip([j for j in jobs if j[0].shape[0]], singles, want):
+        got = from_dev(yd)
+        assert np.array_equal(got.view(np.uint32), single.view(np.uint32))
+        assert f32_err(got, w) <= TOL
+
+
+def test_batch_rejects_bad_arguments(hip, dev, binding):
+    import torch
+    x = torch.zeros((4, 8), device=dev)
+    a = torch.zeros(4, device=dev)
+    with pytest.raises(binding.LevoHipError, match="0 to 16 jobs"):
+        hip.snake_beta_batch([(x, a, a, x)] * 17)
+    with pytest.raises(binding.LevoHipError, match="F32 or F16"):
+        hip.snake_beta_batch([(x, a, a, x, 8)])
