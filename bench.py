@@ -698,6 +698,19 @@ def bench_quant(torch, hip, head, dev, warmup, steps):
         out[f"{name}_dequantize_f32"] = op_entry(per_d, ms, shape=[R, Cc])
         del src, q, deq
         torch.cuda.empty_cache()
+    # the converter's F16 <-> F32 rows (ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row) at the same shape
+    per = 6 * R * Cc
+    n = math.ceil(ROTATE_BYTES / per) + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    f32 = [torch.randn((R, Cc), generator=g, device=dev) * 0.02 for _ in range(n)]
+    f16 = [torch.empty((R, Cc), dtype=torch.float16, device=dev) for _ in range(n)]
+    ms = time_op(torch, head, lambda i: hip.fp32_to_fp16_row(f32[i], f16[i], R * Cc), n, warmup, max(steps, 50))
+    out["fp32_to_fp16_row"] = op_entry(per, ms, shape=[R, Cc])
+    ms = time_op(torch, head, lambda i: hip.fp16_to_fp32_row(f16[i], f32[i], R * Cc), n, warmup, max(steps, 50))
+    out["fp16_to_fp32_row"] = op_entry(per, ms, shape=[R, Cc])
+    del f32, f16
+    torch.cuda.empty_cache()
     return out
 
 

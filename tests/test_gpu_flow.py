@@ -125,6 +125,16 @@ def test_fp16_row_converters(hip, dev, oracle):
     got, want = from_dev(out), oracle.f16_to_f32(allh)
     ok = ~np.isnan(want)
     assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32)) and np.all(np.isnan(got[~ok]))
+    # rows that start off the 16-byte grid (the scalar path) and a ragged tail
+    fd = to_dev(np.concatenate([[0], f]).astype(np.float32), dev)
+    h2 = torch.empty(f.size + 1, dtype=torch.int16, device=dev)
+    hip.fp32_to_fp16_row(fd[1:], h2[1:], f.size - 3)
+    assert np.array_equal(from_dev(h2)[1:f.size - 2].view(np.uint16), oracle.f32_to_f16(f[:f.size - 3]))
+    hd = to_dev(np.concatenate([np.zeros(1, np.uint16), allh]).view(np.int16), dev)
+    out2 = torch.empty(65537, dtype=torch.float32, device=dev)
+    hip.fp16_to_fp32_row(hd[1:], out2[1:], 65533)
+    got2 = from_dev(out2)[1:65534]
+    assert np.array_equal(got2[ok[:65533]].view(np.uint32), want[:65533][ok[:65533]].view(np.uint32))
 
 
 @pytest.mark.parametrize("n,offset", [(64 * 2520, 0), (4099, 0), (1001, 1)])
