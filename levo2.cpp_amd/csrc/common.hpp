@@ -28,6 +28,10 @@ void clear_error();
 // Checks the launch that was just enqueued.
 int launch_status(const char * what);
 
+// Raises `kernel`'s dynamic LDS limit to `bytes` on the current device, once
+// per (kernel, device); thread-safe. LEVO_HIP_OK or LEVO_HIP_ERR_RUNTIME.
+int allow_dynamic_lds(const void * kernel, int bytes, const char * what);
+
 inline hipStream_t as_hip(levo_hip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 // K-quant helpers shared by the quantizer entry points (kquant.hip).

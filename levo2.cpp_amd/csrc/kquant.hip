@@ -439,15 +439,10 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
 
 template <int TYPE, int LPR, int U, int CH>
 int launch_mul_mat_u(kq_params p, hipStream_t st) {
-    static bool attribute_set = false;
-    if (!attribute_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U, CH>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-            set_error("mul_mat_kquant: cannot raise the LDS limit");
-            return LEVO_HIP_ERR_RUNTIME;
-        }
-        attribute_set = true;
-    }
+    if (const int st = allow_dynamic_lds(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U, CH>),
+                                         160 * 1024, "levo_hip_mul_mat_kquant");
+        st != LEVO_HIP_OK)
+        return st;
     constexpr int kRowsPerWave = 64 / LPR;
     const int64_t span = kRowsPerWave * p.row_bytes;
     LEVO_REQUIRE(span + 15 <= int64_t{CH} * 64 * 16, "mul_mat_kquant: row span exceeds the wave's registers");

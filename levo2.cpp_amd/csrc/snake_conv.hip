@@ -544,17 +544,9 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
                    wgs > 256;
     const size_t lds = tiles + (p.snake ? (p.param_ring ? 2 * CI * sizeof(snake_param) : table) : 0);
     LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
-    static bool attribute_set = false;
-    if (!attribute_set) {
-        for (const void * f : {reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, false>),
-                               reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, true>)}) {
-            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 152 * 1024) != hipSuccess) {
-                set_error("snake_conv1d: cannot raise the LDS limit");
-                return LEVO_HIP_ERR_RUNTIME;
-            }
-        }
-        attribute_set = true;
-    }
+    const void * kernel = p.param_ring ? reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, true>)
+                                       : reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, false>);
+    if (const int st = allow_dynamic_lds(kernel, 152 * 1024, what); st != LEVO_HIP_OK) return st;
     const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
                     static_cast<uint32_t>(phases));
     if (p.param_ring) {

@@ -4,7 +4,10 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
+#include <set>
 #include <string>
+#include <utility>
 
 #include "common.hpp"
 
@@ -23,6 +26,24 @@ void set_error(const char * fmt, ...) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+int allow_dynamic_lds(const void * kernel, int bytes, const char * what) {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        set_error("%s: cannot query the current device", what);
+        return LEVO_HIP_ERR_RUNTIME;
+    }
+    static std::mutex mu;
+    static std::set<std::pair<const void *, int>> done;  // (kernel, device) pairs already raised
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count({kernel, device})) return LEVO_HIP_OK;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+        set_error("%s: cannot raise the LDS limit", what);
+        return LEVO_HIP_ERR_RUNTIME;
+    }
+    done.insert({kernel, device});
+    return LEVO_HIP_OK;
+}
 
 int launch_status(const char * what) {
     const hipError_t err = hipGetLastError();
