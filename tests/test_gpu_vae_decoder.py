@@ -66,6 +66,21 @@ def oracle_decode(oracle, w, latent):
     return oracle.conv1d(oracle.snake_beta(h, *w.out_act, threads=8), w.out_w, None, 3, 1, threads=8)
 
 
+def to_f16_params(oracle, w):
+    """The same weights with every SnakeBeta parameter stored as F16 (the
+    reference's F16 artifacts keep them so; they widen exactly)."""
+    narrow = lambda pair: tuple(oracle.f32_to_f16(a) for a in pair)
+    widen = lambda pair: tuple(oracle.f16_to_f32(a) for a in pair)
+    w16, w32 = Weights.__new__(Weights), Weights.__new__(Weights)
+    for dst, f in ((w16, narrow), (w32, lambda pr: widen(narrow(pr)))):
+        dst.input, dst.out_w = w.input, w.out_w
+        dst.out_act = f(w.out_act)
+        dst.stages = [dict(act=f(sg["act"]), up=sg["up"],
+                           res=[dict(pre=f(r["pre"]), conv0=r["conv0"], post=f(r["post"]), conv1=r["conv1"])
+                                for r in sg["res"]]) for sg in w.stages]
+    return w16, w32
+
+
 def device_weights(hip, binding, dev, w):
     import torch
     keep = []
@@ -98,7 +113,7 @@ def device_weights(hip, binding, dev, w):
             dr.conv_1.weight, dr.conv_1.bias = put(ru["conv1"][0]), put(ru["conv1"][1])
     dw.output_activation.alpha_log, dw.output_activation.beta_log = put(w.out_act[0]), put(w.out_act[1])
     dw.output_weight = put(w.out_w)
-    dw.param_type = 0
+    dw.param_type = 1 if w.out_act[0].dtype == np.uint16 else 0
     return dw, keep
 
 
@@ -119,6 +134,25 @@ def test_decoder_matches_oracle_chain(hip, binding, dev, oracle, frames):
     assert got.shape == (2, frames * 1920)
     assert np.isfinite(got).all()
     assert err <= 1e-4
+
+
+def test_decoder_f16_snake_parameters(hip, binding, dev, oracle):
+    """F16 SnakeBeta parameters (param_type F16) widen exactly: the decode
+    equals the oracle chain over the widened values to the same bar."""
+    import torch
+    frames = 1
+    w16, w32 = to_f16_params(oracle, Weights(binding, 4321))
+    latent = oracle.gaussian(64 * frames, 17).reshape(64, frames)
+    want = oracle_decode(oracle, w32, latent)
+    dw, keep = device_weights(hip, binding, dev, w16)
+    assert dw.param_type == 1
+    nbytes = hip.vae_decode_workspace_bytes(frames)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    audio = torch.full((2, frames * 1920), float("nan"), dtype=torch.float32, device=dev)
+    hip.vae_decode(dw, to_dev(latent, dev), frames, audio, ws, nbytes)
+    got = from_dev(audio)
+    assert np.isfinite(got).all()
+    assert f32_err(got, want) <= 1e-4
 
 
 def fill_pointers(struct, address):
