@@ -114,9 +114,10 @@ __device__ __forceinline__ void b_slot(int s, int tid, int & c, int & j) {
     j = KW == 1 ? (tid & 127) : tid + kThreads * (s / conv_chunk<KW>::CI);
 }
 
+// The weight part of a K chunk: NA float4s per thread (see conv_slots).
 template <int KW>
-__device__ __forceinline__ void load_chunk(const conv_params & p, int ci0, int co0, int64_t t0, int tid,
-                                           f32x4v (&ra)[conv_slots<KW>::NA], float (&rb)[conv_slots<KW>::NB]) {
+__device__ __forceinline__ void load_chunk_a(const conv_params & p, int ci0, int co0, int tid,
+                                             f32x4v (&ra)[conv_slots<KW>::NA]) {
     constexpr int CI = conv_slots<KW>::CI;
     const int64_t w_row = static_cast<int64_t>(p.c_in) * KW;
     const bool a_inside = p.w_vec && co0 + kMT <= p.c_out && ci0 + CI <= p.c_in;
@@ -142,6 +143,13 @@ __device__ __forceinline__ void load_chunk(const conv_params & p, int ci0, int c
         }
         ra[u] = v;
     }
+}
+
+template <int KW>
+__device__ __forceinline__ void load_chunk(const conv_params & p, int ci0, int co0, int64_t t0, int tid,
+                                           f32x4v (&ra)[conv_slots<KW>::NA], float (&rb)[conv_slots<KW>::NB]) {
+    constexpr int CI = conv_slots<KW>::CI;
+    load_chunk_a<KW>(p, ci0, co0, tid, ra);
     const int64_t tb = t0 - p.pad;
     const bool b_inside = tb >= 0 && tb + p.b_width <= p.t_in && ci0 + CI <= p.c_in;
     const float * xb = p.x + static_cast<int64_t>(ci0) * p.x_pitch + tb;
@@ -159,6 +167,16 @@ __device__ __forceinline__ void load_chunk(const conv_params & p, int ci0, int c
         }
         rb[s] = v;
     }
+}
+
+// Weight slot u of a thread into the A chunk's permuted layout.
+template <int KW>
+__device__ __forceinline__ void store_a_slot(float * As, int tid, int u, const f32x4v & v) {
+    const int e = tid + kThreads * u;
+    const int r = e % kMT;
+    const int kk = 4 * (e / kMT);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) As[a_index(kk + q, r)] = v[q];
 }
 
 // spc: the SnakeBeta parameters of this chunk's channels ci0 .. ci0 + CI - 1.
@@ -217,6 +235,86 @@ __device__ __forceinline__ void load_snake_logs(const conv_params & p, int c, fl
     if (c < p.c_in) {
         al = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.alpha_log)[c]) : static_cast<const float *>(p.alpha_log)[c];
         bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.beta_log)[c]) : static_cast<const float *>(p.beta_log)[c];
+    }
+}
+
+// The output tile goes through LDS (the A / B buffers, free after the
+// kernel's last barrier) so that bias, residual and y move as whole rows.
+// D[row][col] of a 16 x 16 tile is in lane col + 16 * (row / 4), item row % 4.
+template <bool SCATTER>
+__device__ __forceinline__ void conv_epilogue(const conv_params & p, float * lds, const f32x4v (&acc)[4][4], int tid,
+                                              int h, int vh, int g, int m, int64_t t0, int co0) {
+    float * out = lds;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                out[(h * 64 + 16 * i + 4 * g + u) * kOutStride + vh * 64 + 16 * j + m] = acc[i][j][u];
+    __syncthreads();
+    if (SCATTER && p.scatter) {
+        // transposed convolution: phase z's columns land every o_stride samples
+        const int64_t base = p.o_base + static_cast<int64_t>(blockIdx.z);
+        for (int e = tid; e < kMT * kNT; e += kThreads) {
+            const int r = e / kNT;
+            const int c = e % kNT;
+            const int co = co0 + r;
+            if (co >= p.c_out) break;  // rows only grow with e
+            const int64_t q = t0 + c;
+            const int64_t t = q * p.o_stride + base;
+            if (q >= p.t_out || t < 0 || t >= p.y_len) continue;
+            float v = out[r * kOutStride + c];
+            if (p.bias) v = v + p.bias[co];
+            p.y[co * p.y_pitch + t] = v;
+        }
+        return;
+    }
+    const bool vec = p.y_vec && t0 + kNT <= p.t_out;
+    constexpr int kOutIters = kMT * (kNT / 4) / kThreads;  // float4s of the tile per thread
+    if (vec && co0 + kMT <= p.c_out) {
+        // Whole tile inside y: the thread's residual float4s are loaded
+        // before any store (y may be the residual, so the loads cannot move
+        // past the stores on their own), then each row is finished.
+        f32x4v res[kOutIters];
+        if (p.residual) {
+#pragma unroll
+            for (int it = 0; it < kOutIters; ++it) {
+                const int e = tid + kThreads * it;
+                const int r = e / (kNT / 4);
+                const int c4 = 4 * (e % (kNT / 4));
+                res[it] = *reinterpret_cast<const f32x4v *>(p.residual + (co0 + r) * p.r_pitch + t0 + c4);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kOutIters; ++it) {
+            const int e = tid + kThreads * it;
+            const int r = e / (kNT / 4);
+            const int c4 = 4 * (e % (kNT / 4));
+            const int co = co0 + r;
+            f32x4v v = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
+            if (p.bias) v = v + p.bias[co];
+            if (p.residual) v = res[it] + v;
+            *reinterpret_cast<f32x4v *>(p.y + co * p.y_pitch + t0 + c4) = v;
+        }
+        return;
+    }
+    for (int e = tid; e < kMT * (kNT / 4); e += kThreads) {
+        const int r = e / (kNT / 4);
+        const int c4 = 4 * (e % (kNT / 4));
+        const int co = co0 + r;
+        if (co >= p.c_out) break;  // rows only grow with e
+        const float bv = p.bias ? p.bias[co] : 0.0f;
+        const f32x4v o = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
+        const int64_t t = t0 + c4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (t + q >= p.t_out) break;
+            float v = o[q];
+            if (p.bias) v = v + bv;
+            if (p.residual) v = p.residual[co * p.r_pitch + t + q] + v;
+            p.y[co * p.y_pitch + t + q] = v;
+        }
     }
 }
 
@@ -306,81 +404,7 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         buf ^= 1;
     }
 
-    // The output tile goes through LDS (the A / B buffers, free after the
-    // last barrier) so that bias, residual and y move as whole rows.
-    // D[row][col] of a 16 x 16 tile is in lane col + 16 * (row / 4), item row % 4.
-    float * out = lds;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-                out[(h * 64 + 16 * i + 4 * g + u) * kOutStride + vh * 64 + 16 * j + m] = acc[i][j][u];
-    __syncthreads();
-    if (p.scatter) {
-        // transposed convolution: phase z's columns land every o_stride samples
-        const int64_t base = p.o_base + static_cast<int64_t>(blockIdx.z);
-        for (int e = tid; e < kMT * kNT; e += kThreads) {
-            const int r = e / kNT;
-            const int c = e % kNT;
-            const int co = co0 + r;
-            if (co >= p.c_out) break;  // rows only grow with e
-            const int64_t q = t0 + c;
-            const int64_t t = q * p.o_stride + base;
-            if (q >= p.t_out || t < 0 || t >= p.y_len) continue;
-            float v = out[r * kOutStride + c];
-            if (p.bias) v = v + p.bias[co];
-            p.y[co * p.y_pitch + t] = v;
-        }
-        return;
-    }
-    const bool vec = p.y_vec && t0 + kNT <= p.t_out;
-    constexpr int kOutIters = kMT * (kNT / 4) / kThreads;  // float4s of the tile per thread
-    if (vec && co0 + kMT <= p.c_out) {
-        // Whole tile inside y: the thread's residual float4s are loaded
-        // before any store (y may be the residual, so the loads cannot move
-        // past the stores on their own), then each row is finished.
-        f32x4v res[kOutIters];
-        if (p.residual) {
-#pragma unroll
-            for (int it = 0; it < kOutIters; ++it) {
-                const int e = tid + kThreads * it;
-                const int r = e / (kNT / 4);
-                const int c4 = 4 * (e % (kNT / 4));
-                res[it] = *reinterpret_cast<const f32x4v *>(p.residual + (co0 + r) * p.r_pitch + t0 + c4);
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < kOutIters; ++it) {
-            const int e = tid + kThreads * it;
-            const int r = e / (kNT / 4);
-            const int c4 = 4 * (e % (kNT / 4));
-            const int co = co0 + r;
-            f32x4v v = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
-            if (p.bias) v = v + p.bias[co];
-            if (p.residual) v = res[it] + v;
-            *reinterpret_cast<f32x4v *>(p.y + co * p.y_pitch + t0 + c4) = v;
-        }
-        return;
-    }
-    for (int e = tid; e < kMT * (kNT / 4); e += kThreads) {
-        const int r = e / (kNT / 4);
-        const int c4 = 4 * (e % (kNT / 4));
-        const int co = co0 + r;
-        if (co >= p.c_out) break;  // rows only grow with e
-        const float bv = p.bias ? p.bias[co] : 0.0f;
-        const f32x4v o = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
-        const int64_t t = t0 + c4;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (t + q >= p.t_out) break;
-            float v = o[q];
-            if (p.bias) v = v + bv;
-            if (p.residual) v = p.residual[co * p.r_pitch + t + q] + v;
-            p.y[co * p.y_pitch + t + q] = v;
-        }
-    }
+    conv_epilogue<true>(p, lds, acc, tid, h, vh, g, m, t0, co0);
 }
 
 // ---- narrow output (c_out <= 4): the decoder's 128 -> 2 output conv -------
@@ -524,6 +548,185 @@ int launch_narrow(conv_params p, hipStream_t st, const char * what) {
     return launch_status(what);
 }
 
+// ---- k = 7 with the next chunk's staging interleaved into the MFMAs -------
+//
+// The same tile, chunks and arithmetic as snake_conv1d_kernel<7, false>, but
+// the staging of chunk n + 1 is spread over the second half of chunk n's MFMA
+// steps instead of following them: one weight slot and one input element per
+// K step, with scheduling barriers that alternate each MFMA with two VALU
+// instructions, so a single wave keeps the matrix pipe busy while it stages.
+// The input elements are spread evenly over the 256 threads as the flat index
+// e = tid + 256 s of the chunk's [CI][b_width] rows, which is also the
+// element's LDS offset (the B region is padded to 256 * NB floats, so every
+// thread stores unconditionally; NB = 5 up to dilation 5, else 6). The
+// SnakeBeta in the interleaved part is the reduced-range form only; a thread
+// with an argument beyond its range (or NaN / inf) rewrites its elements with
+// the full form before the barrier. Outputs are bit-identical to
+// snake_conv1d_kernel<7, false>.
+constexpr int kBalSlots = 6;  // at most: CI * b_width <= 1536, dilation <= 10 at k = 7
+
+__device__ __forceinline__ float snake_reduced(float x, const snake_param & q, bool & slow) {
+    const float m = x * q.alpha;
+    slow |= !(__builtin_fabsf(m) <= kSinSqFastMax);
+    return x + div_by(sin_sq_reduced(m), q.beta, q.rbeta);
+}
+
+template <int NB>
+__global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_params p) {
+    constexpr int KW = 7;
+    constexpr int CI = conv_chunk<KW>::CI;
+    constexpr int KC = conv_chunk<KW>::KC;
+    constexpr int NA = conv_slots<KW>::NA;
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    const int buf_floats = a_floats<KW>() + kThreads * NB;
+    snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);  // [c_in] when p.snake
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = wave >> 1;
+    const int vh = wave & 1;
+    const int m = lane & 15;
+    const int g = lane >> 4;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kNT;
+    const int co0 = blockIdx.y * kMT;
+    const int bw = p.b_width;
+    const int64_t tb = t0 - p.pad;
+
+    f32x4v ra[NA];
+    float rb[NB];
+    const int64_t w_row = static_cast<int64_t>(p.c_in) * KW;
+    auto load_a = [&](int ci0) {  // weight rows are 16-byte aligned (w_vec)
+#pragma unroll
+        for (int u = 0; u < NA; ++u) {
+            const int e = tid + kThreads * u;
+            const int r = e % kMT;
+            const int kk = 4 * (e / kMT);
+            const int co = co0 + r;
+            f32x4v v = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+            if (co < p.c_out && ci0 + (kk + 3) / KW < p.c_in)
+                v = *reinterpret_cast<const f32x4v *>(p.w + co * w_row + static_cast<int64_t>(ci0) * KW + kk);
+            ra[u] = v;
+        }
+    };
+    auto load_b = [&](int ci0) {
+#pragma unroll
+        for (int sl = 0; sl < NB; ++sl) {
+            const int e = tid + kThreads * sl;
+            const int c = e / bw;
+            const int64_t t = tb + (e - c * bw);
+            float v = 0.0f;
+            if (e < CI * bw && ci0 + c < p.c_in && t >= 0 && t < p.t_in) v = p.x[static_cast<int64_t>(ci0 + c) * p.x_pitch + t];
+            rb[sl] = v;
+        }
+    };
+    load_a(0);
+    load_b(0);
+    if (p.snake) {
+        for (int c = tid; c < p.c_in; c += kThreads) {
+            float al, bl;
+            load_snake_logs(p, c, al, bl);
+            sp[c] = make_snake_param(al, bl);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NA; ++u) store_a_slot<KW>(lds, tid, u, ra[u]);
+#pragma unroll
+    for (int sl = 0; sl < NB; ++sl) {
+        const int e = tid + kThreads * sl;
+        const int c = e / bw;
+        float v = rb[sl];
+        if (p.snake && e < CI * bw && c < p.c_in) v = snake(v, sp[c]);
+        lds[a_floats<KW>() + e] = v;
+    }
+    __syncthreads();
+
+    f32x4v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    int buf = 0;
+    const int cmax = p.c_in - 1;
+    for (int ci0 = 0; ci0 < p.c_in; ci0 += CI) {
+        const bool more = ci0 + CI < p.c_in;
+        // the next chunk's loads (past the last chunk they are guarded to zeros)
+        load_a(ci0 + CI);
+        load_b(ci0 + CI);
+        const float * As = lds + buf * buf_floats;
+        const float * Bs = As + a_floats<KW>();
+        f32x4v a;
+        float b[4];
+        read_operands<KW>(As, Bs, p, 0, g, h, vh, m, a, b);
+#pragma unroll
+        for (int ks = 0; ks < KC / 8; ++ks) {
+            f32x4v an = a;
+            float bn[4] = {b[0], b[1], b[2], b[3]};
+            read_operands<KW>(As, Bs, p, ks + 1, g, h, vh, m, an, bn);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            a = an;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = bn[j];
+        }
+        // second half: each K step also stages one weight slot and one input
+        // element of the next chunk into the other buffer (last read before
+        // the previous barrier); after the last chunk they go unused
+        float * An = lds + (buf ^ 1) * buf_floats;
+        float * Bn = An + a_floats<KW>();
+        bool slow = false;
+#pragma unroll
+        for (int ks = KC / 8; ks < KC / 4; ++ks) {
+            const int piece = ks - KC / 8;
+            f32x4v an = a;
+            float bn[4] = {b[0], b[1], b[2], b[3]};
+            if (ks + 1 < KC / 4) read_operands<KW>(As, Bs, p, ks + 1, g, h, vh, m, an, bn);
+            if (piece < NA) store_a_slot<KW>(An, tid, piece, ra[piece]);
+            if (piece < NB) {
+                const int e = tid + kThreads * piece;
+                const float v = rb[piece];
+                // without SnakeBeta the value is computed from table entry 0
+                // (allocated, not filled) and discarded by the select
+                const snake_param q = sp[p.snake ? min(ci0 + CI + e / bw, cmax) : 0];
+                const float sv = snake_reduced(v, q, slow);
+                Bn[e] = p.snake ? sv : v;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            // the operand reads first, then each MFMA followed by two VALU
+            // instructions, with an LDS store after every third
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+            for (int q2 = 0; q2 < 16; ++q2) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                if (q2 % 3 == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+            a = an;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = bn[j];
+        }
+        if (slow && p.snake && more) {  // rare: arguments beyond the reduced sine's range
+#pragma unroll
+            for (int sl = 0; sl < NB; ++sl) {
+                const int e = tid + kThreads * sl;
+                const int c = e / bw;
+                if (e < CI * bw && ci0 + CI + c < p.c_in) Bn[e] = snake(rb[sl], sp[ci0 + CI + c]);
+            }
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    conv_epilogue<false>(p, lds, acc, tid, h, vh, g, m, t0, co0);  // never launched with scatter
+}
+
 template <int KW>
 int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
     if (!p.scatter && p.c_out <= 4 && (KW - 1) * p.dil <= kNarrowMaxSpan) return launch_narrow<KW>(p, st, what);
@@ -544,11 +747,37 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
                    wgs > 256;
     const size_t lds = tiles + (p.snake ? (p.param_ring ? 2 * CI * sizeof(snake_param) : table) : 0);
     LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
+                    static_cast<uint32_t>(phases));
+    if constexpr (KW == 7) {
+        // one phase (the kernel applies no per-phase weight offset), and a
+        // table entry even without SnakeBeta: the kernel reads entry 0 then
+        // with the full parameter table even where the other kernel would
+        // take the ring: one workgroup per CU of this kernel outruns two of
+        // that one (measured at 1024 channels)
+        const int nb = static_cast<int>(ceil_div(CI * p.b_width, kThreads));
+        if (!p.scatter && phases == 1 && p.w_vec && nb <= kBalSlots) {
+            const int slots = nb <= 5 ? 5 : kBalSlots;
+            const size_t il = std::max(2 * static_cast<size_t>(a_floats<KW>() + kThreads * slots),
+                                       static_cast<size_t>(kMT) * kOutStride) * sizeof(float) +
+                              (p.snake ? table : sizeof(snake_param));
+            if (il <= 152 * 1024) {
+                p.param_ring = 0;
+                const void * f = slots == 5 ? reinterpret_cast<const void *>(&snake_conv1d_k7_il<5>)
+                                            : reinterpret_cast<const void *>(&snake_conv1d_k7_il<kBalSlots>);
+                if (const int st = allow_dynamic_lds(f, 152 * 1024, what); st != LEVO_HIP_OK) return st;
+                if (slots == 5) {
+                    snake_conv1d_k7_il<5><<<grid, kThreads, il, st>>>(p);
+                } else {
+                    snake_conv1d_k7_il<kBalSlots><<<grid, kThreads, il, st>>>(p);
+                }
+                return launch_status(what);
+            }
+        }
+    }
     const void * kernel = p.param_ring ? reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, true>)
                                        : reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, false>);
     if (const int st = allow_dynamic_lds(kernel, 152 * 1024, what); st != LEVO_HIP_OK) return st;
-    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
-                    static_cast<uint32_t>(phases));
     if (p.param_ring) {
         snake_conv1d_kernel<KW, true><<<grid, kThreads, lds, st>>>(p);
     } else {

@@ -9,8 +9,9 @@ where every output is one product (KAT-style identity / shift / dilation).
 Shapes: the decoder's residual units (k = 7 at dilation 1, 3, 9 with
 padding 3d; k = 1) at the last stage's 128 channels and at 1024 channels,
 the input conv 64 -> 2048 without SnakeBeta, the output conv 128 -> 2, odd
-channel counts and lengths, F16 SnakeBeta parameters, strides, and y
-written over the residual.
+channel counts and lengths, F16 SnakeBeta parameters, strides, y written
+over the residual, and inputs beyond the reduced sine's range (bit-exact
+against levo_hip_snake_beta followed by the conv without SnakeBeta).
 """
 from __future__ import annotations
 
@@ -93,6 +94,44 @@ def test_odd_shapes(hip, dev, oracle, c_in, c_out, t, kw, pad, dil):
     assert f32_err(_run(hip, dev, x, w, b, pad, dil, a, bl), _want(oracle, x, w, b, pad, dil, a, bl)) <= 1e-5
 
 
+def test_partial_chunk(hip, dev, oracle):
+    """k = 7 with 100 input channels: the last chunk of 8 holds 4 (with and
+    without SnakeBeta)."""
+    c_in, c_out, t, pad, dil = 100, 70, 517, 6, 2
+    x = oracle.gaussian(c_in * t, 140).reshape(c_in, t)
+    w = (oracle.gaussian(c_out * c_in * 7, 141) * np.float32(1.0 / np.sqrt(c_in * 7))).reshape(c_out, c_in, 7)
+    b = oracle.gaussian(c_out, 142)
+    a, bl = _params(oracle, c_in, 143)
+    assert f32_err(_run(hip, dev, x, w, b, pad, dil, a, bl), _want(oracle, x, w, b, pad, dil, a, bl)) <= 1e-5
+    assert f32_err(_run(hip, dev, x, w, b, pad, dil), _want(oracle, x, w, b, pad, dil)) <= 1e-5
+
+
+def test_large_arguments(hip, dev, oracle):
+    """Inputs whose alpha * x lies beyond the reduced-argument sine's range
+    (|alpha x| > 8192: the full sinf form) in every chunk. The fused launch
+    must equal, bit for bit, levo_hip_snake_beta followed by the same conv
+    without SnakeBeta (one accumulation order, one SnakeBeta definition).
+    Against the oracle the bar is taken on the output's scale: summands of
+    1e3 cancel to outputs near zero, where F32 sums in any two orders differ
+    by ~1e-3 absolute."""
+    import torch
+    c_in, c_out, t, pad, dil = 100, 70, 517, 6, 2
+    x = oracle.gaussian(c_in * t, 144).reshape(c_in, t)
+    x[3::7] *= np.float32(3.0e4)      # whole rows, every chunk
+    x[:, 100:103] *= np.float32(2.5e4)  # columns across all channels
+    w = (oracle.gaussian(c_out * c_in * 7, 145) * np.float32(1.0 / np.sqrt(c_in * 7))).reshape(c_out, c_in, 7)
+    b = oracle.gaussian(c_out, 146)
+    a, bl = _params(oracle, c_in, 147)
+    fused = _run(hip, dev, x, w, b, pad, dil, a, bl)
+    xs = torch.empty((c_in, t), dtype=torch.float32, device=dev)
+    hip.snake_beta(to_dev(x, dev), to_dev(a, dev), to_dev(bl, dev), xs)
+    torch.cuda.synchronize()
+    two_step = _run(hip, dev, from_dev(xs), w, b, pad, dil)
+    assert np.array_equal(fused.view(np.uint32), two_step.view(np.uint32))
+    want = _want(oracle, x, w, b, pad, dil, a, bl)
+    assert np.max(np.abs(fused.astype(np.float64) - want)) <= 1e-5 * np.max(np.abs(want))
+
+
 def test_delta_kernels_bit_exact(hip, dev, oracle):
     """Identity, one-sample delay and dilated advance: each output is one
     product with 1.0 (exact), plus the bias in its own rounding."""
@@ -140,12 +179,14 @@ def test_strides_and_in_place_residual(hip, dev, oracle):
     assert f32_err(from_dev(rs)[:, :t], want) <= 1e-5
 
 
-@pytest.mark.parametrize("c_in,t,kw,dil", [(1024, 33000, 7, 9), (1280, 33000, 1, 1)])
+@pytest.mark.parametrize("c_in,t,kw,dil", [(1021, 33000, 7, 9), (1280, 33000, 1, 1), (1024, 33000, 7, 9)])
 def test_wide_inputs_parameter_ring(hip, dev, oracle, c_in, t, kw, dil):
     """Wide inputs in a grid of more than one workgroup per CU keep only two
     chunks of SnakeBeta parameters in LDS, each computed one chunk ahead
-    (1024 channels at k = 7, dilation 9, as a 40 s window's first stage;
-    1280 channels at k = 1). 128 outputs: 258 workgroups."""
+    (1021 channels at k = 7, dilation 9: weight rows not 16-byte aligned;
+    1280 channels at k = 1). 128 outputs: 258 workgroups. With 1024
+    channels at k = 7 (a 40 s window's first stage) the interleaved kernel
+    keeps the whole table instead, one workgroup per CU."""
     pad = 3 * dil if kw == 7 else 0
     x = oracle.gaussian(c_in * t, 130 + kw).reshape(c_in, t)
     w = (oracle.gaussian(128 * c_in * kw, 131) * np.float32(1.0 / np.sqrt(c_in * kw))).reshape(128, c_in, kw)
