@@ -76,6 +76,7 @@ struct conv_params {
     // 1 = two slots of CI channels, each chunk's computed one chunk ahead (for
     // wide inputs, where the full table would cost a workgroup per CU)
     int32_t param_ring;
+    int32_t b_magic;          // ceil(2^24 / b_width): row of a flat B index by multiply
 };
 
 // LDS float index of weight (kk, r) in the A chunk: rows r = 64 h + 16 i + m
@@ -548,22 +549,38 @@ int launch_narrow(conv_params p, hipStream_t st, const char * what) {
     return launch_status(what);
 }
 
-// ---- k = 7 with the next chunk's staging interleaved into the MFMAs -------
+// ---- the next chunk's staging interleaved into the MFMAs (k = 2, 7) -------
 //
-// The same tile, chunks and arithmetic as snake_conv1d_kernel<7, false>, but
+// The same tile, chunks and arithmetic as snake_conv1d_kernel<KW, false>, but
 // the staging of chunk n + 1 is spread over the second half of chunk n's MFMA
-// steps instead of following them: one weight slot and one input element per
-// K step, with scheduling barriers that alternate each MFMA with two VALU
-// instructions, so a single wave keeps the matrix pipe busy while it stages.
-// The input elements are spread evenly over the 256 threads as the flat index
-// e = tid + 256 s of the chunk's [CI][b_width] rows, which is also the
-// element's LDS offset (the B region is padded to 256 * NB floats, so every
-// thread stores unconditionally; NB = 5 up to dilation 5, else 6). The
-// SnakeBeta in the interleaved part is the reduced-range form only; a thread
-// with an argument beyond its range (or NaN / inf) rewrites its elements with
-// the full form before the barrier. Outputs are bit-identical to
-// snake_conv1d_kernel<7, false>.
-constexpr int kBalSlots = 6;  // at most: CI * b_width <= 1536, dilation <= 10 at k = 7
+// K steps instead of following them: per K step a share of the weight slots
+// and of the input elements, with scheduling barriers that issue each of the
+// step's 16 MFMAs between VALU instructions, so a single wave keeps the matrix
+// pipe busy while it stages. The input elements are dealt evenly over the 256
+// threads by the flat index e = tid + 256 s of the chunk's [CI][b_width]
+// rows, which is also the element's LDS offset (the B region is padded to
+// 256 * NB floats, so every store is unconditional); at k = 2, e / b_width is
+// a multiply by b_magic = ceil(2^24 / b_width), exact for e < 4096 and
+// b_width in [128, 512]. The SnakeBeta in the interleaved part is the
+// reduced-argument form only; a thread with an argument beyond its range (or
+// NaN / inf) rewrites its elements with the full form before the barrier.
+// Outputs are bit-identical to snake_conv1d_kernel<KW, false>. The parameter
+// table follows the two buffers and may overlap the output tile of the
+// epilogue, which starts after the last barrier.
+template <int KW>
+struct il_shape {
+    static constexpr int CI = conv_chunk<KW>::CI;
+    static constexpr int KS = conv_chunk<KW>::KC / 4;  // K steps per chunk
+    static constexpr int P = KS / 2;                    // steps that stage
+    static constexpr int NA = conv_slots<KW>::NA;
+    static constexpr int APP = (NA + P - 1) / P;        // weight slots per staging step
+    // B slots per thread: the largest chunk ([CI][b_width] over 256 threads)
+    static constexpr int kMaxNB = KW == 2 ? 9 : 6;
+    // per MFMA of a staging step: VALU instructions, and an LDS store every
+    // kDsEvery MFMAs
+    static constexpr int kValu = KW == 7 ? 2 : 4;
+    static constexpr int kDsEvery = KW == 7 ? 3 : 2;
+};
 
 __device__ __forceinline__ float snake_reduced(float x, const snake_param & q, bool & slow) {
     const float m = x * q.alpha;
@@ -571,12 +588,18 @@ __device__ __forceinline__ float snake_reduced(float x, const snake_param & q, b
     return x + div_by(sin_sq_reduced(m), q.beta, q.rbeta);
 }
 
-template <int NB>
-__global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_params p) {
-    constexpr int KW = 7;
-    constexpr int CI = conv_chunk<KW>::CI;
-    constexpr int KC = conv_chunk<KW>::KC;
-    constexpr int NA = conv_slots<KW>::NA;
+__device__ __forceinline__ int b_row(int e, int b_magic) {
+    return static_cast<int>((static_cast<uint32_t>(e) * static_cast<uint32_t>(b_magic)) >> 24);
+}
+
+template <int KW, int NB>
+__global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params p0) {
+    using S = il_shape<KW>;
+    constexpr int CI = S::CI;
+    constexpr int NA = S::NA;
+    constexpr int BPP = (NB + S::P - 1) / S::P;  // input elements per staging step
+    conv_params p = p0;
+    if (KW == 2) p.w += static_cast<int64_t>(blockIdx.z) * p.w_phase;  // this phase's weights (one phase otherwise)
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int buf_floats = a_floats<KW>() + kThreads * NB;
     snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);  // [c_in] when p.snake
@@ -590,6 +613,9 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_par
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kNT;
     const int co0 = blockIdx.y * kMT;
     const int bw = p.b_width;
+    const int n_b = CI * bw;
+    // k = 7 divides (faster there, measured); k = 2 multiplies by b_magic
+    auto row_of = [&](int e) { return KW == 7 ? e / bw : b_row(e, p.b_magic); };
     const int64_t tb = t0 - p.pad;
 
     f32x4v ra[NA];
@@ -612,10 +638,10 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_par
 #pragma unroll
         for (int sl = 0; sl < NB; ++sl) {
             const int e = tid + kThreads * sl;
-            const int c = e / bw;
+            const int c = row_of(e);
             const int64_t t = tb + (e - c * bw);
             float v = 0.0f;
-            if (e < CI * bw && ci0 + c < p.c_in && t >= 0 && t < p.t_in) v = p.x[static_cast<int64_t>(ci0 + c) * p.x_pitch + t];
+            if (e < n_b && ci0 + c < p.c_in && t >= 0 && t < p.t_in) v = p.x[static_cast<int64_t>(ci0 + c) * p.x_pitch + t];
             rb[sl] = v;
         }
     };
@@ -634,9 +660,9 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_par
 #pragma unroll
     for (int sl = 0; sl < NB; ++sl) {
         const int e = tid + kThreads * sl;
-        const int c = e / bw;
+        const int c = row_of(e);
         float v = rb[sl];
-        if (p.snake && e < CI * bw && c < p.c_in) v = snake(v, sp[c]);
+        if (p.snake && e < n_b && c < p.c_in) v = snake(v, sp[c]);
         lds[a_floats<KW>() + e] = v;
     }
     __syncthreads();
@@ -660,7 +686,7 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_par
         float b[4];
         read_operands<KW>(As, Bs, p, 0, g, h, vh, m, a, b);
 #pragma unroll
-        for (int ks = 0; ks < KC / 8; ++ks) {
+        for (int ks = 0; ks < S::KS - S::P; ++ks) {
             f32x4v an = a;
             float bn[4] = {b[0], b[1], b[2], b[3]};
             read_operands<KW>(As, Bs, p, ks + 1, g, h, vh, m, an, bn);
@@ -673,41 +699,49 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_par
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[j] = bn[j];
         }
-        // second half: each K step also stages one weight slot and one input
-        // element of the next chunk into the other buffer (last read before
-        // the previous barrier); after the last chunk they go unused
+        // second half: each K step also stages its share of the next chunk
+        // into the other buffer (last read before the previous barrier);
+        // after the last chunk they go unused
         float * An = lds + (buf ^ 1) * buf_floats;
         float * Bn = An + a_floats<KW>();
         bool slow = false;
 #pragma unroll
-        for (int ks = KC / 8; ks < KC / 4; ++ks) {
-            const int piece = ks - KC / 8;
+        for (int ks = S::KS - S::P; ks < S::KS; ++ks) {
+            const int piece = ks - (S::KS - S::P);
             f32x4v an = a;
             float bn[4] = {b[0], b[1], b[2], b[3]};
-            if (ks + 1 < KC / 4) read_operands<KW>(As, Bs, p, ks + 1, g, h, vh, m, an, bn);
-            if (piece < NA) store_a_slot<KW>(An, tid, piece, ra[piece]);
-            if (piece < NB) {
-                const int e = tid + kThreads * piece;
-                const float v = rb[piece];
-                // without SnakeBeta the value is computed from table entry 0
-                // (allocated, not filled) and discarded by the select
-                const snake_param q = sp[p.snake ? min(ci0 + CI + e / bw, cmax) : 0];
-                const float sv = snake_reduced(v, q, slow);
-                Bn[e] = p.snake ? sv : v;
+            if (ks + 1 < S::KS) read_operands<KW>(As, Bs, p, ks + 1, g, h, vh, m, an, bn);
+#pragma unroll
+            for (int i = 0; i < S::APP; ++i) {
+                const int u = piece * S::APP + i;
+                if (u < NA) store_a_slot<KW>(An, tid, u, ra[u]);
+            }
+#pragma unroll
+            for (int i = 0; i < BPP; ++i) {
+                const int sl = piece * BPP + i;
+                if (sl < NB) {
+                    const int e = tid + kThreads * sl;
+                    const float v = rb[sl];
+                    // without SnakeBeta the value is computed from table
+                    // entry 0 (allocated, not filled) and discarded
+                    const snake_param q = sp[p.snake ? min(ci0 + CI + row_of(e), cmax) : 0];
+                    const float sv = snake_reduced(v, q, slow);
+                    Bn[e] = p.snake ? sv : v;
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
-            // the operand reads first, then each MFMA followed by two VALU
-            // instructions, with an LDS store after every third
+            // the operand reads first, then each MFMA followed by VALU
+            // instructions, with an LDS store after every few
             __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
 #pragma unroll
             for (int q2 = 0; q2 < 16; ++q2) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
-                if (q2 % 3 == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, S::kValu, 0);
+                if (q2 % S::kDsEvery == 0) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
             }
             a = an;
 #pragma unroll
@@ -717,14 +751,32 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_k7_il(const conv_par
 #pragma unroll
             for (int sl = 0; sl < NB; ++sl) {
                 const int e = tid + kThreads * sl;
-                const int c = e / bw;
-                if (e < CI * bw && ci0 + CI + c < p.c_in) Bn[e] = snake(rb[sl], sp[ci0 + CI + c]);
+                const int c = row_of(e);
+                if (e < n_b && ci0 + CI + c < p.c_in) Bn[e] = snake(rb[sl], sp[ci0 + CI + c]);
             }
         }
         __syncthreads();
         buf ^= 1;
     }
-    conv_epilogue<false>(p, lds, acc, tid, h, vh, g, m, t0, co0);  // never launched with scatter
+    conv_epilogue<KW == 2>(p, lds, acc, tid, h, vh, g, m, t0, co0);
+}
+
+// Launches the interleaved kernel when its LDS fits; returns -1 when not.
+template <int KW, int NB>
+int launch_il(conv_params p, int phases, size_t table, hipStream_t st, const char * what) {
+    const size_t bufs = 2 * static_cast<size_t>(a_floats<KW>() + kThreads * NB) * sizeof(float);
+    // a table entry even without SnakeBeta: the kernel reads entry 0 then
+    const size_t lds = std::max(bufs + (p.snake ? table : sizeof(snake_param)),
+                                static_cast<size_t>(kMT) * kOutStride * sizeof(float));
+    if (lds > 152 * 1024) return -1;
+    p.param_ring = 0;
+    p.b_magic = static_cast<int32_t>(((1 << 24) + p.b_width - 1) / p.b_width);
+    const void * f = reinterpret_cast<const void *>(&snake_conv1d_il<KW, NB>);
+    if (const int rc = allow_dynamic_lds(f, 152 * 1024, what); rc != LEVO_HIP_OK) return rc;
+    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
+                    static_cast<uint32_t>(phases));
+    snake_conv1d_il<KW, NB><<<grid, kThreads, lds, st>>>(p);
+    return launch_status(what);
 }
 
 template <int KW>
@@ -749,30 +801,20 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
     LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
     const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
                     static_cast<uint32_t>(phases));
-    if constexpr (KW == 7) {
-        // one phase (the kernel applies no per-phase weight offset), and a
-        // table entry even without SnakeBeta: the kernel reads entry 0 then
-        // with the full parameter table even where the other kernel would
+    if constexpr (KW == 2 || KW == 7) {
+        // With the full parameter table even where the other kernel would
         // take the ring: one workgroup per CU of this kernel outruns two of
-        // that one (measured at 1024 channels)
-        const int nb = static_cast<int>(ceil_div(CI * p.b_width, kThreads));
-        if (!p.scatter && phases == 1 && p.w_vec && nb <= kBalSlots) {
-            const int slots = nb <= 5 ? 5 : kBalSlots;
-            const size_t il = std::max(2 * static_cast<size_t>(a_floats<KW>() + kThreads * slots),
-                                       static_cast<size_t>(kMT) * kOutStride) * sizeof(float) +
-                              (p.snake ? table : sizeof(snake_param));
-            if (il <= 152 * 1024) {
-                p.param_ring = 0;
-                const void * f = slots == 5 ? reinterpret_cast<const void *>(&snake_conv1d_k7_il<5>)
-                                            : reinterpret_cast<const void *>(&snake_conv1d_k7_il<kBalSlots>);
-                if (const int st = allow_dynamic_lds(f, 152 * 1024, what); st != LEVO_HIP_OK) return st;
-                if (slots == 5) {
-                    snake_conv1d_k7_il<5><<<grid, kThreads, il, st>>>(p);
-                } else {
-                    snake_conv1d_k7_il<kBalSlots><<<grid, kThreads, il, st>>>(p);
-                }
-                return launch_status(what);
-            }
+        // that one (measured at 1024 channels, k = 7). Measured per layer:
+        // at k = 7 every decoder layer gains; at k = 2 (the upsamplers) from
+        // 512 input channels (16 K steps per chunk pair and up), below that
+        // the plain kernel's higher occupancy wins; at k = 1 (four chunks a
+        // tile) the plain kernel wins everywhere.
+        const int64_t nb = ceil_div(static_cast<int64_t>(CI) * p.b_width, kThreads);
+        if (p.w_vec && p.b_width >= kNT && nb <= il_shape<KW>::kMaxNB && (KW == 7 || p.c_in >= 512)) {
+            int rc = -1;
+            if (KW == 7 && nb <= 5) rc = launch_il<KW, KW == 7 ? 5 : il_shape<KW>::kMaxNB>(p, phases, table, st, what);
+            if (rc < 0) rc = launch_il<KW, il_shape<KW>::kMaxNB>(p, phases, table, st, what);
+            if (rc >= 0) return rc;
         }
     }
     const void * kernel = p.param_ring ? reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, true>)

@@ -334,3 +334,30 @@ def test_transpose_f16_params_and_no_snake(hip, dev, oracle):
     assert f32_err(got, want) <= 1e-5
     got = _run_transpose(hip, dev, x, w, None, s, 3)
     assert f32_err(got, _want_transpose(oracle, x, w, None, s, 3)) <= 1e-5
+
+
+def test_transpose_wide_partial_chunk_and_large_arguments(hip, dev, oracle):
+    """520 input channels (the last chunk of 16 holds 8), 200 outputs (a
+    partial channel tile), stride 3: with F16 SnakeBeta parameters, without
+    SnakeBeta, and with inputs beyond the reduced sine's range, where the
+    fused launch must equal levo_hip_snake_beta followed by the transposed
+    conv without SnakeBeta, bit for bit."""
+    import torch
+    c_in, c_out, t_in, s, pad = 520, 200, 77, 3, 2
+    x = oracle.gaussian(c_in * t_in, 70).reshape(c_in, t_in)
+    w = (oracle.gaussian(c_in * c_out * 2 * s, 71) * np.float32(1.0 / np.sqrt(2 * c_in))).reshape(c_in, c_out, 2 * s)
+    b = oracle.gaussian(c_out, 72)
+    a16 = oracle.f32_to_f16(_params(oracle, c_in, 73)[0])
+    b16 = oracle.f32_to_f16(_params(oracle, c_in, 73)[1])
+    got = _run_transpose(hip, dev, x, w, b, s, pad, a16, b16, param_type=1)
+    want = _want_transpose(oracle, x, w, b, s, pad, oracle.f16_to_f32(a16), oracle.f16_to_f32(b16))
+    assert f32_err(got, want) <= 1e-5
+    assert f32_err(_run_transpose(hip, dev, x, w, b, s, pad), _want_transpose(oracle, x, w, b, s, pad)) <= 1e-5
+    x[5::11] *= np.float32(3.0e4)
+    a, bl = _params(oracle, c_in, 74)
+    fused = _run_transpose(hip, dev, x, w, b, s, pad, a, bl)
+    xs = torch.empty((c_in, t_in), dtype=torch.float32, device=dev)
+    hip.snake_beta(to_dev(x, dev), to_dev(a, dev), to_dev(bl, dev), xs)
+    torch.cuda.synchronize()
+    two_step = _run_transpose(hip, dev, from_dev(xs), w, b, s, pad)
+    assert np.array_equal(fused.view(np.uint32), two_step.view(np.uint32))
