@@ -77,7 +77,32 @@ struct conv_params {
     // wide inputs, where the full table would cost a workgroup per CU)
     int32_t param_ring;
     int32_t b_magic;          // ceil(2^24 / b_width): row of a flat B index by multiply
+    // Workgroup order: 0 = grid (time tiles, channel tiles, phases); 1 = a 1-D
+    // grid in which the phases of one tile run back to back on one XCD
+    int32_t xcd_order;
+    int32_t tiles_x, tiles, phases;
 };
+
+// The time tile x, channel tile y and phase z of this workgroup. With
+// xcd_order the grid is 1-D, ordered (tile group, phase, tile % 8): the
+// hardware deals workgroups to the 8 XCDs round-robin by linear id, so every
+// phase of a tile runs on the same XCD, right after the others. The phases of
+// a transposed convolution write interleaved samples of the same output
+// lines, which then meet in that XCD's L2 instead of going back to memory as
+// partial lines. Workgroups past the last tile (the padding of the final
+// group of 8) are not live.
+struct tile_id {
+    int x, y, z;
+    bool live;
+};
+
+__device__ __forceinline__ tile_id conv_tile(const conv_params & p) {
+    if (!p.xcd_order) return {static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), static_cast<int>(blockIdx.z), true};
+    const int lin = static_cast<int>(blockIdx.x);
+    const int rest = lin >> 3;
+    const int tile = (rest / p.phases) * 8 + (lin & 7);
+    return {tile % p.tiles_x, tile / p.tiles_x, rest % p.phases, tile < p.tiles};
+}
 
 // LDS float index of weight (kk, r) in the A chunk: rows r = 64 h + 16 i + m
 // are stored as [kk][h][m][i] so lane m of a wave on row half h reads
@@ -244,7 +269,7 @@ __device__ __forceinline__ void load_snake_logs(const conv_params & p, int c, fl
 // D[row][col] of a 16 x 16 tile is in lane col + 16 * (row / 4), item row % 4.
 template <bool SCATTER>
 __device__ __forceinline__ void conv_epilogue(const conv_params & p, float * lds, const f32x4v (&acc)[4][4], int tid,
-                                              int h, int vh, int g, int m, int64_t t0, int co0) {
+                                              int h, int vh, int g, int m, int64_t t0, int co0, int phase) {
     float * out = lds;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -256,7 +281,7 @@ __device__ __forceinline__ void conv_epilogue(const conv_params & p, float * lds
     __syncthreads();
     if (SCATTER && p.scatter) {
         // transposed convolution: phase z's columns land every o_stride samples
-        const int64_t base = p.o_base + static_cast<int64_t>(blockIdx.z);
+        const int64_t base = p.o_base + static_cast<int64_t>(phase);
         for (int e = tid; e < kMT * kNT; e += kThreads) {
             const int r = e / kNT;
             const int c = e % kNT;
@@ -321,8 +346,10 @@ __device__ __forceinline__ void conv_epilogue(const conv_params & p, float * lds
 
 template <int KW, bool RING>
 __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_params p0) {
+    const tile_id tl = conv_tile(p0);
+    if (!tl.live) return;
     conv_params p = p0;
-    p.w += static_cast<int64_t>(blockIdx.z) * p.w_phase;  // this phase's weights
+    p.w += static_cast<int64_t>(tl.z) * p.w_phase;  // this phase's weights
     constexpr int CI = conv_chunk<KW>::CI;
     constexpr int KC = conv_chunk<KW>::KC;
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -340,8 +367,8 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     const int vh = wave & 1;      // column half
     const int m = lane & 15;
     const int g = lane >> 4;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kNT;
-    const int co0 = blockIdx.y * kMT;
+    const int64_t t0 = static_cast<int64_t>(tl.x) * kNT;
+    const int co0 = tl.y * kMT;
 
     f32x4v ra[conv_slots<KW>::NA];
     float rb[conv_slots<KW>::NB];
@@ -405,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         buf ^= 1;
     }
 
-    conv_epilogue<true>(p, lds, acc, tid, h, vh, g, m, t0, co0);
+    conv_epilogue<true>(p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
 }
 
 // ---- narrow output (c_out <= 4): the decoder's 128 -> 2 output conv -------
@@ -599,7 +626,9 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     constexpr int NA = S::NA;
     constexpr int BPP = (NB + S::P - 1) / S::P;  // input elements per staging step
     conv_params p = p0;
-    if (KW == 2) p.w += static_cast<int64_t>(blockIdx.z) * p.w_phase;  // this phase's weights (one phase otherwise)
+    const tile_id tl = conv_tile(p0);
+    if (!tl.live) return;
+    if (KW == 2) p.w += static_cast<int64_t>(tl.z) * p.w_phase;  // this phase's weights (one phase otherwise)
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int buf_floats = a_floats<KW>() + kThreads * NB;
     snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);  // [c_in] when p.snake
@@ -610,8 +639,8 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     const int vh = wave & 1;
     const int m = lane & 15;
     const int g = lane >> 4;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kNT;
-    const int co0 = blockIdx.y * kMT;
+    const int64_t t0 = static_cast<int64_t>(tl.x) * kNT;
+    const int co0 = tl.y * kMT;
     const int bw = p.b_width;
     const int n_b = CI * bw;
     // k = 7 divides (faster there, measured); k = 2 multiplies by b_magic
@@ -758,7 +787,20 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
         __syncthreads();
         buf ^= 1;
     }
-    conv_epilogue<KW == 2>(p, lds, acc, tid, h, vh, g, m, t0, co0);
+    conv_epilogue<KW == 2>(p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
+}
+
+// The launch grid; transposed convolutions (more than one phase) take the
+// XCD-ordered 1-D grid.
+inline dim3 conv_grid(conv_params & p, int phases) {
+    const int64_t tx = ceil_div(p.t_out, kNT);
+    const int64_t ty = ceil_div(p.c_out, kMT);
+    p.xcd_order = p.scatter && phases > 1 && ceil_div(tx * ty, 8) * 8 * phases < INT32_MAX;
+    p.tiles_x = static_cast<int32_t>(tx);
+    p.tiles = static_cast<int32_t>(tx * ty);
+    p.phases = phases;
+    if (p.xcd_order) return dim3(static_cast<uint32_t>(ceil_div(tx * ty, 8) * 8 * phases));
+    return dim3(static_cast<uint32_t>(tx), static_cast<uint32_t>(ty), static_cast<uint32_t>(phases));
 }
 
 // Launches the interleaved kernel when its LDS fits; returns -1 when not.
@@ -773,8 +815,7 @@ int launch_il(conv_params p, int phases, size_t table, hipStream_t st, const cha
     p.b_magic = static_cast<int32_t>(((1 << 24) + p.b_width - 1) / p.b_width);
     const void * f = reinterpret_cast<const void *>(&snake_conv1d_il<KW, NB>);
     if (const int rc = allow_dynamic_lds(f, 152 * 1024, what); rc != LEVO_HIP_OK) return rc;
-    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
-                    static_cast<uint32_t>(phases));
+    const dim3 grid = conv_grid(p, phases);
     snake_conv1d_il<KW, NB><<<grid, kThreads, lds, st>>>(p);
     return launch_status(what);
 }
@@ -799,8 +840,7 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
                    wgs > 256;
     const size_t lds = tiles + (p.snake ? (p.param_ring ? 2 * CI * sizeof(snake_param) : table) : 0);
     LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
-    const dim3 grid(static_cast<uint32_t>(ceil_div(p.t_out, kNT)), static_cast<uint32_t>(ceil_div(p.c_out, kMT)),
-                    static_cast<uint32_t>(phases));
+    const dim3 grid = conv_grid(p, phases);
     if constexpr (KW == 2 || KW == 7) {
         // With the full parameter table even where the other kernel would
         // take the ring: one workgroup per CU of this kernel outruns two of
@@ -858,7 +898,7 @@ extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t 
                  "LeVo audio graph: SnakeBeta alpha_log must be F32 or F16");
     LEVO_REQUIRE(!snake || c_in <= kMaxSnakeChannels, "snake_conv1d: at most %d input channels with SnakeBeta",
                  kMaxSnakeChannels);
-    conv_params p;
+    conv_params p{};
     p.x = x;
     p.x_pitch = x_stride;
     p.t_in = t_in;
@@ -952,7 +992,7 @@ extern "C" int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride
                  kMaxSnakeChannels);
     LEVO_REQUIRE(ceil_div(t_in + 1, kNT) < (int64_t{1} << 31) && ceil_div(c_out, kMT) < 65536,
                  "conv_transpose1d: grid too large");
-    conv_params p;
+    conv_params p{};
     p.x = x;
     p.x_pitch = x_stride;
     p.t_in = t_in;
