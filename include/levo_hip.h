@@ -180,6 +180,19 @@ typedef struct levo_hip_vae_decoder_weights {
  * LEVO_HIP_ERR_INVALID naming the first missing one in the reference's order. */
 int levo_hip_vae_validate_weights(const levo_hip_vae_decoder_weights * weights);
 
+/* One residual unit of the decoder, run_residual (src/levo-vae.cpp:91-100):
+ * y = x + conv_1(snake_post(conv_0(snake_pre(x)))), conv_0 kernel 7 at
+ * `dilation` with padding 3 * dilation, conv_1 kernel 1, each with its bias
+ * (either may be null). x, y, h: [channels][time] F32, rows contiguous. y must
+ * not overlap x: every output sample reads its neighbours' inputs. h receives
+ * conv_0's output unless the unit runs as one launch (128 channels, both
+ * SnakeBeta parameter sets, 16-byte aligned weights), where the intermediate
+ * never leaves the device's caches and h is not touched. */
+int levo_hip_vae_residual_unit(const float * x, int64_t channels, int64_t time,
+                               const levo_hip_vae_residual * unit, int64_t dilation,
+                               levo_hip_type param_type, float * y, float * h,
+                               levo_hip_stream_t stream);
+
 /* Workspace bytes levo_hip_vae_decode needs for `frames` latent frames
  * (three activation buffers of 128 x 1920 x frames floats); < 0 if invalid. */
 int64_t levo_hip_vae_decode_workspace_bytes(int64_t frames);
@@ -188,7 +201,9 @@ int64_t levo_hip_vae_decode_workspace_bytes(int64_t frames);
  * [64][frames] F32 to audio [2][frames * 1920] F32, with the reference's
  * hyper-parameters (latent 64, widths 2048 -> 1024 -> 512 -> 256 -> 128 ->
  * 128, strides 10, 6, 4, 4, 2, dilations 1, 3, 9). 37 fused SnakeBeta +
- * convolution launches (input conv, 7 per stage, output conv); none of the
+ * convolution steps (input conv, 7 per stage, output conv) in 31 launches:
+ * the 128-channel residual units (stages 4 and 5) are one launch each, as
+ * levo_hip_vae_residual_unit runs them. None of the
  * activations leaves the device, the caller's workspace (16-byte aligned,
  * levo_hip_vae_decode_workspace_bytes) holds them. Every weight the
  * reference's validate_weights requires (src/levo-vae.cpp:56-78) must be

@@ -40,6 +40,19 @@ int64_t kquant_block_bytes(levo_hip_type type);  // Q4_K / Q5_K / Q6_K / Q8_K pe
 int dequantize_kquant(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type, int64_t k,
                       hipStream_t stream);
 
+// One VAE residual unit, y = x + conv_1(snake_post(conv_0(snake_pre(x)))),
+// conv_0 k = 7 at dilation d (padding 3d), conv_1 k = 1 (src/levo-vae.cpp:91-100),
+// as a single launch (snake_conv.hip). Applies to 128 channels with 16-byte
+// aligned weights and both SnakeBeta parameter sets; returns kNotFused
+// otherwise (nothing launched). x and y are [128][t] with row stride t and
+// must not overlap.
+constexpr int kNotFused = 1;
+int launch_residual_unit_fused(const float * x, int64_t c, int64_t t, const void * pre_alpha_log,
+                               const void * pre_beta_log, const float * w0, const float * b0,
+                               const void * post_alpha_log, const void * post_beta_log, const float * w1,
+                               const float * b1, int64_t dilation, levo_hip_type param_type, float * y,
+                               hipStream_t stream);
+
 inline bool aligned16(const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -104,6 +104,19 @@ __device__ __forceinline__ tile_id conv_tile(const conv_params & p) {
     return {tile % p.tiles_x, tile / p.tiles_x, rest % p.phases, tile < p.tiles};
 }
 
+// The k = 1 half of a residual unit (src/levo-vae.cpp:96-100) fused into the
+// k = 7 launch, for c = kMT channels: one workgroup holds every channel of
+// its time tile.
+struct fuse_params {
+    const float * w1;          // [c][c] k = 1 weights, 16-byte aligned
+    const float * bias1;       // [c] or null
+    const void * alpha1_log;   // post SnakeBeta [c] (type of conv_params::param_f16)
+    const void * beta1_log;
+    float * y;                 // [c][y_pitch]: the unit's output, not its input
+    int64_t y_pitch;
+    int32_t y_vec;             // y and the input rows 16-byte aligned
+};
+
 // LDS float index of weight (kk, r) in the A chunk: rows r = 64 h + 16 i + m
 // are stored as [kk][h][m][i] so lane m of a wave on row half h reads
 // its four fragments i = 0..3 with one ds_read_b128. Rows of kk are kAStride
@@ -619,8 +632,87 @@ __device__ __forceinline__ int b_row(int e, int b_magic) {
     return static_cast<int>((static_cast<uint32_t>(e) * static_cast<uint32_t>(b_magic)) >> 24);
 }
 
-template <int KW, int NB>
-__global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params p0) {
+// After the k = 7 loop of a fused residual unit: h = acc + bias0 goes through
+// the post SnakeBeta into LDS in the output tile's layout, H[channel][sample],
+// the B operand of the k = 1 conv; the k = 1 weights come straight from
+// global memory (64 KB, shared by every workgroup through L2). K runs in a
+// permuted order, the same for both operands: at step 4q + r lane group g
+// takes channel 16q + 4g + r, so a lane's weights of one row for steps
+// 4q .. 4q + 3 are one float4. The result + bias1 + the unit input goes to y
+// through the shared epilogue.
+__device__ __forceinline__ void residual_tail(const conv_params & p, const fuse_params & f, float * lds,
+                                              f32x4v (&acc)[4][4], int tid, int h, int vh, int g, int m,
+                                              int64_t t0) {
+    float * H = lds;
+    snake_param * sp1 = reinterpret_cast<snake_param *>(lds + kMT * kOutStride);
+    for (int c = tid; c < kMT; c += kThreads) {
+        const float al = p.param_f16 ? h2f(static_cast<const uint16_t *>(f.alpha1_log)[c])
+                                     : static_cast<const float *>(f.alpha1_log)[c];
+        const float bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(f.beta1_log)[c])
+                                     : static_cast<const float *>(f.beta1_log)[c];
+        sp1[c] = make_snake_param(al, bl);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int row = h * 64 + 16 * i + 4 * g + u;
+            const float bv = p.bias ? p.bias[row] : 0.0f;
+            const snake_param q = sp1[row];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = acc[i][j][u];
+                if (p.bias) v = v + bv;  // the conv's bias add, then SnakeBeta
+                H[row * kOutStride + vh * 64 + 16 * j + m] = snake(v, q);
+            }
+        }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+    const float * wrow = f.w1 + (h * 64 + m) * kMT + 4 * g;  // row h*64 + 16 i + m at + 16 i kMT
+    f32x4v wa[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wa[i] = *reinterpret_cast<const f32x4v *>(wrow + 16 * i * kMT);
+#pragma unroll
+    for (int q = 0; q < kMT / 16; ++q) {
+        f32x4v wn[4];
+        if (q + 1 < kMT / 16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wn[i] = *reinterpret_cast<const f32x4v *>(wrow + 16 * i * kMT + 16 * (q + 1));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float * brow = H + (16 * q + 4 * g + r) * kOutStride + vh * 64 + m;
+            float b[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = brow[16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(wa[i][r], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (q + 1 < kMT / 16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wa[i] = wn[i];
+        }
+    }
+    __syncthreads();  // every wave is done with H before the epilogue reuses the LDS
+    conv_params e = p;
+    e.bias = f.bias1;
+    e.residual = p.x;  // the unit input: y = x + conv(snake(h))
+    e.r_pitch = p.x_pitch;
+    e.y = f.y;
+    e.y_pitch = f.y_pitch;
+    e.y_vec = f.y_vec;
+    conv_epilogue<false>(e, lds, acc, tid, h, vh, g, m, t0, 0, 0);
+}
+
+template <int KW, int NB, bool FUSE>
+__global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params p0, const fuse_params f) {
     using S = il_shape<KW>;
     constexpr int CI = S::CI;
     constexpr int NA = S::NA;
@@ -787,7 +879,11 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
         __syncthreads();
         buf ^= 1;
     }
-    conv_epilogue<KW == 2>(p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
+    if constexpr (FUSE) {
+        residual_tail(p, f, lds, acc, tid, h, vh, g, m, t0);
+    } else {
+        conv_epilogue<KW == 2>(p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
+    }
 }
 
 // The launch grid; transposed convolutions (more than one phase) take the
@@ -813,10 +909,10 @@ int launch_il(conv_params p, int phases, size_t table, hipStream_t st, const cha
     if (lds > 152 * 1024) return -1;
     p.param_ring = 0;
     p.b_magic = static_cast<int32_t>(((1 << 24) + p.b_width - 1) / p.b_width);
-    const void * f = reinterpret_cast<const void *>(&snake_conv1d_il<KW, NB>);
+    const void * f = reinterpret_cast<const void *>(&snake_conv1d_il<KW, NB, false>);
     if (const int rc = allow_dynamic_lds(f, 152 * 1024, what); rc != LEVO_HIP_OK) return rc;
     const dim3 grid = conv_grid(p, phases);
-    snake_conv1d_il<KW, NB><<<grid, kThreads, lds, st>>>(p);
+    snake_conv1d_il<KW, NB, false><<<grid, kThreads, lds, st>>>(p, fuse_params{});
     return launch_status(what);
 }
 
@@ -869,6 +965,63 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
 }
 
 }  // namespace
+
+int launch_residual_unit_fused(const float * x, int64_t c, int64_t t, const void * pre_alpha_log,
+                               const void * pre_beta_log, const float * w0, const float * b0,
+                               const void * post_alpha_log, const void * post_beta_log, const float * w1,
+                               const float * b1, int64_t dilation, levo_hip_type param_type, float * y,
+                               hipStream_t st) {
+    if (c != kMT || dilation < 1 || !aligned16(w0) || !aligned16(w1) || pre_alpha_log == nullptr ||
+        pre_beta_log == nullptr || post_alpha_log == nullptr || post_beta_log == nullptr)
+        return kNotFused;
+    conv_params p{};
+    p.x = x;
+    p.x_pitch = t;
+    p.t_in = t;
+    p.alpha_log = pre_alpha_log;
+    p.beta_log = pre_beta_log;
+    p.param_f16 = param_type == LEVO_HIP_TYPE_F16;
+    p.snake = 1;
+    p.w = w0;
+    p.bias = b0;
+    p.y_pitch = t;
+    p.t_out = t;  // k 7 at padding 3d keeps the length
+    p.c_in = kMT;
+    p.c_out = kMT;
+    p.pad = static_cast<int32_t>(3 * dilation);
+    p.dil = static_cast<int32_t>(dilation);
+    p.b_width = (kNT + 6 * p.dil + 3) & ~3;
+    p.w_vec = 1;  // 16-byte aligned, c * 7 % 4 == 0
+    p.o_stride = 1;
+    p.y_len = t;
+    const int64_t nb = ceil_div(static_cast<int64_t>(conv_chunk<7>::CI) * p.b_width, kThreads);
+    if (nb > il_shape<7>::kMaxNB) return kNotFused;
+    const int slots = nb <= 5 ? 5 : il_shape<7>::kMaxNB;
+    const size_t bufs = 2 * static_cast<size_t>(a_floats<7>() + kThreads * slots) * sizeof(float);
+    const size_t lds = std::max(bufs + kMT * sizeof(snake_param),
+                                static_cast<size_t>(kMT) * kOutStride * sizeof(float) + kMT * sizeof(snake_param));
+    if (lds > 152 * 1024) return kNotFused;
+    fuse_params f{};
+    f.w1 = w1;
+    f.bias1 = b1;
+    f.alpha1_log = post_alpha_log;
+    f.beta1_log = post_beta_log;
+    f.y = y;
+    f.y_pitch = t;
+    f.y_vec = aligned16(y) && aligned16(x) && t % 4 == 0;
+    const char * what = "levo_hip_vae_residual_unit";
+    const dim3 grid = conv_grid(p, 1);
+    const void * fn = slots == 5 ? reinterpret_cast<const void *>(&snake_conv1d_il<7, 5, true>)
+                                 : reinterpret_cast<const void *>(&snake_conv1d_il<7, il_shape<7>::kMaxNB, true>);
+    if (const int rc = allow_dynamic_lds(fn, 152 * 1024, what); rc != LEVO_HIP_OK) return rc;
+    if (slots == 5) {
+        snake_conv1d_il<7, 5, true><<<grid, kThreads, lds, st>>>(p, f);
+    } else {
+        snake_conv1d_il<7, il_shape<7>::kMaxNB, true><<<grid, kThreads, lds, st>>>(p, f);
+    }
+    return launch_status(what);
+}
+
 }  // namespace levo_hip
 
 using namespace levo_hip;

@@ -7,8 +7,10 @@
 //   SnakeBeta + output conv (128 -> 2, k 7, padding 3, no bias)
 // with the reference's fixed hyper-parameters (src/levo-vae-model.h:18-33,
 // decode order: strides 10, 6, 4, 4, 2; widths 2048 -> 1024 -> 512 -> 256
-// -> 128 -> 128). Host code only: it orders levo_hip_snake_conv1d and
-// levo_hip_snake_conv_transpose1d launches over three workspace buffers.
+// -> 128 -> 128). Host code only: it orders levo_hip_snake_conv1d,
+// levo_hip_snake_conv_transpose1d and residual-unit launches over three
+// workspace buffers. A residual unit at 128 channels (stages 4 and 5) is one
+// launch: the k = 1 conv runs in the k = 7 conv's epilogue.
 #include "common.hpp"
 
 #include <algorithm>
@@ -83,6 +85,35 @@ extern "C" int levo_hip_vae_validate_weights(const levo_hip_vae_decoder_weights 
     return LEVO_HIP_OK;
 }
 
+extern "C" int levo_hip_vae_residual_unit(const float * x, int64_t channels, int64_t time,
+                                          const levo_hip_vae_residual * unit, int64_t dilation,
+                                          levo_hip_type param_type, float * y, float * h,
+                                          levo_hip_stream_t stream) {
+    LEVO_REQUIRE(unit != nullptr, "vae_residual_unit: null unit");
+    LEVO_REQUIRE(x != nullptr && y != nullptr && h != nullptr, "vae_residual_unit: null tensor");
+    LEVO_REQUIRE(unit->conv_0.weight != nullptr && unit->conv_1.weight != nullptr,
+                 "vae_residual_unit: null convolution weight");
+    LEVO_REQUIRE(channels > 0 && time > 0 && channels <= (1 << 20) && time < (int64_t{1} << 40),
+                 "vae_residual_unit: invalid shape");
+    LEVO_REQUIRE(dilation > 0 && dilation < (1 << 16), "vae_residual_unit: invalid dilation");
+    const uintptr_t xb = reinterpret_cast<uintptr_t>(x);
+    const uintptr_t yb = reinterpret_cast<uintptr_t>(y);
+    const uintptr_t n = static_cast<uintptr_t>(channels * time) * sizeof(float);
+    LEVO_REQUIRE(yb + n <= xb || xb + n <= yb, "vae_residual_unit: y must not overlap x");
+    const int fused = launch_residual_unit_fused(x, channels, time, unit->pre.alpha_log, unit->pre.beta_log,
+                                                 unit->conv_0.weight, unit->conv_0.bias, unit->post.alpha_log,
+                                                 unit->post.beta_log, unit->conv_1.weight, unit->conv_1.bias,
+                                                 dilation, param_type, y, as_hip(stream));
+    if (fused != kNotFused) return fused;
+    const int st = levo_hip_snake_conv1d(x, time, channels, time, unit->pre.alpha_log, unit->pre.beta_log,
+                                         param_type, unit->conv_0.weight, channels, 7, unit->conv_0.bias,
+                                         3 * dilation, dilation, nullptr, 0, h, time, stream);
+    if (st != LEVO_HIP_OK) return st;
+    return levo_hip_snake_conv1d(h, time, channels, time, unit->post.alpha_log, unit->post.beta_log, param_type,
+                                 unit->conv_1.weight, channels, 1, unit->conv_1.bias, 0, 1, x, time, y, time,
+                                 stream);
+}
+
 extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const float * latent, int64_t frames,
                                    float * audio, float * const * stage_outputs, void * workspace,
                                    int64_t workspace_bytes, levo_hip_stream_t stream) {
@@ -117,14 +148,11 @@ extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const
                                                   stride, sg.upsample.bias, (stride + 1) / 2, b, out_len, stream));
         len = out_len;
         const int64_t c = kOutWidth[s];
+        // residual units: x in b, y into a (free since the upsample read it),
+        // then the two swap
         for (int r = 0; r < 3; ++r) {
-            const levo_hip_vae_residual & ru = sg.residual[r];
-            const int64_t d = kDilations[r];
-            LEVO_STEP(levo_hip_snake_conv1d(b, len, c, len, ru.pre.alpha_log, ru.pre.beta_log, pt, ru.conv_0.weight,
-                                            c, 7, ru.conv_0.bias, 3 * d, d, nullptr, 0, h, len, stream));
-            // y = x + conv(snake(h)), written over x (src/levo-vae.cpp:96-100)
-            LEVO_STEP(levo_hip_snake_conv1d(h, len, c, len, ru.post.alpha_log, ru.post.beta_log, pt,
-                                            ru.conv_1.weight, c, 1, ru.conv_1.bias, 0, 1, b, len, b, len, stream));
+            LEVO_STEP(levo_hip_vae_residual_unit(b, c, len, &sg.residual[r], kDilations[r], pt, a, h, stream));
+            std::swap(a, b);
         }
         if (stage_outputs != nullptr && stage_outputs[s] != nullptr) {
             const hipError_t e = hipMemcpyAsync(stage_outputs[s], b, sizeof(float) * c * len,

@@ -2,7 +2,7 @@
 // over decoder weights already in device memory: the same decode() contract,
 // latent [64][frames] channel-major F32 in, audio [2][frames * 1920] out,
 // optional stage tensors, cancellation checked when the decode ends, and the
-// reference's errors (std::runtime_error("LeVo VAE: ...")). The 37 launches of
+// reference's errors (std::runtime_error("LeVo VAE: ...")). The 31 launches of
 // levo_hip_vae_decode run on the decoder's stream; only the latent and the
 // audio cross PCIe. decode_device() is the same decode with the latent and the
 // audio in device memory.

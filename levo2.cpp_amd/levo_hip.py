@@ -166,6 +166,8 @@ class LevoHip:
             "levo_hip_vae_validate_weights": (ctypes.c_int, [ctypes.POINTER(VaeDecoderWeights)]),
             "levo_hip_vae_decode": (ctypes.c_int, [ctypes.POINTER(VaeDecoderWeights), _P, _I64, _P, _P, _P, _I64,
                                                     _P]),
+            "levo_hip_vae_residual_unit": (ctypes.c_int, [_P, _I64, _I64, ctypes.POINTER(VaeResidual), _I64,
+                                                          ctypes.c_int, _P, _P, _P]),
             "levo_hip_residual_rms_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, ctypes.c_int, _P, _P,
                                                           _I64, _I64, _F, _P]),
             "levo_hip_residual_layer_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P,
@@ -263,6 +265,13 @@ class LevoHip:
             stages = (ctypes.c_void_p * 5)(*[_addr(t) for t in stage_outputs])
         return self._check(self.lib.levo_hip_vae_decode(ctypes.byref(weights), _addr(latent), frames, _addr(audio),
                                                         stages, _addr(workspace), workspace_bytes, _stream(stream)))
+
+    def vae_residual_unit(self, x, channels, time, unit: VaeResidual, dilation, y, h, *, param_type=F32,
+                          stream=None):
+        """One residual unit (run_residual): y = x + conv_1(snake(conv_0(snake(x)))); h: conv_0's output
+        unless the unit runs as one launch."""
+        return self._check(self.lib.levo_hip_vae_residual_unit(_addr(x), channels, time, ctypes.byref(unit), dilation,
+                                                               param_type, _addr(y), _addr(h), _stream(stream)))
 
     def rms_norm(self, act_type, x, delta, weight, weight_type, h_out, y, rows, dim, eps, stream=None):
         return self._check(self.lib.levo_hip_residual_rms_norm(act_type, _addr(x), _addr(delta), _addr(weight),

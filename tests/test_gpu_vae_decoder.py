@@ -235,3 +235,102 @@ def test_decoder_stage_outputs(hip, binding, dev, oracle):
             err = f32_err(from_dev(stages[s]), y)
             print(f"stage {s}: err {err:.3g}")
             assert err <= 1e-4
+
+
+# ---- one residual unit (levo_hip_vae_residual_unit, run_residual) -------------
+
+def _unit_weights(rng, c, bias=True):
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    snake = lambda: (f32(rng.standard_normal(c) * 0.3), f32(rng.standard_normal(c) * 0.3))
+    w0 = f32(rng.standard_normal((c, c, 7)) * (0.5 / np.sqrt(c * 7)))
+    w1 = f32(rng.standard_normal((c, c, 1)) * (0.3 / np.sqrt(c)))
+    b0 = f32(rng.standard_normal(c) * 0.05) if bias else None
+    b1 = f32(rng.standard_normal(c) * 0.05) if bias else None
+    return dict(pre=snake(), conv0=(w0, b0), post=snake(), conv1=(w1, b1))
+
+
+def _unit_oracle(oracle, ru, x, d):
+    t = oracle.conv1d(oracle.snake_beta(x, *ru["pre"], threads=8), ru["conv0"][0], ru["conv0"][1], 3 * d, d, threads=8)
+    t = oracle.conv1d(oracle.snake_beta(t, *ru["post"], threads=8), ru["conv1"][0], ru["conv1"][1], 0, 1, threads=8)
+    return (x + t).astype(np.float32)
+
+
+def _unit_struct(binding, dev, ru, misalign_w0=False):
+    import torch
+    keep = []
+
+    def put(a, shift=0):
+        if a is None:
+            return None
+        t = torch.empty(a.size + shift, dtype=torch.float32 if a.dtype == np.float32 else torch.int16, device=dev)
+        t[shift:] = torch.from_numpy(a.view(np.float32 if a.dtype == np.float32 else np.int16).ravel()).to(dev)
+        keep.append(t)
+        return t.data_ptr() + shift * t.element_size()
+
+    u = binding.VaeResidual()
+    u.pre.alpha_log, u.pre.beta_log = put(ru["pre"][0]), put(ru["pre"][1])
+    u.conv_0.weight, u.conv_0.bias = put(ru["conv0"][0], 1 if misalign_w0 else 0), put(ru["conv0"][1])
+    u.post.alpha_log, u.post.beta_log = put(ru["post"][0]), put(ru["post"][1])
+    u.conv_1.weight, u.conv_1.bias = put(ru["conv1"][0]), put(ru["conv1"][1])
+    return u, keep
+
+
+def _run_unit(hip, dev, u, x, d, param_type=0):
+    import torch
+    c, t = x.shape
+    y = torch.full((c, t), float("nan"), dtype=torch.float32, device=dev)
+    h = torch.full((c, t), float("nan"), dtype=torch.float32, device=dev)
+    hip.vae_residual_unit(to_dev(x, dev), c, t, u, d, y, h, param_type=param_type)
+    return from_dev(y)
+
+
+@pytest.mark.parametrize("c,t,d", [(128, 3000, 1), (128, 1001, 3), (128, 517, 9), (128, 128, 9), (128, 1, 1),
+                                   (64, 700, 3), (256, 300, 9)])
+def test_residual_unit(hip, binding, dev, oracle, c, t, d):
+    """128 channels run as one launch (the k = 1 conv in the k = 7 conv's
+    epilogue); other widths as the two fused SnakeBeta + conv launches.
+    Lengths off the 128-sample tile and off 4 (the scalar epilogue)."""
+    rng = np.random.default_rng(c + t + d)
+    ru = _unit_weights(rng, c)
+    x = oracle.gaussian(c * t, 7 * t + d).reshape(c, t)
+    u, keep = _unit_struct(binding, dev, ru)
+    assert f32_err(_run_unit(hip, dev, u, x, d), _unit_oracle(oracle, ru, x, d)) <= 1e-5
+
+
+def test_residual_unit_f16_params_no_bias_and_unfused_twin(hip, binding, dev, oracle):
+    """F16 SnakeBeta parameters (widened exactly), null biases, and the same
+    128-channel unit with a misaligned conv_0 weight, which takes the
+    two-launch path: both agree with the oracle."""
+    rng = np.random.default_rng(77)
+    c, t, d = 128, 2000, 3
+    ru = _unit_weights(rng, c, bias=False)
+    x = oracle.gaussian(c * t, 78).reshape(c, t)
+    want = _unit_oracle(oracle, ru, x, d)
+    u, keep = _unit_struct(binding, dev, ru)
+    fused = _run_unit(hip, dev, u, x, d)
+    assert f32_err(fused, want) <= 1e-5
+    u2, keep2 = _unit_struct(binding, dev, ru, misalign_w0=True)
+    assert f32_err(_run_unit(hip, dev, u2, x, d), want) <= 1e-5
+    ru16 = dict(ru, pre=tuple(oracle.f32_to_f16(a) for a in ru["pre"]),
+                post=tuple(oracle.f32_to_f16(a) for a in ru["post"]))
+    ru16w = dict(ru, pre=tuple(oracle.f16_to_f32(a) for a in ru16["pre"]),
+                 post=tuple(oracle.f16_to_f32(a) for a in ru16["post"]))
+    u3, keep3 = _unit_struct(binding, dev, ru16)
+    assert f32_err(_run_unit(hip, dev, u3, x, d, param_type=1), _unit_oracle(oracle, ru16w, x, d)) <= 1e-5
+
+
+def test_residual_unit_rejects(hip, binding, dev):
+    import torch
+    rng = np.random.default_rng(5)
+    ru = _unit_weights(rng, 128)
+    u, keep = _unit_struct(binding, dev, ru)
+    x = torch.zeros((128, 256), device=dev)
+    h = torch.zeros((128, 256), device=dev)
+    with pytest.raises(binding.LevoHipError, match="must not overlap"):
+        hip.vae_residual_unit(x, 128, 256, u, 1, x, h)
+    with pytest.raises(binding.LevoHipError, match="must not overlap"):
+        hip.vae_residual_unit(x, 128, 256, u, 1, x[:, 4:], h)
+    with pytest.raises(binding.LevoHipError, match="null tensor"):
+        hip.vae_residual_unit(x, 128, 256, u, 1, torch.zeros((128, 256), device=dev), None)
+    with pytest.raises(binding.LevoHipError, match="dilation"):
+        hip.vae_residual_unit(x, 128, 256, u, 0, torch.zeros((128, 256), device=dev), h)
