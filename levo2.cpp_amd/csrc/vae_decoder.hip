@@ -93,7 +93,8 @@ extern "C" int levo_hip_vae_residual_unit(const float * x, int64_t channels, int
     LEVO_REQUIRE(x != nullptr && y != nullptr && h != nullptr, "vae_residual_unit: null tensor");
     LEVO_REQUIRE(unit->conv_0.weight != nullptr && unit->conv_1.weight != nullptr,
                  "vae_residual_unit: null convolution weight");
-    LEVO_REQUIRE(channels > 0 && time > 0 && channels <= (1 << 20) && time < (int64_t{1} << 40),
+    // time < 2^37: ceil(time / 128) sample tiles stay far inside a 32-bit grid
+    LEVO_REQUIRE(channels > 0 && time > 0 && channels <= (1 << 20) && time < (int64_t{1} << 37),
                  "vae_residual_unit: invalid shape");
     LEVO_REQUIRE(dilation > 0 && dilation < (1 << 16), "vae_residual_unit: invalid dilation");
     const uintptr_t xb = reinterpret_cast<uintptr_t>(x);

@@ -334,3 +334,5 @@ def test_residual_unit_rejects(hip, binding, dev):
         hip.vae_residual_unit(x, 128, 256, u, 1, torch.zeros((128, 256), device=dev), None)
     with pytest.raises(binding.LevoHipError, match="dilation"):
         hip.vae_residual_unit(x, 128, 256, u, 0, torch.zeros((128, 256), device=dev), h)
+    with pytest.raises(binding.LevoHipError, match="invalid shape"):  # checked before any access
+        hip.vae_residual_unit(x, 128, 1 << 37, u, 1, torch.zeros((128, 256), device=dev), h)
