@@ -4,17 +4,22 @@
 // (cond and uncond, dwordx4), combined l = u + s*(c - u) in registers and
 // never written back. Everything the sampler needs comes from the
 // register-resident row, touching each value only with cheap compares:
-//   A. unique-token repetition penalty and stream-0 ignore list via LDS
-//      bitmaps (src/levo-sampling.cpp:39-47, :137-147); NaN check and the
-//      row maximum;
+//   A. while the loads of later chunks are still in flight, each chunk is
+//      combined and folded into per-thread online softmax statistics (running
+//      maximum and a rescaled sum of exp2((l - max) * log2(e) / T)); a NaN or
+//      +inf makes the sum NaN, which sends the row to an exact re-check.
+//      The unique-token repetition penalty and stream-0 ignore list are applied
+//      through LDS bitmaps (src/levo-sampling.cpp:39-47, :137-147); such rows
+//      recompute their statistics after the adjustment;
 //   B. a lower bound of the k-th largest value: each wave bisects the
 //      order-preserving keys of its 64 lane maxima with ballots (no barrier)
 //      for its ceil(k/4)-th largest; at least k ids lie at or above the
 //      smallest of the four bounds;
 //   C. the first maximum (std::max_element, :94-96), the optional
-//      full-vocabulary log-sum-exp of l/T, and a gather of the few ids at or
-//      above the bound (value and id) into per-wave LDS segments; the row's
-//      registers are dead after this point;
+//      full-vocabulary log-sum-exp of l/T from the streamed statistics, and a
+//      gather of the few ids at or above the bound (value and id, one compare
+//      per id) into per-wave LDS segments; the row's registers are dead after
+//      this point;
 //   D. the exact k-th value of the stable descending sort (:84-89): one wave
 //      bisects the gathered keys (starting below the common high bits of the
 //      bound and the maximum);
@@ -28,6 +33,7 @@
 // The host keeps the mt19937_64 draw, so the sampled token is the reference's.
 #include "common.hpp"
 
+#include <cfloat>
 #include <climits>
 
 namespace levo_hip {
@@ -58,18 +64,44 @@ __device__ __forceinline__ float cand_weight(float v, float m, float inv_t) {
     return __expf((v - m) * inv_t);
 }
 
+// Per-thread online softmax statistics over groups of four items: tmax is the
+// running maximum (fmaxf skips NaN), sh the shift of the sum (the running
+// maximum, or -FLT_MAX while every value so far is -inf, so that -inf values
+// contribute exp2(-inf) = 0 instead of NaN), s = sum of exp2((v - sh) * c2).
+// A NaN value, or a +inf one, makes s NaN.
+struct row_stats {
+    float tmax = -INFINITY;
+    float sh = -FLT_MAX;
+    float s = 0.0f;
+};
+
+__device__ __forceinline__ void stats_add4(row_stats & st, float r0, float r1, float r2, float r3, float c2) {
+    const float nm = fmaxf(st.tmax, fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)));
+    const float nsh = fmaxf(nm, -FLT_MAX);
+    float acc = st.s * __builtin_amdgcn_exp2f((st.sh - nsh) * c2);
+    acc += __builtin_amdgcn_exp2f((r0 - nsh) * c2);
+    acc += __builtin_amdgcn_exp2f((r1 - nsh) * c2);
+    acc += __builtin_amdgcn_exp2f((r2 - nsh) * c2);
+    acc += __builtin_amdgcn_exp2f((r3 - nsh) * c2);
+    st.tmax = nm;
+    st.sh = nsh;
+    st.s = acc;
+}
+
 // l = u + s * (c - u) for every id this thread owns: id of item i is
-// (i / VEC) * 256 * VEC + tid * VEC + i % VEC.
-template <int VEC, int NCH, bool kCfg>
-__device__ __forceinline__ void load_row(float (&v)[VEC * NCH], const float * __restrict__ crow,
-                                         const float * __restrict__ urow, int V, int tid, float s) {
+// (i / VEC) * 256 * VEC + tid * VEC + i % VEC. Every load is issued before the
+// first is consumed; each chunk is folded into the statistics as it arrives.
+// kFull: the row fills every item (V == 256 * VEC * NCH), no masking.
+template <int VEC, int NCH, bool kCfg, bool kFull>
+__device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, const float * __restrict__ crow,
+                                         const float * __restrict__ urow, int V, int tid, float s, float c2) {
     constexpr int kChunk = kThreads * VEC;
     if constexpr (VEC == 4) {
         f32x4 c[NCH], u[NCH];
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
             const int base = ch * kChunk + tid * 4;
-            const int off = base < V ? base : 0;  // row_pitch % 4 == 0: in bounds
+            const int off = kFull || base < V ? base : 0;  // row_pitch % 4 == 0: in bounds
             c[ch] = *reinterpret_cast<const f32x4 *>(crow + off);
             if constexpr (kCfg) u[ch] = *reinterpret_cast<const f32x4 *>(urow + off);
         }
@@ -82,8 +114,13 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], const float * __
 #pragma unroll
                 for (int q = 0; q < 4; ++q) r[q] = w[q] + s * (r[q] - w[q]);
             }
+            if constexpr (!kFull) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[ch * 4 + q] = base + q < V ? r[q] : -INFINITY;
+                for (int q = 0; q < 4; ++q) r[q] = base + q < V ? r[q] : -INFINITY;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[ch * 4 + q] = r[q];
+            stats_add4(st, r[0], r[1], r[2], r[3], c2);
         }
     } else {
         float c[NCH], u[NCH];
@@ -99,6 +136,13 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], const float * __
             const int base = ch * kChunk + tid;
             const float r = kCfg ? u[ch] + s * (c[ch] - u[ch]) : c[ch];
             v[ch] = base < V ? r : -INFINITY;
+        }
+#pragma unroll
+        for (int g = 0; g < NCH; g += 4) {
+            const float r1 = g + 1 < NCH ? v[g + 1] : -INFINITY;
+            const float r2 = g + 2 < NCH ? v[g + 2] : -INFINITY;
+            const float r3 = g + 3 < NCH ? v[g + 3] : -INFINITY;
+            stats_add4(st, v[g], r1, r2, r3, c2);
         }
     }
 }
@@ -150,12 +194,7 @@ __device__ __forceinline__ void bitmap_prefix(row_lds<kWords> & L, int words) {
             cnt[j] = w < words ? __popc(L.sel[w]) : 0;
             local += cnt[j];
         }
-        int incl = local;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
+        const int incl = wave_inclusive_scan_i32(local);
         int run = incl - local;
 #pragma unroll
         for (int j = 0; j < kWPL; ++j) {
@@ -244,11 +283,12 @@ __device__ __noinline__ void select_general(const levo_hip_sample_args a, row_ld
     }
 }
 
-template <int VEC, int NCH>
+template <int VEC, int NCH, bool kFull>
 __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sample_args a) {
     constexpr int ITEMS = VEC * NCH;
     constexpr int kChunk = kThreads * VEC;                // ids per chunk
     constexpr int kWords = (ITEMS * kThreads + 31) / 32;  // bitmap words covering the row
+    constexpr float kLog2e = 1.44269504088896340736f;
     __shared__ row_lds<kWords> L;
 
     const int tid = threadIdx.x;
@@ -260,19 +300,27 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
     int k = a.top_k[stream];
     if (k <= 0 || k >= V) k = 0;  // keep every id
     const int words = (V + 31) / 32;
+    // exp2 scale of the streamed sum: log2(e) / T when the log-sum-exp is
+    // wanted (the temperature is then validated), log2(e) otherwise (the sum
+    // then only detects NaN / +inf)
+    const float c2 = a.row_lse ? (1.0f / a.temperature) * kLog2e : kLog2e;
 
-    // ---- A. load + CFG -------------------------------------------------------
+    // ---- A. load + CFG + streamed statistics -----------------------------------------
     // All loads of the row are issued before any is consumed (no branch between
     // them: ids past V read a clamped, valid address and are masked to -inf).
     float v[ITEMS];
+    row_stats st;
     const float * crow = a.cond + row * a.row_pitch;
-    if (a.uncond) load_row<VEC, NCH, true>(v, crow, a.uncond + row * a.row_pitch, V, tid, a.cfg_scale);
-    else load_row<VEC, NCH, false>(v, crow, crow, V, tid, a.cfg_scale);
+    if (a.uncond) load_row<VEC, NCH, true, kFull>(v, st, crow, a.uncond + row * a.row_pitch, V, tid, a.cfg_scale, c2);
+    else load_row<VEC, NCH, false, kFull>(v, st, crow, crow, V, tid, a.cfg_scale, c2);
     for (int i = tid; i < words; i += kThreads) L.sel[i] = 0u;
 
     const bool use_pen = a.recent != nullptr && a.n_recent > 0;
     const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
-    if (use_pen || use_ign) {  // uniform per workgroup
+    const bool adjusted = use_pen || use_ign;  // uniform per workgroup
+    bool has_nan;  // a NaN (exact), or in the streamed case possibly a +inf
+    float tmax;
+    if (adjusted) {
         for (int i = tid; i < words; i += kThreads) {
             L.pen[i] = 0u;
             L.ign[i] = 0u;
@@ -302,17 +350,20 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
                 if (L.ign[idx >> 5] & bit) v[i] = -INFINITY;
             }
         }
-    }
-
-    // NaN check and thread maximum (fmaxf skips NaN; NaN is flagged separately)
-    const bool tvalid = tid * VEC < V;
-    bool has_nan = false;
-    float tmax = -INFINITY;
+        // the streamed statistics predate the adjustment: exact NaN check and
+        // thread maximum (fmaxf skips NaN); the log-sum-exp is recomputed below
+        has_nan = false;
+        tmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-        has_nan = has_nan || __builtin_isnan(v[i]);
-        tmax = fmaxf(tmax, v[i]);
+        for (int i = 0; i < ITEMS; ++i) {
+            has_nan = has_nan || __builtin_isnan(v[i]);
+            tmax = fmaxf(tmax, v[i]);
+        }
+    } else {
+        tmax = st.tmax;
+        has_nan = __builtin_isnan(st.s);
     }
+    const bool tvalid = tid * VEC < V;
 
     // ---- B. wave maximum and the per-wave lower bound of the k-th value ----------
     const float wm = wave_max_f32(tmax);
@@ -342,6 +393,18 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
         low = fminf(low, L.wlow[w]);
         row_nan = row_nan || L.wnan[w] != 0;
     }
+    if (row_nan && !adjusted) {  // uniform: a streamed sum went NaN; NaN or +inf?
+        bool hn = false;
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) hn = hn || __builtin_isnan(v[i]);
+        hn = __ballot(hn) != 0;
+        __syncthreads();  // every wave has read the flags above
+        if (lane == 0) L.wnan[wave] = hn ? 1 : 0;
+        __syncthreads();
+        row_nan = false;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) row_nan = row_nan || L.wnan[w] != 0;
+    }
     if (row_nan) {  // uniform: the reference throws "logits contain NaN"
         if (tid == 0) {
             a.best[row] = -1;
@@ -369,28 +432,35 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
         }
     }
     const int my_best = tbest;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) tbest = min(tbest, __shfl_xor(tbest, o, 64));
+    tbest = wave_min_i32(tbest);
     if (lane == 0) L.wbest[wave] = tbest;
 
     if (a.row_lse) {
-        float s = 0.0f;
-        const float inv_t = 1.0f / a.temperature;
+        float s;
+        if (adjusted) {
+            const float inv_t = 1.0f / a.temperature;
+            s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < ITEMS; ++i) s += __expf((v[i] - m) * inv_t);  // padding: exp(-inf) = 0
+            for (int i = 0; i < ITEMS; ++i) s += __expf((v[i] - m) * inv_t);  // padding: exp(-inf) = 0
+        } else {
+            // streamed sum, rescaled from the thread's shift to the row maximum
+            // (only a finite m reaches the log-sum-exp below)
+            s = st.s * __builtin_amdgcn_exp2f((st.sh - fmaxf(m, -FLT_MAX)) * c2);
+        }
         s = wave_sum_f32(s);
         if (lane == 0) L.wlse[wave] = s;
     }
 
     // Gather the ids >= low into this wave's segment, in item order. The
-    // running count is wave-uniform, so slots need no atomics.
-    const bool gather = k >= 1 && kw <= 64;
+    // running count is wave-uniform, so slots need no atomics. Padding ids hold
+    // -inf: a row whose bound is -inf takes the general path unless it is full.
+    const bool gather = k >= 1 && kw <= 64 && (kFull || low > -INFINITY);
     if (gather) {
         int base = 0;
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i) {
             const int idx = (i / VEC) * kChunk + tid * VEC + (i % VEC);
-            const bool p = idx < V && v[i] >= low;
+            const bool p = v[i] >= low;
             const uint64_t mask = __ballot(p);
             if (mask) {
                 const int pos = base + rank_in_mask(mask);
@@ -517,7 +587,11 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
 
 template <int VEC, int NCH>
 int launch_sample(const levo_hip_sample_args & a, hipStream_t stream) {
-    cfg_sample_kernel<VEC, NCH><<<static_cast<uint32_t>(a.rows), kThreads, 0, stream>>>(a);
+    const uint32_t grid = static_cast<uint32_t>(a.rows);
+    if (VEC == 4 && a.vocab == int64_t{kThreads} * VEC * NCH)
+        cfg_sample_kernel<VEC, NCH, true><<<grid, kThreads, 0, stream>>>(a);
+    else
+        cfg_sample_kernel<VEC, NCH, false><<<grid, kThreads, 0, stream>>>(a);
     return launch_status("levo_hip_cfg_sample");
 }
 

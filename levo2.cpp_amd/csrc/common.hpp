@@ -80,25 +80,100 @@ __device__ __forceinline__ uint32_t float_key(float v) {
 }
 
 // ---- wave64 reductions ------------------------------------------------------
+// All-reduce over the 64 lanes: DPP within each row of 16 lanes (quad
+// butterflies, then rotations by 4 and 8), then the four row totals are read
+// with v_readlane and combined in a fixed order, so every lane returns the same
+// value. Each DPP step is a few cycles; an LDS-routed shuffle costs ~100.
+
+namespace dpp {
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+constexpr int kRowRor4 = 0x124;  // row_ror:4
+constexpr int kRowRor8 = 0x128;  // row_ror:8
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t mov(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float mov(float v) {
+    return __builtin_bit_cast(float, mov<kCtrl>(__builtin_bit_cast(uint32_t, v)));
+}
+template <int kCtrl>
+__device__ __forceinline__ int mov(int v) {
+    return static_cast<int>(mov<kCtrl>(static_cast<uint32_t>(v)));
+}
+template <int kCtrl>
+__device__ __forceinline__ double mov(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = mov<kCtrl>(static_cast<uint32_t>(b));
+    const uint64_t hi = mov<kCtrl>(static_cast<uint32_t>(b >> 32));
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+__device__ __forceinline__ uint32_t lane(uint32_t v, int l) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
+}
+__device__ __forceinline__ float lane(float v, int l) {
+    return __builtin_bit_cast(float, lane(__builtin_bit_cast(uint32_t, v), l));
+}
+__device__ __forceinline__ int lane(int v, int l) { return static_cast<int>(lane(static_cast<uint32_t>(v), l)); }
+__device__ __forceinline__ double lane(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = lane(static_cast<uint32_t>(b), l);
+    const uint64_t hi = lane(static_cast<uint32_t>(b >> 32), l);
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+constexpr int kRowShr1 = 0x111;     // row_shr:1
+constexpr int kRowShr2 = 0x112;     // row_shr:2
+constexpr int kRowShr4 = 0x114;     // row_shr:4
+constexpr int kRowShr8 = 0x118;     // row_shr:8
+constexpr int kRowBcast15 = 0x142;  // row_bcast:15
+constexpr int kRowBcast31 = 0x143;  // row_bcast:31
+
+// v from the DPP source lane, or 0 where the source lies outside the row
+// (bound_ctrl) or the destination row is masked off.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ int mov_or_zero(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, kCtrl, kRowMask, 0xF, true);
+}
+
+template <class T, class Op>
+__device__ __forceinline__ T allreduce(T v, Op op) {
+    v = op(v, mov<kQuadXor1>(v));
+    v = op(v, mov<kQuadXor2>(v));
+    v = op(v, mov<kRowRor4>(v));
+    v = op(v, mov<kRowRor8>(v));
+    return op(op(lane(v, 0), lane(v, 16)), op(lane(v, 32), lane(v, 48)));
+}
+}  // namespace dpp
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    return dpp::allreduce(v, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    return dpp::allreduce(v, [](double a, double b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    return dpp::allreduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return dpp::allreduce(v, [](int a, int b) { return a + b; });
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    return dpp::allreduce(v, [](int a, int b) { return a < b ? a : b; });
+}
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele shifts within each row
+// of 16, then row 0's total into row 1 and row 2's into row 3 (row_bcast:15),
+// then lane 31's running total into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ int wave_inclusive_scan_i32(int v) {
+    v += dpp::mov_or_zero<dpp::kRowShr1>(v);
+    v += dpp::mov_or_zero<dpp::kRowShr2>(v);
+    v += dpp::mov_or_zero<dpp::kRowShr4>(v);
+    v += dpp::mov_or_zero<dpp::kRowShr8>(v);
+    v += dpp::mov_or_zero<dpp::kRowBcast15, 0xA>(v);
+    v += dpp::mov_or_zero<dpp::kRowBcast31, 0xC>(v);
     return v;
 }
 

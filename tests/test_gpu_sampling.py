@@ -204,6 +204,28 @@ def test_nan_and_degenerate_rows(hip, binding, dev, oracle):
     assert out["probs"][2, 0] == 1.0 and np.all(out["probs"][2, 1:] == 0.0)  # falls back to best
 
 
+@pytest.mark.parametrize("V", [4096, 5000, 16384])
+def test_special_values_without_lists(hip, binding, dev, oracle, V):
+    """NaN, +inf and -inf runs on rows with no penalty or ignore list: the
+    streamed softmax statistics must send NaN and +inf rows to the exact check,
+    and -inf prefixes (a thread's first values all -inf) must not poison the
+    log-sum-exp. V = 4096 / 16384 fill every item; 5000 leaves padding."""
+    cond = _f16_logits(oracle, 7, V, 1200 + V)
+    cond[0, V // 2] = np.nan
+    cond[1, [7, V - 1]] = np.inf
+    cond[2, :2000] = -np.inf
+    cond[3, :] = -np.inf
+    ids = np.arange(V)
+    cond[4, (ids % 1024) < 8] = -np.inf   # each thread's first group of ids
+    cond[5, 0] = -np.inf
+    out = run_sample(hip, binding, dev, cond, None, top_k=[50], n_streams=1, capacity=V)
+    assert out["best"][0] == -1 and out["count"][0] == -1
+    check_rows(out, cond, [50] * 7, oracle, 0.9, rows=[2, 4, 5, 6])
+    check_rows(out, cond, [50] * 7, oracle, 0.9, rows=[1, 3], lse=False)
+    assert out["lse"][1] == np.inf and out["lse"][3] == -np.inf
+    assert out["count"][3] == V and out["best"][3] == 0
+
+
 def test_capacity_overflow_reports_full_count(hip, binding, dev, oracle):
     V = 3000
     cond = _f16_logits(oracle, 2, V, 1200)
