@@ -204,6 +204,26 @@ def test_nan_and_degenerate_rows(hip, binding, dev, oracle):
     assert out["probs"][2, 0] == 1.0 and np.all(out["probs"][2, 1:] == 0.0)  # falls back to best
 
 
+@pytest.mark.parametrize("V,pitch", [(20000, 20000), (32768, 32768), (24001, 24001), (18432, 18432),
+                                     (16896, 16897)])
+def test_large_vocabularies(hip, binding, dev, oracle, V, pitch):
+    """Rows above the LeLM codebook up to the 32768-id limit: the vector path
+    with 64 logits per thread (full and padded), the largest 36-per-thread
+    shape, and the scalar path (unaligned pitch) at its two largest shapes;
+    with CFG, top-k 50 / 1 and planted ties at the maximum."""
+    R = 6
+    cond = np.zeros((R, pitch), np.float32)
+    uncond = np.zeros((R, pitch), np.float32)
+    cond[:, :V] = _f16_logits(oracle, R, V, 1300 + V)
+    uncond[:, :V] = _f16_logits(oracle, R, V, 1400 + V)
+    cond[1, [5, V - 3]] = 40.0   # tied maxima after CFG (u + 1.5 (c - u) equal only if u equal)
+    uncond[1, [5, V - 3]] = 0.0
+    out = run_sample(hip, binding, dev, cond, uncond, top_k=[50, 1], n_streams=2, vocab=V, pitch=pitch)
+    adjusted = oracle.apply_cfg(cond[:, :V].copy(), uncond[:, :V].copy(), 1.5)
+    check_rows(out, adjusted, [50, 1] * (R // 2), oracle, 0.9)
+    assert out["best"][1] == 5 and out["count"][1] == 2
+
+
 @pytest.mark.parametrize("V", [4096, 5000, 16384])
 def test_special_values_without_lists(hip, binding, dev, oracle, V):
     """NaN, +inf and -inf runs on rows with no penalty or ignore list: the
