@@ -1,8 +1,8 @@
 // Fused residual add + RMSNorm / LayerNorm, one 4-wave workgroup per row.
 //
 // Every load of the row (x, delta, weight, bias) is issued up front with
-// dwordx4 accesses, the row stays in registers, is reduced with cross-lane
-// shuffles and one LDS exchange between the four waves, normalised and
+// dwordx4 accesses, the row stays in registers, is reduced with DPP cross-lane
+// steps and one LDS exchange between the four waves, normalised and
 // written once. The reduction accumulates in double like ggml-cpu's ggml_float
 // row sums, so the F32 mean / variance (and hence every rounding point after
 // it) matches the CPU chain.
