@@ -5,9 +5,12 @@
 // never written back. Everything the sampler needs comes from the
 // register-resident row, touching each value only with cheap compares:
 //   A. while the loads of later chunks are still in flight, each chunk is
-//      combined and folded into per-thread online softmax statistics (running
-//      maximum and a rescaled sum of exp2((l - max) * log2(e) / T)); a NaN or
-//      +inf makes the sum NaN, which sends the row to an exact re-check.
+//      combined and folded into per-thread softmax statistics: the running
+//      maximum and a sum of exp2((l - shift) * log2(e) / T) with a fixed
+//      shift (the thread's first group maximum), one FMA and one exp2 per
+//      value; a NaN, +inf or overflowed sum is summed again from the thread
+//      maximum, and a NaN or +inf logit then leaves it NaN, which sends the row
+//      to an exact re-check.
 //      The unique-token repetition penalty and stream-0 ignore list are applied
 //      through LDS bitmaps (src/levo-sampling.cpp:39-47, :137-147); such rows
 //      recompute their statistics after the adjustment;
@@ -19,17 +22,20 @@
 //      full-vocabulary log-sum-exp of l/T from the streamed statistics, and a
 //      gather of the few ids at or above the bound (value and id, one compare
 //      per id) into per-wave LDS segments; the row's registers are dead after
-//      this point;
-//   D. the exact k-th value of the stable descending sort (:84-89): one wave
+//      this point, and waves 1-7 leave (wave 1 writes the row's max, first
+//      maximum and log-sum-exp), so a new row can start in their registers;
+//   D. the exact k-th value of the stable descending sort (:84-89): wave 0
 //      bisects the gathered keys (starting below the common high bits of the
 //      bound and the maximum);
 //   E. every gathered id >= that value (ties kept, as the reference keeps
 //      them) is marked in an LDS bitmap; a popcount prefix scan over the
 //      bitmap gives each candidate its slot in ascending id order, and its
 //      logit and probability exp((l - max)/T) / sum (:98-107; F32 weights,
-//      double sum) are written there.
+//      double sum) are written there. D and E are one wave's work, with no
+//      workgroup barrier.
 // k == 0 (keep all), k > 256, or more tied candidates than the segments hold
-// take select_general, which re-reads the row instead of holding it.
+// take select_general (the whole workgroup), which re-reads the row instead
+// of holding it.
 // The host keeps the mt19937_64 draw, so the sampled token is the reference's.
 #include "common.hpp"
 
@@ -52,10 +58,19 @@ __device__ __forceinline__ float float_of_key(uint32_t k) {
     return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// k-th largest (1 <= k <= 64) of the 64 lane keys of this wave.
+// k-th largest (1 <= k <= 64) of the 64 lane keys of this wave; 0 when fewer
+// than k lanes hold a non-zero key. The answer lies between the smallest
+// non-zero key and the largest, so the bisection starts below their common
+// high bits (about 24 steps instead of 32 for logits of one magnitude).
 __device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, int k) {
-    uint32_t prefix = 0;
-    for (int bit = 31; bit >= 0; --bit) {
+    if (static_cast<int>(__popcll(__ballot(key != 0u))) < k) return 0u;
+    const uint32_t hi = dpp::allreduce(key, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+    const uint32_t lo = dpp::allreduce(key == 0u ? ~0u : key, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+    const uint32_t diff = lo ^ hi;
+    if (diff == 0u) return lo;
+    const int top = 31 - __builtin_clz(diff);
+    uint32_t prefix = lo & ~((2u << top) - 1u);
+    for (int bit = top; bit >= 0; --bit) {
         const uint32_t cand = prefix | (1u << bit);
         if (static_cast<int>(__popcll(__ballot(key >= cand))) >= k) prefix = cand;
     }
@@ -67,27 +82,48 @@ __device__ __forceinline__ float cand_weight(float v, float m, float inv_t) {
     return __expf((v - m) * inv_t);
 }
 
-// Per-thread online softmax statistics over groups of four items: tmax is the
-// running maximum (fmaxf skips NaN), sh the shift of the sum (the running
-// maximum, or -FLT_MAX while every value so far is -inf, so that -inf values
-// contribute exp2(-inf) = 0 instead of NaN), s = sum of exp2((v - sh) * c2).
-// A NaN value, or a +inf one, makes s NaN.
+// Per-thread softmax statistics over groups of four items: tmax is the
+// running maximum (fmaxf skips NaN); sh is a fixed shift, the largest value of
+// the thread's first group (or -FLT_MAX if it is all -inf), and
+// s = sum of exp2((v - sh) * c2), each term one FMA and one exp2 (no
+// rescaling while the row streams in). A NaN value makes s NaN, +inf makes it
+// +inf; so does a value so far above the shift that its term overflows, which
+// finish_stats then resolves by summing again from the thread maximum.
 struct row_stats {
     float tmax = -INFINITY;
     float sh = -FLT_MAX;
+    float nsc = 0.0f;  // -sh * c2
     float s = 0.0f;
 };
 
+template <bool kFirst>
 __device__ __forceinline__ void stats_add4(row_stats & st, float r0, float r1, float r2, float r3, float c2) {
-    const float nm = fmaxf(st.tmax, fmaxf(fmaxf(r0, r1), fmaxf(r2, r3)));
-    const float nsh = fmaxf(nm, -FLT_MAX);
-    float acc = st.s * __builtin_amdgcn_exp2f((st.sh - nsh) * c2);
-    acc += __builtin_amdgcn_exp2f((r0 - nsh) * c2);
-    acc += __builtin_amdgcn_exp2f((r1 - nsh) * c2);
-    acc += __builtin_amdgcn_exp2f((r2 - nsh) * c2);
-    acc += __builtin_amdgcn_exp2f((r3 - nsh) * c2);
-    st.tmax = nm;
-    st.sh = nsh;
+    const float gm = fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+    if constexpr (kFirst) {
+        st.sh = fmaxf(gm, -FLT_MAX);
+        st.nsc = -st.sh * c2;
+    }
+    st.tmax = fmaxf(st.tmax, gm);
+    float acc = st.s;
+    acc += __builtin_amdgcn_exp2f(__builtin_fmaf(r0, c2, st.nsc));
+    acc += __builtin_amdgcn_exp2f(__builtin_fmaf(r1, c2, st.nsc));
+    acc += __builtin_amdgcn_exp2f(__builtin_fmaf(r2, c2, st.nsc));
+    acc += __builtin_amdgcn_exp2f(__builtin_fmaf(r3, c2, st.nsc));
+    st.s = acc;
+}
+
+// A sum that is not finite, or whose shift lies more than 2^64 (in terms)
+// below the thread maximum, is summed again from the thread maximum. That
+// either makes it finite (an overflow of the fixed shift) or shows a NaN or
+// +inf value (the sum is then NaN); and the thread's largest term can then
+// only vanish in the rescale to the row maximum when it is below 2^-85 of it.
+template <int ITEMS>
+__device__ __forceinline__ void finish_stats(row_stats & st, const float (&v)[ITEMS], float c2) {
+    if (__builtin_isfinite(st.s) && (st.tmax - st.sh) * c2 <= 64.0f) return;
+    st.sh = fmaxf(st.tmax, -FLT_MAX);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) acc += __builtin_amdgcn_exp2f((v[i] - st.sh) * c2);
     st.s = acc;
 }
 
@@ -123,8 +159,10 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, 
             }
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[ch * 4 + q] = r[q];
-            stats_add4(st, r[0], r[1], r[2], r[3], c2);
+            if (ch == 0) stats_add4<true>(st, r[0], r[1], r[2], r[3], c2);
+            else stats_add4<false>(st, r[0], r[1], r[2], r[3], c2);
         }
+        finish_stats(st, v, c2);
     } else {
         float c[NCH], u[NCH];
 #pragma unroll
@@ -145,9 +183,11 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, 
             const float r1 = g + 1 < NCH ? v[g + 1] : -INFINITY;
             const float r2 = g + 2 < NCH ? v[g + 2] : -INFINITY;
             const float r3 = g + 3 < NCH ? v[g + 3] : -INFINITY;
-            stats_add4(st, v[g], r1, r2, r3, c2);
+            if (g == 0) stats_add4<true>(st, v[g], r1, r2, r3, c2);
+            else stats_add4<false>(st, v[g], r1, r2, r3, c2);
         }
     }
+    finish_stats(st, v, c2);
 }
 
 // Shared-memory layout of one row's workgroup.
@@ -160,6 +200,7 @@ struct row_lds {
     float cv[kWaves][kSegCap];  // gathered candidate values, one segment per wave
     int ci[kWaves][kSegCap];    // and their ids
     float wmax[kWaves];
+    float wbv[kWaves];   // each wave's value at its first maximum
     float wlow[kWaves];
     int wnan[kWaves];
     int wbest[kWaves];
@@ -183,30 +224,51 @@ __device__ __forceinline__ float adjusted_logit(const levo_hip_sample_args & a, 
     return v;
 }
 
-// Exclusive prefix of the bitmap popcounts (wave 0), total candidate count.
+// Exclusive prefix of the bitmap popcounts into L.prefix; returns the total
+// candidate count (also stored in L.total). Called by one whole wave; the
+// fences keep its LDS accesses in program order around the cross-lane reads.
 template <int kWords>
-__device__ __forceinline__ void bitmap_prefix(row_lds<kWords> & L, int words) {
+__device__ __forceinline__ int wave_bitmap_prefix(row_lds<kWords> & L, int words) {
     constexpr int kWPL = (kWords + 63) / 64;  // words per lane
     const int lane = threadIdx.x & 63;
-    if (threadIdx.x < 64) {
-        int cnt[kWPL];
-        int local = 0;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    int cnt[kWPL];
+    int local = 0;
 #pragma unroll
-        for (int j = 0; j < kWPL; ++j) {
-            const int w = lane * kWPL + j;
-            cnt[j] = w < words ? __popc(L.sel[w]) : 0;
-            local += cnt[j];
-        }
-        const int incl = wave_inclusive_scan_i32(local);
-        int run = incl - local;
-#pragma unroll
-        for (int j = 0; j < kWPL; ++j) {
-            const int w = lane * kWPL + j;
-            if (w < words) L.prefix[w] = static_cast<uint32_t>(run);
-            run += cnt[j];
-        }
-        if (lane == 63) L.total = incl;
+    for (int j = 0; j < kWPL; ++j) {
+        const int w = lane * kWPL + j;
+        cnt[j] = w < words ? __popc(L.sel[w]) : 0;
+        local += cnt[j];
     }
+    const int incl = wave_inclusive_scan_i32(local);
+    int run = incl - local;
+#pragma unroll
+    for (int j = 0; j < kWPL; ++j) {
+        const int w = lane * kWPL + j;
+        if (w < words) L.prefix[w] = static_cast<uint32_t>(run);
+        run += cnt[j];
+    }
+    const int total = dpp::lane(incl, 63);
+    if (lane == 63) L.total = total;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    return total;
+}
+
+// The same, by wave 0 of a workgroup that synchronizes afterwards.
+template <int kWords>
+__device__ __forceinline__ void bitmap_prefix(row_lds<kWords> & L, int words) {
+    if (threadIdx.x < 64) wave_bitmap_prefix(L, words);
+}
+
+// log sum_v exp(l_v / T) of the row from the per-wave sums of exp((l - m) / T).
+template <int kWords>
+__device__ __forceinline__ float row_log_sum_exp(const row_lds<kWords> & L, float m, float temperature) {
+    float s = L.wlse[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) s += L.wlse[w];
+    if (m == -INFINITY) return -INFINITY;
+    if (m == INFINITY) return INFINITY;
+    return m / temperature + logf(s);
 }
 
 // Slot of a selected id in ascending id order.
@@ -287,7 +349,7 @@ __device__ __noinline__ void select_general(const levo_hip_sample_args a, row_ld
 }
 
 template <int VEC, int NCH, bool kFull>
-__global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sample_args a) {
+__global__ __launch_bounds__(kThreads, 7) void cfg_sample_kernel(const levo_hip_sample_args a) {
     constexpr int ITEMS = VEC * NCH;
     constexpr int kChunk = kThreads * VEC;                // ids per chunk
     constexpr int kWords = (ITEMS * kThreads + 31) / 32;  // bitmap words covering the row
@@ -437,6 +499,7 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
     const int my_best = tbest;
     tbest = wave_min_i32(tbest);
     if (lane == 0) L.wbest[wave] = tbest;
+    if (my_best == tbest && my_best != INT_MAX) L.wbv[wave] = tbest_v;
 
     if (a.row_lse) {
         float s;
@@ -479,8 +542,14 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
     __syncthreads();  // barrier 2
 
     int best = L.wbest[0];
+    int best_wave = 0;
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) best = min(best, L.wbest[w]);
+    for (int w = 1; w < kWaves; ++w) {
+        if (L.wbest[w] < best) {
+            best = L.wbest[w];
+            best_wave = w;
+        }
+    }
     int seg_start[kWaves + 1];
     seg_start[0] = 0;
     bool fits = gather;
@@ -493,101 +562,112 @@ __global__ __launch_bounds__(kThreads) void cfg_sample_kernel(const levo_hip_sam
     const int ncand = seg_start[kWaves];
     fits = fits && ncand <= kBisCap;
 
-    if (!fits) {
+    if (!fits) {  // uniform: every wave takes the general path
         select_general(a, L, row, V, k, m, best, use_pen, use_ign);
+        if (my_best == best && a.row_max) a.row_max[row] = tbest_v;
+        if (tid == 0) {
+            a.best[row] = best;
+            a.count[row] = L.total;
+            if (a.row_lse) a.row_lse[row] = row_log_sum_exp(L, m, a.temperature);
+        }
+        return;
+    }
+
+    // The candidates are in LDS: the other waves leave, so that their
+    // registers take the next row's loads while wave 0 finishes this one
+    // (no workgroup barrier after this point). Wave 1 writes the row's
+    // scalars on its way out.
+    if (wave != 0) {
+        if (wave == 1 && lane == 0) {
+            a.best[row] = best;
+            if (a.row_max) a.row_max[row] = L.wbv[best_wave];
+            if (a.row_lse) a.row_lse[row] = row_log_sum_exp(L, m, a.temperature);
+        }
+        return;
+    }
+
+    // ---- D. exact k-th value (key) among the gathered candidates ------------------
+    // Candidate j = lane + 64 * s in segment order sits at flat index
+    // j + delta[w] of the segment array (delta[w] = w * kSegCap - seg_start[w]);
+    // every load is issued before any is used, with no branch between them.
+    constexpr int kSlots = kBisCap / 64;
+    float cval[kSlots];
+    int cidx[kSlots];
+    uint32_t keys[kSlots];
+    bool valid[kSlots];
+    {
+        const float * cv = &L.cv[0][0];
+        const int * ci = &L.ci[0][0];
+        int flat[kSlots];
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            const int j = lane + 64 * s;
+            int delta = -seg_start[0];
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) delta = j >= seg_start[q] ? q * kSegCap - seg_start[q] : delta;
+            valid[s] = j < ncand;
+            flat[s] = valid[s] ? j + delta : 0;
+        }
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            cval[s] = cv[flat[s]];
+            cidx[s] = ci[flat[s]];
+        }
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) keys[s] = valid[s] ? float_key(cval[s]) : 0u;
+    }
+    uint32_t tau;
+    if (k == 1) {
+        tau = float_key(m);
     } else {
-        // ---- D. exact k-th value (key) among the gathered candidates -------------
-        uint32_t tau;
-        if (k == 1) {
-            tau = float_key(m);
-        } else {
-            if (wave == 0) {
-                uint32_t keys[kBisCap / 64];
+        // tau lies in [low, m]: it shares the common high bits of their keys
+        const uint32_t lo_key = low == -INFINITY ? 0u : float_key(low);
+        const uint32_t hi_key = float_key(m);
+        const uint32_t diff = lo_key ^ hi_key;
+        const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
+        uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
+        for (int bit = top; bit >= 0; --bit) {
+            const uint32_t cand = prefix | (1u << bit);
+            int cnt = 0;
 #pragma unroll
-                for (int s = 0; s < kBisCap / 64; ++s) {
-                    const int j = lane + 64 * s;
-                    uint32_t key = 0u;
-                    if (j < ncand) {
-                        int w = 0;
-#pragma unroll
-                        for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
-                        key = float_key(L.cv[w][j - seg_start[w]]);
-                    }
-                    keys[s] = key;
-                }
-                // tau lies in [low, m]: it shares the common high bits of their keys
-                const uint32_t lo_key = low == -INFINITY ? 0u : float_key(low);
-                const uint32_t hi_key = float_key(m);
-                const uint32_t diff = lo_key ^ hi_key;
-                const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
-                uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
-                for (int bit = top; bit >= 0; --bit) {
-                    const uint32_t cand = prefix | (1u << bit);
-                    int cnt = 0;
-#pragma unroll
-                    for (int s = 0; s < kBisCap / 64; ++s) cnt += static_cast<int>(__popcll(__ballot(keys[s] >= cand)));
-                    if (cnt >= k) prefix = cand;
-                }
-                if (lane == 0) L.tau = prefix;
-            }
-            __syncthreads();  // barrier 3
-            tau = L.tau;
+            for (int s = 0; s < kSlots; ++s) cnt += static_cast<int>(__popcll(__ballot(keys[s] >= cand)));
+            if (cnt >= k) prefix = cand;
         }
-
-        // ---- E. mark the candidates >= tau; weight sum -------------------------------
-        const bool want_probs = a.cand_probs != nullptr;
-        const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
-        double z = 0.0;
-        for (int j = tid; j < ncand; j += kThreads) {
-            int w = 0;
-#pragma unroll
-            for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
-            const float cv = L.cv[w][j - seg_start[w]];
-            if (float_key(cv) >= tau) {
-                const int idx = L.ci[w][j - seg_start[w]];
-                atomicOr(&L.sel[idx >> 5], 1u << (idx & 31));
-                if (want_probs) z += static_cast<double>(cand_weight(cv, m, inv_t));
-            }
-        }
-        z = wave_sum_f64(z);
-        if (lane == 0) L.wz[wave] = z;
-        __syncthreads();  // barrier 4
-        bitmap_prefix(L, words);
-        z = 0.0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) z += L.wz[w];
-        const bool z_ok = z > 0.0 && __builtin_isfinite(z);
-        const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
-        __syncthreads();  // barrier 5
-
-        // ---- write the candidates in ascending id order ------------------------------
-        for (int j = tid; j < ncand; j += kThreads) {
-            int w = 0;
-#pragma unroll
-            for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
-            const float cv = L.cv[w][j - seg_start[w]];
-            if (float_key(cv) >= tau) {
-                const int idx = L.ci[w][j - seg_start[w]];
-                write_candidate(a, row, slot_of(L, idx), idx, cv, best, m, inv_t, z_ok, inv_z);
-            }
-        }
+        tau = prefix;
     }
 
-    if (my_best == best && a.row_max) a.row_max[row] = tbest_v;
-    if (tid == 0) {
-        a.best[row] = best;
-        a.count[row] = L.total;
-        if (a.row_lse) {
-            float s = L.wlse[0];
+    // ---- E. mark the candidates >= tau in the id bitmap; weight sum ---------------
+    const bool want_probs = a.cand_probs != nullptr;
+    const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
+    bool take[kSlots];
+    float wgt[kSlots];
+    double z = 0.0;
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) s += L.wlse[w];
-            float lse;
-            if (m == -INFINITY) lse = -INFINITY;
-            else if (m == INFINITY) lse = INFINITY;
-            else lse = m / a.temperature + logf(s);
-            a.row_lse[row] = lse;
+    for (int s = 0; s < kSlots; ++s) {
+        take[s] = keys[s] >= tau && valid[s];
+        wgt[s] = want_probs && take[s] ? cand_weight(cval[s], m, inv_t) : 0.0f;
+        if (take[s]) atomicOr(&L.sel[cidx[s] >> 5], 1u << (cidx[s] & 31));
+        z += static_cast<double>(wgt[s]);
+    }
+    z = wave_sum_f64(z);
+    const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+    const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
+    // one wave: its LDS operations complete in issue order, so the prefix
+    // pass below reads every bit marked above
+    const int total = wave_bitmap_prefix(L, words);
+
+    // ---- write the candidates in ascending id order --------------------------------
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) {
+        const int pos = take[s] ? slot_of(L, cidx[s]) : a.capacity;
+        if (pos < a.capacity) {
+            const int64_t o = row * a.capacity + pos;
+            a.cand_ids[o] = cidx[s];
+            if (a.cand_logits) a.cand_logits[o] = cval[s];
+            if (want_probs) a.cand_probs[o] = z_ok ? wgt[s] * inv_z : (cidx[s] == best ? 1.0f : 0.0f);
         }
     }
+    if (lane == 0) a.count[row] = total;
 }
 
 template <int VEC, int NCH>

@@ -34,6 +34,9 @@ int allow_dynamic_lds(const void * kernel, int bytes, const char * what);
 
 inline hipStream_t as_hip(levo_hip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Compute units of the current device (cached per device); 0 if the query fails.
+int device_cu_count();
+
 // K-quant helpers shared by the quantizer entry points (kquant.hip).
 bool is_kquant(levo_hip_type type);
 int64_t kquant_block_bytes(levo_hip_type type);  // Q4_K / Q5_K / Q6_K / Q8_K per 256 values; 0 otherwise
@@ -178,6 +181,14 @@ __device__ __forceinline__ int wave_inclusive_scan_i32(int v) {
 }
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Workgroup barrier that orders LDS accesses only: global loads in flight
+// (a prefetch of the next row) and earlier global stores are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // Bits of lanes below the calling lane in a 64-bit ballot mask.
 __device__ __forceinline__ int rank_in_mask(uint64_t mask) {
