@@ -276,10 +276,13 @@ extern "C" int levo_hip_snake_beta_batch(const levo_hip_snake_job * jobs, int n_
     using namespace levo_hip;
     LEVO_REQUIRE(n_jobs >= 0 && n_jobs <= kMaxBatchJobs, "snake_beta_batch: 0 to %d jobs", kMaxBatchJobs);
     LEVO_REQUIRE(n_jobs == 0 || jobs != nullptr, "snake_beta_batch: null job list");
+    // Every job is checked before anything is launched, so a rejected call
+    // leaves every output untouched.
     batch_args args{};
     args.n = 0;
     uint64_t tiles = 0;
     size_t lds = 0;
+    bool scalar[kMaxBatchJobs] = {};
     for (int i = 0; i < n_jobs; ++i) {
         const levo_hip_snake_job & jb = jobs[i];
         LEVO_REQUIRE(jb.channels >= 0 && jb.time >= 0, "LeVo audio graph: SnakeBeta shape must be non-negative");
@@ -297,10 +300,8 @@ extern "C" int levo_hip_snake_beta_batch(const levo_hip_snake_job * jobs, int n_
                      "LeVo audio graph: SnakeBeta tensor exceeds 2^31 elements");
         const bool vec = jb.time % 4 == 0 && jb.x_stride % 4 == 0 && jb.y_stride % 4 == 0 && aligned16(jb.x) &&
                          aligned16(jb.y);
-        if (!vec) {  // the single-job path's scalar kernel
-            const int st = levo_hip_snake_beta(jb.x, jb.x_stride, jb.alpha_log, jb.beta_log, jb.param_type, jb.y,
-                                               jb.y_stride, jb.channels, jb.time, stream);
-            if (st != LEVO_HIP_OK) return st;
+        if (!vec) {  // the single-job path's scalar kernel, launched below
+            scalar[i] = true;
             continue;
         }
         batch_job & b = args.job[args.n++];
@@ -319,6 +320,13 @@ extern "C" int levo_hip_snake_beta_batch(const levo_hip_snake_job * jobs, int n_
         lds = std::max(lds, tile_param_bytes(kThreads * kBatchVPT, t4, jb.channels));
     }
     LEVO_REQUIRE(tiles < (uint64_t{1} << 31), "snake_beta_batch: too many tiles");
+    for (int i = 0; i < n_jobs; ++i) {
+        if (!scalar[i]) continue;
+        const levo_hip_snake_job & jb = jobs[i];
+        const int st = levo_hip_snake_beta(jb.x, jb.x_stride, jb.alpha_log, jb.beta_log, jb.param_type, jb.y,
+                                           jb.y_stride, jb.channels, jb.time, stream);
+        if (st != LEVO_HIP_OK) return st;
+    }
     if (args.n == 0) return LEVO_HIP_OK;
     snake_beta_batch_kernel<<<static_cast<uint32_t>(tiles), kThreads, lds, as_hip(stream)>>>(args);
     return launch_status("levo_hip_snake_beta_batch");

@@ -90,6 +90,8 @@ extern "C" int levo_hip_vae_residual_unit(const float * x, int64_t channels, int
                                           levo_hip_type param_type, float * y, float * h,
                                           levo_hip_stream_t stream) {
     LEVO_REQUIRE(unit != nullptr, "vae_residual_unit: null unit");
+    LEVO_REQUIRE(param_type == LEVO_HIP_TYPE_F32 || param_type == LEVO_HIP_TYPE_F16,
+                 "vae_residual_unit: SnakeBeta parameters must be F32 or F16");
     LEVO_REQUIRE(x != nullptr && y != nullptr && h != nullptr, "vae_residual_unit: null tensor");
     LEVO_REQUIRE(unit->conv_0.weight != nullptr && unit->conv_1.weight != nullptr,
                  "vae_residual_unit: null convolution weight");

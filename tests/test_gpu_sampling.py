@@ -228,20 +228,25 @@ def test_large_vocabularies(hip, binding, dev, oracle, V, pitch):
 def test_special_values_without_lists(hip, binding, dev, oracle, V):
     """NaN, +inf and -inf runs on rows with no penalty or ignore list: the
     streamed softmax statistics must send NaN and +inf rows to the exact check,
-    and -inf prefixes (a thread's first values all -inf) must not poison the
-    log-sum-exp. V = 4096 / 16384 fill every item; 5000 leaves padding."""
-    cond = _f16_logits(oracle, 7, V, 1200 + V)
+    and -inf or very low first groups must not poison the log-sum-exp. A
+    thread's first group is ids 4t .. 4t + 3 (512 threads x 4 ids per chunk,
+    so the first chunk is ids 0 .. 2047); its maximum is the thread's fixed
+    shift. V = 4096 / 16384 fill every item; 5000 leaves padding."""
+    cond = _f16_logits(oracle, 10, V, 1200 + V)
     cond[0, V // 2] = np.nan
     cond[1, [7, V - 1]] = np.inf
     cond[2, :2000] = -np.inf
     cond[3, :] = -np.inf
     ids = np.arange(V)
-    cond[4, (ids % 1024) < 8] = -np.inf   # each thread's first group of ids
+    cond[4, ids < 2048] = -np.inf          # every thread's first group all -inf
     cond[5, 0] = -np.inf
+    cond[7, (ids < 2048) & (ids % 4 == 0)] = -np.inf   # one -inf in every first group
+    cond[8, ids < 2048] = -200.0           # shift so low that later terms overflow
+    cond[9, ids < 2048] = -30.0            # shift 2^48 terms below the later values
     out = run_sample(hip, binding, dev, cond, None, top_k=[50], n_streams=1, capacity=V)
     assert out["best"][0] == -1 and out["count"][0] == -1
-    check_rows(out, cond, [50] * 7, oracle, 0.9, rows=[2, 4, 5, 6])
-    check_rows(out, cond, [50] * 7, oracle, 0.9, rows=[1, 3], lse=False)
+    check_rows(out, cond, [50] * 10, oracle, 0.9, rows=[2, 4, 5, 6, 7, 8, 9])
+    check_rows(out, cond, [50] * 10, oracle, 0.9, rows=[1, 3], lse=False)
     assert out["lse"][1] == np.inf and out["lse"][3] == -np.inf
     assert out["count"][3] == V and out["best"][3] == 0
 

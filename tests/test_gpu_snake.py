@@ -148,3 +148,19 @@ def test_batch_rejects_bad_arguments(hip, dev, binding):
         hip.snake_beta_batch([(x, a, a, x)] * 17)
     with pytest.raises(binding.LevoHipError, match="F32 or F16"):
         hip.snake_beta_batch([(x, a, a, x, 8)])
+
+
+def test_batch_rejected_call_writes_nothing(hip, dev, binding):
+    """A batch whose last job is invalid fails before any job runs: the
+    earlier jobs' outputs (a scalar-path job, T = 1001, and a vector-path job)
+    keep their contents."""
+    import torch
+    xs = torch.ones((4, 1001), device=dev)
+    xv = torch.ones((4, 64), device=dev)
+    a = torch.zeros(4, device=dev)
+    ys = torch.full_like(xs, float("nan"))
+    yv = torch.full_like(xv, float("nan"))
+    with pytest.raises(binding.LevoHipError, match="F32 or F16"):
+        hip.snake_beta_batch([(xs, a, a, ys), (xv, a, a, yv), (xv, a, a, yv, 8)])
+    torch.cuda.synchronize()
+    assert torch.isnan(ys).all() and torch.isnan(yv).all()

@@ -336,3 +336,7 @@ def test_residual_unit_rejects(hip, binding, dev):
         hip.vae_residual_unit(x, 128, 256, u, 0, torch.zeros((128, 256), device=dev), h)
     with pytest.raises(binding.LevoHipError, match="invalid shape"):  # checked before any access
         hip.vae_residual_unit(x, 128, 1 << 37, u, 1, torch.zeros((128, 256), device=dev), h)
+    for channels in (128, 64):  # one-launch and two-launch widths reject it alike
+        with pytest.raises(binding.LevoHipError, match="F32 or F16"):
+            hip.vae_residual_unit(x[:channels], channels, 256, u, 1, torch.zeros((channels, 256), device=dev),
+                                  h[:channels], param_type=8)
