@@ -38,6 +38,7 @@
 // of holding it.
 // The host keeps the mt19937_64 draw, so the sampled token is the reference's.
 #include "common.hpp"
+#include "sample_draw.hpp"
 
 #include <cfloat>
 #include <climits>
@@ -349,7 +350,9 @@ __device__ __noinline__ void select_general(const levo_hip_sample_args a, row_ld
 }
 
 template <int VEC, int NCH, bool kFull>
-__global__ __launch_bounds__(kThreads, 7) void cfg_sample_kernel(const levo_hip_sample_args a) {
+// Seven waves per SIMD (72 VGPRs: three rows per CU) up to 36 logits per
+// thread; the 64-logit rows of the longest vocabularies take four.
+__global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_kernel(const levo_hip_sample_args a) {
     constexpr int ITEMS = VEC * NCH;
     constexpr int kChunk = kThreads * VEC;                // ids per chunk
     constexpr int kWords = (ITEMS * kThreads + 31) / 32;  // bitmap words covering the row
@@ -680,14 +683,522 @@ int launch_sample(const levo_hip_sample_args & a, hipStream_t stream) {
     return launch_status("levo_hip_cfg_sample");
 }
 
+// ---------------------------------------------------------------------------------------
+// Decode-step sampling in one launch (levo_hip_sample_step).
+//
+// A decode step samples a handful of rows, so one workgroup per row would
+// leave all but a few CUs idle and pull each row through one CU. Here every
+// row is split into segments of 4096 ids, one 512-thread workgroup each
+// (8 ids per thread):
+//   1. the workgroup loads its segment, applies CFG, the repetition penalty
+//      and the ignore list (the few list ids inside the segment, found with
+//      wave-uniform compares), and reduces the segment's maximum, first
+//      maximum, NaN flag and softmax sum;
+//   2. it bounds its own k-th largest value from below (per wave the
+//      ceil(k/8)-th largest lane maximum, the smallest of the eight) and hands
+//      the values at or above that bound, the bound and the reductions to the
+//      workspace; any k-th largest of the whole row is at least the largest
+//      of the segment bounds, and every id of the row's top-k set is among
+//      the handed-over candidates;
+//   3. the last segment of a row to arrive (a counter per row) merges them:
+//      the exact k-th value over the candidates (one wave, as phase D above),
+//      the selection in ascending id order (phase E), the row's outputs;
+//   4. the last row to finish (a counter over the rows) makes every row's
+//      draw exactly as levo_hip_sample_draw does.
+// A row whose candidates do not fit (k = 0, very large k, heavy ties) takes
+// select_general in its merging workgroup, from the row itself. The counters
+// start at zero and the kernel leaves them at zero.
+constexpr int kStepPer = 8;                     // ids per thread
+constexpr int kStepSegIds = kThreads * kStepPer; // ids per segment
+constexpr int kStepCandCap = 256;               // candidates a segment hands over
+constexpr int kStepMergeCap = 512;              // candidates the merging wave holds (8 per lane)
+constexpr int kStepWords = kMaxVocab / 32;      // bitmap words of the longest row
+constexpr int kStepMaxSegs = kMaxVocab / kStepSegIds;
+
+struct step_head {
+    float max;      // segment maximum (NaN skipped)
+    float bv;       // value at its first maximum
+    int32_t best;   // first id holding the maximum
+    int32_t nan;    // the segment holds a NaN
+    float low;      // lower bound of the segment's k-th largest value (-inf: none)
+    int32_t count;  // ids at or above `low` (more than kStepCandCap: not handed over)
+    float sum;      // sum over the segment of exp((l - max) / T)
+    int32_t pad;
+};
+
+struct step_seg {
+    step_head h;
+    float val[kStepCandCap];
+    int32_t id[kStepCandCap];
+};
+
+// The workspace starts with a fixed counter region, the same for every row
+// count and vocabulary, so a workspace reused with other shapes keeps its
+// zeroed counters: one arrival counter per row, the last slot counts
+// finished rows.
+constexpr int kStepCounters = 4096;
+constexpr int64_t kStepCounterBytes = kStepCounters * 4;
+constexpr int64_t kStepMaxRows = kStepCounters - 1;
+
+struct step_lds {
+    row_lds<kStepWords> L;
+    float hmax[kStepMaxSegs];
+    float hbv[kStepMaxSegs];
+    int hbest[kStepMaxSegs];
+    int hnan[kStepMaxSegs];
+    float hlow[kStepMaxSegs];
+    int hcount[kStepMaxSegs];
+    float hsum[kStepMaxSegs];
+    int last;
+};
+
+// Id of item q of thread tid in a segment starting at lo: dwordx4 chunks of
+// 4 ids per thread (VEC 4) or single ids kThreads apart (VEC 1); coalesced
+// either way.
+template <int VEC>
+__device__ __forceinline__ int step_id(int lo, int tid, int q) {
+    return VEC == 4 ? lo + (q / 4) * kThreads * 4 + tid * 4 + (q % 4) : lo + tid + kThreads * q;
+}
+
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sample_args a, const levo_hip_draw_args d,
+                                                                uint8_t * ws, int segs) {
+    __shared__ step_lds S;
+    row_lds<kStepWords> & L = S.L;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t row = blockIdx.x / segs;
+    const int seg = static_cast<int>(blockIdx.x % segs);
+    const int V = static_cast<int>(a.vocab);
+    const int lo = seg * kStepSegIds;
+    const int hi = lo + kStepSegIds < V ? lo + kStepSegIds : V;
+    const int stream = static_cast<int>(row % a.n_streams);
+    int k = a.top_k[stream];
+    if (k <= 0 || k >= V) k = 0;  // keep every id
+    const int kw = (k + kWaves - 1) / kWaves;
+    const int words = (V + 31) / 32;
+    uint32_t * counters = reinterpret_cast<uint32_t *>(ws);
+    step_seg * segv = reinterpret_cast<step_seg *>(ws + kStepCounterBytes) + row * segs;
+
+    // ---- 1. loads, CFG, penalty, ignore list, reductions ------------------------------
+    const float * crow = a.cond + row * a.row_pitch;
+    const float * urow = a.uncond ? a.uncond + row * a.row_pitch : nullptr;
+    float c[kStepPer], u[kStepPer];
+    if constexpr (VEC == 4) {
+#pragma unroll
+        for (int ch = 0; ch < kStepPer / 4; ++ch) {
+            const int base = step_id<VEC>(lo, tid, ch * 4);
+            const int off = base < V ? base : lo;  // row_pitch % 4 == 0: in bounds
+            const f32x4 cv = *reinterpret_cast<const f32x4 *>(crow + off);
+            const f32x4 uv = urow ? *reinterpret_cast<const f32x4 *>(urow + off) : cv;
+            c[ch * 4] = cv.x; c[ch * 4 + 1] = cv.y; c[ch * 4 + 2] = cv.z; c[ch * 4 + 3] = cv.w;
+            u[ch * 4] = uv.x; u[ch * 4 + 1] = uv.y; u[ch * 4 + 2] = uv.z; u[ch * 4 + 3] = uv.w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < kStepPer; ++q) {
+            const int id = step_id<VEC>(lo, tid, q);
+            const int off = id < V ? id : lo;
+            c[q] = crow[off];
+            u[q] = urow ? urow[off] : c[q];
+        }
+    }
+    for (int i = tid; i < words; i += kThreads) L.sel[i] = 0u;
+
+    // Penalty and ignore ids inside this segment, as bitmaps of its 4096 ids
+    // (128 words each), built from the lists loaded in parallel.
+    const bool use_pen = a.recent != nullptr && a.n_recent > 0;
+    const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
+    int pen = 0, ign = 0;  // item bits
+    if (use_pen || use_ign) {
+        if (tid < kStepSegIds / 32) {
+            L.pen[tid] = 0u;
+            L.ign[tid] = 0u;
+        }
+        __syncthreads();
+        if (use_pen) {
+            const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
+            const int64_t top = hi < limit ? hi : limit;
+            const int64_t * rec = a.recent + row * a.n_recent;
+            for (int i = tid; i < a.n_recent; i += kThreads) {
+                const int64_t t = rec[i];
+                if (t >= lo && t < top) atomicOr(&L.pen[(t - lo) >> 5], 1u << ((t - lo) & 31));
+            }
+        }
+        if (use_ign) {
+            for (int i = tid; i < a.n_ignore; i += kThreads) {
+                const int64_t t = a.ignore[i];
+                if (t >= lo && t < hi) atomicOr(&L.ign[(t - lo) >> 5], 1u << ((t - lo) & 31));
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < kStepPer; ++q) {
+            const int rel = step_id<VEC>(lo, tid, q) - lo;
+            pen |= (L.pen[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
+            ign |= (L.ign[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
+        }
+    }
+    float v[kStepPer];
+    bool has_nan = false;
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kStepPer; ++q) {
+        float x = urow ? u[q] + a.cfg_scale * (c[q] - u[q]) : c[q];
+        if (pen & (1 << q)) x = x / a.repetition_penalty;
+        if (ign & (1 << q)) x = -INFINITY;
+        v[q] = step_id<VEC>(lo, tid, q) < hi ? x : -INFINITY;
+        has_nan = has_nan || __builtin_isnan(v[q]);
+        tmax = fmaxf(tmax, v[q]);
+    }
+    const bool tvalid = step_id<VEC>(lo, tid, 0) < hi;
+
+    // ---- 2. segment reductions, bound and hand-over -------------------------------------
+    const float wm = wave_max_f32(tmax);
+    const bool wnan = __ballot(has_nan) != 0;
+    float wlow = -INFINITY;
+    if (k > 1 && kw <= 64) {
+        const uint32_t kk = wave_kth_key(tvalid ? float_key(tmax) : 0u, kw);
+        wlow = kk == 0u ? -INFINITY : float_of_key(kk);
+    }
+    if (lane == 0) {
+        L.wmax[wave] = wm;
+        L.wlow[wave] = wlow;
+        L.wnan[wave] = wnan ? 1 : 0;
+    }
+    __syncthreads();
+    float m = L.wmax[0];
+    float low = L.wlow[0];
+    bool seg_nan = L.wnan[0] != 0;
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+        m = fmaxf(m, L.wmax[w]);
+        low = fminf(low, L.wlow[w]);
+        seg_nan = seg_nan || L.wnan[w] != 0;
+    }
+    if (k == 1) low = m;
+    int tbest = INT_MAX;
+    float tbest_v = m;
+#pragma unroll
+    for (int q = 0; q < kStepPer; ++q) {
+        const int id = step_id<VEC>(lo, tid, q);
+        if (id < hi && v[q] == m && id < tbest) {
+            tbest = id;
+            tbest_v = v[q];
+        }
+    }
+    const int my_best = tbest;
+    tbest = wave_min_i32(tbest);
+    if (lane == 0) L.wbest[wave] = tbest;
+    if (my_best == tbest && my_best != INT_MAX) L.wbv[wave] = tbest_v;
+    if (a.row_lse) {
+        const float inv_t = 1.0f / a.temperature;
+        const float mm = fmaxf(m, -FLT_MAX);
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kStepPer; ++q) s += __expf((v[q] - mm) * inv_t);  // -inf and padding add 0
+        s = wave_sum_f32(s);
+        if (lane == 0) L.wlse[wave] = s;
+    }
+    // gather the ids >= low (k >= 1), padding excluded, into the wave's
+    // kSegCap slots; a longer count (up to 512) only marks the segment full
+    const bool gather = k >= 1 && kw <= 64 && !seg_nan;
+    if (gather) {
+        int base = 0;
+#pragma unroll
+        for (int q = 0; q < kStepPer; ++q) {
+            const int id = step_id<VEC>(lo, tid, q);
+            const bool p = id < hi && v[q] >= low;
+            const uint64_t mask = __ballot(p);
+            if (mask) {
+                const int pos = base + rank_in_mask(mask);
+                if (p && pos < kSegCap) {
+                    L.cv[wave][pos] = v[q];
+                    L.ci[wave][pos] = id;
+                }
+                base += static_cast<int>(__popcll(mask));
+            }
+        }
+        if (lane == 0) L.wcnt[wave] = base;
+    }
+    __syncthreads();
+    int seg_start[kWaves + 1];
+    seg_start[0] = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) seg_start[w + 1] = seg_start[w] + (gather ? L.wcnt[w] : 0);
+    const int ncand = gather ? seg_start[kWaves] : kStepCandCap + 1;
+    step_seg & out = segv[seg];
+    if (ncand <= kStepCandCap) {
+        for (int j = tid; j < ncand; j += kThreads) {
+            int w = 0;
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
+            out.val[j] = L.cv[w][j - seg_start[w]];
+            out.id[j] = L.ci[w][j - seg_start[w]];
+        }
+    }
+    if (tid == 0) {
+        int best = L.wbest[0], bw = 0;
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) {
+            if (L.wbest[w] < best) {
+                best = L.wbest[w];
+                bw = w;
+            }
+        }
+        float sum = 0.0f;
+        if (a.row_lse) {
+            sum = L.wlse[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) sum += L.wlse[w];
+        }
+        step_head h;
+        h.max = m;
+        h.bv = best == INT_MAX ? m : L.wbv[bw];
+        h.best = best;
+        h.nan = seg_nan ? 1 : 0;
+        h.low = low;
+        h.count = ncand;
+        h.sum = sum;
+        h.pad = 0;
+        out.h = h;
+    }
+    // release the hand-over, then count the row's arrivals
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (tid == 0) S.last = atomicAdd(&counters[row], 1u) == static_cast<uint32_t>(segs - 1) ? 1 : 0;
+    __syncthreads();
+    if (!S.last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every segment's hand-over is visible
+
+    // ---- 3. merge the row -----------------------------------------------------------------
+    if (tid < segs) {
+        const step_head h = segv[tid].h;
+        S.hmax[tid] = h.max;
+        S.hbv[tid] = h.bv;
+        S.hbest[tid] = h.best;
+        S.hnan[tid] = h.nan;
+        S.hlow[tid] = h.low;
+        S.hcount[tid] = h.count;
+        S.hsum[tid] = h.sum;
+    }
+    if (tid == 0) counters[row] = 0u;  // every segment has arrived: ready for the next launch
+    __syncthreads();
+    bool row_nan = false;
+    float rm = -INFINITY;
+    float bound = -INFINITY;  // every segment bound is <= the row's k-th largest value
+    int handed = 0;
+    bool fits = k >= 1 && kw <= 64;
+    for (int g = 0; g < segs; ++g) {
+        row_nan = row_nan || S.hnan[g] != 0;
+        rm = fmaxf(rm, S.hmax[g]);
+        bound = fmaxf(bound, S.hlow[g]);
+        fits = fits && S.hcount[g] <= kStepCandCap;
+        handed += S.hcount[g] <= kStepCandCap ? S.hcount[g] : 0;
+    }
+    if (k == 1) bound = rm;
+    int best = -1, bseg = 0;
+    for (int g = 0; g < segs; ++g) {
+        if (best < 0 && S.hbest[g] != INT_MAX && S.hmax[g] == rm) {
+            best = S.hbest[g];
+            bseg = g;
+        }
+    }
+    float lse = NAN;
+    if (!row_nan && a.row_lse) {
+        if (rm == -INFINITY) {
+            lse = -INFINITY;
+        } else if (rm == INFINITY) {
+            lse = INFINITY;
+        } else {
+            const float inv_t = 1.0f / a.temperature;
+            float z = 0.0f;
+            for (int g = 0; g < segs; ++g) z += S.hsum[g] * __expf((fmaxf(S.hmax[g], -FLT_MAX) - rm) * inv_t);
+            lse = rm / a.temperature + logf(z);
+        }
+    }
+    if (row_nan) {  // the reference throws "logits contain NaN"
+        if (tid == 0) {
+            a.best[row] = -1;
+            a.count[row] = -1;
+            if (a.row_max) a.row_max[row] = NAN;
+            if (a.row_lse) a.row_lse[row] = NAN;
+        }
+    }
+    // Keep the handed-over candidates >= bound, compacted (in no particular
+    // order; the bitmap orders them) into one flat LDS array.
+    int total_cand = 0;
+    float * fv = &L.cv[0][0];
+    int * fi = &L.ci[0][0];
+    if (!row_nan && fits) {
+        constexpr int kPer = (kStepCandCap * kStepMaxSegs + kThreads - 1) / kThreads;
+        float kv[kPer];
+        int ki[kPer];
+        int kept = 0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int j = tid + i * kThreads;
+            kv[i] = -INFINITY;
+            ki[i] = -1;
+            if (j < handed) {
+                int g = 0, start = 0;
+                while (j >= start + S.hcount[g]) {
+                    start += S.hcount[g];
+                    ++g;
+                }
+                const float x = segv[g].val[j - start];
+                if (x >= bound) {
+                    kv[i] = x;
+                    ki[i] = segv[g].id[j - start];
+                    ++kept;
+                }
+            }
+        }
+        const int incl = wave_inclusive_scan_i32(kept);
+        if (lane == 63) L.wcnt[wave] = incl;
+        __syncthreads();
+        int off = incl - kept;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) off += w < wave ? L.wcnt[w] : 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) total_cand += L.wcnt[w];
+        if (total_cand <= kStepMergeCap) {
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+                if (ki[i] >= 0) {
+                    fv[off] = kv[i];
+                    fi[off] = ki[i];
+                    ++off;
+                }
+            }
+        }
+        fits = total_cand <= kStepMergeCap;
+        __syncthreads();
+    }
+    if (!row_nan && !fits) {
+        // the whole row again, with full-row penalty and ignore bitmaps
+        for (int i = tid; i < words; i += kThreads) {
+            L.pen[i] = 0u;
+            L.ign[i] = 0u;
+        }
+        __syncthreads();
+        if (use_pen) {
+            const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
+            const int64_t * rec = a.recent + row * a.n_recent;
+            for (int i = tid; i < a.n_recent; i += kThreads) {
+                const int64_t t = rec[i];
+                if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
+            }
+        }
+        if (use_ign) {
+            for (int i = tid; i < a.n_ignore; i += kThreads) {
+                const int64_t t = a.ignore[i];
+                if (t >= 0 && t < V) atomicOr(&L.ign[t >> 5], 1u << (t & 31));
+            }
+        }
+        __syncthreads();
+        select_general(a, L, row, V, k, rm, best, use_pen, use_ign);
+        if (tid == 0) {
+            a.best[row] = best;
+            a.count[row] = L.total;
+            if (a.row_max) a.row_max[row] = S.hbv[bseg];
+            if (a.row_lse) a.row_lse[row] = lse;
+        }
+    } else if (!row_nan) {
+        if (wave == 0) {
+            constexpr int kSlots = kStepMergeCap / 64;
+            float cval[kSlots];
+            int cidx[kSlots];
+            uint32_t keys[kSlots];
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) {
+                const int j = lane + 64 * s;
+                const bool ok = j < total_cand;
+                cval[s] = fv[ok ? j : 0];
+                cidx[s] = fi[ok ? j : 0];
+                keys[s] = ok ? float_key(cval[s]) : 0u;
+            }
+            uint32_t tau;
+            if (k == 1) {
+                tau = float_key(rm);
+            } else {
+                const uint32_t lo_key = bound == -INFINITY ? 0u : float_key(bound);
+                const uint32_t hi_key = float_key(rm);
+                const uint32_t diff = lo_key ^ hi_key;
+                const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
+                uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
+                for (int bit = top; bit >= 0; --bit) {
+                    const uint32_t cand = prefix | (1u << bit);
+                    int cnt = 0;
+#pragma unroll
+                    for (int s = 0; s < kSlots; ++s) cnt += static_cast<int>(__popcll(__ballot(keys[s] >= cand)));
+                    if (cnt >= k) prefix = cand;
+                }
+                tau = prefix;
+            }
+            const bool want_probs = a.cand_probs != nullptr;
+            const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
+            bool take[kSlots];
+            float wgt[kSlots];
+            double z = 0.0;
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) {
+                take[s] = keys[s] >= tau && lane + 64 * s < total_cand;
+                wgt[s] = want_probs && take[s] ? cand_weight(cval[s], rm, inv_t) : 0.0f;
+                if (take[s]) atomicOr(&L.sel[cidx[s] >> 5], 1u << (cidx[s] & 31));
+                z += static_cast<double>(wgt[s]);
+            }
+            z = wave_sum_f64(z);
+            const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+            const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
+            const int total = wave_bitmap_prefix(L, words);
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) {
+                const int pos = take[s] ? slot_of(L, cidx[s]) : a.capacity;
+                if (pos < a.capacity) {
+                    const int64_t o = row * a.capacity + pos;
+                    a.cand_ids[o] = cidx[s];
+                    if (a.cand_logits) a.cand_logits[o] = cval[s];
+                    if (want_probs) a.cand_probs[o] = z_ok ? wgt[s] * inv_z : (cidx[s] == best ? 1.0f : 0.0f);
+                }
+            }
+            if (lane == 0) {
+                a.best[row] = best;
+                a.count[row] = total;
+                if (a.row_max) a.row_max[row] = S.hbv[bseg];
+                if (a.row_lse) a.row_lse[row] = lse;
+            }
+        }
+    }
+
+    // ---- 4. the last row to finish draws every row -----------------------------------------
+    if (d.tokens == nullptr) return;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // this row's outputs
+    __syncthreads();
+    if (tid == 0) S.last = atomicAdd(&counters[kStepCounters - 1], 1u) == static_cast<uint32_t>(a.rows - 1) ? 1 : 0;
+    __syncthreads();
+    if (!S.last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every row's outputs
+    for (int64_t r = wave; r < a.rows; r += kWaves) draw_row(d, r);
+    if (tid == 0) counters[kStepCounters - 1] = 0u;
+}
+
+int64_t step_segments(int64_t vocab) { return (vocab + kStepSegIds - 1) / kStepSegIds; }
+
+int64_t step_workspace_bytes(int64_t rows, int64_t vocab) {
+    return kStepCounterBytes + rows * step_segments(vocab) * static_cast<int64_t>(sizeof(step_seg));
+}
+
 }  // namespace
 }  // namespace levo_hip
 
 using namespace levo_hip;
 
-extern "C" int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_stream_t stream) {
-    LEVO_REQUIRE(args != nullptr, "cfg_sample: null argument block");
-    const levo_hip_sample_args & a = *args;
+namespace {
+
+// The checks of levo_hip_cfg_sample (the reference's messages where it has one).
+int check_sample_args(const levo_hip_sample_args & a) {
     LEVO_REQUIRE(a.rows >= 0, "cfg_sample: negative row count");
     if (a.rows == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(a.vocab >= 1, "cannot sample an empty vocabulary");
@@ -707,6 +1218,61 @@ extern "C" int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_s
     LEVO_REQUIRE((a.cand_probs == nullptr && a.row_lse == nullptr) ||
                      (a.temperature > 0.0f && __builtin_isfinite(a.temperature)),
                  "temperature must be finite and positive for softmax outputs");
+    return LEVO_HIP_OK;
+}
+
+// The checks of levo_hip_sample_draw.
+int check_draw_args(const levo_hip_draw_args & a) {
+    LEVO_REQUIRE(a.rows >= 0 && a.rows < (int64_t{1} << 31), "sample_draw: row count out of range");
+    if (a.rows == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(__builtin_isfinite(a.temperature) && a.temperature >= 0.0f,
+                 "temperature must be finite and non-negative");
+    LEVO_REQUIRE(a.capacity >= 1, "sample_draw: candidate capacity must be positive");
+    LEVO_REQUIRE(a.best != nullptr && a.count != nullptr && a.cand_ids != nullptr && a.cand_logits != nullptr &&
+                     a.row_max != nullptr,
+                 "sample_draw: null candidate input");
+    LEVO_REQUIRE(a.tokens != nullptr && a.draws != nullptr, "sample_draw: null output");
+    LEVO_REQUIRE(a.bits != nullptr || a.use_sampling == 0 || a.temperature == 0.0f,
+                 "sample_draw: null uniform bits");
+    return LEVO_HIP_OK;
+}
+
+// Validates a sample_step call and launches it on `ws` (counters zero).
+int launch_step(const levo_hip_sample_args * args, const levo_hip_draw_args * draw, void * ws, int64_t ws_bytes,
+                hipStream_t stream) {
+    LEVO_REQUIRE(args != nullptr, "sample_step: null argument block");
+    const levo_hip_sample_args & a = *args;
+    const int st = check_sample_args(a);
+    if (st != LEVO_HIP_OK || a.rows == 0) return st;
+    levo_hip_draw_args d{};
+    if (draw != nullptr) {
+        d = *draw;
+        const int sd = check_draw_args(d);
+        if (sd != LEVO_HIP_OK) return sd;
+        LEVO_REQUIRE(d.rows == a.rows && d.capacity == a.capacity && d.best == a.best && d.count == a.count &&
+                         d.cand_ids == a.cand_ids && d.cand_logits == a.cand_logits && d.row_max == a.row_max,
+                     "sample_step: the draw must read the rows' own candidate outputs");
+    }
+    const int64_t segs = step_segments(a.vocab);
+    LEVO_REQUIRE(a.rows <= kStepMaxRows, "sample_step: more than %lld rows", static_cast<long long>(kStepMaxRows));
+    LEVO_REQUIRE(ws != nullptr && aligned16(ws), "sample_step: workspace must be 16-byte aligned device memory");
+    LEVO_REQUIRE(ws_bytes >= step_workspace_bytes(a.rows, a.vocab),
+                 "sample_step: workspace smaller than levo_hip_sample_step_workspace_bytes");
+    const uint32_t grid = static_cast<uint32_t>(a.rows * segs);
+    const bool vec = a.row_pitch % 4 == 0 && aligned16(a.cond) && (a.uncond == nullptr || aligned16(a.uncond));
+    uint8_t * w = static_cast<uint8_t *>(ws);
+    if (vec) sample_step_kernel<4><<<grid, kThreads, 0, stream>>>(a, d, w, static_cast<int>(segs));
+    else sample_step_kernel<1><<<grid, kThreads, 0, stream>>>(a, d, w, static_cast<int>(segs));
+    return launch_status("levo_hip_sample_step");
+}
+
+}  // namespace
+
+extern "C" int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_stream_t stream) {
+    LEVO_REQUIRE(args != nullptr, "cfg_sample: null argument block");
+    const levo_hip_sample_args & a = *args;
+    const int checked = check_sample_args(a);
+    if (checked != LEVO_HIP_OK || a.rows == 0) return checked;
     const hipStream_t st = as_hip(stream);
     const bool vec = a.row_pitch % 4 == 0 && aligned16(a.cond) && (a.uncond == nullptr || aligned16(a.uncond));
     const int64_t V = a.vocab;
@@ -724,4 +1290,14 @@ extern "C" int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_s
     if (V <= 16384) return launch_sample<1, 32>(a, st);
     if (V <= 16896) return launch_sample<1, 33>(a, st);
     return launch_sample<1, 64>(a, st);
+}
+
+extern "C" int64_t levo_hip_sample_step_workspace_bytes(int64_t rows, int64_t vocab) {
+    if (rows < 1 || rows > kStepMaxRows || vocab < 1 || vocab > kMaxVocab) return LEVO_HIP_ERR_INVALID;
+    return step_workspace_bytes(rows, vocab);
+}
+
+extern "C" int levo_hip_sample_step(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,
+                                    void * workspace, int64_t workspace_bytes, levo_hip_stream_t stream) {
+    return launch_step(args, draw, workspace, workspace_bytes, as_hip(stream));
 }

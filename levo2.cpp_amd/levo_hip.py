@@ -175,6 +175,9 @@ class LevoHip:
             "levo_hip_cfg_combine": (ctypes.c_int, [_P, _P, _P, _I64, _F, _P]),
             "levo_hip_cfg_sample": (ctypes.c_int, [ctypes.POINTER(SampleArgs), _P]),
             "levo_hip_sample_draw": (ctypes.c_int, [ctypes.POINTER(DrawArgs), _P]),
+            "levo_hip_sample_step_workspace_bytes": (_I64, [_I64, _I64]),
+            "levo_hip_sample_step": (ctypes.c_int, [ctypes.POINTER(SampleArgs), ctypes.POINTER(DrawArgs), _P, _I64,
+                                                    _P]),
             "levo_hip_flow_cfg_euler": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
             "levo_hip_flow_cfg_euler_checked": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P, _P]),
             "levo_hip_check_finite": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _P]),
@@ -292,6 +295,14 @@ class LevoHip:
 
     def sample_draw(self, args: DrawArgs, stream=None):
         return self._check(self.lib.levo_hip_sample_draw(ctypes.byref(args), _stream(stream)))
+
+    def sample_step_workspace_bytes(self, rows: int, vocab: int) -> int:
+        return self._check(self.lib.levo_hip_sample_step_workspace_bytes(rows, vocab))
+
+    def sample_step(self, args: SampleArgs, draw: DrawArgs | None, workspace, workspace_bytes: int, stream=None):
+        d = ctypes.byref(draw) if draw is not None else None
+        return self._check(self.lib.levo_hip_sample_step(ctypes.byref(args), d, _addr(workspace), workspace_bytes,
+                                                         _stream(stream)))
 
     def flow_cfg_euler(self, state, v_uncond, v_cond, n, guidance, dt, stream=None):
         return self._check(self.lib.levo_hip_flow_cfg_euler(_addr(state), _addr(v_uncond), _addr(v_cond), n,
