@@ -363,6 +363,17 @@ int64_t levo_hip_sample_step_workspace_bytes(int64_t rows, int64_t vocab);
 int levo_hip_sample_step(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,
                          void * workspace, int64_t workspace_bytes, levo_hip_stream_t stream);
 
+/* levo_hip_sample_step without a workspace argument and without any
+ * allocation: the workspace is a 2 MiB array the library holds on every GPU
+ * it runs on, until the process ends (enough for 200 rows of 16385 logits;
+ * larger calls fail with LEVO_HIP_ERR_INVALID, naming the sizes). Same
+ * results as levo_hip_sample_step. Calls that overlap on one GPU share that
+ * array and race: serialize them. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (HIP graph capture, serving
+ * loops that forbid hipMalloc). */
+int levo_hip_sample_step_static(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,
+                                levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Flow Euler / CFG latent update                                            */
 /* ------------------------------------------------------------------------ */

@@ -42,6 +42,7 @@
 
 #include <cfloat>
 #include <climits>
+#include <mutex>
 
 namespace levo_hip {
 namespace {
@@ -1268,6 +1269,55 @@ int launch_step(const levo_hip_sample_args * args, const levo_hip_draw_args * dr
 
 }  // namespace
 
+// ---- levo_hip_sample_step_static: the step on library-held scratch ----------------------
+// Callers that cannot allocate (graph capture, serving loops) get the
+// workspace from this array: one copy per GPU, held until the process ends.
+// Device memory of a code object starts zeroed, and every call leaves the
+// counter region zero; set-up clears it once more per device. Calls that
+// overlap on one GPU share the array and race.
+constexpr int64_t kStaticScratchBytes = int64_t{2} << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace {
+
+__global__ void zero_words(uint32_t * p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// The device address of `scratch` on the current device, found once per
+// device (with that device current) and kept; the host-side name is only a
+// stand-in. The first call on a device also clears the counter region on
+// `stream`, ahead of the work it is about to launch there.
+int scratch_address(void ** out, hipStream_t stream) {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static void * ptrs[kMaxDevices] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        set_error("sample_step_static: cannot query the current device");
+        return LEVO_HIP_ERR_RUNTIME;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptrs[device] == nullptr) {
+        void * p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || p == nullptr) {
+            set_error("sample_step_static: cannot find the scratch array on device %d: %s", device,
+                      hipGetErrorString(err));
+            return LEVO_HIP_ERR_RUNTIME;
+        }
+        zero_words<<<kStepCounters / 256, 256, 0, stream>>>(static_cast<uint32_t *>(p), kStepCounters);
+        const int st = launch_status("sample_step_static");
+        if (st != LEVO_HIP_OK) return st;
+        ptrs[device] = p;
+    }
+    *out = ptrs[device];
+    return LEVO_HIP_OK;
+}
+
+}  // namespace
+
 extern "C" int levo_hip_cfg_sample(const levo_hip_sample_args * args, levo_hip_stream_t stream) {
     LEVO_REQUIRE(args != nullptr, "cfg_sample: null argument block");
     const levo_hip_sample_args & a = *args;
@@ -1300,4 +1350,22 @@ extern "C" int64_t levo_hip_sample_step_workspace_bytes(int64_t rows, int64_t vo
 extern "C" int levo_hip_sample_step(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,
                                     void * workspace, int64_t workspace_bytes, levo_hip_stream_t stream) {
     return launch_step(args, draw, workspace, workspace_bytes, as_hip(stream));
+}
+
+extern "C" int levo_hip_sample_step_static(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,
+                                           levo_hip_stream_t stream) {
+    LEVO_REQUIRE(args != nullptr, "sample_step: null argument block");
+    const int checked = check_sample_args(*args);
+    if (checked != LEVO_HIP_OK || args->rows == 0) return checked;
+    LEVO_REQUIRE(args->rows <= kStepMaxRows, "sample_step: more than %lld rows", static_cast<long long>(kStepMaxRows));
+    const int64_t need = step_workspace_bytes(args->rows, args->vocab);
+    LEVO_REQUIRE(need <= kStaticScratchBytes,
+                 "sample_step_static: %lld rows of %lld logits need %lld bytes of scratch; the library holds %lld "
+                 "per GPU (use levo_hip_sample_step with a workspace)",
+                 static_cast<long long>(args->rows), static_cast<long long>(args->vocab),
+                 static_cast<long long>(need), static_cast<long long>(kStaticScratchBytes));
+    void * ws = nullptr;
+    const int st = scratch_address(&ws, as_hip(stream));
+    if (st != LEVO_HIP_OK) return st;
+    return launch_step(args, draw, ws, kStaticScratchBytes, as_hip(stream));
 }

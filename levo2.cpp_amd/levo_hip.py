@@ -178,6 +178,7 @@ class LevoHip:
             "levo_hip_sample_step_workspace_bytes": (_I64, [_I64, _I64]),
             "levo_hip_sample_step": (ctypes.c_int, [ctypes.POINTER(SampleArgs), ctypes.POINTER(DrawArgs), _P, _I64,
                                                     _P]),
+            "levo_hip_sample_step_static": (ctypes.c_int, [ctypes.POINTER(SampleArgs), ctypes.POINTER(DrawArgs), _P]),
             "levo_hip_flow_cfg_euler": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P]),
             "levo_hip_flow_cfg_euler_checked": (ctypes.c_int, [_P, _P, _P, _I64, _F, _F, _P, _P]),
             "levo_hip_check_finite": (ctypes.c_int, [_P, _I64, _P, ctypes.c_int32, _P]),
@@ -298,6 +299,10 @@ class LevoHip:
 
     def sample_step_workspace_bytes(self, rows: int, vocab: int) -> int:
         return self._check(self.lib.levo_hip_sample_step_workspace_bytes(rows, vocab))
+
+    def sample_step_static(self, args: SampleArgs, draw: DrawArgs | None, stream=None):
+        d = ctypes.byref(draw) if draw is not None else None
+        return self._check(self.lib.levo_hip_sample_step_static(ctypes.byref(args), d, _stream(stream)))
 
     def sample_step(self, args: SampleArgs, draw: DrawArgs | None, workspace, workspace_bytes: int, stream=None):
         d = ctypes.byref(draw) if draw is not None else None
