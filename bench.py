@@ -113,45 +113,74 @@ def time_op(torch, head, launch, n_sets, warmup, steps):
     return ms / steps
 
 
-def op_entry(bytes_per_launch, ms, **extra):
+def op_entry(bytes_per_launch, ms, read=None, write=None, **extra):
+    """One op's figures; read / write split the algorithmic bytes for the
+    streaming ceiling of the same mix (default: all read)."""
     gbps = bytes_per_launch / (ms * 1e-3) / 1e9
     e = {"bytes_per_launch": int(bytes_per_launch), "us_per_launch": round(ms * 1e3, 3),
          "GB/s": round(gbps, 1), "frac": round(gbps / PEAK_GBPS, 4)}
+    r = int(bytes_per_launch if read is None else read)
+    e["read_bytes"], e["write_bytes"] = r, int(bytes_per_launch - r if write is None else write)
     e.update(extra)
     return e
 
 
-_COPY_CACHE = {}
+_CEIL_CACHE = {}
 
 
-def copy_ceiling(torch, head, dev, nbytes, warmup, steps):
-    """GB/s of a plain device copy moving the same bytes (half read, half
-    written), timed like the ops with >= 512 MB of rotation: what any single
-    streaming launch of this size reaches on this GPU."""
-    key = int(nbytes)
-    if key in _COPY_CACHE:
-        return _COPY_CACHE[key]
-    half = max(16, key // 2 // 16 * 16)
-    n = math.ceil(ROTATE_BYTES / (2 * half)) + 1
-    src = [torch.empty(half // 4, dtype=torch.float32, device=dev).fill_(1.0) for _ in range(n)]
-    dst = [torch.empty(half // 4, dtype=torch.float32, device=dev) for _ in range(n)]
-    ms = time_op(torch, head, lambda i: dst[i].copy_(src[i]), n, warmup, steps)
-    gbps = round(2 * half / (ms * 1e-3) / 1e9, 1)
+def load_stream_lib():
+    import ctypes
+    path = os.path.join(ROOT, "levo2.cpp_amd", "liblevo_bench_stream.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    lib.levo_bench_stream.restype = ctypes.c_int
+    lib.levo_bench_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                      ctypes.c_void_p]
+    return lib
+
+
+def stream_ceiling(torch, head, dev, read_bytes, write_bytes, warmup, steps):
+    """GB/s (read + write) of the best plain streaming launch moving the same
+    bytes in the same mix: dwordx4 loads and stores, one, two or four vectors
+    per thread (levo2.cpp_amd/bench/stream_ceiling.hip), rotated over >= 512 MB
+    like the ops. What one launch of this size and mix reaches on this GPU."""
+    rb, wb = int(read_bytes) // 16 * 16, int(write_bytes) // 16 * 16
+    key = (rb, wb)
+    if key in _CEIL_CACHE:
+        return _CEIL_CACHE[key]
+    lib = load_stream_lib()
+    n = math.ceil(ROTATE_BYTES / max(rb + wb, 16)) + 1
+    src = [torch.ones(max(rb, 16) // 4, dtype=torch.float32, device=dev) for _ in range(n)]
+    dst = [torch.empty(max(wb, 16) // 4, dtype=torch.float32, device=dev) for _ in range(n)]
+    stream = torch.cuda.current_stream().cuda_stream
+    best = (0.0, 1)
+    for vpt in (1, 2, 4):
+        def launch(i, vpt=vpt):
+            if lib.levo_bench_stream(src[i].data_ptr(), dst[i].data_ptr(), rb, wb, vpt, stream) != 0:
+                raise RuntimeError("levo_bench_stream failed")
+        ms = time_op(torch, head, launch, n, warmup, max(steps, 50))
+        gbps = (rb + wb) / (ms * 1e-3) / 1e9
+        if gbps > best[0]:
+            best = (round(gbps, 1), vpt)
     del src, dst
     torch.cuda.empty_cache()
-    _COPY_CACHE[key] = gbps
-    return gbps
+    _CEIL_CACHE[key] = best
+    return best
 
 
 def add_ceilings(torch, head, dev, ops, warmup, steps):
-    """Annotate every op entry with the copy ceiling at its byte count."""
+    """Annotate every HBM-bound op entry with the streaming ceiling of its byte
+    count and read / write mix (ceiling_GB/s) and its fraction of it."""
     for entry in ops.values():
         entries = entry.values() if "bytes_per_launch" not in entry else [entry]
         for e in entries:
-            if isinstance(e, dict) and "bytes_per_launch" in e and e.get("bound") != "mfma":
-                c = copy_ceiling(torch, head, dev, e["bytes_per_launch"], warmup, steps)
-                e["copy_GB/s"] = c
-                e["of_copy"] = round(e["GB/s"] / c, 3)
+            if isinstance(e, dict) and "bytes_per_launch" in e and e.get("bound") not in ("mfma", "latency"):
+                c, vpt = stream_ceiling(torch, head, dev, e.get("read_bytes", e["bytes_per_launch"]),
+                                        e.get("write_bytes", 0), warmup, steps)
+                e["ceiling_GB/s"] = c
+                e["ceiling_vectors_per_thread"] = vpt
+                e["of_ceiling"] = round(e["GB/s"] / c, 3)
 
 
 def cpu_threads():
@@ -218,7 +247,7 @@ def bench_ladder(torch, hip, head, dev, warmup, steps):
         ys = [torch.empty((C, T), device=dev) for _ in range(n)]
         a, b = sets[0][j][1], sets[0][j][2]
         ms = time_op(torch, head, lambda i: hip.snake_beta(xs[i], a, b, ys[i]), n, warmup, max(steps, n))
-        per_shape[f"{C}x{T}"] = op_entry(snake_bytes(C, T), ms, rotated_sets=n)
+        per_shape[f"{C}x{T}"] = op_entry(snake_bytes(C, T), ms, read=4 * C * T + 8 * C, rotated_sets=n)
         shape_ms.append(ms)
         del xs, ys
     del sets
@@ -238,7 +267,7 @@ def bench_snake_1s(torch, hip, head, dev, warmup, steps):
              torch.from_numpy(rng.uniform(-0.5, 0.5, C).astype(np.float32)).to(dev)) for _ in range(n)]
     outs = [torch.empty((C, T), device=dev) for _ in range(n)]
     ms = time_op(torch, head, lambda i: hip.snake_beta(bufs[i][0], bufs[i][1], bufs[i][2], outs[i]), n, warmup, steps)
-    return op_entry(per, ms, shape=[C, T], dtype="f32")
+    return op_entry(per, ms, read=4 * C * T + 8 * C, shape=[C, T], dtype="f32")
 
 
 def bench_flow(torch, hip, head, dev, warmup, steps):
@@ -277,7 +306,7 @@ def bench_flow(torch, hip, head, dev, warmup, steps):
         graph_ms = time_op(torch, head, lambda i: graph.replay(), 1, 1, reps)
     except Exception as e:  # graph capture is an extra measurement only
         log(f"flow graph capture skipped: {e}")
-    e = op_entry(per, step_ms, shape=[1, 64, 2520], dtype="f32",
+    e = op_entry(per, step_ms, read=12 * n_el, shape=[1, 64, 2520], dtype="f32",
                  solve_50_steps_ms=round(solve_ms, 4),
                  solve_50_steps_GBps=round(per * nsteps / (solve_ms * 1e-3) / 1e9, 1))
     if graph_ms is not None:
@@ -364,7 +393,7 @@ def bench_norm(torch, hip, head, dev, warmup, steps, layer, rows, D):
     else:
         fn = lambda i: hip.rms_norm(1, sets[i][0], sets[i][1], w, 1, sets[i][2], sets[i][3], rows, D, 1e-6)
     ms = time_op(torch, head, fn, n, warmup, max(steps, 50))
-    return op_entry(per, ms, shape=[rows, D], dtype="f16 io / f32 accumulate")
+    return op_entry(per, ms, read=per - 4 * rows * D, shape=[rows, D], dtype="f16 io / f32 accumulate")
 
 
 def bench_sample(torch, hip, binding, head, dev, warmup, steps):
@@ -395,7 +424,7 @@ def bench_sample(torch, hip, binding, head, dev, warmup, steps):
         a.row_max, a.row_lse, a.capacity = mx.data_ptr(), lse.data_ptr(), cap
         args.append(a)
     ms = time_op(torch, head, lambda i: hip.cfg_sample(args[i]), n, warmup, steps)
-    return op_entry(per, ms, shape=[P, 2, S, V], dtype="f32", top_k=50, temperature=0.9)
+    return op_entry(per, ms, read=reads, shape=[P, 2, S, V], dtype="f32", top_k=50, temperature=0.9)
 
 
 def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
@@ -503,7 +532,8 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
         y = torch.empty((n_vec, rows), device=dev)
         ms = time_op(torch, head, lambda i: hip.mul_mat_q8_0(w[i].data_ptr(), xb, y, rows, rows, k, n_vec),
                      n, warmup, max(steps, 50))
-        out[name] = op_entry(per, ms, shape=[rows, k], n_vec=n_vec, dtype="q8_0 weights / q8_0 activations")
+        out[name] = op_entry(per, ms, read=per - n_vec * rows * 4, shape=[rows, k], n_vec=n_vec,
+                             dtype="q8_0 weights / q8_0 activations")
         del w
     layer = [(1536, 1536)] * 4 + [(8960, 1536)] * 2 + [(1536, 8960)]
     layer_bytes = sum(r * (k // 32) * 34 + n_vec * (k // 32) * 34 + n_vec * r * 4 for r, k in layer)
@@ -572,7 +602,7 @@ def bench_mul_mat_kquant(torch, hip, head, dev, warmup, steps):
             per = nbytes + n_vec * (k // 256) * 292 + n_vec * rows * 4
             ms = time_op(torch, head, lambda i: hip.mul_mat_kquant(qtype, w[i].data_ptr(), xb, y, rows, rows, k,
                                                                     n_vec), n, warmup, max(steps, 50))
-            out[f"{tname}_{name}"] = op_entry(per, ms, shape=[rows, k], n_vec=n_vec,
+            out[f"{tname}_{name}"] = op_entry(per, ms, read=per - n_vec * rows * 4, shape=[rows, k], n_vec=n_vec,
                                               dtype=f"{tname} weights / q8_K activations")
             del w
         torch.cuda.empty_cache()
@@ -694,9 +724,9 @@ def bench_quant(torch, hip, head, dev, warmup, steps):
         deq = [torch.empty((R, Cc), dtype=torch.float32, device=dev) for _ in range(n)]
         ms = time_op(torch, head, lambda i: hip.quantize_rows(qt, src[i], 1, Cc, Cc, q[i], R, Cc), n, warmup,
                      max(steps, 50))
-        out[f"{name}_quantize_f16"] = op_entry(per_q, ms, shape=[R, Cc])
+        out[f"{name}_quantize_f16"] = op_entry(per_q, ms, read=2 * R * Cc, shape=[R, Cc])
         ms = time_op(torch, head, lambda i: hip.dequantize(qt, q[i], deq[i], 0, R * Cc), n, warmup, max(steps, 50))
-        out[f"{name}_dequantize_f32"] = op_entry(per_d, ms, shape=[R, Cc])
+        out[f"{name}_dequantize_f32"] = op_entry(per_d, ms, read=qbytes, shape=[R, Cc])
         del src, q, deq
         torch.cuda.empty_cache()
     # the converter's F16 <-> F32 rows (ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row) at the same shape
@@ -707,9 +737,9 @@ def bench_quant(torch, hip, head, dev, warmup, steps):
     f32 = [torch.randn((R, Cc), generator=g, device=dev) * 0.02 for _ in range(n)]
     f16 = [torch.empty((R, Cc), dtype=torch.float16, device=dev) for _ in range(n)]
     ms = time_op(torch, head, lambda i: hip.fp32_to_fp16_row(f32[i], f16[i], R * Cc), n, warmup, max(steps, 50))
-    out["fp32_to_fp16_row"] = op_entry(per, ms, shape=[R, Cc])
+    out["fp32_to_fp16_row"] = op_entry(per, ms, read=4 * R * Cc, shape=[R, Cc])
     ms = time_op(torch, head, lambda i: hip.fp16_to_fp32_row(f16[i], f32[i], R * Cc), n, warmup, max(steps, 50))
-    out["fp16_to_fp32_row"] = op_entry(per, ms, shape=[R, Cc])
+    out["fp16_to_fp32_row"] = op_entry(per, ms, read=2 * R * Cc, shape=[R, Cc])
     del f32, f16
     torch.cuda.empty_cache()
     return out
@@ -866,6 +896,50 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     print(json.dumps({"traffic_probe_launch_order": order}))
 
 
+OP_GROUPS = ("snake", "flow", "norm", "sample", "quant", "gemv", "conv", "vae")
+
+
+def run_ops(torch, hip, binding, head, dev, args, groups):
+    """The op table: every group in `groups`, the same shapes whether run
+    alone (--only) or after the headline."""
+    w, k = args.warmup, args.steps
+    ops = {}
+    if "snake" in groups:
+        log("ops: snake 1 s")
+        ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, w, k)
+    if "flow" in groups:
+        log("ops: flow")
+        ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, w, k)
+        log("ops: flow window step")
+        ops["flow_window_step_1000x64_rows2200"] = bench_flow_window(torch, hip, binding, head, dev, w, k)
+    if "norm" in groups:
+        for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
+            for rows, D in ((756, 2048), (756, 1536), (1, 2048), (2, 2048)):
+                log(f"ops: {name} {rows}x{D}")
+                ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, w, k, layer, rows, D)
+    if "sample" in groups:
+        log("ops: cfg sample")
+        ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, w, k)
+        log("ops: decode-step sampling")
+        ops["decode_step_sample_1x3x16385"] = bench_decode_step(torch, hip, binding, head, dev, w, k)
+    if "quant" in groups:
+        log("ops: quant")
+        ops.update(bench_quant(torch, hip, head, dev, w, k))
+    if "gemv" in groups:
+        log("ops: q8_0 mat-vec")
+        ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, w, k)
+        log("ops: k-quant mat-vec")
+        ops["mul_mat_kquant"] = bench_mul_mat_kquant(torch, hip, head, dev, w, k)
+    if "conv" in groups:
+        log("ops: snake conv1d")
+        ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, w, k)
+    if "vae" in groups:
+        for frames in (252, 1000):
+            log(f"ops: vae decoder window of {frames} frames")
+            ops[f"vae_decode_{frames}_frames"] = bench_vae_decode(torch, hip, binding, head, dev, w, k, frames)
+    return ops
+
+
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -876,8 +950,8 @@ def main() -> int:
     p.add_argument("--only", default="",
                    help="comma-separated op groups to run alone (snake,flow,norm,sample,quant,gemv,conv,vae); "
                         "prints the op table without the headline ladder")
-    p.add_argument("--copy-ceiling", action="store_true",
-                   help="with --only: annotate each op with a plain device copy of the same bytes")
+    p.add_argument("--ceiling", action="store_true",
+                   help="with --only: annotate each op with the plain streaming ceiling of its bytes and mix")
     p.add_argument("--traffic-probe", action="store_true",
                    help="one launch per kernel + a 256 MiB copy, for rocprofv3 --pmc runs")
     args = p.parse_args()
@@ -901,36 +975,8 @@ def main() -> int:
 
     head = HeadStart(torch)
     if args.only:
-        groups = set(args.only.split(","))
-        ops = {}
-        if "snake" in groups:
-            ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
-        if "flow" in groups:
-            ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, args.warmup, args.steps)
-            ops["flow_window_step_1000x64_rows2200"] = bench_flow_window(torch, hip, binding, head, dev,
-                                                                         args.warmup, args.steps)
-        if "norm" in groups:
-            for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
-                for rows, D in ((756, 2048), (1, 2048)):
-                    ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, args.warmup,
-                                                                        args.steps, layer, rows, D)
-        if "sample" in groups:
-            ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup,
-                                                                args.steps)
-            ops["decode_step_sample_1x3x16385"] = bench_decode_step(torch, hip, binding, head, dev, args.warmup,
-                                                                    args.steps)
-        if "quant" in groups:
-            ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
-        if "gemv" in groups:
-            ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
-            ops["mul_mat_kquant"] = bench_mul_mat_kquant(torch, hip, head, dev, args.warmup, args.steps)
-        if "conv" in groups:
-            ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
-        if "vae" in groups:
-            for frames in (252, 1000):
-                ops[f"vae_decode_{frames}_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup,
-                                                                      args.steps, frames)
-        if args.copy_ceiling:
+        ops = run_ops(torch, hip, binding, head, dev, args, set(args.only.split(",")))
+        if args.ceiling:
             add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
         print(json.dumps({"ops": ops}))
         return 0
@@ -960,36 +1006,8 @@ def main() -> int:
                                               "GB/s": round(lad["ladder_bytes"] / (lad["ms_per_step_six"] * 1e-3) / 1e9,
                                                             1)}}
     if not args.no_ops:
-        log("ops: snake 1 s")
-        ops["snake_beta_128x48000"] = bench_snake_1s(torch, hip, head, dev, args.warmup, args.steps)
-        log("ops: flow")
-        ops["flow_cfg_euler_64x2520"] = bench_flow(torch, hip, head, dev, args.warmup, args.steps)
-        log("ops: flow window step")
-        ops["flow_window_step_1000x64_rows2200"] = bench_flow_window(torch, hip, binding, head, dev, args.warmup,
-                                                                     args.steps)
-        for layer, name in ((False, "rmsnorm"), (True, "layernorm")):
-            for rows, D in ((756, 2048), (756, 1536), (1, 2048), (2, 2048)):
-                log(f"ops: {name} {rows}x{D}")
-                ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, args.warmup, args.steps,
-                                                                    layer, rows, D)
-        log("ops: cfg sample")
-        ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, args.warmup, args.steps)
-        log("ops: decode-step sampling")
-        ops["decode_step_sample_1x3x16385"] = bench_decode_step(torch, hip, binding, head, dev, args.warmup,
-                                                                args.steps)
-        log("ops: quant")
-        ops.update(bench_quant(torch, hip, head, dev, args.warmup, args.steps))
-        log("ops: q8_0 mat-vec")
-        ops["mul_mat_q8_0"] = bench_mul_mat(torch, hip, head, dev, args.warmup, args.steps)
-        log("ops: k-quant mat-vec")
-        ops["mul_mat_kquant"] = bench_mul_mat_kquant(torch, hip, head, dev, args.warmup, args.steps)
-        log("ops: snake conv1d")
-        ops["snake_conv1d"] = bench_snake_conv(torch, hip, head, dev, args.warmup, args.steps)
-        for frames in (252, 1000):
-            log(f"ops: vae decoder window of {frames} frames")
-            ops[f"vae_decode_{frames}_frames"] = bench_vae_decode(torch, hip, binding, head, dev, args.warmup,
-                                                                  args.steps, frames)
-        log("ops: plain-copy ceilings")
+        ops.update(run_ops(torch, hip, binding, head, dev, args, OP_GROUPS))
+        log("ops: streaming ceilings")
         add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 
     cpu = None

@@ -2,6 +2,7 @@
 
   levo2.cpp_amd/liblevo_hip.so       C ABI (include/levo_hip.h) + HIP kernels
   levo2.cpp_amd/liblevo_hip_host.so  C++17 drop-in wrappers (levo2.cpp_amd/host/)
+  levo2.cpp_amd/liblevo_bench_stream.so  plain streaming kernels bench.py compares the ops with
 
 Kernels are compiled with hipcc for gfx950 only; the host wrappers contain no
 device code and are plain C++17 (g++) against the HIP runtime API. Every source is recompiled on
@@ -24,6 +25,7 @@ HOST = os.path.join(PKG, "host")
 BUILD = os.path.join(PKG, "_build")
 KERNEL_LIB = os.path.join(PKG, "liblevo_hip.so")
 HOST_LIB = os.path.join(PKG, "liblevo_hip_host.so")
+BENCH_LIB = os.path.join(PKG, "liblevo_bench_stream.so")  # measurement kernels of bench.py, not the C ABI
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
@@ -80,16 +82,22 @@ def build(verbose: bool = False) -> None:
     os.makedirs(BUILD, exist_ok=True)
     kernel_srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     host_srcs = sorted(glob.glob(os.path.join(HOST, "*.cpp")))
+    bench_srcs = sorted(glob.glob(os.path.join(PKG, "bench", "*.hip")))
     jobs = min(8, os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(jobs) as ex:
+        bobjs_f = [ex.submit(_compile, s, []) for s in bench_srcs]
         kobjs = list(ex.map(lambda s: _compile(s, []), kernel_srcs))
         hobjs = list(ex.map(_compile_host, host_srcs))
+        bobjs = [f.result() for f in bobjs_f]
     _run([HIPCC, *DEVICE, "-shared", "-fPIC", "-o", KERNEL_LIB + ".tmp", *kobjs])
     os.replace(KERNEL_LIB + ".tmp", KERNEL_LIB)
     if hobjs:
         _run([CXX, "-shared", "-fPIC", "-o", HOST_LIB + ".tmp", *hobjs,
               "-L", PKG, "-llevo_hip", "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath,$ORIGIN"])
         os.replace(HOST_LIB + ".tmp", HOST_LIB)
+    if bobjs:
+        _run([HIPCC, *DEVICE, "-shared", "-fPIC", "-o", BENCH_LIB + ".tmp", *bobjs])
+        os.replace(BENCH_LIB + ".tmp", BENCH_LIB)
     if verbose:
         print("built", KERNEL_LIB, HOST_LIB if hobjs else "")
 

@@ -130,8 +130,9 @@ __device__ __forceinline__ void finish_stats(row_stats & st, const float (&v)[IT
 }
 
 // l = u + s * (c - u) for every id this thread owns: id of item i is
-// (i / VEC) * 256 * VEC + tid * VEC + i % VEC. Every load is issued before the
+// (i / VEC) * kThreads * VEC + tid * VEC + i % VEC. Every load is issued before the
 // first is consumed; each chunk is folded into the statistics as it arrives.
+// The logits are read once, with streaming (nontemporal) loads.
 // kFull: the row fills every item (V == 256 * VEC * NCH), no masking.
 template <int VEC, int NCH, bool kCfg, bool kFull>
 __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, const float * __restrict__ crow,
@@ -143,8 +144,8 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, 
         for (int ch = 0; ch < NCH; ++ch) {
             const int base = ch * kChunk + tid * 4;
             const int off = kFull || base < V ? base : 0;  // row_pitch % 4 == 0: in bounds
-            c[ch] = *reinterpret_cast<const f32x4 *>(crow + off);
-            if constexpr (kCfg) u[ch] = *reinterpret_cast<const f32x4 *>(urow + off);
+            c[ch] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(crow + off));
+            if constexpr (kCfg) u[ch] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(urow + off));
         }
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {
@@ -171,8 +172,8 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, 
         for (int ch = 0; ch < NCH; ++ch) {
             const int base = ch * kChunk + tid;
             const int off = base < V ? base : 0;
-            c[ch] = crow[off];
-            if constexpr (kCfg) u[ch] = urow[off];
+            c[ch] = __builtin_nontemporal_load(crow + off);
+            if constexpr (kCfg) u[ch] = __builtin_nontemporal_load(urow + off);
         }
 #pragma unroll
         for (int ch = 0; ch < NCH; ++ch) {

@@ -153,21 +153,31 @@ __global__ __launch_bounds__(kThreads) void f32_to_f16_vec8(const float * __rest
     __builtin_nontemporal_store(o, reinterpret_cast<u32x4 *>(y) + i);
 }
 
-__global__ __launch_bounds__(kThreads) void f16_to_f32_vec8(const uint16_t * __restrict__ x, float * y, int64_t n8) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= n8) return;
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x) + i);
-    f32x4 a, b;
-    a[0] = h2f(static_cast<uint16_t>(v[0] & 0xffffu));
-    a[1] = h2f(static_cast<uint16_t>(v[0] >> 16));
-    a[2] = h2f(static_cast<uint16_t>(v[1] & 0xffffu));
-    a[3] = h2f(static_cast<uint16_t>(v[1] >> 16));
-    b[0] = h2f(static_cast<uint16_t>(v[2] & 0xffffu));
-    b[1] = h2f(static_cast<uint16_t>(v[2] >> 16));
-    b[2] = h2f(static_cast<uint16_t>(v[3] & 0xffffu));
-    b[3] = h2f(static_cast<uint16_t>(v[3] >> 16));
-    __builtin_nontemporal_store(a, reinterpret_cast<f32x4 *>(y) + 2 * i);
-    __builtin_nontemporal_store(b, reinterpret_cast<f32x4 *>(y) + 2 * i + 1);
+// Widening, four values per lane: each dwordx2 load and dwordx4 store of a
+// wave covers one contiguous span; thread t of workgroup g converts groups
+// g * 256 * kWidenPer + k * 256 + t, k < kWidenPer.
+constexpr int kWidenPer = 2;
+
+__global__ __launch_bounds__(kThreads) void f16_to_f32_vec4(const uint16_t * __restrict__ x, float * y, int64_t n4) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kThreads * kWidenPer + threadIdx.x;
+    u32x2 v[kWidenPer];
+#pragma unroll
+    for (int k = 0; k < kWidenPer; ++k) {
+        const int64_t i = i0 + k * kThreads;
+        v[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(x) + (i < n4 ? i : n4 - 1));
+    }
+#pragma unroll
+    for (int k = 0; k < kWidenPer; ++k) {
+        const int64_t i = i0 + k * kThreads;
+        if (i >= n4) break;
+        f32x4 a;
+        a[0] = h2f(static_cast<uint16_t>(v[k][0] & 0xffffu));
+        a[1] = h2f(static_cast<uint16_t>(v[k][0] >> 16));
+        a[2] = h2f(static_cast<uint16_t>(v[k][1] & 0xffffu));
+        a[3] = h2f(static_cast<uint16_t>(v[k][1] >> 16));
+        __builtin_nontemporal_store(a, reinterpret_cast<f32x4 *>(y) + i);
+    }
 }
 
 }  // namespace
@@ -290,10 +300,10 @@ extern "C" int levo_hip_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t 
     if (n == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(x != nullptr && y != nullptr, "fp16_to_fp32_row: null pointer");
     int64_t head = 0;
-    if (aligned16(x) && aligned16(y)) {
-        const int64_t n8 = n / 8;
-        if (n8 > 0) f16_to_f32_vec8<<<ceil_div(n8, kThreads), kThreads, 0, as_hip(stream)>>>(x, y, n8);
-        head = n8 * 8;
+    if ((reinterpret_cast<uintptr_t>(x) & 7u) == 0 && aligned16(y)) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) f16_to_f32_vec4<<<ceil_div(n4, kThreads * kWidenPer), kThreads, 0, as_hip(stream)>>>(x, y, n4);
+        head = n4 * 4;
     }
     if (head < n) f16_to_f32_kernel<<<ceil_div(n - head, kThreads), kThreads, 0, as_hip(stream)>>>(x + head, y + head, n - head);
     return launch_status("levo_hip_fp16_to_fp32_row");

@@ -1,9 +1,11 @@
-// Fused residual add + RMSNorm / LayerNorm, one 4-wave workgroup per row.
+// Fused residual add + RMSNorm / LayerNorm, one wave per row up to 2048
+// elements (two or four waves for longer rows).
 //
 // Every load of the row (x, delta, weight, bias) is issued up front with
 // dwordx4 accesses, the row stays in registers, is reduced with DPP cross-lane
-// steps and one LDS exchange between the four waves, normalised and
-// written once. The reduction accumulates in double like ggml-cpu's ggml_float
+// steps (plus one LDS exchange when several waves share the row), normalised
+// and written once; row data is loaded and stored with streaming
+// (nontemporal) accesses. The reduction accumulates in double like ggml-cpu's ggml_float
 // row sums, so the F32 mean / variance (and hence every rounding point after
 // it) matches the CPU chain.
 //
@@ -27,7 +29,6 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kVec = 8;  // elements per lane per group (16 B of F16, 32 B of F32)
-constexpr int kRowWaves = 4;  // waves sharing one row in the vector kernel
 
 template <typename T>
 __device__ __forceinline__ void load8(const T * p, float (&o)[kVec]);
@@ -45,33 +46,6 @@ __device__ __forceinline__ void load8<float>(const float * p, float (&o)[kVec]) 
     o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
 }
 
-// Raw F16 bits are kept for the residual (h = f16(x + d) is formed from them).
-__device__ __forceinline__ void load8_raw(const uint16_t * p, uint16_t (&o)[kVec]) {
-    const u16x8 v = *reinterpret_cast<const u16x8 *>(p);
-#pragma unroll
-    for (int k = 0; k < kVec; ++k) o[k] = v[k];
-}
-
-__device__ __forceinline__ void store8(uint16_t * p, const float (&v)[kVec]) {
-    u16x8 w;
-#pragma unroll
-    for (int k = 0; k < kVec; ++k) w[k] = f2h(v[k]);
-    *reinterpret_cast<u16x8 *>(p) = w;
-}
-__device__ __forceinline__ void store8_bits(uint16_t * p, const uint16_t (&v)[kVec]) {
-    u16x8 w;
-#pragma unroll
-    for (int k = 0; k < kVec; ++k) w[k] = v[k];
-    *reinterpret_cast<u16x8 *>(p) = w;
-}
-__device__ __forceinline__ void store8(float * p, const float (&v)[kVec]) {
-    f32x4 a, b;
-    a.x = v[0]; a.y = v[1]; a.z = v[2]; a.w = v[3];
-    b.x = v[4]; b.y = v[5]; b.z = v[6]; b.w = v[7];
-    reinterpret_cast<f32x4 *>(p)[0] = a;
-    reinterpret_cast<f32x4 *>(p)[1] = b;
-}
-
 template <typename T>
 __device__ __forceinline__ float to_f32(T v) {
     if constexpr (std::is_same<T, uint16_t>::value) return h2f(v);
@@ -86,111 +60,168 @@ __device__ __forceinline__ float norm_out(float n, float w, float b) {
     else return n * w;
 }
 
+// Row loads and stores stream past the caches (each row is touched once);
+// the parameters, shared by every row, are ordinary cached loads.
+__device__ __forceinline__ void load8_row(const uint16_t * p, uint16_t (&o)[kVec]) {
+    const u16x8 v = __builtin_nontemporal_load(reinterpret_cast<const u16x8 *>(p));
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) o[k] = v[k];
+}
+__device__ __forceinline__ void load8_row(const float * p, float (&o)[kVec]) {
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + 1);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void store8_row(uint16_t * p, const uint16_t (&v)[kVec]) {
+    u16x8 w;
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) w[k] = v[k];
+    __builtin_nontemporal_store(w, reinterpret_cast<u16x8 *>(p));
+}
+__device__ __forceinline__ void store8_row(float * p, const float (&v)[kVec]) {
+    f32x4 a, b;
+    a.x = v[0]; a.y = v[1]; a.z = v[2]; a.w = v[3];
+    b.x = v[4]; b.y = v[5]; b.z = v[6]; b.w = v[7];
+    __builtin_nontemporal_store(a, reinterpret_cast<f32x4 *>(p));
+    __builtin_nontemporal_store(b, reinterpret_cast<f32x4 *>(p) + 1);
+}
+
+// Sum in double of this lane's values (kSquare: of their F32 squares) over
+// the groups in range, as a pairwise tree: the dependent chain is a few adds
+// long instead of one per element. Any order differs from the CPU's
+// sequential ggml_float sum; in double the difference stays near 2^-40 of the
+// sum of magnitudes, far below the F32 rounding the result then takes.
+template <int NV, bool kSquare>
+__device__ __forceinline__ double lane_sum(const float (&h)[NV][kVec], const bool (&in)[NV]) {
+    double g[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        double t[kVec];
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) t[k] = static_cast<double>(kSquare ? h[j][k] * h[j][k] : h[j][k]);
+#pragma unroll
+        for (int w = kVec / 2; w >= 1; w /= 2) {
+#pragma unroll
+            for (int k = 0; k < w; ++k) t[k] = t[2 * k] + t[2 * k + 1];
+        }
+        g[j] = in[j] ? t[0] : 0.0;
+    }
+    double s = g[0];
+#pragma unroll
+    for (int j = 1; j < NV; ++j) s += g[j];
+    return s;
+}
+
+// Sum of v over the W waves of one row: DPP within the wave, then (W > 1)
+// one LDS exchange, added in wave order.
+template <int W>
+__device__ __forceinline__ double row_sum(double v, double (*part)[4], int slot, int wave, int lane) {
+    v = wave_sum_f64(v);
+    if constexpr (W == 1) {
+        return v;
+    } else {
+        if (lane == 0) part[slot][wave] = v;
+        lds_barrier();
+        double s = part[slot][0];
+#pragma unroll
+        for (int i = 1; i < W; ++i) s += part[slot][i];
+        return s;
+    }
+}
+
 // T: activation storage (uint16_t = F16, float); P: parameter storage.
-// One row per workgroup of W waves; lane groups g = tid + 64*W*j, NV groups of
-// 8 elements per lane (dim <= 512 * W * NV). The wave sums meet in LDS and are
-// added in wave order.
+// A 256-thread workgroup holds 4 / W rows, W waves per row; lane groups
+// g = t + 64*W*j (t the thread's index within its row), NV groups of 8
+// elements per lane (dim <= 512 * W * NV). A row of up to 2048 elements is one
+// wave's: its sums need no LDS and no barrier.
 // x / d may alias h_out or y (in-place residual): each element is loaded and
 // stored by the same lane, loads first, so no __restrict__ on them.
-template <typename T, typename P, bool kLayer, int NV, int W>
-__global__ __launch_bounds__(64 * W) void norm_kernel_wg(const T * x, const T * d, const P * __restrict__ w,
-                                                         const P * __restrict__ b, T * h_out, T * y,
-                                                         int64_t rows, int dim, float eps) {
+template <typename T, typename P, bool kLayer, bool kDelta, int NV, int W>
+__global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T * d, const P * __restrict__ w,
+                                                           const P * __restrict__ b, T * h_out, T * y,
+                                                           int64_t rows, int dim, float eps) {
     constexpr bool kF16 = std::is_same<T, uint16_t>::value;
-    __shared__ double part[2][W];
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int64_t row = blockIdx.x;
+    constexpr int kRows = 4 / W;
+    __shared__ double part[2][kRows][4];
+    const int t = threadIdx.x % (64 * W);
+    const int slot = threadIdx.x / (64 * W);
+    const int wave = t >> 6;
+    const int lane = t & 63;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kRows + slot;
+    // A slot past the last row computes on the last row and stores nothing, so
+    // every wave reaches the barriers of its row.
+    const bool valid = row0 < rows;
+    const int64_t row = valid ? row0 : rows - 1;
     const T * xr = x + row * dim;
-    const T * dr = d ? d + row * dim : nullptr;
+    const T * dr = kDelta ? d + row * dim : nullptr;
     T * hr = h_out ? h_out + row * dim : nullptr;
     T * yr = y + row * dim;
     bool in[NV];
     int off[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = (tid + 64 * W * j) * kVec;
+        const int e = (t + 64 * W * j) * kVec;
         in[j] = e < dim;
         off[j] = in[j] ? e : 0;
     }
     float h[NV][kVec];
     float wv[NV][kVec];
     float bv[NV][kVec];
-    uint16_t xb[NV][kVec], db[NV][kVec];
-    float df[NV][kVec];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        if constexpr (kF16) load8_raw(xr + off[j], xb[j]);
-        else load8(xr + off[j], h[j]);
-    }
-    if (dr) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            if constexpr (kF16) load8_raw(dr + off[j], db[j]);
-            else load8(dr + off[j], df[j]);
-        }
-    }
+    T xb[NV][kVec], db[NV][kVec];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         load8(w + off[j], wv[j]);
         if constexpr (kLayer) load8(b + off[j], bv[j]);
     }
-    double acc = 0.0;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        if constexpr (kF16) {
-            uint16_t hb[kVec];
+    for (int j = 0; j < NV; ++j) load8_row(xr + off[j], xb[j]);
+    if constexpr (kDelta) {
 #pragma unroll
-            for (int k = 0; k < kVec; ++k) hb[k] = dr ? f2h(h2f(xb[j][k]) + h2f(db[j][k])) : xb[j][k];
-            if (hr && in[j]) store8_bits(hr + off[j], hb);
-#pragma unroll
-            for (int k = 0; k < kVec; ++k) h[j][k] = h2f(hb[k]);
-        } else {
-            if (dr) {
-#pragma unroll
-                for (int k = 0; k < kVec; ++k) h[j][k] = h[j][k] + df[j][k];
-            }
-            if (hr && in[j]) store8(hr + off[j], h[j]);
-        }
-        if (in[j]) {
-#pragma unroll
-            for (int k = 0; k < kVec; ++k) {
-                if constexpr (kLayer) acc += static_cast<double>(h[j][k]);
-                else acc += static_cast<double>(h[j][k] * h[j][k]);
-            }
-        }
+        for (int j = 0; j < NV; ++j) load8_row(dr + off[j], db[j]);
     }
-    acc = wave_sum_f64(acc);
-    if ((tid & 63) == 0) part[0][wave] = acc;
-    __syncthreads();
-    acc = part[0][0];
-#pragma unroll
-    for (int i = 1; i < W; ++i) acc += part[0][i];
-    float scale;
-    if constexpr (kLayer) {
-        const float mean = static_cast<float>(acc / static_cast<double>(dim));
-        double acc2 = 0.0;
+    if constexpr (kDelta) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
 #pragma unroll
             for (int k = 0; k < kVec; ++k) {
-                const float v = h[j][k] - mean;
-                h[j][k] = v;
-                if (in[j]) acc2 += static_cast<double>(v * v);
+                if constexpr (kF16) xb[j][k] = f2h(h2f(xb[j][k]) + h2f(db[j][k]));
+                else xb[j][k] = xb[j][k] + db[j][k];
             }
         }
-        acc2 = wave_sum_f64(acc2);
-        if ((tid & 63) == 0) part[1][wave] = acc2;
-        __syncthreads();
-        acc2 = part[1][0];
+    }
 #pragma unroll
-        for (int i = 1; i < W; ++i) acc2 += part[1][i];
+    for (int j = 0; j < NV; ++j) {
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) h[j][k] = to_f32(xb[j][k]);
+    }
+    double acc = lane_sum<NV, !kLayer>(h, in);
+    // The residual is stored once every load has been consumed: stores share
+    // the load counter on this GPU, so a later wait for a load would also wait
+    // for these stores.
+    if (hr && valid) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            if (in[j]) store8_row(hr + off[j], xb[j]);
+    }
+    acc = row_sum<W>(acc, part[0], slot, wave, lane);
+    float scale;
+    if constexpr (kLayer) {
+        const float mean = static_cast<float>(acc / static_cast<double>(dim));
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) h[j][k] = h[j][k] - mean;
+        }
+        double acc2 = lane_sum<NV, true>(h, in);
+        acc2 = row_sum<W>(acc2, part[1], slot, wave, lane);
         const float variance = static_cast<float>(acc2 / static_cast<double>(dim));
         scale = 1.0f / sqrtf(variance + eps);
     } else {
         const float ms = static_cast<float>(acc / static_cast<double>(dim));
         scale = 1.0f / sqrtf(ms + eps);
     }
+    if (!valid) return;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         if (in[j]) {
@@ -198,7 +229,14 @@ __global__ __launch_bounds__(64 * W) void norm_kernel_wg(const T * x, const T * 
 #pragma unroll
             for (int k = 0; k < kVec; ++k)
                 o[k] = norm_out<T, kLayer>(h[j][k] * scale, wv[j][k], kLayer ? bv[j][k] : 0.0f);
-            store8(yr + off[j], o);
+            if constexpr (kF16) {
+                uint16_t ob[kVec];
+#pragma unroll
+                for (int k = 0; k < kVec; ++k) ob[k] = f2h(o[k]);
+                store8_row(yr + off[j], ob);
+            } else {
+                store8_row(yr + off[j], o);
+            }
         }
     }
 }
@@ -268,16 +306,34 @@ int launch_norm(const void * xv, const void * dv, const void * wv, const void * 
     const int64_t grid = ceil_div(rows, kWaves);
     const bool vec = dim % kVec == 0 && aligned16(x) && (d == nullptr || aligned16(d)) && aligned16(w) &&
                      (b == nullptr || aligned16(b)) && (h == nullptr || aligned16(h)) && aligned16(y) &&
-                     dim <= 64 * kRowWaves * kVec * 4;
+                     dim <= 64 * 4 * kVec * 4;
     if (vec) {
-        // One row per 4-wave workgroup: 8 values per lane at dim 2048, so the
-        // per-lane chain load -> reduce -> store is short and every CU gets rows.
-        constexpr int W = kRowWaves;
-        const int groups = static_cast<int>(ceil_div(dim, 64 * W * kVec));
+        // Many rows: one wave per row up to 2048 elements (two or four waves
+        // for longer rows), four rows per workgroup. A few rows (decode): four
+        // waves per row, so each lane's share and chain stay short.
+        const int groups = static_cast<int>(ceil_div(dim, 64 * kVec));
+        const int wpr = rows < 512 ? 4 : groups <= 4 ? 1 : groups <= 8 ? 2 : 4;
+        const int nv = static_cast<int>(ceil_div(groups, wpr));
         const hipStream_t s = stream;
-        if (groups <= 1) norm_kernel_wg<T, P, kLayer, 1, W><<<rows, 64 * W, 0, s>>>(x, d, w, b, h, y, rows, dim, eps);
-        else if (groups <= 2) norm_kernel_wg<T, P, kLayer, 2, W><<<rows, 64 * W, 0, s>>>(x, d, w, b, h, y, rows, dim, eps);
-        else norm_kernel_wg<T, P, kLayer, 4, W><<<rows, 64 * W, 0, s>>>(x, d, w, b, h, y, rows, dim, eps);
+        const uint32_t grid_w = static_cast<uint32_t>(ceil_div(rows, 4 / wpr));
+#define LEVO_NORM_LAUNCH(NV, W)                                                                            \
+    do {                                                                                                   \
+        if (d) norm_kernel_wg<T, P, kLayer, true, NV, W><<<grid_w, kThreads, 0, s>>>(x, d, w, b, h, y, rows, dim, eps); \
+        else norm_kernel_wg<T, P, kLayer, false, NV, W><<<grid_w, kThreads, 0, s>>>(x, d, w, b, h, y, rows, dim, eps); \
+    } while (0)
+        if (wpr == 1) {
+            if (nv == 1) LEVO_NORM_LAUNCH(1, 1);
+            else if (nv == 2) LEVO_NORM_LAUNCH(2, 1);
+            else if (nv == 3) LEVO_NORM_LAUNCH(3, 1);
+            else LEVO_NORM_LAUNCH(4, 1);
+        } else if (wpr == 2) {
+            LEVO_NORM_LAUNCH(4, 2);
+        } else {
+            if (nv == 1) LEVO_NORM_LAUNCH(1, 4);
+            else if (nv == 2) LEVO_NORM_LAUNCH(2, 4);
+            else LEVO_NORM_LAUNCH(4, 4);
+        }
+#undef LEVO_NORM_LAUNCH
         return launch_status("levo_hip_residual_norm");
     }
     norm_kernel_loop<T, P, kLayer><<<grid, kThreads, 0, stream>>>(x, d, w, b, h, y, rows, dim, eps);

@@ -9,8 +9,8 @@
 // naturally aligned.
 //
 // Quantize: one lane per block; the wave's 64 consecutive blocks (a
-// 16-byte-aligned byte range) are assembled in LDS and written with dwordx4
-// stores. Dequantize: a wave stages 32 blocks in LDS and writes their values
+// 16-byte-aligned byte range) are assembled in LDS and written with
+// streaming (nontemporal) dwordx4 stores. Dequantize: a wave stages 32 blocks in LDS and writes their values
 // as contiguous 16-byte chunks.
 #include "common.hpp"
 #include "quant_block.hpp"
@@ -65,12 +65,29 @@ __device__ __forceinline__ void quantize_block(const float (&x)[32], uint8_t * l
         const uint16_t d16 = quantize_q8_0_block(x, pk);
         stage_block<8>(lds, lane, d16, pk);
     } else {
-        float amax = 0.0f, vmax = 0.0f;
+        // ggml's scan (the first value of largest |x|, NaN never taken) as
+        // four independent scans of 8 values joined in order: the strict
+        // comparison keeps the earliest quarter on ties, as the single scan
+        // keeps the earliest value.
+        float qa[4], qv[4];
 #pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            if (amax < fabsf(x[k])) {
-                amax = fabsf(x[k]);
-                vmax = x[k];
+        for (int q = 0; q < 4; ++q) {
+            qa[q] = 0.0f;
+            qv[q] = 0.0f;
+#pragma unroll
+            for (int k = 8 * q; k < 8 * q + 8; ++k) {
+                if (qa[q] < fabsf(x[k])) {
+                    qa[q] = fabsf(x[k]);
+                    qv[q] = x[k];
+                }
+            }
+        }
+        float amax = qa[0], vmax = qv[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+            if (amax < qa[q]) {
+                amax = qa[q];
+                vmax = qv[q];
             }
         }
         const float d = vmax / -8.0f;
@@ -169,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void quantize_dense_kernel(const S * __re
     const int64_t nvalid = nblocks - b0;
     if (nvalid >= 64 && dst_vec) {
         for (int i = lane; i < 64 * QB / 16; i += 64)
-            reinterpret_cast<u32x4 *>(out)[i] = reinterpret_cast<const u32x4 *>(lds)[i];
+            __builtin_nontemporal_store(reinterpret_cast<const u32x4 *>(lds)[i], reinterpret_cast<u32x4 *>(out) + i);
     } else if (nvalid > 0) {
         const int nbytes = static_cast<int>(nvalid < 64 ? nvalid : 64) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)
@@ -217,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void quantize_kernel(const S * __restrict
     const int64_t nvalid = nblocks - b0;
     if (nvalid >= 64 && dst_vec) {
         for (int i = lane; i < GB / 16; i += 64)
-            reinterpret_cast<u32x4 *>(out)[i] = reinterpret_cast<const u32x4 *>(lds)[i];
+            __builtin_nontemporal_store(reinterpret_cast<const u32x4 *>(lds)[i], reinterpret_cast<u32x4 *>(out) + i);
     } else if (nvalid > 0) {
         const int nbytes = static_cast<int>(nvalid < 64 ? nvalid : 64) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)

@@ -89,17 +89,25 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, ui
 // q = (int8_t)roundf(x * id). Writes the quants as 8 little-endian dwords and
 // returns d rounded to F16 (RNE).
 __device__ __forceinline__ uint16_t quantize_q8_0_block(const float (&x)[32], uint32_t (&pk)[8]) {
-    float amax = 0.0f;  // ggml's MAX(amax, fabsf(v)) in index order
-    float m = 0.0f;     // max of the non-NaN |x|
+    // |x| as an unsigned bit pattern orders like |x|, with every NaN above
+    // +inf: the integer maximum is amax whenever the block holds no NaN, and
+    // then the index-order MAX of the reference gives the same value.
+    uint32_t bits_max = 0u;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const float v = fabsf(x[k]);
-        amax = amax > v ? amax : v;
-        m = __builtin_fmaxf(m, v);
+    for (int k = 0; k < 32; ++k) bits_max = __builtin_elementwise_max(bits_max, __float_as_uint(x[k]) & 0x7fffffffu);
+    const bool has_nan = bits_max > 0x7f800000u;
+    float amax = __uint_as_float(bits_max);
+    if (has_nan) {
+        amax = 0.0f;  // ggml's MAX(amax, fabsf(v)) in index order: a NaN resets it
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const float v = fabsf(x[k]);
+            amax = amax > v ? amax : v;
+        }
     }
     const float d = amax / 127.0f;
     const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
-    if (m == amax) {
+    if (!has_nan) {
         // every |x| <= amax: |x * id| stays within 128 (or is NaN)
 #pragma unroll
         for (int w = 0; w < 8; ++w) {

@@ -137,6 +137,21 @@ def test_fp16_row_converters(hip, dev, oracle):
     assert np.array_equal(got2[ok[:65533]].view(np.uint32), want[:65533][ok[:65533]].view(np.uint32))
 
 
+@pytest.mark.parametrize("n", [4096 * 1536, 4096 * 1536 + 8 * 1023 + 5, 8 * 1024 * 3 + 8])
+def test_fp16_row_converters_large(hip, dev, oracle, n):
+    """Rows spanning many workgroups, each thread converting four groups of
+    eight a grid apart; sizes that leave the last pass ragged."""
+    import torch
+    f = oracle.gaussian(n, 2024 + n % 97) * 3.0
+    h = torch.empty(n, dtype=torch.int16, device=dev)
+    hip.fp32_to_fp16_row(to_dev(f, dev), h, n)
+    hb = from_dev(h).view(np.uint16)
+    assert np.array_equal(hb, oracle.f32_to_f16(f))
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    hip.fp16_to_fp32_row(h, out, n)
+    assert np.array_equal(from_dev(out).view(np.uint32), oracle.f16_to_f32(hb).view(np.uint32))
+
+
 @pytest.mark.parametrize("n,offset", [(64 * 2520, 0), (4099, 0), (1001, 1)])
 def test_checked_euler_matches_unchecked_and_stays_clear(hip, dev, oracle, n, offset):
     """The checked entry point updates bit-identically and leaves the flag 0."""

@@ -78,6 +78,29 @@ def test_f32_reference_chains(hip, dev, oracle, layer, D):
 
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+@pytest.mark.parametrize("rows,D", [(514, 2048), (513, 2056), (600, 3072), (520, 4104), (515, 8192), (511, 1536),
+                                    (7, 8192)])
+def test_row_layouts(hip, dev, oracle, f16, layer, rows, D):
+    """Every workgroup layout of the vector kernel: one wave per row (512 rows
+    or more, rows up to 2048), two or four waves per long row, and four waves
+    per row for fewer than 512 rows; row counts that leave the last
+    workgroup's row slots partly empty."""
+    x, d, w, b = _inputs(oracle, rows, D, rows + D, f16)
+    eps = 1e-6
+    h, y = _run(hip, dev, layer, x, d, w, b, eps)
+    if layer:
+        hw, yw = oracle.layer_norm(x, d, w, b, eps, threads=8)
+    else:
+        hw, yw = oracle.rms_norm(x, d, w, eps, threads=8)
+    assert np.array_equal(h, hw)
+    if f16:
+        assert f16_ulp(y, yw) <= 1
+    else:
+        assert f32_err(y, yw) <= 1e-5
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
 def test_scalar_path_and_optional_buffers(hip, dev, oracle, f16, layer):
     rows, D = 5, 1003
     x, d, w, b = _inputs(oracle, rows, D, 55, f16)

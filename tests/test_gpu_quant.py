@@ -73,6 +73,13 @@ def test_special_blocks(hip, dev, oracle, qt):
     x[7, :] = np.float32(-8.0) * np.arange(32) / 31                   # exact -8 multiples
     x[8, :] = 65504.0
     x[9, 5] = 1e30                                                    # huge outlier, F16 d overflows to inf
+    x[10, 5], x[10, 20] = -0.7, 0.7                                   # Q4_0: equal |x| in different 8-value quarters
+    x[11, 30], x[11, 9] = -0.7, 0.7                                   # ... first one positive, later one negative
+    x[12, 7], x[12, 8] = 0.7, -0.7                                    # ... at a quarter boundary
+    x[13, 24], x[13, 31] = -0.7, 0.7                                  # ... both in the last quarter
+    x[14, 0] = np.nan                                                 # NaN leading, tie later across quarters
+    x[14, 3], x[14, 27] = -0.7, 0.7
+    x[15, 6], x[15, 14], x[15, 22], x[15, 30] = 0.5, -0.6, 0.6, -0.6  # larger |x| in quarters 1, 2, 3
     out = torch.empty(64 * BB[qt], dtype=torch.uint8, device=dev)
     hip.quantize_chunk(qt, to_dev(x, dev), out, 0, 64, 32)
     got, want = from_dev(out), oracle.quantize(qt, x)
