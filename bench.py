@@ -23,10 +23,12 @@ chains; ggml itself is not available) run on a bounded sample on this host.
 from __future__ import annotations
 
 import argparse
+import concurrent.futures as cf
 import importlib.util
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
@@ -183,11 +185,76 @@ def add_ceilings(torch, head, dev, ops, warmup, steps):
                 e["of_ceiling"] = round(e["GB/s"] / c, 3)
 
 
-def cpu_threads():
+def cpu_share():
+    """Threads of the CPU share this process may use: its affinity set,
+    narrowed by OMP_NUM_THREADS when the environment sets one (the GPU box
+    sets it to the share it grants one GPU)."""
     try:
-        return max(1, min(16, len(os.sched_getaffinity(0))))
+        n = len(os.sched_getaffinity(0))
     except AttributeError:
-        return max(1, min(16, os.cpu_count() or 1))
+        n = os.cpu_count() or 1
+    try:
+        omp = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        omp = 0
+    return max(1, min(n, omp) if omp > 0 else n)
+
+
+def cpu_model():
+    """The host CPU as lscpu names it (model, sockets, cores, threads)."""
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    model = info.get("Model name")
+    if not model and os.path.exists("/proc/cpuinfo"):
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    return {"model": model, "sockets": info.get("Socket(s)"), "cores_per_socket": info.get("Core(s) per socket"),
+            "threads_per_core": info.get("Thread(s) per core"), "nproc": os.cpu_count()}
+
+
+class pinned:
+    """Runs the block on the first `threads` CPUs of the allowed set (the
+    reference pins its CPU runs with taskset)."""
+
+    def __init__(self, threads):
+        self.threads = threads
+
+    def __enter__(self):
+        try:
+            self.saved = os.sched_getaffinity(0)
+            os.sched_setaffinity(0, sorted(self.saved)[: self.threads])
+        except (AttributeError, OSError):
+            self.saved = None
+        return self
+
+    def __exit__(self, *exc):
+        if self.saved is not None:
+            os.sched_setaffinity(0, self.saved)
+
+
+def median_seconds(fn, warmup=3, runs=10):
+    """3 warm-ups, then the median wall time of `runs` timed calls."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def split_rows(n, parts):
+    step = -(-n // parts)
+    return [(i, min(n, i + step)) for i in range(0, n, step)]
 
 
 # ---------------------------------------------------------------------------------------
@@ -746,85 +813,143 @@ def bench_quant(torch, hip, head, dev, warmup, steps):
 
 
 # ---------------------------------------------------------------------------------------
-def cpu_baseline(host_ladder, budget_s=12.0):
-    """The oracle's five-pass ggml-cpu SnakeBeta chain on the ladder, all host threads."""
+def cpu_baseline(host_ladder, with_ops=True):
+    """The CPU leg, timed as the reference times its CPU runs: pinned to 1
+    thread and to every thread of the process's CPU share, 3 warm-ups and the
+    median of 10 runs, with the host CPU named. The headline is the oracle's
+    five-pass ggml-cpu SnakeBeta chain (mul, sin, sqr, div, add; rows split
+    over threads as ggml-cpu does) on the whole ladder at all threads; the
+    1-thread figure runs the first 32 channels of the 128 x 48384 rung (the
+    five passes over 1.5M elements take about 0.2 s on one core)."""
     from oracle.levo_oracle import Oracle
     orc = Oracle()
-    threads = cpu_threads()
+    threads = cpu_share()
     total_bytes = sum(snake_bytes(x.shape[0], x.shape[1]) for x, _, _ in host_ladder)
-    done, t0 = 0, time.perf_counter()
-    while True:
+
+    def ladder(t):
         for x, a, b in host_ladder:
-            orc.snake_beta(x, a, b, threads=threads)
-        done += 1
-        if time.perf_counter() - t0 > budget_s or done >= 50:
-            break
-    secs = time.perf_counter() - t0
-    return {"value": round(total_bytes * done / secs / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "ms_per_step": round(secs / done * 1e3, 2),
-            "sample": f"{done} full ladders (72,253,440 elements each) through the oracle's five-pass "
-                      f"ggml-cpu chain (mul, sin, sqr, div, add), {threads} threads, rows split as ggml-cpu"}
+            orc.snake_beta(x, a, b, threads=t)
+
+    with pinned(threads):
+        secs = median_seconds(lambda: ladder(threads))
+    x1, a1, b1 = next(t for t in host_ladder if t[0].shape == (128, 48384))
+    xs, as_, bs = np.ascontiguousarray(x1[:32]), a1[:32].copy(), b1[:32].copy()
+    with pinned(1):
+        secs1 = median_seconds(lambda: orc.snake_beta(xs, as_, bs, threads=1))
+    one = {"value": round(snake_bytes(32, 48384) / secs1 / 1e9, 4), "unit": "GB/s", "cores": 1,
+           "sample": "SnakeBeta 32 x 48384 (the first 32 channels of the 128 x 48384 rung), F32"}
+    out = {"value": round(total_bytes / secs / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+           "ms_per_step": round(secs * 1e3, 2), "one_thread": one, "cpu": cpu_model(),
+           "method": "pinned (sched_setaffinity) to 1 and to all threads of the CPU share; 3 warm-ups, "
+                     "median of 10 runs; oracle C restatement built with -O3",
+           "sample": f"the full ladder (72,253,440 elements) per run through the oracle's five-pass ggml-cpu "
+                     f"chain, {threads} threads"}
+    if with_ops:
+        out["ops"] = cpu_ops_baselines(orc, threads)
+    return out
 
 
-def cpu_ops_baselines():
-    """Bounded CPU timings of the other ops (single sample each)."""
-    from oracle.levo_oracle import Oracle, Reference, have_reference
-    orc = Oracle()
-    threads = cpu_threads()
+def cpu_ops_baselines(orc, threads):
+    """Every other op of the table on the CPU at 1 thread and at `threads`
+    (3 warm-ups, median of 10), in the GPU figures' algorithmic bytes. Ops
+    whose oracle function is single-threaded run as `threads` row chunks on a
+    thread pool (ctypes drops the GIL for the C call)."""
+    from oracle.levo_oracle import Reference, have_reference
     res = {}
+    pool = cf.ThreadPoolExecutor(threads)
+
+    def both(name, nbytes, one_fn, all_fn, sample, kind="port"):
+        with pinned(1):
+            t1 = median_seconds(one_fn)
+        with pinned(threads):
+            tn = median_seconds(all_fn)
+        res[name] = {"1_thread_GB/s": round(nbytes / t1 / 1e9, 3), f"{threads}_threads_GB/s": round(nbytes / tn / 1e9, 3),
+                     "1_thread_ms": round(t1 * 1e3, 3), f"{threads}_threads_ms": round(tn * 1e3, 3),
+                     "bytes": int(nbytes), "kind": kind, "sample": sample}
+
+    def chunked(fn, n):
+        parts = split_rows(n, threads)
+        return lambda: list(pool.map(lambda r: fn(*r), parts))
+
+    # SnakeBeta, one second of audio at 128 channels
+    x = orc.gaussian(128 * 48000, 11).reshape(128, 48000)
+    a = (orc.gaussian(128, 12) * 0.1).astype(np.float32)
+    both("snake_beta_128x48000", snake_bytes(128, 48000), lambda: orc.snake_beta(x, a, a, threads=1),
+         lambda: orc.snake_beta(x, a, a, threads=threads), "the five-pass ggml-cpu chain, rows split over threads")
+    # residual norms, F16 activations and parameters
     rows, D = 756, 2048
-    x = orc.f32_to_f16(orc.gaussian(rows * D, 1).reshape(rows, D))
-    d = orc.f32_to_f16(orc.gaussian(rows * D, 2).reshape(rows, D))
+    xh = orc.f32_to_f16(orc.gaussian(rows * D, 1).reshape(rows, D))
+    dh = orc.f32_to_f16(orc.gaussian(rows * D, 2).reshape(rows, D))
     w = orc.f32_to_f16(orc.gaussian(D, 3) * 0.02 + 1)
-    t0 = time.perf_counter()
-    reps = 0
-    while time.perf_counter() - t0 < 1.0:
-        orc.rms_norm(x, d, w, 1e-6, threads=threads)
-        reps += 1
-    res["rmsnorm_f16_756x2048"] = {"GB/s": round(8 * rows * D * reps / (time.perf_counter() - t0) / 1e9, 3),
-                                   "cores": threads, "kind": "port"}
+    bb = orc.f32_to_f16(orc.gaussian(D, 4) * 0.02)
+    both(f"residual_rmsnorm_f16_{rows}x{D}", 8 * rows * D + 2 * D,
+         lambda: orc.rms_norm(xh, dh, w, 1e-6, threads=1), lambda: orc.rms_norm(xh, dh, w, 1e-6, threads=threads),
+         "add, cast, rms_norm, cast, mul (ggml-cpu chain), rows split over threads")
+    both(f"residual_layernorm_f16_{rows}x{D}", 8 * rows * D + 4 * D,
+         lambda: orc.layer_norm(xh, dh, w, bb, 1e-6, threads=1),
+         lambda: orc.layer_norm(xh, dh, w, bb, 1e-6, threads=threads),
+         "add, norm, mul, add (ggml-cpu chain), rows split over threads")
+    # Flow CFG + Euler, one step of the 64 x 2520 latent
     n = 64 * 2520
     st, vu, vc = orc.gaussian(n, 4), orc.gaussian(n, 5), orc.gaussian(n, 6)
-    t0 = time.perf_counter()
-    reps = 0
-    while time.perf_counter() - t0 < 0.5:
-        orc.flow_cfg_euler(st, vu, vc, 1.5, 0.02)
-        reps += 1
-    res["flow_cfg_euler"] = {"GB/s": round(16 * n * reps / (time.perf_counter() - t0) / 1e9, 3), "cores": 1,
-                             "kind": "port"}
-    xq = orc.f32_to_f16((orc.gaussian(4096 * 1536, 7) * 0.02).reshape(4096, 1536))
-    t0 = time.perf_counter()
-    orc.quantize_f16_padded(8, xq, 1536)
-    secs = time.perf_counter() - t0
-    res["q8_0_quantize_f16"] = {"GB/s": round((2 + 34 / 32) * xq.size / secs / 1e9, 3), "cores": 1, "kind": "port"}
+    both("flow_cfg_euler_64x2520", 16 * n, lambda: orc.flow_cfg_euler(st, vu, vc, 1.5, 0.02),
+         chunked(lambda i, j: orc.flow_cfg_euler(st[i:j], vu[i:j], vc[i:j], 1.5, 0.02), n),
+         "the renderer's host CFG + Euler loop (src/levo-flow-renderer.cpp), one step")
+    # Q8_0 / Q4_0 blocks and F16 <-> F32 rows at [4096, 1536]
+    R, C = 4096, 1536
+    xq = orc.f32_to_f16((orc.gaussian(R * C, 7) * 0.02).reshape(R, C))
+    for qt, name, bsz in ((8, "q8_0", 34), (2, "q4_0", 18)):
+        q = orc.quantize_f16_padded(qt, xq, C)
+        both(f"{name}_quantize_f16", 2 * R * C + R * C // 32 * bsz, lambda: orc.quantize_f16_padded(qt, xq, C),
+             chunked(lambda i, j: orc.quantize_f16_padded(qt, xq[i:j], C), R),
+             "ggml's reference block quantizer over F16 rows (ggml_quantize_chunk's path)")
+        qb = q.reshape(R, -1)
+        both(f"{name}_dequantize_f32", R * C // 32 * bsz + 4 * R * C, lambda: orc.dequantize(qt, q, R * C),
+             chunked(lambda i, j: orc.dequantize(qt, np.ascontiguousarray(qb[i:j]), (j - i) * C), R),
+             "ggml's dequantize_row to F32")
+    f = orc.gaussian(R * C, 9)
+    h = orc.f32_to_f16(f)
+    both("fp32_to_fp16_row", 6 * R * C, lambda: orc.f32_to_f16(f),
+         chunked(lambda i, j: orc.f32_to_f16(f[i * C:j * C]), R), "ggml_fp32_to_fp16_row (RNE)")
+    both("fp16_to_fp32_row", 6 * R * C, lambda: orc.f16_to_f32(h),
+         chunked(lambda i, j: orc.f16_to_f32(h[i * C:j * C]), R), "ggml_fp16_to_fp32_row")
     if have_reference():
         ref = Reference()
-        V = 16384
-        c = orc.gaussian(60 * V, 8) * 3
-        u = orc.gaussian(60 * V, 9) * 3
-        s = ref.sampler(1)
-        t0 = time.perf_counter()
-        for r in range(60):
-            l = ref.apply_cfg(c[r * V:(r + 1) * V], u[r * V:(r + 1) * V], 1.5)
-            s.sample(l, 50, 0.9, True)
-        secs = time.perf_counter() - t0
-        res["cfg_sample_top50"] = {"GB/s": round(60 * 2 * V * 4 / secs / 1e9, 3), "rows_per_s": round(60 / secs, 1),
-                                   "cores": 1, "kind": "reference",
-                                   "sample": "60 rows of 16384: levo::apply_cfg + Sampler::sample(top-50, T=0.9)"}
+        V, per = 16384, 60
+        c = orc.gaussian(per * V, 8) * 3
+        u = orc.gaussian(per * V, 9) * 3
+        samplers = [ref.sampler(1 + t) for t in range(threads)]
+
+        def rows_on(t, lo, hi):
+            for r in range(lo, hi):
+                logit = ref.apply_cfg(c[r * V:(r + 1) * V], u[r * V:(r + 1) * V], 1.5)
+                samplers[t].sample(logit, 50, 0.9, True)
+
+        with pinned(1):
+            t1 = median_seconds(lambda: rows_on(0, 0, per))
+        with pinned(threads):
+            tn = median_seconds(lambda: list(pool.map(lambda t: rows_on(t, 0, per), range(threads))))
+        res["cfg_softmax_top50"] = {
+            "1_thread_GB/s": round(per * 2 * V * 4 / t1 / 1e9, 3),
+            f"{threads}_threads_GB/s": round(threads * per * 2 * V * 4 / tn / 1e9, 3),
+            "1_thread_rows_per_s": round(per / t1, 1), f"{threads}_threads_rows_per_s": round(threads * per / tn, 1),
+            "kind": "reference",
+            "sample": f"{per} rows of 16384 per thread: levo::apply_cfg + Sampler::sample(top-50, T=0.9), "
+                      f"each thread its own Sampler"}
         V2 = 16385
         streams = (orc.gaussian(3 * V2, 10) * 3).reshape(3, V2)
         recent = (np.arange(150, dtype=np.int64) * 97 % (V2 - 1)).reshape(3, 50)
         s2 = ref.sampler(2)
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 1.0:
-            s2.sample_streams(streams, use_sampling=True, temperature=0.9, top_k_mixed=50, top_k_detail=1,
-                              repetition_penalty=1.1, recent=recent, ignore=(0, 1, 2))
-            reps += 1
+        with pinned(1):
+            t1 = median_seconds(lambda: s2.sample_streams(streams, use_sampling=True, temperature=0.9,
+                                                          top_k_mixed=50, top_k_detail=1, repetition_penalty=1.1,
+                                                          recent=recent, ignore=(0, 1, 2)))
         res["decode_step_sample"] = {
-            "us_per_step": round((time.perf_counter() - t0) / reps * 1e6, 1), "cores": 1, "kind": "reference",
+            "1_thread_us_per_step": round(t1 * 1e6, 1), "kind": "reference",
             "sample": "Sampler::sample_streams over 3 host rows of 16385 (penalty window 50, 3 ignored ids, "
-                      "top-k 50/1/1, T = 0.9); the reference first copies 2 x 196 KB of logits to the host"}
+                      "top-k 50/1/1, T = 0.9), one step at a time (a decode step is serial); the reference "
+                      "first copies 2 x 196 KB of logits to the host"}
+    pool.shutdown()
     return res
 
 
@@ -1013,9 +1138,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log("cpu baseline: start")
-        cpu = cpu_baseline(lad["host"])
-        if not args.no_ops:
-            cpu["ops"] = cpu_ops_baselines()
+        cpu = cpu_baseline(lad["host"], with_ops=not args.no_ops)
         log("cpu baseline: done")
 
     value = lad["ladder_bytes"] / (lad["ms_per_step"] * 1e-3) / 1e9
