@@ -202,6 +202,7 @@ struct row_lds {
     uint32_t ign[kWords];     // ignored ids (stream 0)
     float cv[kWaves][kSegCap];  // gathered candidate values, one segment per wave
     int ci[kWaves][kSegCap];    // and their ids
+    uint32_t hist[256];         // digit histogram of the one-wave radix select
     float wmax[kWaves];
     float wbv[kWaves];   // each wave's value at its first maximum
     float wlow[kWaves];
@@ -225,6 +226,63 @@ __device__ __forceinline__ float adjusted_logit(const levo_hip_sample_args & a, 
     if (pen && (L.pen[idx >> 5] & bit)) v = v / a.repetition_penalty;
     if (ign && (L.ign[idx >> 5] & bit)) v = -INFINITY;
     return v;
+}
+
+// One wave's LDS operations complete in issue order; the fence keeps the
+// compiler from moving them across each other and waits for their results.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The k-th largest of the valid keys (k >= 1), all of which share `prefix`'s
+// bits above bit `top`, by one wave: a radix select over digits of up to 8
+// bits from bit `top` down. Each pass histograms the digit of the keys that
+// match the digits chosen so far (LDS atomics), scans the 256 bins from the
+// top (four per lane), and keeps the largest digit d whose keys at or above
+// it number at least the still-needed count. This is the largest t with
+// #{keys >= t} >= k, the same value a bit-by-bit bisection finds; when fewer
+// than k keys exist the remaining digits are 0 (every key is kept).
+template <int NS>
+__device__ __forceinline__ uint32_t radix_kth_key(uint32_t * hist, const uint32_t (&keys)[NS],
+                                                  const bool (&valid)[NS], int k, uint32_t prefix, int top) {
+    const int lane = threadIdx.x & 63;
+    int need = k;
+    for (int hi = top; hi >= 0;) {  // uniform
+        const int width = hi + 1 < 8 ? hi + 1 : 8;
+        const int lo = hi + 1 - width;
+        const uint32_t mask = (1u << width) - 1u;
+        reinterpret_cast<u32x4 *>(hist)[lane] = u32x4{0u, 0u, 0u, 0u};
+        wave_lds_order();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const bool match = hi == 31 || ((keys[s] ^ prefix) >> (hi + 1)) == 0u;
+            if (valid[s] && match) atomicAdd(&hist[(keys[s] >> lo) & mask], 1u);
+        }
+        wave_lds_order();
+        const u32x4 b = reinterpret_cast<const u32x4 *>(hist)[lane];
+        const int local = static_cast<int>(b[0] + b[1] + b[2] + b[3]);
+        const int incl = wave_inclusive_scan_i32(local);
+        const int above = dpp::lane(incl, 63) - incl;  // keys in the bins of higher lanes
+        const int s3 = above + static_cast<int>(b[3]);
+        const int s2 = s3 + static_cast<int>(b[2]);
+        const int s1 = s2 + static_cast<int>(b[1]);
+        const int s0 = s1 + static_cast<int>(b[0]);
+        const uint64_t q = __ballot(s0 >= need);
+        uint32_t digit = 0u;
+        if (q != 0u) {
+            const int owner = 63 - __builtin_clzll(q);
+            const int j = s3 >= need ? 3 : s2 >= need ? 2 : s1 >= need ? 1 : 0;
+            const int higher = j == 3 ? above : j == 2 ? s3 : j == 1 ? s2 : s1;  // keys in bins above the digit
+            digit = static_cast<uint32_t>(__builtin_amdgcn_readlane(4 * lane + j, owner));
+            need -= __builtin_amdgcn_readlane(higher, owner);
+        }
+        prefix = (prefix & ~(mask << lo)) | (digit << lo);
+        hi = lo - 1;
+        wave_lds_order();  // every lane has read the bins before the next pass clears them
+    }
+    return prefix;
 }
 
 // Exclusive prefix of the bitmap popcounts into L.prefix; returns the total
@@ -630,15 +688,8 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
         const uint32_t hi_key = float_key(m);
         const uint32_t diff = lo_key ^ hi_key;
         const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
-        uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
-        for (int bit = top; bit >= 0; --bit) {
-            const uint32_t cand = prefix | (1u << bit);
-            int cnt = 0;
-#pragma unroll
-            for (int s = 0; s < kSlots; ++s) cnt += static_cast<int>(__popcll(__ballot(keys[s] >= cand)));
-            if (cnt >= k) prefix = cand;
-        }
-        tau = prefix;
+        const uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
+        tau = radix_kth_key<kSlots>(L.hist, keys, valid, k, prefix, top);
     }
 
     // ---- E. mark the candidates >= tau in the id bitmap; weight sum ---------------
