@@ -177,7 +177,7 @@ def add_ceilings(torch, head, dev, ops, warmup, steps):
     for entry in ops.values():
         entries = entry.values() if "bytes_per_launch" not in entry else [entry]
         for e in entries:
-            if isinstance(e, dict) and "bytes_per_launch" in e and e.get("bound") not in ("mfma", "latency"):
+            if isinstance(e, dict) and "bytes_per_launch" in e and e.get("bound") not in ("mfma", "latency", "valu"):
                 c, vpt = stream_ceiling(torch, head, dev, e.get("read_bytes", e["bytes_per_launch"]),
                                         e.get("write_bytes", 0), warmup, steps)
                 e["ceiling_GB/s"] = c
@@ -796,6 +796,22 @@ def bench_quant(torch, hip, head, dev, warmup, steps):
         out[f"{name}_dequantize_f32"] = op_entry(per_d, ms, read=qbytes, shape=[R, Cc])
         del src, q, deq
         torch.cuda.empty_cache()
+    # the K-quant profiles' quantizers (quantize_row_q{4,5,6}_K_ref) on the same F16 matrix: a scale search
+    # per 32- (16-) value sub-block, VALU-bound
+    for qt, name, bb in ((12, "q4_K", 144), (13, "q5_K", 176), (14, "q6_K", 210)):
+        qbytes = R * Cc // 256 * bb
+        per_q = 2 * R * Cc + qbytes
+        n = math.ceil(ROTATE_BYTES / per_q) + 1
+        g = torch.Generator(device=dev)
+        g.manual_seed(qt)
+        src = [(torch.randn((R, Cc), generator=g, device=dev) * 0.02).half() for _ in range(n)]
+        q = [torch.empty(qbytes, dtype=torch.uint8, device=dev) for _ in range(n)]
+        ms = time_op(torch, head, lambda i: hip.quantize_rows(qt, src[i], 1, Cc, Cc, q[i], R, Cc), n, warmup,
+                     max(steps, 20))
+        out[f"{name}_quantize_f16"] = op_entry(per_q, ms, read=2 * R * Cc, shape=[R, Cc], bound="valu",
+                                               sub_blocks_per_s=round(R * Cc / (32 if qt != 14 else 16) / (ms * 1e-3)))
+        del src, q
+        torch.cuda.empty_cache()
     # the converter's F16 <-> F32 rows (ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row) at the same shape
     per = 6 * R * Cc
     n = math.ceil(ROTATE_BYTES / per) + 1
@@ -907,6 +923,13 @@ def cpu_ops_baselines(orc, threads):
         both(f"{name}_dequantize_f32", R * C // 32 * bsz + 4 * R * C, lambda: orc.dequantize(qt, q, R * C),
              chunked(lambda i, j: orc.dequantize(qt, np.ascontiguousarray(qb[i:j]), (j - i) * C), R),
              "ggml's dequantize_row to F32")
+    for qt, name, bsz in ((12, "q4_K", 144), (13, "q5_K", 176), (14, "q6_K", 210)):
+        rows_k = 256  # a 256-row slice of the matrix: the scale search costs ~0.1 s per slice on one core
+        xk = np.ascontiguousarray(xq[:rows_k])
+        both(f"{name}_quantize_f16", 2 * rows_k * C + rows_k * C // 256 * bsz,
+             lambda: orc.quantize_f16_padded(qt, xk, C),
+             chunked(lambda i, j: orc.quantize_f16_padded(qt, xk[i:j], C), rows_k),
+             f"ggml's quantize_row_{name}_ref over {rows_k} F16 rows of 1536 (GB/s of the same bytes)")
     f = orc.gaussian(R * C, 9)
     h = orc.f32_to_f16(f)
     both("fp32_to_fp16_row", 6 * R * C, lambda: orc.f32_to_f16(f),

@@ -497,10 +497,14 @@ int64_t levo_hip_row_size(levo_hip_type type, int64_t n_per_row);
 
 /* Replaces ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row,
  * imatrix) as called at tools/levo-quantize.cpp:386-388 (ggml's
- * quantize_row_q8_0_ref / quantize_row_q4_0_ref). Returns the bytes written
- * (nrows * row size) or a negative levo_hip_status. Q8_0 ignores imatrix as
- * ggml does; Q4_0 requires imatrix == NULL. dst needs 2-byte alignment
- * (16-byte aligned destinations take the dwordx4 store path). */
+ * quantize_row_q8_0_ref / quantize_row_q4_0_ref, and for the Q4_K_M / Q5_K_M
+ * / Q6_K profiles quantize_row_q4_K_ref / q5_K_ref / q6_K_ref with n_per_row
+ * a multiple of 256: block_q4_K 144 B, block_q5_K 176 B, block_q6_K 210 B).
+ * Returns the bytes written (nrows * row size) or a negative levo_hip_status.
+ * Q8_0 ignores imatrix as ggml does; the other types require imatrix ==
+ * NULL (the tool passes NULL). Q8_0 / Q4_0 dst needs 2-byte alignment
+ * (16-byte aligned destinations take the dwordx4 store path); K-quant dst
+ * any alignment. The source values must be finite, as the tool checks. */
 int64_t levo_hip_quantize_chunk(levo_hip_type type, const float * src, void * dst,
                                 int64_t start, int64_t nrows, int64_t n_per_row,
                                 const float * imatrix, levo_hip_stream_t stream);
@@ -508,7 +512,8 @@ int64_t levo_hip_quantize_chunk(levo_hip_type type, const float * src, void * ds
 /* write_tensor's chunk path fused into one pass (tools/levo-quantize.cpp:
  * 355-388): rows of src_cols values (src_type F32 or F16, widened exactly),
  * row stride src_row_stride elements, zero-padded to dst_cols (a multiple of
- * 32, >= src_cols) and quantized. Returns bytes written or < 0. */
+ * 32 for Q8_0 / Q4_0, of 256 for Q4_K / Q5_K / Q6_K, >= src_cols) and
+ * quantized. Returns bytes written or < 0. */
 int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, levo_hip_type src_type,
                                int64_t src_cols, int64_t src_row_stride, void * dst,
                                int64_t nrows, int64_t dst_cols, levo_hip_stream_t stream);

@@ -40,6 +40,10 @@ int device_cu_count();
 // K-quant helpers shared by the quantizer entry points (kquant.hip).
 bool is_kquant(levo_hip_type type);
 int64_t kquant_block_bytes(levo_hip_type type);  // Q4_K / Q5_K / Q6_K / Q8_K per 256 values; 0 otherwise
+// ggml's quantize_row_q{4,5,6}_K_ref over rows of src (F32 or F16, src_cols
+// values each, src_stride apart, zero-padded to dst_cols, a multiple of 256).
+int quantize_kquant_rows(levo_hip_type type, const void * src, levo_hip_type src_type, int64_t src_cols,
+                         int64_t src_stride, void * dst, int64_t nrows, int64_t dst_cols, hipStream_t stream);
 int dequantize_kquant(levo_hip_type type, const void * src, void * dst, levo_hip_type dst_type, int64_t k,
                       hipStream_t stream);
 

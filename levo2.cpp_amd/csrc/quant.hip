@@ -369,6 +369,22 @@ extern "C" int64_t levo_hip_row_size(levo_hip_type type, int64_t n_per_row) {
 extern "C" int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, levo_hip_type src_type,
                                           int64_t src_cols, int64_t src_row_stride, void * dst,
                                           int64_t nrows, int64_t dst_cols, levo_hip_stream_t stream) {
+    if (type == LEVO_HIP_TYPE_Q4_K || type == LEVO_HIP_TYPE_Q5_K || type == LEVO_HIP_TYPE_Q6_K) {
+        LEVO_REQUIRE(src_type == LEVO_HIP_TYPE_F32 || src_type == LEVO_HIP_TYPE_F16,
+                     "quantize: source must be F32 or F16");
+        LEVO_REQUIRE(nrows >= 0 && src_cols >= 0 && dst_cols >= 0, "quantize: negative shape");
+        LEVO_REQUIRE(dst_cols % 256 == 0, "quantize: K-quant storage width must be a multiple of 256");
+        LEVO_REQUIRE(dst_cols >= src_cols, "quantize: storage width is smaller than the source width");
+        LEVO_REQUIRE(src_row_stride >= src_cols, "quantize: source row stride is smaller than the width");
+        const int64_t bytes = nrows * (dst_cols / 256) * kquant_block_bytes(type);
+        if (bytes == 0) return 0;
+        LEVO_REQUIRE(src != nullptr && dst != nullptr, "quantize: null pointer");
+        LEVO_REQUIRE((reinterpret_cast<uintptr_t>(src) & (src_type == LEVO_HIP_TYPE_F16 ? 1u : 3u)) == 0,
+                     "quantize: source is not aligned to its element size");
+        const int r = quantize_kquant_rows(type, src, src_type, src_cols, src_row_stride, dst, nrows, dst_cols,
+                                           as_hip(stream));
+        return r == LEVO_HIP_OK ? bytes : r;
+    }
     LEVO_REQUIRE(type == LEVO_HIP_TYPE_Q8_0 || type == LEVO_HIP_TYPE_Q4_0,
                  "quantize: unsupported block type %d", static_cast<int>(type));
     LEVO_REQUIRE(src_type == LEVO_HIP_TYPE_F32 || src_type == LEVO_HIP_TYPE_F16,
@@ -400,13 +416,16 @@ extern "C" int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, 
 extern "C" int64_t levo_hip_quantize_chunk(levo_hip_type type, const float * src, void * dst, int64_t start,
                                            int64_t nrows, int64_t n_per_row, const float * imatrix,
                                            levo_hip_stream_t stream) {
-    LEVO_REQUIRE(type == LEVO_HIP_TYPE_Q8_0 || type == LEVO_HIP_TYPE_Q4_0,
+    const bool kq = type == LEVO_HIP_TYPE_Q4_K || type == LEVO_HIP_TYPE_Q5_K || type == LEVO_HIP_TYPE_Q6_K;
+    LEVO_REQUIRE(type == LEVO_HIP_TYPE_Q8_0 || type == LEVO_HIP_TYPE_Q4_0 || kq,
                  "quantize_chunk: unsupported block type %d", static_cast<int>(type));
-    LEVO_REQUIRE(type != LEVO_HIP_TYPE_Q4_0 || imatrix == nullptr,
-                 "quantize_chunk: Q4_0 with an importance matrix is not implemented");
-    LEVO_REQUIRE(n_per_row > 0 && n_per_row % 32 == 0, "quantize_chunk: row length must be a multiple of 32");
+    LEVO_REQUIRE(type == LEVO_HIP_TYPE_Q8_0 || imatrix == nullptr,
+                 "quantize_chunk: this block type with an importance matrix is not implemented");
+    LEVO_REQUIRE(n_per_row > 0 && n_per_row % (kq ? 256 : 32) == 0,
+                 kq ? "quantize_chunk: K-quant row length must be a multiple of 256"
+                    : "quantize_chunk: row length must be a multiple of 32");
     LEVO_REQUIRE(start >= 0 && start % n_per_row == 0, "quantize_chunk: start must be a row boundary");
-    const int64_t row_size = n_per_row / 32 * block_bytes(type);
+    const int64_t row_size = kq ? n_per_row / 256 * kquant_block_bytes(type) : n_per_row / 32 * block_bytes(type);
     uint8_t * d = dst ? static_cast<uint8_t *>(dst) + (start / n_per_row) * row_size : nullptr;
     return levo_hip_quantize_rows(type, src ? src + start : nullptr, LEVO_HIP_TYPE_F32, n_per_row, n_per_row, d,
                                   nrows, n_per_row, stream);

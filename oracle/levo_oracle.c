@@ -649,17 +649,25 @@ void lo_dequantize_row_q4_0(const void * in, float * y, int64_t k) {
 static size_t lo_row_size(int type, int64_t n) {
     if (type == LO_TYPE_Q8_0) return (size_t)(n / 32) * 34u;
     if (type == LO_TYPE_Q4_0) return (size_t)(n / 32) * 18u;
+    if (type == LO_TYPE_Q4_K) return (size_t)(n / 256) * 144u;
+    if (type == LO_TYPE_Q5_K) return (size_t)(n / 256) * 176u;
+    if (type == LO_TYPE_Q6_K) return (size_t)(n / 256) * 210u;
     return 0;
 }
 
 size_t lo_quantize_chunk(int type, const float * src, void * dst, int64_t start, int64_t nrows,
                          int64_t n_per_row) {
+    const int kq = type == LO_TYPE_Q4_K || type == LO_TYPE_Q5_K || type == LO_TYPE_Q6_K;
     const size_t row_size = lo_row_size(type, n_per_row);
-    if (row_size == 0 || n_per_row % 32 != 0 || start % n_per_row != 0) return 0;
+    if (row_size == 0 || n_per_row % (kq ? 256 : 32) != 0 || start % n_per_row != 0) return 0;
     const int64_t start_row = start / n_per_row;
     unsigned char * out = (unsigned char *)dst + (size_t)start_row * row_size;
-    if (type == LO_TYPE_Q8_0) lo_quantize_row_q8_0(src + start, out, nrows * n_per_row);
-    else lo_quantize_row_q4_0(src + start, out, nrows * n_per_row);
+    const int64_t n = nrows * n_per_row;
+    if (type == LO_TYPE_Q8_0) lo_quantize_row_q8_0(src + start, out, n);
+    else if (type == LO_TYPE_Q4_0) lo_quantize_row_q4_0(src + start, out, n);
+    else if (type == LO_TYPE_Q4_K) lo_quantize_row_q4_K(src + start, out, n);
+    else if (type == LO_TYPE_Q5_K) lo_quantize_row_q5_K(src + start, out, n);
+    else lo_quantize_row_q6_K(src + start, out, n);
     return (size_t)nrows * row_size;
 }
 
@@ -794,6 +802,312 @@ void lo_quantize_row_q8_K(const float * x, void * out, int64_t k) {
             for (int ii = 0; ii < 16; ++ii) sum += qs[j * 16 + ii];
             const int16_t s16 = (int16_t)sum;
             memcpy(blk + 260 + 2 * j, &s16, 2);
+        }
+    }
+}
+
+/* ---- K-quant block quantizers: ggml's quantize_row_q{4,5,6}_K_ref as
+ * reached from ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row,
+ * NULL) (tools/levo-quantize.cpp:386-388; no importance matrix). Restated
+ * from ggml's published source (ggml-quants.c at the reference's pinned
+ * submodule 8846b79e): make_qkx2_quants (Q4_K / Q5_K) and make_qx_quants
+ * with rmse_type 1 (Q6_K). These routines live in ggml-base, built for the
+ * baseline x86-64 ISA (no FMA instructions), so every float operation rounds
+ * on its own, as this library does (-ffp-contract=off). Inputs are finite
+ * (write_tensor rejects non-finite tensors, tools/levo-quantize.cpp:330). */
+
+#define LO_GROUP_MAX_EPS 1e-15f
+
+/* make_qkx2_quants: an affine code L in [0, nmax] with scale and min found by
+ * a grid of nstep + 1 trial inverse scales around nmax / (max - min), each
+ * refined by a weighted least-squares fit of (scale, min) to the codes; the
+ * trial with the smallest weighted squared error wins. `min` and the trial
+ * scales follow each accepted trial (as in ggml). Returns the scale and
+ * stores -min in *the_min. */
+static float lo_make_qkx2_quants(int n, int nmax, const float * x, const float * weights, uint8_t * L,
+                                 float * the_min, uint8_t * Laux, float rmin, float rdelta, int nstep) {
+    float min = x[0];
+    float max = x[0];
+    float sum_w = weights[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *the_min = -min;
+        return 0.f;
+    }
+    float iscale = nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_mad = 0;
+    for (int i = 0; i < n; ++i) {
+        const int l = lo_nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t)(l < 0 ? 0 : l > nmax ? nmax : l);
+        float diff = scale * L[i] + min - x[i];
+        diff = diff * diff;
+        const float w = weights[i];
+        best_mad += w * diff;
+    }
+    if (nstep < 1) {
+        *the_min = -min;
+        return scale;
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = lo_nearest_int(iscale * (x[i] - min));
+            l = l < 0 ? 0 : l > nmax ? nmax : l;
+            Laux[i] = (uint8_t)l;
+            const float w = weights[i];
+            sum_l += w * l;
+            sum_l2 += w * l * l;
+            sum_xl += w * l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float mad = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = this_scale * Laux[i] + this_min - x[i];
+                diff = diff * diff;
+                const float w = weights[i];
+                mad += w * diff;
+            }
+            if (mad < best_mad) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_mad = mad;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+/* make_qx_quants(n, nmax, x, L, rmse_type = 1, qw = NULL): symmetric codes
+ * L - nmax in [-nmax, nmax - 1] from the signed extreme, weights x^2, the
+ * least-squares scale, then 18 trial inverse scales -(nmax + 0.1 is) / max
+ * (is = -9..9, not 0), keeping the one that maximizes sumlx^2 / suml2. */
+static float lo_make_qx_quants(int n, int nmax, const float * x, int8_t * L) {
+    float max = 0;
+    float amax = 0;
+    for (int i = 0; i < n; ++i) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
+        }
+    }
+    if (amax < LO_GROUP_MAX_EPS) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        return 0.f;
+    }
+    float iscale = -nmax / max;
+    float sumlx = 0;
+    float suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = lo_nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+        L[i] = (int8_t)(l + nmax);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * l;
+        suml2 += w * l * l;
+    }
+    float scale = suml2 ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    for (int is = -9; is <= 9; ++is) {
+        if (is == 0) continue;
+        iscale = -(nmax + 0.1f * is) / max;
+        sumlx = suml2 = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = lo_nearest_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * l;
+            suml2 += w * l * l;
+        }
+        if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; ++i) {
+                int l = lo_nearest_int(iscale * x[i]);
+                l = l < -nmax ? -nmax : l > nmax - 1 ? nmax - 1 : l;
+                L[i] = (int8_t)(nmax + l);
+            }
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+static uint16_t lo_h16(float f) { return lo_fp32_to_fp16(f); }
+
+static void lo_put_h(unsigned char * p, float f) {
+    const uint16_t h = lo_h16(f);
+    p[0] = (unsigned char)(h & 0xff);
+    p[1] = (unsigned char)(h >> 8);
+}
+
+/* quantize_row_q4_K_ref (nmax 15, rmin -1, rdelta 0.1, 20 steps) and
+ * quantize_row_q5_K_ref (nmax 31, rmin -0.5, rdelta 0.1, 15 steps): per
+ * 32-value sub-block weights sqrt(mean x^2) + |x|, make_qkx2_quants; the
+ * eight scales and mins quantized to 6 bits against the largest of each
+ * (d = max_scale / 63, dmin = max_min / 63, stored F16); every value then
+ * re-coded as nearest_int((x + dmin*m) / (d*sc)) (a sub-block whose quantized
+ * scale is 0 keeps its make_qkx2_quants codes). */
+static void lo_quantize_row_q45_K(int q5, const float * x, void * out, int64_t k) {
+    unsigned char * y = (unsigned char *)out;
+    const int nmax = q5 ? 31 : 15;
+    const int bsz = q5 ? 176 : 144;
+    for (int64_t i = 0; i < k / 256; ++i, x += 256) {
+        unsigned char * blk = y + i * bsz;
+        uint8_t L[256], Laux[32];
+        float weights[32], mins[8], scales[8];
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < 8; ++j) {
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+            scales[j] = q5 ? lo_make_qkx2_quants(32, nmax, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -0.5f, 0.1f, 15)
+                           : lo_make_qkx2_quants(32, nmax, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+        const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+        unsigned char * sc = blk + 4;
+        memset(sc, 0, 12);
+        for (int j = 0; j < 8; ++j) {
+            uint8_t ls = (uint8_t)lo_nearest_int(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t)lo_nearest_int(inv_min * mins[j]);
+            ls = ls < 63 ? ls : 63;
+            lm = lm < 63 ? lm : 63;
+            if (j < 4) {
+                sc[j] = ls;
+                sc[j + 4] = lm;
+            } else {
+                sc[j + 4] = (unsigned char)((ls & 0xF) | ((lm & 0xF) << 4));
+                sc[j - 4] |= (unsigned char)((ls >> 4) << 6);
+                sc[j - 0] |= (unsigned char)((lm >> 4) << 6);
+            }
+        }
+        lo_put_h(blk, max_scale / 63.f);
+        lo_put_h(blk + 2, max_min / 63.f);
+        const float d16 = lo_h(blk), dmin16 = lo_h(blk + 2);
+        for (int j = 0; j < 8; ++j) {
+            int s, m;
+            lo_scale_min_k4(j, sc, &s, &m);
+            const float d = d16 * s;
+            if (!d) continue;
+            const float dm = dmin16 * m;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = lo_nearest_int((x[32 * j + ii] + dm) / d);
+                l = l < 0 ? 0 : l > nmax ? nmax : l;
+                L[32 * j + ii] = (uint8_t)l;
+            }
+        }
+        if (!q5) {
+            unsigned char * q = blk + 16;
+            for (int j = 0; j < 256; j += 64, q += 32)
+                for (int l = 0; l < 32; ++l) q[l] = (unsigned char)(L[j + l] | (L[j + l + 32] << 4));
+        } else {
+            unsigned char * qh = blk + 16;
+            unsigned char * ql = blk + 48;
+            memset(qh, 0, 32);
+            unsigned m1 = 1, m2 = 2;
+            for (int n = 0; n < 256; n += 64, ql += 32, m1 <<= 2, m2 <<= 2) {
+                for (int j = 0; j < 32; ++j) {
+                    int l1 = L[n + j];
+                    if (l1 > 15) {
+                        l1 -= 16;
+                        qh[j] |= (unsigned char)m1;
+                    }
+                    int l2 = L[n + j + 32];
+                    if (l2 > 15) {
+                        l2 -= 16;
+                        qh[j] |= (unsigned char)m2;
+                    }
+                    ql[j] = (unsigned char)(l1 | (l2 << 4));
+                }
+            }
+        }
+    }
+}
+
+void lo_quantize_row_q4_K(const float * x, void * y, int64_t k) { lo_quantize_row_q45_K(0, x, y, k); }
+void lo_quantize_row_q5_K(const float * x, void * y, int64_t k) { lo_quantize_row_q45_K(1, x, y, k); }
+
+/* quantize_row_q6_K_ref: 16-value sub-blocks, make_qx_quants(16, 32, ., 1);
+ * the scale with the largest magnitude (first of equal magnitudes) sets
+ * iscale = -128 / max_scale, d = F16(1 / iscale), 8-bit sub-block scales
+ * min(127, nearest_int(iscale * scale)); values re-coded as
+ * clamp(nearest_int(x / (d * sc)), -32, 31) + 32 (a zero quantized scale
+ * keeps the make_qx_quants codes); a block whose scales are all below 1e-15
+ * is all zero. */
+void lo_quantize_row_q6_K(const float * x, void * out, int64_t k) {
+    unsigned char * y = (unsigned char *)out;
+    for (int64_t i = 0; i < k / 256; ++i, x += 256) {
+        unsigned char * blk = y + i * 210;
+        int8_t L[256];
+        float scales[16];
+        float max_scale = 0, max_abs_scale = 0;
+        for (int ib = 0; ib < 16; ++ib) {
+            const float scale = lo_make_qx_quants(16, 32, x + 16 * ib, L + 16 * ib);
+            scales[ib] = scale;
+            const float abs_scale = fabsf(scale);
+            if (abs_scale > max_abs_scale) {
+                max_abs_scale = abs_scale;
+                max_scale = scale;
+            }
+        }
+        if (max_abs_scale < LO_GROUP_MAX_EPS) {
+            memset(blk, 0, 210);
+            lo_put_h(blk + 208, 0.f);
+            continue;
+        }
+        const float iscale = -128.f / max_scale;
+        lo_put_h(blk + 208, 1 / iscale);
+        int8_t * sc = (int8_t *)(blk + 192);
+        for (int ib = 0; ib < 16; ++ib) {
+            const int v = lo_nearest_int(iscale * scales[ib]);
+            sc[ib] = (int8_t)(v < 127 ? v : 127);
+        }
+        const float d16 = lo_h(blk + 208);
+        for (int j = 0; j < 16; ++j) {
+            const float d = d16 * sc[j];
+            if (!d) continue;
+            for (int ii = 0; ii < 16; ++ii) {
+                int l = lo_nearest_int(x[16 * j + ii] / d);
+                l = l < -32 ? -32 : l > 31 ? 31 : l;
+                L[16 * j + ii] = (int8_t)(l + 32);
+            }
+        }
+        unsigned char * ql = blk;
+        unsigned char * qh = blk + 128;
+        for (int j = 0; j < 256; j += 128, ql += 64, qh += 32) {
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q1 = L[j + l + 0] & 0xF;
+                const uint8_t q2 = L[j + l + 32] & 0xF;
+                const uint8_t q3 = L[j + l + 64] & 0xF;
+                const uint8_t q4 = L[j + l + 96] & 0xF;
+                ql[l + 0] = (unsigned char)(q1 | (q3 << 4));
+                ql[l + 32] = (unsigned char)(q2 | (q4 << 4));
+                qh[l] = (unsigned char)((L[j + l] >> 4) | ((L[j + l + 32] >> 4) << 2) | ((L[j + l + 64] >> 4) << 4) |
+                                        ((L[j + l + 96] >> 4) << 6));
+            }
         }
     }
 }

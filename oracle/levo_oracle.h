@@ -209,6 +209,12 @@ float lo_vec_dot_kquant_q8_K(int type, const void * w, const void * xq, int64_t 
 void lo_mul_mat_kquant(int type, const void * w, const float * x, float * y, int64_t rows, int64_t k,
                        int64_t n_vec);
 
+/* ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, NULL) for
+ * Q8_0, Q4_0 and the K-quant reference quantizers (quantize_row_q{4,5,6}_K_ref,
+ * n_per_row a multiple of 256). */
+void lo_quantize_row_q4_K(const float * x, void * y, int64_t k);
+void lo_quantize_row_q5_K(const float * x, void * y, int64_t k);
+void lo_quantize_row_q6_K(const float * x, void * y, int64_t k);
 size_t lo_quantize_chunk(int type, const float * src, void * dst, int64_t start, int64_t nrows,
                          int64_t n_per_row);
 /* write_tensor's per-chunk path (tools/levo-quantize.cpp:355-388): widen F16

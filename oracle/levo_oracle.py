@@ -205,10 +205,19 @@ class Oracle:
         self.lib.lo_flow_cfg_euler(_ptr(state), _ptr(v_uncond), _ptr(v_cond), state.size, guidance, dt)
 
     # -- quantization (ggml_quantize_chunk at tools/levo-quantize.cpp:386) --------
+    @staticmethod
+    def row_bytes(qtype, cols):
+        """ggml_row_size for the block formats."""
+        if qtype in KQUANT_BLOCK_BYTES:
+            return (cols // 256) * KQUANT_BLOCK_BYTES[qtype]
+        return (cols // 32) * BLOCK_BYTES[qtype]
+
     def quantize(self, qtype, x_f32: np.ndarray) -> np.ndarray:
+        """ggml_quantize_chunk(type, x, ..., NULL): Q8_0, Q4_0 and the Q4_K /
+        Q5_K / Q6_K reference quantizers."""
         x = np.ascontiguousarray(x_f32, dtype=np.float32)
         rows, cols = x.shape
-        out = np.empty(rows * (cols // 32) * BLOCK_BYTES[qtype], dtype=np.uint8)
+        out = np.empty(rows * self.row_bytes(qtype, cols), dtype=np.uint8)
         n = self.lib.lo_quantize_chunk(qtype, _ptr(x), _ptr(out), 0, rows, cols)
         assert n == out.size
         return out
@@ -216,7 +225,7 @@ class Oracle:
     def quantize_f16_padded(self, qtype, x_f16: np.ndarray, dst_cols: int) -> np.ndarray:
         x = np.ascontiguousarray(x_f16, dtype=np.uint16)
         rows, cols = x.shape
-        out = np.empty(rows * (dst_cols // 32) * BLOCK_BYTES[qtype], dtype=np.uint8)
+        out = np.empty(rows * self.row_bytes(qtype, dst_cols), dtype=np.uint8)
         n = self.lib.lo_quantize_f16_rows_padded(qtype, _ptr(x), rows, cols, dst_cols, _ptr(out))
         assert n == out.size
         return out

@@ -193,3 +193,160 @@ def test_mul_mat_kquant_is_vec_dot_per_row(oracle):
             xb = oracle.quantize_q8_K(x[v])
             for r in range(rows):
                 assert y[v, r] == np.float32(oracle.vec_dot_kquant(qtype, w[r * nbytes:(r + 1) * nbytes], xb, k))
+
+
+# --- the reference quantizers (quantize_row_q{4,5,6}_K_ref) -------------------
+# Unpacked here from the published layout (the inverse of the packers above),
+# so the checks do not lean on the oracle's own packing.
+
+def unpack_q45_K(qtype, blk):
+    d = blk[0:2].view(np.float16)[0].astype(np.float64)
+    dmin = blk[2:4].view(np.float16)[0].astype(np.float64)
+    s = blk[4:16].astype(np.int64)
+    sc = np.zeros(8, np.int64)
+    mn = np.zeros(8, np.int64)
+    for j in range(8):
+        if j < 4:
+            sc[j], mn[j] = s[j] & 63, s[j + 4] & 63
+        else:
+            sc[j] = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4)
+            mn[j] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+    codes = np.zeros(256, np.int64)
+    if qtype == Q4_K:
+        qs = blk[16:144].astype(np.int64)
+        for p in range(4):
+            codes[64 * p:64 * p + 32] = qs[32 * p:32 * p + 32] & 15
+            codes[64 * p + 32:64 * p + 64] = qs[32 * p:32 * p + 32] >> 4
+    else:
+        qh = blk[16:48].astype(np.int64)
+        qs = blk[48:176].astype(np.int64)
+        for p in range(4):
+            codes[64 * p:64 * p + 32] = (qs[32 * p:32 * p + 32] & 15) | (((qh >> (2 * p)) & 1) << 4)
+            codes[64 * p + 32:64 * p + 64] = (qs[32 * p:32 * p + 32] >> 4) | (((qh >> (2 * p + 1)) & 1) << 4)
+    return d, dmin, sc, mn, codes
+
+
+def unpack_q6_K(blk):
+    ql = blk[0:128].astype(np.int64)
+    qh = blk[128:192].astype(np.int64)
+    sc = blk[192:208].view(np.int8).astype(np.int64)
+    d = blk[208:210].view(np.float16)[0].astype(np.float64)
+    codes = np.zeros(256, np.int64)
+    for n in range(2):
+        l, h = ql[64 * n:64 * n + 64], qh[32 * n:32 * n + 32]
+        codes[128 * n + 0:128 * n + 32] = (l[0:32] & 15) | ((h & 3) << 4)
+        codes[128 * n + 32:128 * n + 64] = (l[32:64] & 15) | (((h >> 2) & 3) << 4)
+        codes[128 * n + 64:128 * n + 96] = (l[0:32] >> 4) | (((h >> 4) & 3) << 4)
+        codes[128 * n + 96:128 * n + 128] = (l[32:64] >> 4) | (((h >> 6) & 3) << 4)
+    return d, sc, codes - 32
+
+
+BSZ = {Q4_K: 144, Q5_K: 176, Q6_K: 210}
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+def test_quantize_zero_rows(oracle, qtype):
+    """All-zero super-blocks (and -0.0) quantize to all-zero bytes."""
+    x = np.zeros((2, 512), np.float32)
+    x[1] = -0.0
+    assert not oracle.quantize(qtype, x).any()
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K])
+def test_quantize_q45_K_integer_grid(oracle, qtype):
+    """Sub-blocks of integers 0..nmax holding both ends: the search keeps
+    scale 1 and min 0 (the first trial fits exactly), so every sub-block scale
+    is 63, d = F16(1 / 63), dmin = 0 and every code is the value itself."""
+    nmax = 15 if qtype == Q4_K else 31
+    rng = np.random.default_rng(40 + qtype)
+    x = rng.integers(0, nmax + 1, (3, 512)).astype(np.float32)
+    x[:, ::32] = 0
+    x[:, 1::32] = nmax
+    q = oracle.quantize(qtype, x).reshape(-1, BSZ[qtype])
+    for b, blk in enumerate(q):
+        d, dmin, sc, mn, codes = unpack_q45_K(qtype, blk)
+        assert d == np.float64(np.float16(np.float32(1) / np.float32(63)))
+        assert dmin == 0 and np.all(sc == 63) and np.all(mn == 0)
+        assert np.array_equal(codes, x.reshape(-1, 256)[b].astype(np.int64))
+
+
+def test_quantize_q6_K_integer_grid(oracle):
+    """Sub-blocks of integers in [-32, 31] each holding -32: scale 1 in every
+    sub-block, d = -1/128 and sub-block scales -128, so the codes are the
+    values and dequantization is exact."""
+    rng = np.random.default_rng(46)
+    x = rng.integers(-32, 32, (3, 512)).astype(np.float32)
+    x[:, ::16] = -32
+    q = oracle.quantize(Q6_K, x)
+    for b, blk in enumerate(q.reshape(-1, 210)):
+        d, sc, codes = unpack_q6_K(blk)
+        assert d == -1 / 128 and np.all(sc == -128)
+        assert np.array_equal(codes, x.reshape(-1, 256)[b].astype(np.int64))
+    assert np.array_equal(oracle.dequantize_kquant(Q6_K, q, x.size), x.ravel())
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
+def test_quantize_round_trip(oracle, qtype):
+    """Gaussian rows (and all-positive rows, outliers, sub-blocks of very
+    different size): each code is the nearest integer to the value measured
+    in its sub-block's quantized step (t = (x + dmin*m) / (d*sc), Q6_K
+    t = x / (d*sc)), or clamped at an end of the code range with t beyond
+    it; the largest sub-block scale quantizes to 63 (Q6_K: the
+    largest-magnitude scale to -128); the rms error stays under half a code
+    step of the block's range."""
+    rng = np.random.default_rng(50 + qtype)
+    x = (rng.standard_normal((6, 1024)) * 0.05).astype(np.float32)
+    x[1] += 0.3                                  # all-positive sub-blocks (min clamped to 0)
+    x[2, ::97] = 2.0                             # outliers
+    x[3, :256] *= np.repeat(np.geomspace(1e-4, 1.0, 8), 32).astype(np.float32)  # tiny vs large sub-blocks
+    q = oracle.quantize(qtype, x).reshape(-1, BSZ[qtype])
+    deq = oracle.dequantize_kquant(qtype, q.ravel(), x.size).reshape(-1, 256).astype(np.float64)
+    xs = x.reshape(-1, 256).astype(np.float64)
+    nmax = 63 if qtype == Q6_K else (15 if qtype == Q4_K else 31)
+    for b, blk in enumerate(q):
+        if qtype == Q6_K:
+            d, sc, codes = unpack_q6_K(blk)
+            assert sc[np.argmax(np.abs(sc))] == -128
+            step = d * np.repeat(sc, 16)
+            off = np.zeros(256)
+            lo, hi = -32, 31
+        else:
+            d, dmin, sc, mn, codes = unpack_q45_K(qtype, blk)
+            assert sc.max() == 63
+            step = d * np.repeat(sc, 32)
+            off = dmin * np.repeat(mn, 32)
+            lo, hi = 0, nmax
+        ok = step != 0
+        t = (xs[b][ok] + off[ok]) / step[ok]
+        c = codes[ok]
+        tol = 1e-4 * np.maximum(1.0, np.abs(t))
+        inside = (c > lo) & (c < hi)
+        assert np.all(np.abs(t[inside] - c[inside]) <= 0.5 + tol[inside]), b
+        assert np.all(t[c == lo] <= lo + 0.5 + tol[c == lo]), b
+        assert np.all(t[c == hi] >= hi - 0.5 - tol[c == hi]), b
+        err = np.abs(xs[b] - deq[b])
+        rng_b = xs[b].max() - min(xs[b].min(), 0.0)
+        assert np.sqrt(np.mean(err ** 2)) <= 0.5 * rng_b / nmax + 1e-6, b
+
+
+def test_quantize_search_beats_plain_rounding(oracle):
+    """The scale searches are what the K-quants add over plain rounding: on
+    Gaussian data the least-squares refined (scale, min) of make_qkx2_quants
+    and make_qx_quants must beat the plain affine (min..max over nmax steps)
+    and symmetric (max |x| over 31.5 steps) quantizers in rms error, 6-bit /
+    8-bit scale quantization included (measured: 0.91, 0.96, 0.85 of plain;
+    a search that loses its least-squares step lands at or above 1.0)."""
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((64, 1024)) * 0.05).astype(np.float32)
+    for qtype, nmax, bound in ((Q4_K, 15, 0.93), (Q5_K, 31, 0.975)):
+        deq = oracle.dequantize_kquant(qtype, oracle.quantize(qtype, x), x.size).reshape(-1, 32).astype(np.float64)
+        xs = x.reshape(-1, 32).astype(np.float64)
+        mn = np.minimum(xs.min(1), 0)[:, None]
+        step = (xs.max(1)[:, None] - mn) / nmax
+        plain = np.round((xs - mn) / step) * step + mn
+        assert np.sqrt(np.mean((deq - xs) ** 2)) <= bound * np.sqrt(np.mean((plain - xs) ** 2)), qtype
+    deq = oracle.dequantize_kquant(Q6_K, oracle.quantize(Q6_K, x), x.size).reshape(-1, 16).astype(np.float64)
+    xs = x.reshape(-1, 16).astype(np.float64)
+    step = np.abs(xs).max(1)[:, None] / 31.5
+    plain = np.clip(np.round(xs / step), -32, 31) * step
+    assert np.sqrt(np.mean((deq - xs) ** 2)) <= 0.9 * np.sqrt(np.mean((plain - xs) ** 2))
