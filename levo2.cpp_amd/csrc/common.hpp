@@ -34,9 +34,6 @@ int allow_dynamic_lds(const void * kernel, int bytes, const char * what);
 
 inline hipStream_t as_hip(levo_hip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Compute units of the current device (cached per device); 0 if the query fails.
-int device_cu_count();
-
 // K-quant helpers shared by the quantizer entry points (kquant.hip).
 bool is_kquant(levo_hip_type type);
 int64_t kquant_block_bytes(levo_hip_type type);  // Q4_K / Q5_K / Q6_K / Q8_K per 256 values; 0 otherwise
@@ -155,6 +152,25 @@ __device__ __forceinline__ T allreduce(T v, Op op) {
     return op(op(lane(v, 0), lane(v, 16)), op(lane(v, 32), lane(v, 48)));
 }
 }  // namespace dpp
+
+// Sum over each group of LPR consecutive lanes (16, 32 or 64), in every lane
+// of the group: DPP steps within each row of 16, then the row totals.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp::mov<dpp::kQuadXor1>(v);
+    v += dpp::mov<dpp::kQuadXor2>(v);
+    v += dpp::mov<dpp::kRowRor4>(v);
+    v += dpp::mov<dpp::kRowRor8>(v);
+    if constexpr (LPR == 16) {
+        return v;
+    } else if constexpr (LPR == 32) {
+        const float lo = dpp::lane(v, 0) + dpp::lane(v, 16);
+        const float hi = dpp::lane(v, 32) + dpp::lane(v, 48);
+        return (threadIdx.x & 63) < 32 ? lo : hi;
+    } else {
+        return (dpp::lane(v, 0) + dpp::lane(v, 16)) + (dpp::lane(v, 32) + dpp::lane(v, 48));
+    }
+}
 
 __device__ __forceinline__ float wave_sum_f32(float v) {
     return dpp::allreduce(v, [](float a, float b) { return a + b; });

@@ -205,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_kquant_kernel(const uint8
 // ---- mat-vec: one wave per row, 8 lanes per super-block ----------------------
 
 constexpr int kMaxVec = 8;
-constexpr int kStageBatch = 16;  // activation dwords a thread requests at once
+constexpr int kXVec = 6;  // activation dwordx4 a thread requests up front (24 KiB per workgroup)
 
 struct kq_params {
     const uint8_t * w;      // [rows][nb] blocks, 16-byte aligned
@@ -370,37 +370,56 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
     const int nrows = left < kRowsPerWave ? (left > 0 ? static_cast<int>(left) : 0) : kRowsPerWave;
     const int64_t sb0 = row0 * p.row_bytes;
     const int64_t sb1 = sb0 + nrows * p.row_bytes;
-    u32x4 regs[CH];
-    if (nrows > 0) load_span<CH>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, lane, regs);
-    // 2. the activation blocks are dwords 0 .. 73 nblk of x (73 per 292-byte
-    //    block); kStageBatch of a thread's dwords are requested together
+    // The activation blocks (dwords 0 .. 73 nblk of x, 73 per 292-byte block)
+    // are requested first, as dwordx4 with no branch around them (surplus
+    // requests re-read the first chunk; the chunk crossing the end of x, if
+    // any, reads the one before and is re-read below as dwords): loads
+    // complete in issue order, so they are staged while the weights are in
+    // flight.
     const int ndw = p.n_vec * nb * 73;
+    const int nx4 = (ndw + 3) / 4;
+    const int64_t xbytes = 4 * static_cast<int64_t>(ndw);
     const uint32_t * xw = reinterpret_cast<const uint32_t *>(p.x);
-    for (int e0 = tid; e0 < ndw; e0 += kThreads * kStageBatch) {
-        uint32_t v[kStageBatch];
+    u32x4 xr[kXVec];
 #pragma unroll
-        for (int j = 0; j < kStageBatch; ++j) {
-            const int e = e0 + kThreads * j;
-            v[j] = e < ndw ? xw[e] : 0u;
-        }
-#pragma unroll
-        for (int j = 0; j < kStageBatch; ++j) {
-            const int e = e0 + kThreads * j;
-            if (e < ndw) {
-                const int b = e / 73, wd = e - b * 73;
-                if (wd == 0) {
-                    xd[b] = __builtin_bit_cast(float, v[j]);
-                } else if (wd <= 64) {
-                    reinterpret_cast<uint32_t *>(xq)[b * 64 + wd - 1] = v[j];
-                } else {
-                    reinterpret_cast<uint32_t *>(xs)[b * 8 + wd - 65] = v[j];
-                }
-            }
-        }
+    for (int j = 0; j < kXVec; ++j) {
+        const int c = tid + kThreads * j;
+        const int64_t at = 16 * static_cast<int64_t>(c);
+        const int64_t from = c >= nx4 ? 0 : at + 16 <= xbytes ? at : at - 16;
+        xr[j] = *reinterpret_cast<const u32x4 *>(p.x + from);
     }
-    __syncthreads();
+    u32x4 regs[CH];
+    load_span<CH>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
+    // 2. the activations re-laid out in LDS so that each lane's quants are
+    //    aligned: xq [n_vec][256 nb] int8, xd [n_vec][nb] float, xs [n_vec][16 nb]
+    //    int16 (the bsums)
+    const auto place = [&](int e, uint32_t v) {
+        const int b = e / 73, wd = e - b * 73;
+        if (wd == 0) xd[b] = __builtin_bit_cast(float, v);
+        else if (wd <= 64) reinterpret_cast<uint32_t *>(xq)[b * 64 + wd - 1] = v;
+        else reinterpret_cast<uint32_t *>(xs)[b * 8 + wd - 65] = v;
+    };
+#pragma unroll
+    for (int j = 0; j < kXVec; ++j) {
+        const int c = tid + kThreads * j;
+        if (c >= nx4) continue;
+        u32x4 v = xr[j];
+        if (16 * static_cast<int64_t>(c) + 16 > xbytes) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = 4 * c + q < ndw ? xw[4 * c + q] : 0u;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (4 * c + q < ndw) place(4 * c + q, v[q]);
+    }
+    for (int e = 4 * (tid + kThreads * kXVec); e < ndw; e += 4 * kThreads) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (e + q < ndw) place(e + q, xw[e + q]);
+    }
+    lds_barrier();  // LDS only: the weight loads stay in flight
     // 3. parse and sum
-    if (nrows > 0) store_span<CH>(stage, sb0 & ~int64_t{15}, sb1, lane, regs);
+    store_span<CH>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
     wave_lds_fence();
     const int g = lane / LPR;
     const int li = lane % LPR;
@@ -426,12 +445,8 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
 #pragma unroll
     for (int v = 0; v < kMaxVec; ++v) {
         if (v < p.n_vec) {
-            float sd = acc_d[v], sm = acc_m[v];
-#pragma unroll
-            for (int o = LPR / 2; o > 0; o >>= 1) {
-                sd += __shfl_xor(sd, o, 64);
-                if constexpr (TYPE != LEVO_HIP_TYPE_Q6_K) sm += __shfl_xor(sm, o, 64);
-            }
+            const float sd = group_sum<LPR>(acc_d[v]);
+            const float sm = TYPE != LEVO_HIP_TYPE_Q6_K ? group_sum<LPR>(acc_m[v]) : 0.0f;
             if (live && li == 0) p.y[v * p.y_pitch + row0 + g] = sd - sm;
         }
     }

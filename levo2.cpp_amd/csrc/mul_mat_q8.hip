@@ -37,6 +37,7 @@ constexpr int kQ8Bytes = 34;
 constexpr int kSpanBlocks = 256;
 constexpr int kChunksPerLane = (kSpanBlocks * kQ8Bytes + 15 + 15) / 16 / 64 + 1;
 constexpr int kMaxVectors = 8;
+constexpr int kXChunks = 5;  // activation chunks per thread loaded up front (20 KiB per workgroup)
 constexpr int kMaxBlocksPerRow = 1024;
 
 struct mm_params {
@@ -64,6 +65,17 @@ __device__ __forceinline__ float read_block(const uint8_t * stage, int off, uint
 #pragma unroll
     for (int i = 0; i < 8; ++i) q[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], shift);
     return h2f(*reinterpret_cast<const uint16_t *>(stage + off));
+}
+
+// 16-byte chunk c of the activation blocks (xbytes long); the last, partial
+// chunk is read as half-words so nothing past the buffer is touched.
+__device__ __forceinline__ u32x4 load_x_chunk(const uint8_t * x, int64_t xbytes, int c) {
+    const int64_t at = 16 * static_cast<int64_t>(c);
+    if (at + 16 <= xbytes) return *reinterpret_cast<const u32x4 *>(x + at);
+    uint32_t h[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) h[k] = at + 2 * k + 2 <= xbytes ? *reinterpret_cast<const uint16_t *>(x + at + 2 * k) : 0u;
+    return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
 }
 
 // Rows and blocks of wave `wave` in workgroup `grp`: WPR waves share a row
@@ -102,36 +114,39 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
     const int wave = threadIdx.x >> 6;
     uint8_t * stage = stages + wave * p.stage_bytes;
 
-    // 1. this wave's weight loads
+    // 1. the activation blocks' first chunks, then this wave's weight loads:
+    //    loads complete in issue order, so the activations (a few KiB, from
+    //    L2) are unpacked while the weights are still in flight
+    const int64_t xbytes = static_cast<int64_t>(nvb) * kQ8Bytes;
+    const int nchunks = static_cast<int>((xbytes + 15) >> 4);
+    u32x4 xr[kXChunks];  // unconditional (see load_span): chunks past the end re-read chunk 0
+#pragma unroll
+    for (int i = 0; i < kXChunks; ++i) {
+        const int c = static_cast<int>(threadIdx.x) + kThreads * i;
+        const bool whole = c < nchunks && 16 * static_cast<int64_t>(c) + 16 <= xbytes;
+        xr[i] = *reinterpret_cast<const u32x4 *>(p.x + (whole ? 16 * static_cast<int64_t>(c) : 0));
+    }
     int64_t row0;
     int nrows, kb0, kb1;
     const bool have = wave_span<LPR, WPR>(p, blockIdx.x, wave, row0, nrows, kb0, kb1);
     u32x4 regs[kChunksPerLane];
     const int64_t sb0 = (row0 * p.nb + kb0) * kQ8Bytes;
     const int64_t sb1 = (row0 * p.nb + (WPR > 1 ? kb1 : static_cast<int64_t>(nrows) * p.nb)) * kQ8Bytes;
-    if (have) load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, lane, regs);
+    load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
 
     // 2. activation blocks -> LDS (raw, through the stage area), then
     //    unpacked to aligned quant dwords and F32 scales
     {
-        const int64_t xbytes = static_cast<int64_t>(nvb) * kQ8Bytes;
-        const int nchunks = static_cast<int>((xbytes + 15) >> 4);
-        for (int c = threadIdx.x; c < nchunks; c += kThreads) {
-            const int64_t at = 16 * static_cast<int64_t>(c);
-            u32x4 v;
-            if (at + 16 <= xbytes) {
-                v = *reinterpret_cast<const u32x4 *>(p.x + at);
-            } else {
-                uint32_t h[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    h[k] = at + 2 * k + 2 <= xbytes ? *reinterpret_cast<const uint16_t *>(p.x + at + 2 * k) : 0u;
-                }
-                v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-            }
-            reinterpret_cast<u32x4 *>(stages)[c] = v;
+        for (int i = 0; i < kXChunks; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + kThreads * i;
+            if (c >= nchunks) continue;
+            reinterpret_cast<u32x4 *>(stages)[c] = 16 * static_cast<int64_t>(c) + 16 <= xbytes ? xr[i]
+                                                                                             : load_x_chunk(p.x, xbytes, c);
         }
-        __syncthreads();
+        for (int c = threadIdx.x + kThreads * kXChunks; c < nchunks; c += kThreads)
+            reinterpret_cast<u32x4 *>(stages)[c] = load_x_chunk(p.x, xbytes, c);
+        lds_barrier();  // LDS only: the weight loads stay in flight
         for (int t = threadIdx.x; t < nvb; t += kThreads) {
             uint32_t q[8];
             dx[t] = read_block(stages, t * kQ8Bytes, q);
@@ -139,14 +154,14 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
             dst[0] = u32x4{q[0], q[1], q[2], q[3]};
             dst[1] = u32x4{q[4], q[5], q[6], q[7]};
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // 3. the wave's blocks: lane li of row group g takes kb = kb0 + li + LPR * i
     const int g = lane / LPR;
     const int li = lane % LPR;
     const int lead = static_cast<int>(sb0 & 15);
-    if (have) store_span<kChunksPerLane>(stage, sb0 & ~int64_t{15}, sb1, lane, regs);
+    store_span<kChunksPerLane>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
     wave_lds_fence();
     float acc[kMaxVectors];
 #pragma unroll
@@ -178,8 +193,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
 #pragma unroll
     for (int v = 0; v < kMaxVectors; ++v) {
         if (v >= p.n_vec) break;
-#pragma unroll
-        for (int o = LPR / 2; o > 0; o >>= 1) acc[v] += __shfl_xor(acc[v], o, 64);
+        acc[v] = group_sum<LPR>(acc[v]);
     }
     if constexpr (WPR > 1) {
         // the row's parts meet in LDS, summed in wave order
@@ -204,8 +218,13 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
 }
 
 template <int LPR, int WPR>
+constexpr int rows_per_workgroup() {
+    return WPR > 1 ? kWaves / WPR : kWaves * (64 / LPR);
+}
+
+template <int LPR, int WPR>
 int launch_mm(mm_params p, hipStream_t st) {
-    constexpr int rows_per_block = WPR > 1 ? kWaves / WPR : kWaves * (64 / LPR);
+    constexpr int rows_per_block = rows_per_workgroup<LPR, WPR>();
     const int span_blocks = WPR > 1 ? (p.nb + WPR - 1) / WPR : (64 / LPR) * p.nb;
     p.stage_bytes = (span_blocks * kQ8Bytes + 32 + 15) & ~15;
     const int64_t nvb = static_cast<int64_t>(p.n_vec) * p.nb;
@@ -247,6 +266,9 @@ extern "C" int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks,
     p.n_vec = static_cast<int32_t>(n_vec);
     p.stage_bytes = 0;
     const hipStream_t st = as_hip(stream);
+    // The fewest lanes per row that hold the row's blocks in one wave's span
+    // (more workgroups with fewer rows each measured slower at 1536 rows:
+    // each repeats the activation staging).
     if (p.nb <= 64) return launch_mm<16, 1>(p, st);
     if (p.nb <= 128) return launch_mm<32, 1>(p, st);
     if (p.nb <= 256) return launch_mm<64, 1>(p, st);

@@ -46,21 +46,6 @@ int allow_dynamic_lds(const void * kernel, int bytes, const char * what) {
     return LEVO_HIP_OK;
 }
 
-int device_cu_count() {
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess || device < 0) return 0;
-    constexpr int kMaxDevices = 64;
-    static std::atomic<int> cached[kMaxDevices];
-    if (device < kMaxDevices) {
-        const int c = cached[device].load(std::memory_order_relaxed);
-        if (c > 0) return c;
-    }
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) return 0;
-    if (device < kMaxDevices) cached[device].store(cus, std::memory_order_relaxed);
-    return cus;
-}
-
 int launch_status(const char * what) {
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) {
