@@ -1044,6 +1044,76 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     print(json.dumps({"traffic_probe_launch_order": order}))
 
 
+def run_host_dropins():
+    """The C++ drop-ins that keep the reference's host-vector signatures
+    (levo2.cpp_amd/bench/host_dropins.cpp: Sampler::sample_streams on host
+    logits, flow::solve_flow_euler with a host velocity callback, a host F32
+    chunk quantized to Q8_0), timed wall-clock with their PCIe transfers. Run
+    as a child process before this one touches the GPU."""
+    exe = os.path.join(ROOT, "levo2.cpp_amd", "bench", "host_dropins")
+    if not os.path.exists(exe):
+        return {"error": f"{exe} is not built"}
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": f"host_dropins rc={r.returncode}: {r.stderr[-400:]}"}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def host_dropin_references(gpu):
+    """The reference side of the host drop-ins on one host core: the
+    reference's own Sampler::sample_streams (oracle/_ref), the oracle port of
+    solve_flow_euler's loop (src/levo-flow-renderer.cpp:57-120: in-context
+    rows, callback, require_finite, Euler update, require_finite) with the
+    same fixed-velocity callback, and the oracle port of ggml_quantize_chunk
+    to Q8_0 on the same [4096, 1536] F32 chunk (3 warm-ups, median of 10)."""
+    from oracle.levo_oracle import Oracle, Reference, have_reference
+    orc = Oracle()
+    out = {}
+    with pinned(1):
+        if have_reference():
+            ref = Reference()
+            V = 16385
+            streams = (orc.gaussian(3 * V, 10) * 3).reshape(3, V)
+            recent = (np.arange(150, dtype=np.int64) * 97 % (V - 1)).reshape(3, 50)
+            s2 = ref.sampler(2)
+            t = median_seconds(lambda: s2.sample_streams(streams, use_sampling=True, temperature=0.9, top_k_mixed=50,
+                                                         top_k_detail=1, repetition_penalty=1.1, recent=recent,
+                                                         ignore=(0, 1, 2)))
+            out["sample_streams_3x16385"] = {"gpu_dropin_us": gpu.get("sample_streams_3x16385_us"),
+                                             "reference_cpu_us": round(t * 1e6, 1), "kind": "reference"}
+        F, L, P, steps = 1000, 64, 250, 50
+        noise, ctx, vel = orc.gaussian(F * L, 20), orc.gaussian(F * L, 21), orc.gaussian(F * L, 22) * 0.1
+
+        def solve():
+            state = noise.copy()
+            dt = np.float32(1.0) / np.float32(steps)
+            for step in range(steps):
+                t_ = np.float32(step) * dt
+                orc.flow_incontext(state, noise, ctx, P * L, t_, 1e-4)
+                v = vel  # the callback's fixed velocity
+                if not np.isfinite(v).all():
+                    raise ValueError
+                orc.flow_cfg_euler(state, v, v, 1.0, dt)
+                if not np.isfinite(state).all():
+                    raise ValueError
+            state[:P * L] = ctx[:P * L]
+            return state
+
+        t = median_seconds(solve)
+        out["solve_flow_euler_1000x64_50_steps"] = {"gpu_dropin_us": gpu.get("solve_flow_euler_1000x64_50_steps_us"),
+                                                    "reference_cpu_us": round(t * 1e6, 1), "kind": "port"}
+        x = (orc.gaussian(4096 * 1536, 30) * 0.02).reshape(4096, 1536)
+        t = median_seconds(lambda: orc.quantize(8, x))
+        out["quantize_chunk_q8_0_4096x1536"] = {"gpu_dropin_us": gpu.get("quantize_chunk_q8_0_4096x1536_host_us"),
+                                                "reference_cpu_us": round(t * 1e6, 1), "kind": "port"}
+    for e in out.values():
+        if e.get("gpu_dropin_us"):
+            e["speedup"] = round(e["reference_cpu_us"] / e["gpu_dropin_us"], 2)
+    out["note"] = ("wall-clock per call, host buffers in and out (PCIe transfers included); reference side on one "
+                   "pinned host core")
+    return out
+
+
 OP_GROUPS = ("snake", "flow", "norm", "sample", "quant", "gemv", "conv", "vae")
 
 
@@ -1109,6 +1179,7 @@ def main() -> int:
                          "(every op shards without exchange; see the sharding notes). Run with --gpus 1.\n")
         return 2
 
+    host_dropins = None if (args.no_ops or args.only or args.traffic_probe) else run_host_dropins()
     import torch
     if not torch.cuda.is_available():
         sys.stderr.write("bench.py needs a GPU\n")
@@ -1155,6 +1226,9 @@ def main() -> int:
                                                             1)}}
     if not args.no_ops:
         ops.update(run_ops(torch, hip, binding, head, dev, args, OP_GROUPS))
+        log("ops: host-vector drop-ins (reference side)")
+        ops["host_dropins"] = (host_dropin_references(host_dropins) if "error" not in host_dropins
+                               else host_dropins)
         log("ops: streaming ceilings")
         add_ceilings(torch, head, dev, ops, args.warmup, args.steps)
 

@@ -3,6 +3,7 @@
   levo2.cpp_amd/liblevo_hip.so       C ABI (include/levo_hip.h) + HIP kernels
   levo2.cpp_amd/liblevo_hip_host.so  C++17 drop-in wrappers (levo2.cpp_amd/host/)
   levo2.cpp_amd/liblevo_bench_stream.so  plain streaming kernels bench.py compares the ops with
+  levo2.cpp_amd/bench/host_dropins       bench.py's timing of the host-vector C++ drop-ins
 
 Kernels are compiled with hipcc for gfx950 only; the host wrappers contain no
 device code and are plain C++17 (g++) against the HIP runtime API. Every source is recompiled on
@@ -26,6 +27,7 @@ BUILD = os.path.join(PKG, "_build")
 KERNEL_LIB = os.path.join(PKG, "liblevo_hip.so")
 HOST_LIB = os.path.join(PKG, "liblevo_hip_host.so")
 BENCH_LIB = os.path.join(PKG, "liblevo_bench_stream.so")  # measurement kernels of bench.py, not the C ABI
+BENCH_HOST = os.path.join(PKG, "bench", "host_dropins")    # bench.py's host drop-in timings
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
@@ -98,6 +100,11 @@ def build(verbose: bool = False) -> None:
     if bobjs:
         _run([HIPCC, *DEVICE, "-shared", "-fPIC", "-o", BENCH_LIB + ".tmp", *bobjs])
         os.replace(BENCH_LIB + ".tmp", BENCH_LIB)
+    host_bench = os.path.join(PKG, "bench", "host_dropins.cpp")
+    if hobjs and os.path.exists(host_bench):
+        _run([CXX, *HOST_FLAGS, "-o", BENCH_HOST + ".tmp", host_bench, "-L", PKG, "-llevo_hip_host", "-llevo_hip",
+              "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath,$ORIGIN/.."])
+        os.replace(BENCH_HOST + ".tmp", BENCH_HOST)
     if verbose:
         print("built", KERNEL_LIB, HOST_LIB if hobjs else "")
 
