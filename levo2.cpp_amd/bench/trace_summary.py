@@ -8,6 +8,19 @@ start) and HIP's copies are left out.
 
     python3 levo2.cpp_amd/bench/trace_summary.py <kernel_trace.csv> > table.md
 
+With --vae, the HBM bytes of each of the 31 launches of the last VAE decode
+in two rocprofv3 --pmc runs of `bench.py --only vae` (FETCH_SIZE, then
+WRITE_SIZE), scaled by the copy factors in traffic.json, beside the bytes of
+the launch's activations (inputs and outputs once) and weights:
+
+    python3 levo2.cpp_amd/bench/trace_summary.py --vae <fetch_counter_collection.csv>
+        <write_counter_collection.csv> profiles/traffic.json <frames> > table.md
+
+With --vae-trace, each launch of the last decode of each window size in a
+kernel trace of `bench.py --only vae`, with its duration and TFLOP/s:
+
+    python3 levo2.cpp_amd/bench/trace_summary.py --vae-trace <kernel_trace.csv> > table.md
+
 With --traffic, the HBM bytes per launch of bench.py --traffic-probe from two
 rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
 scaled by what the counter reads for the probe's first launch, a plain
@@ -92,8 +105,105 @@ def traffic(fetch_csv: str, write_csv: str, probe_log: str, json_out: str) -> li
     return rows
 
 
+def vae_flops(frames: int) -> list[float]:
+    """2 * C_out * C_in * taps * T_out of each of the 31 launches (both convs
+    of a one-launch residual unit; a transposed-conv output sample takes 2
+    taps per input channel)."""
+    out = [2.0 * 2048 * 64 * 7 * frames]
+    t = frames
+    for ci, co, st in zip((2048, 1024, 512, 256, 128), (1024, 512, 256, 128, 128), (10, 6, 4, 4, 2)):
+        t *= st
+        out.append(2.0 * co * ci * 2 * t)
+        for _ in range(3):
+            k7, k1 = 2.0 * co * co * 7 * t, 2.0 * co * co * t
+            out += [k7, k1] if co > 128 else [k7 + k1]
+    return out + [2.0 * 2 * 128 * 7 * t]
+
+
+def vae_trace(path: str) -> list[str]:
+    launches = []
+    for r in csv.DictReader(open(path)):
+        n = short_name(r["Kernel_Name"])
+        if n is None or "pack_transpose" in n or "stream_kernel" in n:
+            continue
+        wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        launches.append((int(r["Start_Timestamp"]), n, grid // max(wg, 1),
+                         int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    launches.sort()
+    per = len(vae_launches(1))
+    decodes = [launches[i:i + per] for i in range(0, len(launches) - per + 1, per)]
+    rows = []
+    for frames in (252, 1000):
+        # the input conv's grid tells the window size: ceil(frames / 128) time tiles x 16 channel tiles
+        mine = [d for d in decodes if d[0][2] == -(-frames // 128) * 16]
+        if not mine:
+            continue
+        d = mine[-1]
+        labels = [lab for lab, _, _ in vae_launches(frames)]
+        flops = vae_flops(frames)
+        rows += [f"#### {frames} frames ({frames * 1920 / 48000:.2f} s of audio)", "",
+                 "| launch | kernel | grid (WGs) | µs | TFLOP/s |", "|---|---|---:|---:|---:|"]
+        for lab, (_, n, wgs, ns), fl in zip(labels, d, flops):
+            rows.append(f"| {lab} | `{n}` | {wgs} | {ns / 1e3:.1f} | {fl / ns / 1e3:.1f} |")
+        tot = sum(x[3] for x in d)
+        rows += [f"| **total** | | | **{tot / 1e3:.1f}** | **{sum(flops) / tot / 1e3:.1f}** |", ""]
+    return rows
+
+
+def vae_launches(frames: int) -> list[tuple[str, int, int]]:
+    """(label, activation bytes, weight bytes) of the decoder's 31 launches in
+    order: the input conv; per stage the SnakeBeta + upsampler, then three
+    residual units (two launches at 256-1024 channels, k = 7 then k = 1 with
+    the residual add; one at 128); the SnakeBeta + output conv."""
+    f4 = 4
+    out = [("input conv 64->2048 k7", (64 + 2048) * frames * f4, (2048 * 64 * 7 + 2048) * f4)]
+    t = frames
+    for s, (ci, co, st) in enumerate(zip((2048, 1024, 512, 256, 128), (1024, 512, 256, 128, 128),
+                                         (10, 6, 4, 4, 2))):
+        t_in, t = t, t * st
+        out.append((f"stage {s + 1} snake+upsample {ci}->{co} x{st}", (ci * t_in + co * t) * f4,
+                    (ci * co * 2 * st + co + 2 * ci) * f4))
+        for d in (1, 3, 9):
+            if co > 128:
+                out.append((f"stage {s + 1} snake+conv k7 d{d} {co}", 2 * co * t * f4, (co * co * 7 + 3 * co) * f4))
+                out.append((f"stage {s + 1} snake+conv k1 +res {co}", 3 * co * t * f4, (co * co + 3 * co) * f4))
+            else:
+                out.append((f"stage {s + 1} residual unit d{d} {co} (one launch)", 2 * co * t * f4,
+                            (co * co * 8 + 6 * co) * f4))
+    out.append(("snake+output conv 128->2 k7", (128 + 2) * t * f4, (2 * 128 * 7 + 2 * 128) * f4))
+    return out
+
+
+def vae_traffic(fetch_csv: str, write_csv: str, traffic_json: str, frames: str) -> list[str]:
+    scales = json.load(open(traffic_json))
+    labels = vae_launches(int(frames))
+    lib = lambda rows: [r for r in rows if "levo_hip::" in r[1]][-len(labels):]  # HIP's copies left out
+    fe = lib(counters(fetch_csv, "FETCH_SIZE"))
+    wr = lib(counters(write_csv, "WRITE_SIZE"))
+    rows = [f"FETCH_SIZE x {scales['fetch_scale']:.4f}, WRITE_SIZE x {scales['write_scale']:.4f} (the copy factors "
+            f"of traffic.json); the last {len(labels)} launches of each run, the {frames}-frame decode.", "",
+            "| launch | activations (MB) | weights (MB) | FETCH (MB) | WRITE (MB) | HBM ÷ (activations + weights) |",
+            "|---|---:|---:|---:|---:|---:|"]
+    tot = [0.0] * 4
+    for (label, act, wts), (_, _, f), (_, _, w) in zip(labels, fe, wr):
+        fb = f * 1024 * scales["fetch_scale"]
+        wb = w * 1024 * scales["write_scale"]
+        for i, v in enumerate((act, wts, fb, wb)):
+            tot[i] += v
+        rows.append(f"| {label} | {act / 1e6:.1f} | {wts / 1e6:.1f} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | "
+                    f"{(fb + wb) / (act + wts):.2f} |")
+    rows.append(f"| **total** | **{tot[0] / 1e6:.0f}** | **{tot[1] / 1e6:.0f}** | **{tot[2] / 1e6:.0f}** | "
+                f"**{tot[3] / 1e6:.0f}** | **{(tot[2] + tot[3]) / (tot[0] + tot[1]):.2f}** |")
+    return rows
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "--traffic":
         print("\n".join(traffic(*sys.argv[2:6])))
+    elif sys.argv[1] == "--vae-trace":
+        print("\n".join(vae_trace(sys.argv[2])))
+    elif sys.argv[1] == "--vae":
+        print("\n".join(vae_traffic(*sys.argv[2:6])))
     else:
         print("\n".join(summarize(sys.argv[1])))

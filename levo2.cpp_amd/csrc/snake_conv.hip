@@ -78,19 +78,27 @@ struct conv_params {
     int32_t param_ring;
     int32_t b_magic;          // ceil(2^24 / b_width): row of a flat B index by multiply
     // Workgroup order: 0 = grid (time tiles, channel tiles, phases); 1 = a 1-D
-    // grid in which the phases of one tile run back to back on one XCD
+    // grid that gives each XCD a run of consecutive tiles, every phase of a
+    // tile back to back
     int32_t xcd_order;
     int32_t tiles_x, tiles, phases;
 };
 
 // The time tile x, channel tile y and phase z of this workgroup. With
-// xcd_order the grid is 1-D, ordered (tile group, phase, tile % 8): the
-// hardware deals workgroups to the 8 XCDs round-robin by linear id, so every
-// phase of a tile runs on the same XCD, right after the others. The phases of
-// a transposed convolution write interleaved samples of the same output
-// lines, which then meet in that XCD's L2 instead of going back to memory as
-// partial lines. Workgroups past the last tile (the padding of the final
-// group of 8) are not live.
+// xcd_order the grid is 1-D: the hardware deals workgroups to the 8 XCDs
+// round-robin by linear id, and XCD j takes the j-th run of ceil(tiles / 8)
+// consecutive tiles (tile = y * tiles_x + x, so a run is one channel tile's
+// time tiles, or a part of them), each tile's phases back to back.
+// - Every phase of a tile runs on one XCD, right after the others. The
+//   phases of a transposed convolution write interleaved samples of the same
+//   output lines, which then meet in that XCD's L2 instead of going back to
+//   memory as partial lines; their shared input tile is read from there too.
+// - A channel tile's weights (every phase's) are read by the XCDs its run
+//   covers, one or two, and by the others not at all, where the deal of
+//   consecutive tiles to the 8 XCDs had every XCD read all of them; and the
+//   k = 7 halo of a time tile is mostly read by the XCD that read its
+//   neighbours' inputs.
+// Workgroups past the last tile (the short last run) are not live.
 struct tile_id {
     int x, y, z;
     bool live;
@@ -99,9 +107,10 @@ struct tile_id {
 __device__ __forceinline__ tile_id conv_tile(const conv_params & p) {
     if (!p.xcd_order) return {static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), static_cast<int>(blockIdx.z), true};
     const int lin = static_cast<int>(blockIdx.x);
-    const int rest = lin >> 3;
-    const int tile = (rest / p.phases) * 8 + (lin & 7);
-    return {tile % p.tiles_x, tile / p.tiles_x, rest % p.phases, tile < p.tiles};
+    const int k = lin >> 3;              // this workgroup's place in its XCD's run
+    const int run = (p.tiles + 7) >> 3;  // tiles per XCD
+    const int tile = (lin & 7) * run + k / p.phases;
+    return {tile % p.tiles_x, tile / p.tiles_x, k % p.phases, tile < p.tiles};
 }
 
 // The k = 1 half of a residual unit (src/levo-vae.cpp:96-100) fused into the
@@ -886,12 +895,11 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     }
 }
 
-// The launch grid; transposed convolutions (more than one phase) take the
-// XCD-ordered 1-D grid.
+// The launch grid: the XCD-ordered 1-D grid for more than 8 workgroups.
 inline dim3 conv_grid(conv_params & p, int phases) {
     const int64_t tx = ceil_div(p.t_out, kNT);
     const int64_t ty = ceil_div(p.c_out, kMT);
-    p.xcd_order = p.scatter && phases > 1 && ceil_div(tx * ty, 8) * 8 * phases < INT32_MAX;
+    p.xcd_order = tx * ty * phases > 8 && ceil_div(tx * ty, 8) * 8 * phases < INT32_MAX;
     p.tiles_x = static_cast<int32_t>(tx);
     p.tiles = static_cast<int32_t>(tx * ty);
     p.phases = phases;
