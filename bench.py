@@ -498,9 +498,11 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     """Sampling of one LeLM decode step on the device: 1 position x 3 streams
     x 16385 ids, CFG s = 1.5, penalty window 50, a 3-id ignore list, top-k
     50/1/1, T = 0.9; levo_hip_cfg_sample + levo_hip_sample_draw. Latency-bound
-    (393 KB per step). `device_us`: both launches back to back; `roundtrip_us`:
-    median wall time from the first launch until the 3 ids and draw counts
-    are in pinned host memory (Python launch overhead included)."""
+    (393 KB per step). `device_us`: both launches back to back;
+    `sample_step_us`: the same step through levo_hip_sample_step (rows split
+    into 4096-id segment workgroups, then one merge-and-draw workgroup);
+    `roundtrip_us`: median wall time from the first launch until the 3 ids and
+    draw counts are in pinned host memory (Python launch overhead included)."""
     S, V, cap = 3, 16385, 64
     n = 64
     g = torch.Generator(device=dev)
@@ -540,6 +542,10 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
 
     device_ms = time_op(torch, head, step, n, warmup, max(steps, 200))
     sample_ms = time_op(torch, head, lambda i: hip.cfg_sample(sargs[i]), n, warmup, max(steps, 200))
+    # the same step through levo_hip_sample_step (segment launch + merge-and-draw launch)
+    ws_bytes = hip.sample_step_workspace_bytes(S, V)
+    ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=dev)
+    split_ms = time_op(torch, head, lambda i: hip.sample_step(sargs[i], d, ws, ws_bytes), n, warmup, max(steps, 200))
     h_tok = torch.empty(S, dtype=torch.int64, pin_memory=True)
     h_draws = torch.empty(S, dtype=torch.int32, pin_memory=True)
     stream = torch.cuda.current_stream()
@@ -557,6 +563,7 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     return op_entry(per, device_ms, shape=[1, 2, S, V], dtype="f32 logits / f64 weights", top_k=[50, 1, 1],
                     temperature=0.9, cfg_sample_us=round(sample_ms * 1e3, 3),
                     sample_draw_us=round((device_ms - sample_ms) * 1e3, 3),
+                    sample_step_us=round(split_ms * 1e3, 3),
                     roundtrip_us=round(roundtrip_ms * 1e3, 2), bytes_to_host=S * (8 + 4),
                     bound="latency")
 

@@ -346,18 +346,18 @@ int levo_hip_sample_draw(const levo_hip_draw_args * args, levo_hip_stream_t stre
  * logits; < 0 if invalid. */
 int64_t levo_hip_sample_step_workspace_bytes(int64_t rows, int64_t vocab);
 
-/* One decode step of Sampler::sample_streams (src/levo-sampling.cpp:129-152)
- * in a single launch: levo_hip_cfg_sample's outputs for every row (CFG,
- * penalty, ignore list, first maximum, top-k candidates of
- * sample_top_k_counted :75-116), then, when `draw` is not NULL, the tokens
- * and draw counts of levo_hip_sample_draw (:97-115). The results equal those
- * two calls'. Each row is split over several workgroups (2048 ids each) whose
- * partial results meet in `workspace`; it is made for the few rows of a
- * decode step (rows <= 4095). workspace: 16-byte aligned device memory of
- * levo_hip_sample_step_workspace_bytes(rows, vocab) bytes whose first
- * 16384 bytes (the row counters) are zero before the first call; every call
- * leaves them zero, so one workspace serves calls of any shape. Calls that
- * share a workspace must not overlap. `draw`
+/* One decode step of Sampler::sample_streams (src/levo-sampling.cpp:129-152):
+ * levo_hip_cfg_sample's outputs for every row (CFG, penalty, ignore list,
+ * first maximum, top-k candidates of sample_top_k_counted :75-116), then,
+ * when `draw` is not NULL, the tokens and draw counts of levo_hip_sample_draw
+ * (:97-115). The results equal those two calls'. Each row is split over
+ * workgroups of 4096 ids that hand their own top-k sets to `workspace`; a
+ * second launch merges them and, with at most 8 rows, draws (more rows take a
+ * third launch for the draw). It is made for the few rows of a decode step
+ * (rows <= 4095). workspace: 16-byte aligned device memory of
+ * levo_hip_sample_step_workspace_bytes(rows, vocab) bytes, whose contents
+ * need no initialization; one workspace serves calls of any shape. Calls
+ * that share a workspace must not overlap. `draw`
  * reads the rows' own outputs: its best, count, cand_ids, cand_logits,
  * row_max, rows and capacity must be those of `args`. */
 int levo_hip_sample_step(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,

@@ -56,6 +56,20 @@ constexpr int kSegCap = 256;   // gathered candidates per wave segment
 constexpr int kBisCap = 256;   // candidates the one-wave bisection holds (4 per lane)
 constexpr int kMaxVocab = 32768;
 
+// The penalty and ignore lists enter a row's bitmaps through one entry per
+// thread: entry i < n_pen of the row's recent ids, then entry i - n_pen of the
+// ignore list. The first kThreads entries are requested before the row's
+// logits, so the two memory round trips overlap; the load takes no branch (a
+// lane without an entry reads kNoListEntry), which keeps the compiler from
+// waiting for it before the row's loads are issued.
+__device__ const int64_t kNoListEntry = -1;
+
+__device__ __forceinline__ int64_t list_entry(const int64_t * rec, int n_pen, const int64_t * ign, int n_ign,
+                                              int i) {
+    const int64_t * p = i < n_pen ? rec + i : i < n_pen + n_ign ? ign + (i - n_pen) : &kNoListEntry;
+    return *p;
+}
+
 __device__ __forceinline__ float float_of_key(uint32_t k) {
     return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
@@ -434,8 +448,17 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
     const float c2 = a.row_lse ? (1.0f / a.temperature) * kLog2e : kLog2e;
 
     // ---- A. load + CFG + streamed statistics -----------------------------------------
-    // All loads of the row are issued before any is consumed (no branch between
-    // them: ids past V read a clamped, valid address and are masked to -inf).
+    // The list entries first, then all loads of the row, issued before any is
+    // consumed (no branch between them: ids past V read a clamped, valid
+    // address and are masked to -inf).
+    const bool use_pen = a.recent != nullptr && a.n_recent > 0;
+    const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
+    const bool adjusted = use_pen || use_ign;  // uniform per workgroup
+    const int n_pen = use_pen ? a.n_recent : 0;
+    const int n_ign = use_ign ? a.n_ignore : 0;
+    const int64_t * rec = use_pen ? a.recent + row * a.n_recent : &kNoListEntry;
+    const int64_t * ign = use_ign ? a.ignore : &kNoListEntry;
+    const int64_t entry = list_entry(rec, n_pen, ign, n_ign, tid);
     float v[ITEMS];
     row_stats st;
     const float * crow = a.cond + row * a.row_pitch;
@@ -443,9 +466,6 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
     else load_row<VEC, NCH, false, kFull>(v, st, crow, crow, V, tid, a.cfg_scale, c2);
     for (int i = tid; i < words; i += kThreads) L.sel[i] = 0u;
 
-    const bool use_pen = a.recent != nullptr && a.n_recent > 0;
-    const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
-    const bool adjusted = use_pen || use_ign;  // uniform per workgroup
     bool has_nan;  // a NaN (exact), or in the streamed case possibly a +inf
     float tmax;
     if (adjusted) {
@@ -454,17 +474,12 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
             L.ign[i] = 0u;
         }
         __syncthreads();
-        if (use_pen) {
-            const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
-            const int64_t * rec = a.recent + row * a.n_recent;
-            for (int i = tid; i < a.n_recent; i += kThreads) {
-                const int64_t t = rec[i];
+        const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
+        for (int i = tid; i < n_pen + n_ign; i += kThreads) {
+            const int64_t t = i < kThreads ? entry : list_entry(rec, n_pen, ign, n_ign, i);
+            if (i < n_pen) {
                 if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
-            }
-        }
-        if (use_ign) {
-            for (int i = tid; i < a.n_ignore; i += kThreads) {
-                const int64_t t = a.ignore[i];
+            } else {
                 if (t >= 0 && t < V) atomicOr(&L.ign[t >> 5], 1u << (t & 31));
             }
         }
@@ -737,35 +752,38 @@ int launch_sample(const levo_hip_sample_args & a, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Decode-step sampling in one launch (levo_hip_sample_step).
+// Decode-step sampling in two launches (levo_hip_sample_step).
 //
-// A decode step samples a handful of rows, so one workgroup per row would
-// leave all but a few CUs idle and pull each row through one CU. Here every
-// row is split into segments of 4096 ids, one 512-thread workgroup each
-// (8 ids per thread):
-//   1. the workgroup loads its segment, applies CFG, the repetition penalty
-//      and the ignore list (the few list ids inside the segment, found with
-//      wave-uniform compares), and reduces the segment's maximum, first
-//      maximum, NaN flag and softmax sum;
-//   2. it bounds its own k-th largest value from below (per wave the
-//      ceil(k/8)-th largest lane maximum, the smallest of the eight) and hands
-//      the values at or above that bound, the bound and the reductions to the
-//      workspace; any k-th largest of the whole row is at least the largest
-//      of the segment bounds, and every id of the row's top-k set is among
-//      the handed-over candidates;
-//   3. the last segment of a row to arrive (a counter per row) merges them:
-//      the exact k-th value over the candidates (one wave, as phase D above),
-//      the selection in ascending id order (phase E), the row's outputs;
-//   4. the last row to finish (a counter over the rows) makes every row's
-//      draw exactly as levo_hip_sample_draw does.
-// A row whose candidates do not fit (k = 0, very large k, heavy ties) takes
-// select_general in its merging workgroup, from the row itself. The counters
-// start at zero and the kernel leaves them at zero.
-constexpr int kStepPer = 8;                     // ids per thread
-constexpr int kStepSegIds = kThreads * kStepPer; // ids per segment
-constexpr int kStepCandCap = 256;               // candidates a segment hands over
-constexpr int kStepMergeCap = 512;              // candidates the merging wave holds (8 per lane)
-constexpr int kStepWords = kMaxVocab / 32;      // bitmap words of the longest row
+// A decode step samples a handful of rows. One workgroup per row pulls each
+// row (two 16385-logit inputs under CFG: 131 KB) through one CU, at that CU's
+// share of the HBM bandwidth: about 5 us before any selection starts. Here
+// every row is split into segments of 4096 ids:
+//   1. segment launch, one 512-thread workgroup per (row, segment), 8 ids per
+//      thread: loads, CFG, the repetition penalty and the ignore list (the
+//      list ids inside the segment); the segment's maximum, first maximum,
+//      NaN flag and softmax sum; and the segment's own top-k candidate set,
+//      found as the row kernel finds a row's (gather above a per-wave bound,
+//      the exact k-th key by a one-wave radix select, ties kept), written to
+//      the workspace in ascending id order with the segment's head. The
+//      row's k-th largest value is at least every segment's k-th largest, so
+//      the union of the segment sets holds every candidate of the row.
+//   2. merge launch, one wave per row, 8 rows per workgroup: the row's
+//      maximum, first maximum and log-sum-exp from the heads; its k-th key by
+//      a radix select over the handed-over candidates (at most 64 per
+//      segment, read with the heads in one round trip); and the candidates
+//      at or above it, whose ascending id order is the segments' order and
+//      each list's own. When every row fits one workgroup it then makes
+//      every row's draw, as levo_hip_sample_draw does, after a workgroup
+//      barrier; with more rows the draw is a third launch.
+// No workgroup waits for another. A row that does not fit (k = 0, k > 512,
+// more than 64 candidates in a segment, as with heavy ties) takes
+// select_general over the whole row in the merge launch.
+constexpr int kStepPer = 8;                       // ids per thread
+constexpr int kStepSegIds = kThreads * kStepPer;  // ids per segment
+constexpr int kStepSegWords = kStepSegIds / 32;   // bitmap words of a segment
+constexpr int kStepCandCap = 256;                 // candidate slots of a segment in the workspace
+constexpr int kStepHandCap = 64;                  // candidates per segment the merging wave reads
+constexpr int kStepWords = kMaxVocab / 32;        // bitmap words of the longest row
 constexpr int kStepMaxSegs = kMaxVocab / kStepSegIds;
 
 struct step_head {
@@ -773,8 +791,8 @@ struct step_head {
     float bv;       // value at its first maximum
     int32_t best;   // first id holding the maximum
     int32_t nan;    // the segment holds a NaN
-    float low;      // lower bound of the segment's k-th largest value (-inf: none)
-    int32_t count;  // ids at or above `low` (more than kStepCandCap: not handed over)
+    uint32_t tau;   // key of the segment's k-th largest value (0: fewer than k ids)
+    int32_t count;  // candidates handed over in ascending id order; -1: none (general path)
     float sum;      // sum over the segment of exp((l - max) / T)
     int32_t pad;
 };
@@ -785,25 +803,11 @@ struct step_seg {
     int32_t id[kStepCandCap];
 };
 
-// The workspace starts with a fixed counter region, the same for every row
-// count and vocabulary, so a workspace reused with other shapes keeps its
-// zeroed counters: one arrival counter per row, the last slot counts
-// finished rows.
+// The workspace starts with a reserved region of fixed size, the same for
+// every row count and vocabulary; the segment records follow.
 constexpr int kStepCounters = 4096;
 constexpr int64_t kStepCounterBytes = kStepCounters * 4;
 constexpr int64_t kStepMaxRows = kStepCounters - 1;
-
-struct step_lds {
-    row_lds<kStepWords> L;
-    float hmax[kStepMaxSegs];
-    float hbv[kStepMaxSegs];
-    int hbest[kStepMaxSegs];
-    int hnan[kStepMaxSegs];
-    float hlow[kStepMaxSegs];
-    int hcount[kStepMaxSegs];
-    float hsum[kStepMaxSegs];
-    int last;
-};
 
 // Id of item q of thread tid in a segment starting at lo: dwordx4 chunks of
 // 4 ids per thread (VEC 4) or single ids kThreads apart (VEC 1); coalesced
@@ -814,10 +818,8 @@ __device__ __forceinline__ int step_id(int lo, int tid, int q) {
 }
 
 template <int VEC>
-__global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sample_args a, const levo_hip_draw_args d,
-                                                                uint8_t * ws, int segs) {
-    __shared__ step_lds S;
-    row_lds<kStepWords> & L = S.L;
+__global__ __launch_bounds__(kThreads) void step_segment_kernel(const levo_hip_sample_args a, uint8_t * ws, int segs) {
+    __shared__ row_lds<kStepSegWords> L;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -830,11 +832,17 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
     int k = a.top_k[stream];
     if (k <= 0 || k >= V) k = 0;  // keep every id
     const int kw = (k + kWaves - 1) / kWaves;
-    const int words = (V + 31) / 32;
-    uint32_t * counters = reinterpret_cast<uint32_t *>(ws);
-    step_seg * segv = reinterpret_cast<step_seg *>(ws + kStepCounterBytes) + row * segs;
+    step_seg & out = reinterpret_cast<step_seg *>(ws + kStepCounterBytes)[row * segs + seg];
 
     // ---- 1. loads, CFG, penalty, ignore list, reductions ------------------------------
+    // the list entries first (see list_entry), then the segment's logits
+    const bool use_pen = a.recent != nullptr && a.n_recent > 0;
+    const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
+    const int n_pen = use_pen ? a.n_recent : 0;
+    const int n_ign = use_ign ? a.n_ignore : 0;
+    const int64_t * rec = use_pen ? a.recent + row * a.n_recent : &kNoListEntry;
+    const int64_t * ign = use_ign ? a.ignore : &kNoListEntry;
+    const int64_t entry = list_entry(rec, n_pen, ign, n_ign, tid);
     const float * crow = a.cond + row * a.row_pitch;
     const float * urow = a.uncond ? a.uncond + row * a.row_pitch : nullptr;
     float c[kStepPer], u[kStepPer];
@@ -857,31 +865,24 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
             u[q] = urow ? urow[off] : c[q];
         }
     }
-    for (int i = tid; i < words; i += kThreads) L.sel[i] = 0u;
+    if (tid < kStepSegWords) L.sel[tid] = 0u;
 
     // Penalty and ignore ids inside this segment, as bitmaps of its 4096 ids
-    // (128 words each), built from the lists loaded in parallel.
-    const bool use_pen = a.recent != nullptr && a.n_recent > 0;
-    const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
-    int pen = 0, ign = 0;  // item bits
+    // (128 words each).
+    int pen = 0, ign_bits = 0;  // item bits
     if (use_pen || use_ign) {
         if (tid < kStepSegIds / 32) {
             L.pen[tid] = 0u;
             L.ign[tid] = 0u;
         }
         __syncthreads();
-        if (use_pen) {
-            const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
-            const int64_t top = hi < limit ? hi : limit;
-            const int64_t * rec = a.recent + row * a.n_recent;
-            for (int i = tid; i < a.n_recent; i += kThreads) {
-                const int64_t t = rec[i];
+        const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
+        const int64_t top = hi < limit ? hi : limit;
+        for (int i = tid; i < n_pen + n_ign; i += kThreads) {
+            const int64_t t = i < kThreads ? entry : list_entry(rec, n_pen, ign, n_ign, i);
+            if (i < n_pen) {
                 if (t >= lo && t < top) atomicOr(&L.pen[(t - lo) >> 5], 1u << ((t - lo) & 31));
-            }
-        }
-        if (use_ign) {
-            for (int i = tid; i < a.n_ignore; i += kThreads) {
-                const int64_t t = a.ignore[i];
+            } else {
                 if (t >= lo && t < hi) atomicOr(&L.ign[(t - lo) >> 5], 1u << ((t - lo) & 31));
             }
         }
@@ -890,7 +891,7 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
         for (int q = 0; q < kStepPer; ++q) {
             const int rel = step_id<VEC>(lo, tid, q) - lo;
             pen |= (L.pen[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
-            ign |= (L.ign[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
+            ign_bits |= (L.ign[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
         }
     }
     float v[kStepPer];
@@ -900,14 +901,14 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
     for (int q = 0; q < kStepPer; ++q) {
         float x = urow ? u[q] + a.cfg_scale * (c[q] - u[q]) : c[q];
         if (pen & (1 << q)) x = x / a.repetition_penalty;
-        if (ign & (1 << q)) x = -INFINITY;
+        if (ign_bits & (1 << q)) x = -INFINITY;
         v[q] = step_id<VEC>(lo, tid, q) < hi ? x : -INFINITY;
         has_nan = has_nan || __builtin_isnan(v[q]);
         tmax = fmaxf(tmax, v[q]);
     }
     const bool tvalid = step_id<VEC>(lo, tid, 0) < hi;
 
-    // ---- 2. segment reductions, bound and hand-over -------------------------------------
+    // ---- 2. segment reductions and the per-wave bound of the k-th value -------------------
     const float wm = wave_max_f32(tmax);
     const bool wnan = __ballot(has_nan) != 0;
     float wlow = -INFINITY;
@@ -955,7 +956,7 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
         if (lane == 0) L.wlse[wave] = s;
     }
     // gather the ids >= low (k >= 1), padding excluded, into the wave's
-    // kSegCap slots; a longer count (up to 512) only marks the segment full
+    // kSegCap slots; a longer count only marks the segment as not fitting
     const bool gather = k >= 1 && kw <= 64 && !seg_nan;
     if (gather) {
         int base = 0;
@@ -976,169 +977,266 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
         if (lane == 0) L.wcnt[wave] = base;
     }
     __syncthreads();
-    int seg_start[kWaves + 1];
-    seg_start[0] = 0;
+    if (wave != 0) return;
+
+    // ---- 3. wave 0: the segment's exact k-th key and its candidates in id order ------------
+    int best = L.wbest[0], bw = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) seg_start[w + 1] = seg_start[w] + (gather ? L.wcnt[w] : 0);
-    const int ncand = gather ? seg_start[kWaves] : kStepCandCap + 1;
-    step_seg & out = segv[seg];
-    if (ncand <= kStepCandCap) {
-        for (int j = tid; j < ncand; j += kThreads) {
-            int w = 0;
-#pragma unroll
-            for (int q = 1; q < kWaves; ++q) w += j >= seg_start[q] ? 1 : 0;
-            out.val[j] = L.cv[w][j - seg_start[w]];
-            out.id[j] = L.ci[w][j - seg_start[w]];
+    for (int w = 1; w < kWaves; ++w) {
+        if (L.wbest[w] < best) {
+            best = L.wbest[w];
+            bw = w;
         }
     }
-    if (tid == 0) {
-        int best = L.wbest[0], bw = 0;
+    float sum = 0.0f;
+    if (a.row_lse) {
+        sum = L.wlse[0];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) {
-            if (L.wbest[w] < best) {
-                best = L.wbest[w];
-                bw = w;
+        for (int w = 1; w < kWaves; ++w) sum += L.wlse[w];
+    }
+    int seg_start[kWaves + 1];
+    seg_start[0] = 0;
+    bool fits = gather;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const int c = fits ? L.wcnt[w] : 0;
+        fits = fits && c <= kSegCap;
+        seg_start[w + 1] = seg_start[w] + c;
+    }
+    const int ncand = seg_start[kWaves];
+    fits = fits && ncand <= kBisCap;
+    int count = -1;
+    uint32_t tau = 0u;
+    if (fits) {  // uniform
+        constexpr int kSlots = kBisCap / 64;
+        float cval[kSlots];
+        int cidx[kSlots];
+        uint32_t keys[kSlots];
+        bool valid[kSlots];
+        const float * cv = &L.cv[0][0];
+        const int * ci = &L.ci[0][0];
+        int flat[kSlots];
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            const int j = lane + 64 * s;
+            int delta = -seg_start[0];
+#pragma unroll
+            for (int q = 1; q < kWaves; ++q) delta = j >= seg_start[q] ? q * kSegCap - seg_start[q] : delta;
+            valid[s] = j < ncand;
+            flat[s] = valid[s] ? j + delta : 0;
+        }
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            cval[s] = cv[flat[s]];
+            cidx[s] = ci[flat[s]];
+        }
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) keys[s] = valid[s] ? float_key(cval[s]) : 0u;
+        if (k == 1) {
+            tau = float_key(m);
+        } else {
+            const uint32_t lo_key = low == -INFINITY ? 0u : float_key(low);
+            const uint32_t hi_key = float_key(m);
+            const uint32_t diff = lo_key ^ hi_key;
+            const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
+            const uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
+            tau = radix_kth_key<kSlots>(L.hist, keys, valid, k, prefix, top);
+        }
+        bool take[kSlots];
+#pragma unroll
+        for (int s = 0; s < kSlots; ++s) {
+            take[s] = valid[s] && keys[s] >= tau;
+            if (take[s]) atomicOr(&L.sel[(cidx[s] - lo) >> 5], 1u << ((cidx[s] - lo) & 31));
+        }
+        const int total = wave_bitmap_prefix(L, kStepSegWords);
+        if (total <= kStepCandCap) {
+            count = total;
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) {
+                if (take[s]) {
+                    const int pos = slot_of(L, cidx[s] - lo);
+                    out.val[pos] = cval[s];
+                    out.id[pos] = cidx[s];
+                }
             }
         }
-        float sum = 0.0f;
-        if (a.row_lse) {
-            sum = L.wlse[0];
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) sum += L.wlse[w];
-        }
+    }
+    if (lane == 0) {
         step_head h;
         h.max = m;
         h.bv = best == INT_MAX ? m : L.wbv[bw];
         h.best = best;
         h.nan = seg_nan ? 1 : 0;
-        h.low = low;
-        h.count = ncand;
+        h.tau = tau;
+        h.count = count;
         h.sum = sum;
         h.pad = 0;
         out.h = h;
     }
-    // release the hand-over, then count the row's arrivals
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (tid == 0) S.last = atomicAdd(&counters[row], 1u) == static_cast<uint32_t>(segs - 1) ? 1 : 0;
-    __syncthreads();
-    if (!S.last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every segment's hand-over is visible
+}
 
-    // ---- 3. merge the row -----------------------------------------------------------------
-    if (tid < segs) {
-        const step_head h = segv[tid].h;
-        S.hmax[tid] = h.max;
-        S.hbv[tid] = h.bv;
-        S.hbest[tid] = h.best;
-        S.hnan[tid] = h.nan;
-        S.hlow[tid] = h.low;
-        S.hcount[tid] = h.count;
-        S.hsum[tid] = h.sum;
+struct merge_lds {
+    row_lds<kStepWords> L;                           // the general path
+    __attribute__((aligned(16))) uint32_t hist[kWaves][256];  // one radix-select histogram per wave
+    int slow[kWaves];                                // rows that take the general path
+    float rm[kWaves];
+    int best[kWaves];
+    float bv[kWaves];
+    float lse[kWaves];
+};
+
+__global__ __launch_bounds__(kThreads) void step_merge_kernel(const levo_hip_sample_args a, const levo_hip_draw_args d,
+                                                               const uint8_t * ws, int segs) {
+    __shared__ merge_lds S;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+    const bool live = row < a.rows;  // uniform per wave
+    const int V = static_cast<int>(a.vocab);
+    if (live) {
+        const int stream = static_cast<int>(row % a.n_streams);
+        int k = a.top_k[stream];
+        if (k <= 0 || k >= V) k = 0;
+        const int kw = (k + kWaves - 1) / kWaves;
+        const step_seg * segv = reinterpret_cast<const step_seg *>(ws + kStepCounterBytes) + row * segs;
+        // every load first: lane g < segs takes head g, and every lane the
+        // first kStepHandCap candidate slots of each segment
+        const step_head h = segv[lane < segs ? lane : 0].h;
+        float cval[kStepMaxSegs];
+        int cidx[kStepMaxSegs];
+#pragma unroll
+        for (int s = 0; s < kStepMaxSegs; ++s) {
+            const int g = s < segs ? s : 0;
+            cval[s] = segv[g].val[lane];
+            cidx[s] = segv[g].id[lane];
+        }
+        const bool mine = lane < segs;
+        const bool row_nan = __ballot(mine && h.nan != 0) != 0;
+        const float rm = wave_max_f32(mine ? h.max : -INFINITY);
+        // the first maximum lies in the first segment whose maximum is the row's
+        const uint64_t at_max = __ballot(mine && h.max == rm && h.best != INT_MAX);
+        const int bseg = at_max != 0 ? __builtin_ctzll(at_max) : 0;
+        const int best = at_max != 0 ? dpp::lane(h.best, bseg) : -1;
+        const float bv = dpp::lane(h.bv, bseg);
+        float lse = NAN;
+        if (!row_nan && a.row_lse) {
+            if (rm == -INFINITY) {
+                lse = -INFINITY;
+            } else if (rm == INFINITY) {
+                lse = INFINITY;
+            } else {
+                const float inv_t = 1.0f / a.temperature;
+                float z = 0.0f;
+                for (int g = 0; g < segs; ++g)
+                    z += dpp::lane(h.sum, g) * __expf((fmaxf(dpp::lane(h.max, g), -FLT_MAX) - rm) * inv_t);
+                lse = rm / a.temperature + logf(z);
+            }
+        }
+        const bool counts_ok = __ballot(mine && (h.count < 0 || h.count > kStepHandCap)) == 0;
+        const bool fast = !row_nan && k >= 1 && kw <= 64 && counts_ok;
+        if (row_nan) {  // the reference throws "logits contain NaN"
+            if (lane == 0) {
+                a.best[row] = -1;
+                a.count[row] = -1;
+                if (a.row_max) a.row_max[row] = NAN;
+                if (a.row_lse) a.row_lse[row] = NAN;
+            }
+        } else if (fast) {
+            // The row's k-th key is at least every segment's (a segment with
+            // fewer than k ids reports 0): candidates below the largest of
+            // them cannot be selected and are left out, so the rest lie
+            // between it and the maximum's key.
+            const uint32_t lo_key =
+                k == 1 ? 0u : dpp::allreduce(mine ? h.tau : 0u, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+            uint32_t keys[kStepMaxSegs];
+            bool valid[kStepMaxSegs];
+#pragma unroll
+            for (int s = 0; s < kStepMaxSegs; ++s) {
+                const int c = s < segs ? dpp::lane(h.count, s) : 0;
+                keys[s] = float_key(cval[s]);
+                valid[s] = lane < c && keys[s] >= lo_key;
+                keys[s] = valid[s] ? keys[s] : 0u;
+            }
+            uint32_t tau;
+            if (k == 1) {
+                tau = float_key(rm);
+            } else {
+                // it shares the common high bits of lo_key and the maximum's key
+                const uint32_t hi_key = float_key(rm);
+                const uint32_t diff = lo_key ^ hi_key;
+                const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
+                const uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
+                tau = radix_kth_key<kStepMaxSegs>(S.hist[wave], keys, valid, k, prefix, top);
+            }
+            // slot = candidates taken in earlier segments + rank within this one
+            const bool want_probs = a.cand_probs != nullptr;
+            const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
+            bool take[kStepMaxSegs];
+            int pos[kStepMaxSegs];
+            float wgt[kStepMaxSegs];
+            int total = 0;
+            double z = 0.0;
+#pragma unroll
+            for (int s = 0; s < kStepMaxSegs; ++s) {
+                take[s] = valid[s] && keys[s] >= tau;
+                const uint64_t mask = __ballot(take[s]);
+                pos[s] = total + rank_in_mask(mask);
+                total += static_cast<int>(__popcll(mask));
+                wgt[s] = want_probs && take[s] ? cand_weight(cval[s], rm, inv_t) : 0.0f;
+                z += static_cast<double>(wgt[s]);
+            }
+            z = wave_sum_f64(z);
+            const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+            const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
+#pragma unroll
+            for (int s = 0; s < kStepMaxSegs; ++s) {
+                if (take[s] && pos[s] < a.capacity) {
+                    const int64_t o = row * a.capacity + pos[s];
+                    a.cand_ids[o] = cidx[s];
+                    if (a.cand_logits) a.cand_logits[o] = cval[s];
+                    if (want_probs) a.cand_probs[o] = z_ok ? wgt[s] * inv_z : (cidx[s] == best ? 1.0f : 0.0f);
+                }
+            }
+            if (lane == 0) {
+                a.best[row] = best;
+                a.count[row] = total;
+                if (a.row_max) a.row_max[row] = bv;
+                if (a.row_lse) a.row_lse[row] = lse;
+            }
+        }
+        if (lane == 0) {
+            S.slow[wave] = !row_nan && !fast ? 1 : 0;
+            S.rm[wave] = rm;
+            S.best[wave] = best;
+            S.bv[wave] = bv;
+            S.lse[wave] = lse;
+        }
+    } else if (lane == 0) {
+        S.slow[wave] = 0;
     }
-    if (tid == 0) counters[row] = 0u;  // every segment has arrived: ready for the next launch
     __syncthreads();
-    bool row_nan = false;
-    float rm = -INFINITY;
-    float bound = -INFINITY;  // every segment bound is <= the row's k-th largest value
-    int handed = 0;
-    bool fits = k >= 1 && kw <= 64;
-    for (int g = 0; g < segs; ++g) {
-        row_nan = row_nan || S.hnan[g] != 0;
-        rm = fmaxf(rm, S.hmax[g]);
-        bound = fmaxf(bound, S.hlow[g]);
-        fits = fits && S.hcount[g] <= kStepCandCap;
-        handed += S.hcount[g] <= kStepCandCap ? S.hcount[g] : 0;
-    }
-    if (k == 1) bound = rm;
-    int best = -1, bseg = 0;
-    for (int g = 0; g < segs; ++g) {
-        if (best < 0 && S.hbest[g] != INT_MAX && S.hmax[g] == rm) {
-            best = S.hbest[g];
-            bseg = g;
-        }
-    }
-    float lse = NAN;
-    if (!row_nan && a.row_lse) {
-        if (rm == -INFINITY) {
-            lse = -INFINITY;
-        } else if (rm == INFINITY) {
-            lse = INFINITY;
-        } else {
-            const float inv_t = 1.0f / a.temperature;
-            float z = 0.0f;
-            for (int g = 0; g < segs; ++g) z += S.hsum[g] * __expf((fmaxf(S.hmax[g], -FLT_MAX) - rm) * inv_t);
-            lse = rm / a.temperature + logf(z);
-        }
-    }
-    if (row_nan) {  // the reference throws "logits contain NaN"
-        if (tid == 0) {
-            a.best[row] = -1;
-            a.count[row] = -1;
-            if (a.row_max) a.row_max[row] = NAN;
-            if (a.row_lse) a.row_lse[row] = NAN;
-        }
-    }
-    // Keep the handed-over candidates >= bound, compacted (in no particular
-    // order; the bitmap orders them) into one flat LDS array.
-    int total_cand = 0;
-    float * fv = &L.cv[0][0];
-    int * fi = &L.ci[0][0];
-    if (!row_nan && fits) {
-        constexpr int kPer = (kStepCandCap * kStepMaxSegs + kThreads - 1) / kThreads;
-        float kv[kPer];
-        int ki[kPer];
-        int kept = 0;
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int j = tid + i * kThreads;
-            kv[i] = -INFINITY;
-            ki[i] = -1;
-            if (j < handed) {
-                int g = 0, start = 0;
-                while (j >= start + S.hcount[g]) {
-                    start += S.hcount[g];
-                    ++g;
-                }
-                const float x = segv[g].val[j - start];
-                if (x >= bound) {
-                    kv[i] = x;
-                    ki[i] = segv[g].id[j - start];
-                    ++kept;
-                }
-            }
-        }
-        const int incl = wave_inclusive_scan_i32(kept);
-        if (lane == 63) L.wcnt[wave] = incl;
-        __syncthreads();
-        int off = incl - kept;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) off += w < wave ? L.wcnt[w] : 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) total_cand += L.wcnt[w];
-        if (total_cand <= kStepMergeCap) {
-#pragma unroll
-            for (int i = 0; i < kPer; ++i) {
-                if (ki[i] >= 0) {
-                    fv[off] = kv[i];
-                    fi[off] = ki[i];
-                    ++off;
-                }
-            }
-        }
-        fits = total_cand <= kStepMergeCap;
-        __syncthreads();
-    }
-    if (!row_nan && !fits) {
-        // the whole row again, with full-row penalty and ignore bitmaps
+
+    // ---- rows that do not fit: the whole row again, by the whole workgroup ------------------
+    const int words = (V + 31) / 32;
+    for (int w = 0; w < kWaves; ++w) {
+        if (!S.slow[w]) continue;  // uniform
+        const int64_t r = static_cast<int64_t>(blockIdx.x) * kWaves + w;
+        const int stream = static_cast<int>(r % a.n_streams);
+        int k = a.top_k[stream];
+        if (k <= 0 || k >= V) k = 0;
+        const bool use_pen = a.recent != nullptr && a.n_recent > 0;
+        const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
+        row_lds<kStepWords> & L = S.L;
         for (int i = tid; i < words; i += kThreads) {
+            L.sel[i] = 0u;
             L.pen[i] = 0u;
             L.ign[i] = 0u;
         }
         __syncthreads();
         if (use_pen) {
             const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
-            const int64_t * rec = a.recent + row * a.n_recent;
+            const int64_t * rec = a.recent + r * a.n_recent;
             for (int i = tid; i < a.n_recent; i += kThreads) {
                 const int64_t t = rec[i];
                 if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
@@ -1151,90 +1249,20 @@ __global__ __launch_bounds__(kThreads) void sample_step_kernel(const levo_hip_sa
             }
         }
         __syncthreads();
-        select_general(a, L, row, V, k, rm, best, use_pen, use_ign);
+        select_general(a, L, r, V, k, S.rm[w], S.best[w], use_pen, use_ign);
         if (tid == 0) {
-            a.best[row] = best;
-            a.count[row] = L.total;
-            if (a.row_max) a.row_max[row] = S.hbv[bseg];
-            if (a.row_lse) a.row_lse[row] = lse;
+            a.best[r] = S.best[w];
+            a.count[r] = L.total;
+            if (a.row_max) a.row_max[r] = S.bv[w];
+            if (a.row_lse) a.row_lse[r] = S.lse[w];
         }
-    } else if (!row_nan) {
-        if (wave == 0) {
-            constexpr int kSlots = kStepMergeCap / 64;
-            float cval[kSlots];
-            int cidx[kSlots];
-            uint32_t keys[kSlots];
-#pragma unroll
-            for (int s = 0; s < kSlots; ++s) {
-                const int j = lane + 64 * s;
-                const bool ok = j < total_cand;
-                cval[s] = fv[ok ? j : 0];
-                cidx[s] = fi[ok ? j : 0];
-                keys[s] = ok ? float_key(cval[s]) : 0u;
-            }
-            uint32_t tau;
-            if (k == 1) {
-                tau = float_key(rm);
-            } else {
-                const uint32_t lo_key = bound == -INFINITY ? 0u : float_key(bound);
-                const uint32_t hi_key = float_key(rm);
-                const uint32_t diff = lo_key ^ hi_key;
-                const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
-                uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
-                for (int bit = top; bit >= 0; --bit) {
-                    const uint32_t cand = prefix | (1u << bit);
-                    int cnt = 0;
-#pragma unroll
-                    for (int s = 0; s < kSlots; ++s) cnt += static_cast<int>(__popcll(__ballot(keys[s] >= cand)));
-                    if (cnt >= k) prefix = cand;
-                }
-                tau = prefix;
-            }
-            const bool want_probs = a.cand_probs != nullptr;
-            const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
-            bool take[kSlots];
-            float wgt[kSlots];
-            double z = 0.0;
-#pragma unroll
-            for (int s = 0; s < kSlots; ++s) {
-                take[s] = keys[s] >= tau && lane + 64 * s < total_cand;
-                wgt[s] = want_probs && take[s] ? cand_weight(cval[s], rm, inv_t) : 0.0f;
-                if (take[s]) atomicOr(&L.sel[cidx[s] >> 5], 1u << (cidx[s] & 31));
-                z += static_cast<double>(wgt[s]);
-            }
-            z = wave_sum_f64(z);
-            const bool z_ok = z > 0.0 && __builtin_isfinite(z);
-            const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
-            const int total = wave_bitmap_prefix(L, words);
-#pragma unroll
-            for (int s = 0; s < kSlots; ++s) {
-                const int pos = take[s] ? slot_of(L, cidx[s]) : a.capacity;
-                if (pos < a.capacity) {
-                    const int64_t o = row * a.capacity + pos;
-                    a.cand_ids[o] = cidx[s];
-                    if (a.cand_logits) a.cand_logits[o] = cval[s];
-                    if (want_probs) a.cand_probs[o] = z_ok ? wgt[s] * inv_z : (cidx[s] == best ? 1.0f : 0.0f);
-                }
-            }
-            if (lane == 0) {
-                a.best[row] = best;
-                a.count[row] = total;
-                if (a.row_max) a.row_max[row] = S.hbv[bseg];
-                if (a.row_lse) a.row_lse[row] = lse;
-            }
-        }
+        __syncthreads();  // the next row reuses the bitmaps
     }
 
-    // ---- 4. the last row to finish draws every row -----------------------------------------
+    // ---- the draw of every row (all rows are in this workgroup) ----------------------------
     if (d.tokens == nullptr) return;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // this row's outputs
-    __syncthreads();
-    if (tid == 0) S.last = atomicAdd(&counters[kStepCounters - 1], 1u) == static_cast<uint32_t>(a.rows - 1) ? 1 : 0;
-    __syncthreads();
-    if (!S.last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // every row's outputs
-    for (int64_t r = wave; r < a.rows; r += kWaves) draw_row(d, r);
-    if (tid == 0) counters[kStepCounters - 1] = 0u;
+    __syncthreads();  // every row's outputs are written and visible to the workgroup
+    if (live) draw_row(d, row);
 }
 
 int64_t step_segments(int64_t vocab) { return (vocab + kStepSegIds - 1) / kStepSegIds; }
@@ -1268,6 +1296,7 @@ int check_sample_args(const levo_hip_sample_args & a) {
                      (a.repetition_penalty > 0.0f && __builtin_isfinite(a.repetition_penalty)),
                  "repetition penalty must be finite and positive");
     LEVO_REQUIRE(a.n_recent >= 0 && a.n_ignore >= 0, "cfg_sample: negative list length");
+    LEVO_REQUIRE(a.n_recent <= (1 << 30) && a.n_ignore <= (1 << 30), "cfg_sample: list longer than 2^30 ids");
     LEVO_REQUIRE((a.cand_probs == nullptr && a.row_lse == nullptr) ||
                      (a.temperature > 0.0f && __builtin_isfinite(a.temperature)),
                  "temperature must be finite and positive for softmax outputs");
@@ -1314,9 +1343,19 @@ int launch_step(const levo_hip_sample_args * args, const levo_hip_draw_args * dr
     const uint32_t grid = static_cast<uint32_t>(a.rows * segs);
     const bool vec = a.row_pitch % 4 == 0 && aligned16(a.cond) && (a.uncond == nullptr || aligned16(a.uncond));
     uint8_t * w = static_cast<uint8_t *>(ws);
-    if (vec) sample_step_kernel<4><<<grid, kThreads, 0, stream>>>(a, d, w, static_cast<int>(segs));
-    else sample_step_kernel<1><<<grid, kThreads, 0, stream>>>(a, d, w, static_cast<int>(segs));
-    return launch_status("levo_hip_sample_step");
+    if (vec) step_segment_kernel<4><<<grid, kThreads, 0, stream>>>(a, w, static_cast<int>(segs));
+    else step_segment_kernel<1><<<grid, kThreads, 0, stream>>>(a, w, static_cast<int>(segs));
+    const int sa = launch_status("levo_hip_sample_step");
+    if (sa != LEVO_HIP_OK) return sa;
+    // the merge launch draws when every row is in its one workgroup; otherwise
+    // the draw is a launch of its own
+    const uint32_t merge_groups = static_cast<uint32_t>(ceil_div(a.rows, kWaves));
+    levo_hip_draw_args dm = d;
+    if (merge_groups > 1) dm.tokens = nullptr;
+    step_merge_kernel<<<merge_groups, kThreads, 0, stream>>>(a, dm, w, static_cast<int>(segs));
+    const int sb = launch_status("levo_hip_sample_step");
+    if (sb != LEVO_HIP_OK || draw == nullptr || merge_groups == 1) return sb;
+    return levo_hip_sample_draw(&d, reinterpret_cast<levo_hip_stream_t>(stream));
 }
 
 }  // namespace
@@ -1324,24 +1363,17 @@ int launch_step(const levo_hip_sample_args * args, const levo_hip_draw_args * dr
 // ---- levo_hip_sample_step_static: the step on library-held scratch ----------------------
 // Callers that cannot allocate (graph capture, serving loops) get the
 // workspace from this array: one copy per GPU, held until the process ends.
-// Device memory of a code object starts zeroed, and every call leaves the
-// counter region zero; set-up clears it once more per device. Calls that
-// overlap on one GPU share the array and race.
+// Every call writes the segment records it reads, so nothing needs clearing.
+// Calls that overlap on one GPU share the array and race.
 constexpr int64_t kStaticScratchBytes = int64_t{2} << 20;
 static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
 
 namespace {
 
-__global__ void zero_words(uint32_t * p, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
-
 // The device address of `scratch` on the current device, found once per
 // device (with that device current) and kept; the host-side name is only a
-// stand-in. The first call on a device also clears the counter region on
-// `stream`, ahead of the work it is about to launch there.
-int scratch_address(void ** out, hipStream_t stream) {
+// stand-in.
+int scratch_address(void ** out) {
     constexpr int kMaxDevices = 64;
     static std::mutex mu;
     static void * ptrs[kMaxDevices] = {};
@@ -1359,9 +1391,6 @@ int scratch_address(void ** out, hipStream_t stream) {
                       hipGetErrorString(err));
             return LEVO_HIP_ERR_RUNTIME;
         }
-        zero_words<<<kStepCounters / 256, 256, 0, stream>>>(static_cast<uint32_t *>(p), kStepCounters);
-        const int st = launch_status("sample_step_static");
-        if (st != LEVO_HIP_OK) return st;
         ptrs[device] = p;
     }
     *out = ptrs[device];
@@ -1417,7 +1446,7 @@ extern "C" int levo_hip_sample_step_static(const levo_hip_sample_args * args, co
                  static_cast<long long>(args->rows), static_cast<long long>(args->vocab),
                  static_cast<long long>(need), static_cast<long long>(kStaticScratchBytes));
     void * ws = nullptr;
-    const int st = scratch_address(&ws, as_hip(stream));
+    const int st = scratch_address(&ws);
     if (st != LEVO_HIP_OK) return st;
     return launch_step(args, draw, ws, kStaticScratchBytes, as_hip(stream));
 }

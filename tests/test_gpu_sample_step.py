@@ -1,5 +1,6 @@
-"""levo_hip_sample_step (one launch: CFG, penalty, ignore list, top-k
-candidates and the draw of a decode step, rows split over workgroups) against
+"""levo_hip_sample_step (CFG, penalty, ignore list, top-k candidates and the
+draw of a decode step; rows split over segment workgroups, merged and drawn
+in a second launch) against
 levo_hip_cfg_sample + levo_hip_sample_draw on the same inputs, against the
 oracle, and against the compiled reference Sampler (src/levo-sampling.cpp).
 
@@ -254,22 +255,22 @@ def test_reference_sampler_decode_loop(hip, binding, dev, oracle, ref):
             consumed += int(got["draws"][-1])
             recent = np.concatenate([recent[:, 1:], got["tokens"][:, None]], axis=1)
         assert consumed == s.draw_count
-    # the counters (the first 16 KiB) are back at zero
+    # the reserved region (the first 16 KiB) is left as it was
     head = from_dev(ws[0])[:4096]
     assert np.all(head.view(np.uint32) == 0)
 
 
 def test_workspace_reused_across_shapes(hip, binding, dev, oracle):
-    """One workspace, sized for the largest call, serves calls of other row
-    counts and vocabularies in any order: the counters sit at a fixed place
-    and every call leaves them zero."""
+    """One workspace, sized for the largest call and never cleared (it starts
+    full of NaN bytes), serves calls of other row counts and vocabularies in
+    any order."""
     ws = workspace(hip, dev, 40, 16385)
+    ws[0].fill_(float("nan"))
     for rows, V in ((3, 16385), (40, 16385), (5, 2049), (40, 4096), (1, 7), (3, 16385)):
         cond = _f16_logits(oracle, rows, V, 2900 + rows + V)
         c = Case(binding, dev, cond, None, top_k=[50, 1, 3], n_streams=3)
         bits = peek_bits(oracle, rows + V, 0, rows)
         same_outputs(c.step(hip, ws=ws, bits=bits), c.two_launch(hip, bits), c, draws=True)
-    assert np.all(from_dev(ws[0])[:4096].view(np.uint32) == 0)
 
 
 def test_rejects_bad_arguments(hip, binding, dev, oracle):
