@@ -574,7 +574,8 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
     quantized to Q8_0; weights rotated over >= 512 MB. `layer`: one decoder
     layer's decode step as it runs: the 4 activation quantizations
     (levo_hip_quantize_chunk: attention input, attention output, FFN input,
-    FFN hidden) and the 7 matrices (q, k, v, o, gate, up, down)."""
+    FFN hidden) and the 7 matrices (q, k, v, o, gate, up, down); then the
+    same work in 5 launches (levo_hip_mul_mat_q8_0_multi)."""
     shapes = {"attn_1536x1536": (1536, 1536), "ffn_up_8960x1536": (8960, 1536),
               "ffn_down_1536x8960": (1536, 8960), "head_16385x1536": (16385, 1536)}
     n_vec = 2
@@ -637,6 +638,24 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
     out["layer_4_quantize_7_matrices"] = op_entry(layer_bytes, ms, n_vec=n_vec,
                                                   dtype="q8_0 weights / q8_0 activations",
                                                   us_per_token_28_layers=round(28 * ms * 1e3, 1))
+    # the same layer with the matrices that share an input in one launch each
+    # (levo_hip_mul_mat_q8_0_multi: q / k / v, o, gate / up with the F32
+    # activations quantized inside the launch), ffn_down as before: 5 launches
+    yq = [torch.empty((n_vec, 1536), device=dev) for _ in range(4)]
+    yf = [torch.empty((n_vec, 8960), device=dev) for _ in range(2)]
+
+    def run_layer_multi(i):
+        hip.mul_mat_q8_0_multi([(mats[i][j], yq[j], 1536, 1536) for j in range(3)], 1536, n_vec,
+                               x=x_attn, x_pitch=1536)
+        hip.mul_mat_q8_0_multi([(mats[i][3], yq[3], 1536, 1536)], 1536, n_vec, x=x_out, x_pitch=1536)
+        hip.mul_mat_q8_0_multi([(mats[i][4], yf[0], 8960, 8960), (mats[i][5], yf[1], 8960, 8960)], 1536, n_vec,
+                               x=x_ffn, x_pitch=1536)
+        hip.quantize_chunk(8, x_hid, xb_hid, 0, n_vec, 8960)
+        hip.mul_mat_q8_0(mats[i][6].data_ptr(), xb_hid, ys[1536], 1536, 1536, 8960, n_vec)
+
+    ms = time_op(torch, head, run_layer_multi, n, warmup, max(steps, 20))
+    out["layer_5_launches"] = op_entry(layer_bytes, ms, n_vec=n_vec, dtype="q8_0 weights / q8_0 activations",
+                                       us_per_token_28_layers=round(28 * ms * 1e3, 1))
     return out
 
 

@@ -542,6 +542,28 @@ int levo_hip_dequantize(levo_hip_type type, const void * src, void * dst, levo_h
 int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks, float * y, int64_t y_pitch,
                           int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream);
 
+/* One matrix of levo_hip_mul_mat_q8_0_multi. */
+typedef struct levo_hip_mat_q8_0 {
+    const void * weight;  /* [rows][k/32] block_q8_0, 16-byte aligned */
+    float * y;            /* [n_vec][y_pitch] F32 */
+    int64_t y_pitch;      /* >= rows */
+    int64_t rows;
+} levo_hip_mat_q8_0;
+
+/* levo_hip_mul_mat_q8_0 for 1 to 4 matrices that read the same activation
+ * columns (a decode layer's q / k / v, or gate / up: ggml_mul_mat calls that
+ * share src1, each quantizing it to its vec_dot_type first) in one launch.
+ * The activations come either as Q8_0 blocks (x_blocks, as for
+ * levo_hip_mul_mat_q8_0) or as F32 x [n_vec][x_pitch] (16-byte aligned,
+ * x_pitch >= k and a multiple of 4), which the launch quantizes itself with
+ * levo_hip_quantize_chunk's block function, for n_vec * k / 32 <= 256
+ * blocks; pass exactly one of the two. Every y equals what
+ * levo_hip_quantize_chunk + levo_hip_mul_mat_q8_0 give for that matrix, bit
+ * for bit. Matrices of zero rows are skipped. */
+int levo_hip_mul_mat_q8_0_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, const void * x_blocks,
+                                const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
+                                levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* K-quants on the decode path (ggml block layouts, QK_K = 256):              */
 /*   block_q4_K {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}            144 B */

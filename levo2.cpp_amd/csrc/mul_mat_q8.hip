@@ -23,7 +23,16 @@
 // nb <= 512 / 1024: a row is split over 2 / 4 waves (2 / 1 rows per
 // workgroup), whose partial sums meet in LDS in wave order (LeLM's
 // ffn_down, K = 8960 / 11008).
+//
+// levo_hip_mul_mat_q8_0_multi runs up to four matrices that read the same
+// activation columns (q / k / v, gate / up) in one launch: each matrix owns
+// a contiguous range of workgroups. It can also take the activations in F32
+// and quantize them inside the launch (one block per thread, the block
+// function of levo_hip_quantize_chunk, requested before the weights and
+// computed while they are in flight), for n_vec * K / 32 <= 256 blocks; the
+// results equal levo_hip_quantize_chunk + levo_hip_mul_mat_q8_0 bit for bit.
 #include "common.hpp"
+#include "quant_block.hpp"
 #include "span_load.hpp"
 
 #include <algorithm>
@@ -40,6 +49,8 @@ constexpr int kMaxVectors = 8;
 constexpr int kXChunks = 5;  // activation chunks per thread loaded up front (20 KiB per workgroup)
 constexpr int kMaxBlocksPerRow = 1024;
 
+constexpr int kMaxMats = 4;
+
 struct mm_params {
     const uint8_t * w;    // [rows][nb] weight blocks, 16-byte aligned
     const uint8_t * x;    // [n_vec][nb] activation blocks, 16-byte aligned
@@ -50,6 +61,23 @@ struct mm_params {
     int32_t nb;           // blocks per row (K / 32)
     int32_t n_vec;
     int32_t stage_bytes;  // LDS bytes per wave for its weight span
+};
+
+// One launch over n_mats matrices sharing the activations: matrix m takes
+// workgroups [first[m], first[m + 1]). p holds the shared fields (x, nb,
+// n_vec, stage_bytes); w / y / rows / y_pitch are per matrix. With xf the
+// activations come in F32 ([n_vec][x_pitch], 16-byte aligned rows) and are
+// quantized in the workgroup.
+struct mm_launch {
+    mm_params p;
+    const uint8_t * w[kMaxMats];
+    float * y[kMaxMats];
+    int64_t rows[kMaxMats];
+    int64_t y_pitch[kMaxMats];
+    int32_t first[kMaxMats + 1];
+    int32_t n_mats;
+    const float * xf;
+    int64_t x_pitch;
 };
 
 // Block at LDS byte offset `off` (even): its F16 scale and 8 quant dwords.
@@ -102,9 +130,30 @@ __device__ __forceinline__ bool wave_span(const mm_params & p, int64_t grp, int 
     }
 }
 
-template <int LPR, int WPR>
-__global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params p) {
+template <int LPR, int WPR, bool FUSED>
+__global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch ml) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    // this workgroup's matrix, selected among arguments read at fixed
+    // offsets (an index into the argument arrays would make the weight
+    // addresses wait for a second, dependent argument load)
+    mm_params p = ml.p;
+    p.w = ml.w[0];
+    p.y = ml.y[0];
+    p.rows = ml.rows[0];
+    p.y_pitch = ml.y_pitch[0];
+    int first = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxMats; ++i) {
+        if (i < ml.n_mats && static_cast<int>(blockIdx.x) >= ml.first[i]) {
+            p.w = ml.w[i];
+            p.y = ml.y[i];
+            p.rows = ml.rows[i];
+            p.y_pitch = ml.y_pitch[i];
+            first = ml.first[i];
+        }
+    }
+    p.w_bytes = p.rows * p.nb * kQ8Bytes;
+    const int64_t grp = static_cast<int64_t>(blockIdx.x) - first;
     const int nvb = p.n_vec * p.nb;
     uint32_t * xq = reinterpret_cast<uint32_t *>(smem);                   // [n_vec][nb][8]
     float * dx = reinterpret_cast<float *>(smem + nvb * 32);               // [n_vec][nb]
@@ -119,24 +168,52 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_params 
     //    L2) are unpacked while the weights are still in flight
     const int64_t xbytes = static_cast<int64_t>(nvb) * kQ8Bytes;
     const int nchunks = static_cast<int>((xbytes + 15) >> 4);
-    u32x4 xr[kXChunks];  // unconditional (see load_span): chunks past the end re-read chunk 0
+    // FUSED: thread t < nvb quantizes activation block t (column t / nb,
+    // block t % nb); other threads read block 0 and drop it
+    const int xt = static_cast<int>(threadIdx.x) < nvb ? static_cast<int>(threadIdx.x) : 0;
+    constexpr int kXr = FUSED ? 8 : kXChunks;
+    u32x4 xr[kXr];  // unconditional (see load_span): chunks past the end re-read chunk 0
 #pragma unroll
-    for (int i = 0; i < kXChunks; ++i) {
-        const int c = static_cast<int>(threadIdx.x) + kThreads * i;
-        const bool whole = c < nchunks && 16 * static_cast<int64_t>(c) + 16 <= xbytes;
-        xr[i] = *reinterpret_cast<const u32x4 *>(p.x + (whole ? 16 * static_cast<int64_t>(c) : 0));
+    for (int i = 0; i < kXr; ++i) {
+        if constexpr (FUSED) {
+            const float * src = ml.xf + (xt / p.nb) * ml.x_pitch + (xt % p.nb) * 32;
+            xr[i] = *reinterpret_cast<const u32x4 *>(src + 4 * i);
+        } else {
+            const int c = static_cast<int>(threadIdx.x) + kThreads * i;
+            const bool whole = c < nchunks && 16 * static_cast<int64_t>(c) + 16 <= xbytes;
+            xr[i] = *reinterpret_cast<const u32x4 *>(p.x + (whole ? 16 * static_cast<int64_t>(c) : 0));
+        }
     }
     int64_t row0;
     int nrows, kb0, kb1;
-    const bool have = wave_span<LPR, WPR>(p, blockIdx.x, wave, row0, nrows, kb0, kb1);
+    const bool have = wave_span<LPR, WPR>(p, grp, wave, row0, nrows, kb0, kb1);
     u32x4 regs[kChunksPerLane];
     const int64_t sb0 = (row0 * p.nb + kb0) * kQ8Bytes;
     const int64_t sb1 = (row0 * p.nb + (WPR > 1 ? kb1 : static_cast<int64_t>(nrows) * p.nb)) * kQ8Bytes;
     load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
 
     // 2. activation blocks -> LDS (raw, through the stage area), then
-    //    unpacked to aligned quant dwords and F32 scales
-    {
+    //    unpacked to aligned quant dwords and F32 scales; or, FUSED,
+    //    quantized from F32 straight into that form
+    if constexpr (FUSED) {
+        float xs[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            xs[4 * i] = __uint_as_float(xr[i].x);
+            xs[4 * i + 1] = __uint_as_float(xr[i].y);
+            xs[4 * i + 2] = __uint_as_float(xr[i].z);
+            xs[4 * i + 3] = __uint_as_float(xr[i].w);
+        }
+        uint32_t q[8];
+        const uint16_t d = quantize_q8_0_block(xs, q);
+        if (static_cast<int>(threadIdx.x) < nvb) {
+            dx[threadIdx.x] = h2f(d);
+            u32x4 * dst = reinterpret_cast<u32x4 *>(xq + threadIdx.x * 8);
+            dst[0] = u32x4{q[0], q[1], q[2], q[3]};
+            dst[1] = u32x4{q[4], q[5], q[6], q[7]};
+        }
+        lds_barrier();  // LDS only: the weight loads stay in flight
+    } else {
 #pragma unroll
         for (int i = 0; i < kXChunks; ++i) {
             const int c = static_cast<int>(threadIdx.x) + kThreads * i;
@@ -223,8 +300,9 @@ constexpr int rows_per_workgroup() {
 }
 
 template <int LPR, int WPR>
-int launch_mm(mm_params p, hipStream_t st) {
+int launch_mm(mm_launch ml, hipStream_t st, const char * what) {
     constexpr int rows_per_block = rows_per_workgroup<LPR, WPR>();
+    mm_params & p = ml.p;
     const int span_blocks = WPR > 1 ? (p.nb + WPR - 1) / WPR : (64 / LPR) * p.nb;
     p.stage_bytes = (span_blocks * kQ8Bytes + 32 + 15) & ~15;
     const int64_t nvb = static_cast<int64_t>(p.n_vec) * p.nb;
@@ -233,10 +311,31 @@ int launch_mm(mm_params p, hipStream_t st) {
     const int64_t stages = std::max<int64_t>(int64_t{kWaves} * p.stage_bytes, (nvb * kQ8Bytes + 16 + 15) & ~int64_t{15});
     const size_t lds = ((static_cast<size_t>(nvb) * 36 + kWaves * kMaxVectors * 4 + 15) & ~size_t{15}) +
                        static_cast<size_t>(stages);
-    LEVO_REQUIRE(lds <= 64 * 1024, "mul_mat_q8_0: n_vec * K too large for the workgroup's LDS");
-    const uint32_t blocks = static_cast<uint32_t>(ceil_div(p.rows, rows_per_block));
-    mul_mat_q8_0_kernel<LPR, WPR><<<blocks, kThreads, lds, st>>>(p);
-    return launch_status("levo_hip_mul_mat_q8_0");
+    LEVO_REQUIRE(lds <= 64 * 1024, "%s: n_vec * K too large for the workgroup's LDS", what);
+    int64_t groups = 0;
+    for (int m = 0; m < ml.n_mats; ++m) {
+        ml.first[m] = static_cast<int32_t>(groups);
+        groups += ceil_div(ml.rows[m], rows_per_block);
+    }
+    for (int m = ml.n_mats; m <= kMaxMats; ++m) ml.first[m] = static_cast<int32_t>(groups);
+    LEVO_REQUIRE(groups < (int64_t{1} << 31), "%s: too many rows", what);
+    if (groups == 0) return LEVO_HIP_OK;
+    const uint32_t blocks = static_cast<uint32_t>(groups);
+    if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, true><<<blocks, kThreads, lds, st>>>(ml);
+    else mul_mat_q8_0_kernel<LPR, WPR, false><<<blocks, kThreads, lds, st>>>(ml);
+    return launch_status(what);
+}
+
+// The fewest lanes per row that hold the row's blocks in one wave's span
+// (more workgroups with fewer rows each measured slower at 1536 rows: each
+// repeats the activation staging).
+int launch_geometry(const mm_launch & ml, hipStream_t st, const char * what) {
+    const int nb = ml.p.nb;
+    if (nb <= 64) return launch_mm<16, 1>(ml, st, what);
+    if (nb <= 128) return launch_mm<32, 1>(ml, st, what);
+    if (nb <= 256) return launch_mm<64, 1>(ml, st, what);
+    if (nb <= 512) return launch_mm<64, 2>(ml, st, what);
+    return launch_mm<64, 4>(ml, st, what);
 }
 
 }  // namespace
@@ -255,23 +354,59 @@ extern "C" int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks,
     LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "mul_mat_q8_0: null tensor");
     LEVO_REQUIRE(aligned16(weight) && aligned16(x_blocks), "mul_mat_q8_0: block buffers must be 16-byte aligned");
     LEVO_REQUIRE(y_pitch >= rows, "mul_mat_q8_0: y pitch smaller than the row count");
-    mm_params p;
-    p.w = static_cast<const uint8_t *>(weight);
-    p.x = static_cast<const uint8_t *>(x_blocks);
-    p.y = y;
-    p.rows = rows;
-    p.nb = static_cast<int32_t>(k / 32);
-    p.w_bytes = rows * p.nb * kQ8Bytes;
-    p.y_pitch = y_pitch;
-    p.n_vec = static_cast<int32_t>(n_vec);
-    p.stage_bytes = 0;
-    const hipStream_t st = as_hip(stream);
-    // The fewest lanes per row that hold the row's blocks in one wave's span
-    // (more workgroups with fewer rows each measured slower at 1536 rows:
-    // each repeats the activation staging).
-    if (p.nb <= 64) return launch_mm<16, 1>(p, st);
-    if (p.nb <= 128) return launch_mm<32, 1>(p, st);
-    if (p.nb <= 256) return launch_mm<64, 1>(p, st);
-    if (p.nb <= 512) return launch_mm<64, 2>(p, st);
-    return launch_mm<64, 4>(p, st);
+    mm_launch ml{};
+    ml.p.x = static_cast<const uint8_t *>(x_blocks);
+    ml.p.nb = static_cast<int32_t>(k / 32);
+    ml.p.n_vec = static_cast<int32_t>(n_vec);
+    ml.n_mats = 1;
+    ml.w[0] = static_cast<const uint8_t *>(weight);
+    ml.y[0] = y;
+    ml.rows[0] = rows;
+    ml.y_pitch[0] = y_pitch;
+    return launch_geometry(ml, as_hip(stream), "levo_hip_mul_mat_q8_0");
+}
+
+extern "C" int levo_hip_mul_mat_q8_0_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, const void * x_blocks,
+                                           const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
+                                           levo_hip_stream_t stream) {
+    const char * what = "mul_mat_q8_0_multi";
+    LEVO_REQUIRE(n_mats >= 1 && n_mats <= kMaxMats, "%s: 1 to %d matrices", what, kMaxMats);
+    LEVO_REQUIRE(mats != nullptr, "%s: null matrix list", what);
+    LEVO_REQUIRE(n_vec >= 0, "%s: negative size", what);
+    LEVO_REQUIRE(k > 0 && k % 32 == 0, "%s: K must be a positive multiple of 32 (pad the rows)", what);
+    LEVO_REQUIRE(k / 32 <= kMaxBlocksPerRow, "%s: K exceeds %d", what, kMaxBlocksPerRow * 32);
+    LEVO_REQUIRE(n_vec <= kMaxVectors, "%s: at most %d activation columns", what, kMaxVectors);
+    LEVO_REQUIRE((x_blocks == nullptr) != (x == nullptr), "%s: pass exactly one of x_blocks and x", what);
+    if (x_blocks != nullptr) {
+        LEVO_REQUIRE(aligned16(x_blocks), "%s: block buffers must be 16-byte aligned", what);
+    } else {
+        LEVO_REQUIRE(n_vec * (k / 32) <= kThreads,
+                     "%s: F32 activations are quantized in the launch for n_vec * K / 32 <= %d blocks; "
+                     "quantize larger ones with levo_hip_quantize_chunk", what, kThreads);
+        LEVO_REQUIRE(aligned16(x) && x_pitch >= k && x_pitch % 4 == 0,
+                     "%s: F32 activations need 16-byte aligned rows of at least K values", what);
+    }
+    mm_launch ml{};
+    ml.p.x = static_cast<const uint8_t *>(x_blocks);
+    ml.p.nb = static_cast<int32_t>(k / 32);
+    ml.p.n_vec = static_cast<int32_t>(n_vec);
+    ml.xf = x;
+    ml.x_pitch = x_pitch;
+    ml.n_mats = 0;
+    for (int32_t i = 0; i < n_mats; ++i) {
+        const levo_hip_mat_q8_0 & mt = mats[i];
+        LEVO_REQUIRE(mt.rows >= 0, "%s: negative size", what);
+        LEVO_REQUIRE(mt.rows < (int64_t{1} << 31) / 4, "%s: too many rows", what);
+        if (mt.rows == 0) continue;
+        LEVO_REQUIRE(mt.weight != nullptr && mt.y != nullptr, "%s: null tensor", what);
+        LEVO_REQUIRE(aligned16(mt.weight), "%s: block buffers must be 16-byte aligned", what);
+        LEVO_REQUIRE(mt.y_pitch >= mt.rows, "%s: y pitch smaller than the row count", what);
+        ml.w[ml.n_mats] = static_cast<const uint8_t *>(mt.weight);
+        ml.y[ml.n_mats] = mt.y;
+        ml.rows[ml.n_mats] = mt.rows;
+        ml.y_pitch[ml.n_mats] = mt.y_pitch;
+        ++ml.n_mats;
+    }
+    if (ml.n_mats == 0 || n_vec == 0) return LEVO_HIP_OK;
+    return launch_geometry(ml, as_hip(stream), what);
 }

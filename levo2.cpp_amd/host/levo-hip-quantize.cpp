@@ -39,6 +39,14 @@ void mul_mat_q8_0_quantized(const void * weight, const void * x_blocks, float * 
     check_status(levo_hip_mul_mat_q8_0(weight, x_blocks, y, rows, rows, k, n_vec, stream));
 }
 
+void mul_mat_q8_0_shared_input(const q8_0_matrix * mats, int n_mats, const float * x, int64_t k, int64_t n_vec,
+                               stream_t stream) {
+    levo_hip_mat_q8_0 m[4] = {};
+    const int n = n_mats < 0 ? 0 : n_mats;
+    for (int i = 0; i < n && i < 4; ++i) m[i] = levo_hip_mat_q8_0{mats[i].weight, mats[i].y, mats[i].rows, mats[i].rows};
+    check_status(levo_hip_mul_mat_q8_0_multi(m, n_mats, nullptr, x, k, k, n_vec, stream));
+}
+
 void mul_mat_kquant(levo_hip_type type, const void * weight, const float * x, void * x_blocks, float * y,
                     int64_t rows, int64_t k, int64_t n_vec, stream_t stream) {
     if (rows == 0 || n_vec == 0) return;

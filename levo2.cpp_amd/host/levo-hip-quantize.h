@@ -50,6 +50,19 @@ void mul_mat_q8_0(const void * weight, const float * x, void * x_blocks, float *
 void mul_mat_q8_0_quantized(const void * weight, const void * x_blocks, float * y, int64_t rows, int64_t k,
                             int64_t n_vec, stream_t stream = nullptr);
 
+// Up to four Q8_0 matrices that read the same F32 input x [n_vec][k] (a
+// layer's q / k / v, or gate / up) in one launch, the input quantized inside
+// it: each y equals mul_mat_q8_0's for that matrix, bit for bit. Needs
+// n_vec * k / 32 <= 256 and x 16-byte aligned; quantize larger inputs with
+// mul_mat_q8_0 and reuse the blocks.
+struct q8_0_matrix {
+    const void * weight;  // [rows][k / 32] block_q8_0, 16-byte aligned
+    float * y;            // [n_vec][rows]
+    int64_t rows;
+};
+void mul_mat_q8_0_shared_input(const q8_0_matrix * mats, int n_mats, const float * x, int64_t k, int64_t n_vec,
+                               stream_t stream = nullptr);
+
 // ggml_mul_mat(W, x) for a Q4_K / Q5_K / Q6_K weight at decode (the Q4_K_M,
 // Q5_K_M and Q6_K profiles' matrices, src/levo-quantization.h:47-55, 96-118),
 // as ggml's CPU backend computes it: x [n_vec][k] F32 is quantized to Q8_K

@@ -56,6 +56,12 @@ class DrawArgs(ctypes.Structure):
 TOKEN_NAN, TOKEN_OVERFLOW, TOKEN_RECHECK = -1, -2, -3
 
 
+class MatQ8_0(ctypes.Structure):
+    """levo_hip_mat_q8_0 (include/levo_hip.h)."""
+
+    _fields_ = [("weight", _P), ("y", _P), ("y_pitch", _I64), ("rows", _I64)]
+
+
 class FlowInputArgs(ctypes.Structure):
     """levo_hip_flow_input_args (include/levo_hip.h)."""
 
@@ -189,6 +195,7 @@ class LevoHip:
             "levo_hip_flow_normalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_flow_denormalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_mul_mat_q8_0": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+            "levo_hip_mul_mat_q8_0_multi": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_quantize_q8_K": (ctypes.c_int, [_P, _P, _I64, _P]),
             "levo_hip_mul_mat_kquant": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
             "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
@@ -345,6 +352,15 @@ class LevoHip:
     def mul_mat_q8_0(self, weight, x_blocks, y, y_pitch, rows, k, n_vec, stream=None):
         return self._check(self.lib.levo_hip_mul_mat_q8_0(_addr(weight), _addr(x_blocks), _addr(y), y_pitch,
                                                           rows, k, n_vec, _stream(stream)))
+
+    def mul_mat_q8_0_multi(self, mats, k, n_vec, x_blocks=None, x=None, x_pitch=0, stream=None):
+        """mats: (weight, y, y_pitch, rows) tuples sharing the activations,
+        given as Q8_0 blocks (x_blocks) or as F32 rows (x, x_pitch)."""
+        arr = (MatQ8_0 * max(len(mats), 1))()
+        for i, (w, y, y_pitch, rows) in enumerate(mats):
+            arr[i] = MatQ8_0(_addr(w), _addr(y), y_pitch, rows)
+        return self._check(self.lib.levo_hip_mul_mat_q8_0_multi(arr, len(mats), _addr(x_blocks), _addr(x), x_pitch,
+                                                                k, n_vec, _stream(stream)))
 
     def quantize_q8_K(self, x, y, k, stream=None):
         return self._check(self.lib.levo_hip_quantize_q8_K(_addr(x), _addr(y), k, _stream(stream)))

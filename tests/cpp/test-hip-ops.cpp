@@ -297,6 +297,21 @@ void mul_mat_surface() {
     expect_throw<std::invalid_argument>("multiple of 32", [&] {
         mul_mat_q8_0_quantized(dw.data(), dxb.data(), dy.data(), rows, 100, n_vec);
     });
+
+    // two matrices sharing the F32 input in one launch (the second is the
+    // first 7 rows of the same blocks): the same exact integers
+    device_vec<float> dy40(static_cast<std::size_t>(2 * ir)), dy7(2 * 7);
+    const q8_0_matrix mats[2] = {{diw.data(), dy40.data(), ir}, {diw.data(), dy7.data(), 7}};
+    mul_mat_q8_0_shared_input(mats, 2, dix.data(), ik, 2);
+    CHECK(bit_equal(dy40.get().data(), igot.data(), igot.size()));
+    const std::vector<float> got7 = dy7.get();
+    for (int64_t v = 0; v < 2; ++v) {
+        CHECK(bit_equal(got7.data() + v * 7, igot.data() + v * ir, 7));
+    }
+    expect_throw<std::invalid_argument>("<= 256 blocks", [&] {
+        const q8_0_matrix big[1] = {{dw.data(), dy.data(), rows}};
+        mul_mat_q8_0_shared_input(big, 1, dx.data(), k, n_vec);
+    });
 }
 
 // K-quant decode path: padded_input_columns for 256-value blocks
