@@ -68,28 +68,19 @@ __device__ __forceinline__ void quantize_block(const float (&x)[32], uint8_t * l
         // ggml's scan (the first value of largest |x|, NaN never taken) as
         // four independent scans of 8 values joined in order: the strict
         // comparison keeps the earliest quarter on ties, as the single scan
-        // keeps the earliest value.
-        float qa[4], qv[4];
+        // keeps the earliest value. The scan's amax is always |max|, so only
+        // the signed value is kept and compared through |.| (a compare with
+        // absolute-value operands and one select per value).
+        float qv[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            qa[q] = 0.0f;
             qv[q] = 0.0f;
 #pragma unroll
-            for (int k = 8 * q; k < 8 * q + 8; ++k) {
-                if (qa[q] < fabsf(x[k])) {
-                    qa[q] = fabsf(x[k]);
-                    qv[q] = x[k];
-                }
-            }
+            for (int k = 8 * q; k < 8 * q + 8; ++k) qv[q] = fabsf(qv[q]) < fabsf(x[k]) ? x[k] : qv[q];
         }
-        float amax = qa[0], vmax = qv[0];
+        float vmax = qv[0];
 #pragma unroll
-        for (int q = 1; q < 4; ++q) {
-            if (amax < qa[q]) {
-                amax = qa[q];
-                vmax = qv[q];
-            }
-        }
+        for (int q = 1; q < 4; ++q) vmax = fabsf(vmax) < fabsf(qv[q]) ? qv[q] : vmax;
         const float d = vmax / -8.0f;
         const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
         uint32_t pk[4];

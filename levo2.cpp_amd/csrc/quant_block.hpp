@@ -84,6 +84,21 @@ __device__ __forceinline__ uint32_t pack4(uint32_t a, uint32_t b, uint32_t c, ui
     return a | (b << 8) | (c << 16) | (d << 24);
 }
 
+// v_cvt_i32_f32 of v (truncation; 0 for NaN), all 32 bits.
+__device__ __forceinline__ uint32_t trunc_i32(float v) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return static_cast<uint32_t>(r);
+}
+
+// The low bytes of a, b, c, d as one little-endian dword, by two byte
+// permutes (selector byte s takes byte s of {hi:lo}, 0x0c gives 0) and an OR.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);  // a0, b0, 0, 0
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000c0cu);  // 0, 0, c0, d0
+    return ab | cd;
+}
+
 // Quantizes one block of 32 values as quantize_row_q8_0_ref does:
 // amax = MAX(amax, |x|) in index order, d = amax / 127, id = d ? 1 / d : 0,
 // q = (int8_t)roundf(x * id). Writes the quants as 8 little-endian dwords and
@@ -108,13 +123,14 @@ __device__ __forceinline__ uint16_t quantize_q8_0_block(const float (&x)[32], ui
     const float d = amax / 127.0f;
     const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
     if (!has_nan) {
-        // every |x| <= amax: |x * id| stays within 128 (or is NaN)
+        // every |x| <= amax: |x * id| stays within 128 (or is NaN), so the
+        // low byte of the truncated int32 is the reference's (int8_t)
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
             uint32_t q[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) q[k] = low_byte_i8(half_away_offset(x[4 * w + k] * id));
-            pk[w] = pack4(q[0], q[1], q[2], q[3]);
+            for (int k = 0; k < 4; ++k) q[k] = trunc_i32(half_away_offset(x[4 * w + k] * id));
+            pk[w] = pack_low_bytes(q[0], q[1], q[2], q[3]);
         }
     } else {
         // A NaN reset the running MAX, so earlier values may exceed amax
