@@ -58,10 +58,10 @@ constexpr int kMaxVocab = 32768;
 
 // The penalty and ignore lists enter a row's bitmaps through one entry per
 // thread: entry i < n_pen of the row's recent ids, then entry i - n_pen of the
-// ignore list. The first kThreads entries are requested before the row's
-// logits, so the two memory round trips overlap; the load takes no branch (a
-// lane without an entry reads kNoListEntry), which keeps the compiler from
-// waiting for it before the row's loads are issued.
+// ignore list. The decode step's segment kernel requests the first kThreads
+// entries before its logits, so the two memory round trips overlap; the load
+// takes no branch (a lane without an entry reads kNoListEntry), which keeps
+// the compiler from waiting for it before the logits' loads are issued.
 __device__ const int64_t kNoListEntry = -1;
 
 __device__ __forceinline__ int64_t list_entry(const int64_t * rec, int n_pen, const int64_t * ign, int n_ign,
@@ -448,9 +448,10 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
     const float c2 = a.row_lse ? (1.0f / a.temperature) * kLog2e : kLog2e;
 
     // ---- A. load + CFG + streamed statistics -----------------------------------------
-    // The list entries first, then all loads of the row, issued before any is
-    // consumed (no branch between them: ids past V read a clamped, valid
-    // address and are masked to -inf).
+    // All loads of the row are issued before any is consumed (no branch
+    // between them: ids past V read a clamped, valid address and are masked
+    // to -inf). The penalty / ignore lists are read after the row (requesting
+    // them ahead of it measured slower: one more load in every row's queue).
     const bool use_pen = a.recent != nullptr && a.n_recent > 0;
     const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
     const bool adjusted = use_pen || use_ign;  // uniform per workgroup
@@ -458,7 +459,6 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
     const int n_ign = use_ign ? a.n_ignore : 0;
     const int64_t * rec = use_pen ? a.recent + row * a.n_recent : &kNoListEntry;
     const int64_t * ign = use_ign ? a.ignore : &kNoListEntry;
-    const int64_t entry = list_entry(rec, n_pen, ign, n_ign, tid);
     float v[ITEMS];
     row_stats st;
     const float * crow = a.cond + row * a.row_pitch;
@@ -476,7 +476,7 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
         __syncthreads();
         const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
         for (int i = tid; i < n_pen + n_ign; i += kThreads) {
-            const int64_t t = i < kThreads ? entry : list_entry(rec, n_pen, ign, n_ign, i);
+            const int64_t t = list_entry(rec, n_pen, ign, n_ign, i);
             if (i < n_pen) {
                 if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
             } else {
