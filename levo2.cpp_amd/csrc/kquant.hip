@@ -350,7 +350,9 @@ __device__ __forceinline__ void kq_compute(const kq_unit<TYPE> & w, int ib, int 
 //   3. each wave stores its span to its LDS stage area; each lane parses its
 //      units there and adds their terms; a reduction over the row's LPR lanes
 //      gives y.
-template <int TYPE, int LPR, int U, int CH>
+// WPR > 1 (LPR = 64): WPR waves share a row, each a contiguous part of its
+// super-blocks; their partial sums meet in LDS and are added in wave order.
+template <int TYPE, int LPR, int U, int CH, int WPR = 1>
 __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_params p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
     const int nb = p.nb;
@@ -364,12 +366,28 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
     uint8_t * stage = lds_raw + p.x_lds_bytes + wave * p.stage_bytes;
     constexpr int kRowsPerWave = 64 / LPR;
     constexpr int kBytes = TYPE == LEVO_HIP_TYPE_Q4_K ? 144 : TYPE == LEVO_HIP_TYPE_Q5_K ? 176 : 210;
-    // 1. the wave's rows [row0, row0 + nrows): bytes [sb0, sb1)
-    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * kRowsPerWave;
-    const int64_t left = p.rows - row0;
-    const int nrows = left < kRowsPerWave ? (left > 0 ? static_cast<int>(left) : 0) : kRowsPerWave;
-    const int64_t sb0 = row0 * p.row_bytes;
-    const int64_t sb1 = sb0 + nrows * p.row_bytes;
+    // 1. the wave's rows [row0, row0 + nrows): bytes [sb0, sb1); with WPR > 1
+    //    the WPR waves of a row each take a contiguous part of its blocks,
+    //    [kb0, kb1)
+    int64_t row0;
+    int nrows, kb0, kb1;
+    if constexpr (WPR > 1) {
+        row0 = static_cast<int64_t>(blockIdx.x) * (kThreads / 64 / WPR) + wave / WPR;
+        nrows = row0 < p.rows ? 1 : 0;
+        const int qb = (nb + WPR - 1) / WPR;
+        kb0 = (wave % WPR) * qb;
+        kb1 = kb0 + qb < nb ? kb0 + qb : nb;
+        if (kb0 >= kb1) nrows = 0;
+    } else {
+        row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * kRowsPerWave;
+        const int64_t left = p.rows - row0;
+        nrows = left < kRowsPerWave ? (left > 0 ? static_cast<int>(left) : 0) : kRowsPerWave;
+        kb0 = 0;
+        kb1 = nb;
+    }
+    const int64_t sb0 = row0 * p.row_bytes + static_cast<int64_t>(kb0) * kBytes;
+    const int64_t sb1 = WPR > 1 ? row0 * p.row_bytes + static_cast<int64_t>(kb1) * kBytes
+                                : sb0 + nrows * p.row_bytes;
     // The activation blocks (dwords 0 .. 73 nblk of x, 73 per 292-byte block)
     // are requested first, as dwordx4 with no branch around them (surplus
     // requests re-read the first chunk; the chunk crossing the end of x, if
@@ -425,7 +443,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
     const int li = lane % LPR;
     const bool live = g < nrows;
     const int lead = static_cast<int>(sb0 & 15);
-    const int units = nb * 8;
+    const int units = (kb1 - kb0) * 8;
     float acc_d[kMaxVec], acc_m[kMaxVec];
 #pragma unroll
     for (int v = 0; v < kMaxVec; ++v) acc_d[v] = acc_m[v] = 0.0f;
@@ -437,48 +455,82 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
                 const int off = lead + g * static_cast<int>(p.row_bytes) + (unit >> 3) * kBytes;
                 kq_unit<TYPE> w;
                 w.load(stage + off, unit & 7, (off & 2) != 0);
-                kq_compute<TYPE>(w, unit >> 3, unit & 7, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
+                kq_compute<TYPE>(w, kb0 + (unit >> 3), unit & 7, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
             }
         }
     }
     // every lane of the wave takes part in the shuffles
+    if constexpr (WPR > 1) {
+        // the row's parts meet in LDS, each at the start of its wave's own
+        // stage area (no longer read once the wave has computed), summed in
+        // wave order
+        float * part = reinterpret_cast<float *>(stage);
 #pragma unroll
-    for (int v = 0; v < kMaxVec; ++v) {
-        if (v < p.n_vec) {
-            const float sd = group_sum<LPR>(acc_d[v]);
-            const float sm = TYPE != LEVO_HIP_TYPE_Q6_K ? group_sum<LPR>(acc_m[v]) : 0.0f;
-            if (live && li == 0) p.y[v * p.y_pitch + row0 + g] = sd - sm;
+        for (int v = 0; v < kMaxVec; ++v) {
+            if (v < p.n_vec) {
+                const float sd = group_sum<LPR>(acc_d[v]);
+                const float sm = TYPE != LEVO_HIP_TYPE_Q6_K ? group_sum<LPR>(acc_m[v]) : 0.0f;
+                if (lane == 0) {
+                    part[2 * v] = sd;
+                    part[2 * v + 1] = sm;
+                }
+            }
+        }
+        __syncthreads();
+        if (wave % WPR == 0 && lane < p.n_vec && row0 < p.rows) {
+            float sd = part[2 * lane], sm = part[2 * lane + 1];
+#pragma unroll
+            for (int w = 1; w < WPR; ++w) {
+                const float * other = reinterpret_cast<const float *>(stage + w * p.stage_bytes);
+                sd += other[2 * lane];
+                sm += other[2 * lane + 1];
+            }
+            p.y[lane * p.y_pitch + row0] = sd - sm;
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < kMaxVec; ++v) {
+            if (v < p.n_vec) {
+                const float sd = group_sum<LPR>(acc_d[v]);
+                const float sm = TYPE != LEVO_HIP_TYPE_Q6_K ? group_sum<LPR>(acc_m[v]) : 0.0f;
+                if (live && li == 0) p.y[v * p.y_pitch + row0 + g] = sd - sm;
+            }
         }
     }
 }
 
-template <int TYPE, int LPR, int U, int CH>
+template <int TYPE, int LPR, int U, int CH, int WPR = 1>
 int launch_mul_mat_u(kq_params p, hipStream_t st) {
-    if (const int st = allow_dynamic_lds(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U, CH>),
+    if (const int st = allow_dynamic_lds(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U, CH, WPR>),
                                          160 * 1024, "levo_hip_mul_mat_kquant");
         st != LEVO_HIP_OK)
         return st;
     constexpr int kRowsPerWave = 64 / LPR;
-    const int64_t span = kRowsPerWave * p.row_bytes;
+    const int64_t span = WPR > 1 ? ceil_div(p.nb, WPR) * (p.row_bytes / p.nb) : kRowsPerWave * p.row_bytes;
     LEVO_REQUIRE(span + 15 <= int64_t{CH} * 64 * 16, "mul_mat_kquant: row span exceeds the wave's registers");
+    LEVO_REQUIRE(WPR == 1 || ceil_div(p.nb, WPR) * 8 <= int64_t{U} * LPR, "mul_mat_kquant: row part exceeds the lanes");
     p.stage_bytes = static_cast<int32_t>((span + 15 + 15) & ~int64_t{15});
     const size_t lds = static_cast<size_t>(p.x_lds_bytes) + static_cast<size_t>(kThreads / 64) * p.stage_bytes;
     LEVO_REQUIRE(lds <= 160 * 1024, "mul_mat_kquant: n_vec * k too large for the workgroup's LDS");
-    const int64_t rows_per_block = (kThreads / 64) * kRowsPerWave;
+    const int64_t rows_per_block = WPR > 1 ? (kThreads / 64) / WPR : (kThreads / 64) * kRowsPerWave;
     const dim3 grid(static_cast<uint32_t>(ceil_div(p.rows, rows_per_block)));
-    mul_mat_kquant_kernel<TYPE, LPR, U, CH><<<grid, kThreads, lds, st>>>(p);
+    mul_mat_kquant_kernel<TYPE, LPR, U, CH, WPR><<<grid, kThreads, lds, st>>>(p);
     return launch_status("levo_hip_mul_mat_kquant");
 }
 
 // Lanes per row, units per lane and span chunks per lane by the row's 8 nb
-// units (k <= 16384): a wave's span is 64 / LPR rows.
+// units (k <= 16384): a wave's span is 64 / LPR rows, or half a row.
 template <int TYPE>
 int launch_mul_mat(const kq_params & p, hipStream_t st) {
     const int units = p.nb * 8;
     if (units <= 64) return launch_mul_mat_u<TYPE, 16, 4, 8>(p, st);
     if (units <= 128) return launch_mul_mat_u<TYPE, 16, 8, 16>(p, st);
     if (units <= 256) return launch_mul_mat_u<TYPE, 32, 8, 16>(p, st);
-    return launch_mul_mat_u<TYPE, 64, 8, 16>(p, st);
+    // K > 8192 (LeLM's ffn_down, K = 8960): a row over two waves, each half
+    // its super-blocks, so each lane takes ~2 units instead of ~4 (Q4_K
+    // 10.2 -> 9.4 us; four waves per row, 11.1 us, repeat the activation
+    // staging in twice as many workgroups)
+    return launch_mul_mat_u<TYPE, 64, 4, 7, 2>(p, st);
 }
 
 }  // namespace
