@@ -502,7 +502,9 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     `sample_step_us`: the same step through levo_hip_sample_step (rows split
     into 4096-id segment workgroups, then one merge-and-draw workgroup);
     `roundtrip_us`: median wall time from the first launch until the 3 ids and
-    draw counts are in pinned host memory (Python launch overhead included)."""
+    draw counts are in pinned host memory (Python launch overhead included);
+    `graph_roundtrip_us`: the same with both launches and both copies
+    captured once into a HIP graph and replayed."""
     S, V, cap = 3, 16385, 64
     n = 64
     g = torch.Generator(device=dev)
@@ -559,12 +561,35 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
         stream.synchronize()
         walls.append(time.perf_counter() - t0)
     roundtrip_ms = float(np.median(walls[warmup:])) * 1e3
+    # the same step and copies captured once into a HIP graph and replayed
+    graph_rt_ms = None
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            step(0)
+            h_tok.copy_(tokens, non_blocking=True)
+            h_draws.copy_(draws, non_blocking=True)
+        torch.cuda.synchronize()
+        gwalls = []
+        for i in range(warmup + 200):
+            stream.synchronize()
+            t0 = time.perf_counter()
+            graph.replay()
+            stream.synchronize()
+            gwalls.append(time.perf_counter() - t0)
+        graph_rt_ms = float(np.median(gwalls[warmup:])) * 1e3
+    except Exception as e:  # graph capture is an extra measurement only
+        log(f"decode-step graph capture skipped: {e}")
     per = 2 * S * V * 4 + S * 50 * 8 + 3 * 8 + S * (4 + 4 + 4 + cap * 8 + 8 + 8 + 4)
     return op_entry(per, device_ms, shape=[1, 2, S, V], dtype="f32 logits / f64 weights", top_k=[50, 1, 1],
                     temperature=0.9, cfg_sample_us=round(sample_ms * 1e3, 3),
                     sample_draw_us=round((device_ms - sample_ms) * 1e3, 3),
                     sample_step_us=round(split_ms * 1e3, 3),
-                    roundtrip_us=round(roundtrip_ms * 1e3, 2), bytes_to_host=S * (8 + 4),
+                    roundtrip_us=round(roundtrip_ms * 1e3, 2),
+                    graph_roundtrip_us=None if graph_rt_ms is None else round(graph_rt_ms * 1e3, 2),
+                    bytes_to_host=S * (8 + 4),
                     bound="latency")
 
 

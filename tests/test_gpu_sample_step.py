@@ -291,3 +291,52 @@ def test_rejects_bad_arguments(hip, binding, dev, oracle):
     with pytest.raises(binding.LevoHipError):
         hip.sample_step_workspace_bytes(2, 40000)
     torch.cuda.synchronize()
+
+
+def test_decode_step_replayed_from_a_graph(hip, binding, dev, oracle):
+    """The decode step captured once into a HIP graph (torch.cuda.graph) and
+    replayed at 4 positions, each with new logits and raw values copied into
+    the graph's fixed input buffers, and eager calls between the replays:
+    every replay's tokens, draw counts and candidate sets equal the eager
+    calls' on the same inputs. Captured three ways: cfg_sample + sample_draw,
+    sample_step on a workspace, and sample_step_static (the entry point for
+    callers that cannot allocate, graph capture among them)."""
+    import torch
+    S, V, P = 3, 16385, 4
+    cond = _f16_logits(oracle, P * S, V, 3100)
+    uncond = _f16_logits(oracle, P * S, V, 3101)
+    recent = np.stack([np.arange(50, dtype=np.int64) * (7 + q) % (V - 1) for q in range(S)])
+    case = Case(binding, dev, cond[:S], uncond[:S], top_k=[50, 1, 1], n_streams=3, recent=recent,
+                penalty_limit=V - 1, ignore=(3, 9))
+    a, o = case.outputs()
+    d = case.draw_args(o, peek_bits(oracle, 7, 0, S), 0.9, True)
+    bits_t = case.keep[-1]
+    ws = workspace(hip, dev, S, V)
+    variants = {
+        "cfg_sample + sample_draw": lambda: (hip.cfg_sample(a), hip.sample_draw(d)),
+        "sample_step": lambda: hip.sample_step(a, d, ws[0], ws[1]),
+        "sample_step_static": lambda: hip.sample_step_static(a, d),
+    }
+    for name, fn in variants.items():
+        fn()  # eager first call (the static variant's per-device set-up)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.graph(graph, stream=side):
+            fn()
+        torch.cuda.synchronize()
+        for pos in range(P):
+            rows = slice(pos * S, pos * S + S)
+            case.keep[0].copy_(to_dev(cond[rows], dev))
+            case.keep[1].copy_(to_dev(uncond[rows], dev))
+            bits = peek_bits(oracle, 7, S * pos, S)
+            bits_t.copy_(torch.tensor(bits.view(np.int64), device=dev))
+            want = case.two_launch(hip, bits=bits, temperature=0.9)  # eager, on the same inputs
+            for t in o.values():
+                t.fill_(-5)
+            graph.replay()
+            torch.cuda.synchronize()
+            got = {k: from_dev(v) for k, v in o.items()}
+            print(f"{name}, position {pos}: tokens {got['tokens'].tolist()}")
+            same_outputs(got, want, case, draws=True)
