@@ -308,11 +308,15 @@ int launch_norm(const void * xv, const void * dv, const void * wv, const void * 
                      (b == nullptr || aligned16(b)) && (h == nullptr || aligned16(h)) && aligned16(y) &&
                      dim <= 64 * 4 * kVec * 4;
     if (vec) {
-        // Many rows: one wave per row up to 2048 elements (two or four waves
-        // for longer rows), four rows per workgroup. A few rows (decode): four
-        // waves per row, so each lane's share and chain stay short.
+        // Many rows: one wave per row up to 1536 elements, four rows per
+        // workgroup; a row of 1537-2048 elements over four waves (one group
+        // of 8 per lane: at 756 x 2048 RMS 4.18 -> 3.85 us and LayerNorm
+        // 4.77 -> 4.39 us against one wave per row; at 1536 elements four
+        // waves leave a quarter of the lanes idle and gain nothing); two or
+        // four waves for longer rows. A few rows (decode): four waves per
+        // row, so each lane's share and chain stay short.
         const int groups = static_cast<int>(ceil_div(dim, 64 * kVec));
-        const int wpr = rows < 512 ? 4 : groups <= 4 ? 1 : groups <= 8 ? 2 : 4;
+        const int wpr = rows < 512 ? 4 : groups <= 3 ? 1 : groups == 4 ? 4 : groups <= 8 ? 2 : 4;
         const int nv = static_cast<int>(ceil_div(groups, wpr));
         const hipStream_t s = stream;
         const uint32_t grid_w = static_cast<uint32_t>(ceil_div(rows, 4 / wpr));
