@@ -180,6 +180,46 @@ __global__ __launch_bounds__(kThreads) void f16_to_f32_vec4(const uint16_t * __r
     }
 }
 
+// Widening, 8 G values per lane: each lane requests G dwordx4 of 8 halves (a
+// wave's 512 G halves, G KiB, in G instructions); the wave's block goes
+// through its own G KiB of LDS so that each of its 2 G dwordx4 stores covers
+// one contiguous KiB of floats (lane l stores floats 4 l .. 4 l + 3 of each
+// quarter-KiB of halves). G = 2: 6.7 us for 4096 x 1536 values, 0.98 of the
+// streaming ceiling (G = 1 7.8 us; four values per lane with dwordx2 loads,
+// the form for 8-byte aligned sources, 8.6 us).
+template <int G>
+__global__ __launch_bounds__(kThreads) void f16_to_f32_x8(const uint16_t * __restrict__ x, float * y, int64_t n8) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kThreads / 64][256 * G];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * 64 * G;  // the wave's first group
+    u32x4 v[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int64_t g = base + 64 * k + lane;
+        v[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(x) + (g < n8 ? g : n8 - 1));
+    }
+    uint32_t * st = stage[wave];
+#pragma unroll
+    for (int k = 0; k < G; ++k) reinterpret_cast<u32x4 *>(st)[64 * k + lane] = v[k];
+    // one wave's LDS operations complete in issue order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int h = 0; h < 2 * G; ++h) {
+        const u32x2 w = reinterpret_cast<const u32x2 *>(st)[64 * h + lane];  // halves 256 h + 4 lane ..
+        if (base + 32 * h + (lane >> 1) >= n8) continue;
+        f32x4 a;
+        a[0] = h2f(static_cast<uint16_t>(w[0] & 0xffffu));
+        a[1] = h2f(static_cast<uint16_t>(w[0] >> 16));
+        a[2] = h2f(static_cast<uint16_t>(w[1] & 0xffffu));
+        a[3] = h2f(static_cast<uint16_t>(w[1] >> 16));
+        __builtin_nontemporal_store(a, reinterpret_cast<f32x4 *>(y) + 2 * base + 64 * h + lane);
+    }
+}
+
 }  // namespace
 }  // namespace levo_hip
 
@@ -300,7 +340,12 @@ extern "C" int levo_hip_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t 
     if (n == 0) return LEVO_HIP_OK;
     LEVO_REQUIRE(x != nullptr && y != nullptr, "fp16_to_fp32_row: null pointer");
     int64_t head = 0;
-    if ((reinterpret_cast<uintptr_t>(x) & 7u) == 0 && aligned16(y)) {
+    if (aligned16(x) && aligned16(y)) {
+        const int64_t n8 = n / 8;
+        if (n8 > 0) f16_to_f32_x8<2><<<ceil_div(n8, 2 * kThreads), kThreads, 0, as_hip(stream)>>>(x, y, n8);
+        head = n8 * 8;
+    }
+    if (head == 0 && (reinterpret_cast<uintptr_t>(x) & 7u) == 0 && aligned16(y)) {
         const int64_t n4 = n / 4;
         if (n4 > 0) f16_to_f32_vec4<<<ceil_div(n4, kThreads * kWidenPer), kThreads, 0, as_hip(stream)>>>(x, y, n4);
         head = n4 * 4;
