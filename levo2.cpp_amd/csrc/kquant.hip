@@ -523,7 +523,16 @@ int launch_mul_mat_u(kq_params p, hipStream_t st) {
 template <int TYPE>
 int launch_mul_mat(const kq_params & p, hipStream_t st) {
     const int units = p.nb * 8;
-    if (units <= 64) return launch_mul_mat_u<TYPE, 16, 4, 8>(p, st);
+    if (units <= 64) {
+        // K <= 2048: the fewest lanes per row (the most rows per workgroup,
+        // each workgroup staging the activations once) that still give 256
+        // workgroups or more: 16 rows per workgroup from 4096 rows, 8 from
+        // 2048, else 4 (1536 x 1536 Q4_K 4.69 -> 3.68 us, Q6_K 5.29 -> 3.99;
+        // at 8960 and 16385 rows 16 lanes per row stay fastest)
+        if (p.rows >= 4096) return launch_mul_mat_u<TYPE, 16, 4, 8>(p, st);
+        if (p.rows >= 2048) return launch_mul_mat_u<TYPE, 32, 2, 4>(p, st);
+        return launch_mul_mat_u<TYPE, 64, 1, 2>(p, st);
+    }
     if (units <= 128) return launch_mul_mat_u<TYPE, 16, 8, 16>(p, st);
     if (units <= 256) return launch_mul_mat_u<TYPE, 32, 8, 16>(p, st);
     // K > 8192 (LeLM's ffn_down, K = 8960): a row over two waves, each half
