@@ -210,8 +210,11 @@ __device__ __forceinline__ void load_row(float (&v)[VEC * NCH], row_stats & st, 
 // Shared-memory layout of one row's workgroup.
 template <int kWords>
 struct row_lds {
-    uint32_t sel[kWords];     // selected-id bitmap
-    uint32_t prefix[kWords];  // exclusive popcount prefix per bitmap word
+    // the bitmap and its prefix padded to a whole number of words per lane,
+    // so that one wave reads and writes them without a branch per word
+    static constexpr int kPadWords = (kWords + 63) / 64 * 64;
+    uint32_t sel[kPadWords];     // selected-id bitmap
+    uint32_t prefix[kPadWords];  // exclusive popcount prefix per bitmap word
     uint32_t pen[kWords];     // repetition-penalty ids
     uint32_t ign[kWords];     // ignored ids (stream 0)
     float cv[kWaves][kSegCap];  // gathered candidate values, one segment per wave
@@ -304,23 +307,28 @@ __device__ __forceinline__ uint32_t radix_kth_key(uint32_t * hist, const uint32_
 // fences keep its LDS accesses in program order around the cross-lane reads.
 template <int kWords>
 __device__ __forceinline__ int wave_bitmap_prefix(row_lds<kWords> & L, int words) {
-    constexpr int kWPL = (kWords + 63) / 64;  // words per lane
+    constexpr int kWPL = row_lds<kWords>::kPadWords / 64;  // words per lane
     const int lane = threadIdx.x & 63;
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    // Every word of the padded bitmap is read and every prefix word written
+    // with no branch around them, so the reads are issued together and waited
+    // for once (a read under a per-word condition waits for each in turn);
+    // words from `words` on (not cleared) count as empty.
+    uint32_t bits[kWPL];
+#pragma unroll
+    for (int j = 0; j < kWPL; ++j) bits[j] = L.sel[lane * kWPL + j];
     int cnt[kWPL];
     int local = 0;
 #pragma unroll
     for (int j = 0; j < kWPL; ++j) {
-        const int w = lane * kWPL + j;
-        cnt[j] = w < words ? __popc(L.sel[w]) : 0;
+        cnt[j] = lane * kWPL + j < words ? __popc(bits[j]) : 0;
         local += cnt[j];
     }
     const int incl = wave_inclusive_scan_i32(local);
     int run = incl - local;
 #pragma unroll
     for (int j = 0; j < kWPL; ++j) {
-        const int w = lane * kWPL + j;
-        if (w < words) L.prefix[w] = static_cast<uint32_t>(run);
+        L.prefix[lane * kWPL + j] = static_cast<uint32_t>(run);
         run += cnt[j];
     }
     const int total = dpp::lane(incl, 63);
@@ -728,9 +736,13 @@ __global__ __launch_bounds__(kThreads, VEC * NCH <= 36 ? 7 : 4) void cfg_sample_
     const int total = wave_bitmap_prefix(L, words);
 
     // ---- write the candidates in ascending id order --------------------------------
+    // every slot's lookup is read (id 0 for slots not taken), then waited for once
+    int slot[kSlots];
+#pragma unroll
+    for (int s = 0; s < kSlots; ++s) slot[s] = slot_of(L, take[s] ? cidx[s] : 0);
 #pragma unroll
     for (int s = 0; s < kSlots; ++s) {
-        const int pos = take[s] ? slot_of(L, cidx[s]) : a.capacity;
+        const int pos = take[s] ? slot[s] : a.capacity;
         if (pos < a.capacity) {
             const int64_t o = row * a.capacity + pos;
             a.cand_ids[o] = cidx[s];
@@ -1051,12 +1063,14 @@ __global__ __launch_bounds__(kThreads) void step_segment_kernel(const levo_hip_s
         const int total = wave_bitmap_prefix(L, kStepSegWords);
         if (total <= kStepCandCap) {
             count = total;
+            int slot[kSlots];  // every lookup issued, then waited for once
+#pragma unroll
+            for (int s = 0; s < kSlots; ++s) slot[s] = slot_of(L, take[s] ? cidx[s] - lo : 0);
 #pragma unroll
             for (int s = 0; s < kSlots; ++s) {
                 if (take[s]) {
-                    const int pos = slot_of(L, cidx[s] - lo);
-                    out.val[pos] = cval[s];
-                    out.id[pos] = cidx[s];
+                    out.val[slot[s]] = cval[s];
+                    out.id[slot[s]] = cidx[s];
                 }
             }
         }
