@@ -75,20 +75,37 @@ __device__ __forceinline__ float float_of_key(uint32_t k) {
 }
 
 // k-th largest (1 <= k <= 64) of the 64 lane keys of this wave; 0 when fewer
-// than k lanes hold a non-zero key. The answer lies between the smallest
-// non-zero key and the largest, so the bisection starts below their common
-// high bits (about 24 steps instead of 32 for logits of one magnitude).
+// than k lanes hold a non-zero key. A bisection from the top bit, unrolled
+// without branches: each step is one compare, one ballot popcount and one
+// scalar select, so the 32 steps cost less than the dependent reductions a
+// narrower starting range would need.
 __device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, int k) {
     if (static_cast<int>(__popcll(__ballot(key != 0u))) < k) return 0u;
-    const uint32_t hi = dpp::allreduce(key, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
-    const uint32_t lo = dpp::allreduce(key == 0u ? ~0u : key, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
-    const uint32_t diff = lo ^ hi;
-    if (diff == 0u) return lo;
-    const int top = 31 - __builtin_clz(diff);
-    uint32_t prefix = lo & ~((2u << top) - 1u);
-    for (int bit = top; bit >= 0; --bit) {
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = prefix | (1u << bit);
-        if (static_cast<int>(__popcll(__ballot(key >= cand))) >= k) prefix = cand;
+        prefix = static_cast<int>(__popcll(__ballot(key >= cand))) >= k ? cand : prefix;
+    }
+    return prefix;
+}
+
+// The same over NS keys per lane (invalid keys 0): the largest t with at least
+// k keys >= t, or 0 when fewer than k keys are non-zero.
+template <int NS>
+__device__ __forceinline__ uint32_t wave_kth_key_slots(const uint32_t (&key)[NS], int k) {
+    int nz = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) nz += static_cast<int>(__popcll(__ballot(key[s] != 0u)));
+    if (nz < k) return 0u;
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = prefix | (1u << bit);
+        int c = 0;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) c += static_cast<int>(__popcll(__ballot(key[s] >= cand)));
+        prefix = c >= k ? cand : prefix;
     }
     return prefix;
 }
@@ -766,102 +783,133 @@ int launch_sample(const levo_hip_sample_args & a, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------
 // Decode-step sampling in two launches (levo_hip_sample_step).
 //
-// A decode step samples a handful of rows. One workgroup per row pulls each
-// row (two 16385-logit inputs under CFG: 131 KB) through one CU, at that CU's
-// share of the HBM bandwidth: about 5 us before any selection starts. Here
-// every row is split into segments of 4096 ids:
-//   1. segment launch, one 512-thread workgroup per (row, segment), 8 ids per
-//      thread: loads, CFG, the repetition penalty and the ignore list (the
-//      list ids inside the segment); the segment's maximum, first maximum,
-//      NaN flag and softmax sum; and the segment's own top-k candidate set,
-//      found as the row kernel finds a row's (gather above a per-wave bound,
-//      the exact k-th key by a one-wave radix select, ties kept), written to
-//      the workspace in ascending id order with the segment's head. The
-//      row's k-th largest value is at least every segment's k-th largest, so
-//      the union of the segment sets holds every candidate of the row.
-//   2. merge launch, one wave per row, 8 rows per workgroup: the row's
-//      maximum, first maximum and log-sum-exp from the heads; its k-th key by
-//      a radix select over the handed-over candidates (at most 64 per
-//      segment, read with the heads in one round trip); and the candidates
-//      at or above it, whose ascending id order is the segments' order and
-//      each list's own. When every row fits one workgroup it then makes
-//      every row's draw, as levo_hip_sample_draw does, after a workgroup
-//      barrier; with more rows the draw is a third launch.
-// No workgroup waits for another. A row that does not fit (k = 0, k > 512,
-// more than 64 candidates in a segment, as with heavy ties) takes
-// select_general over the whole row in the merge launch.
-constexpr int kStepPer = 8;                       // ids per thread
-constexpr int kStepSegIds = kThreads * kStepPer;  // ids per segment
-constexpr int kStepSegWords = kStepSegIds / 32;   // bitmap words of a segment
-constexpr int kStepCandCap = 256;                 // candidate slots of a segment in the workspace
-constexpr int kStepHandCap = 64;                  // candidates per segment the merging wave reads
-constexpr int kStepWords = kMaxVocab / 32;        // bitmap words of the longest row
-constexpr int kStepMaxSegs = kMaxVocab / kStepSegIds;
+// A decode step samples a handful of rows of ~16K logits. Through one
+// workgroup per row, a row's 131 KB (cond and uncond) arrive at the miss
+// concurrency of one CU, several microseconds, and every selection phase
+// then runs at one wave's serial latency. Here the loads are spread over many
+// CUs and the row's exact selection runs once:
+//   1. part launch, one wave per 512 ids of a row: the list ids first (the
+//      repetition penalty and the ignore list enter LDS bitmaps of the
+//      part), then the logits, CFG; the part's NaN flag, maximum, first
+//      maximum and softmax sum; and a bound, the G-th largest of the 64 lane
+//      maxima, so that at least G ids lie at or above it. Every id at or
+//      above the bound is handed to the workspace (value and id, ascending
+//      ids) with the part's head.
+//   2. join launch, one workgroup per row, whose first wave reads every
+//      part's head and handed-over ids in one round trip. Let L be the
+//      largest part bound. The row's k-th largest value (the stable sort's
+//      threshold, :84-89) is found among the handed-over ids at or above L,
+//      the survivors, whenever there are at least k of them: if t is the k-th
+//      largest survivor, t >= L, and a row id at or above t is at or above
+//      its own part's bound, so it was handed over and survived; the row then
+//      holds exactly the survivors' ids at or above t, and t is the row's
+//      k-th largest. A radix select over the survivors gives t; the
+//      candidates at or above it are written in ascending id order, followed
+//      by the draw of levo_hip_sample_draw when the rows are few.
+// G = min(k, 64, ceil(3 k * 512 / V) + 6): three times the candidates a part
+// holds on average, plus six. With G >= k every part hands over at least its
+// own top k and the survivors always suffice; LeVo's k = 50 over 16385 ids
+// takes G = 11, and in simulations of Gaussian rows no row fell short.
+// A row with fewer than k survivors or more than the joining wave holds, a
+// part with more than kPartCap ids at or above its bound (heavy ties), or
+// k = 0 takes select_general over the whole row in the join launch.
+constexpr int kPartIds = 512;                          // ids per part (one wave)
+constexpr int kPartPer = kPartIds / 64;                // ids per lane
+constexpr int kPartCap = 32;                           // handed-over ids per part
+constexpr int kMaxParts = kMaxVocab / kPartIds;        // parts of the longest row
+constexpr int kJoinCap = 256;                          // survivors the joining wave selects from
+constexpr int kJoinDrawRows = 8;                       // rows whose draws the join launch makes
+constexpr int kEarlyChunks = (kJoinDrawRows - 1) * kMaxParts / 64;  // earlier rows' heads, 64 per chunk
+constexpr int kStepWords = kMaxVocab / 32;             // bitmap words of the longest row
+constexpr int64_t kStepMaxRows = 4095;
+constexpr int32_t kPartOverflow = -1;
+constexpr int32_t kPartNaN = -2;
 
-struct step_head {
-    float max;      // segment maximum (NaN skipped)
-    float bv;       // value at its first maximum
-    int32_t best;   // first id holding the maximum
-    int32_t nan;    // the segment holds a NaN
-    uint32_t tau;   // key of the segment's k-th largest value (0: fewer than k ids)
-    int32_t count;  // candidates handed over in ascending id order; -1: none (general path)
-    float sum;      // sum over the segment of exp((l - max) / T)
-    int32_t pad;
+struct alignas(16) part_head {
+    float max;       // value at the part's first maximum (NaN skipped)
+    int32_t best;    // the part's first id holding its maximum
+    uint32_t bound;  // key of the part's bound (0: every id of the part handed over)
+    int32_t count;   // ids handed over, or kPartOverflow / kPartNaN
 };
 
-struct step_seg {
-    step_head h;
-    float val[kStepCandCap];
-    int32_t id[kStepCandCap];
+struct alignas(8) part_cand {
+    float v;
+    int32_t id;
 };
 
-// The workspace starts with a reserved region of fixed size, the same for
-// every row count and vocabulary; the segment records follow.
-constexpr int kStepCounters = 4096;
-constexpr int64_t kStepCounterBytes = kStepCounters * 4;
-constexpr int64_t kStepMaxRows = kStepCounters - 1;
+// The workspace: every (row, part) head, then the softmax sums, then the
+// handed-over ids, kPartCap slots per part.
+struct step_ws {
+    part_head * heads;
+    float * sums;
+    part_cand * cands;
+};
 
-// Id of item q of thread tid in a segment starting at lo: dwordx4 chunks of
-// 4 ids per thread (VEC 4) or single ids kThreads apart (VEC 1); coalesced
-// either way.
+int64_t step_parts(int64_t vocab) { return (vocab + kPartIds - 1) / kPartIds; }
+
+int64_t step_workspace_bytes(int64_t rows, int64_t vocab) {
+    const int64_t n = rows * step_parts(vocab);
+    return n * static_cast<int64_t>(sizeof(part_head)) + (n * 4 + 15) / 16 * 16 +
+           n * kPartCap * static_cast<int64_t>(sizeof(part_cand));
+}
+
+step_ws carve_step_ws(void * ws, int64_t rows, int64_t vocab) {
+    const int64_t n = rows * step_parts(vocab);
+    uint8_t * p = static_cast<uint8_t *>(ws);
+    step_ws w;
+    w.heads = reinterpret_cast<part_head *>(p);
+    p += n * static_cast<int64_t>(sizeof(part_head));
+    w.sums = reinterpret_cast<float *>(p);
+    p += (n * 4 + 15) / 16 * 16;
+    w.cands = reinterpret_cast<part_cand *>(p);
+    return w;
+}
+
+// Lane maxima at or above a part's bound (see above).
+__device__ __forceinline__ int part_groups(int k, int V) {
+    const int g = (3 * k * kPartIds + V - 1) / V + 6;
+    const int m = g < k ? g : k;
+    return m < 64 ? m : 64;
+}
+
+// Id of item q of a lane in the part starting at lo, ascending in (q, lane)
+// for VEC 1 (64 consecutive ids per item) and in (q / 4, lane, q % 4) for
+// VEC 4 (two chunks of 256, four consecutive ids per lane).
 template <int VEC>
-__device__ __forceinline__ int step_id(int lo, int tid, int q) {
-    return VEC == 4 ? lo + (q / 4) * kThreads * 4 + tid * 4 + (q % 4) : lo + tid + kThreads * q;
+__device__ __forceinline__ int part_item_id(int lo, int lane, int q) {
+    return VEC == 4 ? lo + (q >> 2) * 256 + lane * 4 + (q & 3) : lo + q * 64 + lane;
 }
 
 template <int VEC>
-__global__ __launch_bounds__(kThreads) void step_segment_kernel(const levo_hip_sample_args a, uint8_t * ws, int segs) {
-    __shared__ row_lds<kStepSegWords> L;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int64_t row = blockIdx.x / segs;
-    const int seg = static_cast<int>(blockIdx.x % segs);
+__global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_args a, const step_ws w, int parts) {
+    __shared__ uint32_t pen_map[kPartIds / 32];
+    __shared__ uint32_t ign_map[kPartIds / 32];
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x / static_cast<uint32_t>(parts);
+    const int part = static_cast<int>(blockIdx.x % static_cast<uint32_t>(parts));
     const int V = static_cast<int>(a.vocab);
-    const int lo = seg * kStepSegIds;
-    const int hi = lo + kStepSegIds < V ? lo + kStepSegIds : V;
+    const int lo = part * kPartIds;
+    const int hi = lo + kPartIds < V ? lo + kPartIds : V;
     const int stream = static_cast<int>(row % a.n_streams);
     int k = a.top_k[stream];
-    if (k <= 0 || k >= V) k = 0;  // keep every id
-    const int kw = (k + kWaves - 1) / kWaves;
-    step_seg & out = reinterpret_cast<step_seg *>(ws + kStepCounterBytes)[row * segs + seg];
+    if (k <= 0 || k >= V) k = 0;  // keep every id: the general path
+    const int64_t rp = row * parts + part;
 
-    // ---- 1. loads, CFG, penalty, ignore list, reductions ------------------------------
-    // the list entries first (see list_entry), then the segment's logits
+    // ---- the list entries first (see list_entry), then the part's logits ----------------
     const bool use_pen = a.recent != nullptr && a.n_recent > 0;
     const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
     const int n_pen = use_pen ? a.n_recent : 0;
     const int n_ign = use_ign ? a.n_ignore : 0;
     const int64_t * rec = use_pen ? a.recent + row * a.n_recent : &kNoListEntry;
     const int64_t * ign = use_ign ? a.ignore : &kNoListEntry;
-    const int64_t entry = list_entry(rec, n_pen, ign, n_ign, tid);
+    const int64_t entry = list_entry(rec, n_pen, ign, n_ign, lane);
     const float * crow = a.cond + row * a.row_pitch;
     const float * urow = a.uncond ? a.uncond + row * a.row_pitch : nullptr;
-    float c[kStepPer], u[kStepPer];
+    float c[kPartPer], u[kPartPer];
     if constexpr (VEC == 4) {
 #pragma unroll
-        for (int ch = 0; ch < kStepPer / 4; ++ch) {
-            const int base = step_id<VEC>(lo, tid, ch * 4);
+        for (int ch = 0; ch < kPartPer / 4; ++ch) {
+            const int base = part_item_id<VEC>(lo, lane, ch * 4);
             const int off = base < V ? base : lo;  // row_pitch % 4 == 0: in bounds
             const f32x4 cv = *reinterpret_cast<const f32x4 *>(crow + off);
             const f32x4 uv = urow ? *reinterpret_cast<const f32x4 *>(urow + off) : cv;
@@ -870,269 +918,232 @@ __global__ __launch_bounds__(kThreads) void step_segment_kernel(const levo_hip_s
         }
     } else {
 #pragma unroll
-        for (int q = 0; q < kStepPer; ++q) {
-            const int id = step_id<VEC>(lo, tid, q);
+        for (int q = 0; q < kPartPer; ++q) {
+            const int id = part_item_id<VEC>(lo, lane, q);
             const int off = id < V ? id : lo;
             c[q] = crow[off];
             u[q] = urow ? urow[off] : c[q];
         }
     }
-    if (tid < kStepSegWords) L.sel[tid] = 0u;
 
-    // Penalty and ignore ids inside this segment, as bitmaps of its 4096 ids
-    // (128 words each).
+    // Penalty and ignore ids inside this part, as bitmaps of its 512 ids.
     int pen = 0, ign_bits = 0;  // item bits
     if (use_pen || use_ign) {
-        if (tid < kStepSegIds / 32) {
-            L.pen[tid] = 0u;
-            L.ign[tid] = 0u;
+        if (lane < kPartIds / 32) {
+            pen_map[lane] = 0u;
+            ign_map[lane] = 0u;
         }
-        __syncthreads();
+        wave_lds_order();
         const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
         const int64_t top = hi < limit ? hi : limit;
-        for (int i = tid; i < n_pen + n_ign; i += kThreads) {
-            const int64_t t = i < kThreads ? entry : list_entry(rec, n_pen, ign, n_ign, i);
+        for (int i = lane; i < n_pen + n_ign; i += 64) {
+            const int64_t t = i < 64 ? entry : list_entry(rec, n_pen, ign, n_ign, i);
             if (i < n_pen) {
-                if (t >= lo && t < top) atomicOr(&L.pen[(t - lo) >> 5], 1u << ((t - lo) & 31));
+                if (t >= lo && t < top) atomicOr(&pen_map[(t - lo) >> 5], 1u << ((t - lo) & 31));
             } else {
-                if (t >= lo && t < hi) atomicOr(&L.ign[(t - lo) >> 5], 1u << ((t - lo) & 31));
+                if (t >= lo && t < hi) atomicOr(&ign_map[(t - lo) >> 5], 1u << ((t - lo) & 31));
             }
         }
-        __syncthreads();
+        wave_lds_order();
 #pragma unroll
-        for (int q = 0; q < kStepPer; ++q) {
-            const int rel = step_id<VEC>(lo, tid, q) - lo;
-            pen |= (L.pen[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
-            ign_bits |= (L.ign[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
+        for (int q = 0; q < kPartPer; ++q) {
+            const int rel = part_item_id<VEC>(lo, lane, q) - lo;
+            pen |= (pen_map[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
+            ign_bits |= (ign_map[rel >> 5] >> (rel & 31)) & 1u ? 1 << q : 0;
         }
     }
-    float v[kStepPer];
+    float v[kPartPer];
     bool has_nan = false;
     float tmax = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < kStepPer; ++q) {
+    for (int q = 0; q < kPartPer; ++q) {
         float x = urow ? u[q] + a.cfg_scale * (c[q] - u[q]) : c[q];
         if (pen & (1 << q)) x = x / a.repetition_penalty;
         if (ign_bits & (1 << q)) x = -INFINITY;
-        v[q] = step_id<VEC>(lo, tid, q) < hi ? x : -INFINITY;
+        v[q] = part_item_id<VEC>(lo, lane, q) < hi ? x : -INFINITY;
         has_nan = has_nan || __builtin_isnan(v[q]);
         tmax = fmaxf(tmax, v[q]);
     }
-    const bool tvalid = step_id<VEC>(lo, tid, 0) < hi;
 
-    // ---- 2. segment reductions and the per-wave bound of the k-th value -------------------
-    const float wm = wave_max_f32(tmax);
-    const bool wnan = __ballot(has_nan) != 0;
-    float wlow = -INFINITY;
-    if (k > 1 && kw <= 64) {
-        const uint32_t kk = wave_kth_key(tvalid ? float_key(tmax) : 0u, kw);
-        wlow = kk == 0u ? -INFINITY : float_of_key(kk);
-    }
-    if (lane == 0) {
-        L.wmax[wave] = wm;
-        L.wlow[wave] = wlow;
-        L.wnan[wave] = wnan ? 1 : 0;
-    }
-    __syncthreads();
-    float m = L.wmax[0];
-    float low = L.wlow[0];
-    bool seg_nan = L.wnan[0] != 0;
+    // ---- maximum, first maximum, bound --------------------------------------------------
+    const bool part_nan = __ballot(has_nan) != 0;
+    const float m = wave_max_f32(tmax);
+    int best = INT_MAX;
+    float bv = m;
+    if constexpr (VEC == 4) {
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-        m = fmaxf(m, L.wmax[w]);
-        low = fminf(low, L.wlow[w]);
-        seg_nan = seg_nan || L.wnan[w] != 0;
-    }
-    if (k == 1) low = m;
-    int tbest = INT_MAX;
-    float tbest_v = m;
+        for (int ch = 0; ch < kPartPer / 4; ++ch) {
+            int fe = 4;
+            float fv = m;
 #pragma unroll
-    for (int q = 0; q < kStepPer; ++q) {
-        const int id = step_id<VEC>(lo, tid, q);
-        if (id < hi && v[q] == m && id < tbest) {
-            tbest = id;
-            tbest_v = v[q];
-        }
-    }
-    const int my_best = tbest;
-    tbest = wave_min_i32(tbest);
-    if (lane == 0) L.wbest[wave] = tbest;
-    if (my_best == tbest && my_best != INT_MAX) L.wbv[wave] = tbest_v;
-    if (a.row_lse) {
-        const float inv_t = 1.0f / a.temperature;
-        const float mm = fmaxf(m, -FLT_MAX);
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < kStepPer; ++q) s += __expf((v[q] - mm) * inv_t);  // -inf and padding add 0
-        s = wave_sum_f32(s);
-        if (lane == 0) L.wlse[wave] = s;
-    }
-    // gather the ids >= low (k >= 1), padding excluded, into the wave's
-    // kSegCap slots; a longer count only marks the segment as not fitting
-    const bool gather = k >= 1 && kw <= 64 && !seg_nan;
-    if (gather) {
-        int base = 0;
-#pragma unroll
-        for (int q = 0; q < kStepPer; ++q) {
-            const int id = step_id<VEC>(lo, tid, q);
-            const bool p = id < hi && v[q] >= low;
-            const uint64_t mask = __ballot(p);
-            if (mask) {
-                const int pos = base + rank_in_mask(mask);
-                if (p && pos < kSegCap) {
-                    L.cv[wave][pos] = v[q];
-                    L.ci[wave][pos] = id;
+            for (int e = 3; e >= 0; --e) {
+                const int q = ch * 4 + e;
+                if (part_item_id<VEC>(lo, lane, q) < hi && v[q] == m) {
+                    fe = e;
+                    fv = v[q];
                 }
-                base += static_cast<int>(__popcll(mask));
+            }
+            const uint64_t mask = __ballot(fe < 4);
+            if (mask != 0 && best == INT_MAX) {
+                const int l = __builtin_ctzll(mask);
+                best = lo + ch * 256 + l * 4 + __builtin_amdgcn_readlane(fe, l);
+                bv = dpp::lane(fv, l);
             }
         }
-        if (lane == 0) L.wcnt[wave] = base;
-    }
-    __syncthreads();
-    if (wave != 0) return;
-
-    // ---- 3. wave 0: the segment's exact k-th key and its candidates in id order ------------
-    int best = L.wbest[0], bw = 0;
+    } else {
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) {
-        if (L.wbest[w] < best) {
-            best = L.wbest[w];
-            bw = w;
+        for (int q = 0; q < kPartPer; ++q) {
+            const uint64_t mask = __ballot(part_item_id<VEC>(lo, lane, q) < hi && v[q] == m);
+            if (mask != 0 && best == INT_MAX) {
+                const int l = __builtin_ctzll(mask);
+                best = lo + q * 64 + l;
+                bv = dpp::lane(v[q], l);
+            }
+        }
+    }
+    uint32_t bkey = 0u;
+    if (k == 1) {
+        bkey = float_key(m);  // the ties of the maximum
+    } else if (k > 1 && !part_nan) {
+        const bool lane_valid = part_item_id<VEC>(lo, lane, 0) < hi;
+        bkey = wave_kth_key(lane_valid ? float_key(tmax) : 0u, part_groups(k, V));
+    }
+
+    // ---- hand over every id at or above the bound, ascending ---------------------------
+    int32_t count;
+    if (part_nan) {
+        count = kPartNaN;
+    } else if (k == 0) {
+        count = kPartOverflow;
+    } else {
+        bool take[kPartPer];
+        int pos[kPartPer];
+        int total = 0;
+#pragma unroll
+        for (int q = 0; q < kPartPer; ++q) take[q] = part_item_id<VEC>(lo, lane, q) < hi && float_key(v[q]) >= bkey;
+        if constexpr (VEC == 4) {
+#pragma unroll
+            for (int ch = 0; ch < kPartPer / 4; ++ch) {
+                // (lane, e) order: the takes of lower lanes, then this lane's lower e
+                int below = 0, in_chunk = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint64_t mask = __ballot(take[ch * 4 + e]);
+                    below += rank_in_mask(mask);
+                    in_chunk += static_cast<int>(__popcll(mask));
+                }
+                int run = total + below;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    pos[ch * 4 + e] = run;
+                    run += take[ch * 4 + e] ? 1 : 0;
+                }
+                total += in_chunk;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < kPartPer; ++q) {
+                const uint64_t mask = __ballot(take[q]);
+                pos[q] = total + rank_in_mask(mask);
+                total += static_cast<int>(__popcll(mask));
+            }
+        }
+        count = total <= kPartCap ? total : kPartOverflow;
+        if (total <= kPartCap) {
+            part_cand * out = w.cands + rp * kPartCap;
+#pragma unroll
+            for (int q = 0; q < kPartPer; ++q)
+                if (take[q]) out[pos[q]] = part_cand{v[q], part_item_id<VEC>(lo, lane, q)};
         }
     }
     float sum = 0.0f;
-    if (a.row_lse) {
-        sum = L.wlse[0];
+    if (a.row_lse && !part_nan) {
+        const float inv_t = 1.0f / a.temperature;
+        const float mm = fmaxf(m, -FLT_MAX);
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) sum += L.wlse[w];
-    }
-    int seg_start[kWaves + 1];
-    seg_start[0] = 0;
-    bool fits = gather;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-        const int c = fits ? L.wcnt[w] : 0;
-        fits = fits && c <= kSegCap;
-        seg_start[w + 1] = seg_start[w] + c;
-    }
-    const int ncand = seg_start[kWaves];
-    fits = fits && ncand <= kBisCap;
-    int count = -1;
-    uint32_t tau = 0u;
-    if (fits) {  // uniform
-        constexpr int kSlots = kBisCap / 64;
-        float cval[kSlots];
-        int cidx[kSlots];
-        uint32_t keys[kSlots];
-        bool valid[kSlots];
-        const float * cv = &L.cv[0][0];
-        const int * ci = &L.ci[0][0];
-        int flat[kSlots];
-#pragma unroll
-        for (int s = 0; s < kSlots; ++s) {
-            const int j = lane + 64 * s;
-            int delta = -seg_start[0];
-#pragma unroll
-            for (int q = 1; q < kWaves; ++q) delta = j >= seg_start[q] ? q * kSegCap - seg_start[q] : delta;
-            valid[s] = j < ncand;
-            flat[s] = valid[s] ? j + delta : 0;
-        }
-#pragma unroll
-        for (int s = 0; s < kSlots; ++s) {
-            cval[s] = cv[flat[s]];
-            cidx[s] = ci[flat[s]];
-        }
-#pragma unroll
-        for (int s = 0; s < kSlots; ++s) keys[s] = valid[s] ? float_key(cval[s]) : 0u;
-        if (k == 1) {
-            tau = float_key(m);
-        } else {
-            const uint32_t lo_key = low == -INFINITY ? 0u : float_key(low);
-            const uint32_t hi_key = float_key(m);
-            const uint32_t diff = lo_key ^ hi_key;
-            const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
-            const uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
-            tau = radix_kth_key<kSlots>(L.hist, keys, valid, k, prefix, top);
-        }
-        bool take[kSlots];
-#pragma unroll
-        for (int s = 0; s < kSlots; ++s) {
-            take[s] = valid[s] && keys[s] >= tau;
-            if (take[s]) atomicOr(&L.sel[(cidx[s] - lo) >> 5], 1u << ((cidx[s] - lo) & 31));
-        }
-        const int total = wave_bitmap_prefix(L, kStepSegWords);
-        if (total <= kStepCandCap) {
-            count = total;
-            int slot[kSlots];  // every lookup issued, then waited for once
-#pragma unroll
-            for (int s = 0; s < kSlots; ++s) slot[s] = slot_of(L, take[s] ? cidx[s] - lo : 0);
-#pragma unroll
-            for (int s = 0; s < kSlots; ++s) {
-                if (take[s]) {
-                    out.val[slot[s]] = cval[s];
-                    out.id[slot[s]] = cidx[s];
-                }
-            }
-        }
+        for (int q = 0; q < kPartPer; ++q) sum += __expf((v[q] - mm) * inv_t);  // -inf and padding add 0
+        sum = wave_sum_f32(sum);
     }
     if (lane == 0) {
-        step_head h;
-        h.max = m;
-        h.bv = best == INT_MAX ? m : L.wbv[bw];
-        h.best = best;
-        h.nan = seg_nan ? 1 : 0;
-        h.tau = tau;
-        h.count = count;
-        h.sum = sum;
-        h.pad = 0;
-        out.h = h;
+        w.heads[rp] = part_head{bv, best, bkey, count};
+        if (a.row_lse) w.sums[rp] = sum;
     }
 }
 
-struct merge_lds {
-    row_lds<kStepWords> L;                           // the general path
-    __attribute__((aligned(16))) uint32_t hist[kWaves][256];  // one radix-select histogram per wave
-    int slow[kWaves];                                // rows that take the general path
-    float rm[kWaves];
-    int best[kWaves];
-    float bv[kWaves];
-    float lse[kWaves];
+struct join_lds {
+    row_lds<kStepWords> L;                                   // the general path
+    float sv[kJoinCap];                                      // survivors, ascending ids: values
+    int32_t si[kJoinCap];                                    // and ids
+    float cv[kJoinCap];                                      // the row's candidates, ascending ids
+    int32_t ci[kJoinCap];
+    int slow;
+    float rm;
+    int best;
+    float bv;
+    float lse;
 };
 
-__global__ __launch_bounds__(kThreads) void step_merge_kernel(const levo_hip_sample_args a, const levo_hip_draw_args d,
-                                                               const uint8_t * ws, int segs) {
-    __shared__ merge_lds S;
+// Bits [lo, hi) of a 64-lane mask, the bounds clamped to [0, 64].
+__device__ __forceinline__ uint64_t lane_range(int lo, int hi) {
+    lo = lo < 0 ? 0 : lo > 64 ? 64 : lo;
+    hi = hi < 0 ? 0 : hi > 64 ? 64 : hi;
+    const uint64_t below_hi = hi == 64 ? ~uint64_t{0} : (uint64_t{1} << hi) - 1u;
+    const uint64_t below_lo = lo == 64 ? ~uint64_t{0} : (uint64_t{1} << lo) - 1u;
+    return below_hi & ~below_lo;
+}
+
+// NS: handed-over slots per lane of the joining wave, ceil(parts / 2); every
+// slot load is issued before the first is used.
+template <int NS>
+__global__ __launch_bounds__(kThreads) void step_join_kernel(const levo_hip_sample_args a, const levo_hip_draw_args d,
+                                                              const step_ws w, int parts) {
+    __shared__ join_lds S;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
-    const bool live = row < a.rows;  // uniform per wave
+    const int64_t row = blockIdx.x;
     const int V = static_cast<int>(a.vocab);
-    if (live) {
-        const int stream = static_cast<int>(row % a.n_streams);
-        int k = a.top_k[stream];
-        if (k <= 0 || k >= V) k = 0;
-        const int kw = (k + kWaves - 1) / kWaves;
-        const step_seg * segv = reinterpret_cast<const step_seg *>(ws + kStepCounterBytes) + row * segs;
-        // every load first: lane g < segs takes head g, and every lane the
-        // first kStepHandCap candidate slots of each segment
-        const step_head h = segv[lane < segs ? lane : 0].h;
-        float cval[kStepMaxSegs];
-        int cidx[kStepMaxSegs];
+    const int stream = static_cast<int>(row % a.n_streams);
+    int k = a.top_k[stream];
+    if (k <= 0 || k >= V) k = 0;
+    const bool drawing = d.tokens != nullptr;
+    const bool sampling = drawing && d.use_sampling != 0 && d.temperature != 0.0f;
+    int before = 0;            // draws taken by the rows before this one (wave 0)
+    uint64_t raw_at_r = 0;     // the raw value at the row index (wave 0)
+
+    if (wave == 0) {
+        // ---- every load first: the heads, the handed-over ids, the draw inputs ------------
+        const int64_t rp0 = row * parts;
+        const bool mine = lane < parts;
+        const part_head h = w.heads[rp0 + (mine ? lane : 0)];
+        const float hsum = a.row_lse != nullptr ? w.sums[rp0 + (mine ? lane : 0)] : 0.0f;
+        const int nslots = parts * kPartCap;
+        const part_cand * cand = w.cands + rp0 * kPartCap;
+        part_cand sl[NS];
 #pragma unroll
-        for (int s = 0; s < kStepMaxSegs; ++s) {
-            const int g = s < segs ? s : 0;
-            cval[s] = segv[g].val[lane];
-            cidx[s] = segv[g].id[lane];
+        for (int s = 0; s < NS; ++s) {
+            const int j = lane + 64 * s;
+            sl[s] = cand[j < nslots ? j : nslots - 1];
         }
-        const bool mine = lane < segs;
-        const bool row_nan = __ballot(mine && h.nan != 0) != 0;
+        if (sampling) raw_at_r = d.bits[row];
+        // the heads of the earlier rows (at most kJoinDrawRows - 1 of them)
+        const int nearly = sampling ? static_cast<int>(row) * parts : 0;
+        part_head eh[kEarlyChunks];
+#pragma unroll
+        for (int i = 0; i < kEarlyChunks; ++i) {
+            const int f = lane + 64 * i;
+            eh[i] = w.heads[f < nearly ? f : 0];
+        }
+
+        // ---- the row's maximum, first maximum, NaN flag and log-sum-exp ---------------------
+        const bool row_nan = __ballot(mine && h.count == kPartNaN) != 0;
+        const bool overflow = __ballot(mine && h.count == kPartOverflow) != 0;
         const float rm = wave_max_f32(mine ? h.max : -INFINITY);
-        // the first maximum lies in the first segment whose maximum is the row's
-        const uint64_t at_max = __ballot(mine && h.max == rm && h.best != INT_MAX);
-        const int bseg = at_max != 0 ? __builtin_ctzll(at_max) : 0;
-        const int best = at_max != 0 ? dpp::lane(h.best, bseg) : -1;
-        const float bv = dpp::lane(h.bv, bseg);
+        // the first maximum lies in the first part whose maximum is the row's
+        const uint64_t at_max = __ballot(mine && h.max == rm);
+        const int bpart = at_max != 0 ? __builtin_ctzll(at_max) : 0;
+        const int best = row_nan ? -1 : dpp::lane(h.best, bpart);
+        const float bv = dpp::lane(h.max, bpart);
         float lse = NAN;
         if (!row_nan && a.row_lse) {
             if (rm == -INFINITY) {
@@ -1141,148 +1152,207 @@ __global__ __launch_bounds__(kThreads) void step_merge_kernel(const levo_hip_sam
                 lse = INFINITY;
             } else {
                 const float inv_t = 1.0f / a.temperature;
-                float z = 0.0f;
-                for (int g = 0; g < segs; ++g)
-                    z += dpp::lane(h.sum, g) * __expf((fmaxf(dpp::lane(h.max, g), -FLT_MAX) - rm) * inv_t);
-                lse = rm / a.temperature + logf(z);
+                const float term = mine ? hsum * __expf((fmaxf(h.max, -FLT_MAX) - rm) * inv_t) : 0.0f;
+                lse = rm / a.temperature + logf(wave_sum_f32(term));
             }
         }
-        const bool counts_ok = __ballot(mine && (h.count < 0 || h.count > kStepHandCap)) == 0;
-        const bool fast = !row_nan && k >= 1 && kw <= 64 && counts_ok;
-        if (row_nan) {  // the reference throws "logits contain NaN"
-            if (lane == 0) {
-                a.best[row] = -1;
-                a.count[row] = -1;
-                if (a.row_max) a.row_max[row] = NAN;
-                if (a.row_lse) a.row_lse[row] = NAN;
-            }
-        } else if (fast) {
-            // The row's k-th key is at least every segment's (a segment with
-            // fewer than k ids reports 0): candidates below the largest of
-            // them cannot be selected and are left out, so the rest lie
-            // between it and the maximum's key.
-            const uint32_t lo_key =
-                k == 1 ? 0u : dpp::allreduce(mine ? h.tau : 0u, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
-            uint32_t keys[kStepMaxSegs];
-            bool valid[kStepMaxSegs];
+
+        // ---- survivors: handed-over ids at or above the largest part bound ------------------
+        const uint32_t hi_key = float_key(rm);
+        const uint32_t lo_key =
+            k == 1 ? hi_key : dpp::allreduce(mine ? h.bound : 0u, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+        bool fast = !row_nan && !overflow && k >= 1;
+        int nsurv = 0;
+        if (fast) {
+            // lo_key as a value (every lo_key is some value's key; 0 admits every
+            // handed-over id): a value is at or above it exactly when its key is
+            const float lo_v = lo_key == 0u ? -INFINITY : float_of_key(lo_key);
 #pragma unroll
-            for (int s = 0; s < kStepMaxSegs; ++s) {
-                const int c = s < segs ? dpp::lane(h.count, s) : 0;
-                keys[s] = float_key(cval[s]);
-                valid[s] = lane < c && keys[s] >= lo_key;
-                keys[s] = valid[s] ? keys[s] : 0u;
+            for (int s = 0; s < NS; ++s) {
+                // slot j = lane + 64 s is slot j % kPartCap of part j / kPartCap: part
+                // 2 s in lanes 0-31, 2 s + 1 in lanes 32-63, each with its count
+                const int c_lo = 2 * s < parts ? __builtin_amdgcn_readlane(h.count, 2 * s) : 0;
+                const int c_hi = 2 * s + 1 < parts ? __builtin_amdgcn_readlane(h.count, 2 * s + 1) : 0;
+                const uint64_t filled = (c_lo >= 32 ? 0xFFFFFFFFull : (uint64_t{1} << c_lo) - 1u) |
+                                        ((c_hi >= 32 ? 0xFFFFFFFFull : (uint64_t{1} << c_hi) - 1u) << 32);
+                const uint64_t mask = __ballot(sl[s].v >= lo_v) & filled;
+                const bool surv = (mask >> lane) & 1u;
+                const int p = nsurv + rank_in_mask(mask);
+                if (surv && p < kJoinCap) {
+                    S.sv[p] = sl[s].v;
+                    S.si[p] = sl[s].id;
+                }
+                nsurv += static_cast<int>(__popcll(mask));
             }
-            uint32_t tau;
-            if (k == 1) {
-                tau = float_key(rm);
-            } else {
-                // it shares the common high bits of lo_key and the maximum's key
-                const uint32_t hi_key = float_key(rm);
-                const uint32_t diff = lo_key ^ hi_key;
-                const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
-                const uint32_t prefix = top < 0 ? lo_key : (lo_key & ~((2u << top) - 1u));
-                tau = radix_kth_key<kStepMaxSegs>(S.hist[wave], keys, valid, k, prefix, top);
+            fast = nsurv >= k && nsurv <= kJoinCap;
+        }
+
+        // ---- the exact k-th value and the candidates at or above it, ascending ids ----------
+        int n = 0;
+        if (fast) {
+            wave_lds_order();
+            constexpr int kT = kJoinCap / 64;
+            uint32_t keys[kT];
+            bool valid[kT];
+            float cval[kT];
+            int32_t cid[kT];
+#pragma unroll
+            for (int t = 0; t < kT; ++t) {
+                const int idx = lane + 64 * t;
+                valid[t] = idx < nsurv;
+                const int at = valid[t] ? idx : 0;
+                cval[t] = S.sv[at];
+                cid[t] = S.si[at];
+                keys[t] = valid[t] ? float_key(cval[t]) : 0u;
             }
-            // slot = candidates taken in earlier segments + rank within this one
+            const uint32_t tau = k > 1 ? wave_kth_key_slots<kT>(keys, k) : hi_key;
             const bool want_probs = a.cand_probs != nullptr;
             const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
-            bool take[kStepMaxSegs];
-            int pos[kStepMaxSegs];
-            float wgt[kStepMaxSegs];
-            int total = 0;
+            bool take[kT];
+            int pos[kT];
+            float wgt[kT];
             double z = 0.0;
 #pragma unroll
-            for (int s = 0; s < kStepMaxSegs; ++s) {
-                take[s] = valid[s] && keys[s] >= tau;
-                const uint64_t mask = __ballot(take[s]);
-                pos[s] = total + rank_in_mask(mask);
-                total += static_cast<int>(__popcll(mask));
-                wgt[s] = want_probs && take[s] ? cand_weight(cval[s], rm, inv_t) : 0.0f;
-                z += static_cast<double>(wgt[s]);
+            for (int t = 0; t < kT; ++t) {
+                take[t] = valid[t] && keys[t] >= tau;
+                const uint64_t mask = __ballot(take[t]);
+                pos[t] = n + rank_in_mask(mask);
+                n += static_cast<int>(__popcll(mask));
+                wgt[t] = want_probs && take[t] ? cand_weight(cval[t], rm, inv_t) : 0.0f;
+                z += static_cast<double>(wgt[t]);
+                if (take[t]) {
+                    S.cv[pos[t]] = cval[t];
+                    S.ci[pos[t]] = cid[t];
+                }
             }
-            z = wave_sum_f64(z);
+            if (want_probs) z = wave_sum_f64(z);
             const bool z_ok = z > 0.0 && __builtin_isfinite(z);
             const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
 #pragma unroll
-            for (int s = 0; s < kStepMaxSegs; ++s) {
-                if (take[s] && pos[s] < a.capacity) {
-                    const int64_t o = row * a.capacity + pos[s];
-                    a.cand_ids[o] = cidx[s];
-                    if (a.cand_logits) a.cand_logits[o] = cval[s];
-                    if (want_probs) a.cand_probs[o] = z_ok ? wgt[s] * inv_z : (cidx[s] == best ? 1.0f : 0.0f);
+            for (int t = 0; t < kT; ++t) {
+                if (take[t] && pos[t] < a.capacity) {
+                    const int64_t o = row * a.capacity + pos[t];
+                    a.cand_ids[o] = cid[t];
+                    if (a.cand_logits) a.cand_logits[o] = cval[t];
+                    if (want_probs) a.cand_probs[o] = z_ok ? wgt[t] * inv_z : (cid[t] == best ? 1.0f : 0.0f);
                 }
             }
             if (lane == 0) {
                 a.best[row] = best;
-                a.count[row] = total;
+                a.count[row] = n;
                 if (a.row_max) a.row_max[row] = bv;
                 if (a.row_lse) a.row_lse[row] = lse;
             }
+        } else if (row_nan && lane == 0) {  // the reference throws "logits contain NaN"
+            a.best[row] = -1;
+            a.count[row] = -1;
+            if (a.row_max) a.row_max[row] = NAN;
+            if (a.row_lse) a.row_lse[row] = NAN;
+        }
+
+        // ---- the draw index: earlier rows draw unless they hold a NaN or a +-inf maximum ----
+        if (sampling && row > 0) {
+            uint64_t kill[kEarlyChunks], live[kEarlyChunks];
+#pragma unroll
+            for (int i = 0; i < kEarlyChunks; ++i) {
+                if (i * 64 >= nearly) break;  // uniform
+                const bool in = lane + 64 * i < nearly;
+                kill[i] = __ballot(in && (eh[i].count == kPartNaN || eh[i].max == INFINITY));
+                live[i] = __ballot(in && eh[i].max > -INFINITY);
+            }
+            for (int r = 0; r < static_cast<int>(row); ++r) {
+                bool killed = false, alive = false;
+#pragma unroll
+                for (int i = 0; i < kEarlyChunks; ++i) {
+                    if (i * 64 >= nearly) break;  // uniform
+                    const uint64_t range = lane_range(r * parts - 64 * i, (r + 1) * parts - 64 * i);
+                    killed = killed || (kill[i] & range) != 0;
+                    alive = alive || (live[i] & range) != 0;
+                }
+                before += !killed && alive ? 1 : 0;
+            }
+        }
+        const bool slow = !row_nan && !fast;
+        if (drawing && !slow) {
+            wave_lds_order();
+            const bool draws = sampling && !row_nan && __builtin_isfinite(bv);
+            int64_t token;
+            if (row_nan) token = LEVO_HIP_TOKEN_NAN;
+            else if (!draws) token = best;
+            else if (n > d.capacity) token = LEVO_HIP_TOKEN_OVERFLOW;
+            else {
+                const int first = lane < n ? lane : 0;
+                const uint64_t raw = before == row ? raw_at_r : d.bits[before];
+                token = draw_token(S.cv, S.ci, S.cv[first], S.ci[first], n, bv, d.temperature, raw);
+            }
+            if (lane == 0) {
+                d.draws[row] = before + (draws ? 1 : 0);
+                d.tokens[row] = token;
+            }
         }
         if (lane == 0) {
-            S.slow[wave] = !row_nan && !fast ? 1 : 0;
-            S.rm[wave] = rm;
-            S.best[wave] = best;
-            S.bv[wave] = bv;
-            S.lse[wave] = lse;
+            S.slow = slow ? 1 : 0;
+            S.rm = rm;
+            S.best = best;
+            S.bv = bv;
+            S.lse = lse;
         }
-    } else if (lane == 0) {
-        S.slow[wave] = 0;
     }
     __syncthreads();
+    if (!S.slow) return;  // uniform
 
-    // ---- rows that do not fit: the whole row again, by the whole workgroup ------------------
+    // ---- a row the fast path does not cover: the whole row again, by the whole workgroup ----
+    const bool use_pen = a.recent != nullptr && a.n_recent > 0;
+    const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
+    row_lds<kStepWords> & L = S.L;
     const int words = (V + 31) / 32;
-    for (int w = 0; w < kWaves; ++w) {
-        if (!S.slow[w]) continue;  // uniform
-        const int64_t r = static_cast<int64_t>(blockIdx.x) * kWaves + w;
-        const int stream = static_cast<int>(r % a.n_streams);
-        int k = a.top_k[stream];
-        if (k <= 0 || k >= V) k = 0;
-        const bool use_pen = a.recent != nullptr && a.n_recent > 0;
-        const bool use_ign = a.ignore != nullptr && a.n_ignore > 0 && stream == 0;
-        row_lds<kStepWords> & L = S.L;
-        for (int i = tid; i < words; i += kThreads) {
-            L.sel[i] = 0u;
-            L.pen[i] = 0u;
-            L.ign[i] = 0u;
-        }
-        __syncthreads();
-        if (use_pen) {
-            const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
-            const int64_t * rec = a.recent + r * a.n_recent;
-            for (int i = tid; i < a.n_recent; i += kThreads) {
-                const int64_t t = rec[i];
-                if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
-            }
-        }
-        if (use_ign) {
-            for (int i = tid; i < a.n_ignore; i += kThreads) {
-                const int64_t t = a.ignore[i];
-                if (t >= 0 && t < V) atomicOr(&L.ign[t >> 5], 1u << (t & 31));
-            }
-        }
-        __syncthreads();
-        select_general(a, L, r, V, k, S.rm[w], S.best[w], use_pen, use_ign);
-        if (tid == 0) {
-            a.best[r] = S.best[w];
-            a.count[r] = L.total;
-            if (a.row_max) a.row_max[r] = S.bv[w];
-            if (a.row_lse) a.row_lse[r] = S.lse[w];
-        }
-        __syncthreads();  // the next row reuses the bitmaps
+    for (int i = tid; i < words; i += kThreads) {
+        L.sel[i] = 0u;
+        L.pen[i] = 0u;
+        L.ign[i] = 0u;
     }
-
-    // ---- the draw of every row (all rows are in this workgroup) ----------------------------
-    if (d.tokens == nullptr) return;
-    __syncthreads();  // every row's outputs are written and visible to the workgroup
-    if (live) draw_row(d, row);
-}
-
-int64_t step_segments(int64_t vocab) { return (vocab + kStepSegIds - 1) / kStepSegIds; }
-
-int64_t step_workspace_bytes(int64_t rows, int64_t vocab) {
-    return kStepCounterBytes + rows * step_segments(vocab) * static_cast<int64_t>(sizeof(step_seg));
+    __syncthreads();
+    if (use_pen) {
+        const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
+        const int64_t * rec = a.recent + row * a.n_recent;
+        for (int i = tid; i < a.n_recent; i += kThreads) {
+            const int64_t t = rec[i];
+            if (t >= 0 && t < limit) atomicOr(&L.pen[t >> 5], 1u << (t & 31));
+        }
+    }
+    if (use_ign) {
+        for (int i = tid; i < a.n_ignore; i += kThreads) {
+            const int64_t t = a.ignore[i];
+            if (t >= 0 && t < V) atomicOr(&L.ign[t >> 5], 1u << (t & 31));
+        }
+    }
+    __syncthreads();
+    select_general(a, L, row, V, k, S.rm, S.best, use_pen, use_ign);
+    if (tid == 0) {
+        a.best[row] = S.best;
+        a.count[row] = L.total;
+        if (a.row_max) a.row_max[row] = S.bv;
+        if (a.row_lse) a.row_lse[row] = S.lse;
+    }
+    if (!drawing) return;
+    __syncthreads();  // the row's candidates are written and visible to the workgroup
+    if (wave != 0) return;
+    const int n = L.total;
+    const bool draws = sampling && __builtin_isfinite(S.bv);
+    int64_t token;
+    if (!draws) token = S.best;
+    else if (n > d.capacity) token = LEVO_HIP_TOKEN_OVERFLOW;
+    else {
+        const float * vals = a.cand_logits + row * a.capacity;
+        const int32_t * ids = a.cand_ids + row * a.capacity;
+        const int first = lane < n ? lane : 0;
+        const uint64_t raw = before == row ? raw_at_r : d.bits[before];
+        token = draw_token(vals, ids, vals[first], ids[first], n, S.bv, d.temperature, raw);
+    }
+    if (lane == 0) {
+        d.draws[row] = before + (draws ? 1 : 0);
+        d.tokens[row] = token;
+    }
 }
 
 }  // namespace
@@ -1349,26 +1419,31 @@ int launch_step(const levo_hip_sample_args * args, const levo_hip_draw_args * dr
                          d.cand_ids == a.cand_ids && d.cand_logits == a.cand_logits && d.row_max == a.row_max,
                      "sample_step: the draw must read the rows' own candidate outputs");
     }
-    const int64_t segs = step_segments(a.vocab);
+    const int64_t parts = step_parts(a.vocab);
     LEVO_REQUIRE(a.rows <= kStepMaxRows, "sample_step: more than %lld rows", static_cast<long long>(kStepMaxRows));
     LEVO_REQUIRE(ws != nullptr && aligned16(ws), "sample_step: workspace must be 16-byte aligned device memory");
     LEVO_REQUIRE(ws_bytes >= step_workspace_bytes(a.rows, a.vocab),
                  "sample_step: workspace smaller than levo_hip_sample_step_workspace_bytes");
-    const uint32_t grid = static_cast<uint32_t>(a.rows * segs);
+    const step_ws w = carve_step_ws(ws, a.rows, a.vocab);
+    const uint32_t grid = static_cast<uint32_t>(a.rows * parts);
     const bool vec = a.row_pitch % 4 == 0 && aligned16(a.cond) && (a.uncond == nullptr || aligned16(a.uncond));
-    uint8_t * w = static_cast<uint8_t *>(ws);
-    if (vec) step_segment_kernel<4><<<grid, kThreads, 0, stream>>>(a, w, static_cast<int>(segs));
-    else step_segment_kernel<1><<<grid, kThreads, 0, stream>>>(a, w, static_cast<int>(segs));
+    if (vec) step_part_kernel<4><<<grid, 64, 0, stream>>>(a, w, static_cast<int>(parts));
+    else step_part_kernel<1><<<grid, 64, 0, stream>>>(a, w, static_cast<int>(parts));
     const int sa = launch_status("levo_hip_sample_step");
     if (sa != LEVO_HIP_OK) return sa;
-    // the merge launch draws when every row is in its one workgroup; otherwise
-    // the draw is a launch of its own
-    const uint32_t merge_groups = static_cast<uint32_t>(ceil_div(a.rows, kWaves));
+    // the join launch draws when the rows are few; otherwise the draw is a
+    // launch of its own
+    const bool join_draws = a.rows <= kJoinDrawRows;
     levo_hip_draw_args dm = d;
-    if (merge_groups > 1) dm.tokens = nullptr;
-    step_merge_kernel<<<merge_groups, kThreads, 0, stream>>>(a, dm, w, static_cast<int>(segs));
+    if (!join_draws) dm.tokens = nullptr;
+    const uint32_t jg = static_cast<uint32_t>(a.rows);
+    const int np = static_cast<int>(parts);
+    if (parts <= 8) step_join_kernel<4><<<jg, kThreads, 0, stream>>>(a, dm, w, np);
+    else if (parts <= 16) step_join_kernel<8><<<jg, kThreads, 0, stream>>>(a, dm, w, np);
+    else if (parts <= 34) step_join_kernel<17><<<jg, kThreads, 0, stream>>>(a, dm, w, np);
+    else step_join_kernel<32><<<jg, kThreads, 0, stream>>>(a, dm, w, np);
     const int sb = launch_status("levo_hip_sample_step");
-    if (sb != LEVO_HIP_OK || draw == nullptr || merge_groups == 1) return sb;
+    if (sb != LEVO_HIP_OK || draw == nullptr || join_draws) return sb;
     return levo_hip_sample_draw(&d, reinterpret_cast<levo_hip_stream_t>(stream));
 }
 

@@ -200,6 +200,26 @@ __device__ __forceinline__ int wave_inclusive_scan_i32(int v) {
     return v;
 }
 
+// The same over doubles: each DPP step moves both halves of the 64-bit value;
+// lanes outside a step's source row receive +0.0, which leaves sums unchanged.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ double scan_step_f64(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint64_t lo = static_cast<uint32_t>(dpp::mov_or_zero<kCtrl, kRowMask>(static_cast<int>(static_cast<uint32_t>(b))));
+    const uint64_t hi =
+        static_cast<uint32_t>(dpp::mov_or_zero<kCtrl, kRowMask>(static_cast<int>(static_cast<uint32_t>(b >> 32))));
+    return x + __builtin_bit_cast(double, lo | (hi << 32));
+}
+__device__ __forceinline__ double wave_inclusive_scan_f64(double v) {
+    v = scan_step_f64<dpp::kRowShr1>(v);
+    v = scan_step_f64<dpp::kRowShr2>(v);
+    v = scan_step_f64<dpp::kRowShr4>(v);
+    v = scan_step_f64<dpp::kRowShr8>(v);
+    v = scan_step_f64<dpp::kRowBcast15, 0xA>(v);
+    v = scan_step_f64<dpp::kRowBcast31, 0xC>(v);
+    return v;
+}
+
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
 // Workgroup barrier that orders LDS accesses only: global loads in flight

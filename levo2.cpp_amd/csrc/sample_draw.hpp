@@ -14,19 +14,24 @@
 // rows 0..r consumed, so the caller advances its engine by draws[rows - 1].
 //
 // One wave per row; no LDS, no barriers. Lane i computes the weights of
-// candidates i, i + 64, ...; the sums run in candidate (ascending id) order
-// through readlane broadcasts, so every addition is the reference's. Up to
-// 64 candidates (top-k 50) take one pass that leaves each lane its own
-// cumulative sum; larger sets take two (total, then the search).
+// candidates i, i + 64, ...; the cumulative sums in candidate (ascending id)
+// order come from one prefix scan per 64 candidates (six DPP steps) instead
+// of the reference's chain of n dependent additions. Up to 64 candidates
+// (top-k 50) take one pass that leaves each lane its own cumulative sum;
+// larger sets take two (total, then the search).
 //
 // Exactness: the F32 steps (v - max, / T) are IEEE and equal to the host's;
 // the double exp of the device library and of the host's libm may differ in
-// the last bit. Such a difference moves a cumulative boundary by at most
-// about (n + 4) * 2^-51 * total, so the pick can differ from the reference's
-// only when the target lies that close to a boundary. The kernel flags those
-// rows (margin (n + 4) * 2^-44 * total) as LEVO_HIP_TOKEN_RECHECK for the
-// caller to draw on the host with the same raw value; for random targets
-// that happens with probability about (n + 4) * 2^-43 per draw.
+// the last bit, and the scan rounds its sums in another order than the
+// reference's sequential loop (each prefix of non-negative terms is then off
+// by at most (depth + 1) * 2^-53 of the total, depth <= 6 + n / 64, against
+// (n - 1) * 2^-53 for the sequential sum). Together these move a cumulative
+// boundary or the target by at most about (2 n + 16) * 2^-52 * total, so the
+// pick can differ from the reference's only when the target lies that close
+// to a boundary. The kernel flags those rows (margin (n + 4) * 2^-44 * total,
+// over a hundred times wider) as LEVO_HIP_TOKEN_RECHECK for the caller to
+// draw on the host with the same raw value; for random targets that happens
+// with probability about (n + 4) * 2^-43 per draw.
 
 #include "common.hpp"
 
@@ -52,6 +57,74 @@ __device__ __forceinline__ double draw_weight(float v, float m, float t) {
 
 __device__ __forceinline__ bool row_draws(const levo_hip_draw_args & a, int64_t r) {
     return a.best[r] >= 0 && __builtin_isfinite(a.row_max[r]);
+}
+
+// The token of a row that draws, computed by one whole wave: its n
+// candidates in ascending id order (lane l holds candidate l in v0 / id0 when
+// l < n; `vals` / `ids` hold the whole list and are read only when n > 64),
+// the maximum m, the temperature t and the row's raw value. Returns the id,
+// or LEVO_HIP_TOKEN_RECHECK; the same value in every lane.
+__device__ __forceinline__ int64_t draw_token(const float * vals, const int32_t * ids, float v0, int32_t id0, int n,
+                                              float m, float t, uint64_t raw) {
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    const double u = (static_cast<double>(raw >> 11) + 0.5) * kTwoPowMinus53;
+
+    double total = 0.0;
+    double cumulative = 0.0;
+    double below = 0.0;
+    double above = 0.0;
+    double target;
+    int found = -1;
+    if (n <= 64) {
+        // Lane l's cumulative sum through candidate l by one prefix scan;
+        // lanes past n add +0.0.
+        const double w = lane < n ? draw_weight(v0, m, t) : 0.0;
+        const double mine = wave_inclusive_scan_f64(w);
+        total = read_lane_f64(mine, 63);
+        target = u * total;
+        const uint64_t hit = __ballot(lane < n && target < mine);
+        if (hit != 0) {
+            found = __builtin_ctzll(hit);
+            above = read_lane_f64(mine, found);
+            if (found > 0) below = read_lane_f64(mine, found - 1);
+        } else {
+            below = total;
+        }
+        cumulative = total;
+    } else {
+        // Pass 1: the total, 64 candidates per prefix scan.
+        for (int base = 0; base < n; base += 64) {
+            const int i = base + lane;
+            const double w = i < n ? draw_weight(vals[i], m, t) : 0.0;
+            total += read_lane_f64(wave_inclusive_scan_f64(w), 63);
+        }
+        // Pass 2: the first candidate whose cumulative sum exceeds the
+        // target; `below` / `above` are the sums on either side of it.
+        target = u * total;
+        for (int base = 0; base < n && found < 0; base += 64) {
+            const int i = base + lane;
+            const double w = i < n ? draw_weight(vals[i], m, t) : 0.0;
+            const double mine = cumulative + wave_inclusive_scan_f64(w);
+            const uint64_t hit = __ballot(i < n && target < mine);
+            if (hit != 0) {
+                const int l = __builtin_ctzll(hit);
+                found = base + l;
+                above = read_lane_f64(mine, l);
+                below = l > 0 ? read_lane_f64(mine, l - 1) : cumulative;
+            } else {
+                cumulative = read_lane_f64(mine, 63);
+                below = cumulative;
+            }
+        }
+    }
+    const double margin = static_cast<double>(n + 4) * kMarginUlps * total;
+    bool recheck = target - below <= margin && below != 0.0;
+    if (found >= 0) recheck = recheck || above - target <= margin;
+    else recheck = recheck || target - cumulative <= margin;
+    if (recheck) return LEVO_HIP_TOKEN_RECHECK;
+    const int pick = found >= 0 ? found : n - 1;
+    if (n <= 64) return __builtin_amdgcn_readlane(id0, pick);
+    return ids[pick];
 }
 
 // Row r's token and draw count, computed by one whole wave.
@@ -99,83 +172,14 @@ __device__ __forceinline__ void draw_row(const levo_hip_draw_args & a, int64_t r
         if (lane == 0) a.tokens[r] = LEVO_HIP_TOKEN_OVERFLOW;
         return;
     }
-    const float t = a.temperature;
     const uint64_t raw = before == r ? raw_at_r : a.bits[before];
-    const double u = (static_cast<double>(raw >> 11) + 0.5) * kTwoPowMinus53;
-
-    double total = 0.0;
-    double cumulative = 0.0;
-    double below = 0.0;
-    double above = 0.0;
-    double target;
-    int found = -1;
-    if (n <= 64) {
-        // One pass: lane l keeps the cumulative sum through candidate l.
-        // Lanes past n hold +0.0, which leaves every partial sum unchanged.
-        const double w = lane < n ? draw_weight(v0, m, t) : 0.0;
-        double mine = 0.0;
-#pragma unroll
-        for (int l = 0; l < 64; ++l) {
-            total += read_lane_f64(w, l);
-            if (lane == l) mine = total;
-        }
-        target = u * total;
-        const uint64_t hit = __ballot(lane < n && target < mine);
-        if (hit != 0) {
-            found = __builtin_ctzll(hit);
-            above = read_lane_f64(mine, found);
-            if (found > 0) below = read_lane_f64(mine, found - 1);
-        } else {
-            below = total;
-        }
-        cumulative = total;
-    } else {
-        // Pass 1: the total in candidate order.
-        for (int base = 0; base < n; base += 64) {
-            const int i = base + lane;
-            const double w = i < n ? draw_weight(vals[i], m, t) : 0.0;
-#pragma unroll
-            for (int l = 0; l < 64; ++l) total += read_lane_f64(w, l);
-        }
-        // Pass 2: the first candidate whose cumulative sum exceeds the
-        // target; `below` / `above` are the sums on either side of it.
-        target = u * total;
-        for (int base = 0; base < n && found < 0; base += 64) {
-            const int i = base + lane;
-            const double w = i < n ? draw_weight(vals[i], m, t) : 0.0;
-#pragma unroll
-            for (int l = 0; l < 64; ++l) {
-                cumulative += read_lane_f64(w, l);
-                if (found < 0 && base + l < n) {
-                    if (target < cumulative) {
-                        found = base + l;
-                        above = cumulative;
-                    } else {
-                        below = cumulative;
-                    }
-                }
-            }
-        }
-    }
-    const double margin = static_cast<double>(n + 4) * kMarginUlps * total;
-    bool recheck = target - below <= margin && below != 0.0;
-    if (found >= 0) recheck = recheck || above - target <= margin;
-    else recheck = recheck || target - cumulative <= margin;
-    if (recheck) {
-        if (lane == 0) a.tokens[r] = LEVO_HIP_TOKEN_RECHECK;
-        return;
-    }
-    const int pick = found >= 0 ? found : n - 1;
-    if (n <= 64) {
-        const int32_t id = __builtin_amdgcn_readlane(id0, pick);
-        if (lane == 0) a.tokens[r] = id;
-    } else if (lane == 0) {
-        a.tokens[r] = ids[pick];
-    }
+    const int64_t token = draw_token(vals, ids, v0, id0, n, m, a.temperature, raw);
+    if (lane == 0) a.tokens[r] = token;
 }
 
 }  // namespace draw_detail
 
 using draw_detail::draw_row;
+using draw_detail::draw_token;
 
 }  // namespace levo_hip

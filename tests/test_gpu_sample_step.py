@@ -1,6 +1,7 @@
 """levo_hip_sample_step (CFG, penalty, ignore list, top-k candidates and the
-draw of a decode step; rows split over segment workgroups, merged and drawn
-in a second launch) against
+draw of a decode step; rows split over one-wave parts of 512 ids that hand
+over the ids above a bound, joined, selected and drawn in a second launch)
+against
 levo_hip_cfg_sample + levo_hip_sample_draw on the same inputs, against the
 oracle, and against the compiled reference Sampler (src/levo-sampling.cpp).
 
@@ -157,9 +158,9 @@ def test_decode_step_matches_two_launches_and_oracle(hip, binding, dev, oracle):
 @pytest.mark.parametrize("V,pitch", [(16384, 16384), (16385, 16388), (2048, 2048), (2049, 2049), (7, 7),
                                      (5000, 5000), (32768, 32768)])
 def test_shapes_match_two_launches(hip, binding, dev, oracle, V, pitch):
-    """Aligned (vector loads) and unaligned rows, one segment, a partial last
-    segment of one id, tiny and maximal vocabularies; several rows and
-    streams with different k."""
+    """Aligned (vector loads) and unaligned rows, one part, a partial last
+    part of one id, tiny and maximal vocabularies; several rows and streams
+    with different k."""
     rows = 8
     cond = _f16_logits(oracle, rows, V, 2200 + V)
     uncond = _f16_logits(oracle, rows, V, 2300 + V)
@@ -174,8 +175,8 @@ def test_shapes_match_two_launches(hip, binding, dev, oracle, V, pitch):
 @pytest.mark.parametrize("k", [1, 2, 50, 100, 300, 512, 513, 0, 16383, 16384])
 def test_ties_and_k(hip, binding, dev, oracle, k):
     """Ties at the maximum and at the k-th value, +-0, a constant row (more
-    candidates than a segment hands over: the row is selected again from its
-    logits), k = 0 and k >= V (keep every id)."""
+    ids at a part's bound than a part hands over: the row is selected again
+    from its logits), k = 0 and k >= V (keep every id)."""
     V, R = 16384, 6
     cond = _f16_logits(oracle, R, V, 2400 + k)
     cond[0, [5, 900, 15000]] = cond[0].max() + 1.0
@@ -196,7 +197,7 @@ def test_ties_and_k(hip, binding, dev, oracle, k):
 
 def test_special_rows(hip, binding, dev, oracle):
     """NaN rows (best = count = -1, token -1), all -inf and +inf maxima (no
-    draw), NaN in the last, partial segment."""
+    draw), NaN in the last, partial part."""
     V = 4097
     cond = _f16_logits(oracle, 6, V, 2500)
     cond[1, 17] = np.nan
@@ -255,9 +256,6 @@ def test_reference_sampler_decode_loop(hip, binding, dev, oracle, ref):
             consumed += int(got["draws"][-1])
             recent = np.concatenate([recent[:, 1:], got["tokens"][:, None]], axis=1)
         assert consumed == s.draw_count
-    # the reserved region (the first 16 KiB) is left as it was
-    head = from_dev(ws[0])[:4096]
-    assert np.all(head.view(np.uint32) == 0)
 
 
 def test_workspace_reused_across_shapes(hip, binding, dev, oracle):
