@@ -62,7 +62,7 @@ constexpr int kMaxVocab = 32768;
 // entries before its logits, so the two memory round trips overlap; the load
 // takes no branch (a lane without an entry reads kNoListEntry), which keeps
 // the compiler from waiting for it before the logits' loads are issued.
-__device__ const int64_t kNoListEntry = -1;
+__device__ int64_t kNoListEntry = -1;  // read only; global, so that the pointer choice stays a global load
 
 __device__ __forceinline__ int64_t list_entry(const int64_t * rec, int n_pen, const int64_t * ign, int n_ign,
                                               int i) {
@@ -102,10 +102,17 @@ __device__ __forceinline__ uint32_t wave_kth_key_slots(const uint32_t (&key)[NS]
 #pragma unroll
     for (int bit = 31; bit >= 0; --bit) {
         const uint32_t cand = prefix | (1u << bit);
+        uint64_t m[NS];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) m[s] = __ballot(key[s] >= cand);
         int c = 0;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) c += static_cast<int>(__popcll(__ballot(key[s] >= cand)));
+        for (int s = 0; s < NS; ++s) c += static_cast<int>(__popcll(m[s]));
         prefix = c >= k ? cand : prefix;
+        // the NS compares back to back, each into its own register pair, then
+        // the scalar counts: one compare-to-count latency per step, not NS
+        __builtin_amdgcn_sched_group_barrier(0x2, NS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x4, 2 * NS + 2, 0);
     }
     return prefix;
 }
@@ -903,8 +910,13 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
     const int64_t * rec = use_pen ? a.recent + row * a.n_recent : &kNoListEntry;
     const int64_t * ign = use_ign ? a.ignore : &kNoListEntry;
     const int64_t entry = list_entry(rec, n_pen, ign, n_ign, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the entry's load is issued before the logits'
+    // Without CFG the second input is the first again: every load is issued
+    // unconditionally, so none waits for another (a per-item choice of source
+    // would make each pair of loads a round trip of its own).
+    const bool cfg = a.uncond != nullptr;
     const float * crow = a.cond + row * a.row_pitch;
-    const float * urow = a.uncond ? a.uncond + row * a.row_pitch : nullptr;
+    const float * urow = cfg ? a.uncond + row * a.row_pitch : crow;
     float c[kPartPer], u[kPartPer];
     if constexpr (VEC == 4) {
 #pragma unroll
@@ -912,7 +924,7 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
             const int base = part_item_id<VEC>(lo, lane, ch * 4);
             const int off = base < V ? base : lo;  // row_pitch % 4 == 0: in bounds
             const f32x4 cv = *reinterpret_cast<const f32x4 *>(crow + off);
-            const f32x4 uv = urow ? *reinterpret_cast<const f32x4 *>(urow + off) : cv;
+            const f32x4 uv = *reinterpret_cast<const f32x4 *>(urow + off);
             c[ch * 4] = cv.x; c[ch * 4 + 1] = cv.y; c[ch * 4 + 2] = cv.z; c[ch * 4 + 3] = cv.w;
             u[ch * 4] = uv.x; u[ch * 4 + 1] = uv.y; u[ch * 4 + 2] = uv.z; u[ch * 4 + 3] = uv.w;
         }
@@ -922,7 +934,7 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
             const int id = part_item_id<VEC>(lo, lane, q);
             const int off = id < V ? id : lo;
             c[q] = crow[off];
-            u[q] = urow ? urow[off] : c[q];
+            u[q] = urow[off];
         }
     }
 
@@ -936,14 +948,17 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
         wave_lds_order();
         const int64_t limit = a.penalty_limit > 0 && a.penalty_limit < V ? a.penalty_limit : V;
         const int64_t top = hi < limit ? hi : limit;
-        for (int i = lane; i < n_pen + n_ign; i += 64) {
-            const int64_t t = i < 64 ? entry : list_entry(rec, n_pen, ign, n_ign, i);
+        // the first 64 entries outside any loop: only their own load is waited
+        // for, and the bitmaps fill while the logits are still in flight
+        const auto mark = [&](int i, int64_t t) {
             if (i < n_pen) {
                 if (t >= lo && t < top) atomicOr(&pen_map[(t - lo) >> 5], 1u << ((t - lo) & 31));
-            } else {
+            } else if (i < n_pen + n_ign) {
                 if (t >= lo && t < hi) atomicOr(&ign_map[(t - lo) >> 5], 1u << ((t - lo) & 31));
             }
-        }
+        };
+        mark(lane, entry);
+        for (int i = lane + 64; i < n_pen + n_ign; i += 64) mark(i, list_entry(rec, n_pen, ign, n_ign, i));
         wave_lds_order();
 #pragma unroll
         for (int q = 0; q < kPartPer; ++q) {
@@ -957,7 +972,7 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
     float tmax = -INFINITY;
 #pragma unroll
     for (int q = 0; q < kPartPer; ++q) {
-        float x = urow ? u[q] + a.cfg_scale * (c[q] - u[q]) : c[q];
+        float x = cfg ? u[q] + a.cfg_scale * (c[q] - u[q]) : c[q];
         if (pen & (1 << q)) x = x / a.repetition_penalty;
         if (ign_bits & (1 << q)) x = -INFINITY;
         v[q] = part_item_id<VEC>(lo, lane, q) < hi ? x : -INFINITY;
@@ -966,41 +981,26 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
     }
 
     // ---- maximum, first maximum, bound --------------------------------------------------
+    // One all-reduce of (key << 32 | ~id): the largest value and, among its
+    // ties (+-0 alike), the smallest id, the first maximum of std::max_element
+    // (:94-96); the value itself comes from the lane that holds it.
     const bool part_nan = __ballot(has_nan) != 0;
-    const float m = wave_max_f32(tmax);
-    int best = INT_MAX;
-    float bv = m;
-    if constexpr (VEC == 4) {
+    uint64_t lk = 0u;
+    float fv = -INFINITY;
 #pragma unroll
-        for (int ch = 0; ch < kPartPer / 4; ++ch) {
-            int fe = 4;
-            float fv = m;
-#pragma unroll
-            for (int e = 3; e >= 0; --e) {
-                const int q = ch * 4 + e;
-                if (part_item_id<VEC>(lo, lane, q) < hi && v[q] == m) {
-                    fe = e;
-                    fv = v[q];
-                }
-            }
-            const uint64_t mask = __ballot(fe < 4);
-            if (mask != 0 && best == INT_MAX) {
-                const int l = __builtin_ctzll(mask);
-                best = lo + ch * 256 + l * 4 + __builtin_amdgcn_readlane(fe, l);
-                bv = dpp::lane(fv, l);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int q = 0; q < kPartPer; ++q) {
-            const uint64_t mask = __ballot(part_item_id<VEC>(lo, lane, q) < hi && v[q] == m);
-            if (mask != 0 && best == INT_MAX) {
-                const int l = __builtin_ctzll(mask);
-                best = lo + q * 64 + l;
-                bv = dpp::lane(v[q], l);
-            }
+    for (int q = 0; q < kPartPer; ++q) {
+        const int id = part_item_id<VEC>(lo, lane, q);
+        const uint64_t c = (static_cast<uint64_t>(float_key(v[q])) << 32) | static_cast<uint32_t>(~id);
+        if (id < hi && c > lk) {
+            lk = c;
+            fv = v[q];
         }
     }
+    const uint64_t top = dpp::allreduce(lk, [](uint64_t x, uint64_t y) { return x > y ? x : y; });
+    const int best = static_cast<int>(~static_cast<uint32_t>(top));
+    const int owner = VEC == 4 ? ((best - lo) & 255) >> 2 : (best - lo) & 63;
+    const float bv = dpp::lane(fv, owner);
+    const float m = bv;  // the part's maximum (when it holds no NaN)
     uint32_t bkey = 0u;
     if (k == 1) {
         bkey = float_key(m);  // the ties of the maximum

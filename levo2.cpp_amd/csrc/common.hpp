@@ -115,6 +115,13 @@ __device__ __forceinline__ double mov(double v) {
     return __builtin_bit_cast(double, lo | (hi << 32));
 }
 
+template <int kCtrl>
+__device__ __forceinline__ uint64_t mov(uint64_t v) {
+    const uint64_t lo = mov<kCtrl>(static_cast<uint32_t>(v));
+    const uint64_t hi = mov<kCtrl>(static_cast<uint32_t>(v >> 32));
+    return lo | (hi << 32);
+}
+
 __device__ __forceinline__ uint32_t lane(uint32_t v, int l) {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), l));
 }
@@ -122,6 +129,9 @@ __device__ __forceinline__ float lane(float v, int l) {
     return __builtin_bit_cast(float, lane(__builtin_bit_cast(uint32_t, v), l));
 }
 __device__ __forceinline__ int lane(int v, int l) { return static_cast<int>(lane(static_cast<uint32_t>(v), l)); }
+__device__ __forceinline__ uint64_t lane(uint64_t v, int l) {
+    return lane(static_cast<uint32_t>(v), l) | (static_cast<uint64_t>(lane(static_cast<uint32_t>(v >> 32), l)) << 32);
+}
 __device__ __forceinline__ double lane(double v, int l) {
     const uint64_t b = __builtin_bit_cast(uint64_t, v);
     const uint64_t lo = lane(static_cast<uint32_t>(b), l);
