@@ -91,16 +91,21 @@ __device__ __forceinline__ uint32_t wave_kth_key(uint32_t key, int k) {
 }
 
 // The same over NS keys per lane (invalid keys 0): the largest t with at least
-// k keys >= t, or 0 when fewer than k keys are non-zero.
+// k keys >= t, or 0 when fewer than k keys are non-zero. Every valid key lies
+// in [lo, hi]: the bits above their highest differing bit are lo's, and the
+// bisection starts below them.
 template <int NS>
-__device__ __forceinline__ uint32_t wave_kth_key_slots(const uint32_t (&key)[NS], int k) {
+__device__ __forceinline__ uint32_t wave_kth_key_slots(const uint32_t (&key)[NS], int k, uint32_t lo, uint32_t hi) {
     int nz = 0;
 #pragma unroll
     for (int s = 0; s < NS; ++s) nz += static_cast<int>(__popcll(__ballot(key[s] != 0u)));
     if (nz < k) return 0u;
-    uint32_t prefix = 0u;
+    const uint32_t diff = lo ^ hi;
+    const int top = diff == 0u ? -1 : 31 - __builtin_clz(diff);
+    uint32_t prefix = top < 0 ? lo : lo & ~((2u << top) - 1u);
 #pragma unroll
     for (int bit = 31; bit >= 0; --bit) {
+        if (bit > top) continue;  // uniform
         const uint32_t cand = prefix | (1u << bit);
         uint64_t m[NS];
 #pragma unroll
@@ -825,6 +830,7 @@ constexpr int kPartPer = kPartIds / 64;                // ids per lane
 constexpr int kPartCap = 32;                           // handed-over ids per part
 constexpr int kMaxParts = kMaxVocab / kPartIds;        // parts of the longest row
 constexpr int kJoinCap = 256;                          // survivors the joining wave selects from
+constexpr int kJoinFirst = 16;                         // slots per part the join reads before the heads arrive
 constexpr int kJoinDrawRows = 8;                       // rows whose draws the join launch makes
 constexpr int kEarlyChunks = (kJoinDrawRows - 1) * kMaxParts / 64;  // earlier rows' heads, 64 per chunk
 constexpr int kStepWords = kMaxVocab / 32;             // bitmap words of the longest row
@@ -1070,6 +1076,49 @@ __global__ __launch_bounds__(64) void step_part_kernel(const levo_hip_sample_arg
     }
 }
 
+// Slots [0, SPP) of every part into NS slots per lane: slot s of lane l is
+// slot (l + 64 s) % SPP of part (l + 64 s) / SPP, ascending ids within a part
+// and across parts. Every load is issued before any is used.
+template <int SPP, int NS>
+__device__ __forceinline__ void load_slots(part_cand (&sl)[NS], const part_cand * cand, int parts, int lane) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int j = lane + 64 * s;
+        const int g = j / SPP < parts ? j / SPP : parts - 1;
+        sl[s] = cand[g * kPartCap + j % SPP];
+    }
+}
+
+// The handed-over ids at or above lo_v, in ascending id order, into
+// sv / si[0, kJoinCap); returns their number (which may exceed kJoinCap).
+// count: this lane's part count (lane g holds part g's).
+template <int SPP, int NS>
+__device__ __forceinline__ int collect_survivors(const part_cand (&sl)[NS], int count, int parts, float lo_v, float * sv,
+                                                 int32_t * si, int lane) {
+    // each slot's part count, fetched for every slot row at once (lane shuffles
+    // issued back to back); parts past the row's last count 0
+    int cnt[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int g = (lane + 64 * s) / SPP;
+        cnt[s] = __shfl(count, g < 64 ? g : 0);
+        cnt[s] = g < parts ? cnt[s] : 0;
+    }
+    int n = 0;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const bool surv = (lane + 64 * s) % SPP < cnt[s] && sl[s].v >= lo_v;
+        const uint64_t mask = __ballot(surv);
+        const int p = n + rank_in_mask(mask);
+        if (surv && p < kJoinCap) {
+            sv[p] = sl[s].v;
+            si[p] = sl[s].id;
+        }
+        n += static_cast<int>(__popcll(mask));
+    }
+    return n;
+}
+
 struct join_lds {
     row_lds<kStepWords> L;                                   // the general path
     float sv[kJoinCap];                                      // survivors, ascending ids: values
@@ -1117,14 +1166,11 @@ __global__ __launch_bounds__(kThreads) void step_join_kernel(const levo_hip_samp
         const bool mine = lane < parts;
         const part_head h = w.heads[rp0 + (mine ? lane : 0)];
         const float hsum = a.row_lse != nullptr ? w.sums[rp0 + (mine ? lane : 0)] : 0.0f;
-        const int nslots = parts * kPartCap;
+        // the first kJoinFirst slots of every part (most parts hand over fewer)
         const part_cand * cand = w.cands + rp0 * kPartCap;
-        part_cand sl[NS];
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int j = lane + 64 * s;
-            sl[s] = cand[j < nslots ? j : nslots - 1];
-        }
+        constexpr int NF = (NS + 1) / 2;
+        part_cand sl[NF];
+        load_slots<kJoinFirst, NF>(sl, cand, parts, lane);
         if (sampling) raw_at_r = d.bits[row];
         // the heads of the earlier rows (at most kJoinDrawRows - 1 of them)
         const int nearly = sampling ? static_cast<int>(row) * parts : 0;
@@ -1167,22 +1213,12 @@ __global__ __launch_bounds__(kThreads) void step_join_kernel(const levo_hip_samp
             // lo_key as a value (every lo_key is some value's key; 0 admits every
             // handed-over id): a value is at or above it exactly when its key is
             const float lo_v = lo_key == 0u ? -INFINITY : float_of_key(lo_key);
-#pragma unroll
-            for (int s = 0; s < NS; ++s) {
-                // slot j = lane + 64 s is slot j % kPartCap of part j / kPartCap: part
-                // 2 s in lanes 0-31, 2 s + 1 in lanes 32-63, each with its count
-                const int c_lo = 2 * s < parts ? __builtin_amdgcn_readlane(h.count, 2 * s) : 0;
-                const int c_hi = 2 * s + 1 < parts ? __builtin_amdgcn_readlane(h.count, 2 * s + 1) : 0;
-                const uint64_t filled = (c_lo >= 32 ? 0xFFFFFFFFull : (uint64_t{1} << c_lo) - 1u) |
-                                        ((c_hi >= 32 ? 0xFFFFFFFFull : (uint64_t{1} << c_hi) - 1u) << 32);
-                const uint64_t mask = __ballot(sl[s].v >= lo_v) & filled;
-                const bool surv = (mask >> lane) & 1u;
-                const int p = nsurv + rank_in_mask(mask);
-                if (surv && p < kJoinCap) {
-                    S.sv[p] = sl[s].v;
-                    S.si[p] = sl[s].id;
-                }
-                nsurv += static_cast<int>(__popcll(mask));
+            if (__ballot(mine && h.count > kJoinFirst) == 0) {
+                nsurv = collect_survivors<kJoinFirst, NF>(sl, h.count, parts, lo_v, S.sv, S.si, lane);
+            } else {  // a part handed over more: read every slot of every part again
+                part_cand all[NS];
+                load_slots<kPartCap, NS>(all, cand, parts, lane);
+                nsurv = collect_survivors<kPartCap, NS>(all, h.count, parts, lo_v, S.sv, S.si, lane);
             }
             fast = nsurv >= k && nsurv <= kJoinCap;
         }
@@ -1205,7 +1241,7 @@ __global__ __launch_bounds__(kThreads) void step_join_kernel(const levo_hip_samp
                 cid[t] = S.si[at];
                 keys[t] = valid[t] ? float_key(cval[t]) : 0u;
             }
-            const uint32_t tau = k > 1 ? wave_kth_key_slots<kT>(keys, k) : hi_key;
+            const uint32_t tau = k > 1 ? wave_kth_key_slots<kT>(keys, k, lo_key, hi_key) : hi_key;
             const bool want_probs = a.cand_probs != nullptr;
             const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
             bool take[kT];
