@@ -815,7 +815,7 @@ int launch_sample(const levo_hip_sample_args & a, hipStream_t stream) {
 //      largest survivor, t >= L, and a row id at or above t is at or above
 //      its own part's bound, so it was handed over and survived; the row then
 //      holds exactly the survivors' ids at or above t, and t is the row's
-//      k-th largest. A radix select over the survivors gives t; the
+//      k-th largest. A bisection over the survivors' keys gives t; the
 //      candidates at or above it are written in ascending id order, followed
 //      by the draw of levo_hip_sample_draw when the rows are few.
 // G = min(k, 64, ceil(3 k * 512 / V) + 6): three times the candidates a part
