@@ -500,7 +500,7 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     50/1/1, T = 0.9; levo_hip_cfg_sample + levo_hip_sample_draw. Latency-bound
     (393 KB per step). `device_us`: both launches back to back;
     `sample_step_us`: the same step through levo_hip_sample_step (rows split
-    into 4096-id segment workgroups, then one merge-and-draw workgroup);
+    into one-wave parts of 512 ids, then one join-and-draw workgroup per row);
     `roundtrip_us`: median wall time from the first launch until the 3 ids and
     draw counts are in pinned host memory (Python launch overhead included);
     `graph_roundtrip_us`: the same with both launches and both copies
@@ -544,7 +544,7 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
 
     device_ms = time_op(torch, head, step, n, warmup, max(steps, 200))
     sample_ms = time_op(torch, head, lambda i: hip.cfg_sample(sargs[i]), n, warmup, max(steps, 200))
-    # the same step through levo_hip_sample_step (segment launch + merge-and-draw launch)
+    # the same step through levo_hip_sample_step (part launch + join-and-draw launch)
     ws_bytes = hip.sample_step_workspace_bytes(S, V)
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=dev)
     split_ms = time_op(torch, head, lambda i: hip.sample_step(sargs[i], d, ws, ws_bytes), n, warmup, max(steps, 200))

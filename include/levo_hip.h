@@ -351,9 +351,11 @@ int64_t levo_hip_sample_step_workspace_bytes(int64_t rows, int64_t vocab);
  * first maximum, top-k candidates of sample_top_k_counted :75-116), then,
  * when `draw` is not NULL, the tokens and draw counts of levo_hip_sample_draw
  * (:97-115). The results equal those two calls'. Each row is split over
- * workgroups of 4096 ids that hand their own top-k sets to `workspace`; a
- * second launch merges them and, with at most 8 rows, draws (more rows take a
- * third launch for the draw). It is made for the few rows of a decode step
+ * one-wave parts of 512 ids that hand the ids above a bound to `workspace`;
+ * a second launch checks that they hold the row's top k, selects it and, with
+ * at most 8 rows, draws (more rows take a third launch for the draw; a row
+ * the hand-over does not cover is selected again from its logits). It is
+ * made for the few rows of a decode step
  * (rows <= 4095). workspace: 16-byte aligned device memory of
  * levo_hip_sample_step_workspace_bytes(rows, vocab) bytes, whose contents
  * need no initialization; one workspace serves calls of any shape. Calls
@@ -365,7 +367,7 @@ int levo_hip_sample_step(const levo_hip_sample_args * args, const levo_hip_draw_
 
 /* levo_hip_sample_step without a workspace argument and without any
  * allocation: the workspace is a 2 MiB array the library holds on every GPU
- * it runs on, until the process ends (enough for 200 rows of 16385 logits;
+ * it runs on, until the process ends (enough for 230 rows of 16385 logits;
  * larger calls fail with LEVO_HIP_ERR_INVALID, naming the sizes). Same
  * results as levo_hip_sample_step. Calls that overlap on one GPU share that
  * array and race: serialize them. No counterpart in the reference: it is for
