@@ -446,21 +446,29 @@ def bench_flow_window(torch, hip, binding, head, dev, warmup, steps):
                     replaced_copies_us=round(copies_ms * 1e3, 1), bound="latency")
 
 
-def bench_norm(torch, hip, head, dev, warmup, steps, layer, rows, D):
-    per = 8 * rows * D + (4 * D if layer else 2 * D)
+def bench_norm(torch, hip, head, dev, warmup, steps, layer, rows, D, f16=True):
+    """Residual + RMS / LayerNorm over [rows, D]: F16 activations and
+    parameters (the LeLM norms), or F32 (f16=False: the Flow estimator's
+    LayerNorm, [2 x 1000 frames, 2200])."""
+    es = 2 if f16 else 4
+    per = 4 * es * rows * D + ((2 if layer else 1) * es * D)
     n = max(2, math.ceil(ROTATE_BYTES / per) + 1) if rows > 2 else 64
     g = torch.Generator(device=dev)
     g.manual_seed(rows * D + layer)
-    mk = lambda shape, s=1.0, m=0.0: (torch.randn(shape, generator=g, device=dev) * s + m).half()
+    dt = torch.float16 if f16 else torch.float32
+    mk = lambda shape, s=1.0, m=0.0: (torch.randn(shape, generator=g, device=dev) * s + m).to(dt)
     w, b = mk(D, 0.02, 1.0), mk(D, 0.02)
-    sets = [(mk((rows, D)), mk((rows, D)), torch.empty((rows, D), device=dev, dtype=torch.float16),
-             torch.empty((rows, D), device=dev, dtype=torch.float16)) for _ in range(n)]
+    sets = [(mk((rows, D)), mk((rows, D)), torch.empty((rows, D), device=dev, dtype=dt),
+             torch.empty((rows, D), device=dev, dtype=dt)) for _ in range(n)]
+    t = 1 if f16 else 0
+    eps = 1e-6 if f16 else 1e-5  # the LeLM's and the Flow estimator's
     if layer:
-        fn = lambda i: hip.layer_norm(1, sets[i][0], sets[i][1], w, b, 1, sets[i][2], sets[i][3], rows, D, 1e-6)
+        fn = lambda i: hip.layer_norm(t, sets[i][0], sets[i][1], w, b, t, sets[i][2], sets[i][3], rows, D, eps)
     else:
-        fn = lambda i: hip.rms_norm(1, sets[i][0], sets[i][1], w, 1, sets[i][2], sets[i][3], rows, D, 1e-6)
+        fn = lambda i: hip.rms_norm(t, sets[i][0], sets[i][1], w, t, sets[i][2], sets[i][3], rows, D, eps)
     ms = time_op(torch, head, fn, n, warmup, max(steps, 50))
-    return op_entry(per, ms, read=per - 4 * rows * D, shape=[rows, D], dtype="f16 io / f32 accumulate")
+    return op_entry(per, ms, read=per - 2 * es * rows * D, shape=[rows, D],
+                    dtype=("f16" if f16 else "f32") + " io / f32 accumulate")
 
 
 def bench_sample(torch, hip, binding, head, dev, warmup, steps):
@@ -1186,6 +1194,8 @@ def run_ops(torch, hip, binding, head, dev, args, groups):
             for rows, D in ((756, 2048), (756, 1536), (1, 2048), (2, 2048)):
                 log(f"ops: {name} {rows}x{D}")
                 ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, w, k, layer, rows, D)
+        log("ops: layernorm f32 2000x2200 (Flow estimator)")
+        ops["residual_layernorm_f32_2000x2200"] = bench_norm(torch, hip, head, dev, w, k, True, 2000, 2200, f16=False)
     if "sample" in groups:
         log("ops: cfg sample")
         ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, w, k)

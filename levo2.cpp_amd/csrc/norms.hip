@@ -331,7 +331,8 @@ int launch_norm(const void * xv, const void * dv, const void * wv, const void * 
             else if (nv == 3) LEVO_NORM_LAUNCH(3, 1);
             else LEVO_NORM_LAUNCH(4, 1);
         } else if (wpr == 2) {
-            LEVO_NORM_LAUNCH(4, 2);
+            if (nv == 3) LEVO_NORM_LAUNCH(3, 2);  // 2049-3072 elements: no idle fourth group of registers
+            else LEVO_NORM_LAUNCH(4, 2);
         } else {
             if (nv == 1) LEVO_NORM_LAUNCH(1, 4);
             else if (nv == 2) LEVO_NORM_LAUNCH(2, 4);

@@ -76,6 +76,19 @@ def test_f32_reference_chains(hip, dev, oracle, layer, D):
     assert f32_err(y, yw) <= 1e-5
 
 
+def test_flow_estimator_layernorm_full_shape(hip, dev, oracle):
+    """The Flow estimator's residual + LayerNorm at its real shape: F32
+    activations [2 (CFG), 1000 frames, 2200] = 2000 rows of 2200 values, F32
+    gamma / beta, eps 1e-5 (src/levo-flow-estimator.cpp:20, :106-109, :221-247):
+    the residual bit-exact, y within 1e-5 of the oracle."""
+    rows, D = 2000, 2200
+    x, d, w, b = _inputs(oracle, rows, D, 2200, False)
+    h, y = _run(hip, dev, True, x, d, w, b, 1e-5)
+    hw, yw = oracle.layer_norm(x, d, w, b, 1e-5, threads=8)
+    assert np.array_equal(h.view(np.uint32), hw.view(np.uint32))
+    assert f32_err(y, yw) <= 1e-5
+
+
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
 @pytest.mark.parametrize("rows,D", [(514, 2048), (513, 2056), (600, 3072), (520, 4104), (515, 8192), (511, 1536),
