@@ -29,6 +29,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kVec = 8;  // elements per lane per group (16 B of F16, 32 B of F32)
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 __device__ __forceinline__ void load8(const T * p, float (&o)[kVec]);
@@ -67,24 +68,40 @@ __device__ __forceinline__ void load8_row(const uint16_t * p, uint16_t (&o)[kVec
 #pragma unroll
     for (int k = 0; k < kVec; ++k) o[k] = v[k];
 }
-__device__ __forceinline__ void load8_row(const float * p, float (&o)[kVec]) {
-    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
-    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p) + 1);
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
-    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-}
 __device__ __forceinline__ void store8_row(uint16_t * p, const uint16_t (&v)[kVec]) {
     u16x8 w;
 #pragma unroll
     for (int k = 0; k < kVec; ++k) w[k] = v[k];
     __builtin_nontemporal_store(w, reinterpret_cast<u16x8 *>(p));
 }
-__device__ __forceinline__ void store8_row(float * p, const float (&v)[kVec]) {
-    f32x4 a, b;
-    a.x = v[0]; a.y = v[1]; a.z = v[2]; a.w = v[3];
-    b.x = v[4]; b.y = v[5]; b.z = v[6]; b.w = v[7];
-    __builtin_nontemporal_store(a, reinterpret_cast<f32x4 *>(p));
-    __builtin_nontemporal_store(b, reinterpret_cast<f32x4 *>(p) + 1);
+
+// F32 groups as two 4-value pieces (see norm_kernel_wg): parameters (cached),
+// row values and their stores (streaming); a store of a piece past the row is
+// left out.
+__device__ __forceinline__ void load4x2(const float * p0, const float * p1, float (&o)[kVec]) {
+    const f32x4 a = *reinterpret_cast<const f32x4 *>(p0);
+    const f32x4 b = *reinterpret_cast<const f32x4 *>(p1);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void load4x2(const uint16_t * p0, const uint16_t * p1, float (&o)[kVec]) {
+    const u16x4 a = *reinterpret_cast<const u16x4 *>(p0);
+    const u16x4 b = *reinterpret_cast<const u16x4 *>(p1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        o[k] = h2f(a[k]);
+        o[k + 4] = h2f(b[k]);
+    }
+}
+__device__ __forceinline__ void load4x2_row(const float * p0, const float * p1, float (&o)[kVec]) {
+    const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p0));
+    const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p1));
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+__device__ __forceinline__ void store4x2_row(float * p0, float * p1, const float (&v)[kVec], bool in0, bool in1) {
+    if (in0) __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4 *>(p0));
+    if (in1) __builtin_nontemporal_store(f32x4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4 *>(p1));
 }
 
 // Sum in double of this lane's values (kSquare: of their F32 squares) over
@@ -157,13 +174,29 @@ __global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T 
     const T * dr = kDelta ? d + row * dim : nullptr;
     T * hr = h_out ? h_out + row * dim : nullptr;
     T * yr = y + row * dim;
-    bool in[NV];
-    int off[NV];
+    // Group j of a lane: F16, 8 consecutive values (one 16-byte access per
+    // lane, contiguous across the wave); F32, two pieces of 4 values 64 * W
+    // pieces apart, so that each 16-byte access of the wave covers one
+    // contiguous KiB (8 consecutive floats per lane would leave every access
+    // at a 32-byte lane stride, two half-used cache lines per lane).
+    bool in[NV], in2[NV];
+    int off[NV], off2[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = (t + 64 * W * j) * kVec;
-        in[j] = e < dim;
-        off[j] = in[j] ? e : 0;
+        if constexpr (kF16) {
+            const int e = (t + 64 * W * j) * kVec;
+            in[j] = e < dim;
+            in2[j] = in[j];
+            off[j] = in[j] ? e : 0;
+            off2[j] = off[j] + 4;
+        } else {
+            const int e0 = (t + 64 * W * (2 * j)) * 4;
+            const int e1 = (t + 64 * W * (2 * j + 1)) * 4;
+            in[j] = e0 < dim;
+            in2[j] = e1 < dim;
+            off[j] = in[j] ? e0 : 0;
+            off2[j] = in2[j] ? e1 : 0;
+        }
     }
     float h[NV][kVec];
     float wv[NV][kVec];
@@ -171,14 +204,25 @@ __global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T 
     T xb[NV][kVec], db[NV][kVec];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        load8(w + off[j], wv[j]);
-        if constexpr (kLayer) load8(b + off[j], bv[j]);
+        if constexpr (kF16) {
+            load8(w + off[j], wv[j]);
+            if constexpr (kLayer) load8(b + off[j], bv[j]);
+        } else {
+            load4x2(w + off[j], w + off2[j], wv[j]);
+            if constexpr (kLayer) load4x2(b + off[j], b + off2[j], bv[j]);
+        }
     }
 #pragma unroll
-    for (int j = 0; j < NV; ++j) load8_row(xr + off[j], xb[j]);
+    for (int j = 0; j < NV; ++j) {
+        if constexpr (kF16) load8_row(xr + off[j], xb[j]);
+        else load4x2_row(xr + off[j], xr + off2[j], xb[j]);
+    }
     if constexpr (kDelta) {
 #pragma unroll
-        for (int j = 0; j < NV; ++j) load8_row(dr + off[j], db[j]);
+        for (int j = 0; j < NV; ++j) {
+            if constexpr (kF16) load8_row(dr + off[j], db[j]);
+            else load4x2_row(dr + off[j], dr + off2[j], db[j]);
+        }
     }
     if constexpr (kDelta) {
 #pragma unroll
@@ -190,10 +234,11 @@ __global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T 
             }
         }
     }
+    // a second piece past the row holds no value (F32; F16 groups are whole)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) h[j][k] = to_f32(xb[j][k]);
+        for (int k = 0; k < kVec; ++k) h[j][k] = k < 4 || in2[j] ? to_f32(xb[j][k]) : 0.0f;
     }
     double acc = lane_sum<NV, !kLayer>(h, in);
     // The residual is stored once every load has been consumed: stores share
@@ -201,8 +246,13 @@ __global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T 
     // for these stores.
     if (hr && valid) {
 #pragma unroll
-        for (int j = 0; j < NV; ++j)
-            if (in[j]) store8_row(hr + off[j], xb[j]);
+        for (int j = 0; j < NV; ++j) {
+            if constexpr (kF16) {
+                if (in[j]) store8_row(hr + off[j], xb[j]);
+            } else {
+                store4x2_row(hr + off[j], hr + off2[j], xb[j], in[j], in2[j]);
+            }
+        }
     }
     acc = row_sum<W>(acc, part[0], slot, wave, lane);
     float scale;
@@ -211,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T 
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
 #pragma unroll
-            for (int k = 0; k < kVec; ++k) h[j][k] = h[j][k] - mean;
+            for (int k = 0; k < kVec; ++k) h[j][k] = k < 4 || in2[j] ? h[j][k] - mean : 0.0f;
         }
         double acc2 = lane_sum<NV, true>(h, in);
         acc2 = row_sum<W>(acc2, part[1], slot, wave, lane);
@@ -224,19 +274,19 @@ __global__ __launch_bounds__(kThreads) void norm_kernel_wg(const T * x, const T 
     if (!valid) return;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        if (in[j]) {
-            float o[kVec];
+        float o[kVec];
 #pragma unroll
-            for (int k = 0; k < kVec; ++k)
-                o[k] = norm_out<T, kLayer>(h[j][k] * scale, wv[j][k], kLayer ? bv[j][k] : 0.0f);
-            if constexpr (kF16) {
+        for (int k = 0; k < kVec; ++k)
+            o[k] = norm_out<T, kLayer>(h[j][k] * scale, wv[j][k], kLayer ? bv[j][k] : 0.0f);
+        if constexpr (kF16) {
+            if (in[j]) {
                 uint16_t ob[kVec];
 #pragma unroll
                 for (int k = 0; k < kVec; ++k) ob[k] = f2h(o[k]);
                 store8_row(yr + off[j], ob);
-            } else {
-                store8_row(yr + off[j], o);
             }
+        } else {
+            store4x2_row(yr + off[j], yr + off2[j], o, in[j], in2[j]);
         }
     }
 }

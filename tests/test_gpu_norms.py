@@ -91,6 +91,42 @@ def test_flow_estimator_layernorm_full_shape(hip, dev, oracle):
 
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+@pytest.mark.parametrize("rows,D", [(1025, 2056), (1500, 3072), (1111, 4096)])
+def test_long_rows(hip, dev, oracle, f16, layer, rows, D):
+    """1024 rows or more of 2049-4096 elements (two waves per row): three and
+    four groups per lane, F32 groups as two 4-value pieces with the second
+    piece of the last groups past the row, row counts that leave the last
+    workgroup's second slot empty."""
+    x, d, w, b = _inputs(oracle, rows, D, rows * 3 + D, f16)
+    eps = 1e-5
+    h, y = _run(hip, dev, layer, x, d, w, b, eps)
+    if layer:
+        hw, yw = oracle.layer_norm(x, d, w, b, eps, threads=8)
+    else:
+        hw, yw = oracle.rms_norm(x, d, w, eps, threads=8)
+    assert np.array_equal(h, hw)
+    if f16:
+        assert f16_ulp(y, yw) <= 1
+    else:
+        assert f32_err(y, yw) <= 1e-5
+
+
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
+def test_long_rows_without_delta(hip, dev, oracle, layer):
+    """Two waves per F32 row with no residual input and no residual output."""
+    rows, D = 1200, 2200
+    x, d, w, b = _inputs(oracle, rows, D, 99, False)
+    zero = np.zeros_like(x)
+    _, y = _run(hip, dev, layer, x, d, w, b, 1e-5, with_delta=False, with_h=False)
+    if layer:
+        _, yw = oracle.layer_norm(x, zero, w, b, 1e-5, threads=8)
+    else:
+        _, yw = oracle.rms_norm(x, zero, w, 1e-5, threads=8)
+    assert f32_err(y, yw) <= 1e-5
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("layer", [False, True], ids=["rms", "ln"])
 @pytest.mark.parametrize("rows,D", [(514, 2048), (513, 2056), (600, 3072), (520, 4104), (515, 8192), (511, 1536),
                                     (7, 8192)])
 def test_row_layouts(hip, dev, oracle, f16, layer, rows, D):
