@@ -358,19 +358,24 @@ def bench_flow(torch, hip, head, dev, warmup, steps):
                       n_sets * nsteps, warmup, max(steps, 50))
     reps = max(1, steps // 5)
     solve_ms = time_op(torch, head, solve, n_sets, 1, reps)
-    # the same 50 launches captured once into a HIP graph and replayed
+    # the same 50 launches captured into a HIP graph per buffer set and
+    # replayed with the sets rotated as above, so both figures see the same
+    # cache state
     graph_ms = None
     try:
         stream = torch.cuda.Stream()
         stream.wait_stream(torch.cuda.current_stream())
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            solve(0)
+        graphs = []
+        for s_ in range(n_sets):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                solve(s_)
+            graphs.append(graph)
         torch.cuda.synchronize()
-        for _ in range(3):
+        for graph in graphs:
             graph.replay()
         torch.cuda.synchronize()
-        graph_ms = time_op(torch, head, lambda i: graph.replay(), 1, 1, reps)
+        graph_ms = time_op(torch, head, lambda i: graphs[i].replay(), n_sets, 1, reps)
     except Exception as e:  # graph capture is an extra measurement only
         log(f"flow graph capture skipped: {e}")
     e = op_entry(per, step_ms, read=12 * n_el, shape=[1, 64, 2520], dtype="f32",
