@@ -818,18 +818,20 @@ int launch_sample(const levo_hip_sample_args & a, hipStream_t stream) {
 //      k-th largest. A bisection over the survivors' keys gives t; the
 //      candidates at or above it are written in ascending id order, followed
 //      by the draw of levo_hip_sample_draw when the rows are few.
-// G = min(k, 64, ceil(3 k * 512 / V) + 6): three times the candidates a part
-// holds on average, plus six. With G >= k every part hands over at least its
-// own top k and the survivors always suffice; LeVo's k = 50 over 16385 ids
-// takes G = 11, and in simulations of Gaussian rows no row fell short.
-// A row with fewer than k survivors or more than the joining wave holds, a
+// G = min(k, 64, ceil(2.5 k * 512 / V) + 6): two and a half times the
+// candidates a part holds on average, plus six. With G >= k every part hands
+// over at least its own top k and the survivors always suffice; LeVo's k = 50
+// over 16384-16385 ids takes G = 10: in 20000 simulated Gaussian rows no row
+// fell short and none had more than 251 survivors (G = 9: 0.05% short; G = 11:
+// 0.22% above 256).
+// A row with fewer than k survivors or more than the joining wave holds (512), a
 // part with more than kPartCap ids at or above its bound (heavy ties), or
 // k = 0 takes select_general over the whole row in the join launch.
 constexpr int kPartIds = 512;                          // ids per part (one wave)
 constexpr int kPartPer = kPartIds / 64;                // ids per lane
 constexpr int kPartCap = 32;                           // handed-over ids per part
 constexpr int kMaxParts = kMaxVocab / kPartIds;        // parts of the longest row
-constexpr int kJoinCap = 256;                          // survivors the joining wave selects from
+constexpr int kJoinCap = 512;                          // survivors the joining wave selects from
 constexpr int kJoinFirst = 16;                         // slots per part the join reads before the heads arrive
 constexpr int kJoinDrawRows = 8;                       // rows whose draws the join launch makes
 constexpr int kEarlyChunks = (kJoinDrawRows - 1) * kMaxParts / 64;  // earlier rows' heads, 64 per chunk
@@ -880,7 +882,7 @@ step_ws carve_step_ws(void * ws, int64_t rows, int64_t vocab) {
 
 // Lane maxima at or above a part's bound (see above).
 __device__ __forceinline__ int part_groups(int k, int V) {
-    const int g = (3 * k * kPartIds + V - 1) / V + 6;
+    const int g = (5 * k * kPartIds + 2 * V - 1) / (2 * V) + 6;
     const int m = g < k ? g : k;
     return m < 64 ? m : 64;
 }
@@ -1119,6 +1121,63 @@ __device__ __forceinline__ int collect_survivors(const part_cand (&sl)[NS], int 
     return n;
 }
 
+// The exact k-th value of the nsurv survivors (sv / si, ascending ids; KT per
+// lane) and the candidates at or above it: their ids, logits and
+// probabilities written to the row's outputs, and to cv / ci in ascending id
+// order for the draw. Returns the candidate count.
+template <int KT>
+__device__ __forceinline__ int join_select(const levo_hip_sample_args & a, const float * sv, const int32_t * si,
+                                           float * cv, int32_t * ci, int nsurv, int k, uint32_t lo_key,
+                                           uint32_t hi_key, int64_t row, float rm, int best, int lane) {
+    uint32_t keys[KT];
+    bool valid[KT];
+    float cval[KT];
+    int32_t cid[KT];
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        const int idx = lane + 64 * t;
+        valid[t] = idx < nsurv;
+        const int at = valid[t] ? idx : 0;
+        cval[t] = sv[at];
+        cid[t] = si[at];
+        keys[t] = valid[t] ? float_key(cval[t]) : 0u;
+    }
+    const uint32_t tau = k > 1 ? wave_kth_key_slots<KT>(keys, k, lo_key, hi_key) : hi_key;
+    const bool want_probs = a.cand_probs != nullptr;
+    const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
+    bool take[KT];
+    int pos[KT];
+    float wgt[KT];
+    double z = 0.0;
+    int n = 0;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        take[t] = valid[t] && keys[t] >= tau;
+        const uint64_t mask = __ballot(take[t]);
+        pos[t] = n + rank_in_mask(mask);
+        n += static_cast<int>(__popcll(mask));
+        wgt[t] = want_probs && take[t] ? cand_weight(cval[t], rm, inv_t) : 0.0f;
+        z += static_cast<double>(wgt[t]);
+        if (take[t]) {
+            cv[pos[t]] = cval[t];
+            ci[pos[t]] = cid[t];
+        }
+    }
+    if (want_probs) z = wave_sum_f64(z);
+    const bool z_ok = z > 0.0 && __builtin_isfinite(z);
+    const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+        if (take[t] && pos[t] < a.capacity) {
+            const int64_t o = row * a.capacity + pos[t];
+            a.cand_ids[o] = cid[t];
+            if (a.cand_logits) a.cand_logits[o] = cval[t];
+            if (want_probs) a.cand_probs[o] = z_ok ? wgt[t] * inv_z : (cid[t] == best ? 1.0f : 0.0f);
+        }
+    }
+    return n;
+}
+
 struct join_lds {
     row_lds<kStepWords> L;                                   // the general path
     float sv[kJoinCap];                                      // survivors, ascending ids: values
@@ -1227,52 +1286,10 @@ __global__ __launch_bounds__(kThreads) void step_join_kernel(const levo_hip_samp
         int n = 0;
         if (fast) {
             wave_lds_order();
-            constexpr int kT = kJoinCap / 64;
-            uint32_t keys[kT];
-            bool valid[kT];
-            float cval[kT];
-            int32_t cid[kT];
-#pragma unroll
-            for (int t = 0; t < kT; ++t) {
-                const int idx = lane + 64 * t;
-                valid[t] = idx < nsurv;
-                const int at = valid[t] ? idx : 0;
-                cval[t] = S.sv[at];
-                cid[t] = S.si[at];
-                keys[t] = valid[t] ? float_key(cval[t]) : 0u;
-            }
-            const uint32_t tau = k > 1 ? wave_kth_key_slots<kT>(keys, k, lo_key, hi_key) : hi_key;
-            const bool want_probs = a.cand_probs != nullptr;
-            const float inv_t = want_probs ? 1.0f / a.temperature : 0.0f;
-            bool take[kT];
-            int pos[kT];
-            float wgt[kT];
-            double z = 0.0;
-#pragma unroll
-            for (int t = 0; t < kT; ++t) {
-                take[t] = valid[t] && keys[t] >= tau;
-                const uint64_t mask = __ballot(take[t]);
-                pos[t] = n + rank_in_mask(mask);
-                n += static_cast<int>(__popcll(mask));
-                wgt[t] = want_probs && take[t] ? cand_weight(cval[t], rm, inv_t) : 0.0f;
-                z += static_cast<double>(wgt[t]);
-                if (take[t]) {
-                    S.cv[pos[t]] = cval[t];
-                    S.ci[pos[t]] = cid[t];
-                }
-            }
-            if (want_probs) z = wave_sum_f64(z);
-            const bool z_ok = z > 0.0 && __builtin_isfinite(z);
-            const float inv_z = z_ok ? static_cast<float>(1.0 / z) : 0.0f;
-#pragma unroll
-            for (int t = 0; t < kT; ++t) {
-                if (take[t] && pos[t] < a.capacity) {
-                    const int64_t o = row * a.capacity + pos[t];
-                    a.cand_ids[o] = cid[t];
-                    if (a.cand_logits) a.cand_logits[o] = cval[t];
-                    if (want_probs) a.cand_probs[o] = z_ok ? wgt[t] * inv_z : (cid[t] == best ? 1.0f : 0.0f);
-                }
-            }
+            // 4 survivors per lane, or 8 for the rare rows with more than 256
+            n = nsurv <= kJoinCap / 2
+                    ? join_select<kJoinCap / 128>(a, S.sv, S.si, S.cv, S.ci, nsurv, k, lo_key, hi_key, row, rm, best, lane)
+                    : join_select<kJoinCap / 64>(a, S.sv, S.si, S.cv, S.ci, nsurv, k, lo_key, hi_key, row, rm, best, lane);
             if (lane == 0) {
                 a.best[row] = best;
                 a.count[row] = n;

@@ -195,6 +195,28 @@ def test_ties_and_k(hip, binding, dev, oracle, k):
     check_rows(got, cond, [k] * R, oracle, 0.9)
 
 
+def test_many_survivors(hip, binding, dev, oracle):
+    """A row whose handed-over ids at or above the largest part bound number
+    about 290 (the join's second tier, 8 survivors per lane): every part of
+    512 ids holds 20 large, distinct values in 20 lanes, so its bound (the
+    10th largest lane maximum at k = 50) hands over 10 of them, and the
+    largest bound keeps 9 per part. The second row is ordinary."""
+    V, R = 16385, 2
+    cond = _f16_logits(oracle, R, V, 3300)
+    for p in range(V // 512 + 1):
+        for l in range(20):
+            i = 512 * p + l
+            if i < V:
+                cond[0, i] = np.float32(100 + 0.01 * l + 1e-5 * p)
+    c = Case(binding, dev, cond, None, top_k=[50], n_streams=1, capacity=64)
+    bits = peek_bits(oracle, 33, 0, R)
+    want = c.two_launch(hip, bits)
+    got = c.step(hip, bits=bits)
+    same_outputs(got, want, c, draws=True)
+    check_rows(got, cond, [50] * R, oracle, 0.9)
+    assert got["count"][0] == 50
+
+
 def test_special_rows(hip, binding, dev, oracle):
     """NaN rows (best = count = -1, token -1), all -inf and +inf maxima (no
     draw), NaN in the last, partial part."""
