@@ -363,10 +363,14 @@ int launch_norm(const void * xv, const void * dv, const void * wv, const void * 
         // of 8 per lane: at 756 x 2048 RMS 4.18 -> 3.85 us and LayerNorm
         // 4.77 -> 4.39 us against one wave per row; at 1536 elements four
         // waves leave a quarter of the lanes idle and gain nothing); two or
-        // four waves for longer rows. A few rows (decode): four waves per
-        // row, so each lane's share and chain stay short.
+        // four waves for longer rows, except F32 rows of 2049-2560 elements
+        // (the Flow estimator's 2200), one wave each (five groups per lane,
+        // sums without LDS or barrier: 16.2 -> 15.8 us at 2000 x 2200). A
+        // few rows (decode): four waves per row, so each lane's share and
+        // chain stay short.
         const int groups = static_cast<int>(ceil_div(dim, 64 * kVec));
-        const int wpr = rows < 512 ? 4 : groups <= 3 ? 1 : groups == 4 ? 4 : groups <= 8 ? 2 : 4;
+        constexpr bool kF32 = std::is_same<T, float>::value;
+        const int wpr = rows < 512 ? 4 : groups <= 3 || (kF32 && groups == 5) ? 1 : groups == 4 ? 4 : groups <= 8 ? 2 : 4;
         const int nv = static_cast<int>(ceil_div(groups, wpr));
         const hipStream_t s = stream;
         const uint32_t grid_w = static_cast<uint32_t>(ceil_div(rows, 4 / wpr));
@@ -379,6 +383,7 @@ int launch_norm(const void * xv, const void * dv, const void * wv, const void * 
             if (nv == 1) LEVO_NORM_LAUNCH(1, 1);
             else if (nv == 2) LEVO_NORM_LAUNCH(2, 1);
             else if (nv == 3) LEVO_NORM_LAUNCH(3, 1);
+            else if (nv == 5) LEVO_NORM_LAUNCH(5, 1);
             else LEVO_NORM_LAUNCH(4, 1);
         } else if (wpr == 2) {
             if (nv == 3) LEVO_NORM_LAUNCH(3, 2);  // 2049-3072 elements: no idle fourth group of registers
