@@ -1075,6 +1075,15 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     order.append(("rmsnorm_f16_756x2048", 8 * rows * D + 2 * D))
     hip.layer_norm(1, xh, dh, w, w, 1, hh, yh, rows, D, 1e-6)
     order.append(("layernorm_f16_756x2048", 8 * rows * D + 4 * D))
+    del xh, dh, hh, yh
+    rows, D = 2000, 2200  # the Flow estimator's F32 LayerNorm
+    xf = torch.randn((rows, D), generator=g, device=dev)
+    df = torch.randn((rows, D), generator=g, device=dev)
+    wf = torch.ones(D, device=dev)
+    hf, yf = torch.empty_like(xf), torch.empty_like(xf)
+    hip.layer_norm(0, xf, df, wf, wf, 0, hf, yf, rows, D, 1e-5)
+    order.append(("layernorm_f32_2000x2200", 16 * rows * D + 8 * D))
+    del xf, df, hf, yf
     n = 64 * 2520
     st, vu, vc = (torch.randn(n, generator=g, device=dev) for _ in range(3))
     hip.flow_cfg_euler(st, vu, vc, n, 1.5, 0.02)
