@@ -3,10 +3,11 @@
 
 Headline workload (one "step"): the SnakeBeta ladder of one 10.08 s Oobleck
 VAE window, F32 (C, T) = (2048,252), (1024,504), (512,2016), (256,8064),
-(128,48384), (128,483840), one kernel launch per shape as the decoder issues
-them, x ~ N(0,1), per-channel log-parameters ~ U(-0.5, 0.5), inputs resident
-in HBM. `value` = ladder algorithmic bytes (read x + write y + parameters) per
-step / wall time per step.
+(128,48384), (128,483840), all six shapes in one batched launch
+(levo_hip_snake_beta_batch; six single launches are timed beside it),
+x ~ N(0,1), per-channel log-parameters ~ U(-0.5, 0.5), inputs resident in
+HBM. `value` = ladder algorithmic bytes (read x + write y + parameters) per
+step / time per step.
 
 Also reported, per op (rotated buffer sets so that every timed launch reads
 data untouched for >= 512 MB of traffic, i.e. from HBM, not the 256 MB
@@ -18,7 +19,13 @@ queued first keeps the GPU busy while the host enqueues each timed region, so
 the timed launches run back to back.
 
 The CPU baseline is the CPU oracle (a port of the reference's ggml-cpu op
-chains; ggml itself is not available) run on a bounded sample on this host.
+chains; ggml itself is not available) on this host's cores: the whole ladder
+at every thread of the process's CPU share, a 32-channel slice of one rung at
+one thread, and each other op at 1 and all threads.
+
+The last stdout line is the JSON result: headline, roofline, the CPU leg and
+a one-entry-per-op summary, kept under LINE_BUDGET bytes; the full per-op and
+CPU tables go to --ops-out.
 """
 from __future__ import annotations
 
@@ -1189,6 +1196,88 @@ def host_dropin_references(gpu):
 
 OP_GROUPS = ("snake", "flow", "norm", "sample", "quant", "gemv", "conv", "vae")
 
+# The result line is the last line of stdout and has to stay small enough for
+# a log tail to hold it whole; the full per-op tables go to a file instead.
+LINE_BUDGET = 7168
+
+
+def ops_summary(ops):
+    """One [us per launch, GB/s, fraction of 8 TB/s, fraction of the streaming
+    ceiling] entry per timed op ("group/name" for nested tables). Entries
+    without an HBM figure (MFMA-bound convolutions, whole decoder windows)
+    carry [us, TFLOP/s, fraction of the F32 MFMA peak, null]."""
+    out = {}
+
+    def num(v, nd):
+        return None if v is None else round(float(v), nd)
+
+    def visit(name, e):
+        if not isinstance(e, dict):
+            return
+        us = e.get("us_per_launch")
+        if us is None and "ms_per_step" in e:
+            us = e["ms_per_step"] * 1e3
+        if us is None and "ms_per_window" in e:
+            us = e["ms_per_window"] * 1e3
+        if us is not None and ("GB/s" in e or "TFLOP/s" in e):
+            if e.get("bound") == "mfma" or ("GB/s" not in e):
+                out[name] = [num(us, 2), num(e.get("TFLOP/s"), 1), num(e.get("frac_f32_mfma"), 3), None]
+            else:
+                out[name] = [num(us, 2), num(e["GB/s"], 1), num(e.get("frac"), 3), num(e.get("of_ceiling"), 3)]
+            return
+        for k, v in e.items():
+            visit(f"{name}/{k}" if name else k, v)
+
+    visit("", {k: v for k, v in ops.items() if k != "host_dropins"})
+    return out
+
+
+def compact_cpu(cpu):
+    """The CPU leg without its per-op sample descriptions: headline keys plus
+    [1-thread GB/s, all-threads GB/s] per op."""
+    if not cpu:
+        return cpu
+    keep = ("value", "unit", "cores", "kind", "sample", "ms_per_step", "method")
+    out = {k: cpu[k] for k in keep if k in cpu}
+    if "one_thread" in cpu:
+        out["one_thread"] = {k: cpu["one_thread"][k] for k in ("value", "unit", "cores", "sample")
+                             if k in cpu["one_thread"]}
+    if "cpu" in cpu:
+        out["cpu_model"] = cpu["cpu"].get("model")
+    if "ops" in cpu:
+        per = {}
+        for name, e in cpu["ops"].items():
+            if not isinstance(e, dict):
+                continue
+            all_key = next((k for k in e if k.endswith("_threads_GB/s")), None)
+            per[name] = [e.get("1_thread_GB/s"), e.get(all_key) if all_key else None]
+        out["ops_GBps_1_and_all_threads"] = per
+    return out
+
+
+def final_line(full, ops_file=None):
+    """The JSON result line: headline keys, config, roofline, the compact CPU
+    leg and one short entry per op. Falls back to dropping the op summary if
+    the line would exceed LINE_BUDGET bytes, so the headline always fits."""
+    line = {k: v for k, v in full.items() if k not in ("ops", "cpu_baseline")}
+    line["cpu_baseline"] = compact_cpu(full.get("cpu_baseline"))
+    if full.get("ops"):
+        line["ops_summary_fields"] = ["us", "GB/s (TFLOP/s if MFMA-bound)", "frac of 8 TB/s (of F32 MFMA peak)",
+                                      "of streaming ceiling"]
+        line["ops_summary"] = ops_summary(full["ops"])
+        if ops_file:
+            line["ops_full_table"] = os.path.relpath(ops_file, ROOT)
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text.encode()) > LINE_BUDGET:
+        log(f"result line {len(text)} B exceeds {LINE_BUDGET} B: op summary left to the full table")
+        line.pop("ops_summary", None)
+        line.pop("ops_summary_fields", None)
+        line["ops_summary_dropped"] = True
+        text = json.dumps(line, separators=(",", ":"))
+    if len(text.encode()) > LINE_BUDGET:
+        raise SystemExit(f"bench.py: result line of {len(text)} B exceeds {LINE_BUDGET} B")
+    return text
+
 
 def run_ops(torch, hip, binding, head, dev, args, groups):
     """The op table: every group in `groups`, the same shapes whether run
@@ -1247,6 +1336,9 @@ def main() -> int:
                    help="with --only: annotate each op with the plain streaming ceiling of its bytes and mix")
     p.add_argument("--traffic-probe", action="store_true",
                    help="one launch per kernel + a 256 MiB copy, for rocprofv3 --pmc runs")
+    p.add_argument("--ops-out", default=os.path.join(ROOT, "gpurun_out", "bench_ops.json"),
+                   help="file for the full per-op and CPU tables (the result line carries a summary); "
+                        "empty to skip")
     args = p.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -1314,7 +1406,7 @@ def main() -> int:
         log("cpu baseline: done")
 
     value = lad["ladder_bytes"] / (lad["ms_per_step"] * 1e-3) / 1e9
-    line = {
+    full = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(lad["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
@@ -1327,7 +1419,12 @@ def main() -> int:
         "cpu_baseline": cpu,
         "ops": ops,
     }
-    print(json.dumps(line))
+    if args.ops_out:
+        os.makedirs(os.path.dirname(os.path.abspath(args.ops_out)), exist_ok=True)
+        with open(args.ops_out, "w") as fh:
+            json.dump(full, fh, indent=1)
+        log(f"full op and CPU tables: {args.ops_out}")
+    print(final_line(full, ops_file=args.ops_out or None))
     return 0
 
 

@@ -17,17 +17,33 @@
 #include <string>
 #include <utility>
 
+// The cancellation exception. Built inside the reference tree with
+// -DLEVO_HIP_WITH_LEVO_H and the reference's include/ directory on the include
+// path, the wrappers throw the reference's own levo::operation_cancelled
+// (include/levo.h:21-24), so its catch sites (src/levo-flow-renderer.cpp:249,
+// 325; src/cantor-abi.cpp:909) match unchanged. Built standalone, the library
+// defines a class of its own with the same base and message.
+#if defined(LEVO_HIP_WITH_LEVO_H)
+#include <levo.h>
+
 namespace levo::hip {
-
-using stream_t = hipStream_t;
-
-// Thrown when the cancellation callback returns true (include/levo.h:21-26).
+using operation_cancelled = ::levo::operation_cancelled;
+using cancellation_callback = ::levo::cancellation_callback;
+} // namespace levo::hip
+#else
+namespace levo::hip {
 class operation_cancelled : public std::runtime_error {
 public:
     operation_cancelled() : std::runtime_error("LeVo operation cancelled") {}
 };
 
 using cancellation_callback = std::function<bool()>;
+} // namespace levo::hip
+#endif
+
+namespace levo::hip {
+
+using stream_t = hipStream_t;
 
 // Throws std::runtime_error("LeVo HIP: <what>: <HIP error>") if status is not hipSuccess.
 void check_hip(hipError_t status, const char * what);
