@@ -370,9 +370,12 @@ int levo_hip_sample_step(const levo_hip_sample_args * args, const levo_hip_draw_
  * it runs on, until the process ends (enough for 230 rows of 16385 logits;
  * larger calls fail with LEVO_HIP_ERR_INVALID, naming the sizes). Same
  * results as levo_hip_sample_step. Calls that overlap on one GPU share that
- * array and race: serialize them. No counterpart in the reference: it is for
- * callers that cannot allocate device memory (HIP graph capture, serving
- * loops that forbid hipMalloc). */
+ * array and race: serialize them. The first call on each GPU looks the
+ * array's address up (hipGetSymbolAddress, which may load the code object):
+ * make that first call outside stream capture, e.g. one eager call before
+ * capturing; later calls only launch kernels. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (HIP graph
+ * capture, serving loops that forbid hipMalloc). */
 int levo_hip_sample_step_static(const levo_hip_sample_args * args, const levo_hip_draw_args * draw,
                                 levo_hip_stream_t stream);
 

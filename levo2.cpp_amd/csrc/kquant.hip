@@ -188,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void dequantize_kquant_kernel(const uint8
                 const uint32_t hw2 = l < 4 ? qh.x : qh.y;
                 code += ((hw2 >> (8 * (l & 3) + j)) & 1u) ? 16 : 0;
             }
-            out[l] = __builtin_fmaf(d1, static_cast<float>(code), -m1);
+            out[l] = d1 * static_cast<float>(code) - m1;
         }
     }
     Out * o = dst + i * kQK + 32 * j + 8 * p;

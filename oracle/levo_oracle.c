@@ -1113,8 +1113,10 @@ void lo_quantize_row_q6_K(const float * x, void * out, int64_t k) {
 }
 
 /* dequantize_row_q4_K / q5_K: y = d1 * q - m1 with d1 = d * sc, m1 = dmin * m,
- * the last step in one rounding (fmaf), as ggml's backends are compiled
- * (floating-point contraction on). */
+ * every operation rounded on its own (ggml-base built for the baseline x86-64
+ * ISA, as for the quantizers). d (F16, 11 significant bits) times a 6-bit scale
+ * times a code below 32 needs at most 22 bits, so d1 * q is exact in F32 and a
+ * contracted build gives the same bits. */
 void lo_dequantize_row_q4_K(const void * in, float * y, int64_t k) {
     const unsigned char * x = (const unsigned char *)in;
     for (int64_t i = 0; i < k / 256; ++i) {
@@ -1128,8 +1130,8 @@ void lo_dequantize_row_q4_K(const void * in, float * y, int64_t k) {
             lo_scale_min_k4(2 * j + 1, sc, &s1, &m1);
             const float d1 = d * (float)s0, mn1 = min * (float)m0;
             const float d2 = d * (float)s1, mn2 = min * (float)m1;
-            for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float)(q[l] & 0xF), -mn1);
-            for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float)(q[l] >> 4), -mn2);
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] & 0xF) - mn1;
+            for (int l = 0; l < 32; ++l) *y++ = d2 * (float)(q[l] >> 4) - mn2;
         }
     }
 }
@@ -1149,8 +1151,8 @@ void lo_dequantize_row_q5_K(const void * in, float * y, int64_t k) {
             lo_scale_min_k4(2 * j + 1, sc, &s1, &m1);
             const float d1 = d * (float)s0, mn1 = min * (float)m0;
             const float d2 = d * (float)s1, mn2 = min * (float)m1;
-            for (int l = 0; l < 32; ++l) *y++ = fmaf(d1, (float)((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)), -mn1);
-            for (int l = 0; l < 32; ++l) *y++ = fmaf(d2, (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)), -mn2);
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)((ql[l] & 0xF) + ((qh[l] & u1) ? 16 : 0)) - mn1;
+            for (int l = 0; l < 32; ++l) *y++ = d2 * (float)((ql[l] >> 4) + ((qh[l] & u2) ? 16 : 0)) - mn2;
         }
     }
 }

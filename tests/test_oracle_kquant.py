@@ -350,3 +350,56 @@ def test_quantize_search_beats_plain_rounding(oracle):
     step = np.abs(xs).max(1)[:, None] / 31.5
     plain = np.clip(np.round(xs / step), -32, 31) * step
     assert np.sqrt(np.mean((deq - xs) ** 2)) <= 0.9 * np.sqrt(np.mean((plain - xs) ** 2))
+
+
+def _finite_f16():
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    return h[np.isfinite(h)].astype(np.float32)
+
+
+def test_dequantize_products_exact_for_every_scale():
+    """Why the dequantizers cannot depend on floating-point contraction.
+    Q4_K / Q5_K compute d1 * q - m1 with d1 = d * sc, m1 = dmin * m, d and
+    dmin F16, sc and m in [0, 63], q in [0, 31]; Q6_K computes d * sc * q
+    with sc an int8 and q in [-32, 31]. Over every finite F16 d, every scale
+    and every code, each F32 product equals the exact (float64) product, so
+    an FMA for the last step rounds exactly as a multiply then a subtract,
+    and an F32 product never rounds. Exhaustive: 63,488 x 64 x 32 (Q4_K/Q5_K)
+    and 63,488 x 256 x 64 (Q6_K) products."""
+    d = _finite_f16()
+    for scales, codes in ((np.arange(64), range(32)), (np.arange(-128, 128), range(-32, 32))):
+        sc = scales.astype(np.float32)
+        for lo in range(0, d.size, 2048):  # chunks of 2048 F16 values keep each array at a few MB
+            dd = d[lo:lo + 2048, None]
+            d1 = dd * sc[None, :]
+            assert np.array_equal(d1.astype(np.float64), dd.astype(np.float64) * sc[None, :])
+            d1_64 = d1.astype(np.float64)
+            for q in codes:
+                assert np.array_equal((d1 * np.float32(q)).astype(np.float64), d1_64 * q), (lo, q)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K])
+def test_dequantize_non_representable_scales(oracle, qtype):
+    """Blocks with F16 d, dmin whose products with the scales and codes fill
+    all 22 product bits (no power-of-two scales): every value equals the
+    float32 multiply-then-subtract, which by the exactness above is also the
+    correctly rounded d1 * q - m1 computed in float64."""
+    rng = np.random.default_rng(100 + qtype)
+    pack = pack_q4_K if qtype == Q4_K else pack_q5_K
+    top = 16 if qtype == Q4_K else 32
+    blocks, want = [], []
+    for _ in range(16):
+        d = np.float16(rng.uniform(1e-4, 2.0))
+        dmin = np.float16(rng.uniform(1e-4, 2.0))
+        sc = rng.integers(33, 64, 8)
+        mn = rng.integers(33, 64, 8)
+        codes = rng.integers(0, top, 256).astype(np.uint8)
+        d1 = np.float32(d) * np.repeat(sc, 32).astype(np.float32)
+        m1 = np.float32(dmin) * np.repeat(mn, 32).astype(np.float32)
+        w32 = d1 * codes.astype(np.float32) - m1
+        exact = (d1.astype(np.float64) * codes - m1.astype(np.float64)).astype(np.float32)
+        assert np.array_equal(w32, exact)
+        blocks.append(pack(float(d), float(dmin), sc, mn, codes))
+        want.append(w32)
+    got = oracle.dequantize_kquant(qtype, np.concatenate(blocks), 256 * len(blocks))
+    assert np.array_equal(got.view(np.uint32), np.concatenate(want).view(np.uint32))
