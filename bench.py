@@ -483,6 +483,51 @@ def bench_norm(torch, hip, head, dev, warmup, steps, layer, rows, D, f16=True):
                     dtype=("f16" if f16 else "f32") + " io / f32 accumulate")
 
 
+def modulated_norm_args(torch, binding, dev, g, rows, D, rpb, x, d, h, y, keep):
+    """levo_hip_modulated_norm_args of a Flow estimator block boundary: gate /
+    scale / shift are chunks 2 / 4 / 3 of a [batch][6 D] time modulation plus
+    the block's learned [6 D] table (modulation_chunk)."""
+    batches = rows // rpb
+    tm = torch.randn((batches, 6 * D), generator=g, device=dev) * 0.3
+    table = torch.randn(6 * D, generator=g, device=dev) * 0.3
+    gamma = torch.randn(D, generator=g, device=dev) * 0.02 + 1
+    beta = torch.randn(D, generator=g, device=dev) * 0.02
+    keep.extend([tm, table, gamma, beta])
+    vec = lambda k: binding.BatchVector(tm.data_ptr() + 4 * k * D, 6 * D, table.data_ptr() + 4 * k * D)
+    a = binding.ModulatedNormArgs()
+    a.x, a.delta, a.gate = x.data_ptr(), d.data_ptr(), vec(2)
+    a.gamma, a.beta, a.param_type = gamma.data_ptr(), beta.data_ptr(), 0
+    a.scale, a.shift = vec(4), vec(3)
+    a.h_out, a.y = h.data_ptr(), y.data_ptr()
+    a.rows, a.rows_per_batch, a.dim, a.eps = rows, rpb, D, 1e-5
+    return a
+
+
+def bench_norm_modulated(torch, hip, binding, head, dev, warmup, steps):
+    """The Flow estimator's block boundary, [2 x 1000 frames, 2200] F32: gated
+    residual + LayerNorm + AdaLN modulation in one launch
+    (levo_hip_residual_layer_norm_modulated)."""
+    rows, D, rpb = 2000, 2200, 1000
+    row_bytes = 16 * rows * D                 # read x, delta; write h, y
+    vec_bytes = 8 * D + 3 * (2 * D * 4 + D * 4)  # gamma, beta; 3 x (2 dynamic rows + learned)
+    per = row_bytes + vec_bytes
+    n = math.ceil(ROTATE_BYTES / per) + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(2200)
+    keep = []
+    args = []
+    for _ in range(n):
+        x, d = torch.randn((rows, D), generator=g, device=dev), torch.randn((rows, D), generator=g, device=dev)
+        h, y = torch.empty_like(x), torch.empty_like(x)
+        keep.extend([x, d, h, y])
+        args.append(modulated_norm_args(torch, binding, dev, g, rows, D, rpb, x, d, h, y, keep))
+    ms = time_op(torch, head, lambda i: hip.layer_norm_modulated(args[i]), n, warmup, max(steps, 50))
+    e = op_entry(per, ms, read=per - 8 * rows * D, shape=[rows, D], dtype="f32 io / f32 accumulate")
+    e["replaces"] = ("ggml_mul(out, gate), ggml_add(., residual), ggml_norm, ggml_mul(gamma), ggml_add(beta), "
+                     "ggml_mul(1 + scale), ggml_add(shift): 3 full-tensor passes with the plain fused LayerNorm")
+    return e
+
+
 def bench_sample(torch, hip, binding, head, dev, warmup, steps):
     P, S, V, cap = 750, 3, 16384, 64
     rows = P * S
@@ -1073,16 +1118,16 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     hip.snake_beta_batch(jobs)
     order.append(("snake_beta_batch_ladder", sum(snake_bytes(C, T) for C, T in LADDER)))
     del jobs
-    rows, D = 756, 2048
-    xh = torch.randn((rows, D), generator=g, device=dev).half()
-    dh = torch.randn((rows, D), generator=g, device=dev).half()
-    w = torch.ones(D, device=dev).half()
-    hh, yh = torch.empty_like(xh), torch.empty_like(xh)
-    hip.rms_norm(1, xh, dh, w, 1, hh, yh, rows, D, 1e-6)
-    order.append(("rmsnorm_f16_756x2048", 8 * rows * D + 2 * D))
-    hip.layer_norm(1, xh, dh, w, w, 1, hh, yh, rows, D, 1e-6)
-    order.append(("layernorm_f16_756x2048", 8 * rows * D + 4 * D))
-    del xh, dh, hh, yh
+    for rows, D in ((756, 2048), (756, 1536)):
+        xh = torch.randn((rows, D), generator=g, device=dev).half()
+        dh = torch.randn((rows, D), generator=g, device=dev).half()
+        w = torch.ones(D, device=dev).half()
+        hh, yh = torch.empty_like(xh), torch.empty_like(xh)
+        hip.rms_norm(1, xh, dh, w, 1, hh, yh, rows, D, 1e-6)
+        order.append((f"rmsnorm_f16_{rows}x{D}", 8 * rows * D + 2 * D))
+        hip.layer_norm(1, xh, dh, w, w, 1, hh, yh, rows, D, 1e-6)
+        order.append((f"layernorm_f16_{rows}x{D}", 8 * rows * D + 4 * D))
+        del xh, dh, hh, yh
     rows, D = 2000, 2200  # the Flow estimator's F32 LayerNorm
     xf = torch.randn((rows, D), generator=g, device=dev)
     df = torch.randn((rows, D), generator=g, device=dev)
@@ -1090,7 +1135,11 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     hf, yf = torch.empty_like(xf), torch.empty_like(xf)
     hip.layer_norm(0, xf, df, wf, wf, 0, hf, yf, rows, D, 1e-5)
     order.append(("layernorm_f32_2000x2200", 16 * rows * D + 8 * D))
-    del xf, df, hf, yf
+    keep = []
+    a = modulated_norm_args(torch, binding, dev, g, rows, D, 1000, xf, df, hf, yf, keep)
+    hip.layer_norm_modulated(a)
+    order.append(("gated_layernorm_adaln_f32_2000x2200", 16 * rows * D + 8 * D + 3 * 12 * D))
+    del xf, df, hf, yf, keep
     n = 64 * 2520
     st, vu, vc = (torch.randn(n, generator=g, device=dev) for _ in range(3))
     hip.flow_cfg_euler(st, vu, vc, n, 1.5, 0.02)
@@ -1103,6 +1152,11 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     deq = torch.empty((R, Cc), device=dev)
     hip.dequantize(8, q, deq, 0, R * Cc)
     order.append(("q8_0_dequantize_f32", q.numel() + 4 * R * Cc))
+    q4 = torch.empty(R * Cc // 32 * 18, dtype=torch.uint8, device=dev)
+    hip.quantize_rows(2, wq, 1, Cc, Cc, q4, R, Cc)
+    order.append(("q4_0_quantize_f16", 2 * R * Cc + q4.numel()))
+    hip.dequantize(2, q4, deq, 0, R * Cc)
+    order.append(("q4_0_dequantize_f32", q4.numel() + 4 * R * Cc))
     P, S, V = 750, 3, 16384
     c = torch.randn((P * S, V), generator=g, device=dev) * 3
     u = torch.randn((P * S, V), generator=g, device=dev) * 3
@@ -1299,6 +1353,9 @@ def run_ops(torch, hip, binding, head, dev, args, groups):
                 ops[f"residual_{name}_f16_{rows}x{D}"] = bench_norm(torch, hip, head, dev, w, k, layer, rows, D)
         log("ops: layernorm f32 2000x2200 (Flow estimator)")
         ops["residual_layernorm_f32_2000x2200"] = bench_norm(torch, hip, head, dev, w, k, True, 2000, 2200, f16=False)
+        log("ops: gated residual + layernorm + modulation f32 2000x2200 (Flow estimator block boundary)")
+        ops["gated_residual_layernorm_adaln_f32_2000x2200"] = bench_norm_modulated(torch, hip, binding, head, dev,
+                                                                                   w, k)
     if "sample" in groups:
         log("ops: cfg sample")
         ops["cfg_softmax_top50_750x3x16384"] = bench_sample(torch, hip, binding, head, dev, w, k)

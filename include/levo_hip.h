@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LEVO_HIP_ABI_VERSION 3
+#define LEVO_HIP_ABI_VERSION 4
 
 /* Same tag as HIP's hipStream_t, so a hipStream_t converts without a cast. */
 typedef struct ihipStream_t * levo_hip_stream_t;
@@ -242,6 +242,44 @@ int levo_hip_residual_layer_norm(levo_hip_type act_type, const void * x, const v
                                  const void * gamma, const void * beta, levo_hip_type param_type,
                                  void * h_out, void * y, int64_t rows, int64_t dim, float eps,
                                  levo_hip_stream_t stream);
+
+/* One per-batch vector of the Flow estimator's modulation
+ * (modulation_chunk, src/levo-flow-estimator.cpp:95-104): entry b, channel c
+ * is dynamic[b * stride + c] + learned[c] (ggml_add(dynamic, learned)), or
+ * dynamic[b * stride + c] when learned is NULL. dynamic NULL: no vector. */
+typedef struct levo_hip_batch_vector {
+    const float * dynamic;  /* [batches] entries of dim floats, `stride` floats apart */
+    int64_t stride;
+    const float * learned;  /* [dim], or NULL */
+} levo_hip_batch_vector;
+
+typedef struct levo_hip_modulated_norm_args {
+    const float * x;              /* [rows][dim] F32 residual stream */
+    const float * delta;          /* [rows][dim] branch output, or NULL (h = x) */
+    levo_hip_batch_vector gate;   /* h = (delta * gate) + x; no gate: h = x + delta */
+    const void * gamma;           /* [dim] */
+    const void * beta;            /* [dim] */
+    levo_hip_type param_type;     /* F32 or F16 gamma / beta */
+    levo_hip_batch_vector scale;  /* y = (t * (scale + 1)) + shift; no scale: y = t */
+    levo_hip_batch_vector shift;  /* given exactly when scale is */
+    float * h_out;                /* [rows][dim], or NULL */
+    float * y;                    /* [rows][dim] */
+    int64_t rows;                 /* a multiple of rows_per_batch */
+    int64_t rows_per_batch;       /* row r uses batch entry r / rows_per_batch */
+    int64_t dim;                  /* a multiple of 4, at most 4096 */
+    float eps;
+} levo_hip_modulated_norm_args;
+
+/* A Flow estimator block boundary in one pass, one rounding per ggml op as the
+ * graph computes it: the gated residual current = (out * gate) + residual
+ * (src/levo-flow-estimator.cpp:221-227, 243-246), layer_norm
+ * t = (norm(current, eps) * gamma) + beta (:106-109) and add_scale_shift
+ * y = (t * (scale + 1)) + shift (:89-93, at :214, :233, :260). h_out receives
+ * current (the next residual). x, delta, h_out, y, gamma, beta and each
+ * vector's rows are 16-byte aligned (8-byte for F16 gamma / beta); x may be
+ * h_out (in place). */
+int levo_hip_residual_layer_norm_modulated(const levo_hip_modulated_norm_args * args,
+                                           levo_hip_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* CFG combine + temperature softmax + argmax / top-k (LeLM sampling)        */

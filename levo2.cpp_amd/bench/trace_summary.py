@@ -29,6 +29,12 @@ and prints the table:
 
     python3 levo2.cpp_amd/bench/trace_summary.py --traffic <fetch_counter_collection.csv>
         <write_counter_collection.csv> <probe stdout> <traffic.json> > traffic.md
+
+With --issue, per launch of the same probe from one rocprofv3 --pmc run of SQ
+counters: waves, instructions per wave by kind, wave lifetime and the share
+of it spent issuing VALU work:
+
+    python3 levo2.cpp_amd/bench/trace_summary.py --issue <sq_counter_collection.csv> <probe stdout> > issue.md
 """
 from __future__ import annotations
 
@@ -198,8 +204,48 @@ def vae_traffic(fetch_csv: str, write_csv: str, traffic_json: str, frames: str) 
     return rows
 
 
+def issue(sq_csv: str, probe_log: str) -> list[str]:
+    """Per launch of bench.py --traffic-probe, from one rocprofv3 --pmc run of
+    SQ_WAVES, SQ_INSTS_VALU, SQ_INSTS_SALU, SQ_INSTS_VMEM_RD, SQ_INSTS_LDS,
+    SQ_WAVE_CYCLES, SQ_ACTIVE_INST_VALU, SQ_BUSY_CYCLES (+ GRBM_GUI_ACTIVE):
+    instructions per wave, a wave's average lifetime and the share of it spent
+    issuing VALU work (SQ_ACTIVE_INST_VALU / SQ_WAVE_CYCLES, both in the same
+    per-wave cycle units)."""
+    order = None
+    for line in open(probe_log):
+        if "traffic_probe_launch_order" in line:
+            order = json.loads(line[line.index("{"):])["traffic_probe_launch_order"]
+    per = defaultdict(dict)
+    names = {}
+    for r in csv.DictReader(open(sq_csv)):
+        n = r["Kernel_Name"]
+        if not ("levo_hip::" in n or "copyBuffer" in n):
+            continue
+        did = int(r["Dispatch_Id"])
+        per[did][r["Counter_Name"]] = per[did].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        names[did] = n
+    ids = sorted(per)
+    if order is None or len(ids) != len(order):
+        raise SystemExit(f"launch counts differ: order {None if order is None else len(order)}, counted {len(ids)}")
+    rows = ["| launch | kernel | waves | VALU / wave | SALU / wave | VMEM rd / wave | LDS / wave | "
+            "wave lifetime (cycles) | VALU-active share of lifetime |",
+            "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for (name, _), did in zip(order, ids):
+        c = per[did]
+        waves = c.get("SQ_WAVES", 0.0) or 1.0
+        life = c.get("SQ_WAVE_CYCLES", 0.0) / waves
+        act = c.get("SQ_ACTIVE_INST_VALU", 0.0) / max(c.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+        kname = short_name(names[did]) or names[did].split("(")[0].strip()
+        rows.append(f"| {name} | `{kname}` | {int(waves):,} | {c.get('SQ_INSTS_VALU', 0) / waves:.1f} | "
+                    f"{c.get('SQ_INSTS_SALU', 0) / waves:.1f} | {c.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} | "
+                    f"{c.get('SQ_INSTS_LDS', 0) / waves:.1f} | {life:.0f} | {act:.3f} |")
+    return rows
+
+
 if __name__ == "__main__":
-    if sys.argv[1] == "--traffic":
+    if sys.argv[1] == "--issue":
+        print("\n".join(issue(sys.argv[2], sys.argv[3])))
+    elif sys.argv[1] == "--traffic":
         print("\n".join(traffic(*sys.argv[2:6])))
     elif sys.argv[1] == "--vae-trace":
         print("\n".join(vae_trace(sys.argv[2])))

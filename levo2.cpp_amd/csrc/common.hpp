@@ -240,6 +240,19 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Makes the values of `v` present in registers at this point: the wait for the
+// loads that produced them (and any conversion) happens here, not where they
+// are first used. Stores and loads share one vector-memory counter on this
+// GPU, so a wait for a load issued before a store also waits until that store
+// has completed; calling this after the last load is issued and before the
+// first store keeps every load wait ahead of every store. The memory clobber
+// keeps loads above and stores below this point.
+template <typename T, int N>
+__device__ __forceinline__ void consume_now(T (&v)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) asm volatile("" : "+v"(v[k])::"memory");
+}
+
 // Bits of lanes below the calling lane in a 64-bit ballot mask.
 __device__ __forceinline__ int rank_in_mask(uint64_t mask) {
     return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),

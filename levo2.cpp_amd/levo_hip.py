@@ -85,6 +85,22 @@ class FlowStepArgs(ctypes.Structure):
     ]
 
 
+class BatchVector(ctypes.Structure):
+    """levo_hip_batch_vector (include/levo_hip.h)."""
+
+    _fields_ = [("dynamic", _P), ("stride", _I64), ("learned", _P)]
+
+
+class ModulatedNormArgs(ctypes.Structure):
+    """levo_hip_modulated_norm_args (include/levo_hip.h)."""
+
+    _fields_ = [
+        ("x", _P), ("delta", _P), ("gate", BatchVector), ("gamma", _P), ("beta", _P), ("param_type", ctypes.c_int),
+        ("scale", BatchVector), ("shift", BatchVector), ("h_out", _P), ("y", _P), ("rows", _I64),
+        ("rows_per_batch", _I64), ("dim", _I64), ("eps", _F),
+    ]
+
+
 class SnakeJob(ctypes.Structure):
     """levo_hip_snake_job (include/levo_hip.h)."""
 
@@ -178,6 +194,7 @@ class LevoHip:
                                                           _I64, _I64, _F, _P]),
             "levo_hip_residual_layer_norm": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P,
                                                             _I64, _I64, _F, _P]),
+            "levo_hip_residual_layer_norm_modulated": (ctypes.c_int, [ctypes.POINTER(ModulatedNormArgs), _P]),
             "levo_hip_cfg_combine": (ctypes.c_int, [_P, _P, _P, _I64, _F, _P]),
             "levo_hip_cfg_sample": (ctypes.c_int, [ctypes.POINTER(SampleArgs), _P]),
             "levo_hip_sample_draw": (ctypes.c_int, [ctypes.POINTER(DrawArgs), _P]),
@@ -293,6 +310,9 @@ class LevoHip:
         return self._check(self.lib.levo_hip_residual_layer_norm(act_type, _addr(x), _addr(delta), _addr(gamma),
                                                                  _addr(beta), param_type, _addr(h_out), _addr(y),
                                                                  rows, dim, eps, _stream(stream)))
+
+    def layer_norm_modulated(self, args: ModulatedNormArgs, stream=None):
+        return self._check(self.lib.levo_hip_residual_layer_norm_modulated(ctypes.byref(args), _stream(stream)))
 
     def cfg_combine(self, out, uncond, cond, n, scale, stream=None):
         return self._check(self.lib.levo_hip_cfg_combine(_addr(out), _addr(uncond), _addr(cond), n, scale,

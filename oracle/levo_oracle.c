@@ -358,6 +358,51 @@ void lo_residual_layer_norm_f16(const uint16_t * x, const uint16_t * delta, cons
     lo_parallel(lo_ln_f16_rows, &ctx, n_threads);
 }
 
+/* Entry b, channel c of a per-batch modulation vector: ggml_add(dynamic,
+ * learned) of modulation_chunk (src/levo-flow-estimator.cpp:95-104), or the
+ * dynamic part alone. */
+static float lo_batch_value(const lo_batch_vector * v, int64_t b, int64_t c) {
+    const float dyn = v->dynamic[b * v->stride + c];
+    return v->learned ? dyn + v->learned[c] : dyn;
+}
+
+/* A Flow estimator block boundary (src/levo-flow-estimator.cpp:221-233,
+ * 243-261), one ggml op at a time:
+ *   current = (delta * gate) + x     ggml_add(ggml_mul(out, gate), residual) :221-227, 243-246
+ *   t = (norm(current) * gamma) + beta   layer_norm :106-109
+ *   y = (t * (scale + 1)) + shift    add_scale_shift :89-93 (ggml_scale_bias(scale, 1, 1))
+ * with gate / scale / shift taken at batch entry b = row / rows_per_batch. */
+void lo_residual_layer_norm_modulated_f32(const float * x, const float * delta, const lo_batch_vector * gate,
+                                          const float * gamma, const float * beta,
+                                          const lo_batch_vector * scale, const lo_batch_vector * shift,
+                                          float * h_out, float * y, int64_t rows, int64_t rows_per_batch,
+                                          int64_t dim, float eps) {
+    float * h = (float *)malloc(sizeof(float) * (size_t)dim);
+    float * n = (float *)malloc(sizeof(float) * (size_t)dim);
+    for (int64_t r = 0; r < rows; ++r) {
+        const int64_t b = r / rows_per_batch;
+        const float * xr = x + r * dim;
+        const float * dr = delta ? delta + r * dim : NULL;
+        for (int64_t c = 0; c < dim; ++c) {
+            if (!dr) h[c] = xr[c];
+            else if (gate) h[c] = (dr[c] * lo_batch_value(gate, b, c)) + xr[c];
+            else h[c] = xr[c] + dr[c];
+            if (h_out) h_out[r * dim + c] = h[c];
+        }
+        lo_norm_row(h, n, dim, eps);
+        for (int64_t c = 0; c < dim; ++c) {
+            float t = (n[c] * gamma[c]) + beta[c];
+            if (scale) {
+                const float one_plus = lo_batch_value(scale, b, c) + 1.0f;
+                t = (t * one_plus) + lo_batch_value(shift, b, c);
+            }
+            y[r * dim + c] = t;
+        }
+    }
+    free(n);
+    free(h);
+}
+
 /* ------------------------------------------------------------------------- */
 /* CFG                                                                        */
 /* ------------------------------------------------------------------------- */

@@ -20,6 +20,9 @@
  *   lo_residual_rms_norm_* /
  *   lo_residual_layer_norm_* ............. float64 closed forms (constant rows, +-1 rows),
  *                                          float64 brute force, numpy float16 pipeline
+ *   lo_residual_layer_norm_modulated_f32 . float64 brute force of the ggml op chain,
+ *                                          reductions to lo_residual_layer_norm_f32 (no gate,
+ *                                          no modulation; gate 1, scale 0, shift 0)
  *   lo_apply_cfg ......................... reference KATs (tests/test-sampling.cpp:8,
  *                                          tests/test-renderer-pattern.cpp:88-90) and the
  *                                          compiled reference (oracle/_ref) bit-for-bit
@@ -103,6 +106,24 @@ void lo_residual_layer_norm_f32(const float * x, const float * delta, const floa
 void lo_residual_layer_norm_f16(const uint16_t * x, const uint16_t * delta, const uint16_t * gamma,
                                 const uint16_t * beta, uint16_t * h_out, uint16_t * y,
                                 int64_t rows, int64_t dim, float eps, int n_threads);
+
+/* Per-batch modulation vector of the Flow estimator's blocks: entry b is
+ * dynamic[b * stride + c] + learned[c] (learned may be NULL). */
+typedef struct lo_batch_vector {
+    const float * dynamic;
+    int64_t stride;
+    const float * learned;
+} lo_batch_vector;
+/* Gated residual + LayerNorm + AdaLN modulation (src/levo-flow-estimator.cpp:
+ * 89-109, 221-233, 243-261): current = (delta * gate) + x;
+ * y = ((norm(current) * gamma + beta) * (scale + 1)) + shift. gate NULL:
+ * current = x + delta; delta NULL: current = x; scale NULL: no modulation
+ * (shift is then ignored). Single-threaded. */
+void lo_residual_layer_norm_modulated_f32(const float * x, const float * delta, const lo_batch_vector * gate,
+                                          const float * gamma, const float * beta,
+                                          const lo_batch_vector * scale, const lo_batch_vector * shift,
+                                          float * h_out, float * y, int64_t rows, int64_t rows_per_batch,
+                                          int64_t dim, float eps);
 
 /* ---- CFG (src/levo-sampling.cpp:22-28; src/levo-renderer-pattern.cpp:123-135):
  *      out = u + s * (c - u), two F32 roundings, no FMA. */

@@ -42,6 +42,11 @@ class MT19937_64(ctypes.Structure):
     _fields_ = [("state", ctypes.c_uint64 * 312), ("index", ctypes.c_int)]
 
 
+class BatchVector(ctypes.Structure):
+    """lo_batch_vector: entry b is dynamic[b * stride + c] + learned[c]."""
+    _fields_ = [("dynamic", _P), ("stride", _I64), ("learned", _P)]
+
+
 class Oracle:
     """The C restatement (oracle/levo_oracle.c)."""
 
@@ -58,6 +63,8 @@ class Oracle:
             "lo_residual_rms_norm_f32": (None, [_P, _P, _P, _P, _P, _I64, _I64, _F, ctypes.c_int]),
             "lo_residual_layer_norm_f16": (None, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, ctypes.c_int]),
             "lo_residual_layer_norm_f32": (None, [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, ctypes.c_int]),
+            "lo_residual_layer_norm_modulated_f32": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                                             _I64, _F]),
             "lo_apply_cfg": (None, [_P, _P, _P, _I64, _F]),
             "lo_mt_seed": (None, [_P, ctypes.c_uint64]),
             "lo_mt_next": (ctypes.c_uint64, [_P]),
@@ -135,6 +142,33 @@ class Oracle:
         y = np.empty_like(x)
         fn = self.lib.lo_residual_layer_norm_f16 if dt == np.uint16 else self.lib.lo_residual_layer_norm_f32
         fn(_ptr(x), _ptr(delta), _ptr(gamma), _ptr(beta), _ptr(h), _ptr(y), rows, dim, eps, threads)
+        return h, y
+
+    def layer_norm_modulated(self, x, delta, gate, gamma, beta, scale, shift, rows_per_batch, eps):
+        """lo_residual_layer_norm_modulated_f32 (src/levo-flow-estimator.cpp:
+        89-109, 221-261). gate / scale / shift: None or (dynamic, learned)
+        with dynamic [batches][stride >= dim] and learned [dim] or None."""
+        x = np.ascontiguousarray(x, np.float32)
+        rows, dim = x.shape
+        keep = []
+
+        def vec(v):
+            if v is None:
+                return None
+            dyn, learned = v
+            dyn = np.ascontiguousarray(dyn, np.float32)
+            learned = None if learned is None else np.ascontiguousarray(learned, np.float32)
+            keep.extend([dyn, learned])
+            return ctypes.byref(BatchVector(dyn.ctypes.data, dyn.shape[-1], _ptr(learned)))
+
+        delta = None if delta is None else np.ascontiguousarray(delta, np.float32)
+        gamma = np.ascontiguousarray(gamma, np.float32)
+        beta = np.ascontiguousarray(beta, np.float32)
+        h = np.empty_like(x)
+        y = np.empty_like(x)
+        self.lib.lo_residual_layer_norm_modulated_f32(_ptr(x), _ptr(delta), vec(gate), _ptr(gamma), _ptr(beta),
+                                                      vec(scale), vec(shift), _ptr(h), _ptr(y), rows,
+                                                      rows_per_batch, dim, eps)
         return h, y
 
     # -- CFG / sampling (src/levo-sampling.cpp) ------------------------------

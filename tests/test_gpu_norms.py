@@ -215,3 +215,142 @@ def test_f16_subnormal_results_follow_the_f32_then_f16_chain(hip, dev, oracle, l
     assert np.count_nonzero(sub) > 1000
     print(f"differing elements: {np.count_nonzero(y != yw)}")
     assert f16_ulp(y, yw) <= 1
+
+
+# ---- gated residual + LayerNorm + AdaLN modulation (Flow estimator blocks) ----------
+
+def _mod_vec(rng, batches, dim, stride, learned=True, scale=0.3):
+    dyn = (rng.standard_normal((batches, stride)) * scale).astype(np.float32)
+    lrn = (rng.standard_normal(dim) * scale).astype(np.float32) if learned else None
+    return dyn, lrn
+
+
+def _run_mod(hip, binding, dev, x, d, gate, gamma, beta, scale, shift, rpb, eps, f16_params=False,
+             in_place=False, with_h=True):
+    """levo_hip_residual_layer_norm_modulated on device copies; returns (h, y)."""
+    import torch
+    keep = []
+
+    def put(a):
+        t = to_dev(a, dev)
+        keep.append(t)
+        return t
+
+    def vec(v):
+        """v: None, (dynamic, learned) or (dynamic, learned, first column)."""
+        bv = binding.BatchVector()
+        if v is None:
+            return bv
+        dyn, lrn = v[0], v[1]
+        col = v[2] if len(v) > 2 else 0
+        bv.dynamic, bv.stride = put(dyn).data_ptr() + 4 * col, dyn.shape[1]
+        bv.learned = put(lrn).data_ptr() if lrn is not None else None
+        return bv
+
+    rows, dim = x.shape
+    xd = put(x)
+    a = binding.ModulatedNormArgs()
+    a.x = xd.data_ptr()
+    a.delta = put(d).data_ptr() if d is not None else None
+    a.gate, a.scale, a.shift = vec(gate), vec(scale), vec(shift)
+    conv = (lambda t: oracle_f16(t)) if f16_params else (lambda t: t)
+    a.gamma, a.beta = put(conv(gamma)).data_ptr(), put(conv(beta)).data_ptr()
+    a.param_type = 1 if f16_params else 0
+    hd = xd if in_place else (torch.empty_like(xd) if with_h else None)
+    yd = torch.empty_like(xd)
+    a.h_out = hd.data_ptr() if hd is not None else None
+    a.y = yd.data_ptr()
+    a.rows, a.rows_per_batch, a.dim, a.eps = rows, rpb, dim, eps
+    hip.layer_norm_modulated(a)
+    return (from_dev(hd) if hd is not None else None), from_dev(yd)
+
+
+def oracle_f16(a):
+    return a.astype(np.float16).view(np.int16)
+
+
+def _mod_inputs(rows, dim, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    d = rng.standard_normal((rows, dim)).astype(np.float32)
+    gamma = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    beta = (0.02 * rng.standard_normal(dim)).astype(np.float32)
+    return rng, x, d, gamma, beta
+
+
+def test_modulated_flow_estimator_full_shape(hip, binding, dev, oracle):
+    """The Flow estimator's block boundary at its real shape: batch 2 x 1000
+    frames x 2200, gate / scale / shift = chunks 2 / 4 / 3 of a [batch][6 x
+    2200] time modulation (read in place, 6 x 2200 floats apart) plus the
+    block's learned table (modulation_chunk), eps 1e-5. h bit-exact; y within
+    1e-5 of the oracle."""
+    rows, dim, rpb = 2000, 2200, 1000
+    rng, x, d, gamma, beta = _mod_inputs(rows, dim, 31)
+    tm = (rng.standard_normal((2, 6 * dim)) * 0.3).astype(np.float32)
+    table = (rng.standard_normal(6 * dim) * 0.3).astype(np.float32)
+    chunk = lambda k: (tm, table[k * dim:(k + 1) * dim], k * dim)
+    h, y = _run_mod(hip, binding, dev, x, d, chunk(2), gamma, beta, chunk(4), chunk(3), rpb, 1e-5)
+    view = lambda k: (tm[:, k * dim:], table[k * dim:(k + 1) * dim])
+    hw, yw = oracle.layer_norm_modulated(x, d, view(2), gamma, beta, view(4), view(3), rpb, 1e-5)
+    assert np.array_equal(h.view(np.uint32), hw.view(np.uint32))
+    assert f32_err(y, yw) <= 1e-5, f"{np.count_nonzero(y != yw)} values differ"
+
+
+@pytest.mark.parametrize("delta,gate,mod", [(True, True, True), (True, True, False), (True, False, True),
+                                            (True, False, False), (False, False, True), (False, False, False)])
+@pytest.mark.parametrize("dim", [512, 1028, 2200, 2560, 2564, 4096])
+def test_modulated_variants(hip, binding, dev, oracle, delta, gate, mod, dim):
+    """Every combination of delta / gate / modulation at each row-length
+    instance (up to 1024, 2560, 4096 values; lengths that leave a lane's last
+    piece past the row), 3 batch entries of 7 rows (workgroups of 4 rows end
+    inside an entry)."""
+    rows, rpb = 21, 7
+    rng, x, d, gamma, beta = _mod_inputs(rows, dim, dim + 8 * delta + 4 * gate + 2 * mod)
+    g = _mod_vec(rng, 3, dim, dim + 12) if gate else None
+    s = _mod_vec(rng, 3, dim, dim + 4) if mod else None
+    sh = _mod_vec(rng, 3, dim, dim, learned=False) if mod else None
+    h, y = _run_mod(hip, binding, dev, x, d if delta else None, g, gamma, beta, s, sh, rpb, 1e-5)
+    hw, yw = oracle.layer_norm_modulated(x, d if delta else None, g, gamma, beta, s, sh, rpb, 1e-5)
+    assert np.array_equal(h.view(np.uint32), hw.view(np.uint32))
+    assert f32_err(y, yw) <= 1e-5
+
+
+def test_modulated_f16_params_in_place(hip, binding, dev, oracle):
+    """F16 gamma / beta (widened exactly) and the residual written over x."""
+    rows, dim, rpb = 16, 2200, 8
+    rng, x, d, gamma, beta = _mod_inputs(rows, dim, 41)
+    gamma16 = gamma.astype(np.float16).astype(np.float32)
+    beta16 = beta.astype(np.float16).astype(np.float32)
+    g, s, sh = (_mod_vec(rng, 2, dim, 6 * dim) for _ in range(3))
+    h, y = _run_mod(hip, binding, dev, x, d, g, gamma16, beta16, s, sh, rpb, 1e-5, f16_params=True, in_place=True)
+    hw, yw = oracle.layer_norm_modulated(x, d, g, gamma16, beta16, s, sh, rpb, 1e-5)
+    assert np.array_equal(h.view(np.uint32), hw.view(np.uint32))
+    assert f32_err(y, yw) <= 1e-5
+    _, y2 = _run_mod(hip, binding, dev, x, d, g, gamma16, beta16, s, sh, rpb, 1e-5, f16_params=True, with_h=False)
+    assert np.array_equal(y2.view(np.uint32), y.view(np.uint32))
+
+
+def test_modulated_rejects_bad_arguments(hip, binding, dev):
+    import torch
+    x = torch.zeros((8, 64), device=dev)
+    p = torch.ones(64, device=dev)
+    v = torch.zeros((2, 64), device=dev)
+
+    def args(**kw):
+        a = binding.ModulatedNormArgs()
+        a.x, a.y, a.gamma, a.beta = x.data_ptr(), x.data_ptr(), p.data_ptr(), p.data_ptr()
+        a.rows, a.rows_per_batch, a.dim, a.eps = 8, 4, 64, 1e-5
+        for k, val in kw.items():
+            setattr(a, k, val)
+        return a
+
+    bv = binding.BatchVector(v.data_ptr(), 64, None)
+    for bad, msg in ((args(gate=bv), "gate needs delta"), (args(scale=bv), "scale and shift"),
+                     (args(rows_per_batch=3), "whole number"), (args(dim=62), "multiple of 4"),
+                     (args(dim=4100), "multiple of 4"), (args(x=x.data_ptr() + 4), "aligned"),
+                     (args(scale=binding.BatchVector(v.data_ptr(), 60, None),
+                           shift=binding.BatchVector(v.data_ptr(), 60, None)), "stride"),
+                     (args(param_type=2), "F32 or F16")):
+        with pytest.raises(binding.LevoHipError, match=msg):
+            hip.layer_norm_modulated(bad)
+    hip.layer_norm_modulated(args(rows=0))  # nothing to do

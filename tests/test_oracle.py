@@ -642,3 +642,147 @@ def test_conv_transpose1d_delta_kernel_upsamples(oracle):
             if 0 <= o < y.shape[1]:
                 want[:, o] = x[:, i]
         assert np.array_equal(y, want), tap
+
+
+def test_f16_residual_single_rounding_equals_f32_chain():
+    """The F16 residual kernels add packed halves (one rounding of the exact
+    sum) where the reference rounds f32(x) + f32(d) to F32 and then to F16
+    (src/levo-kv.cpp:462, 507). Equal by Figueroa's double-rounding bound (24
+    >= 2 * 11 + 2); checked here for every finite F16 x against 96 d each:
+    64 random halves and 32 placed at, just inside and just outside the
+    rounding midpoints of x (including binade edges and subnormals). The
+    correctly rounded sum is the exact float64 sum rounded to F16."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    x16 = bits.view(np.float16)
+    x16 = x16[np.isfinite(x16)]
+    rng = np.random.default_rng(5)
+    rand = rng.integers(0, 1 << 16, size=(x16.size, 64), dtype=np.uint32).astype(np.uint16).view(np.float16)
+    with np.errstate(over="ignore"):  # spacing of the largest finite half is inf in F16
+        ulp = np.spacing(np.abs(x16)).astype(np.float64)
+    half = np.concatenate([ulp[:, None] * f for f in (0.5, 0.25)], axis=1)
+    near = []
+    for h in (half[:, :1], half[:, 1:2]):
+        for m in (1.0, 1.0 + 2.0 ** -9, 1.0 - 2.0 ** -9, 1.0 + 2.0 ** -3, 1.0 - 2.0 ** -3, 3.0, 2.0 ** -5, 2.0 ** -12):
+            near.append(h * m)
+            near.append(-h * m)
+    with np.errstate(over="ignore", invalid="ignore"):
+        placed = np.concatenate(near, axis=1).astype(np.float16)
+    d16 = np.concatenate([rand, placed], axis=1)
+    d16 = np.where(np.isfinite(d16), d16, np.float16(0))
+    for lo in range(0, x16.size, 4096):
+        xs, ds = x16[lo:lo + 4096, None], d16[lo:lo + 4096]
+        with np.errstate(over="ignore", invalid="ignore"):
+            chain = (xs.astype(np.float32) + ds.astype(np.float32)).astype(np.float16)
+            direct = (xs.astype(np.float64) + ds.astype(np.float64)).astype(np.float16)
+        same = (chain.view(np.uint16) == direct.view(np.uint16)) | (np.isnan(chain) & np.isnan(direct))
+        assert same.all(), (lo, np.argwhere(~same)[:5])
+
+
+# ---- gated residual + LayerNorm + AdaLN modulation (Flow estimator blocks) ----------
+
+def _modulation(rng, batches, dim, stride, scale=0.3):
+    """(dynamic [batches][stride], learned [dim]) as modulation_chunk reads them."""
+    dyn = (rng.standard_normal((batches, stride)) * scale).astype(np.float32)
+    learned = (rng.standard_normal(dim) * scale).astype(np.float32)
+    return dyn, learned
+
+
+def _chain_f64(x, d, gate, gamma, beta, scale, shift, rpb, eps):
+    """The ggml chain of src/levo-flow-estimator.cpp:89-109, 221-261 evaluated
+    in float64 throughout (a brute force: no F32 rounding anywhere)."""
+    rows, dim = x.shape
+    b = np.arange(rows) // rpb
+
+    def vec(v):
+        dyn, learned = v
+        out = dyn[:, :dim].astype(np.float64)
+        return out + (0.0 if learned is None else learned.astype(np.float64))
+
+    x64 = x.astype(np.float64)
+    cur = x64 if d is None else (x64 + d.astype(np.float64) * (vec(gate)[b] if gate else 1.0))
+    mean = cur.mean(axis=1, keepdims=True)
+    var = ((cur - mean) ** 2).mean(axis=1, keepdims=True)
+    t = (cur - mean) / np.sqrt(var + eps) * gamma.astype(np.float64) + beta.astype(np.float64)
+    if scale is not None:
+        t = t * (vec(scale)[b] + 1.0) + vec(shift)[b]
+    return cur, t
+
+
+def test_modulated_norm_without_gate_or_modulation_is_the_layer_norm(oracle):
+    """No gate and no modulation: bit-identical to lo_residual_layer_norm_f32
+    (itself pinned above), with and without delta."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((12, 2200)).astype(np.float32)
+    d = rng.standard_normal((12, 2200)).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(2200)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(2200)).astype(np.float32)
+    for delta in (d, None):
+        h, y = oracle.layer_norm_modulated(x, delta, None, g, b, None, None, 6, 1e-5)
+        h2, y2 = oracle.layer_norm(x, delta, g, b, 1e-5)
+        assert np.array_equal(h, h2) and np.array_equal(y, y2)
+
+
+def test_modulated_norm_identity_modulation(oracle):
+    """gate = 1, scale = 0, shift = 0 (dynamic parts zero, learned parts 1 /
+    0 / 0) change no value: d * 1 + x = x + d and t * (0 + 1) + 0 = t."""
+    rng = np.random.default_rng(22)
+    rows, dim = 8, 1024
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    d = rng.standard_normal((rows, dim)).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(dim)).astype(np.float32)
+    zeros = np.zeros((2, dim), np.float32)
+    gate = (zeros, np.ones(dim, np.float32))
+    zero = (zeros, np.zeros(dim, np.float32))
+    h, y = oracle.layer_norm_modulated(x, d, gate, g, b, zero, zero, 4, 1e-5)
+    h2, y2 = oracle.layer_norm(x, d, g, b, 1e-5)
+    assert np.array_equal(h, h2) and np.array_equal(y, y2)
+
+
+@pytest.mark.parametrize("learned", [True, False])
+def test_modulated_norm_against_float64_chain(oracle, learned):
+    """Three batch entries of distinct gate / scale / shift (modulation rows
+    6 * dim apart, as the time modulation's chunks are) against the chain in
+    float64: within the F32 bar everywhere, and far outside it for the plausible
+    slips (a row taking another entry's vectors, scale used without the + 1,
+    gate on x instead of delta, the modulation before beta)."""
+    rng = np.random.default_rng(23 + learned)
+    rows, dim, rpb, eps = 3 * 5, 2200, 5, 1e-5
+    x = rng.standard_normal((rows, dim)).astype(np.float32)
+    d = rng.standard_normal((rows, dim)).astype(np.float32)
+    gamma = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    beta = (0.02 * rng.standard_normal(dim)).astype(np.float32)
+    vecs = []
+    for _ in range(3):
+        dyn, lrn = _modulation(rng, 3, dim, 6 * dim)
+        vecs.append((dyn, lrn if learned else None))
+    gate, scale, shift = vecs
+    h, y = oracle.layer_norm_modulated(x, d, gate, gamma, beta, scale, shift, rpb, eps)
+    h64, y64 = _chain_f64(x, d, gate, gamma, beta, scale, shift, rpb, eps)
+    assert f32_err(h, h64) <= 1e-6
+    assert f32_err(y, y64) <= 1e-5
+    # the slips a restatement could make all land far outside the bar
+    wrong_batch = _chain_f64(x, d, gate, gamma, beta, scale, shift, rows, eps)[1]
+    no_plus_one = _chain_f64(x, d, gate, gamma, beta, (scale[0] - 1.0, scale[1]), shift, rpb, eps)[1]
+    gate_on_x = _chain_f64(d, x, gate, gamma, beta, scale, shift, rpb, eps)[1]
+    for slip in (wrong_batch, no_plus_one, gate_on_x):
+        assert f32_err(y, slip) > 1e-2
+
+
+def test_modulated_norm_constant_rows(oracle):
+    """A constant row normalizes to 0, so y = (beta * (scale + 1)) + shift,
+    each F32 operation rounded once (closed form)."""
+    rng = np.random.default_rng(24)
+    rows, dim = 6, 512
+    x = np.repeat(rng.standard_normal((rows, 1)), dim, axis=1).astype(np.float32)
+    gamma = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)
+    beta = (0.5 * rng.standard_normal(dim)).astype(np.float32)
+    scale = _modulation(rng, 2, dim, dim)
+    shift = _modulation(rng, 2, dim, dim)
+    _, y = oracle.layer_norm_modulated(x, None, None, gamma, beta, scale, shift, 3, 1e-5)
+    for r in range(rows):
+        b = r // 3
+        ops = (scale[0][b] + scale[1]).astype(np.float32) + np.float32(1)
+        sh = (shift[0][b] + shift[1]).astype(np.float32)
+        want = (beta * ops).astype(np.float32) + sh
+        assert np.array_equal(y[r], want)
