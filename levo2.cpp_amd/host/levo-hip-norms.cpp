@@ -64,4 +64,65 @@ void residual_layer_norm(const tensor_view * x, const tensor_view * delta, const
                                               stream));
 }
 
+namespace {
+
+// levo_hip_batch_vector of a view; `batches` entries of `dim` values.
+levo_hip_batch_vector batch_vector(const batch_vector_view & v, int64_t dim, int64_t batches, const char * name) {
+    levo_hip_batch_vector out{nullptr, 0, nullptr};
+    if (v.dynamic == nullptr) {
+        if (v.learned != nullptr) fail(std::string(name) + ": a learned part needs a dynamic part");
+        return out;
+    }
+    const tensor_view & d = *v.dynamic;
+    if (d.type != LEVO_HIP_TYPE_F32) fail(std::string(name) + " must be F32");
+    if (d.ne[0] != dim || d.ne[1] * d.ne[2] * d.ne[3] != batches) {
+        fail(std::string(name) + " must have shape [dim, batch]");
+    }
+    if (d.nb[0] != sizeof(float) || d.nb[1] % sizeof(float) != 0) fail(std::string(name) + " rows must be dense floats");
+    if (d.ne[1] > 1 && d.ne[2] * d.ne[3] != 1) fail(std::string(name) + " must be two-dimensional");
+    out.dynamic = static_cast<const float *>(d.data);
+    out.stride = d.ne[1] > 1 ? static_cast<int64_t>(d.nb[1] / sizeof(float)) : dim;
+    if (v.learned != nullptr) {
+        const tensor_view & l = *v.learned;
+        if (l.type != LEVO_HIP_TYPE_F32 || l.ne[0] != dim || l.ne[1] * l.ne[2] * l.ne[3] != 1 || !is_contiguous(l)) {
+            fail(std::string(name) + ": the learned part must be an F32 [dim] vector");
+        }
+        out.learned = static_cast<const float *>(l.data);
+    }
+    return out;
+}
+
+} // namespace
+
+void residual_layer_norm_modulated(const tensor_view * x, const tensor_view * delta, const batch_vector_view & gate,
+                                   const tensor_view * gamma, const tensor_view * beta,
+                                   const batch_vector_view & scale, const batch_vector_view & shift, float eps,
+                                   const tensor_view * h_out, const tensor_view * y, stream_t stream) {
+    const int64_t rows = check_activations(x, delta, h_out, y);
+    if (x->type != LEVO_HIP_TYPE_F32) fail("the modulated LayerNorm takes F32 activations");
+    check_param(gamma, x, "gamma");
+    check_param(beta, x, "beta");
+    if (gamma->type != beta->type) fail("gamma and beta must share one type");
+    if ((scale.dynamic == nullptr) != (shift.dynamic == nullptr)) fail("scale and shift come together");
+    if (gate.dynamic != nullptr && delta == nullptr) fail("a gate needs delta");
+    const int64_t dim = x->ne[0];
+    const int64_t batches = x->ne[2] * x->ne[3];
+    levo_hip_modulated_norm_args a{};
+    a.x = static_cast<const float *>(x->data);
+    a.delta = delta ? static_cast<const float *>(delta->data) : nullptr;
+    a.gate = batch_vector(gate, dim, batches, "gate");
+    a.gamma = gamma->data;
+    a.beta = beta->data;
+    a.param_type = gamma->type;
+    a.scale = batch_vector(scale, dim, batches, "scale");
+    a.shift = batch_vector(shift, dim, batches, "shift");
+    a.h_out = h_out ? static_cast<float *>(h_out->data) : nullptr;
+    a.y = static_cast<float *>(y->data);
+    a.rows = rows;
+    a.rows_per_batch = x->ne[1];
+    a.dim = dim;
+    a.eps = eps;
+    check_status(levo_hip_residual_layer_norm_modulated(&a, stream));
+}
+
 } // namespace levo::hip

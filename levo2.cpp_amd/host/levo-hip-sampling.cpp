@@ -6,6 +6,8 @@
 #include <cmath>
 #include <cstring>
 #include <limits>
+#include <map>
+#include <mutex>
 #include <stdexcept>
 
 namespace levo::hip {
@@ -313,29 +315,81 @@ int64_t sample_host_row(sample_workspace & ws, const logits & input, std::size_t
 
 // ---- CFG ----------------------------------------------------------------------
 
-logits apply_cfg(const logits & conditional, const logits & unconditional, float scale) {
-    if (conditional.size() != unconditional.size()) throw std::invalid_argument("CFG logits have different sizes");
-    logits out(conditional.size());
-    if (out.empty()) return out;
-    const std::size_t n = out.size();
-    device_buffer<float> d(3 * n);
-    d.upload(unconditional.data(), n, nullptr);
-    check_hip(hipMemcpyAsync(d.data() + n, conditional.data(), n * sizeof(float), hipMemcpyHostToDevice, nullptr),
-              "host-to-device copy");
-    check_status(levo_hip_cfg_combine(d.data() + 2 * n, d.data(), d.data() + n, static_cast<int64_t>(n), scale,
-                                      nullptr));
-    check_hip(hipMemcpyAsync(out.data(), d.data() + 2 * n, n * sizeof(float), hipMemcpyDeviceToHost, nullptr),
+namespace {
+
+// Device and pinned staging for the host-vector CFG calls, one per GPU, kept
+// (and grown) for the process's lifetime; calls are serialized.
+struct cfg_workspace {
+    device_buffer<float> dev;   // [uncond | cond | out]
+    pinned_buffer<float> host;  // the same, staged
+};
+
+std::mutex cfg_mutex;
+
+cfg_workspace & cfg_workspace_for_current_device() {
+    static std::map<int, cfg_workspace *> per_device;  // never freed: the runtime may be gone at exit
+    int device = 0;
+    check_hip(hipGetDevice(&device), "current device");
+    cfg_workspace *& ws = per_device[device];
+    if (ws == nullptr) ws = new cfg_workspace;
+    return *ws;
+}
+
+// out[i] = apply_cfg(cond[i], uncond[i], scale) for every pair at once: one
+// upload of all rows, one levo_hip_cfg_combine launch over them, one download.
+void cfg_batch(const logits * const * cond, const logits * const * uncond, std::size_t pairs, float scale,
+               logits * out) {
+    std::size_t total = 0;
+    for (std::size_t i = 0; i < pairs; ++i) total += cond[i]->size();
+    for (std::size_t i = 0; i < pairs; ++i) out[i].assign(cond[i]->size(), 0.0F);
+    if (total == 0) return;
+    std::lock_guard<std::mutex> lock(cfg_mutex);
+    cfg_workspace & ws = cfg_workspace_for_current_device();
+    ws.dev.reserve_discard(3 * total);
+    ws.host.reserve_discard(3 * total);
+    float * hu = ws.host.data();
+    float * hc = hu + total;
+    for (std::size_t i = 0, at = 0; i < pairs; at += cond[i]->size(), ++i) {
+        std::copy(uncond[i]->begin(), uncond[i]->end(), hu + at);
+        std::copy(cond[i]->begin(), cond[i]->end(), hc + at);
+    }
+    ws.dev.upload(hu, 2 * total, nullptr);
+    float * du = ws.dev.data();
+    check_status(levo_hip_cfg_combine(du + 2 * total, du, du + total, static_cast<int64_t>(total), scale, nullptr));
+    check_hip(hipMemcpyAsync(hu + 2 * total, du + 2 * total, total * sizeof(float), hipMemcpyDeviceToHost, nullptr),
               "device-to-host copy");
     synchronize(nullptr);
+    for (std::size_t i = 0, at = 0; i < pairs; at += out[i].size(), ++i) {
+        std::copy(hu + 2 * total + at, hu + 2 * total + at + out[i].size(), out[i].begin());
+    }
+}
+
+} // namespace
+
+logits apply_cfg(const logits & conditional, const logits & unconditional, float scale) {
+    if (conditional.size() != unconditional.size()) throw std::invalid_argument("CFG logits have different sizes");
+    const logits * c = &conditional;
+    const logits * u = &unconditional;
+    logits out;
+    cfg_batch(&c, &u, 1, scale, &out);
     return out;
 }
 
 std::vector<logits> apply_cfg(const std::vector<logits> & conditional,
                               const std::vector<logits> & unconditional, float scale) {
     if (conditional.size() != unconditional.size()) throw std::invalid_argument("CFG batch sizes differ");
-    std::vector<logits> out;
-    out.reserve(conditional.size());
-    for (std::size_t i = 0; i < conditional.size(); ++i) out.push_back(apply_cfg(conditional[i], unconditional[i], scale));
+    // The reference (src/levo-sampling.cpp:30-37) throws at the first pair of
+    // different sizes; every pair is checked before any work starts.
+    std::vector<const logits *> c(conditional.size()), u(conditional.size());
+    for (std::size_t i = 0; i < conditional.size(); ++i) {
+        if (conditional[i].size() != unconditional[i].size()) {
+            throw std::invalid_argument("CFG logits have different sizes");
+        }
+        c[i] = &conditional[i];
+        u[i] = &unconditional[i];
+    }
+    std::vector<logits> out(conditional.size());
+    cfg_batch(c.data(), u.data(), c.size(), scale, out.data());
     return out;
 }
 

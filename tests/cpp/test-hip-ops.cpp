@@ -195,6 +195,53 @@ void norm_parity() {
     });
 }
 
+// The Flow estimator's block boundary through the tensor-view wrapper: gate /
+// scale / shift as ggml_view_2d chunks 2 / 4 / 3 of a [6 * dim, batch] time
+// modulation (rows 6 * dim floats apart) plus a block table
+// (src/levo-flow-estimator.cpp:95-104, 221-233).
+void modulated_norm_parity() {
+    const int64_t D = 2200, F = 100, B = 2;
+    const std::size_t n = static_cast<std::size_t>(D * F * B);
+    const std::vector<float> x = gaussian(n, 61), d = gaussian(n, 62);
+    const std::vector<float> g = gaussian(static_cast<std::size_t>(D), 63, 0.02F, 1.0F);
+    const std::vector<float> b = gaussian(static_cast<std::size_t>(D), 64, 0.02F);
+    const std::vector<float> tm = gaussian(static_cast<std::size_t>(6 * D * B), 65, 0.3F);
+    const std::vector<float> table = gaussian(static_cast<std::size_t>(6 * D), 66, 0.3F);
+    device_vec<float> dx(x), dd(d), dg(g), db(b), dtm(tm), dtab(table), dh(n), dy(n);
+    const tensor_view vx = make_tensor_view(dx.data(), LEVO_HIP_TYPE_F32, D, F, B);
+    const tensor_view vd = make_tensor_view(dd.data(), LEVO_HIP_TYPE_F32, D, F, B);
+    const tensor_view vh = make_tensor_view(dh.data(), LEVO_HIP_TYPE_F32, D, F, B);
+    const tensor_view vy = make_tensor_view(dy.data(), LEVO_HIP_TYPE_F32, D, F, B);
+    const tensor_view vg = make_tensor_view(dg.data(), LEVO_HIP_TYPE_F32, D);
+    const tensor_view vb = make_tensor_view(db.data(), LEVO_HIP_TYPE_F32, D);
+    tensor_view chunk[6], learned[6];
+    for (int k = 0; k < 6; ++k) {
+        chunk[k] = make_tensor_view(dtm.data() + k * D, LEVO_HIP_TYPE_F32, D, B);
+        chunk[k].nb[1] = static_cast<std::size_t>(6 * D) * sizeof(float);  // ggml_view_2d of the modulation
+        chunk[k].nb[2] = chunk[k].nb[3] = chunk[k].nb[1] * static_cast<std::size_t>(B);
+        learned[k] = make_tensor_view(dtab.data() + k * D, LEVO_HIP_TYPE_F32, D);
+    }
+    residual_layer_norm_modulated(&vx, &vd, {&chunk[2], &learned[2]}, &vg, &vb, {&chunk[4], &learned[4]},
+                                  {&chunk[3], &learned[3]}, 1.0e-5F, &vh, &vy);
+    const lo_batch_vector gate{tm.data() + 2 * D, 6 * D, table.data() + 2 * D};
+    const lo_batch_vector scale{tm.data() + 4 * D, 6 * D, table.data() + 4 * D};
+    const lo_batch_vector shift{tm.data() + 3 * D, 6 * D, table.data() + 3 * D};
+    std::vector<float> wh(n), wy(n);
+    lo_residual_layer_norm_modulated_f32(x.data(), d.data(), &gate, g.data(), b.data(), &scale, &shift, wh.data(),
+                                         wy.data(), F * B, F, D, 1.0e-5F);
+    CHECK(dh.get() == wh);
+    CHECK(rel_err(dy.get(), wy) <= 1.0e-5F);
+
+    expect_throw<std::invalid_argument>("LeVo HIP norm: scale must have shape [dim, batch]", [&] {
+        const tensor_view one = make_tensor_view(dtm.data(), LEVO_HIP_TYPE_F32, D, 1);
+        residual_layer_norm_modulated(&vx, &vd, {}, &vg, &vb, {&one, nullptr}, {&chunk[3], nullptr}, 1.0e-5F,
+                                      nullptr, &vy);
+    });
+    expect_throw<std::invalid_argument>("LeVo HIP norm: scale and shift come together", [&] {
+        residual_layer_norm_modulated(&vx, &vd, {}, &vg, &vb, {&chunk[4], nullptr}, {}, 1.0e-5F, nullptr, &vy);
+    });
+}
+
 void quantize_surface() {
     // tests/test-quantization.cpp:45-51: a 4 x 32 matrix with six live columns.
     std::vector<float> original(32 * 4, 0.0F);
@@ -382,6 +429,7 @@ int main() {
         snake_reference_kat();
         snake_parity();
         norm_parity();
+        modulated_norm_parity();
         quantize_surface();
         mul_mat_surface();
         kquant_surface();

@@ -78,6 +78,18 @@ void error_behaviour() {
     expect_throw<std::invalid_argument>("CFG logits have different sizes", [] { (void) apply_cfg({1, 2}, {1}, 1.5F); });
     expect_throw<std::invalid_argument>("CFG batch sizes differ",
                                         [] { (void) apply_cfg(std::vector<logits>{{1}}, std::vector<logits>{}, 1.5F); });
+    expect_throw<std::invalid_argument>("CFG logits have different sizes", [] {
+        (void) apply_cfg(std::vector<logits>{{1, 2}, {1, 2, 3}}, std::vector<logits>{{1, 2}, {1, 2}}, 1.5F);
+    });
+    // One launch over rows of different lengths, an empty row among them.
+    {
+        const std::vector<logits> c{{2, 4}, {}, {1, 2, 3}}, u{{1, 1}, {}, {3, 6, 0.5F}};
+        const std::vector<logits> got = apply_cfg(c, u, 1.5F);
+        CHECK(got.size() == 3 && got[1].empty());
+        for (int i : {0, 2}) CHECK(got[static_cast<std::size_t>(i)] == apply_cfg(c[static_cast<std::size_t>(i)],
+                                                                                  u[static_cast<std::size_t>(i)], 1.5F));
+        CHECK(got[0] == logits({2.5F, 5.5F}));  // tests/test-sampling.cpp:8
+    }
     expect_throw<std::invalid_argument>("recent-token stream count differs",
                                         [] { Sampler().sample_streams({{1, 2}, {3, 4}}, {}, {{1}}); });
     sampling_config bad;
