@@ -356,10 +356,10 @@ template <int TYPE, int LPR, int U, int CH, int WPR = 1>
 __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_params p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
     const int nb = p.nb;
-    const int k = nb * kQK;
+    const int nblk = p.n_vec * nb;
     int8_t * xq = reinterpret_cast<int8_t *>(lds_raw);
-    float * xd = reinterpret_cast<float *>(lds_raw + static_cast<size_t>(p.n_vec) * k);
-    int16_t * xs = reinterpret_cast<int16_t *>(xd + p.n_vec * nb);
+    float * xd = reinterpret_cast<float *>(lds_raw + static_cast<size_t>(nblk) * kQK);
+    int16_t * xs = reinterpret_cast<int16_t *>(xd + ((nblk + 3) & ~3));
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -388,53 +388,41 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
     const int64_t sb0 = row0 * p.row_bytes + static_cast<int64_t>(kb0) * kBytes;
     const int64_t sb1 = WPR > 1 ? row0 * p.row_bytes + static_cast<int64_t>(kb1) * kBytes
                                 : sb0 + nrows * p.row_bytes;
-    // The activation blocks (dwords 0 .. 73 nblk of x, 73 per 292-byte block)
-    // are requested first, as dwordx4 with no branch around them (surplus
-    // requests re-read the first chunk; the chunk crossing the end of x, if
-    // any, reads the one before and is re-read below as dwords): loads
-    // complete in issue order, so they are staged while the weights are in
-    // flight.
-    const int ndw = p.n_vec * nb * 73;
-    const int nx4 = (ndw + 3) / 4;
-    const int64_t xbytes = 4 * static_cast<int64_t>(ndw);
-    const uint32_t * xw = reinterpret_cast<const uint32_t *>(p.x);
+    // The activations: n_vec * nb block_q8_K of 292 bytes (f32 d, int8
+    // qs[256], int16 bsums[16]) go to LDS as xq [nblk][256], xd [nblk] and
+    // xs [nblk][16], by whole pieces: 16 quant chunks, the scale and 2 bsum
+    // chunks per block, chunk c of a region at byte 16 c (LDS stores stay
+    // 16-byte aligned; the global reads are 4-byte aligned). The first chunks
+    // are requested before the weights, with no branch around them (surplus
+    // requests re-read the last chunk): loads complete in issue order, so they
+    // are stored while the weights are in flight.
+    const uint8_t * xg = p.x;
+    const auto qchunk = [&](int c) {
+        return *reinterpret_cast<const u32x4 *>(xg + 292 * static_cast<int64_t>(c >> 4) + 4 + 16 * (c & 15));
+    };
+    const auto schunk = [&](int c) {
+        return *reinterpret_cast<const u32x4 *>(xg + 292 * static_cast<int64_t>(c >> 1) + 260 + 16 * (c & 1));
+    };
+    const auto dword = [&](int b) { return *reinterpret_cast<const uint32_t *>(xg + 292 * static_cast<int64_t>(b)); };
+    const int n_q = 16 * nblk;
     u32x4 xr[kXVec];
 #pragma unroll
-    for (int j = 0; j < kXVec; ++j) {
-        const int c = tid + kThreads * j;
-        const int64_t at = 16 * static_cast<int64_t>(c);
-        const int64_t from = c >= nx4 ? 0 : at + 16 <= xbytes ? at : at - 16;
-        xr[j] = *reinterpret_cast<const u32x4 *>(p.x + from);
-    }
+    for (int j = 0; j < kXVec; ++j) xr[j] = qchunk(min(tid + kThreads * j, n_q - 1));
+    const uint32_t d0 = dword(min(tid, nblk - 1));
+    const u32x4 s0 = schunk(min(tid, 2 * nblk - 1));
     u32x4 regs[CH];
     load_span<CH>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
-    // 2. the activations re-laid out in LDS so that each lane's quants are
-    //    aligned: xq [n_vec][256 nb] int8, xd [n_vec][nb] float, xs [n_vec][16 nb]
-    //    int16 (the bsums)
-    const auto place = [&](int e, uint32_t v) {
-        const int b = e / 73, wd = e - b * 73;
-        if (wd == 0) xd[b] = __builtin_bit_cast(float, v);
-        else if (wd <= 64) reinterpret_cast<uint32_t *>(xq)[b * 64 + wd - 1] = v;
-        else reinterpret_cast<uint32_t *>(xs)[b * 8 + wd - 65] = v;
-    };
+    // 2. store them (and fetch any the first requests did not cover)
 #pragma unroll
     for (int j = 0; j < kXVec; ++j) {
         const int c = tid + kThreads * j;
-        if (c >= nx4) continue;
-        u32x4 v = xr[j];
-        if (16 * static_cast<int64_t>(c) + 16 > xbytes) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = 4 * c + q < ndw ? xw[4 * c + q] : 0u;
-        }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (4 * c + q < ndw) place(4 * c + q, v[q]);
+        if (c < n_q) reinterpret_cast<u32x4 *>(xq)[c] = xr[j];
     }
-    for (int e = 4 * (tid + kThreads * kXVec); e < ndw; e += 4 * kThreads) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            if (e + q < ndw) place(e + q, xw[e + q]);
-    }
+    if (tid < nblk) xd[tid] = __builtin_bit_cast(float, d0);
+    if (tid < 2 * nblk) reinterpret_cast<u32x4 *>(xs)[tid] = s0;
+    for (int c = tid + kThreads * kXVec; c < n_q; c += kThreads) reinterpret_cast<u32x4 *>(xq)[c] = qchunk(c);
+    for (int b = tid + kThreads; b < nblk; b += kThreads) xd[b] = __builtin_bit_cast(float, dword(b));
+    for (int c = tid + kThreads; c < 2 * nblk; c += kThreads) reinterpret_cast<u32x4 *>(xs)[c] = schunk(c);
     lds_barrier();  // LDS only: the weight loads stay in flight
     // 3. parse and sum
     store_span<CH>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
@@ -619,7 +607,9 @@ extern "C" int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, 
     p.w_bytes = rows * p.row_bytes;
     p.nb = static_cast<int32_t>(nb);
     p.n_vec = static_cast<int32_t>(n_vec);
-    p.x_lds_bytes = static_cast<int32_t>((n_vec * nb * (kQK + sizeof(float) + 16 * sizeof(int16_t)) + 15) & ~int64_t{15});
+    // xq, then xd padded to 16 bytes, then xs (the kernel's layout)
+    const int64_t nblk = n_vec * nb;
+    p.x_lds_bytes = static_cast<int32_t>(nblk * kQK + ((4 * nblk + 15) & ~int64_t{15}) + 32 * nblk);
     p.stage_bytes = 0;
     const hipStream_t st = as_hip(stream);
     switch (type) {
