@@ -789,6 +789,68 @@ def bench_mul_mat_kquant(torch, hip, head, dev, warmup, steps):
                                               dtype=f"{tname} weights / q8_K activations")
             del w
         torch.cuda.empty_cache()
+    out.update(bench_kquant_layer(torch, hip, head, dev, warmup, steps, g))
+    return out
+
+
+def bench_kquant_layer(torch, hip, head, dev, warmup, steps, g):
+    """One LeLM medium decode layer's seven matrices under the Q4_K_M profile
+    (q, k, gate, up Q4_K; v, o, down promoted to Q6_K,
+    src/levo-quantization.h:75-95), CFG pair of activation columns: as 4 Q8_K
+    quantizations + 7 mat-vecs, and with the matrices that share an input in
+    one levo_hip_mul_mat_kquant_multi launch each (q / k / v, o, gate / up,
+    the F32 activations quantized inside the launch) + ffn_down's
+    quantization and mat-vec: 5 launches."""
+    n_vec = 2
+    Q4, Q6 = 12, 14
+    layer = [(Q4, 1536, 1536), (Q4, 1536, 1536), (Q6, 1536, 1536), (Q6, 1536, 1536), (Q4, 8960, 1536),
+             (Q4, 8960, 1536), (Q6, 1536, 8960)]
+    bb = {Q4: 144, Q6: 210}
+    wbytes = [r * (k // 256) * bb[t] for t, r, k in layer]
+    layer_bytes = sum(wbytes) + sum(n_vec * r * 4 for _, r, _ in layer) + n_vec * 4 * (3 * 1536 + 8960)
+    n = math.ceil(ROTATE_BYTES / layer_bytes) + 1
+    mats = []
+    for _ in range(n):
+        ms_ = []
+        for (t, r, k), nb_ in zip(layer, wbytes):
+            w = torch.randint(0, 256, (nb_,), generator=g, device=dev, dtype=torch.uint8)
+            blocks = w.view(-1, bb[t])
+            scale = torch.full((blocks.shape[0], 1), 0x1400, dtype=torch.int16, device=dev).view(torch.uint8)
+            if t == Q6:
+                blocks[:, 208:210] = scale
+            else:
+                blocks[:, 0:2] = scale
+                blocks[:, 2:4] = scale
+            ms_.append(w)
+        mats.append(ms_)
+    xs = {name: torch.randn((n_vec, k), generator=g, device=dev) for name, k in
+          (("attn", 1536), ("out", 1536), ("ffn", 1536), ("hid", 8960))}
+    xbs = {name: torch.empty(n_vec * (x.shape[1] // 256) * 292, dtype=torch.uint8, device=dev)
+           for name, x in xs.items()}
+    y1 = [torch.empty((n_vec, 1536), device=dev) for _ in range(5)]
+    y8 = [torch.empty((n_vec, 8960), device=dev) for _ in range(2)]
+    ys = [y1[0], y1[1], y1[2], y1[3], y8[0], y8[1], y1[4]]
+    src = ["attn", "attn", "attn", "out", "ffn", "ffn", "hid"]
+
+    def run_layer(i):
+        for name in ("attn", "out", "ffn", "hid"):
+            hip.quantize_q8_K(xs[name], xbs[name], xs[name].numel())
+        for j, (t, r, k) in enumerate(layer):
+            hip.mul_mat_kquant(t, mats[i][j].data_ptr(), xbs[src[j]], ys[j], r, r, k, n_vec)
+
+    def run_layer_multi(i):
+        m = lambda j: (layer[j][0], mats[i][j], ys[j], layer[j][1], layer[j][1])
+        hip.mul_mat_kquant_multi([m(0), m(1), m(2)], 1536, n_vec, x=xs["attn"], x_pitch=1536)
+        hip.mul_mat_kquant_multi([m(3)], 1536, n_vec, x=xs["out"], x_pitch=1536)
+        hip.mul_mat_kquant_multi([m(4), m(5)], 1536, n_vec, x=xs["ffn"], x_pitch=1536)
+        hip.quantize_q8_K(xs["hid"], xbs["hid"], xs["hid"].numel())
+        hip.mul_mat_kquant(Q6, mats[i][6].data_ptr(), xbs["hid"], ys[6], 1536, 1536, 8960, n_vec)
+
+    out = {}
+    for name, fn in (("q4_K_M_layer_11_launches", run_layer), ("q4_K_M_layer_5_launches", run_layer_multi)):
+        ms = time_op(torch, head, fn, n, warmup, max(steps, 20))
+        out[name] = op_entry(layer_bytes, ms, n_vec=n_vec, dtype="q4_K / q6_K weights / q8_K activations",
+                             us_per_token_28_layers=round(28 * ms * 1e3, 1))
     return out
 
 

@@ -640,6 +640,33 @@ int levo_hip_quantize_q8_K(const float * x, void * y, int64_t k, levo_hip_stream
 int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
                             int64_t y_pitch, int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream);
 
+/* One matrix of levo_hip_mul_mat_kquant_multi. */
+typedef struct levo_hip_mat_kquant {
+    levo_hip_type type;   /* Q4_K, Q5_K or Q6_K */
+    const void * weight;  /* [rows][k / 256] blocks, 16-byte aligned */
+    float * y;            /* [n_vec][y_pitch] F32 */
+    int64_t y_pitch;      /* >= rows */
+    int64_t rows;
+} levo_hip_mat_kquant;
+
+/* levo_hip_mul_mat_kquant for 1 to 4 matrices, of any of the three types,
+ * that read the same activation columns (a decode layer's q / k / v, or
+ * gate / up: ggml_mul_mat calls that share src1 and quantize it to Q8_K
+ * first; the Q4_K_M / Q5_K_M profiles mix Q4_K or Q5_K with Q6_K in such a
+ * group, src/levo-quantization.h:75-95) in one launch. The activations come
+ * either as block_q8_K (x_blocks, as for levo_hip_mul_mat_kquant) or as F32
+ * x [n_vec][x_pitch] (16-byte aligned, x_pitch >= k and a multiple of 4),
+ * which the launch quantizes itself exactly as levo_hip_quantize_q8_K does,
+ * for n_vec * k <= 4096; pass exactly one of the two. Each y equals what
+ * levo_hip_quantize_q8_K + levo_hip_mul_mat_kquant give for that matrix bit
+ * for bit when the matrices have equal row counts (the launch shares one lane
+ * geometry, chosen for the largest matrix; with unequal row counts the sums
+ * may associate differently, within F32 rounding). Matrices of zero rows are
+ * skipped. */
+int levo_hip_mul_mat_kquant_multi(const levo_hip_mat_kquant * mats, int32_t n_mats, const void * x_blocks,
+                                  const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
+                                  levo_hip_stream_t stream);
+
 /* ggml_fp32_to_fp16_row / ggml_fp16_to_fp32_row (tools/levo-quantize.cpp:
  * 358, 369): IEEE round-to-nearest-even narrowing, exact widening. */
 int levo_hip_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, levo_hip_stream_t stream);

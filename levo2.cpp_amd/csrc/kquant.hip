@@ -80,12 +80,12 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 
 // ---- Q8_K quantizer: one wave per 256-value block ----------------------------
 
-__global__ __launch_bounds__(kThreads) void quantize_q8_K_kernel(const float * __restrict__ x, uint8_t * y,
-                                                                  int64_t nb) {
-    const int lane = threadIdx.x & 63;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
-    if (i >= nb) return;
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(x + i * kQK + 4 * lane);
+// quantize_row_q8_K_ref for the block whose values 4 lane .. 4 lane + 3 this
+// lane holds: its 4 quants packed in a dword, the block's scale d and, in
+// lanes 0-7, bsums 2 lane and 2 lane + 1 packed in a dword. A block of zeros
+// gives d = 0, zero quants and zero bsums.
+__device__ __forceinline__ void q8_K_block(const f32x4 v, int lane, uint32_t & packed, float & d,
+                                           uint32_t & bsum_pair) {
     // first element of largest |x| (NaN never compares larger), as the
     // reference's `if (ax > amax)` scan: key = |x| bits, then lowest index
     uint64_t key = 0;
@@ -101,17 +101,16 @@ __global__ __launch_bounds__(kThreads) void quantize_q8_K_kernel(const float * _
         const uint64_t other = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(key), o, 64));
         key = other > key ? other : key;
     }
-    uint8_t * blk = y + i * 292;
-    if ((key >> 32) == 0) {  // amax == 0: an all-zero block (bsums zero too)
-        reinterpret_cast<uint32_t *>(blk + 4)[lane] = 0u;
-        if (lane < 8) reinterpret_cast<uint32_t *>(blk + 260)[lane] = 0u;
-        if (lane == 0) *reinterpret_cast<float *>(blk) = 0.0f;
+    if ((key >> 32) == 0) {  // amax == 0: an all-zero block
+        packed = 0u;
+        d = 0.0f;
+        bsum_pair = 0u;
         return;
     }
     const int arg = 255 - static_cast<int>(key & 0xffu);
     const float max = __shfl(v[arg & 3], arg >> 2, 64);
     const float iscale = -127.0f / max;
-    uint32_t packed = 0;
+    packed = 0;
     int sum = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -120,17 +119,28 @@ __global__ __launch_bounds__(kThreads) void quantize_q8_K_kernel(const float * _
         sum += l;
         packed |= (static_cast<uint32_t>(l) & 0xffu) << (8 * q);
     }
-    reinterpret_cast<uint32_t *>(blk + 4)[lane] = packed;
     // bsums[j]: elements 16 j .. 16 j + 15 = lanes 4 j .. 4 j + 3
     sum += __shfl_xor(sum, 1, 64);
     sum += __shfl_xor(sum, 2, 64);
     const int lo = __shfl(sum, 8 * (lane & 7), 64);
     const int hi = __shfl(sum, 8 * (lane & 7) + 4, 64);
-    if (lane < 8) {
-        reinterpret_cast<uint32_t *>(blk + 260)[lane] =
-                (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
-    }
-    if (lane == 0) *reinterpret_cast<float *>(blk) = 1.0f / iscale;
+    bsum_pair = (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
+    d = 1.0f / iscale;
+}
+
+__global__ __launch_bounds__(kThreads) void quantize_q8_K_kernel(const float * __restrict__ x, uint8_t * y,
+                                                                  int64_t nb) {
+    const int lane = threadIdx.x & 63;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+    if (i >= nb) return;
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(x + i * kQK + 4 * lane);
+    uint32_t packed, bsum_pair;
+    float d;
+    q8_K_block(v, lane, packed, d, bsum_pair);
+    uint8_t * blk = y + i * 292;
+    reinterpret_cast<uint32_t *>(blk + 4)[lane] = packed;
+    if (lane < 8) reinterpret_cast<uint32_t *>(blk + 260)[lane] = bsum_pair;
+    if (lane == 0) *reinterpret_cast<float *>(blk) = d;
 }
 
 // ---- dequantizers: 8 outputs per thread --------------------------------------
@@ -205,16 +215,28 @@ __global__ __launch_bounds__(kThreads) void dequantize_kquant_kernel(const uint8
 // ---- mat-vec: one wave per row, 8 lanes per super-block ----------------------
 
 constexpr int kMaxVec = 8;
-constexpr int kXVec = 6;  // activation dwordx4 a thread requests up front (24 KiB per workgroup)
+constexpr int kXVec = 6;         // activation dwordx4 a thread requests up front (24 KiB per workgroup)
+constexpr int kMaxMats = 4;      // matrices of one launch
+constexpr int kFusedBlocks = 16; // F32 activations quantized in the launch: n_vec * k / 256 <= 16
 
-struct kq_params {
+// One matrix of a launch: workgroups [first_wg, next matrix's first_wg).
+struct kq_mat {
     const uint8_t * w;      // [rows][nb] blocks, 16-byte aligned
-    const uint8_t * x;      // [n_vec][nb] block_q8_K
     float * y;              // [n_vec][y_pitch]
     int64_t y_pitch;
     int64_t rows;
     int64_t row_bytes;
     int64_t w_bytes;        // rows * row_bytes
+    int32_t type;
+    int32_t first_wg;
+};
+
+struct kq_params {
+    kq_mat m[kMaxMats];
+    int32_t n_mats;
+    const uint8_t * x;      // [n_vec][nb] block_q8_K, or null
+    const float * xf;       // F32 activations [n_vec][xf_pitch] (quantized in the launch), or null
+    int64_t xf_pitch;
     int32_t nb;
     int32_t n_vec;
     int32_t x_lds_bytes;    // staged activations, 16-byte multiple
@@ -352,7 +374,45 @@ __device__ __forceinline__ void kq_compute(const kq_unit<TYPE> & w, int ib, int 
 //      gives y.
 // WPR > 1 (LPR = 64): WPR waves share a row, each a contiguous part of its
 // super-blocks; their partial sums meet in LDS and are added in wave order.
-template <int TYPE, int LPR, int U, int CH, int WPR = 1>
+// The units of the wave's rows that lane li of row group g takes, parsed
+// from the wave's LDS stage (the row's blocks kb0 .. kb0 + units / 8).
+template <int TYPE, int LPR, int U>
+__device__ __forceinline__ void kq_units(const uint8_t * stage, int lead, int g, int li, int row_bytes, int units,
+                                         int kb0, int nb, int n_vec, const int8_t * xq, const float * xd,
+                                         const int16_t * xs, float (&acc_d)[kMaxVec], float (&acc_m)[kMaxVec]) {
+    constexpr int kBytes = TYPE == LEVO_HIP_TYPE_Q4_K ? 144 : TYPE == LEVO_HIP_TYPE_Q5_K ? 176 : 210;
+#pragma unroll
+    for (int i = 0; i < U; ++i) {
+        const int unit = li + LPR * i;
+        if (unit < units) {
+            const int off = lead + g * row_bytes + (unit >> 3) * kBytes;
+            kq_unit<TYPE> w;
+            w.load(stage + off, unit & 7, (off & 2) != 0);
+            kq_compute<TYPE>(w, kb0 + (unit >> 3), unit & 7, nb, n_vec, xq, xd, xs, acc_d, acc_m);
+        }
+    }
+}
+
+// LPR lanes per row, 64 / LPR rows per wave; lane li of its row's group
+// takes the units li + LPR i (i < U) of the row's 8 nb units (unit = eighth of
+// a 256-value block, 32 weights). Per workgroup (4 waves, 4 * 64 / LPR rows of
+// one matrix, the matrix's type chosen once per workgroup):
+//   1. each wave requests its rows' contiguous weight bytes with coalesced
+//      dwordx4 loads (CH chunks per lane, all in flight);
+//   2. meanwhile the workgroup stages the Q8_K activations in LDS, laid out
+//      so that each lane's quants are aligned: xq [n_vec][256 nb] int8, then
+//      xd [n_vec][nb] float, xs [n_vec][16 nb] int16 (the bsums); FUSED: it
+//      quantizes F32 activations into that layout itself, one wave per block
+//      as levo_hip_quantize_q8_K does;
+//   3. each wave stores its span to its LDS stage area; each lane parses its
+//      units there and adds their terms; a reduction over the row's LPR lanes
+//      gives y.
+// WPR > 1 (LPR = 64): WPR waves share a row, each a contiguous part of its
+// super-blocks; their partial sums meet in LDS and are added in wave order.
+// TYPE: the weight type when every matrix of the launch has it, else 0 (the
+// type read per workgroup from its matrix). ONE: a launch of one matrix (no
+// per-workgroup matrix lookup: its fields load with the other arguments).
+template <int TYPE, int LPR, int U, int CH, int WPR, bool FUSED, bool ONE>
 __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_params p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_raw[];
     const int nb = p.nb;
@@ -365,67 +425,106 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
     const int wave = tid >> 6;
     uint8_t * stage = lds_raw + p.x_lds_bytes + wave * p.stage_bytes;
     constexpr int kRowsPerWave = 64 / LPR;
-    constexpr int kBytes = TYPE == LEVO_HIP_TYPE_Q4_K ? 144 : TYPE == LEVO_HIP_TYPE_Q5_K ? 176 : 210;
+    // this workgroup's matrix (uniform) and its index within the matrix
+    int mi = 0;
+    if constexpr (!ONE) {
+#pragma unroll
+        for (int i = 1; i < kMaxMats; ++i) {
+            if (i < p.n_mats && static_cast<int>(blockIdx.x) >= p.m[i].first_wg) mi = i;
+        }
+    }
+    const kq_mat & M = p.m[mi];
+    const int64_t lb = static_cast<int64_t>(blockIdx.x) - M.first_wg;
+    const int kbytes = TYPE == LEVO_HIP_TYPE_Q4_K   ? 144
+                       : TYPE == LEVO_HIP_TYPE_Q5_K ? 176
+                       : TYPE == LEVO_HIP_TYPE_Q6_K ? 210
+                                                    : static_cast<int>(M.row_bytes / nb);
     // 1. the wave's rows [row0, row0 + nrows): bytes [sb0, sb1); with WPR > 1
     //    the WPR waves of a row each take a contiguous part of its blocks,
     //    [kb0, kb1)
     int64_t row0;
     int nrows, kb0, kb1;
     if constexpr (WPR > 1) {
-        row0 = static_cast<int64_t>(blockIdx.x) * (kThreads / 64 / WPR) + wave / WPR;
-        nrows = row0 < p.rows ? 1 : 0;
+        row0 = lb * (kThreads / 64 / WPR) + wave / WPR;
+        nrows = row0 < M.rows ? 1 : 0;
         const int qb = (nb + WPR - 1) / WPR;
         kb0 = (wave % WPR) * qb;
         kb1 = kb0 + qb < nb ? kb0 + qb : nb;
         if (kb0 >= kb1) nrows = 0;
     } else {
-        row0 = (static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + wave) * kRowsPerWave;
-        const int64_t left = p.rows - row0;
+        row0 = (lb * (kThreads / 64) + wave) * kRowsPerWave;
+        const int64_t left = M.rows - row0;
         nrows = left < kRowsPerWave ? (left > 0 ? static_cast<int>(left) : 0) : kRowsPerWave;
         kb0 = 0;
         kb1 = nb;
     }
-    const int64_t sb0 = row0 * p.row_bytes + static_cast<int64_t>(kb0) * kBytes;
-    const int64_t sb1 = WPR > 1 ? row0 * p.row_bytes + static_cast<int64_t>(kb1) * kBytes
-                                : sb0 + nrows * p.row_bytes;
-    // The activations: n_vec * nb block_q8_K of 292 bytes (f32 d, int8
-    // qs[256], int16 bsums[16]) go to LDS as xq [nblk][256], xd [nblk] and
-    // xs [nblk][16], by whole pieces: 16 quant chunks, the scale and 2 bsum
-    // chunks per block, chunk c of a region at byte 16 c (LDS stores stay
-    // 16-byte aligned; the global reads are 4-byte aligned). The first chunks
-    // are requested before the weights, with no branch around them (surplus
-    // requests re-read the last chunk): loads complete in issue order, so they
-    // are stored while the weights are in flight.
-    const uint8_t * xg = p.x;
-    const auto qchunk = [&](int c) {
-        return *reinterpret_cast<const u32x4 *>(xg + 292 * static_cast<int64_t>(c >> 4) + 4 + 16 * (c & 15));
-    };
-    const auto schunk = [&](int c) {
-        return *reinterpret_cast<const u32x4 *>(xg + 292 * static_cast<int64_t>(c >> 1) + 260 + 16 * (c & 1));
-    };
-    const auto dword = [&](int b) { return *reinterpret_cast<const uint32_t *>(xg + 292 * static_cast<int64_t>(b)); };
-    const int n_q = 16 * nblk;
-    u32x4 xr[kXVec];
-#pragma unroll
-    for (int j = 0; j < kXVec; ++j) xr[j] = qchunk(min(tid + kThreads * j, n_q - 1));
-    const uint32_t d0 = dword(min(tid, nblk - 1));
-    const u32x4 s0 = schunk(min(tid, 2 * nblk - 1));
+    const int64_t sb0 = row0 * M.row_bytes + static_cast<int64_t>(kb0) * kbytes;
+    const int64_t sb1 = WPR > 1 ? row0 * M.row_bytes + static_cast<int64_t>(kb1) * kbytes
+                                : sb0 + nrows * M.row_bytes;
     u32x4 regs[CH];
-    load_span<CH>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
-    // 2. store them (and fetch any the first requests did not cover)
+    if constexpr (FUSED) {
+        // F32 activations, block b = (vector b / nb, super-block b % nb): the
+        // wave's blocks b = wave + 4 i are requested first, then the weights
+        f32x4 xv[kFusedBlocks / 4];
 #pragma unroll
-    for (int j = 0; j < kXVec; ++j) {
-        const int c = tid + kThreads * j;
-        if (c < n_q) reinterpret_cast<u32x4 *>(xq)[c] = xr[j];
+        for (int i = 0; i < kFusedBlocks / 4; ++i) {
+            const int b = min(wave + 4 * i, nblk - 1);
+            xv[i] = *reinterpret_cast<const f32x4 *>(p.xf + (b / nb) * p.xf_pitch + (b % nb) * kQK + 4 * lane);
+        }
+        load_span<CH>(M.w, M.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
+#pragma unroll
+        for (int i = 0; i < kFusedBlocks / 4; ++i) {
+            const int b = wave + 4 * i;
+            if (b < nblk) {
+                uint32_t packed, bsum_pair;
+                float d;
+                q8_K_block(xv[i], lane, packed, d, bsum_pair);
+                reinterpret_cast<uint32_t *>(xq)[b * 64 + lane] = packed;
+                if (lane < 8) reinterpret_cast<uint32_t *>(xs)[b * 8 + lane] = bsum_pair;
+                if (lane == 0) xd[b] = d;
+            }
+        }
+    } else {
+        // The activations: n_vec * nb block_q8_K of 292 bytes (f32 d, int8
+        // qs[256], int16 bsums[16]) go to LDS by whole pieces: 16 quant
+        // chunks, the scale and 2 bsum chunks per block, chunk c of a region
+        // at byte 16 c (LDS stores stay 16-byte aligned; the global reads are
+        // 4-byte aligned). The first chunks are requested before the weights,
+        // with no branch around them (surplus requests re-read the last
+        // chunk): loads complete in issue order, so they are stored while the
+        // weights are in flight.
+        const uint8_t * xg = p.x;
+        const auto qchunk = [&](int c) {
+            return *reinterpret_cast<const u32x4 *>(xg + 292 * static_cast<int64_t>(c >> 4) + 4 + 16 * (c & 15));
+        };
+        const auto schunk = [&](int c) {
+            return *reinterpret_cast<const u32x4 *>(xg + 292 * static_cast<int64_t>(c >> 1) + 260 + 16 * (c & 1));
+        };
+        const auto dword = [&](int b) {
+            return *reinterpret_cast<const uint32_t *>(xg + 292 * static_cast<int64_t>(b));
+        };
+        const int n_q = 16 * nblk;
+        u32x4 xr[kXVec];
+#pragma unroll
+        for (int j = 0; j < kXVec; ++j) xr[j] = qchunk(min(tid + kThreads * j, n_q - 1));
+        const uint32_t d0 = dword(min(tid, nblk - 1));
+        const u32x4 s0 = schunk(min(tid, 2 * nblk - 1));
+        load_span<CH>(M.w, M.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
+        // 2. store them (and fetch any the first requests did not cover)
+#pragma unroll
+        for (int j = 0; j < kXVec; ++j) {
+            const int c = tid + kThreads * j;
+            if (c < n_q) reinterpret_cast<u32x4 *>(xq)[c] = xr[j];
+        }
+        if (tid < nblk) xd[tid] = __builtin_bit_cast(float, d0);
+        if (tid < 2 * nblk) reinterpret_cast<u32x4 *>(xs)[tid] = s0;
+        for (int c = tid + kThreads * kXVec; c < n_q; c += kThreads) reinterpret_cast<u32x4 *>(xq)[c] = qchunk(c);
+        for (int b = tid + kThreads; b < nblk; b += kThreads) xd[b] = __builtin_bit_cast(float, dword(b));
+        for (int c = tid + kThreads; c < 2 * nblk; c += kThreads) reinterpret_cast<u32x4 *>(xs)[c] = schunk(c);
     }
-    if (tid < nblk) xd[tid] = __builtin_bit_cast(float, d0);
-    if (tid < 2 * nblk) reinterpret_cast<u32x4 *>(xs)[tid] = s0;
-    for (int c = tid + kThreads * kXVec; c < n_q; c += kThreads) reinterpret_cast<u32x4 *>(xq)[c] = qchunk(c);
-    for (int b = tid + kThreads; b < nblk; b += kThreads) xd[b] = __builtin_bit_cast(float, dword(b));
-    for (int c = tid + kThreads; c < 2 * nblk; c += kThreads) reinterpret_cast<u32x4 *>(xs)[c] = schunk(c);
     lds_barrier();  // LDS only: the weight loads stay in flight
     // 3. parse and sum
-    store_span<CH>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
+    store_span<CH>(stage, M.w, M.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
     wave_lds_fence();
     const int g = lane / LPR;
     const int li = lane % LPR;
@@ -436,18 +535,21 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
 #pragma unroll
     for (int v = 0; v < kMaxVec; ++v) acc_d[v] = acc_m[v] = 0.0f;
     if (live) {
-#pragma unroll
-        for (int i = 0; i < U; ++i) {
-            const int unit = li + LPR * i;
-            if (unit < units) {
-                const int off = lead + g * static_cast<int>(p.row_bytes) + (unit >> 3) * kBytes;
-                kq_unit<TYPE> w;
-                w.load(stage + off, unit & 7, (off & 2) != 0);
-                kq_compute<TYPE>(w, kb0 + (unit >> 3), unit & 7, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
-            }
+        const int rb = static_cast<int>(M.row_bytes);
+        if constexpr (TYPE != 0) {
+            kq_units<TYPE, LPR, U>(stage, lead, g, li, rb, units, kb0, nb, p.n_vec, xq, xd, xs, acc_d, acc_m);
+        } else if (M.type == LEVO_HIP_TYPE_Q4_K) {
+            kq_units<LEVO_HIP_TYPE_Q4_K, LPR, U>(stage, lead, g, li, rb, units, kb0, nb, p.n_vec, xq, xd, xs, acc_d,
+                                                 acc_m);
+        } else if (M.type == LEVO_HIP_TYPE_Q5_K) {
+            kq_units<LEVO_HIP_TYPE_Q5_K, LPR, U>(stage, lead, g, li, rb, units, kb0, nb, p.n_vec, xq, xd, xs, acc_d,
+                                                 acc_m);
+        } else {
+            kq_units<LEVO_HIP_TYPE_Q6_K, LPR, U>(stage, lead, g, li, rb, units, kb0, nb, p.n_vec, xq, xd, xs, acc_d,
+                                                 acc_m);
         }
     }
-    // every lane of the wave takes part in the shuffles
+    // every lane of the wave takes part in the shuffles (acc_m stays 0 for Q6_K)
     if constexpr (WPR > 1) {
         // the row's parts meet in LDS, each at the start of its wave's own
         // stage area (no longer read once the wave has computed), summed in
@@ -457,7 +559,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
         for (int v = 0; v < kMaxVec; ++v) {
             if (v < p.n_vec) {
                 const float sd = group_sum<LPR>(acc_d[v]);
-                const float sm = TYPE != LEVO_HIP_TYPE_Q6_K ? group_sum<LPR>(acc_m[v]) : 0.0f;
+                const float sm = group_sum<LPR>(acc_m[v]);
                 if (lane == 0) {
                     part[2 * v] = sd;
                     part[2 * v + 1] = sm;
@@ -465,7 +567,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
             }
         }
         __syncthreads();
-        if (wave % WPR == 0 && lane < p.n_vec && row0 < p.rows) {
+        if (wave % WPR == 0 && lane < p.n_vec && row0 < M.rows) {
             float sd = part[2 * lane], sm = part[2 * lane + 1];
 #pragma unroll
             for (int w = 1; w < WPR; ++w) {
@@ -473,43 +575,83 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
                 sd += other[2 * lane];
                 sm += other[2 * lane + 1];
             }
-            p.y[lane * p.y_pitch + row0] = sd - sm;
+            M.y[lane * M.y_pitch + row0] = sd - sm;
         }
     } else {
 #pragma unroll
         for (int v = 0; v < kMaxVec; ++v) {
             if (v < p.n_vec) {
                 const float sd = group_sum<LPR>(acc_d[v]);
-                const float sm = TYPE != LEVO_HIP_TYPE_Q6_K ? group_sum<LPR>(acc_m[v]) : 0.0f;
-                if (live && li == 0) p.y[v * p.y_pitch + row0 + g] = sd - sm;
+                const float sm = group_sum<LPR>(acc_m[v]);
+                if (live && li == 0) M.y[v * M.y_pitch + row0 + g] = sd - sm;
             }
         }
     }
 }
 
-template <int TYPE, int LPR, int U, int CH, int WPR = 1>
-int launch_mul_mat_u(kq_params p, hipStream_t st) {
-    if (const int st = allow_dynamic_lds(reinterpret_cast<const void *>(&mul_mat_kquant_kernel<TYPE, LPR, U, CH, WPR>),
-                                         160 * 1024, "levo_hip_mul_mat_kquant");
-        st != LEVO_HIP_OK)
-        return st;
+template <int TYPE, int LPR, int U, int CH, int WPR, bool FUSED>
+int launch_mul_mat_t(kq_params p, int64_t max_row_bytes, hipStream_t st) {
+    const auto kernel = TYPE != 0 && p.n_mats == 1 ? mul_mat_kquant_kernel<TYPE, LPR, U, CH, WPR, FUSED, true>
+                                                   : mul_mat_kquant_kernel<TYPE, LPR, U, CH, WPR, FUSED, false>;
+    if (const int rc = allow_dynamic_lds(reinterpret_cast<const void *>(kernel), 160 * 1024, "levo_hip_mul_mat_kquant");
+        rc != LEVO_HIP_OK)
+        return rc;
     constexpr int kRowsPerWave = 64 / LPR;
-    const int64_t span = WPR > 1 ? ceil_div(p.nb, WPR) * (p.row_bytes / p.nb) : kRowsPerWave * p.row_bytes;
+    const int64_t span = WPR > 1 ? ceil_div(p.nb, WPR) * (max_row_bytes / p.nb) : kRowsPerWave * max_row_bytes;
     LEVO_REQUIRE(span + 15 <= int64_t{CH} * 64 * 16, "mul_mat_kquant: row span exceeds the wave's registers");
     LEVO_REQUIRE(WPR == 1 || ceil_div(p.nb, WPR) * 8 <= int64_t{U} * LPR, "mul_mat_kquant: row part exceeds the lanes");
+    LEVO_REQUIRE(WPR > 1 || int64_t{p.nb} * 8 <= int64_t{U} * LPR, "mul_mat_kquant: row exceeds the lanes");
     p.stage_bytes = static_cast<int32_t>((span + 15 + 15) & ~int64_t{15});
     const size_t lds = static_cast<size_t>(p.x_lds_bytes) + static_cast<size_t>(kThreads / 64) * p.stage_bytes;
     LEVO_REQUIRE(lds <= 160 * 1024, "mul_mat_kquant: n_vec * k too large for the workgroup's LDS");
     const int64_t rows_per_block = WPR > 1 ? (kThreads / 64) / WPR : (kThreads / 64) * kRowsPerWave;
-    const dim3 grid(static_cast<uint32_t>(ceil_div(p.rows, rows_per_block)));
-    mul_mat_kquant_kernel<TYPE, LPR, U, CH, WPR><<<grid, kThreads, lds, st>>>(p);
+    int64_t wgs = 0;
+    for (int i = 0; i < p.n_mats; ++i) {
+        p.m[i].first_wg = static_cast<int32_t>(wgs);
+        wgs += ceil_div(p.m[i].rows, rows_per_block);
+    }
+    LEVO_REQUIRE(wgs < (int64_t{1} << 31) / kThreads, "mul_mat_kquant: too many rows");
+    kernel<<<dim3(static_cast<uint32_t>(wgs)), kThreads, lds, st>>>(p);
     return launch_status("levo_hip_mul_mat_kquant");
 }
 
+// The instance for the launch's types (one shared type, or mixed) and
+// activation source. F32 activations (at most 16 blocks, so k <= 4096) only
+// reach the geometries of up to 16 units per lane row.
+template <int LPR, int U, int CH, int WPR = 1>
+int launch_mul_mat_u(kq_params p, int64_t max_row_bytes, hipStream_t st) {
+    int type = p.m[0].type;
+    for (int i = 1; i < p.n_mats; ++i) type = p.m[i].type == type ? type : 0;
+    constexpr bool kFusable = WPR == 1 && U * LPR <= 128;
+    if (p.xf != nullptr) {
+        if constexpr (kFusable) {
+            switch (type) {
+                case LEVO_HIP_TYPE_Q4_K: return launch_mul_mat_t<LEVO_HIP_TYPE_Q4_K, LPR, U, CH, WPR, true>(p, max_row_bytes, st);
+                case LEVO_HIP_TYPE_Q5_K: return launch_mul_mat_t<LEVO_HIP_TYPE_Q5_K, LPR, U, CH, WPR, true>(p, max_row_bytes, st);
+                case LEVO_HIP_TYPE_Q6_K: return launch_mul_mat_t<LEVO_HIP_TYPE_Q6_K, LPR, U, CH, WPR, true>(p, max_row_bytes, st);
+                default: return launch_mul_mat_t<0, LPR, U, CH, WPR, true>(p, max_row_bytes, st);
+            }
+        } else {
+            LEVO_REQUIRE(false, "mul_mat_kquant: F32 activations need k <= 4096");
+        }
+    }
+    switch (type) {
+        case LEVO_HIP_TYPE_Q4_K: return launch_mul_mat_t<LEVO_HIP_TYPE_Q4_K, LPR, U, CH, WPR, false>(p, max_row_bytes, st);
+        case LEVO_HIP_TYPE_Q5_K: return launch_mul_mat_t<LEVO_HIP_TYPE_Q5_K, LPR, U, CH, WPR, false>(p, max_row_bytes, st);
+        case LEVO_HIP_TYPE_Q6_K: return launch_mul_mat_t<LEVO_HIP_TYPE_Q6_K, LPR, U, CH, WPR, false>(p, max_row_bytes, st);
+        default: return launch_mul_mat_t<0, LPR, U, CH, WPR, false>(p, max_row_bytes, st);
+    }
+}
+
 // Lanes per row, units per lane and span chunks per lane by the row's 8 nb
-// units (k <= 16384): a wave's span is 64 / LPR rows, or half a row.
-template <int TYPE>
-int launch_mul_mat(const kq_params & p, hipStream_t st) {
+// units (k <= 16384) and the largest matrix's rows: a wave's span is 64 / LPR
+// rows, or half a row. Spans are sized for the largest row of the launch.
+int launch_mul_mat(kq_params & p, hipStream_t st) {
+    int64_t rows = 0, rb = 0;
+    for (int i = 0; i < p.n_mats; ++i) {
+        rows = p.m[i].rows > rows ? p.m[i].rows : rows;
+        rb = p.m[i].row_bytes > rb ? p.m[i].row_bytes : rb;
+    }
     const int units = p.nb * 8;
     if (units <= 64) {
         // K <= 2048: the fewest lanes per row (the most rows per workgroup,
@@ -517,17 +659,20 @@ int launch_mul_mat(const kq_params & p, hipStream_t st) {
         // workgroups or more: 16 rows per workgroup from 4096 rows, 8 from
         // 2048, else 4 (1536 x 1536 Q4_K 4.69 -> 3.68 us, Q6_K 5.29 -> 3.99;
         // at 8960 and 16385 rows 16 lanes per row stay fastest)
-        if (p.rows >= 4096) return launch_mul_mat_u<TYPE, 16, 4, 8>(p, st);
-        if (p.rows >= 2048) return launch_mul_mat_u<TYPE, 32, 2, 4>(p, st);
-        return launch_mul_mat_u<TYPE, 64, 1, 2>(p, st);
+        if (rows >= 4096) return launch_mul_mat_u<16, 4, 8>(p, rb, st);
+        if (rows >= 2048) return launch_mul_mat_u<32, 2, 4>(p, rb, st);
+        return launch_mul_mat_u<64, 1, 2>(p, rb, st);
     }
-    if (units <= 128) return launch_mul_mat_u<TYPE, 16, 8, 16>(p, st);
-    if (units <= 256) return launch_mul_mat_u<TYPE, 32, 8, 16>(p, st);
+    if (units <= 128) return launch_mul_mat_u<16, 8, 16>(p, rb, st);
+    if (units <= 256) return launch_mul_mat_u<32, 8, 16>(p, rb, st);
     // K > 8192 (LeLM's ffn_down, K = 8960): a row over two waves, each half
     // its super-blocks, so each lane takes ~2 units instead of ~4 (Q4_K
-    // 10.2 -> 9.4 us; four waves per row, 11.1 us, repeat the activation
-    // staging in twice as many workgroups)
-    return launch_mul_mat_u<TYPE, 64, 4, 7, 2>(p, st);
+    // 10.2 -> 9.4 us). Up to 38 super-blocks the half-row spans fit 4 chunks
+    // per lane and 3 units per lane (Q4_K 6.75 -> 6.40 us, Q6_K 7.9 -> 7.6 us
+    // against 7 chunks and 4 units); one row per wave measured 6.9 / 8.8 us
+    // and four waves per row 6.95 / 8.2 us.
+    if (p.nb <= 38) return launch_mul_mat_u<64, 3, 4, 2>(p, rb, st);
+    return launch_mul_mat_u<64, 4, 7, 2>(p, rb, st);
 }
 
 }  // namespace
@@ -583,38 +728,71 @@ extern "C" int levo_hip_quantize_q8_K(const float * x, void * y, int64_t k, levo
     return launch_status("levo_hip_quantize_q8_K");
 }
 
-extern "C" int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
-                                       int64_t y_pitch, int64_t rows, int64_t k, int64_t n_vec,
-                                       levo_hip_stream_t stream) {
-    LEVO_REQUIRE(is_kquant(type), "mul_mat_kquant: weight type must be Q4_K, Q5_K or Q6_K");
+namespace {
+
+int mul_mat_kquant_launch(const levo_hip_mat_kquant * mats, int32_t n_mats, const void * x_blocks, const float * x,
+                          int64_t x_pitch, int64_t k, int64_t n_vec, hipStream_t st) {
+    LEVO_REQUIRE(n_mats >= 1 && n_mats <= kMaxMats, "mul_mat_kquant: 1 to 4 matrices per launch");
+    LEVO_REQUIRE(mats != nullptr, "mul_mat_kquant: null matrix list");
     LEVO_REQUIRE(k > 0 && k % kQK == 0, "mul_mat_kquant: k must be a positive multiple of 256");
     LEVO_REQUIRE(k <= 16384, "mul_mat_kquant: k must be at most 16384");
-    LEVO_REQUIRE(rows >= 0 && rows < (int64_t{1} << 31), "mul_mat_kquant: bad row count");
     LEVO_REQUIRE(n_vec >= 1 && n_vec <= kMaxVec, "mul_mat_kquant: n_vec must be 1..8");
-    LEVO_REQUIRE(y_pitch >= rows, "mul_mat_kquant: y_pitch smaller than rows");
     const int64_t nb = k / kQK;
-    if (rows == 0) return LEVO_HIP_OK;
-    LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "mul_mat_kquant: null pointer");
-    LEVO_REQUIRE(aligned16(weight), "mul_mat_kquant: weight must be 16-byte aligned");
-    LEVO_REQUIRE((reinterpret_cast<uintptr_t>(x_blocks) & 3u) == 0, "mul_mat_kquant: x_blocks must be 4-byte aligned");
-    kq_params p;
-    p.w = static_cast<const uint8_t *>(weight);
+    const int64_t nblk = n_vec * nb;
+    kq_params p{};
+    p.n_mats = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        const levo_hip_mat_kquant & m = mats[i];
+        LEVO_REQUIRE(is_kquant(m.type), "mul_mat_kquant: weight type must be Q4_K, Q5_K or Q6_K");
+        LEVO_REQUIRE(m.rows >= 0 && m.rows < (int64_t{1} << 31), "mul_mat_kquant: bad row count");
+        LEVO_REQUIRE(m.y_pitch >= m.rows, "mul_mat_kquant: y_pitch smaller than rows");
+        if (m.rows == 0) continue;
+        LEVO_REQUIRE(m.weight != nullptr && m.y != nullptr, "mul_mat_kquant: null pointer");
+        LEVO_REQUIRE(aligned16(m.weight), "mul_mat_kquant: weight must be 16-byte aligned");
+        kq_mat & q = p.m[p.n_mats++];
+        q.w = static_cast<const uint8_t *>(m.weight);
+        q.y = m.y;
+        q.y_pitch = m.y_pitch;
+        q.rows = m.rows;
+        q.row_bytes = nb * kquant_block_bytes(m.type);
+        q.w_bytes = m.rows * q.row_bytes;
+        q.type = static_cast<int32_t>(m.type);
+        q.first_wg = 0;
+    }
+    if (p.n_mats == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE((x_blocks == nullptr) != (x == nullptr), "mul_mat_kquant: pass exactly one of x_blocks and x");
+    if (x_blocks != nullptr) {
+        LEVO_REQUIRE((reinterpret_cast<uintptr_t>(x_blocks) & 3u) == 0,
+                     "mul_mat_kquant: x_blocks must be 4-byte aligned");
+    } else {
+        LEVO_REQUIRE(nblk <= kFusedBlocks,
+                     "mul_mat_kquant: F32 activations take n_vec * k <= 4096 (quantize larger ones to Q8_K first)");
+        LEVO_REQUIRE(aligned16(x) && x_pitch >= k && x_pitch % 4 == 0,
+                     "mul_mat_kquant: x must be 16-byte aligned with x_pitch >= k, a multiple of 4");
+    }
     p.x = static_cast<const uint8_t *>(x_blocks);
-    p.y = y;
-    p.y_pitch = y_pitch;
-    p.rows = rows;
-    p.row_bytes = nb * kquant_block_bytes(type);
-    p.w_bytes = rows * p.row_bytes;
+    p.xf = x;
+    p.xf_pitch = x_pitch;
     p.nb = static_cast<int32_t>(nb);
     p.n_vec = static_cast<int32_t>(n_vec);
     // xq, then xd padded to 16 bytes, then xs (the kernel's layout)
-    const int64_t nblk = n_vec * nb;
     p.x_lds_bytes = static_cast<int32_t>(nblk * kQK + ((4 * nblk + 15) & ~int64_t{15}) + 32 * nblk);
     p.stage_bytes = 0;
-    const hipStream_t st = as_hip(stream);
-    switch (type) {
-        case LEVO_HIP_TYPE_Q4_K: return launch_mul_mat<LEVO_HIP_TYPE_Q4_K>(p, st);
-        case LEVO_HIP_TYPE_Q5_K: return launch_mul_mat<LEVO_HIP_TYPE_Q5_K>(p, st);
-        default: return launch_mul_mat<LEVO_HIP_TYPE_Q6_K>(p, st);
-    }
+    return launch_mul_mat(p, st);
+}
+
+}  // namespace
+
+extern "C" int levo_hip_mul_mat_kquant(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
+                                       int64_t y_pitch, int64_t rows, int64_t k, int64_t n_vec,
+                                       levo_hip_stream_t stream) {
+    LEVO_REQUIRE(x_blocks != nullptr || rows == 0, "mul_mat_kquant: null pointer");
+    const levo_hip_mat_kquant m{type, weight, y, y_pitch, rows};
+    return mul_mat_kquant_launch(&m, 1, x_blocks, nullptr, 0, k, n_vec, as_hip(stream));
+}
+
+extern "C" int levo_hip_mul_mat_kquant_multi(const levo_hip_mat_kquant * mats, int32_t n_mats, const void * x_blocks,
+                                             const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
+                                             levo_hip_stream_t stream) {
+    return mul_mat_kquant_launch(mats, n_mats, x_blocks, x, x_pitch, k, n_vec, as_hip(stream));
 }

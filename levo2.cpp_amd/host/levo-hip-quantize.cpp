@@ -59,6 +59,16 @@ void mul_mat_kquant_quantized(levo_hip_type type, const void * weight, const voi
     check_status(levo_hip_mul_mat_kquant(type, weight, x_blocks, y, rows, rows, k, n_vec, stream));
 }
 
+void mul_mat_kquant_shared_input(const kquant_matrix * mats, int n_mats, const float * x, int64_t k, int64_t n_vec,
+                                 stream_t stream) {
+    levo_hip_mat_kquant m[4] = {};
+    const int n = n_mats < 0 ? 0 : n_mats;
+    for (int i = 0; i < n && i < 4; ++i) {
+        m[i] = levo_hip_mat_kquant{mats[i].type, mats[i].weight, mats[i].y, mats[i].rows, mats[i].rows};
+    }
+    check_status(levo_hip_mul_mat_kquant_multi(m, n_mats, nullptr, x, k, k, n_vec, stream));
+}
+
 void dequantize_row(levo_hip_type type, const void * src, float * dst, int64_t k, stream_t stream) {
     check_status(levo_hip_dequantize(type, src, dst, LEVO_HIP_TYPE_F32, k, stream));
 }

@@ -76,6 +76,22 @@ void mul_mat_kquant(levo_hip_type type, const void * weight, const float * x, vo
 void mul_mat_kquant_quantized(levo_hip_type type, const void * weight, const void * x_blocks, float * y,
                               int64_t rows, int64_t k, int64_t n_vec, stream_t stream = nullptr);
 
+// Up to four K-quant matrices, of any of Q4_K / Q5_K / Q6_K, that read the same
+// F32 input x [n_vec][k] (a layer's q / k / v or gate / up under the Q4_K_M
+// and Q5_K_M profiles, which mix in Q6_K matrices) in one launch, the input
+// quantized to Q8_K inside it: each y equals mul_mat_kquant's for that matrix,
+// bit for bit, when the matrices have equal row counts. Needs n_vec * k <=
+// 4096 and x 16-byte aligned; quantize larger inputs with mul_mat_kquant and
+// pass the blocks to mul_mat_kquant_quantized.
+struct kquant_matrix {
+    levo_hip_type type;
+    const void * weight;  // [rows][k / 256] blocks, 16-byte aligned
+    float * y;            // [n_vec][rows]
+    int64_t rows;
+};
+void mul_mat_kquant_shared_input(const kquant_matrix * mats, int n_mats, const float * x, int64_t k, int64_t n_vec,
+                                 stream_t stream = nullptr);
+
 void fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n, stream_t stream = nullptr);
 void fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n, stream_t stream = nullptr);
 

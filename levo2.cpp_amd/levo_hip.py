@@ -62,6 +62,12 @@ class MatQ8_0(ctypes.Structure):
     _fields_ = [("weight", _P), ("y", _P), ("y_pitch", _I64), ("rows", _I64)]
 
 
+class MatKquant(ctypes.Structure):
+    """levo_hip_mat_kquant (include/levo_hip.h)."""
+
+    _fields_ = [("type", ctypes.c_int), ("weight", _P), ("y", _P), ("y_pitch", _I64), ("rows", _I64)]
+
+
 class FlowInputArgs(ctypes.Structure):
     """levo_hip_flow_input_args (include/levo_hip.h)."""
 
@@ -215,6 +221,7 @@ class LevoHip:
             "levo_hip_mul_mat_q8_0_multi": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_quantize_q8_K": (ctypes.c_int, [_P, _P, _I64, _P]),
             "levo_hip_mul_mat_kquant": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+            "levo_hip_mul_mat_kquant_multi": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_row_size": (_I64, [ctypes.c_int, _I64]),
             "levo_hip_quantize_chunk": (_I64, [ctypes.c_int, _P, _P, _I64, _I64, _I64, _P, _P]),
             "levo_hip_quantize_rows": (_I64, [ctypes.c_int, _P, ctypes.c_int, _I64, _I64, _P, _I64, _I64, _P]),
@@ -388,6 +395,15 @@ class LevoHip:
     def mul_mat_kquant(self, qtype, weight, x_blocks, y, y_pitch, rows, k, n_vec, stream=None):
         return self._check(self.lib.levo_hip_mul_mat_kquant(qtype, _addr(weight), _addr(x_blocks), _addr(y), y_pitch,
                                                             rows, k, n_vec, _stream(stream)))
+
+    def mul_mat_kquant_multi(self, mats, k, n_vec, x_blocks=None, x=None, x_pitch=0, stream=None):
+        """mats: (type, weight, y, y_pitch, rows) tuples sharing the activations,
+        given as Q8_K blocks (x_blocks) or as F32 rows (x, x_pitch)."""
+        arr = (MatKquant * max(len(mats), 1))()
+        for i, (t, w, y, y_pitch, rows) in enumerate(mats):
+            arr[i] = MatKquant(t, _addr(w), _addr(y), y_pitch, rows)
+        return self._check(self.lib.levo_hip_mul_mat_kquant_multi(arr, len(mats), _addr(x_blocks), _addr(x),
+                                                                  x_pitch, k, n_vec, _stream(stream)))
 
     def row_size(self, qtype, n):
         return self._check(self.lib.levo_hip_row_size(qtype, n))

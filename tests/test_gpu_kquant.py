@@ -171,7 +171,8 @@ def test_mul_mat_matches_oracle(hip, dev, oracle, qtype, rows, k, n_vec):
 
 @pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("rows,k,n_vec", [(1, 256, 1), (3, 256, 2), (7, 2304, 3), (65, 512, 2), (5, 8960, 8),
-                                          (2049, 768, 2), (4095, 256, 1)])  # 32 lanes per row, last workgroup short
+                                          (2049, 768, 2), (4095, 256, 1),  # 32 lanes per row, last workgroup short
+                                          (9, 9728, 2), (11, 9984, 3), (6, 16384, 4)])  # half-row instances
 def test_mul_mat_ragged(hip, dev, oracle, qtype, rows, k, n_vec):
     w = oracle.gaussian(rows * k, 7 * rows + k + qtype) * np.float32(0.02)
     wb = realistic_blocks(qtype, w.reshape(-1, 256))
@@ -219,3 +220,102 @@ def test_rejects_bad_arguments(hip, dev, binding):
     assert hip.row_size(Q4_K, 2304) == 9 * 144
     assert hip.row_size(Q6_K, 4608) == 18 * 210
     assert hip.row_size(15, 256) == 292
+
+
+# ---- shared-input launches (levo_hip_mul_mat_kquant_multi) ---------------------------
+
+def _weights(qtype, rows, k, seed, oracle):
+    w = oracle.gaussian(rows * k, seed) * np.float32(0.02)
+    return realistic_blocks(qtype, w.reshape(-1, 256))
+
+
+def _single(hip, dev, qtype, wb, xb, rows, k, n_vec):
+    import torch
+    y = torch.full((n_vec * rows,), float("nan"), dtype=torch.float32, device=dev)
+    hip.mul_mat_kquant(qtype, to_dev(wb, dev), xb, y, rows, rows, k, n_vec)
+    return from_dev(y).reshape(n_vec, rows)
+
+
+def _multi(hip, dev, specs, k, n_vec, x=None, xb=None, pitch=0):
+    """specs: (qtype, blocks, rows); returns each matrix's y [n_vec][rows]."""
+    import torch
+    keep, mats, ys = [], [], []
+    for qtype, wb, rows in specs:
+        wd = to_dev(wb, dev)
+        y = torch.full((n_vec * (rows + 5),), float("nan"), dtype=torch.float32, device=dev)
+        keep += [wd, y]
+        mats.append((qtype, wd, y, rows + 5, rows))
+        ys.append((y, rows))
+    xd = None
+    if x is not None:
+        xd = to_dev(np.ascontiguousarray(x, np.float32), dev)
+    hip.mul_mat_kquant_multi(mats, k, n_vec, x_blocks=xb, x=xd, x_pitch=pitch)
+    return [from_dev(y).reshape(n_vec, rows + 5)[:, :rows] for y, rows in ys]
+
+
+@pytest.mark.parametrize("types", [(Q4_K, Q4_K, Q6_K), (Q5_K, Q5_K, Q6_K), (Q6_K, Q6_K, Q6_K)],
+                         ids=["q4_k_m", "q5_k_m", "q6_k"])
+def test_multi_attention_group_equals_separate_calls(hip, dev, oracle, types):
+    """A decode layer's q / k / v under each profile (src/levo-quantization.h:
+    75-95: attn_v is promoted to Q6_K in the K_M profiles), 1536 x 1536, the
+    CFG pair of activation columns given as F32 and quantized in the launch:
+    every y equals quantize_q8_K + mul_mat_kquant for that matrix, bit for bit,
+    and the oracle within 1e-5."""
+    rows, k, n_vec = 1536, 1536, 2
+    x = oracle.gaussian(n_vec * k, 501).reshape(n_vec, k)
+    specs = [(t, _weights(t, rows, k, 510 + i, oracle), rows) for i, t in enumerate(types)]
+    got = _multi(hip, dev, specs, k, n_vec, x=x, pitch=k)
+    xb = q8_K_dev(hip, dev, x)
+    for (t, wb, _), g in zip(specs, got):
+        assert np.array_equal(g.view(np.uint32), _single(hip, dev, t, wb, xb, rows, k, n_vec).view(np.uint32))
+        assert f32_err(g, oracle.mul_mat_kquant(t, wb, x, rows, k)) <= 1e-5
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q5_K])
+def test_multi_gate_up_from_blocks(hip, dev, oracle, qtype):
+    """gate / up, 8960 x 1536, from Q8_K blocks: bit-identical to separate calls."""
+    rows, k, n_vec = 8960, 1536, 2
+    x = oracle.gaussian(n_vec * k, 520).reshape(n_vec, k)
+    xb = q8_K_dev(hip, dev, x)
+    specs = [(qtype, _weights(qtype, rows, k, 521 + i, oracle), rows) for i in range(2)]
+    got = _multi(hip, dev, specs, k, n_vec, xb=xb)
+    for (t, wb, _), g in zip(specs, got):
+        assert np.array_equal(g.view(np.uint32), _single(hip, dev, t, wb, xb, rows, k, n_vec).view(np.uint32))
+
+
+@pytest.mark.parametrize("k,n_vec,pitch", [(4096, 1, 4096), (2048, 2, 2052), (256, 8, 260), (2304, 1, 2304)])
+def test_multi_uneven_rows_and_fused_limits(hip, dev, oracle, k, n_vec, pitch):
+    """Matrices of different row counts and types (one empty, skipped), F32
+    activations at the in-launch quantization's limit (n_vec * k <= 4096) and
+    with a row pitch: each y within 1e-5 of the oracle."""
+    rng = np.random.default_rng(k + n_vec)
+    x = np.zeros((n_vec, pitch), np.float32)
+    x[:, :k] = rng.standard_normal((n_vec, k)).astype(np.float32)
+    x[0, :256] = 0.0  # an all-zero Q8_K block
+    specs = [(Q6_K, _weights(Q6_K, 1000, k, 530, oracle), 1000), (Q4_K, _weights(Q4_K, 37, k, 531, oracle), 37),
+             (Q5_K, np.zeros(0, np.uint8), 0), (Q4_K, _weights(Q4_K, 4100, k, 532, oracle), 4100)]
+    got = _multi(hip, dev, specs, k, n_vec, x=x, pitch=pitch)
+    for (t, wb, rows), g in zip(specs, got):
+        if rows:
+            assert f32_err(g, oracle.mul_mat_kquant(t, wb, x[:, :k], rows, k)) <= 1e-5
+
+
+def test_multi_rejects_bad_arguments(hip, dev, binding):
+    import torch
+    w = torch.zeros(144 * 8, dtype=torch.uint8, device=dev)
+    xb = torch.zeros(292 * 8, dtype=torch.uint8, device=dev)
+    xf = torch.zeros(8192, device=dev)
+    y = torch.zeros(64, device=dev)
+    m = [(Q4_K, w, y, 4, 4)]
+    with pytest.raises(binding.LevoHipError, match="exactly one"):
+        hip.mul_mat_kquant_multi(m, 256, 1, x_blocks=xb, x=xf, x_pitch=256)
+    with pytest.raises(binding.LevoHipError, match="exactly one"):
+        hip.mul_mat_kquant_multi(m, 256, 1)
+    with pytest.raises(binding.LevoHipError, match="1 to 4 matrices"):
+        hip.mul_mat_kquant_multi(m * 5, 256, 1, x_blocks=xb)
+    with pytest.raises(binding.LevoHipError, match="4096"):
+        hip.mul_mat_kquant_multi(m, 4096, 2, x=xf, x_pitch=4096)
+    with pytest.raises(binding.LevoHipError, match="x_pitch"):
+        hip.mul_mat_kquant_multi(m, 256, 1, x=xf, x_pitch=250)
+    with pytest.raises(binding.LevoHipError, match="Q4_K, Q5_K or Q6_K"):
+        hip.mul_mat_kquant_multi([(8, w, y, 4, 4)], 256, 1, x_blocks=xb)
