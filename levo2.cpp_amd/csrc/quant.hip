@@ -8,9 +8,10 @@
 // with d stored as IEEE F16 (RNE). Blocks are 34 / 18 bytes and therefore not
 // naturally aligned.
 //
-// Quantize: one lane per block; the wave's 64 consecutive blocks (a
-// 16-byte-aligned byte range) are assembled in LDS and written with
-// streaming (nontemporal) dwordx4 stores. Dequantize: a wave stages 32 blocks in LDS and writes their values
+// Quantize: packed rows take two lanes per block, other layouts one lane per
+// block; a wave's consecutive blocks (32 or 64: a 16-byte-aligned byte range)
+// are assembled in LDS and written with streaming (nontemporal) dwordx4
+// stores. Dequantize: a wave stages 32 blocks in LDS and writes their values
 // as contiguous 16-byte chunks.
 #include "common.hpp"
 #include "quant_block.hpp"
@@ -111,52 +112,65 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 // Packed rows (source value i of block b is src[32 b + i]), 16-byte aligned
-// source. The wave's 64 blocks are read with coalesced dwordx4 loads (lane l
-// takes 16-byte chunks l, l + 64, ...), transposed through LDS (each block in
-// its own 16-byte-padded slot, so the per-lane reads of one block spread over
-// distinct bank groups), and each lane then quantizes one block.
+// source, two lanes per block: lane 2 b + h of a wave quantizes half of
+// block b of the wave's 32 (Q8_0: values 16 h .. 16 h + 15; Q4_0: values
+// 8 h .. 8 h + 7 and 16 + 8 h .. 16 + 8 h + 7, the two of each packed byte),
+// so each lane's chain from its loads to its stores is half as long as with a
+// lane per block. The wave's 32 blocks are read with coalesced dwordx4 loads
+// and transposed through LDS (each block in a 16-byte-padded slot). The
+// halves meet with DPP swaps: their partial maxima (with the reference's
+// index-order rule, below) and, at the end, the second half's quants, which
+// the first lane stages with the block's scale.
 template <int QT, typename S>
-__global__ __launch_bounds__(kThreads) void quantize_dense_kernel(const S * __restrict__ src,
-                                                                  uint8_t * __restrict__ dst, int64_t nblocks,
-                                                                  bool dst_vec) {
+__global__ __launch_bounds__(kThreads) void quantize_pair_kernel(const S * __restrict__ src,
+                                                                 uint8_t * __restrict__ dst, int64_t nblocks,
+                                                                 bool dst_vec) {
     constexpr int QB = qtraits<QT>::bytes;
     constexpr int CPB = 32 * static_cast<int>(sizeof(S)) / 16;  // 16-byte chunks per block: 4 (F16) or 8 (F32)
+    constexpr int CPL = CPB / 2;                                // chunks per lane
+    constexpr int VPC = 16 / static_cast<int>(sizeof(S));       // values per chunk
     constexpr int SLOT = (CPB + 1) * 16;                        // padded block slot in LDS
-    constexpr int STAGE = 64 * SLOT;                            // >= 64 * QB output bytes
+    constexpr int STAGE = 32 * SLOT;                            // >= 32 * QB output bytes
     __shared__ __attribute__((aligned(16))) uint8_t stage[kWaves][STAGE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * 64;
+    const int b = lane >> 1;
+    const int h = lane & 1;
+    const int64_t b0 = (static_cast<int64_t>(blockIdx.x) * kWaves + wave) * 32;
     uint8_t * lds = stage[wave];
     const u32x4 * in = reinterpret_cast<const u32x4 *>(src);
     const int64_t last = nblocks * CPB - 1;  // last valid chunk of the source
 
     // Every load is issued before any is used: chunks past the end read the
     // last valid chunk (no branch around a load) and are zeroed afterwards.
-    u32x4 v[CPB];
+    u32x4 v[CPL];
 #pragma unroll
-    for (int j = 0; j < CPB; ++j) {
+    for (int j = 0; j < CPL; ++j) {
         const int64_t g = b0 * CPB + lane + 64 * j;
         v[j] = __builtin_nontemporal_load(in + (g < last ? g : last));
     }
 #pragma unroll
-    for (int j = 0; j < CPB; ++j) {
+    for (int j = 0; j < CPL; ++j) {
         if (b0 * CPB + lane + 64 * j > last) v[j] = u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int j = 0; j < CPB; ++j) {
+    for (int j = 0; j < CPL; ++j) {
         const int c = lane + 64 * j;
         *reinterpret_cast<u32x4 *>(lds + (c / CPB) * SLOT + (c % CPB) * 16) = v[j];
     }
     wave_lds_fence();
-    float x[32];
+    // this lane's 16 values, x[i] = block value at(i)
+    float x[16];
 #pragma unroll
-    for (int j = 0; j < CPB; ++j) {
-        const u32x4 w = *reinterpret_cast<const u32x4 *>(lds + lane * SLOT + j * 16);
+    for (int j = 0; j < CPL; ++j) {
+        // Q8_0: chunks CPL h + j; Q4_0: the chunks of values 8 h .. and 16 + 8 h ..
+        const int chunk = QT == LEVO_HIP_TYPE_Q8_0 ? CPL * h + j
+                                                   : (j < CPL / 2 ? (8 * h) / VPC + j : (16 + 8 * h) / VPC + j - CPL / 2);
+        const u32x4 w = *reinterpret_cast<const u32x4 *>(lds + b * SLOT + chunk * 16);
         if constexpr (std::is_same<S, uint16_t>::value) {
-            const u16x8 h = __builtin_bit_cast(u16x8, w);
+            const u16x8 hv = __builtin_bit_cast(u16x8, w);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) x[j * 8 + k] = h2f(h[k]);
+            for (int k = 0; k < 8; ++k) x[j * 8 + k] = h2f(hv[k]);
         } else {
             // Cast the whole vector: ROCm 7.2's clang lowers a bit_cast of a
             // single ext_vector element (w.y, ...) as a cast of element 0.
@@ -170,16 +184,119 @@ __global__ __launch_bounds__(kThreads) void quantize_dense_kernel(const S * __re
     // The output reuses the stage: the fence keeps every read above ahead of
     // the writes below, and the wave's LDS operations execute in that order.
     wave_lds_fence();
-    quantize_block<QT>(x, lds, lane);
+
+    uint16_t d16;
+    uint32_t pk[8];  // Q8_0: 4 dwords of this half's quants (8 once the halves meet); Q4_0: 2 (4)
+    if constexpr (QT == LEVO_HIP_TYPE_Q8_0) {
+        // amax = MAX(amax, |x|) in index order. Without a NaN that is the
+        // largest |x|: the |x| bit patterns order like the values. A NaN makes
+        // the running MAX restart at the next value, so a half holding one
+        // ends the same whatever came before it: the block's amax is the
+        // second half's own scan from 0 if it holds a NaN, else the first
+        // half's scan continued over the second (restarting if the first
+        // half's scan ended on its NaN).
+        uint32_t bm = 0u;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) bm = __builtin_elementwise_max(bm, __float_as_uint(x[k]) & 0x7fffffffu);
+        const uint32_t bm_o = dpp::mov<dpp::kQuadXor1>(bm);
+        const uint32_t bits_max = bm > bm_o ? bm : bm_o;
+        const bool has_nan = bits_max > 0x7f800000u;  // the pair's (both lanes agree)
+        float amax = __uint_as_float(bits_max);
+        if (has_nan) {
+            float fold = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const float a = fabsf(x[k]);
+                fold = fold > a ? fold : a;
+            }
+            const float fold_o = dpp::mov<dpp::kQuadXor1>(fold);
+            const float first = h ? fold_o : fold;          // the first half's scan from 0
+            const uint32_t bm1 = h ? bm : bm_o;             // the second half's |x| maximum
+            const float second = h ? fold : fold_o;         // the second half's scan from 0
+            amax = bm1 > 0x7f800000u ? second
+                                     : (first != first ? __uint_as_float(bm1) : fmaxf(first, __uint_as_float(bm1)));
+        }
+        const float d = amax / 127.0f;
+        const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
+        if (!has_nan) {
+            // |x * id| <= 128 (or NaN): the truncated int32's low byte is the
+            // reference's (int8_t)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = trunc_i32(half_away_offset(x[4 * w + k] * id));
+                pk[w] = pack_low_bytes(q[0], q[1], q[2], q[3]);
+            }
+        } else {
+            // earlier values may exceed amax and leave the int32 range:
+            // there cvttss2si gives 0x80000000 (low byte 0)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t q[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float vq = half_away_offset(x[4 * w + k] * id);
+                    q[k] = __builtin_fabsf(vq) < 0x1p31f ? trunc_i32(vq) : 0u;
+                }
+                pk[w] = pack_low_bytes(q[0], q[1], q[2], q[3]);
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pk[4 + w] = dpp::mov<dpp::kQuadXor1>(pk[w]);
+        d16 = f2h(d);
+    } else {
+        // ggml's scan (the first value of largest |x|, NaN never taken) in
+        // the four quarters of 8 values, joined in order with strict
+        // comparisons (the earliest quarter wins a tie, as the single scan
+        // keeps the earliest value): this lane scans quarters h and 2 + h.
+        float qa = 0.0f, qb = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) qa = fabsf(qa) < fabsf(x[k]) ? x[k] : qa;
+#pragma unroll
+        for (int k = 8; k < 16; ++k) qb = fabsf(qb) < fabsf(x[k]) ? x[k] : qb;
+        const float oa = dpp::mov<dpp::kQuadXor1>(qa);
+        const float ob = dpp::mov<dpp::kQuadXor1>(qb);
+        const float q0 = h ? oa : qa, q1 = h ? qa : oa, q2 = h ? ob : qb, q3 = h ? qb : ob;
+        float vmax = q0;
+        vmax = fabsf(vmax) < fabsf(q1) ? q1 : vmax;
+        vmax = fabsf(vmax) < fabsf(q2) ? q2 : vmax;
+        vmax = fabsf(vmax) < fabsf(q3) ? q3 : vmax;
+        const float d = vmax / -8.0f;
+        const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            uint32_t bq[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = 4 * w + k;  // byte 8 h + i: values 8 h + i and 16 + 8 h + i
+                const uint32_t c0 = low_byte_i8(x[i] * id + 8.5f);
+                const uint32_t c1 = low_byte_i8(x[8 + i] * id + 8.5f);
+                bq[k] = (c0 < 15u ? c0 : 15u) | ((c1 < 15u ? c1 : 15u) << 4);
+            }
+            pk[w] = pack4(bq[0], bq[1], bq[2], bq[3]);
+        }
+#pragma unroll
+        for (int w = 0; w < 2; ++w) pk[2 + w] = dpp::mov<dpp::kQuadXor1>(pk[w]);
+        d16 = f2h(d);
+    }
+    if (h == 0) {
+        if constexpr (QT == LEVO_HIP_TYPE_Q8_0) {
+            stage_block<8>(lds, b, d16, pk);
+        } else {
+            const uint32_t q4[4] = {pk[0], pk[1], pk[2], pk[3]};
+            stage_block<4>(lds, b, d16, q4);
+        }
+    }
     wave_lds_fence();
 
     uint8_t * out = dst + b0 * QB;
     const int64_t nvalid = nblocks - b0;
-    if (nvalid >= 64 && dst_vec) {
-        for (int i = lane; i < 64 * QB / 16; i += 64)
+    if (nvalid >= 32 && dst_vec) {
+        for (int i = lane; i < 32 * QB / 16; i += 64)
             __builtin_nontemporal_store(reinterpret_cast<const u32x4 *>(lds)[i], reinterpret_cast<u32x4 *>(out) + i);
     } else if (nvalid > 0) {
-        const int nbytes = static_cast<int>(nvalid < 64 ? nvalid : 64) * QB;
+        const int nbytes = static_cast<int>(nvalid < 32 ? nvalid : 32) * QB;
         for (int i = lane; i < nbytes / 2; i += 64)
             reinterpret_cast<uint16_t *>(out)[i] = reinterpret_cast<const uint16_t *>(lds)[i];
     }
@@ -333,7 +450,7 @@ int launch_quant(const void * src, int64_t src_cols, int64_t src_stride, void * 
     uint8_t * d = static_cast<uint8_t *>(dst);
     const bool dst_vec = aligned16(dst);
     if (vec && dense)
-        quantize_dense_kernel<QT, S><<<grid, kThreads, 0, stream>>>(s, d, nblocks, dst_vec);
+        quantize_pair_kernel<QT, S><<<ceil_div(nblocks, 32 * kWaves), kThreads, 0, stream>>>(s, d, nblocks, dst_vec);
     else if (vec)
         quantize_kernel<QT, S, true><<<grid, kThreads, 0, stream>>>(s, src_cols, src_stride, d, nb_row, nblocks, dense, dst_vec);
     else
@@ -386,6 +503,7 @@ extern "C" int64_t levo_hip_quantize_rows(levo_hip_type type, const void * src, 
     LEVO_REQUIRE(src_row_stride >= src_cols, "quantize: source row stride is smaller than the width");
     const int64_t bytes = nrows * (dst_cols / 32) * block_bytes(type);
     if (bytes == 0) return 0;
+    LEVO_REQUIRE(nrows * (dst_cols / 32) < (int64_t{1} << 31), "quantize: more than 2^31 - 1 blocks in one call");
     LEVO_REQUIRE(src != nullptr && dst != nullptr, "quantize: null pointer");
     LEVO_REQUIRE((reinterpret_cast<uintptr_t>(dst) & 1u) == 0, "quantize: destination must be 2-byte aligned");
     LEVO_REQUIRE((reinterpret_cast<uintptr_t>(src) & (src_type == LEVO_HIP_TYPE_F16 ? 1u : 3u)) == 0,
