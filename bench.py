@@ -859,15 +859,20 @@ def bench_snake_conv(torch, hip, head, dev, warmup, steps):
     residual units at a 10.08 s window's real stage lengths: stage 5
     (128 channels x 483840 samples; k = 7 at dilation 1 / 3 / 9, k = 1 with
     the residual add), stage 3 (256 x 60480) and stage 1 (1024 x 2520).
-    Matrix-core bound: `TFLOP/s` is 2 * C_out * C_in * k * T_out per launch
-    over the launch time, against the F32 MFMA peak; bytes are x, y (and the
-    residual) once."""
+    Every case runs levo_hip_snake_conv1d_split with a workspace, as the
+    decoder does: stage 1's 160 output tiles (fewer than the 256 CUs) split
+    their input channels three ways plus the combine launch (both timed);
+    the larger grids run unsplit. Stage 1 is also timed without the
+    workspace (`stage1_k7_d9_unsplit`). Matrix-core bound: `TFLOP/s` is
+    2 * C_out * C_in * k * T_out per call over the call's time, against the
+    F32 MFMA peak; bytes are x, y (and the residual) once."""
     out = {}
     g = torch.Generator(device=dev)
     g.manual_seed(7)
     cases = [("stage5_k7_d1", 128, 483840, 7, 1), ("stage5_k7_d9", 128, 483840, 7, 9),
              ("stage5_k1_residual", 128, 483840, 1, 1), ("stage3_k7_d3", 256, 60480, 7, 3),
-             ("stage1_k7_d9", 1024, 2520, 7, 9)]
+             ("stage1_k7_d9", 1024, 2520, 7, 9), ("stage1_k7_d9_unsplit", 1024, 2520, 7, 9),
+             ("stage1_k1_residual", 1024, 2520, 1, 1)]
     for name, c, t, kw, dil in cases:
         pad = 3 * dil if kw == 7 else 0
         x = torch.randn((c, t), generator=g, device=dev)
@@ -877,8 +882,15 @@ def bench_snake_conv(torch, hip, head, dev, warmup, steps):
         bl = torch.randn(c, generator=g, device=dev) * 0.5
         r = torch.randn((c, t), generator=g, device=dev) if kw == 1 else None
         y = torch.empty((c, t), device=dev)
-        fn = lambda i: hip.snake_conv1d(x, c, t, w, c, kw, alpha_log=a, beta_log=bl, bias=b, padding=pad,
-                                        dilation=dil, residual=r, y=y)
+        if name.endswith("_unsplit"):
+            fn = lambda i: hip.snake_conv1d(x, c, t, w, c, kw, alpha_log=a, beta_log=bl, bias=b, padding=pad,
+                                            dilation=dil, residual=r, y=y)
+        else:
+            nws = hip.snake_conv1d_split_workspace_floats(c, t)
+            ws = torch.empty(nws, device=dev)
+            fn = lambda i: hip.snake_conv1d_split(x, c, t, w, c, kw, workspace=ws, workspace_floats=nws,
+                                                  alpha_log=a, beta_log=bl, bias=b, padding=pad, dilation=dil,
+                                                  residual=r, y=y)
         ms = time_op(torch, head, fn, 1, warmup, max(steps // 4, 5))
         flops = 2.0 * c * c * kw * t
         tflops = flops / (ms * 1e-3) / 1e12

@@ -113,6 +113,29 @@ int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t c_in, int64
                           int64_t padding, int64_t dilation, const float * residual, int64_t residual_stride,
                           float * y, int64_t y_stride, levo_hip_stream_t stream);
 
+/* Floats of workspace levo_hip_snake_conv1d_split uses at most for an output
+ * of c_out x t_out: four partial sums of the output, rows padded to a
+ * multiple of 4 floats; < 0 if invalid. */
+int64_t levo_hip_snake_conv1d_split_workspace_floats(int64_t c_out, int64_t t_out);
+
+/* levo_hip_snake_conv1d (the same arguments, results and errors) with a
+ * device workspace of workspace_floats floats (16-byte aligned, overlapping
+ * none of the tensors). When the output has fewer 128 x 128 tiles than the
+ * GPU has compute units, the input channels are split over up to four
+ * workgroups per tile (as many partial sums as the workspace holds), each
+ * writing its partial sum to the workspace, and a second launch adds the
+ * partials in split order, then the bias and the residual. The result is
+ * deterministic; it differs from levo_hip_snake_conv1d's by the F32 rounding
+ * of the other summation order. A grid that already fills the GPU, c_out <= 4
+ * or too small a workspace run levo_hip_snake_conv1d's path unchanged. Same
+ * reference call sites as levo_hip_snake_conv1d. */
+int levo_hip_snake_conv1d_split(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                                const float * weight, int64_t c_out, int64_t kernel, const float * bias,
+                                int64_t padding, int64_t dilation, const float * residual, int64_t residual_stride,
+                                float * y, int64_t y_stride, float * workspace, int64_t workspace_floats,
+                                levo_hip_stream_t stream);
+
 /* Weights of a ConvTranspose1d with kernel 2 * stride (the decoder's
  * upsamplers) rearranged for levo_hip_snake_conv_transpose1d: weight is
  * ggml's [c_in][c_out][2 * stride] (ne = [kernel, c_out, c_in]); packed

@@ -34,6 +34,10 @@ int allow_dynamic_lds(const void * kernel, int bytes, const char * what);
 
 inline hipStream_t as_hip(levo_hip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Compute units of the current device (queried once per device; 0 if the
+// query fails).
+int device_cu_count();
+
 // K-quant helpers shared by the quantizer entry points (kquant.hip).
 bool is_kquant(levo_hip_type type);
 int64_t kquant_block_bytes(levo_hip_type type);  // Q4_K / Q5_K / Q6_K / Q8_K per 256 values; 0 otherwise

@@ -82,7 +82,43 @@ struct conv_params {
     // tile back to back
     int32_t xcd_order;
     int32_t tiles_x, tiles, phases;
+    // Split K: with splits > 1 the grid's phase axis is the split index z.
+    // Split z sums the input channels of chunks [z n / splits, (z + 1) n /
+    // splits) of the n chunks and writes that partial sum, without bias or
+    // residual, to part + z * part_slice (rows part_pitch floats apart,
+    // 16-byte aligned); split_combine_kernel then adds the partials in split
+    // order and applies the epilogue.
+    int32_t splits;
+    float * part;
+    int64_t part_slice;
+    int64_t part_pitch;
 };
+
+// Input channels [begin, end) of split z (all of them without a split).
+template <int CI>
+__device__ __forceinline__ void split_range(const conv_params & p, int z, int & begin, int & end) {
+    if (p.splits <= 1) {
+        begin = 0;
+        end = p.c_in;
+        return;
+    }
+    const int n = (p.c_in + CI - 1) / CI;
+    begin = CI * (z * n / p.splits);
+    end = min(p.c_in, CI * ((z + 1) * n / p.splits));
+}
+
+// Where split z's partial sum goes: the epilogue's plain path into the
+// partial slice, with no bias and no residual.
+__device__ __forceinline__ conv_params split_target(const conv_params & p, int z) {
+    conv_params e = p;
+    e.y = p.part + static_cast<int64_t>(z) * p.part_slice;
+    e.y_pitch = p.part_pitch;
+    e.bias = nullptr;
+    e.residual = nullptr;
+    e.y_vec = 1;
+    e.scatter = 0;
+    return e;
+}
 
 // The time tile x, channel tile y and phase z of this workgroup. With
 // xcd_order the grid is 1-D: the hardware deals workgroups to the 8 XCDs
@@ -392,20 +428,25 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     const int64_t t0 = static_cast<int64_t>(tl.x) * kNT;
     const int co0 = tl.y * kMT;
 
+    // input channels of this workgroup (a split's share, or all); the
+    // parameter table is indexed from ci_begin
+    int ci_begin, ci_end;
+    split_range<CI>(p, tl.z, ci_begin, ci_end);
+
     f32x4v ra[conv_slots<KW>::NA];
     float rb[conv_slots<KW>::NB];
-    load_chunk<KW>(p, 0, co0, t0, tid, ra, rb);
+    load_chunk<KW>(p, ci_begin, co0, t0, tid, ra, rb);
 
     if (p.snake) {
-        const int n = RING ? 2 * CI : p.c_in;  // ring: chunks 0 and 1
+        const int n = RING ? 2 * CI : ci_end - ci_begin;  // ring: the first two chunks
         for (int c = tid; c < n; c += kThreads) {
             float al, bl;
-            load_snake_logs(p, c, al, bl);
+            load_snake_logs(p, ci_begin + c, al, bl);
             sp[c] = make_snake_param(al, bl);
         }
         __syncthreads();
     }
-    store_chunk<KW>(p, 0, tid, lds, lds + a_floats<KW>(), sp, ra, rb);
+    store_chunk<KW>(p, ci_begin, tid, lds, lds + a_floats<KW>(), sp, ra, rb);
     __syncthreads();
 
     f32x4v acc[4][4];
@@ -415,11 +456,11 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     int buf = 0;
-    for (int ci0 = 0; ci0 < p.c_in; ci0 += CI) {
-        const bool more = ci0 + CI < p.c_in;
+    for (int ci0 = ci_begin; ci0 < ci_end; ci0 += CI) {
+        const bool more = ci0 + CI < ci_end;
         if (more) load_chunk<KW>(p, ci0 + CI, co0, t0, tid, ra, rb);  // in flight during the MFMAs
         // parameters of the chunk after next, computed in this chunk's store phase
-        const bool params = RING && p.snake && ci0 + 2 * CI < p.c_in && tid < CI;
+        const bool params = RING && p.snake && ci0 + 2 * CI < ci_end && tid < CI;
         float al = 0.0f, bl = 0.0f;
         if (params) load_snake_logs(p, ci0 + 2 * CI + tid, al, bl);
         const float * As = lds + buf * buf_floats;
@@ -445,8 +486,8 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         if (more) {
             // the other buffer was last read before the previous barrier
             float * An = lds + (buf ^ 1) * buf_floats;
-            store_chunk<KW>(p, ci0 + CI, tid, An, An + a_floats<KW>(), sp + (RING ? (buf ^ 1) * CI : ci0 + CI),
-                            ra, rb);
+            store_chunk<KW>(p, ci0 + CI, tid, An, An + a_floats<KW>(),
+                            sp + (RING ? (buf ^ 1) * CI : ci0 + CI - ci_begin), ra, rb);
         }
         // slot buf held this chunk's parameters, last read before the previous barrier
         if (RING && params) sp[buf * CI + tid] = make_snake_param(al, bl);
@@ -454,7 +495,7 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         buf ^= 1;
     }
 
-    conv_epilogue<true>(p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
+    conv_epilogue<true>(p.splits > 1 ? split_target(p, tl.z) : p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
 }
 
 // ---- narrow output (c_out <= 4): the decoder's 128 -> 2 output conv -------
@@ -744,6 +785,10 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     const int co0 = tl.y * kMT;
     const int bw = p.b_width;
     const int n_b = CI * bw;
+    // input channels of this workgroup (a split's share, or all); the
+    // parameter table is indexed from ci_begin
+    int ci_begin, ci_end;
+    split_range<CI>(p, tl.z, ci_begin, ci_end);
     // k = 7 divides (faster there, measured); k = 2 multiplies by b_magic
     auto row_of = [&](int e) { return KW == 7 ? e / bw : b_row(e, p.b_magic); };
     const int64_t tb = t0 - p.pad;
@@ -775,12 +820,12 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
             rb[sl] = v;
         }
     };
-    load_a(0);
-    load_b(0);
+    load_a(ci_begin);
+    load_b(ci_begin);
     if (p.snake) {
-        for (int c = tid; c < p.c_in; c += kThreads) {
+        for (int c = tid; c < ci_end - ci_begin; c += kThreads) {
             float al, bl;
-            load_snake_logs(p, c, al, bl);
+            load_snake_logs(p, ci_begin + c, al, bl);
             sp[c] = make_snake_param(al, bl);
         }
     }
@@ -792,7 +837,7 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
         const int e = tid + kThreads * sl;
         const int c = row_of(e);
         float v = rb[sl];
-        if (p.snake && e < n_b && c < p.c_in) v = snake(v, sp[c]);
+        if (p.snake && e < n_b && ci_begin + c < p.c_in) v = snake(v, sp[c]);
         lds[a_floats<KW>() + e] = v;
     }
     __syncthreads();
@@ -804,9 +849,9 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
 
     int buf = 0;
-    const int cmax = p.c_in - 1;
-    for (int ci0 = 0; ci0 < p.c_in; ci0 += CI) {
-        const bool more = ci0 + CI < p.c_in;
+    const int cmax = ci_end - 1;
+    for (int ci0 = ci_begin; ci0 < ci_end; ci0 += CI) {
+        const bool more = ci0 + CI < ci_end;
         // the next chunk's loads (past the last chunk they are guarded to zeros)
         load_a(ci0 + CI);
         load_b(ci0 + CI);
@@ -854,7 +899,7 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
                     const float v = rb[sl];
                     // without SnakeBeta the value is computed from table
                     // entry 0 (allocated, not filled) and discarded
-                    const snake_param q = sp[p.snake ? min(ci0 + CI + row_of(e), cmax) : 0];
+                    const snake_param q = sp[p.snake ? min(ci0 + CI + row_of(e), cmax) - ci_begin : 0];
                     const float sv = snake_reduced(v, q, slow);
                     Bn[e] = p.snake ? sv : v;
                 }
@@ -882,7 +927,7 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
             for (int sl = 0; sl < NB; ++sl) {
                 const int e = tid + kThreads * sl;
                 const int c = row_of(e);
-                if (e < n_b && ci0 + CI + c < p.c_in) Bn[e] = snake(rb[sl], sp[ci0 + CI + c]);
+                if (e < n_b && ci0 + CI + c < p.c_in) Bn[e] = snake(rb[sl], sp[ci0 + CI + c - ci_begin]);
             }
         }
         __syncthreads();
@@ -891,7 +936,36 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     if constexpr (FUSE) {
         residual_tail(p, f, lds, acc, tid, h, vh, g, m, t0);
     } else {
-        conv_epilogue<KW == 2>(p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
+        conv_epilogue<KW == 2>(p.splits > 1 ? split_target(p, tl.z) : p, lds, acc, tid, h, vh, g, m, t0, co0,
+                               tl.z);
+    }
+}
+
+// y = ((part_0 + part_1) + ...) + bias (+ residual) per float4 of a row: the
+// split launch's partial sums in split order, then the unsplit epilogue's
+// bias and residual adds. Rows of the partials are padded to a multiple of 4
+// floats; the padding is summed and dropped.
+__global__ __launch_bounds__(kThreads) void split_combine_kernel(const conv_params p) {
+    const int64_t groups = (p.t_out + 3) / 4;  // float4 groups per row
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e >= groups * p.c_out) return;
+    const int co = static_cast<int>(e / groups);
+    const int64_t t = 4 * (e - co * groups);
+    const float * src = p.part + co * p.part_pitch + t;
+    f32x4v v = *reinterpret_cast<const f32x4v *>(src);
+    for (int z = 1; z < p.splits; ++z) v = v + *reinterpret_cast<const f32x4v *>(src + z * p.part_slice);
+    if (p.bias) v = v + p.bias[co];
+    if (p.y_vec && t + 4 <= p.t_out) {
+        if (p.residual) v = *reinterpret_cast<const f32x4v *>(p.residual + co * p.r_pitch + t) + v;
+        *reinterpret_cast<f32x4v *>(p.y + co * p.y_pitch + t) = v;
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (t + q >= p.t_out) break;
+        float o = v[q];
+        if (p.residual) o = p.residual[co * p.r_pitch + t + q] + o;
+        p.y[co * p.y_pitch + t + q] = o;
     }
 }
 
@@ -924,10 +998,20 @@ int launch_il(conv_params p, int phases, size_t table, hipStream_t st, const cha
     return launch_status(what);
 }
 
+int launch_split_combine(const conv_params & p, hipStream_t st, const char * what) {
+    const int64_t groups = ceil_div(p.t_out, 4) * p.c_out;
+    split_combine_kernel<<<dim3(static_cast<uint32_t>(ceil_div(groups, kThreads))), kThreads, 0, st>>>(p);
+    return launch_status(what);
+}
+
+// One convolution launch (with p.splits > 1: the split launch, then the
+// combine). phases > 1 (transposed convolutions) never comes with splits.
 template <int KW>
 int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
     if (!p.scatter && p.c_out <= 4 && (KW - 1) * p.dil <= kNarrowMaxSpan) return launch_narrow<KW>(p, st, what);
     constexpr int CI = conv_chunk<KW>::CI;
+    const int splits = p.splits > 1 ? p.splits : 1;
+    const int gphases = phases * splits;  // the grid's phase axis: phases or splits
     p.b_width = (kNT + (KW - 1) * p.dil + 3) & ~3;
     // each thread stages at most two samples of an input row (one for KW = 2)
     LEVO_REQUIRE(KW == 1 || p.b_width <= (KW == 2 ? 1 : 2) * kThreads, "snake_conv1d: dilation too large");
@@ -936,15 +1020,17 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
               (p.residual == nullptr || (aligned16(p.residual) && p.r_pitch % 4 == 0));
     const size_t buf = static_cast<size_t>(a_floats<KW>() + CI * p.b_width);
     const size_t tiles = std::max(2 * buf, static_cast<size_t>(kMT) * kOutStride) * sizeof(float);
-    const int64_t wgs = ceil_div(p.t_out, kNT) * ceil_div(p.c_out, kMT) * phases;
+    const int64_t wgs = ceil_div(p.t_out, kNT) * ceil_div(p.c_out, kMT) * gphases;
+    // parameter table: the channels of one workgroup (a split's largest share)
+    const int64_t table_channels = splits > 1 ? CI * ceil_div(ceil_div(p.c_in, CI), splits) : p.c_in;
+    const size_t table = static_cast<size_t>(table_channels) * sizeof(snake_param);
     // the full parameter table unless it alone keeps a second workgroup off
     // a CU (160 KB of LDS) in a grid that has more than one per CU
-    const size_t table = static_cast<size_t>(p.c_in) * sizeof(snake_param);
-    p.param_ring = p.snake && 2 * (tiles + table) > 160 * 1024 && 2 * (tiles + 2 * CI * sizeof(snake_param)) <= 160 * 1024 &&
-                   wgs > 256;
+    p.param_ring = splits == 1 && p.snake && 2 * (tiles + table) > 160 * 1024 &&
+                   2 * (tiles + 2 * CI * sizeof(snake_param)) <= 160 * 1024 && wgs > 256;
     const size_t lds = tiles + (p.snake ? (p.param_ring ? 2 * CI * sizeof(snake_param) : table) : 0);
     LEVO_REQUIRE(lds <= 152 * 1024, "snake_conv1d: dilation or channel count too large for LDS");
-    const dim3 grid = conv_grid(p, phases);
+    const auto finish = [&](int rc) { return rc == LEVO_HIP_OK && splits > 1 ? launch_split_combine(p, st, what) : rc; };
     if constexpr (KW == 2 || KW == 7) {
         // With the full parameter table even where the other kernel would
         // take the ring: one workgroup per CU of this kernel outruns two of
@@ -956,20 +1042,21 @@ int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
         const int64_t nb = ceil_div(static_cast<int64_t>(CI) * p.b_width, kThreads);
         if (p.w_vec && p.b_width >= kNT && nb <= il_shape<KW>::kMaxNB && (KW == 7 || p.c_in >= 512)) {
             int rc = -1;
-            if (KW == 7 && nb <= 5) rc = launch_il<KW, KW == 7 ? 5 : il_shape<KW>::kMaxNB>(p, phases, table, st, what);
-            if (rc < 0) rc = launch_il<KW, il_shape<KW>::kMaxNB>(p, phases, table, st, what);
-            if (rc >= 0) return rc;
+            if (KW == 7 && nb <= 5) rc = launch_il<KW, KW == 7 ? 5 : il_shape<KW>::kMaxNB>(p, gphases, table, st, what);
+            if (rc < 0) rc = launch_il<KW, il_shape<KW>::kMaxNB>(p, gphases, table, st, what);
+            if (rc >= 0) return finish(rc);
         }
     }
+    const dim3 grid = conv_grid(p, gphases);
     const void * kernel = p.param_ring ? reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, true>)
                                        : reinterpret_cast<const void *>(&snake_conv1d_kernel<KW, false>);
-    if (const int st = allow_dynamic_lds(kernel, 152 * 1024, what); st != LEVO_HIP_OK) return st;
+    if (const int rc = allow_dynamic_lds(kernel, 152 * 1024, what); rc != LEVO_HIP_OK) return rc;
     if (p.param_ring) {
         snake_conv1d_kernel<KW, true><<<grid, kThreads, lds, st>>>(p);
     } else {
         snake_conv1d_kernel<KW, false><<<grid, kThreads, lds, st>>>(p);
     }
-    return launch_status(what);
+    return finish(launch_status(what));
 }
 
 }  // namespace
@@ -1034,12 +1121,27 @@ int launch_residual_unit_fused(const float * x, int64_t c, int64_t t, const void
 
 using namespace levo_hip;
 
-extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
-                                     const void * alpha_log, const void * beta_log, levo_hip_type param_type,
-                                     const float * weight, int64_t c_out, int64_t kernel, const float * bias,
-                                     int64_t padding, int64_t dilation, const float * residual,
-                                     int64_t residual_stride, float * y, int64_t y_stride,
-                                     levo_hip_stream_t stream) {
+namespace levo_hip {
+namespace {
+
+constexpr int kMaxSplits = 4;
+
+int64_t split_pitch(int64_t t_out) { return (t_out + 3) / 4 * 4; }
+
+bool ranges_overlap(const void * a, int64_t a_bytes, const void * b, int64_t b_bytes) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return pa < pb + static_cast<uintptr_t>(b_bytes) && pb < pa + static_cast<uintptr_t>(a_bytes);
+}
+
+// levo_hip_snake_conv1d, and with a workspace the split-K form when the grid
+// would leave compute units idle: up to two workgroups per CU (at most
+// kMaxSplits splits), each split at least two K chunks, as many partial
+// slices as the workspace holds.
+int conv1d_entry(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in, const void * alpha_log,
+                 const void * beta_log, levo_hip_type param_type, const float * weight, int64_t c_out,
+                 int64_t kernel, const float * bias, int64_t padding, int64_t dilation, const float * residual,
+                 int64_t residual_stride, float * y, int64_t y_stride, float * ws, int64_t ws_floats,
+                 hipStream_t st, const char * what) {
     LEVO_REQUIRE(c_in > 0 && c_out > 0 && t_in > 0, "LeVo audio graph: incompatible Conv1d weight/input shapes");
     LEVO_REQUIRE(padding >= 0 && dilation > 0, "LeVo audio graph: invalid Conv1d stride, padding, or dilation");
     LEVO_REQUIRE(kernel == 1 || kernel == 3 || kernel == 5 || kernel == 7, "snake_conv1d: kernel size must be 1, 3, 5 or 7");
@@ -1087,14 +1189,65 @@ extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t 
     p.w_phase = 0;
     p.scatter = 0;
     p.param_ring = 0;
-    const hipStream_t st = as_hip(stream);
-    const char * what = "levo_hip_snake_conv1d";
+    p.splits = 1;
+    if (ws != nullptr && c_out > 4) {
+        LEVO_REQUIRE(aligned16(ws) && ws_floats >= 0, "snake_conv1d: workspace must be 16-byte aligned");
+        const int64_t tiles = ceil_div(t_out, kNT) * ceil_div(c_out, kMT);
+        const int cus = device_cu_count();
+        const int64_t chunks = ceil_div(c_in, kernel == 1 ? conv_chunk<1>::CI : conv_chunk<7>::CI);
+        const int64_t pitch = split_pitch(t_out);
+        int64_t splits = cus > 0 && tiles < cus ? std::min<int64_t>(kMaxSplits, 2 * cus / tiles) : 1;
+        while (splits > 1 && (chunks / splits < 2 || splits * c_out * pitch > ws_floats)) --splits;
+        if (splits > 1) {
+            const int64_t bytes = splits * c_out * pitch * static_cast<int64_t>(sizeof(float));
+            const int64_t elt = static_cast<int64_t>(sizeof(float));
+            LEVO_REQUIRE(!ranges_overlap(ws, bytes, y, c_out * y_stride * elt) &&
+                             !ranges_overlap(ws, bytes, x, c_in * x_stride * elt) &&
+                             (residual == nullptr || !ranges_overlap(ws, bytes, residual, c_out * residual_stride * elt)),
+                         "snake_conv1d: workspace overlaps a tensor");
+            p.splits = static_cast<int32_t>(splits);
+            p.part = ws;
+            p.part_slice = c_out * pitch;
+            p.part_pitch = pitch;
+        }
+    }
     switch (kernel) {
         case 1: return launch_conv<1>(p, 1, st, what);
         case 3: return launch_conv<3>(p, 1, st, what);
         case 5: return launch_conv<5>(p, 1, st, what);
         default: return launch_conv<7>(p, 1, st, what);
     }
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                     const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                                     const float * weight, int64_t c_out, int64_t kernel, const float * bias,
+                                     int64_t padding, int64_t dilation, const float * residual,
+                                     int64_t residual_stride, float * y, int64_t y_stride,
+                                     levo_hip_stream_t stream) {
+    return conv1d_entry(x, x_stride, c_in, t_in, alpha_log, beta_log, param_type, weight, c_out, kernel, bias,
+                        padding, dilation, residual, residual_stride, y, y_stride, nullptr, 0, as_hip(stream),
+                        "levo_hip_snake_conv1d");
+}
+
+extern "C" int64_t levo_hip_snake_conv1d_split_workspace_floats(int64_t c_out, int64_t t_out) {
+    if (c_out <= 0 || t_out <= 0 || c_out > (1 << 20) || t_out >= (int64_t{1} << 40)) return -1;
+    return kMaxSplits * c_out * split_pitch(t_out);
+}
+
+extern "C" int levo_hip_snake_conv1d_split(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                           const void * alpha_log, const void * beta_log,
+                                           levo_hip_type param_type, const float * weight, int64_t c_out,
+                                           int64_t kernel, const float * bias, int64_t padding, int64_t dilation,
+                                           const float * residual, int64_t residual_stride, float * y,
+                                           int64_t y_stride, float * workspace, int64_t workspace_floats,
+                                           levo_hip_stream_t stream) {
+    return conv1d_entry(x, x_stride, c_in, t_in, alpha_log, beta_log, param_type, weight, c_out, kernel, bias,
+                        padding, dilation, residual, residual_stride, y, y_stride, workspace, workspace_floats,
+                        as_hip(stream), "levo_hip_snake_conv1d_split");
 }
 
 namespace levo_hip {

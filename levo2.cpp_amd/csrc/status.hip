@@ -5,6 +5,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <map>
 #include <mutex>
 #include <set>
 #include <string>
@@ -44,6 +45,20 @@ int allow_dynamic_lds(const void * kernel, int bytes, const char * what) {
     }
     done.insert({kernel, device});
     return LEVO_HIP_OK;
+}
+
+int device_cu_count() {
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0) return 0;
+    static std::mutex mu;
+    static std::map<int, int> counts;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = counts.find(device);
+    if (it != counts.end()) return it->second;
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) n = 0;
+    counts[device] = n;
+    return n;
 }
 
 int launch_status(const char * what) {

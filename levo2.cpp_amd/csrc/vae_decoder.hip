@@ -66,6 +66,34 @@ const char * missing_weight(const levo_hip_vae_decoder_weights & w) {
 
 bool weights_present(const levo_hip_vae_decoder_weights & w) { return missing_weight(w) == nullptr; }
 
+// The free tail of a decoder buffer of n floats whose first `used` floats
+// hold a tensor: workspace for a split-K convolution writing that tensor.
+struct tail {
+    float * p;
+    int64_t floats;
+};
+tail tail_of(float * buf, int64_t n, int64_t used) {
+    const int64_t start = (used + 63) / 64 * 64;  // 256-byte aligned
+    return start < n ? tail{buf + start, n - start} : tail{nullptr, 0};
+}
+
+// run_residual (src/levo-vae.cpp:91-100); conv_0 writes h, conv_1 writes y.
+// With workspaces (the free tails of the decoder's h and y buffers) the two
+// convolutions of the two-launch form take the split-K path.
+int residual_unit(const float * x, int64_t c, int64_t len, const levo_hip_vae_residual & u, int64_t dilation,
+                  levo_hip_type pt, float * y, float * h, tail ws_h, tail ws_y, levo_hip_stream_t stream) {
+    const int fused = launch_residual_unit_fused(x, c, len, u.pre.alpha_log, u.pre.beta_log, u.conv_0.weight,
+                                                 u.conv_0.bias, u.post.alpha_log, u.post.beta_log, u.conv_1.weight,
+                                                 u.conv_1.bias, dilation, pt, y, as_hip(stream));
+    if (fused != kNotFused) return fused;
+    const int st = levo_hip_snake_conv1d_split(x, len, c, len, u.pre.alpha_log, u.pre.beta_log, pt, u.conv_0.weight,
+                                               c, 7, u.conv_0.bias, 3 * dilation, dilation, nullptr, 0, h, len,
+                                               ws_h.p, ws_h.floats, stream);
+    if (st != LEVO_HIP_OK) return st;
+    return levo_hip_snake_conv1d_split(h, len, c, len, u.post.alpha_log, u.post.beta_log, pt, u.conv_1.weight, c, 1,
+                                       u.conv_1.bias, 0, 1, x, len, y, len, ws_y.p, ws_y.floats, stream);
+}
+
 }  // namespace
 }  // namespace levo_hip
 
@@ -103,18 +131,8 @@ extern "C" int levo_hip_vae_residual_unit(const float * x, int64_t channels, int
     const uintptr_t yb = reinterpret_cast<uintptr_t>(y);
     const uintptr_t n = static_cast<uintptr_t>(channels * time) * sizeof(float);
     LEVO_REQUIRE(yb + n <= xb || xb + n <= yb, "vae_residual_unit: y must not overlap x");
-    const int fused = launch_residual_unit_fused(x, channels, time, unit->pre.alpha_log, unit->pre.beta_log,
-                                                 unit->conv_0.weight, unit->conv_0.bias, unit->post.alpha_log,
-                                                 unit->post.beta_log, unit->conv_1.weight, unit->conv_1.bias,
-                                                 dilation, param_type, y, as_hip(stream));
-    if (fused != kNotFused) return fused;
-    const int st = levo_hip_snake_conv1d(x, time, channels, time, unit->pre.alpha_log, unit->pre.beta_log,
-                                         param_type, unit->conv_0.weight, channels, 7, unit->conv_0.bias,
-                                         3 * dilation, dilation, nullptr, 0, h, time, stream);
-    if (st != LEVO_HIP_OK) return st;
-    return levo_hip_snake_conv1d(h, time, channels, time, unit->post.alpha_log, unit->post.beta_log, param_type,
-                                 unit->conv_1.weight, channels, 1, unit->conv_1.bias, 0, 1, x, time, y, time,
-                                 stream);
+    return residual_unit(x, channels, time, *unit, dilation, param_type, y, h, tail{nullptr, 0}, tail{nullptr, 0},
+                         stream);
 }
 
 extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const float * latent, int64_t frames,
@@ -139,8 +157,10 @@ extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const
         if (st != LEVO_HIP_OK) return st; \
     } while (0)
     // input projection: no SnakeBeta in front (src/levo-vae.cpp:219-221)
-    LEVO_STEP(levo_hip_snake_conv1d(latent, frames, kLatent, frames, nullptr, nullptr, pt, w->input.weight,
-                                    kInWidth[0], 7, w->input.bias, 3, 1, nullptr, 0, a, frames, stream));
+    const tail ws_in = tail_of(a, n, kInWidth[0] * frames);
+    LEVO_STEP(levo_hip_snake_conv1d_split(latent, frames, kLatent, frames, nullptr, nullptr, pt, w->input.weight,
+                                          kInWidth[0], 7, w->input.bias, 3, 1, nullptr, 0, a, frames, ws_in.p,
+                                          ws_in.floats, stream));
     int64_t len = frames;
     for (int s = 0; s < 5; ++s) {
         const levo_hip_vae_stage & sg = w->stage[s];
@@ -154,7 +174,8 @@ extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const
         // residual units: x in b, y into a (free since the upsample read it),
         // then the two swap
         for (int r = 0; r < 3; ++r) {
-            LEVO_STEP(levo_hip_vae_residual_unit(b, c, len, &sg.residual[r], kDilations[r], pt, a, h, stream));
+            LEVO_STEP(residual_unit(b, c, len, sg.residual[r], kDilations[r], pt, a, h, tail_of(h, n, c * len),
+                                    tail_of(a, n, c * len), stream));
             std::swap(a, b);
         }
         if (stage_outputs != nullptr && stage_outputs[s] != nullptr) {

@@ -187,6 +187,9 @@ class LevoHip:
             "levo_hip_snake_beta_batch": (ctypes.c_int, [ctypes.POINTER(SnakeJob), ctypes.c_int, _P]),
             "levo_hip_snake_conv1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64, _P,
                                                      _I64, _I64, _P, _I64, _P, _I64, _P]),
+            "levo_hip_snake_conv1d_split_workspace_floats": (_I64, [_I64, _I64]),
+            "levo_hip_snake_conv1d_split": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64, _I64,
+                                                           _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
             "levo_hip_conv_transpose1d_pack_weights": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_snake_conv_transpose1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64,
                                                                _I64, _P, _I64, _P, _I64, _P]),
@@ -270,6 +273,20 @@ class LevoHip:
             _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
             _addr(weight), c_out, kernel, _addr(bias), padding, dilation, _addr(residual),
             residual_stride or t_out, _addr(y), y_stride or t_out, _stream(stream)))
+
+    def snake_conv1d_split_workspace_floats(self, c_out, t_out) -> int:
+        return int(self.lib.levo_hip_snake_conv1d_split_workspace_floats(c_out, t_out))
+
+    def snake_conv1d_split(self, x, c_in, t_in, weight, c_out, kernel, *, workspace, workspace_floats,
+                           alpha_log=None, beta_log=None, param_type=F32, bias=None, padding=0, dilation=1,
+                           residual=None, y=None, x_stride=None, residual_stride=None, y_stride=None, stream=None):
+        """snake_conv1d with a workspace: split K over several workgroups per tile when the grid is small."""
+        t_out = t_in + 2 * padding - dilation * (kernel - 1)
+        return self._check(self.lib.levo_hip_snake_conv1d_split(
+            _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
+            _addr(weight), c_out, kernel, _addr(bias), padding, dilation, _addr(residual),
+            residual_stride or t_out, _addr(y), y_stride or t_out, _addr(workspace), workspace_floats,
+            _stream(stream)))
 
     def conv_transpose1d_pack_weights(self, weight, packed, c_in, c_out, stride, stream=None):
         return self._check(self.lib.levo_hip_conv_transpose1d_pack_weights(_addr(weight), _addr(packed), c_in, c_out,
