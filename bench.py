@@ -899,6 +899,33 @@ def bench_snake_conv(torch, hip, head, dev, warmup, steps):
                      "frac_f32_mfma": round(tflops / PEAK_F32_MFMA_TFLOPS, 4), "bytes_per_launch": nbytes,
                      "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": "mfma"}
         del x, w, y, r
+    # stage 1's upsampler (SnakeBeta + ConvTranspose1d 2048 -> 1024, stride 10) at the same window:
+    # 252 input frames, 160 workgroups over the ten stride phases, split three ways
+    ci, co, t_in, s = 2048, 1024, 252, 10
+    pad = (s + 1) // 2
+    t_out = (t_in + 1) * s - 2 * pad
+    x = torch.randn((ci, t_in), generator=g, device=dev)
+    packed = torch.randn(s * co * ci * 2, generator=g, device=dev) / math.sqrt(2 * ci)
+    b = torch.randn(co, generator=g, device=dev) * 0.1
+    a = torch.randn(ci, generator=g, device=dev) * 0.5
+    bl = torch.randn(ci, generator=g, device=dev) * 0.5
+    y = torch.empty((co, t_out), device=dev)
+    nws = hip.snake_conv_transpose1d_split_workspace_floats(co, t_in, s)
+    ws = torch.empty(nws, device=dev)
+    for name, split in (("stage1_upsample_x10", True), ("stage1_upsample_x10_unsplit", False)):
+        if split:
+            fn = lambda i: hip.snake_conv_transpose1d_split(x, ci, t_in, packed, co, s, workspace=ws,
+                                                            workspace_floats=nws, alpha_log=a, beta_log=bl, bias=b,
+                                                            padding=pad, y=y)
+        else:
+            fn = lambda i: hip.snake_conv_transpose1d(x, ci, t_in, packed, co, s, alpha_log=a, beta_log=bl, bias=b,
+                                                      padding=pad, y=y)
+        ms = time_op(torch, head, fn, 1, warmup, max(steps // 4, 5))
+        tflops = 2.0 * ci * co * 2 * s * (t_in + 1) / (ms * 1e-3) / 1e12  # two taps per phase column
+        nbytes = 4 * (ci * t_in + co * t_out)
+        out[name] = {"shape": [ci, co, t_in, s], "us_per_launch": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1),
+                     "frac_f32_mfma": round(tflops / PEAK_F32_MFMA_TFLOPS, 4), "bytes_per_launch": nbytes,
+                     "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "bound": "mfma"}
     return out
 
 

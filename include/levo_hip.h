@@ -163,6 +163,26 @@ int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride, int64_t c
                                     const float * packed_weight, int64_t c_out, int64_t stride, const float * bias,
                                     int64_t padding, float * y, int64_t y_stride, levo_hip_stream_t stream);
 
+/* Floats of workspace levo_hip_snake_conv_transpose1d_split uses at most:
+ * four partial sums of every phase's t_in + 1 output columns, rows padded to
+ * a multiple of 4 floats; < 0 if invalid. */
+int64_t levo_hip_snake_conv_transpose1d_split_workspace_floats(int64_t c_out, int64_t t_in, int64_t stride);
+
+/* levo_hip_snake_conv_transpose1d (the same arguments, results and errors)
+ * with a device workspace (16-byte aligned, overlapping none of the
+ * tensors): when the launch has fewer workgroups (128 x 128 tiles times
+ * stride phases) than the GPU has compute units, the input channels are
+ * split over up to four workgroups per tile and phase, as
+ * levo_hip_snake_conv1d_split does, and a second launch adds each output
+ * sample's partial sums in split order, then the bias. Deterministic; it
+ * differs from levo_hip_snake_conv_transpose1d by the F32 rounding of the
+ * other summation order. Same reference call sites. */
+int levo_hip_snake_conv_transpose1d_split(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                          const void * alpha_log, const void * beta_log, levo_hip_type param_type,
+                                          const float * packed_weight, int64_t c_out, int64_t stride,
+                                          const float * bias, int64_t padding, float * y, int64_t y_stride,
+                                          float * workspace, int64_t workspace_floats, levo_hip_stream_t stream);
+
 /* The VAE decoder's weights in device memory, the fields of
  * vae_decoder_weights (src/levo-vae-model.h:39-66). Convolution weights are
  * F32 in ggml order ([k][c_in][c_out] ne = W[c_out][c_in][k] in memory);

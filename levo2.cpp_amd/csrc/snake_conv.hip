@@ -82,12 +82,14 @@ struct conv_params {
     // tile back to back
     int32_t xcd_order;
     int32_t tiles_x, tiles, phases;
-    // Split K: with splits > 1 the grid's phase axis is the split index z.
-    // Split z sums the input channels of chunks [z n / splits, (z + 1) n /
-    // splits) of the n chunks and writes that partial sum, without bias or
-    // residual, to part + z * part_slice (rows part_pitch floats apart,
-    // 16-byte aligned); split_combine_kernel then adds the partials in split
-    // order and applies the epilogue.
+    // Split K: the grid's phase axis z covers n_phase stride phases times
+    // `splits` splits, phase z % n_phase and split z / n_phase. Split j sums
+    // the input channels of chunks [j n / splits, (j + 1) n / splits) of the
+    // n chunks and writes that partial sum (columns q of the phase, without
+    // bias or residual) to part + z * part_slice, rows part_pitch floats
+    // apart, 16-byte aligned; a combine kernel then adds the partials in
+    // split order and applies the epilogue.
+    int32_t n_phase;
     int32_t splits;
     float * part;
     int64_t part_slice;
@@ -407,7 +409,10 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     const tile_id tl = conv_tile(p0);
     if (!tl.live) return;
     conv_params p = p0;
-    p.w += static_cast<int64_t>(tl.z) * p.w_phase;  // this phase's weights
+    const int n_phase = p.n_phase > 0 ? p.n_phase : 1;
+    const int phase = tl.z % n_phase;
+    const int split = tl.z / n_phase;
+    p.w += static_cast<int64_t>(phase) * p.w_phase;  // this phase's weights
     constexpr int CI = conv_chunk<KW>::CI;
     constexpr int KC = conv_chunk<KW>::KC;
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -431,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
     // input channels of this workgroup (a split's share, or all); the
     // parameter table is indexed from ci_begin
     int ci_begin, ci_end;
-    split_range<CI>(p, tl.z, ci_begin, ci_end);
+    split_range<CI>(p, split, ci_begin, ci_end);
 
     f32x4v ra[conv_slots<KW>::NA];
     float rb[conv_slots<KW>::NB];
@@ -495,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void snake_conv1d_kernel(const conv_param
         buf ^= 1;
     }
 
-    conv_epilogue<true>(p.splits > 1 ? split_target(p, tl.z) : p, lds, acc, tid, h, vh, g, m, t0, co0, tl.z);
+    conv_epilogue<true>(p.splits > 1 ? split_target(p, tl.z) : p, lds, acc, tid, h, vh, g, m, t0, co0, phase);
 }
 
 // ---- narrow output (c_out <= 4): the decoder's 128 -> 2 output conv -------
@@ -770,7 +775,10 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     conv_params p = p0;
     const tile_id tl = conv_tile(p0);
     if (!tl.live) return;
-    if (KW == 2) p.w += static_cast<int64_t>(tl.z) * p.w_phase;  // this phase's weights (one phase otherwise)
+    const int n_phase = p.n_phase > 0 ? p.n_phase : 1;
+    const int phase = tl.z % n_phase;
+    const int split = tl.z / n_phase;
+    if (KW == 2) p.w += static_cast<int64_t>(phase) * p.w_phase;  // this phase's weights (one phase otherwise)
     extern __shared__ __attribute__((aligned(16))) float lds[];
     const int buf_floats = a_floats<KW>() + kThreads * NB;
     snake_param * sp = reinterpret_cast<snake_param *>(lds + 2 * buf_floats);  // [c_in] when p.snake
@@ -788,7 +796,7 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     // input channels of this workgroup (a split's share, or all); the
     // parameter table is indexed from ci_begin
     int ci_begin, ci_end;
-    split_range<CI>(p, tl.z, ci_begin, ci_end);
+    split_range<CI>(p, split, ci_begin, ci_end);
     // k = 7 divides (faster there, measured); k = 2 multiplies by b_magic
     auto row_of = [&](int e) { return KW == 7 ? e / bw : b_row(e, p.b_magic); };
     const int64_t tb = t0 - p.pad;
@@ -937,7 +945,7 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
         residual_tail(p, f, lds, acc, tid, h, vh, g, m, t0);
     } else {
         conv_epilogue<KW == 2>(p.splits > 1 ? split_target(p, tl.z) : p, lds, acc, tid, h, vh, g, m, t0, co0,
-                               tl.z);
+                               phase);
     }
 }
 
@@ -967,6 +975,25 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(const conv_para
         if (p.residual) o = p.residual[co * p.r_pitch + t + q] + o;
         p.y[co * p.y_pitch + t + q] = o;
     }
+}
+
+// The transposed convolution's combine, per output sample t of y (coalesced
+// writes): t + padding = q * o_stride + r is column q of phase r, whose
+// partial sums are added in split order, then the bias, as the scatter
+// epilogue adds it. Every t in [0, y_len) is one (q, r) with q <= t_in.
+__global__ __launch_bounds__(kThreads) void split_combine_scatter_kernel(const conv_params p) {
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (e >= p.y_len * p.c_out) return;
+    const int co = static_cast<int>(e / p.y_len);
+    const int64_t t = e - co * p.y_len;
+    const int64_t u = t - p.o_base;  // o_base = -padding <= 0
+    const int64_t q = u / p.o_stride;
+    const int r = static_cast<int>(u - q * p.o_stride);
+    const float * src = p.part + r * p.part_slice + co * p.part_pitch + q;
+    float v = src[0];
+    for (int j = 1; j < p.splits; ++j) v = v + src[static_cast<int64_t>(j) * p.n_phase * p.part_slice];
+    if (p.bias) v = v + p.bias[co];
+    p.y[co * p.y_pitch + t] = v;
 }
 
 // The launch grid: the XCD-ordered 1-D grid for more than 8 workgroups.
@@ -999,19 +1026,25 @@ int launch_il(conv_params p, int phases, size_t table, hipStream_t st, const cha
 }
 
 int launch_split_combine(const conv_params & p, hipStream_t st, const char * what) {
-    const int64_t groups = ceil_div(p.t_out, 4) * p.c_out;
-    split_combine_kernel<<<dim3(static_cast<uint32_t>(ceil_div(groups, kThreads))), kThreads, 0, st>>>(p);
+    if (p.scatter) {
+        const int64_t n = p.y_len * p.c_out;
+        split_combine_scatter_kernel<<<dim3(static_cast<uint32_t>(ceil_div(n, kThreads))), kThreads, 0, st>>>(p);
+    } else {
+        const int64_t groups = ceil_div(p.t_out, 4) * p.c_out;
+        split_combine_kernel<<<dim3(static_cast<uint32_t>(ceil_div(groups, kThreads))), kThreads, 0, st>>>(p);
+    }
     return launch_status(what);
 }
 
 // One convolution launch (with p.splits > 1: the split launch, then the
-// combine). phases > 1 (transposed convolutions) never comes with splits.
+// combine).
 template <int KW>
 int launch_conv(conv_params p, int phases, hipStream_t st, const char * what) {
     if (!p.scatter && p.c_out <= 4 && (KW - 1) * p.dil <= kNarrowMaxSpan) return launch_narrow<KW>(p, st, what);
     constexpr int CI = conv_chunk<KW>::CI;
     const int splits = p.splits > 1 ? p.splits : 1;
-    const int gphases = phases * splits;  // the grid's phase axis: phases or splits
+    const int gphases = phases * splits;  // the grid's phase axis: phases times splits
+    p.n_phase = phases;
     p.b_width = (kNT + (KW - 1) * p.dil + 3) & ~3;
     // each thread stages at most two samples of an input row (one for KW = 2)
     LEVO_REQUIRE(KW == 1 || p.b_width <= (KW == 2 ? 1 : 2) * kThreads, "snake_conv1d: dilation too large");
@@ -1284,11 +1317,13 @@ extern "C" int levo_hip_conv_transpose1d_pack_weights(const float * weight, floa
     return launch_status("levo_hip_conv_transpose1d_pack_weights");
 }
 
-extern "C" int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
-                                               const void * alpha_log, const void * beta_log,
-                                               levo_hip_type param_type, const float * packed_weight,
-                                               int64_t c_out, int64_t stride, const float * bias, int64_t padding,
-                                               float * y, int64_t y_stride, levo_hip_stream_t stream) {
+namespace levo_hip {
+namespace {
+
+int conv_transpose_entry(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in, const void * alpha_log,
+                         const void * beta_log, levo_hip_type param_type, const float * packed_weight,
+                         int64_t c_out, int64_t stride, const float * bias, int64_t padding, float * y,
+                         int64_t y_stride, float * ws, int64_t ws_floats, hipStream_t st, const char * what) {
     LEVO_REQUIRE(c_in > 0 && c_out > 0 && t_in > 0, "LeVo audio graph: incompatible ConvTranspose1d weight/input shapes");
     LEVO_REQUIRE(stride > 0 && padding >= 0, "LeVo audio graph: invalid ConvTranspose1d stride or padding");
     LEVO_REQUIRE(stride <= 64 && c_in <= (1 << 20) && c_out <= (1 << 20) && t_in < (int64_t{1} << 36),
@@ -1334,5 +1369,57 @@ extern "C" int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride
     p.w_phase = c_out * c_in * 2;
     p.scatter = 1;
     p.param_ring = 0;
-    return launch_conv<2>(p, static_cast<int>(stride), as_hip(stream), "levo_hip_snake_conv_transpose1d");
+    p.splits = 1;
+    if (ws != nullptr) {
+        LEVO_REQUIRE(aligned16(ws) && ws_floats >= 0, "conv_transpose1d: workspace must be 16-byte aligned");
+        const int64_t wgs = ceil_div(t_in + 1, kNT) * ceil_div(c_out, kMT) * stride;
+        const int cus = device_cu_count();
+        const int64_t chunks = ceil_div(c_in, conv_chunk<2>::CI);
+        const int64_t pitch = split_pitch(t_in + 1);
+        int64_t splits = cus > 0 && wgs < cus ? std::min<int64_t>(kMaxSplits, 2 * cus / wgs) : 1;
+        while (splits > 1 && (chunks / splits < 2 || splits * stride * c_out * pitch > ws_floats)) --splits;
+        if (splits > 1) {
+            const int64_t bytes = splits * stride * c_out * pitch * static_cast<int64_t>(sizeof(float));
+            const int64_t elt = static_cast<int64_t>(sizeof(float));
+            LEVO_REQUIRE(!ranges_overlap(ws, bytes, y, c_out * y_stride * elt) &&
+                             !ranges_overlap(ws, bytes, x, c_in * x_stride * elt),
+                         "conv_transpose1d: workspace overlaps a tensor");
+            p.splits = static_cast<int32_t>(splits);
+            p.part = ws;
+            p.part_slice = c_out * pitch;
+            p.part_pitch = pitch;
+        }
+    }
+    return launch_conv<2>(p, static_cast<int>(stride), st, what);
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+extern "C" int levo_hip_snake_conv_transpose1d(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                               const void * alpha_log, const void * beta_log,
+                                               levo_hip_type param_type, const float * packed_weight,
+                                               int64_t c_out, int64_t stride, const float * bias, int64_t padding,
+                                               float * y, int64_t y_stride, levo_hip_stream_t stream) {
+    return conv_transpose_entry(x, x_stride, c_in, t_in, alpha_log, beta_log, param_type, packed_weight, c_out,
+                                stride, bias, padding, y, y_stride, nullptr, 0, as_hip(stream),
+                                "levo_hip_snake_conv_transpose1d");
+}
+
+extern "C" int64_t levo_hip_snake_conv_transpose1d_split_workspace_floats(int64_t c_out, int64_t t_in,
+                                                                         int64_t stride) {
+    if (c_out <= 0 || t_in <= 0 || stride <= 0 || c_out > (1 << 20) || stride > 64 || t_in >= (int64_t{1} << 36))
+        return -1;
+    return kMaxSplits * stride * c_out * split_pitch(t_in + 1);
+}
+
+extern "C" int levo_hip_snake_conv_transpose1d_split(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in,
+                                                     const void * alpha_log, const void * beta_log,
+                                                     levo_hip_type param_type, const float * packed_weight,
+                                                     int64_t c_out, int64_t stride, const float * bias,
+                                                     int64_t padding, float * y, int64_t y_stride, float * workspace,
+                                                     int64_t workspace_floats, levo_hip_stream_t stream) {
+    return conv_transpose_entry(x, x_stride, c_in, t_in, alpha_log, beta_log, param_type, packed_weight, c_out,
+                                stride, bias, padding, y, y_stride, workspace, workspace_floats, as_hip(stream),
+                                "levo_hip_snake_conv_transpose1d_split");
 }

@@ -166,9 +166,11 @@ extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const
         const levo_hip_vae_stage & sg = w->stage[s];
         const int64_t stride = kStrides[s];
         const int64_t out_len = len * stride;  // (len + 1) s - 2 ((s + 1) / 2) for even s
-        LEVO_STEP(levo_hip_snake_conv_transpose1d(a, len, kInWidth[s], len, sg.activation.alpha_log,
-                                                  sg.activation.beta_log, pt, sg.upsample.weight, kOutWidth[s],
-                                                  stride, sg.upsample.bias, (stride + 1) / 2, b, out_len, stream));
+        const tail ws_up = tail_of(b, n, kOutWidth[s] * out_len);
+        LEVO_STEP(levo_hip_snake_conv_transpose1d_split(a, len, kInWidth[s], len, sg.activation.alpha_log,
+                                                        sg.activation.beta_log, pt, sg.upsample.weight,
+                                                        kOutWidth[s], stride, sg.upsample.bias, (stride + 1) / 2, b,
+                                                        out_len, ws_up.p, ws_up.floats, stream));
         len = out_len;
         const int64_t c = kOutWidth[s];
         // residual units: x in b, y into a (free since the upsample read it),

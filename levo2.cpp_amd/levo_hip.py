@@ -193,6 +193,9 @@ class LevoHip:
             "levo_hip_conv_transpose1d_pack_weights": (ctypes.c_int, [_P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_snake_conv_transpose1d": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P, _I64,
                                                                _I64, _P, _I64, _P, _I64, _P]),
+            "levo_hip_snake_conv_transpose1d_split_workspace_floats": (_I64, [_I64, _I64, _I64]),
+            "levo_hip_snake_conv_transpose1d_split": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, ctypes.c_int, _P,
+                                                                     _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
             "levo_hip_vae_decode_workspace_bytes": (_I64, [_I64]),
             "levo_hip_vae_validate_weights": (ctypes.c_int, [ctypes.POINTER(VaeDecoderWeights)]),
             "levo_hip_vae_decode": (ctypes.c_int, [ctypes.POINTER(VaeDecoderWeights), _P, _I64, _P, _P, _P, _I64,
@@ -300,6 +303,19 @@ class LevoHip:
             _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
             _addr(packed_weight), c_out, stride, _addr(bias), padding, _addr(y), y_stride or t_out,
             _stream(stream)))
+
+    def snake_conv_transpose1d_split_workspace_floats(self, c_out, t_in, stride) -> int:
+        return int(self.lib.levo_hip_snake_conv_transpose1d_split_workspace_floats(c_out, t_in, stride))
+
+    def snake_conv_transpose1d_split(self, x, c_in, t_in, packed_weight, c_out, stride, *, workspace,
+                                     workspace_floats, alpha_log=None, beta_log=None, param_type=F32, bias=None,
+                                     padding=0, y=None, x_stride=None, y_stride=None, stream=None):
+        """snake_conv_transpose1d with a workspace: split K when the grid is small."""
+        t_out = (t_in + 1) * stride - 2 * padding
+        return self._check(self.lib.levo_hip_snake_conv_transpose1d_split(
+            _addr(x), x_stride or t_in, c_in, t_in, _addr(alpha_log), _addr(beta_log), param_type,
+            _addr(packed_weight), c_out, stride, _addr(bias), padding, _addr(y), y_stride or t_out,
+            _addr(workspace), workspace_floats, _stream(stream)))
 
     def vae_validate_weights(self, weights: VaeDecoderWeights):
         return self._check(self.lib.levo_hip_vae_validate_weights(ctypes.byref(weights)))

@@ -182,3 +182,86 @@ def test_rejects_bad_workspace(hip, dev, binding):
         hip.snake_conv1d_split(x, c, t, w, c, 7, workspace=big, workspace_floats=n, padding=3, y=big)
     assert hip.snake_conv1d_split_workspace_floats(0, 5) < 0
     assert hip.snake_conv1d_split_workspace_floats(3, 5) == 4 * 3 * 8
+
+
+# ---- transposed convolution (levo_hip_snake_conv_transpose1d_split) --------
+
+def _run_t(hip, dev, x, w, b, stride, pad, a=None, bl=None, param_type=0, split=True):
+    import torch
+    c_in, t_in = x.shape
+    _, c_out, _ = w.shape
+    t_out = (t_in + 1) * stride - 2 * pad
+    packed = torch.empty(stride * c_out * c_in * 2, dtype=torch.float32, device=dev)
+    hip.conv_transpose1d_pack_weights(to_dev(w, dev), packed, c_in, c_out, stride)
+    y = torch.full((c_out, t_out), float("nan"), dtype=torch.float32, device=dev)
+    kwargs = dict(alpha_log=to_dev(a, dev) if a is not None else None,
+                  beta_log=to_dev(bl, dev) if bl is not None else None, param_type=param_type,
+                  bias=to_dev(b, dev) if b is not None else None, padding=pad, y=y)
+    if split:
+        n = hip.snake_conv_transpose1d_split_workspace_floats(c_out, t_in, stride)
+        ws = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
+        hip.snake_conv_transpose1d_split(to_dev(x, dev), c_in, t_in, packed, c_out, stride, workspace=ws,
+                                         workspace_floats=n, **kwargs)
+    else:
+        hip.snake_conv_transpose1d(to_dev(x, dev), c_in, t_in, packed, c_out, stride, **kwargs)
+    torch.cuda.synchronize()
+    return from_dev(y)
+
+
+def _f64_transpose_rows(oracle, x, w, b, stride, pad, a, bl, rows):
+    """ggml_conv_transpose_1d + crop + bias (src/levo-audio-ops.cpp:89-123) in
+    float64 for output channels `rows`: input sample q feeds outputs
+    q * stride + k - pad for k < 2 * stride."""
+    xs = (oracle.snake_beta(x, a, bl, threads=8) if a is not None else x).astype(np.float64)
+    t_in = x.shape[1]
+    full = np.zeros((len(rows), (t_in + 1) * stride))
+    for k in range(2 * stride):
+        full[:, k:k + t_in * stride:stride] += w[:, rows, k].astype(np.float64).T @ xs
+    t_out = (t_in + 1) * stride - 2 * pad
+    y = full[:, pad:pad + t_out]
+    return y + b[rows, None] if b is not None else y
+
+
+def _t_case(oracle, c_in, c_out, t_in, stride, seed):
+    x = oracle.gaussian(c_in * t_in, seed).reshape(c_in, t_in)
+    w = (oracle.gaussian(c_in * c_out * 2 * stride, seed + 1) *
+         np.float32(1.0 / np.sqrt(2 * c_in))).reshape(c_in, c_out, 2 * stride)
+    b = (oracle.gaussian(c_out, seed + 2) * np.float32(0.1)).astype(np.float32)
+    a, bl = _params(oracle, c_in, seed + 3)
+    return x, w, b, a, bl
+
+
+def test_transpose_stage1_window(hip, dev, oracle):
+    """Stage 1's upsampler at a 10.08 s window (2048 -> 1024 channels, 252
+    frames, stride 10: 160 workgroups, three splits): float64 rows, two calls
+    bit-identical, the unsplit launch within two F32 errors."""
+    c_in, c_out, t_in, s = 2048, 1024, 252, 10
+    pad = (s + 1) // 2
+    x, w, b, a, bl = _t_case(oracle, c_in, c_out, t_in, s, 80)
+    got = _run_t(hip, dev, x, w, b, s, pad, a, bl)
+    rows = np.arange(0, c_out, 16)
+    assert f32_err(got[rows], _f64_transpose_rows(oracle, x, w, b, s, pad, a, bl, rows)) <= 1e-5
+    again = _run_t(hip, dev, x, w, b, s, pad, a, bl)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    assert f32_err(got, _run_t(hip, dev, x, w, b, s, pad, a, bl, split=False)) <= 2e-5
+
+
+@pytest.mark.parametrize("c_in,c_out,t_in,stride,pad,f16", [(2048, 1024, 60, 10, 5, False), (520, 200, 77, 3, 2, True),
+                                                            (64, 130, 255, 1, 0, False), (256, 128, 103, 4, 2, True)])
+def test_transpose_split_shapes(hip, dev, oracle, c_in, c_out, t_in, stride, pad, f16):
+    """Against float64 (every output channel) and the oracle's
+    conv_transpose_1d restatement: four splits at stage 1's channels, a
+    partial last chunk (520 channels: 33 chunks of 16), stride 1, column
+    counts not a multiple of 4, F16 SnakeBeta parameters."""
+    x, w, b, a, bl = _t_case(oracle, c_in, c_out, t_in, stride, c_in + t_in)
+    pt = 0
+    if f16:
+        a16, b16 = oracle.f32_to_f16(a), oracle.f32_to_f16(bl)
+        got = _run_t(hip, dev, x, w, b, stride, pad, a16, b16, param_type=1)
+        a, bl = oracle.f16_to_f32(a16), oracle.f16_to_f32(b16)
+    else:
+        got = _run_t(hip, dev, x, w, b, stride, pad, a, bl, param_type=pt)
+    rows = np.arange(c_out)
+    assert f32_err(got, _f64_transpose_rows(oracle, x, w, b, stride, pad, a, bl, rows)) <= 1e-5
+    xs = oracle.snake_beta(x, a, bl, threads=8)
+    assert f32_err(got, oracle.conv_transpose1d(xs, w, b, stride, pad)) <= 2e-5
