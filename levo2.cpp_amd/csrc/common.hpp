@@ -55,6 +55,15 @@ int dequantize_kquant(levo_hip_type type, const void * src, void * dst, levo_hip
 // otherwise (nothing launched). x and y are [128][t] with row stride t and
 // must not overlap.
 constexpr int kNotFused = 1;
+
+// levo_hip_snake_conv1d_split on contiguous rows (x, y: row stride t) with a
+// SnakeBeta of its own applied to the output (after the bias):
+// y = snake_post(conv(snake(x)) + bias). The decoder's residual units store
+// their k = 1 conv's activated input this way, one SnakeBeta per sample.
+int snake_conv1d_post(const float * x, int64_t c_in, int64_t t, const void * alpha_log, const void * beta_log,
+                      levo_hip_type param_type, const float * weight, int64_t c_out, int64_t kernel,
+                      const float * bias, int64_t padding, int64_t dilation, float * y, const void * post_alpha_log,
+                      const void * post_beta_log, float * ws, int64_t ws_floats, hipStream_t stream);
 int launch_residual_unit_fused(const float * x, int64_t c, int64_t t, const void * pre_alpha_log,
                                const void * pre_beta_log, const float * w0, const float * b0,
                                const void * post_alpha_log, const void * post_beta_log, const float * w1,

@@ -91,6 +91,11 @@ struct conv_params {
     // split order and applies the epilogue.
     int32_t n_phase;
     int32_t splits;
+    // SnakeBeta applied to the output after the bias and residual (null: none;
+    // same parameter type as alpha_log): the decoder's residual units store
+    // snake_post(conv_0(...)), the input of their k = 1 conv, once per sample.
+    const void * post_alpha_log;
+    const void * post_beta_log;
     float * part;
     int64_t part_slice;
     int64_t part_pitch;
@@ -117,6 +122,7 @@ __device__ __forceinline__ conv_params split_target(const conv_params & p, int z
     e.y_pitch = p.part_pitch;
     e.bias = nullptr;
     e.residual = nullptr;
+    e.post_alpha_log = nullptr;
     e.y_vec = 1;
     e.scatter = 0;
     return e;
@@ -324,6 +330,15 @@ __device__ __forceinline__ void load_snake_logs(const conv_params & p, int c, fl
     }
 }
 
+// The post-output SnakeBeta parameters of output channel co.
+__device__ __forceinline__ snake_param post_param(const conv_params & p, int co) {
+    const float al = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.post_alpha_log)[co])
+                                 : static_cast<const float *>(p.post_alpha_log)[co];
+    const float bl = p.param_f16 ? h2f(static_cast<const uint16_t *>(p.post_beta_log)[co])
+                                 : static_cast<const float *>(p.post_beta_log)[co];
+    return make_snake_param(al, bl);
+}
+
 // The output tile goes through LDS (the A / B buffers, free after the
 // kernel's last barrier) so that bias, residual and y move as whole rows.
 // D[row][col] of a 16 x 16 tile is in lane col + 16 * (row / 4), item row % 4.
@@ -381,6 +396,11 @@ __device__ __forceinline__ void conv_epilogue(const conv_params & p, float * lds
             f32x4v v = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
             if (p.bias) v = v + p.bias[co];
             if (p.residual) v = res[it] + v;
+            if (p.post_alpha_log) {
+                const snake_param q = post_param(p, co);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = snake(v[u], q);
+            }
             *reinterpret_cast<f32x4v *>(p.y + co * p.y_pitch + t0 + c4) = v;
         }
         return;
@@ -393,12 +413,15 @@ __device__ __forceinline__ void conv_epilogue(const conv_params & p, float * lds
         const float bv = p.bias ? p.bias[co] : 0.0f;
         const f32x4v o = *reinterpret_cast<const f32x4v *>(out + r * kOutStride + c4);
         const int64_t t = t0 + c4;
+        snake_param sq{};
+        if (p.post_alpha_log) sq = post_param(p, co);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if (t + q >= p.t_out) break;
             float v = o[q];
             if (p.bias) v = v + bv;
             if (p.residual) v = p.residual[co * p.r_pitch + t + q] + v;
+            if (p.post_alpha_log) v = snake(v, sq);
             p.y[co * p.y_pitch + t + q] = v;
         }
     }
@@ -949,9 +972,9 @@ __global__ __launch_bounds__(kThreads, 2) void snake_conv1d_il(const conv_params
     }
 }
 
-// y = ((part_0 + part_1) + ...) + bias (+ residual) per float4 of a row: the
-// split launch's partial sums in split order, then the unsplit epilogue's
-// bias and residual adds. Rows of the partials are padded to a multiple of 4
+// y = ((part_0 + part_1) + ...) + bias (+ residual), then the post SnakeBeta
+// if any, per float4 of a row: the split launch's partial sums in split
+// order, then the unsplit epilogue's steps. Rows of the partials are padded to a multiple of 4
 // floats; the padding is summed and dropped.
 __global__ __launch_bounds__(kThreads) void split_combine_kernel(const conv_params p) {
     const int64_t groups = (p.t_out + 3) / 4;  // float4 groups per row
@@ -963,8 +986,14 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(const conv_para
     f32x4v v = *reinterpret_cast<const f32x4v *>(src);
     for (int z = 1; z < p.splits; ++z) v = v + *reinterpret_cast<const f32x4v *>(src + z * p.part_slice);
     if (p.bias) v = v + p.bias[co];
+    snake_param sq{};
+    if (p.post_alpha_log) sq = post_param(p, co);
     if (p.y_vec && t + 4 <= p.t_out) {
         if (p.residual) v = *reinterpret_cast<const f32x4v *>(p.residual + co * p.r_pitch + t) + v;
+        if (p.post_alpha_log) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = snake(v[u], sq);
+        }
         *reinterpret_cast<f32x4v *>(p.y + co * p.y_pitch + t) = v;
         return;
     }
@@ -973,6 +1002,7 @@ __global__ __launch_bounds__(kThreads) void split_combine_kernel(const conv_para
         if (t + q >= p.t_out) break;
         float o = v[q];
         if (p.residual) o = p.residual[co * p.r_pitch + t + q] + o;
+        if (p.post_alpha_log) o = snake(o, sq);
         p.y[co * p.y_pitch + t + q] = o;
     }
 }
@@ -1174,7 +1204,7 @@ int conv1d_entry(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in, 
                  const void * beta_log, levo_hip_type param_type, const float * weight, int64_t c_out,
                  int64_t kernel, const float * bias, int64_t padding, int64_t dilation, const float * residual,
                  int64_t residual_stride, float * y, int64_t y_stride, float * ws, int64_t ws_floats,
-                 hipStream_t st, const char * what) {
+                 const void * post_alpha_log, const void * post_beta_log, hipStream_t st, const char * what) {
     LEVO_REQUIRE(c_in > 0 && c_out > 0 && t_in > 0, "LeVo audio graph: incompatible Conv1d weight/input shapes");
     LEVO_REQUIRE(padding >= 0 && dilation > 0, "LeVo audio graph: invalid Conv1d stride, padding, or dilation");
     LEVO_REQUIRE(kernel == 1 || kernel == 3 || kernel == 5 || kernel == 7, "snake_conv1d: kernel size must be 1, 3, 5 or 7");
@@ -1223,6 +1253,12 @@ int conv1d_entry(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in, 
     p.scatter = 0;
     p.param_ring = 0;
     p.splits = 1;
+    p.post_alpha_log = post_alpha_log;
+    p.post_beta_log = post_beta_log;
+    LEVO_REQUIRE(post_alpha_log == nullptr || (post_beta_log != nullptr && c_out > 4),
+                 "snake_conv1d: post SnakeBeta needs both parameters and more than 4 outputs");
+    LEVO_REQUIRE(post_alpha_log == nullptr || param_type == LEVO_HIP_TYPE_F32 || param_type == LEVO_HIP_TYPE_F16,
+                 "LeVo audio graph: SnakeBeta alpha_log must be F32 or F16");
     if (ws != nullptr && c_out > 4) {
         LEVO_REQUIRE(aligned16(ws) && ws_floats >= 0, "snake_conv1d: workspace must be 16-byte aligned");
         const int64_t tiles = ceil_div(t_out, kNT) * ceil_div(c_out, kMT);
@@ -1262,9 +1298,22 @@ extern "C" int levo_hip_snake_conv1d(const float * x, int64_t x_stride, int64_t 
                                      int64_t residual_stride, float * y, int64_t y_stride,
                                      levo_hip_stream_t stream) {
     return conv1d_entry(x, x_stride, c_in, t_in, alpha_log, beta_log, param_type, weight, c_out, kernel, bias,
-                        padding, dilation, residual, residual_stride, y, y_stride, nullptr, 0, as_hip(stream),
-                        "levo_hip_snake_conv1d");
+                        padding, dilation, residual, residual_stride, y, y_stride, nullptr, 0, nullptr, nullptr,
+                        as_hip(stream), "levo_hip_snake_conv1d");
 }
+
+namespace levo_hip {
+
+int snake_conv1d_post(const float * x, int64_t c_in, int64_t t, const void * alpha_log, const void * beta_log,
+                      levo_hip_type param_type, const float * weight, int64_t c_out, int64_t kernel,
+                      const float * bias, int64_t padding, int64_t dilation, float * y, const void * post_alpha_log,
+                      const void * post_beta_log, float * ws, int64_t ws_floats, hipStream_t st) {
+    return conv1d_entry(x, t, c_in, t, alpha_log, beta_log, param_type, weight, c_out, kernel, bias, padding,
+                        dilation, nullptr, 0, y, t, ws, ws_floats, post_alpha_log, post_beta_log, st,
+                        "levo_hip_vae_decode");
+}
+
+}  // namespace levo_hip
 
 extern "C" int64_t levo_hip_snake_conv1d_split_workspace_floats(int64_t c_out, int64_t t_out) {
     if (c_out <= 0 || t_out <= 0 || c_out > (1 << 20) || t_out >= (int64_t{1} << 40)) return -1;
@@ -1280,7 +1329,7 @@ extern "C" int levo_hip_snake_conv1d_split(const float * x, int64_t x_stride, in
                                            levo_hip_stream_t stream) {
     return conv1d_entry(x, x_stride, c_in, t_in, alpha_log, beta_log, param_type, weight, c_out, kernel, bias,
                         padding, dilation, residual, residual_stride, y, y_stride, workspace, workspace_floats,
-                        as_hip(stream), "levo_hip_snake_conv1d_split");
+                        nullptr, nullptr, as_hip(stream), "levo_hip_snake_conv1d_split");
 }
 
 namespace levo_hip {

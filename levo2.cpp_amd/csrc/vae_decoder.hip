@@ -78,20 +78,33 @@ tail tail_of(float * buf, int64_t n, int64_t used) {
 }
 
 // run_residual (src/levo-vae.cpp:91-100); conv_0 writes h, conv_1 writes y.
-// With workspaces (the free tails of the decoder's h and y buffers) the two
-// convolutions of the two-launch form take the split-K path.
+// Inside the decoder (post_in_h): conv_0 stores snake_post(h), computed once
+// per sample in its epilogue, and conv_1 reads it without a SnakeBeta of its
+// own (the same F32 values the k = 1 conv's staging would compute from h),
+// and both convolutions take the split-K path with the free tails of the
+// decoder's h and y buffers. The public unit keeps h = conv_0's output.
 int residual_unit(const float * x, int64_t c, int64_t len, const levo_hip_vae_residual & u, int64_t dilation,
-                  levo_hip_type pt, float * y, float * h, tail ws_h, tail ws_y, levo_hip_stream_t stream) {
+                  levo_hip_type pt, float * y, float * h, bool post_in_h, tail ws_h, tail ws_y,
+                  levo_hip_stream_t stream) {
     const int fused = launch_residual_unit_fused(x, c, len, u.pre.alpha_log, u.pre.beta_log, u.conv_0.weight,
                                                  u.conv_0.bias, u.post.alpha_log, u.post.beta_log, u.conv_1.weight,
                                                  u.conv_1.bias, dilation, pt, y, as_hip(stream));
     if (fused != kNotFused) return fused;
-    const int st = levo_hip_snake_conv1d_split(x, len, c, len, u.pre.alpha_log, u.pre.beta_log, pt, u.conv_0.weight,
-                                               c, 7, u.conv_0.bias, 3 * dilation, dilation, nullptr, 0, h, len,
-                                               ws_h.p, ws_h.floats, stream);
+    const bool post = post_in_h && u.post.alpha_log != nullptr && u.post.beta_log != nullptr && c > 4;
+    int st;
+    if (post) {
+        st = snake_conv1d_post(x, c, len, u.pre.alpha_log, u.pre.beta_log, pt, u.conv_0.weight, c, 7, u.conv_0.bias,
+                               3 * dilation, dilation, h, u.post.alpha_log, u.post.beta_log, ws_h.p, ws_h.floats,
+                               as_hip(stream));
+    } else {
+        st = levo_hip_snake_conv1d_split(x, len, c, len, u.pre.alpha_log, u.pre.beta_log, pt, u.conv_0.weight, c, 7,
+                                         u.conv_0.bias, 3 * dilation, dilation, nullptr, 0, h, len, ws_h.p,
+                                         ws_h.floats, stream);
+    }
     if (st != LEVO_HIP_OK) return st;
-    return levo_hip_snake_conv1d_split(h, len, c, len, u.post.alpha_log, u.post.beta_log, pt, u.conv_1.weight, c, 1,
-                                       u.conv_1.bias, 0, 1, x, len, y, len, ws_y.p, ws_y.floats, stream);
+    return levo_hip_snake_conv1d_split(h, len, c, len, post ? nullptr : u.post.alpha_log,
+                                       post ? nullptr : u.post.beta_log, pt, u.conv_1.weight, c, 1, u.conv_1.bias, 0,
+                                       1, x, len, y, len, ws_y.p, ws_y.floats, stream);
 }
 
 }  // namespace
@@ -131,8 +144,8 @@ extern "C" int levo_hip_vae_residual_unit(const float * x, int64_t channels, int
     const uintptr_t yb = reinterpret_cast<uintptr_t>(y);
     const uintptr_t n = static_cast<uintptr_t>(channels * time) * sizeof(float);
     LEVO_REQUIRE(yb + n <= xb || xb + n <= yb, "vae_residual_unit: y must not overlap x");
-    return residual_unit(x, channels, time, *unit, dilation, param_type, y, h, tail{nullptr, 0}, tail{nullptr, 0},
-                         stream);
+    return residual_unit(x, channels, time, *unit, dilation, param_type, y, h, false, tail{nullptr, 0},
+                         tail{nullptr, 0}, stream);
 }
 
 extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const float * latent, int64_t frames,
@@ -176,7 +189,7 @@ extern "C" int levo_hip_vae_decode(const levo_hip_vae_decoder_weights * w, const
         // residual units: x in b, y into a (free since the upsample read it),
         // then the two swap
         for (int r = 0; r < 3; ++r) {
-            LEVO_STEP(residual_unit(b, c, len, sg.residual[r], kDilations[r], pt, a, h, tail_of(h, n, c * len),
+            LEVO_STEP(residual_unit(b, c, len, sg.residual[r], kDilations[r], pt, a, h, true, tail_of(h, n, c * len),
                                     tail_of(a, n, c * len), stream));
             std::swap(a, b);
         }

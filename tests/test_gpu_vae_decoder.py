@@ -306,3 +306,93 @@ def test_residual_unit_rejects(hip, binding, dev):
         with pytest.raises(binding.LevoHipError, match="F32 or F16"):
             hip.vae_residual_unit(x[:channels], channels, 256, u, 1, torch.zeros((channels, 256), device=dev),
                                   h[:channels], param_type=8)
+
+
+# ---- the decode as its public steps ------------------------------------------
+
+def _compose_decode(hip, binding, dev, w, latent):
+    """decode through the public entry points, in the decoder's order:
+    levo_hip_snake_conv1d_split (input conv; each two-launch unit's conv_0,
+    then conv_1 with the post SnakeBeta and the residual),
+    levo_hip_snake_conv_transpose1d_split, levo_hip_vae_residual_unit (the
+    one-launch 128-channel units) and levo_hip_snake_conv1d (output conv).
+    Each split call gets the workspace the decoder gives it: the free tail of
+    the workspace buffer its output lives in (a third of
+    levo_hip_vae_decode_workspace_bytes, after the output rounded up to 64
+    floats), so both split alike."""
+    import torch
+    frames = latent.shape[1]
+    n_buf = hip.vae_decode_workspace_bytes(frames) // 4 // 3
+    tail = lambda out_floats: n_buf - (out_floats + 63) // 64 * 64
+    keep = []
+
+    def d(a):
+        if a is None:
+            return None
+        t = to_dev(a, dev)
+        keep.append(t)
+        return t
+
+    def conv(x, ci, t, wb, co, k, pad, dil, act=None, res=None):
+        t_out = t + 2 * pad - dil * (k - 1)
+        y = torch.empty((co, t_out), dtype=torch.float32, device=dev)
+        n = tail(co * t_out)
+        ws = torch.empty(n, dtype=torch.float32, device=dev)
+        keep.extend([y, ws])
+        hip.snake_conv1d_split(x, ci, t, d(wb[0]), co, k, workspace=ws, workspace_floats=n,
+                               alpha_log=d(act[0]) if act else None, beta_log=d(act[1]) if act else None,
+                               bias=d(wb[1]), padding=pad, dilation=dil, residual=res, y=y)
+        return y
+
+    x = conv(d(latent), 64, frames, w.input, 2048, 7, 3, 1)
+    length = frames
+    for s, sg in enumerate(w.stages):
+        st = binding.VAE_STRIDES[s]
+        ci, co = binding.VAE_IN_WIDTH[s], binding.VAE_OUT_WIDTH[s]
+        packed = torch.empty(st * co * ci * 2, dtype=torch.float32, device=dev)
+        hip.conv_transpose1d_pack_weights(d(sg["up"][0]), packed, ci, co, st)
+        y = torch.empty((co, length * st), dtype=torch.float32, device=dev)
+        n = tail(co * length * st)
+        ws = torch.empty(n, dtype=torch.float32, device=dev)
+        keep.extend([packed, y, ws])
+        hip.snake_conv_transpose1d_split(x, ci, length, packed, co, st, workspace=ws, workspace_floats=n,
+                                         alpha_log=d(sg["act"][0]), beta_log=d(sg["act"][1]), bias=d(sg["up"][1]),
+                                         padding=(st + 1) // 2, y=y)
+        x, length = y, length * st
+        for r, dil in enumerate((1, 3, 9)):
+            ru = sg["res"][r]
+            if co == 128:
+                u, k2 = _unit_struct(binding, dev, ru)
+                keep.extend(k2)
+                y = torch.empty((co, length), dtype=torch.float32, device=dev)
+                h = torch.empty((co, length), dtype=torch.float32, device=dev)
+                keep.extend([y, h])
+                hip.vae_residual_unit(x, co, length, u, dil, y, h)
+            else:
+                h = conv(x, co, length, ru["conv0"], co, 7, 3 * dil, dil, act=ru["pre"])
+                y = conv(h, co, length, ru["conv1"], co, 1, 0, 1, act=ru["post"], res=x)
+            x = y
+    audio = torch.empty((2, length), dtype=torch.float32, device=dev)
+    hip.snake_conv1d(x, 128, length, d(w.out_w), 2, 7, alpha_log=d(w.out_act[0]), beta_log=d(w.out_act[1]),
+                     padding=3, y=audio)
+    torch.cuda.synchronize()
+    return from_dev(audio)
+
+
+@pytest.mark.parametrize("frames", [1, 3])
+def test_decoder_equals_its_public_steps(hip, binding, dev, oracle, frames):
+    """Bit for bit: the decoder stores each two-launch unit's conv_0 output
+    through the post SnakeBeta (one evaluation per sample in the epilogue or
+    the split combine) where the public steps apply it in conv_1's staging;
+    both compute snake(h) from the same F32 h with the same parameters."""
+    import torch
+    w = Weights(binding, 4321 + frames)
+    latent = oracle.gaussian(64 * frames, 17 + frames).reshape(64, frames)
+    dw, keep = device_weights(hip, binding, dev, w)
+    nbytes = hip.vae_decode_workspace_bytes(frames)
+    ws = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+    audio = torch.full((2, frames * 1920), float("nan"), dtype=torch.float32, device=dev)
+    hip.vae_decode(dw, to_dev(latent, dev), frames, audio, ws, nbytes)
+    got = from_dev(audio)
+    want = _compose_decode(hip, binding, dev, w, latent)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
