@@ -8,7 +8,8 @@ start) and HIP's copies are left out.
 
     python3 levo2.cpp_amd/bench/trace_summary.py <kernel_trace.csv> > table.md
 
-With --vae, the HBM bytes of each of the 31 launches of the last VAE decode
+With --vae, the HBM bytes of each of the 31 steps of the last VAE decode (a
+split-K convolution's combine launch counted with its split launch)
 in two rocprofv3 --pmc runs of `bench.py --only vae` (FETCH_SIZE, then
 WRITE_SIZE), scaled by the copy factors in traffic.json, beside the bytes of
 the launch's activations (inputs and outputs once) and weights:
@@ -16,8 +17,9 @@ the launch's activations (inputs and outputs once) and weights:
     python3 levo2.cpp_amd/bench/trace_summary.py --vae <fetch_counter_collection.csv>
         <write_counter_collection.csv> profiles/traffic.json <frames> > table.md
 
-With --vae-trace, each launch of the last decode of each window size in a
-kernel trace of `bench.py --only vae`, with its duration and TFLOP/s:
+With --vae-trace, each step of the last decode of each window size in a
+kernel trace of `bench.py --only vae` (a split-K convolution and its combine
+launch as one step), with its duration and TFLOP/s:
 
     python3 levo2.cpp_amd/bench/trace_summary.py --vae-trace <kernel_trace.csv> > table.md
 
@@ -126,6 +128,10 @@ def vae_flops(frames: int) -> list[float]:
     return out + [2.0 * 2 * 128 * 7 * t]
 
 
+def is_combine(name: str) -> bool:
+    return "split_combine" in name
+
+
 def vae_trace(path: str) -> list[str]:
     launches = []
     for r in csv.DictReader(open(path)):
@@ -137,23 +143,34 @@ def vae_trace(path: str) -> list[str]:
         launches.append((int(r["Start_Timestamp"]), n, grid // max(wg, 1),
                          int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
     launches.sort()
+    # a split-K convolution is two launches, the split one and its combine:
+    # one step of the decode, timed from the first's start to the second's end
+    steps = []
+    for start, n, wgs, ns in launches:
+        if is_combine(n) and steps:
+            s0, n0, w0, _ = steps[-1]
+            steps[-1] = (s0, n0 + " + combine", w0, start + ns - s0)
+        else:
+            steps.append((start, n, wgs, ns))
     per = len(vae_launches(1))
-    decodes = [launches[i:i + per] for i in range(0, len(launches) - per + 1, per)]
+    decodes = [steps[i:i + per] for i in range(0, len(steps) - per + 1, per)]
     rows = []
     for frames in (252, 1000):
-        # the input conv's grid tells the window size: ceil(frames / 128) time tiles x 16 channel tiles
-        mine = [d for d in decodes if d[0][2] == -(-frames // 128) * 16]
+        # the output conv's grid tells the window size: 1024 of the frames * 1920 samples per workgroup
+        mine = [d for d in decodes if d[-1][2] == -(-frames * 1920 // 1024)]
         if not mine:
             continue
         d = mine[-1]
         labels = [lab for lab, _, _ in vae_launches(frames)]
         flops = vae_flops(frames)
         rows += [f"#### {frames} frames ({frames * 1920 / 48000:.2f} s of audio)", "",
-                 "| launch | kernel | grid (WGs) | µs | TFLOP/s |", "|---|---|---:|---:|---:|"]
+                 "| step | kernel | grid (WGs) | µs | TFLOP/s |", "|---|---|---:|---:|---:|"]
         for lab, (_, n, wgs, ns), fl in zip(labels, d, flops):
             rows.append(f"| {lab} | `{n}` | {wgs} | {ns / 1e3:.1f} | {fl / ns / 1e3:.1f} |")
-        tot = sum(x[3] for x in d)
-        rows += [f"| **total** | | | **{tot / 1e3:.1f}** | **{sum(flops) / tot / 1e3:.1f}** |", ""]
+        tot = d[-1][0] + d[-1][3] - d[0][0]
+        busy = sum(x[3] for x in d)
+        rows += [f"| **total** (first start to last end; {busy / 1e3:.1f} µs inside the steps) | | | "
+                 f"**{tot / 1e3:.1f}** | **{sum(flops) / tot / 1e3:.1f}** |", ""]
     return rows
 
 
@@ -184,7 +201,17 @@ def vae_launches(frames: int) -> list[tuple[str, int, int]]:
 def vae_traffic(fetch_csv: str, write_csv: str, traffic_json: str, frames: str) -> list[str]:
     scales = json.load(open(traffic_json))
     labels = vae_launches(int(frames))
-    lib = lambda rows: [r for r in rows if "levo_hip::" in r[1]][-len(labels):]  # HIP's copies left out
+    def lib(rows):
+        # HIP's copies left out; a split-K convolution's combine counted with its split launch
+        steps = []
+        for r in rows:
+            if "levo_hip::" not in r[1]:
+                continue
+            if is_combine(r[1]) and steps:
+                steps[-1] = (steps[-1][0], steps[-1][1], steps[-1][2] + r[2])
+            else:
+                steps.append(r)
+        return steps[-len(labels):]
     fe = lib(counters(fetch_csv, "FETCH_SIZE"))
     wr = lib(counters(write_csv, "WRITE_SIZE"))
     rows = [f"FETCH_SIZE x {scales['fetch_scale']:.4f}, WRITE_SIZE x {scales['write_scale']:.4f} (the copy factors "
