@@ -943,7 +943,8 @@ def vae_decode_flops(frames):
 def bench_vae_decode(torch, hip, binding, head, dev, warmup, steps, frames=252):
     """The whole Oobleck VAE decoder (levo_hip_vae_decode: 37 SnakeBeta +
     convolution steps in 31 launches, the six 128-channel residual units one
-    launch each) on one window: latent [64][frames] to stereo audio
+    launch each, plus a combine launch for each convolution whose grid is
+    split over its input channels) on one window: latent [64][frames] to stereo audio
     [2][frames * 1920], random weights of the decoder's shapes. 252 frames is
     10.08 s of audio; 1000 frames is the renderer's decode window
     (renderer_window_frames, src/levo-renderer-pattern.h:11)."""
@@ -989,7 +990,7 @@ def bench_vae_decode(torch, hip, binding, head, dev, warmup, steps, frames=252):
     del keep, ws
     torch.cuda.empty_cache()
     return {"frames": frames, "audio_seconds": seconds, "ms_per_window": round(ms, 3),
-            "realtime_factor": round(seconds / (ms * 1e-3), 1), "launches": 31, "flops_per_window": flops,
+            "realtime_factor": round(seconds / (ms * 1e-3), 1), "steps": 31, "flops_per_window": flops,
             "TFLOP/s": round(tflops, 1), "frac_f32_mfma": round(tflops / PEAK_F32_MFMA_TFLOPS, 4), "bound": "mfma"}
 
 

@@ -246,9 +246,12 @@ int64_t levo_hip_vae_decode_workspace_bytes(int64_t frames);
  * 128, strides 10, 6, 4, 4, 2, dilations 1, 3, 9). 37 fused SnakeBeta +
  * convolution steps (input conv, 7 per stage, output conv) in 31 launches:
  * the 128-channel residual units (stages 4 and 5) are one launch each, as
- * levo_hip_vae_residual_unit runs them. None of the
- * activations leaves the device, the caller's workspace (16-byte aligned,
- * levo_hip_vae_decode_workspace_bytes) holds them. Every weight the
+ * levo_hip_vae_residual_unit runs them; a convolution whose grid would
+ * leave compute units idle runs split-K (levo_hip_snake_conv1d_split) with
+ * one more combine launch, its partial sums in the free tail of a workspace
+ * buffer. None of the activations leaves the device, the caller's
+ * workspace (16-byte aligned, levo_hip_vae_decode_workspace_bytes) holds
+ * them. Every weight the
  * reference's validate_weights requires (src/levo-vae.cpp:56-78) must be
  * non-null. stage_outputs, when non-null, holds 5 device pointers (each may
  * be null): stage s's output [width_s][frames * prod(strides[0..s])] is
