@@ -1266,6 +1266,18 @@ int conv1d_entry(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in, 
         const int64_t chunks = ceil_div(c_in, kernel == 1 ? conv_chunk<1>::CI : conv_chunk<7>::CI);
         const int64_t pitch = split_pitch(t_out);
         int64_t splits = cus > 0 && tiles < cus ? std::min<int64_t>(kMaxSplits, 2 * cus / tiles) : 1;
+        if (splits == 1 && kernel == 7 && snake && dilation <= 9) {
+            // A grid that fills the GPU, but whose interleaved k = 7 kernel
+            // holds the whole SnakeBeta table at one workgroup per CU (the
+            // 1024 input channels of stage 1): two splits halve the table,
+            // and two workgroups share a CU.
+            const int64_t b_width = (kNT + 6 * dilation + 3) & ~int64_t{3};
+            const int64_t nb = ceil_div(conv_chunk<7>::CI * b_width, kThreads) <= 5 ? 5 : il_shape<7>::kMaxNB;
+            const int64_t bufs = 2 * (a_floats<7>() + kThreads * nb) * static_cast<int64_t>(sizeof(float));
+            const int64_t entry = static_cast<int64_t>(sizeof(snake_param));
+            const int64_t half = conv_chunk<7>::CI * ceil_div(ceil_div(c_in, conv_chunk<7>::CI), 2);
+            if (bufs + c_in * entry > 80 * 1024 && bufs + half * entry <= 80 * 1024) splits = 2;
+        }
         while (splits > 1 && (chunks / splits < 2 || splits * c_out * pitch > ws_floats)) --splits;
         if (splits > 1) {
             const int64_t bytes = splits * c_out * pitch * static_cast<int64_t>(sizeof(float));
