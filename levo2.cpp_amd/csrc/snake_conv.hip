@@ -1196,6 +1196,49 @@ bool ranges_overlap(const void * a, int64_t a_bytes, const void * b, int64_t b_b
     return pa < pb + static_cast<uintptr_t>(b_bytes) && pb < pa + static_cast<uintptr_t>(a_bytes);
 }
 
+// LDS bytes of the launch launch_conv<KW> makes (interleaved or plain
+// kernel) with a SnakeBeta table of table_ch channels.
+template <int KW>
+int64_t conv_lds_bytes(int64_t c_in, int64_t table_ch, int64_t dil, bool snake, bool w_vec) {
+    constexpr int CI = conv_chunk<KW>::CI;
+    const int64_t b_width = (kNT + (KW - 1) * dil + 3) & ~int64_t{3};
+    const int64_t entry = static_cast<int64_t>(sizeof(snake_param));
+    const int64_t out_tile = int64_t{kMT} * kOutStride * static_cast<int64_t>(sizeof(float));
+    if constexpr (KW == 2 || KW == 7) {
+        const int64_t nb = ceil_div(CI * b_width, kThreads);
+        if (w_vec && b_width >= kNT && nb <= il_shape<KW>::kMaxNB && (KW == 7 || c_in >= 512)) {
+            const int64_t slots = KW == 7 && nb <= 5 ? 5 : il_shape<KW>::kMaxNB;
+            const int64_t bufs = 2 * (a_floats<KW>() + kThreads * slots) * static_cast<int64_t>(sizeof(float));
+            return std::max(bufs + (snake ? table_ch * entry : entry), out_tile);
+        }
+    }
+    const int64_t buf = (a_floats<KW>() + CI * b_width) * static_cast<int64_t>(sizeof(float));
+    return std::max(2 * buf, out_tile) + (snake ? table_ch * entry : 0);
+}
+
+// Splits of a launch of `wgs` workgroups (tiles times stride phases) over
+// `chunks` K chunks of CI channels. A grid with fewer workgroups than CUs
+// splits up to kMaxSplits ways (two workgroups per CU). A larger grid splits
+// in two when that evens its last round: with w workgroups per CU (two when
+// the launch's LDS fits twice in a CU, one otherwise; a split halves the
+// SnakeBeta table) the launch takes ceil(wgs / (w CUs)) rounds of whole
+// tiles, or ceil(2 wgs / (w' CUs)) rounds of half tiles; two splits are taken
+// when they need at most 0.8 of the time (632 workgroups of stage 1 at
+// 1000 frames: 2 rounds of whole tiles against 3 of halves).
+template <int KW>
+int64_t pick_splits(int64_t wgs, int64_t chunks, int64_t c_in, int64_t dil, bool snake, bool w_vec) {
+    const int cus = device_cu_count();
+    if (cus <= 0) return 1;
+    if (wgs < cus) return std::min<int64_t>(kMaxSplits, 2 * cus / wgs);
+    constexpr int CI = conv_chunk<KW>::CI;
+    const int64_t per_cu_1 = conv_lds_bytes<KW>(c_in, c_in, dil, snake, w_vec) <= 80 * 1024 ? 2 : 1;
+    const int64_t half = CI * ceil_div(chunks, 2);
+    const int64_t per_cu_2 = conv_lds_bytes<KW>(c_in, half, dil, snake, w_vec) <= 80 * 1024 ? 2 : 1;
+    const int64_t rounds_1 = ceil_div(wgs, per_cu_1 * cus);
+    const int64_t rounds_2 = ceil_div(2 * wgs, per_cu_2 * cus);  // of half tiles
+    return rounds_2 * 5 <= rounds_1 * 8 ? 2 : 1;                 // rounds_2 / 2 <= 0.8 rounds_1
+}
+
 // levo_hip_snake_conv1d, and with a workspace the split-K form when the grid
 // would leave compute units idle: up to two workgroups per CU (at most
 // kMaxSplits splits), each split at least two K chunks, as many partial
@@ -1262,21 +1305,15 @@ int conv1d_entry(const float * x, int64_t x_stride, int64_t c_in, int64_t t_in, 
     if (ws != nullptr && c_out > 4) {
         LEVO_REQUIRE(aligned16(ws) && ws_floats >= 0, "snake_conv1d: workspace must be 16-byte aligned");
         const int64_t tiles = ceil_div(t_out, kNT) * ceil_div(c_out, kMT);
-        const int cus = device_cu_count();
         const int64_t chunks = ceil_div(c_in, kernel == 1 ? conv_chunk<1>::CI : conv_chunk<7>::CI);
         const int64_t pitch = split_pitch(t_out);
-        int64_t splits = cus > 0 && tiles < cus ? std::min<int64_t>(kMaxSplits, 2 * cus / tiles) : 1;
-        if (splits == 1 && kernel == 7 && snake && dilation <= 9) {
-            // A grid that fills the GPU, but whose interleaved k = 7 kernel
-            // holds the whole SnakeBeta table at one workgroup per CU (the
-            // 1024 input channels of stage 1): two splits halve the table,
-            // and two workgroups share a CU.
-            const int64_t b_width = (kNT + 6 * dilation + 3) & ~int64_t{3};
-            const int64_t nb = ceil_div(conv_chunk<7>::CI * b_width, kThreads) <= 5 ? 5 : il_shape<7>::kMaxNB;
-            const int64_t bufs = 2 * (a_floats<7>() + kThreads * nb) * static_cast<int64_t>(sizeof(float));
-            const int64_t entry = static_cast<int64_t>(sizeof(snake_param));
-            const int64_t half = conv_chunk<7>::CI * ceil_div(ceil_div(c_in, conv_chunk<7>::CI), 2);
-            if (bufs + c_in * entry > 80 * 1024 && bufs + half * entry <= 80 * 1024) splits = 2;
+        const bool w_vec = aligned16(weight) && (c_in * kernel) % 4 == 0;
+        int64_t splits;
+        switch (kernel) {
+            case 1: splits = pick_splits<1>(tiles, chunks, c_in, dilation, snake, w_vec); break;
+            case 3: splits = pick_splits<3>(tiles, chunks, c_in, dilation, snake, w_vec); break;
+            case 5: splits = pick_splits<5>(tiles, chunks, c_in, dilation, snake, w_vec); break;
+            default: splits = pick_splits<7>(tiles, chunks, c_in, dilation, snake, w_vec); break;
         }
         while (splits > 1 && (chunks / splits < 2 || splits * c_out * pitch > ws_floats)) --splits;
         if (splits > 1) {
@@ -1434,10 +1471,10 @@ int conv_transpose_entry(const float * x, int64_t x_stride, int64_t c_in, int64_
     if (ws != nullptr) {
         LEVO_REQUIRE(aligned16(ws) && ws_floats >= 0, "conv_transpose1d: workspace must be 16-byte aligned");
         const int64_t wgs = ceil_div(t_in + 1, kNT) * ceil_div(c_out, kMT) * stride;
-        const int cus = device_cu_count();
         const int64_t chunks = ceil_div(c_in, conv_chunk<2>::CI);
         const int64_t pitch = split_pitch(t_in + 1);
-        int64_t splits = cus > 0 && wgs < cus ? std::min<int64_t>(kMaxSplits, 2 * cus / wgs) : 1;
+        const bool w_vec = aligned16(packed_weight) && (c_in * 2) % 4 == 0 && (c_out * c_in * 2) % 4 == 0;
+        int64_t splits = pick_splits<2>(wgs, chunks, c_in, 1, snake, w_vec);
         while (splits > 1 && (chunks / splits < 2 || splits * stride * c_out * pitch > ws_floats)) --splits;
         if (splits > 1) {
             const int64_t bytes = splits * stride * c_out * pitch * static_cast<int64_t>(sizeof(float));
