@@ -194,8 +194,8 @@ def add_ceilings(torch, head, dev, ops, warmup, steps):
 
 def cpu_share():
     """Threads of the CPU share this process may use: its affinity set,
-    narrowed by OMP_NUM_THREADS when the environment sets one (the GPU box
-    sets it to the share it grants one GPU)."""
+    narrowed by OMP_NUM_THREADS when the environment sets one (a host that
+    shares its cores between GPUs sets it to one GPU's share)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
