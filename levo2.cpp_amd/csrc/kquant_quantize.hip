@@ -55,12 +55,41 @@ __device__ __forceinline__ void load_values(const S * row, int64_t col0, int64_t
     }
 }
 
+// The code of a search value v, clamp(nearest_int(v), lo, hi), as a float.
+// nearest_int rounds by adding 1.5 * 2^23: for |v| < 2^22 the sum stays in
+// [2^23, 2^24), where the float spacing is 1, so it is v rounded to nearest,
+// ties to even (the sum's parity is v's, 1.5 * 2^23 being even), which is
+// v_rndne_f32; the clamp of the integer and its conversion back equal a
+// float median of three. kFast takes that form (four instructions per code
+// with the product instead of seven); its callers establish |v| < 2^22 for
+// every value of a trial beforehand (in_trial_range), and a lane where that
+// fails repeats its search in the integer form.
+template <bool kFast>
+__device__ __forceinline__ float code_of(float v, float lo, float hi) {
+    if constexpr (kFast) return __builtin_amdgcn_fmed3f(__builtin_rintf(v), lo, hi);
+    else return static_cast<float>(clampi(nearest_int(v), static_cast<int>(lo), static_cast<int>(hi)));
+}
+
+// Every v = iscale * (x - min) of a trial has |v| < 2^22 when this holds, for
+// finite x in [xlo, xhi]: rounding is monotonic, so fl(x - min) lies between
+// fl(xlo - min) and fl(xhi - min), and |fl(iscale * d)| <= fl(|iscale| * |d|).
+// NaN or infinite scales or bounds fail it.
+__device__ __forceinline__ bool in_trial_range(float iscale, float min, float xlo, float xhi) {
+    const float d = fmaxf(__builtin_fabsf(xhi - min), __builtin_fabsf(min - xlo));
+    return __builtin_fabsf(iscale) * d < 0x1p22f;
+}
+
 // make_qkx2_quants(32, NMAX, x, w, L, &the_min, Laux, rmin, 0.1, NSTEP, false).
 // Returns the scale, -min in the_min, and the inverse scale and offset that
 // produced the winning codes (code = clamp(nearest_int(iscale_l * (x - min_l)))).
-template <int NMAX, int NSTEP>
+// A trial's codes (Laux) are kept in registers for its error sum, as ggml
+// keeps them in Laux; every float operation is ggml's, in its order. kFast
+// (finite x only) clears in_range when a trial's values may leave the float
+// code form's range; the caller then repeats the search with kFast false.
+template <int NMAX, int NSTEP, bool kFast>
 __device__ __forceinline__ float make_qkx2(const float (&x)[32], const float (&w)[32], float rmin, float & the_min,
-                                           float & iscale_l, float & min_l, bool & zero_codes) {
+                                           float & iscale_l, float & min_l, bool & zero_codes, bool & in_range) {
+    constexpr float kMax = static_cast<float>(NMAX);
     float min = x[0];
     float max = x[0];
     float sum_w = w[0];
@@ -72,6 +101,7 @@ __device__ __forceinline__ float make_qkx2(const float (&x)[32], const float (&w
         sum_w += w[i];
         sum_x += w[i] * x[i];
     }
+    const float xlo = min;
     if (min > 0) min = 0;
     zero_codes = false;
     if (max == min) {
@@ -84,24 +114,31 @@ __device__ __forceinline__ float make_qkx2(const float (&x)[32], const float (&w
     float iscale = NMAX / (max - min);
     float scale = 1 / iscale;
     float best_mad = 0;
+    if (kFast) in_range = in_range && in_trial_range(iscale, min, xlo, max);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        const int l = clampi(nearest_int(iscale * (x[i] - min)), 0, NMAX);
-        float diff = scale * static_cast<float>(l) + min - x[i];
+        const float l = code_of<kFast>(iscale * (x[i] - min), 0.0f, kMax);
+        float diff = scale * l + min - x[i];
         diff = diff * diff;
         best_mad += w[i] * diff;
     }
     iscale_l = iscale;
     min_l = min;
+    // one trial per iteration, not unrolled: the trials are sequential (each
+    // may move min) and an unrolled copy per trial would not fit the registers
+#pragma unroll 1
     for (int is = 0; is <= NSTEP; ++is) {
         iscale = (rmin + 0.1f * static_cast<float>(is) + static_cast<float>(NMAX)) / (max - min);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        float laux[32];
+        if (kFast) in_range = in_range && in_trial_range(iscale, min, xlo, max);
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const float l = static_cast<float>(clampi(nearest_int(iscale * (x[i] - min)), 0, NMAX));
-            sum_l += w[i] * l;
-            sum_l2 += w[i] * l * l;
-            sum_xl += w[i] * l * x[i];
+            laux[i] = code_of<kFast>(iscale * (x[i] - min), 0.0f, kMax);
+            const float wl = w[i] * laux[i];
+            sum_l += wl;
+            sum_l2 += wl * laux[i];
+            sum_xl += wl * x[i];
         }
         const float D = sum_w * sum_l2 - sum_l * sum_l;
         if (D > 0) {
@@ -114,7 +151,8 @@ __device__ __forceinline__ float make_qkx2(const float (&x)[32], const float (&w
             float mad = 0;
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
-                const float l = static_cast<float>(clampi(nearest_int(iscale * (x[i] - min)), 0, NMAX));
+                // the integer form recomputes the trial's codes (fewer live registers)
+                const float l = kFast ? laux[i] : code_of<false>(iscale * (x[i] - min), 0.0f, kMax);
                 float diff = this_scale * l + this_min - x[i];
                 diff = diff * diff;
                 mad += w[i] * diff;
@@ -134,7 +172,11 @@ __device__ __forceinline__ float make_qkx2(const float (&x)[32], const float (&w
 
 // make_qx_quants(16, 32, x, L, rmse_type 1, NULL). Returns the scale and the
 // inverse scale of the winning codes (code = clamp(nearest_int(iscale_l * x),
-// -32, 31) + 32), or zero_codes for an all-zero group.
+// -32, 31) + 32), or zero_codes for an all-zero group. The weights x^2 and
+// their products with x (ggml's w * x[i] * l is (w * x[i]) * l) are formed
+// once, outside the trials. For finite x every |iscale * x| stays within
+// 32.9 (|x| <= |max|), so kFast needs only finite values (the caller's check).
+template <bool kFast>
 __device__ __forceinline__ float make_qx(const float (&x)[16], float & iscale_l, bool & zero_codes) {
     constexpr int nmax = 32;
     float max = 0;
@@ -150,15 +192,20 @@ __device__ __forceinline__ float make_qx(const float (&x)[16], float & iscale_l,
     zero_codes = amax < 1e-15f;
     iscale_l = 0.0f;
     if (zero_codes) return 0.f;
+    float w[16], wx[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        w[i] = x[i] * x[i];
+        wx[i] = w[i] * x[i];
+    }
     float iscale = static_cast<float>(-nmax) / max;
     float sumlx = 0;
     float suml2 = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const float l = static_cast<float>(clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1));
-        const float w = x[i] * x[i];
-        sumlx += w * x[i] * l;
-        suml2 += w * l * l;
+        const float l = code_of<kFast>(iscale * x[i], -32.0f, 31.0f);
+        sumlx += wx[i] * l;
+        suml2 += (w[i] * l) * l;
     }
     iscale_l = iscale;
     float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
@@ -169,10 +216,9 @@ __device__ __forceinline__ float make_qx(const float (&x)[16], float & iscale_l,
         sumlx = suml2 = 0;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float l = static_cast<float>(clampi(nearest_int(iscale * x[i]), -nmax, nmax - 1));
-            const float w = x[i] * x[i];
-            sumlx += w * x[i] * l;
-            suml2 += w * l * l;
+            const float l = code_of<kFast>(iscale * x[i], -32.0f, 31.0f);
+            sumlx += wx[i] * l;
+            suml2 += (w[i] * l) * l;
         }
         if (suml2 > 0 && sumlx * sumlx > best * suml2) {
             iscale_l = iscale;
@@ -201,10 +247,38 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// One lane's sub-block of a Q4_K / Q5_K super-block: ggml's search over its
+// 32 values with the weights sqrt(mean x^2) + |x|. kFast returns false when a
+// lane of the wave met a code value outside the float form's range; the
+// caller then runs the integer form, which loads the values again (so
+// nothing of the first run stays live across it).
+template <bool Q5, typename S, bool kFast>
+__device__ __forceinline__ bool q45_search(const S * row, int64_t col0, int64_t src_cols, float & scale,
+                                           float & the_min, float & iscale_l, float & min_l, bool & zero_codes) {
+    // a compiler barrier: the values are loaded here, not reused from an
+    // earlier load of the same addresses (which would keep them live)
+    asm volatile("" ::: "memory");
+    float x[32];
+    load_values<S, 32>(row, col0, src_cols, x);
+    float sum_x2 = 0;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
+    const float av_x = sqrtf(sum_x2 / 32);
+    float w[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
+    // the float code form needs finite values (a NaN or inf in x, or squares
+    // that overflow, make sum_x2 NaN or inf)
+    bool in_range = __builtin_isfinite(sum_x2);
+    scale = make_qkx2<Q5 ? 31 : 15, Q5 ? 15 : 20, kFast>(x, w, Q5 ? -0.5f : -1.f, the_min, iscale_l, min_l,
+                                                         zero_codes, in_range);
+    return !kFast || __ballot(!in_range) == 0;
+}
+
 // Q4_K (Q5 = false) / Q5_K: eight lanes per super-block, eight super-blocks
 // per wave. Super-block sb is row sb / nsb_row, columns (sb % nsb_row) * 256.
 template <bool Q5, typename S>
-__global__ __launch_bounds__(kThreads) void quantize_q45_k_kernel(const S * __restrict__ src, int64_t src_cols,
+__global__ __launch_bounds__(kThreads, 3) void quantize_q45_k_kernel(const S * __restrict__ src, int64_t src_cols,
                                                                   int64_t src_stride, uint8_t * __restrict__ dst,
                                                                   int64_t nsb_row, int64_t nsb) {
     constexpr int NMAX = Q5 ? 31 : 15;
@@ -221,18 +295,13 @@ __global__ __launch_bounds__(kThreads) void quantize_q45_k_kernel(const S * __re
     const int64_t r = sbc / nsb_row;
     const int64_t col0 = (sbc - r * nsb_row) * 256 + 32 * j;
 
-    float x[32];
-    load_values<S, 32>(src + r * src_stride, col0, src_cols, x);
-    float sum_x2 = 0;
-#pragma unroll
-    for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
-    const float av_x = sqrtf(sum_x2 / 32);
-    float w[32];
-#pragma unroll
-    for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
-    float the_min, iscale_l, min_l;
+    float scale, the_min, iscale_l, min_l;
     bool zero_codes;
-    const float scale = make_qkx2<NMAX, Q5 ? 15 : 20>(x, w, Q5 ? -0.5f : -1.f, the_min, iscale_l, min_l, zero_codes);
+    if (!q45_search<Q5, S, true>(src + r * src_stride, col0, src_cols, scale, the_min, iscale_l, min_l, zero_codes))
+        q45_search<Q5, S, false>(src + r * src_stride, col0, src_cols, scale, the_min, iscale_l, min_l, zero_codes);
+    asm volatile("" ::: "memory");
+    float x[32];  // the values again (a cache hit), for the codes
+    load_values<S, 32>(src + r * src_stride, col0, src_cols, x);
     L.scale[g][j] = scale;
     L.min[g][j] = the_min;
     wave_lds_sync();
@@ -322,7 +391,12 @@ __global__ __launch_bounds__(kThreads) void quantize_q6_k_kernel(const S * __res
     load_values<S, 16>(src + r * src_stride, col0, src_cols, x);
     float iscale_l;
     bool zero_codes;
-    const float scale = make_qx(x, iscale_l, zero_codes);
+    float abs_sum = 0.0f;  // NaN or inf when a value is not finite (or the sum overflows)
+#pragma unroll
+    for (int l = 0; l < 16; ++l) abs_sum += fabsf(x[l]);
+    float scale;
+    if (__ballot(!__builtin_isfinite(abs_sum)) == 0) scale = make_qx<true>(x, iscale_l, zero_codes);
+    else scale = make_qx<false>(x, iscale_l, zero_codes);
     L.scale[g][j] = scale;
     wave_lds_sync();
     float max_scale = 0, max_abs_scale = 0;  // first of the largest magnitudes, as ggml

@@ -113,3 +113,26 @@ def test_rejects_bad_arguments(hip, dev, binding):
         hip.quantize_chunk(Q6_K, x, out, 0, 1, 256, imatrix=x)
     with pytest.raises(binding.LevoHipError, match="multiple of 256"):
         hip.quantize_rows(Q5_K, x, 0, 200, 200, out, 1, 224)
+
+
+def test_non_finite_and_extreme_blocks_bit_exact(hip, dev, oracle):
+    """Sub-blocks holding NaN, +-inf or values at the F16 range's ends: the
+    search's codes come from ggml's integer rounding (nearest_int's 1.5 * 2^23
+    addition) on every input, including where that is not a rounding of its
+    argument; the kernels' float code form must not be taken there."""
+    rng = np.random.default_rng(91)
+    cols = 1024
+    x = (rng.standard_normal((10, cols)) * 0.02).astype(np.float32)
+    x[0, 3] = np.nan
+    x[1, 40] = np.inf
+    x[2, 7] = -np.inf
+    x[3, :32] = 60000.0
+    x[3, 5] = -60000.0
+    x[4, 100] = 65504.0
+    x[5, ::37] = np.nan
+    x[6, 256:512] = np.inf
+    x[7, 300] = 3e38          # finite, with squares that overflow
+    x[8, :16] = -65504.0
+    x[9, 17] = 1e-30
+    for qtype in KQ:
+        _check(qtype, _gpu_quantize(hip, dev, qtype, x), oracle.quantize(qtype, x))
