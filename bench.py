@@ -1259,6 +1259,11 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     order.append(("q4_0_quantize_f16", 2 * R * Cc + q4.numel()))
     hip.dequantize(2, q4, deq, 0, R * Cc)
     order.append(("q4_0_dequantize_f32", q4.numel() + 4 * R * Cc))
+    for qt, name, bb in ((12, "q4_K", 144), (13, "q5_K", 176), (14, "q6_K", 210)):
+        qk = torch.empty(R * Cc // 256 * bb, dtype=torch.uint8, device=dev)
+        hip.quantize_rows(qt, wq, 1, Cc, Cc, qk, R, Cc)
+        order.append((f"{name}_quantize_f16", 2 * R * Cc + qk.numel()))
+        del qk
     P, S, V = 750, 3, 16384
     c = torch.randn((P * S, V), generator=g, device=dev) * 3
     u = torch.randn((P * S, V), generator=g, device=dev) * 3

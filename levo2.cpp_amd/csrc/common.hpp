@@ -108,9 +108,12 @@ constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
 constexpr int kRowRor4 = 0x124;  // row_ror:4
 constexpr int kRowRor8 = 0x128;  // row_ror:8
 
+// Every control used through mov (quad permutes, row rotations) gives each
+// lane a source inside its row, so no "old" value is needed: v_mov_b32_dpp
+// without one spares the register a zero (or a copy) would take.
 template <int kCtrl>
 __device__ __forceinline__ uint32_t mov(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, 0xF, 0xF, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xF, 0xF, false));
 }
 template <int kCtrl>
 __device__ __forceinline__ float mov(float v) {

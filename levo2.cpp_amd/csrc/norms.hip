@@ -110,6 +110,21 @@ __device__ __forceinline__ void store4x2_row(float * p0, float * p1, const float
     if (in1) __builtin_nontemporal_store(f32x4{v[4], v[5], v[6], v[7]}, reinterpret_cast<f32x4 *>(p1));
 }
 
+// Sum in double of one group's 8 values (kSquare: of their F32 squares) as a
+// pairwise tree, 0 for a group past the row.
+template <bool kSquare>
+__device__ __forceinline__ double group_sum8(const float (&h)[kVec], bool in) {
+    double t[kVec];
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) t[k] = static_cast<double>(kSquare ? h[k] * h[k] : h[k]);
+#pragma unroll
+    for (int w = kVec / 2; w >= 1; w /= 2) {
+#pragma unroll
+        for (int k = 0; k < w; ++k) t[k] = t[2 * k] + t[2 * k + 1];
+    }
+    return in ? t[0] : 0.0;
+}
+
 // Sum in double of this lane's values (kSquare: of their F32 squares) over
 // the groups in range, as a pairwise tree: the dependent chain is a few adds
 // long instead of one per element. Any order differs from the CPU's
@@ -236,18 +251,26 @@ __global__ __launch_bounds__(64 * W * R) void norm_kernel_wg(const T * x, const 
             if constexpr (kLayer) load4x2(b + off[j], b + off2[j], bv[j]);
         }
     }
+    // F16 rows: x and delta of group j requested together, so that group j
+    // is complete while later groups are still in flight (its residual,
+    // widening and partial sum run then, below)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        if constexpr (kF16) xw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr + off[j]));
-        else load4x2_row(xr + off[j], xr + off2[j], xb[j]);
-    }
-    if constexpr (kDelta) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            if constexpr (kF16) dw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(dr + off[j]));
-            else load4x2_row(dr + off[j], dr + off2[j], db[j]);
+        if constexpr (kF16) {
+            xw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr + off[j]));
+            if constexpr (kDelta) dw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(dr + off[j]));
+        } else {
+            load4x2_row(xr + off[j], xr + off2[j], xb[j]);
         }
     }
+    if constexpr (kDelta && !kF16) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) load4x2_row(dr + off[j], dr + off2[j], db[j]);
+    }
+    // every load is issued before any loaded value is used (the scheduler
+    // would otherwise start converting the first parameters, and wait for
+    // them, before requesting the row)
+    __builtin_amdgcn_sched_barrier(0);
     // The parameters (cached, first to arrive) are converted while the row is
     // in flight, and no load is waited for after the residual store below.
 #pragma unroll
@@ -255,13 +278,27 @@ __global__ __launch_bounds__(64 * W * R) void norm_kernel_wg(const T * x, const 
         consume_now(wv[j]);
         if constexpr (kLayer) consume_now(bv[j]);
     }
-    if constexpr (kDelta) {
+    // Residual, widening and the first pass's per-group sums, group by group
+    // in the order the loads were requested (F16: each group as soon as its
+    // x and delta are in).
+    double gsum[NV];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            if constexpr (kF16) {
+    for (int j = 0; j < NV; ++j) {
+        if constexpr (kF16) {
+            if constexpr (kDelta) {
 #pragma unroll
                 for (int i = 0; i < kVec / 2; ++i) xw[j][i] = add_f16x2(xw[j][i], dw[j][i]);
-            } else {
+            }
+#pragma unroll
+            for (int k = 0; k < kVec; ++k) h[j][k] = h2f(static_cast<uint16_t>(xw[j][k / 2] >> (16 * (k & 1))));
+            gsum[j] = group_sum8<!kLayer>(h[j], in[j]);
+            // group j's work stays ahead of the wait for group j + 1: its sum
+            // is pinned here (an empty asm with no memory clobber) and the
+            // scheduler may not move group j + 1 above this point
+            asm volatile("" : "+v"(gsum[j]));
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            if constexpr (kDelta) {
 #pragma unroll
                 for (int k = 0; k < kVec; ++k) xb[j][k] = xb[j][k] + db[j][k];
             }
@@ -269,22 +306,22 @@ __global__ __launch_bounds__(64 * W * R) void norm_kernel_wg(const T * x, const 
     }
     // The whole row is in registers before the residual store. A second F32
     // piece past the row holds no value; an F16 group past the row is left out
-    // by the lane sums.
+    // of the sums.
     if constexpr (kF16) {
         consume_now(xw);
     } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j) consume_now(xb[j]);
-    }
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
+        for (int j = 0; j < NV; ++j) {
 #pragma unroll
-        for (int k = 0; k < kVec; ++k) {
-            if constexpr (kF16) h[j][k] = h2f(static_cast<uint16_t>(xw[j][k / 2] >> (16 * (k & 1))));
-            else h[j][k] = k < 4 || in2[j] ? xb[j][k] : 0.0f;
+            for (int k = 0; k < kVec; ++k) h[j][k] = k < 4 || in2[j] ? xb[j][k] : 0.0f;
+            gsum[j] = group_sum8<!kLayer>(h[j], in[j]);
         }
     }
-    double acc = lane_sum<NV, !kLayer>(h, in);
+    double acc = gsum[0];
+#pragma unroll
+    for (int j = 1; j < NV; ++j) acc += gsum[j];
     // The residual is stored once every load has been consumed: stores share
     // the load counter on this GPU, so a later wait for a load would also wait
     // for these stores.
