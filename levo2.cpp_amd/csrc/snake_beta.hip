@@ -69,8 +69,12 @@ __global__ __launch_bounds__(kThreads) void snake_beta_vec(
     const uint32_t last = min(first + tile, total4) - 1;
     const uint32_t c0 = div_of(first, div_t4);
     const uint32_t c1 = div_of(last, div_t4);
-    load_tile_params(params, alpha_log, beta_log, c0, c1 - c0 + 1);
 
+    // Four vectors per thread (the mid-size tensors): x is requested first
+    // and the parameter set-up overlaps its loads (128 x 48000: 9.87 -> 9.44
+    // us); two (the largest): the parameters first, which measured 0.7%
+    // faster there.
+    if constexpr (VPT < 4) load_tile_params(params, alpha_log, beta_log, c0, c1 - c0 + 1);
     f32x4 v[VPT];
     uint32_t ch[VPT];
     uint32_t t4[VPT];
@@ -83,6 +87,10 @@ __global__ __launch_bounds__(kThreads) void snake_beta_vec(
             v[j] = __builtin_nontemporal_load(
                 reinterpret_cast<const f32x4 *>(x + static_cast<int64_t>(ch[j]) * x_stride) + t4[j]);
         }
+    }
+    if constexpr (VPT >= 4) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile_params(params, alpha_log, beta_log, c0, c1 - c0 + 1);
     }
     __syncthreads();
 #pragma unroll
