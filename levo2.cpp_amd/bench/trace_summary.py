@@ -47,6 +47,11 @@ import sys
 from collections import defaultdict
 
 
+N_SIMDS = 256 * 4     # MI355X: 256 CUs of 4 SIMDs
+CLOCK_MHZ = 2400.0    # engine clock (cycles per microsecond)
+N_SE = 32             # shader engines (8 XCDs of 4) that SQ_BUSY_CYCLES is summed over
+
+
 def short_name(name: str) -> str | None:
     if "levo_hip::" in name or "stream_kernel" in name:
         n = re.sub(r"^void ", "", name)
@@ -255,17 +260,28 @@ def issue(sq_csv: str, probe_log: str) -> list[str]:
     if order is None or len(ids) != len(order):
         raise SystemExit(f"launch counts differ: order {None if order is None else len(order)}, counted {len(ids)}")
     rows = ["| launch | kernel | waves | VALU / wave | SALU / wave | VMEM rd / wave | LDS / wave | "
-            "wave lifetime (cycles) | VALU-active share of lifetime |",
-            "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+            "wave lifetime (cycles) | VALU-active share of lifetime | VALU busy per SIMD (us) | "
+            "VALU share of SQ-busy cycles |",
+            "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
     for (name, _), did in zip(order, ids):
         c = per[did]
         waves = c.get("SQ_WAVES", 0.0) or 1.0
         life = c.get("SQ_WAVE_CYCLES", 0.0) / waves
         act = c.get("SQ_ACTIVE_INST_VALU", 0.0) / max(c.get("SQ_WAVE_CYCLES", 0.0), 1.0)
+        # the launch's VALU issue cycles (4-cycle units) spread over the
+        # GPU's SIMDs, at the 2.4 GHz engine clock: the shortest time the
+        # launch's VALU work can take
+        busy_us = c.get("SQ_ACTIVE_INST_VALU", 0.0) * 4.0 / N_SIMDS / CLOCK_MHZ
+        # the same VALU cycles per SIMD over the launch's SQ-busy cycles per
+        # shader engine (SQ_BUSY_CYCLES sums the engines): near 1 when every
+        # SIMD issues VALU work for the whole launch
+        se_busy = c.get("SQ_BUSY_CYCLES", 0.0) / N_SE
+        share = c.get("SQ_ACTIVE_INST_VALU", 0.0) * 4.0 / N_SIMDS / se_busy if se_busy > 0 else 0.0
         kname = short_name(names[did]) or names[did].split("(")[0].strip()
         rows.append(f"| {name} | `{kname}` | {int(waves):,} | {c.get('SQ_INSTS_VALU', 0) / waves:.1f} | "
                     f"{c.get('SQ_INSTS_SALU', 0) / waves:.1f} | {c.get('SQ_INSTS_VMEM_RD', 0) / waves:.1f} | "
-                    f"{c.get('SQ_INSTS_LDS', 0) / waves:.1f} | {life:.0f} | {act:.3f} |")
+                    f"{c.get('SQ_INSTS_LDS', 0) / waves:.1f} | {life:.0f} | {act:.3f} | {busy_us:.2f} | "
+                    f"{share:.2f} |")
     return rows
 
 
