@@ -562,14 +562,14 @@ def bench_sample(torch, hip, binding, head, dev, warmup, steps):
 def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     """Sampling of one LeLM decode step on the device: 1 position x 3 streams
     x 16385 ids, CFG s = 1.5, penalty window 50, a 3-id ignore list, top-k
-    50/1/1, T = 0.9; levo_hip_cfg_sample + levo_hip_sample_draw. Latency-bound
-    (393 KB per step). `device_us`: both launches back to back;
-    `sample_step_us`: the same step through levo_hip_sample_step (rows split
-    into one-wave parts of 512 ids, then one join-and-draw workgroup per row);
-    `roundtrip_us`: median wall time from the first launch until the 3 ids and
-    draw counts are in pinned host memory (Python launch overhead included);
-    `graph_roundtrip_us`: the same with both launches and both copies
-    captured once into a HIP graph and replayed."""
+    50/1/1, T = 0.9, through levo_hip_sample_step (rows split into one-wave
+    parts of 512 ids, then one join-and-draw workgroup per row), the path the
+    C++ Sampler takes. Latency-bound (393 KB per step). `us_per_launch`: the
+    step; `cfg_sample_plus_draw_us`: the same step as levo_hip_cfg_sample +
+    levo_hip_sample_draw back to back; `roundtrip_us`: median wall time from
+    the first launch until the 3 ids and draw counts are in pinned host memory
+    (Python launch overhead included); `graph_roundtrip_us`: the same with the
+    step and both copies captured once into a HIP graph and replayed."""
     S, V, cap = 3, 16385, 64
     n = 64
     g = torch.Generator(device=dev)
@@ -603,16 +603,20 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     d.rows, d.capacity, d.temperature, d.use_sampling = S, cap, 0.9, 1
     d.bits, d.tokens, d.draws = bits.data_ptr(), tokens.data_ptr(), draws.data_ptr()
 
-    def step(i):
+    def two_launches(i):
         hip.cfg_sample(sargs[i])
         hip.sample_draw(d)
 
-    device_ms = time_op(torch, head, step, n, warmup, max(steps, 200))
+    device_ms = time_op(torch, head, two_launches, n, warmup, max(steps, 200))
     sample_ms = time_op(torch, head, lambda i: hip.cfg_sample(sargs[i]), n, warmup, max(steps, 200))
-    # the same step through levo_hip_sample_step (part launch + join-and-draw launch)
+    # the step through levo_hip_sample_step (part launch + join-and-draw launch)
     ws_bytes = hip.sample_step_workspace_bytes(S, V)
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=dev)
-    split_ms = time_op(torch, head, lambda i: hip.sample_step(sargs[i], d, ws, ws_bytes), n, warmup, max(steps, 200))
+
+    def step(i):
+        hip.sample_step(sargs[i], d, ws, ws_bytes)
+
+    split_ms = time_op(torch, head, step, n, warmup, max(steps, 200))
     h_tok = torch.empty(S, dtype=torch.int64, pin_memory=True)
     h_draws = torch.empty(S, dtype=torch.int32, pin_memory=True)
     stream = torch.cuda.current_stream()
@@ -648,10 +652,9 @@ def bench_decode_step(torch, hip, binding, head, dev, warmup, steps):
     except Exception as e:  # graph capture is an extra measurement only
         log(f"decode-step graph capture skipped: {e}")
     per = 2 * S * V * 4 + S * 50 * 8 + 3 * 8 + S * (4 + 4 + 4 + cap * 8 + 8 + 8 + 4)
-    return op_entry(per, device_ms, shape=[1, 2, S, V], dtype="f32 logits / f64 weights", top_k=[50, 1, 1],
-                    temperature=0.9, cfg_sample_us=round(sample_ms * 1e3, 3),
-                    sample_draw_us=round((device_ms - sample_ms) * 1e3, 3),
-                    sample_step_us=round(split_ms * 1e3, 3),
+    return op_entry(per, split_ms, shape=[1, 2, S, V], dtype="f32 logits / f64 weights", top_k=[50, 1, 1],
+                    temperature=0.9, cfg_sample_plus_draw_us=round(device_ms * 1e3, 3),
+                    cfg_sample_us=round(sample_ms * 1e3, 3), sample_draw_us=round((device_ms - sample_ms) * 1e3, 3),
                     roundtrip_us=round(roundtrip_ms * 1e3, 2),
                     graph_roundtrip_us=None if graph_rt_ms is None else round(graph_rt_ms * 1e3, 2),
                     bytes_to_host=S * (8 + 4),

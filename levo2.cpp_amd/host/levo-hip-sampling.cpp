@@ -1,4 +1,5 @@
-// levo::hip sampling surface over levo_hip_cfg_sample / levo_hip_cfg_combine /
+// levo::hip sampling surface over levo_hip_sample_step (levo_hip_cfg_sample /
+// levo_hip_sample_draw for many rows) / levo_hip_cfg_combine /
 // levo_hip_repetition_penalty. Behaviour follows src/levo-sampling.cpp:12-152.
 #include "levo-hip-sampling.h"
 
@@ -36,8 +37,33 @@ struct sample_workspace {
     pinned_buffer<uint64_t> h_bits;
     pinned_buffer<int64_t> h_tokens;
     pinned_buffer<int32_t> h_draws;
+    device_buffer<uint8_t> step;      // levo_hip_sample_step's hand-over workspace
     std::size_t capacity = 64;        // candidate slots per row; grows on demand
 };
+
+// Rows per call that levo_hip_sample_step takes (the decode step's few rows);
+// more rows take levo_hip_cfg_sample and levo_hip_sample_draw.
+constexpr int64_t kStepRows = 4095;
+
+// The candidates of args.rows rows and, with d, their draws: one
+// levo_hip_sample_step call (a part launch and a join-and-draw launch, the
+// same results as levo_hip_cfg_sample followed by levo_hip_sample_draw) when
+// the rows fit it, else those two launches.
+void launch_rows(sample_workspace & ws, const levo_hip_sample_args & args, const levo_hip_draw_args * d,
+                 stream_t stream) {
+    if (args.rows >= 1 && args.rows <= kStepRows) {
+        // < 0 for a vocabulary the kernels do not take: the two launches
+        // below then report it with their own message
+        const int64_t bytes = levo_hip_sample_step_workspace_bytes(args.rows, args.vocab);
+        if (bytes >= 0) {
+            ws.step.reserve_discard(static_cast<std::size_t>(bytes));
+            check_status(levo_hip_sample_step(&args, d, ws.step.data(), bytes, stream));
+            return;
+        }
+    }
+    check_status(levo_hip_cfg_sample(&args, stream));
+    if (d) check_status(levo_hip_sample_draw(d, stream));
+}
 
 int64_t pick_candidate(const int32_t * ids, const float * values, std::size_t n, int32_t best, float temperature,
                        uint64_t raw) {
@@ -131,9 +157,9 @@ int64_t recheck_row(sample_workspace & ws, std::size_t r, std::size_t cap, float
 
 // The ids sample_top_k_counted returns (src/levo-sampling.cpp:75-116) for
 // args.rows consecutive rows, in row order as sample_streams takes them
-// (:135-150). One levo_hip_cfg_sample launch; for sampled rows a
-// levo_hip_sample_draw launch fed with the engine's next raw values (read
-// from a copy, so nothing is consumed yet). Only the ids and the draw counts
+// (:135-150). The candidates and, for sampled rows, the draws fed with the
+// engine's next raw values (read from a copy, so nothing is consumed yet)
+// come from launch_rows. Only the ids and the draw counts
 // come back; the engine then advances by exactly the values the reference's
 // rows would have consumed, also when a NaN row ends the batch.
 std::vector<int64_t> sample_rows(sample_workspace & ws, levo_hip_sample_args args, bool greedy, float temperature,
@@ -153,7 +179,7 @@ std::vector<int64_t> sample_rows(sample_workspace & ws, levo_hip_sample_args arg
         args.cand_logits = nullptr;
         args.row_max = nullptr;
         args.capacity = 1;
-        check_status(levo_hip_cfg_sample(&args, stream));
+        launch_rows(ws, args, nullptr, stream);
         ws.best.download(ws.h_best.data(), rows, stream);
         synchronize(stream);
         for (std::size_t r = 0; r < rows; ++r) {
@@ -183,7 +209,6 @@ std::vector<int64_t> sample_rows(sample_workspace & ws, levo_hip_sample_args arg
         args.cand_logits = ws.cand_logits.data();
         args.row_max = ws.row_max.data();
         args.capacity = static_cast<int32_t>(cap);
-        check_status(levo_hip_cfg_sample(&args, stream));
         levo_hip_draw_args d;
         std::memset(&d, 0, sizeof(d));
         d.best = ws.best.data();
@@ -198,7 +223,7 @@ std::vector<int64_t> sample_rows(sample_workspace & ws, levo_hip_sample_args arg
         d.bits = ws.bits.data();
         d.tokens = ws.tokens.data();
         d.draws = ws.draws.data();
-        check_status(levo_hip_sample_draw(&d, stream));
+        launch_rows(ws, args, &d, stream);
         ws.tokens.download(ws.h_tokens.data(), rows, stream);
         ws.draws.download(ws.h_draws.data(), rows, stream);
         synchronize(stream);
