@@ -172,6 +172,22 @@ def test_shapes_match_two_launches(hip, binding, dev, oracle, V, pitch):
     check_rows(got, oracle.apply_cfg(cond, uncond, 1.5), [50, 1, 2, 64] * 2, oracle, 0.9)
 
 
+@pytest.mark.parametrize("rows", [9, 24])
+def test_more_rows_than_the_join_draws(hip, binding, dev, oracle, rows):
+    """Past 8 rows the join launch leaves the draw to a launch of its own (the
+    C++ Sampler takes this entry point up to 4095 rows): candidates, tokens
+    and draw counts equal the two-launch path's and the oracle's."""
+    V = 16385
+    cond = _f16_logits(oracle, rows, V, 2400 + rows)
+    uncond = _f16_logits(oracle, rows, V, 2500 + rows)
+    c = Case(binding, dev, cond, uncond, top_k=[50, 1, 1], n_streams=3)
+    bits = peek_bits(oracle, 60 + rows, 0, rows)
+    want = c.two_launch(hip, bits)
+    got = c.step(hip, bits=bits)
+    same_outputs(got, want, c, draws=True)
+    check_rows(got, oracle.apply_cfg(cond, uncond, 1.5), [50, 1, 1] * (rows // 3), oracle, 0.9)
+
+
 @pytest.mark.parametrize("k", [1, 2, 50, 100, 300, 512, 513, 0, 16383, 16384])
 def test_ties_and_k(hip, binding, dev, oracle, k):
     """Ties at the maximum and at the k-th value, +-0, a constant row (more
