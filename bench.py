@@ -1267,6 +1267,29 @@ def traffic_probe(torch, hip, binding, dev) -> None:
         hip.quantize_rows(qt, wq, 1, Cc, Cc, qk, R, Cc)
         order.append((f"{name}_quantize_f16", 2 * R * Cc + qk.numel()))
         del qk
+    # decode mat-vecs at LeLM's ffn_down (1536 x 8960), two activation columns,
+    # with their weight and activation quantizations
+    Rw, Kw, NV = 1536, 8960, 2
+    wf = (torch.randn((Rw, Kw), generator=g, device=dev) * 0.02).half()
+    xf = torch.randn((NV, Kw), generator=g, device=dev)
+    yv = torch.empty((NV, Rw), device=dev)
+    wq8 = torch.empty(Rw * Kw // 32 * 34, dtype=torch.uint8, device=dev)
+    hip.quantize_rows(8, wf, 1, Kw, Kw, wq8, Rw, Kw)
+    order.append(("prep_q8_0_weights", 2 * Rw * Kw + wq8.numel()))
+    xq8 = torch.empty(NV * Kw // 32 * 34, dtype=torch.uint8, device=dev)
+    hip.quantize_chunk(8, xf, xq8, 0, NV, Kw)
+    order.append(("prep_q8_0_activations", 4 * NV * Kw + xq8.numel()))
+    hip.mul_mat_q8_0(wq8, xq8, yv, Rw, Rw, Kw, NV)
+    order.append(("mul_mat_q8_0_ffn_down_1536x8960", wq8.numel() + xq8.numel() + 4 * NV * Rw))
+    wq4k = torch.empty(Rw * Kw // 256 * 144, dtype=torch.uint8, device=dev)
+    hip.quantize_rows(12, wf, 1, Kw, Kw, wq4k, Rw, Kw)
+    order.append(("prep_q4_K_weights", 2 * Rw * Kw + wq4k.numel()))
+    xq8k = torch.empty(NV * (Kw // 256) * 292, dtype=torch.uint8, device=dev)
+    hip.quantize_q8_K(xf, xq8k, NV * Kw)
+    order.append(("prep_q8_K_activations", 4 * NV * Kw + xq8k.numel()))
+    hip.mul_mat_kquant(12, wq4k, xq8k, yv, Rw, Rw, Kw, NV)
+    order.append(("mul_mat_q4_K_ffn_down_1536x8960", wq4k.numel() + xq8k.numel() + 4 * NV * Rw))
+    del wf, xf, yv, wq8, xq8, wq4k, xq8k
     P, S, V = 750, 3, 16384
     c = torch.randn((P * S, V), generator=g, device=dev) * 3
     u = torch.randn((P * S, V), generator=g, device=dev) * 3
