@@ -7,6 +7,7 @@
 #include "levo-hip-flow-renderer.h"
 
 #include <cmath>
+#include <cstring>
 #include <limits>
 #include <string>
 
@@ -108,6 +109,61 @@ void save(euler_resume_state * checkpoint, std::size_t completed, const float * 
     checkpoint->completed_steps = completed;
 }
 
+// The steps [first, steps) of a solve without checkpoints, with one
+// synchronization per step. After step s's update the next step's prefix
+// interpolation and the copy of its state to pinned memory are queued behind
+// it, with the copy of s's finiteness flags; the synchronization at the top
+// of step s + 1 then covers all of them, and the host checks s's flags, calls
+// progress and the cancellation poll in the reference's order before it
+// hands the state to the velocity callback. A cancellation or a non-finite
+// step throws before any further callback, as in the reference; the queued
+// work only touches this solve's own buffers.
+void pipelined_steps(const euler_input & input, std::size_t steps, std::size_t first, float dt,
+                     const velocity_callback & velocity, const euler_progress_callback & progress,
+                     const cancellation_callback & cancelled, device_buffer<float> & state,
+                     const device_buffer<float> & noise, const device_buffer<float> & context,
+                     device_buffer<float> & vel, std::vector<float> & host_state, stream_t stream) {
+    const std::size_t n = host_state.size();
+    const std::size_t prefix = input.incontext_frames * input.latent_dim;
+    pinned_buffer<float> stage(n), vstage(n);
+    device_buffer<int32_t> dflags(2);  // the finiteness flags of even and odd steps
+    pinned_buffer<int32_t> hflags(2);
+    const auto queue_state = [&](std::size_t step) {
+        const float time = static_cast<float>(step) * dt;
+        interpolate_prefix(state.data(), noise.data(), context.data(), prefix, time, input.sigma_min, stream);
+        check_hip(hipMemcpyAsync(stage.data(), state.data(), n * sizeof(float), hipMemcpyDeviceToHost, stream),
+                  "device-to-host copy");
+    };
+    const auto check_step = [&](std::size_t step) {
+        const int32_t f = hflags[step & 1];
+        if (f & LEVO_HIP_NONFINITE_VELOCITY) fail("Euler velocity contains a non-finite value");
+        if (f & LEVO_HIP_NONFINITE_STATE) fail("Euler state contains a non-finite value");
+        if (progress) progress(step + 1U, steps);
+    };
+    queue_state(first);
+    for (std::size_t step = first; step < steps; ++step) {
+        synchronize(stream);
+        if (step > first) check_step(step - 1);
+        if (cancelled && cancelled()) throw operation_cancelled();
+        const float time = static_cast<float>(step) * dt;
+        std::memcpy(host_state.data(), stage.data(), n * sizeof(float));
+        const std::vector<float> current_velocity = velocity(host_state, time);
+        if (current_velocity.size() != n) fail("Euler velocity callback returned an unexpected shape");
+        std::memcpy(vstage.data(), current_velocity.data(), n * sizeof(float));
+        vel.upload(vstage.data(), n, stream);
+        int32_t * flag = dflags.data() + (step & 1);
+        check_hip(hipMemsetAsync(flag, 0, sizeof(int32_t), stream), "flag clear");
+        check_status(levo_hip_flow_cfg_euler_checked(state.data(), vel.data(), nullptr, static_cast<int64_t>(n), 1.0F,
+                                                     dt, flag, stream),
+                     error_kind::runtime_error);
+        check_hip(hipMemcpyAsync(hflags.data() + (step & 1), flag, sizeof(int32_t), hipMemcpyDeviceToHost, stream),
+                  "device-to-host copy");
+        if (step + 1 < steps) queue_state(step + 1);
+    }
+    synchronize(stream);
+    check_step(steps - 1);
+}
+
 } // namespace
 
 std::vector<float> solve_flow_euler(const euler_input & input, std::size_t steps, const velocity_callback & velocity,
@@ -146,6 +202,11 @@ std::vector<float> solve_flow_euler(const euler_input & input, std::size_t steps
 
     const std::size_t prefix = input.incontext_frames * input.latent_dim;
     const float dt = 1.0F / static_cast<float>(steps);
+    if (!checkpoint && completed_steps < steps) {
+        pipelined_steps(input, steps, completed_steps, dt, velocity, progress, cancelled, state, noise, context, vel,
+                        host_state, stream);
+        completed_steps = steps;
+    }
     for (std::size_t step = completed_steps; step < steps; ++step) {
         if (cancelled && cancelled()) throw operation_cancelled();
         const float time = static_cast<float>(step) * dt;
