@@ -668,7 +668,9 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
     layer's decode step as it runs: the 4 activation quantizations
     (levo_hip_quantize_chunk: attention input, attention output, FFN input,
     FFN hidden) and the 7 matrices (q, k, v, o, gate, up, down); then the
-    same work in 5 launches (levo_hip_mul_mat_q8_0_multi)."""
+    same work in 5 launches (levo_hip_mul_mat_q8_0_multi). `*_packed`: the
+    same matrices repacked once at load (levo_hip_repack_q8_0) with the
+    activations as columns (levo_hip_quantize_q8_0_columns)."""
     shapes = {"attn_1536x1536": (1536, 1536), "ffn_up_8960x1536": (8960, 1536),
               "ffn_down_1536x8960": (1536, 8960), "head_16385x1536": (16385, 1536)}
     n_vec = 2
@@ -691,18 +693,39 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
         hip.quantize_chunk(8, x, xb, 0, n_vec, k)
         return x, xb
 
+    def columns(x, k):
+        xc = torch.empty(n_vec * (k // 32) * 36, dtype=torch.uint8, device=dev)
+        hip.quantize_q8_0_columns(x, k, xc, n_vec, k)
+        return xc
+
+    def repacked(w, rows, k):
+        p = torch.empty_like(w)
+        for i in range(w.shape[0]):
+            hip.repack_q8_0(w[i], p[i], rows, k)
+        return p
+
     for name, (rows, k) in shapes.items():
         nbytes = rows * (k // 32) * 34
         per = nbytes + n_vec * (k // 32) * 34 + n_vec * rows * 4
         n = math.ceil(ROTATE_BYTES / nbytes) + 1
         w = mk(rows, k, n)
-        _, xb = quantized(k)
+        x, xb = quantized(k)
         y = torch.empty((n_vec, rows), device=dev)
         ms = time_op(torch, head, lambda i: hip.mul_mat_q8_0(w[i].data_ptr(), xb, y, rows, rows, k, n_vec),
                      n, warmup, max(steps, 50))
         out[name] = op_entry(per, ms, read=per - n_vec * rows * 4, shape=[rows, k], n_vec=n_vec,
                              dtype="q8_0 weights / q8_0 activations")
+        # the same matrix repacked once at load (levo_hip_repack_q8_0), the
+        # activations as columns (levo_hip_quantize_q8_0_columns)
+        p = repacked(w, rows, k)
         del w
+        xc = columns(x, k)
+        per_p = nbytes + xc.numel() + n_vec * rows * 4
+        ms = time_op(torch, head, lambda i: hip.mul_mat_q8_0_packed(p[i].data_ptr(), xc, y, rows, rows, k, n_vec),
+                     n, warmup, max(steps, 50))
+        out[name + "_packed"] = op_entry(per_p, ms, read=per_p - n_vec * rows * 4, shape=[rows, k], n_vec=n_vec,
+                                         dtype="q8_0 weights (packed) / q8_0 activation columns")
+        del p
     layer = [(1536, 1536)] * 4 + [(8960, 1536)] * 2 + [(1536, 8960)]
     layer_bytes = sum(r * (k // 32) * 34 + n_vec * (k // 32) * 34 + n_vec * r * 4 for r, k in layer)
     layer_bytes += 3 * n_vec * 1536 * (4 + 34 / 32) + n_vec * 8960 * (4 + 34 / 32)
@@ -749,6 +772,25 @@ def bench_mul_mat(torch, hip, head, dev, warmup, steps):
     ms = time_op(torch, head, run_layer_multi, n, warmup, max(steps, 20))
     out["layer_5_launches"] = op_entry(layer_bytes, ms, n_vec=n_vec, dtype="q8_0 weights / q8_0 activations",
                                        us_per_token_28_layers=round(28 * ms * 1e3, 1))
+    # the 5-launch layer on packed matrices (repacked once, outside the
+    # timing), ffn_down's input quantized to columns
+    pmats = [[repacked(m.view(1, -1), r, k)[0] for m, (r, k) in zip(mats[i], layer)] for i in range(n)]
+    del mats
+    xc_hid = torch.empty(n_vec * (8960 // 32) * 36, dtype=torch.uint8, device=dev)
+
+    def run_layer_packed(i):
+        hip.mul_mat_q8_0_multi([(pmats[i][j], yq[j], 1536, 1536) for j in range(3)], 1536, n_vec,
+                               x=x_attn, x_pitch=1536, packed=True)
+        hip.mul_mat_q8_0_multi([(pmats[i][3], yq[3], 1536, 1536)], 1536, n_vec, x=x_out, x_pitch=1536, packed=True)
+        hip.mul_mat_q8_0_multi([(pmats[i][4], yf[0], 8960, 8960), (pmats[i][5], yf[1], 8960, 8960)], 1536, n_vec,
+                               x=x_ffn, x_pitch=1536, packed=True)
+        hip.quantize_q8_0_columns(x_hid, 8960, xc_hid, n_vec, 8960)
+        hip.mul_mat_q8_0_packed(pmats[i][6].data_ptr(), xc_hid, ys[1536], 1536, 1536, 8960, n_vec)
+
+    ms = time_op(torch, head, run_layer_packed, n, warmup, max(steps, 20))
+    out["layer_5_launches_packed"] = op_entry(layer_bytes, ms, n_vec=n_vec,
+                                              dtype="q8_0 weights (packed) / q8_0 activation columns",
+                                              us_per_token_28_layers=round(28 * ms * 1e3, 1))
     return out
 
 

@@ -653,6 +653,40 @@ int levo_hip_mul_mat_q8_0_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, 
                                 const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
                                 levo_hip_stream_t stream);
 
+/* A Q8_0 matrix rearranged once, when the model is loaded, for the decode
+ * mat-vec: the same bytes (rows * k/32 * 34) in aligned pieces. Row r takes
+ * bytes [32 k/32 r, 32 k/32 (r + 1)): the first 16 quants of each of its
+ * blocks in block order, then the last 16 of each; the F16 scales follow all
+ * rows, [rows][k/32], at byte 32 k/32 rows. No counterpart in the reference
+ * (ggml keeps block_q8_0 in its buffers; its CPU backend has repacked
+ * buffer types for some formats): the layout lets every lane load whole
+ * blocks with aligned 16-byte loads. blocks and packed are device memory,
+ * 16-byte aligned, not overlapping; k a multiple of 32, k <= 32768. */
+int levo_hip_repack_q8_0(const void * blocks, void * packed, int64_t rows, int64_t k, levo_hip_stream_t stream);
+
+/* Activation columns for the packed mat-vec: x [n_vec][x_pitch] F32 (16-byte
+ * aligned, x_pitch >= k and a multiple of 4) quantized to Q8_0 by
+ * levo_hip_quantize_chunk's block function, stored as the quants of every
+ * column in value order ([n_vec][k] int8) followed by the block scales
+ * widened to F32 ([n_vec][k/32]): n_vec * k / 32 * 36 bytes, 16-byte
+ * aligned. The same numbers as levo_hip_quantize_chunk's blocks, in the form
+ * the mat-vec keeps in LDS. 1 <= n_vec <= 8, k a multiple of 32. */
+int levo_hip_quantize_q8_0_columns(const float * x, int64_t x_pitch, void * columns, int64_t n_vec, int64_t k,
+                                   levo_hip_stream_t stream);
+
+/* levo_hip_mul_mat_q8_0 and levo_hip_mul_mat_q8_0_multi on matrices repacked
+ * by levo_hip_repack_q8_0 (levo_hip_mat_q8_0.weight points at the packed
+ * matrix), with the activations as columns (levo_hip_quantize_q8_0_columns)
+ * where the block-layout entry points take Q8_0 blocks; the multi form also
+ * takes F32 x as levo_hip_mul_mat_q8_0_multi does. Same limits, and y equal
+ * bit for bit to what the block-layout entry points give on the original
+ * blocks and the same activations. */
+int levo_hip_mul_mat_q8_0_packed(const void * packed, const void * x_columns, float * y, int64_t y_pitch,
+                                 int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream);
+int levo_hip_mul_mat_q8_0_packed_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, const void * x_columns,
+                                       const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
+                                       levo_hip_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* K-quants on the decode path (ggml block layouts, QK_K = 256):              */
 /*   block_q4_K {f16 d; f16 dmin; u8 scales[12]; u8 qs[128]}            144 B */

@@ -50,6 +50,11 @@ constexpr int kXChunks = 5;  // activation chunks per thread loaded up front (20
 constexpr int kMaxBlocksPerRow = 1024;
 
 constexpr int kMaxMats = 4;
+// The activations' form: Q8_0 blocks, F32 values quantized in the launch, or
+// columns (levo_hip_quantize_q8_0_columns: quants in value order, then F32 scales).
+constexpr int kXBlocks = 0;
+constexpr int kXF32 = 1;
+constexpr int kXColumns = 2;
 
 struct mm_params {
     const uint8_t * w;    // [rows][nb] weight blocks, 16-byte aligned
@@ -95,6 +100,17 @@ __device__ __forceinline__ float read_block(const uint8_t * stage, int off, uint
     return h2f(*reinterpret_cast<const uint16_t *>(stage + off));
 }
 
+// The dwords of chunk c below xbytes (a multiple of 4), global -> LDS.
+__device__ __forceinline__ void copy_tail_dwords(uint8_t * dst, const uint8_t * src, int64_t xbytes, int c) {
+    const int64_t at = 16 * static_cast<int64_t>(c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (at + 4 * k + 4 <= xbytes) {
+            *reinterpret_cast<uint32_t *>(dst + at + 4 * k) = *reinterpret_cast<const uint32_t *>(src + at + 4 * k);
+        }
+    }
+}
+
 // 16-byte chunk c of the activation blocks (xbytes long); the last, partial
 // chunk is read as half-words so nothing past the buffer is touched.
 __device__ __forceinline__ u32x4 load_x_chunk(const uint8_t * x, int64_t xbytes, int c) {
@@ -130,8 +146,41 @@ __device__ __forceinline__ bool wave_span(const mm_params & p, int64_t grp, int 
     }
 }
 
-template <int LPR, int WPR, bool FUSED>
+// One block's terms for every activation column: sumi by 8 v_dot4 over the
+// block's quant dwords q, then acc[v] += sumi * (d_w * d_x).
+__device__ __forceinline__ void block_terms(const uint32_t (&q)[8], float dw, const uint32_t * xq, const float * dx,
+                                            int nb, int kb, int n_vec, float (&acc)[kMaxVectors]) {
+#pragma unroll
+    for (int v = 0; v < kMaxVectors; ++v) {
+        if (v >= n_vec) break;
+        const u32x4 * xb = reinterpret_cast<const u32x4 *>(xq + (v * nb + kb) * 8);
+        const u32x4 x0 = xb[0];
+        const u32x4 x1 = xb[1];
+        int s = 0;
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[0]), static_cast<int>(x0.x), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[1]), static_cast<int>(x0.y), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[2]), static_cast<int>(x0.z), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[3]), static_cast<int>(x0.w), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[4]), static_cast<int>(x1.x), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[5]), static_cast<int>(x1.y), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[6]), static_cast<int>(x1.z), s, false);
+        s = __builtin_amdgcn_sdot4(static_cast<int>(q[7]), static_cast<int>(x1.w), s, false);
+        acc[v] += static_cast<float>(s) * (dw * dx[v * nb + kb]);
+    }
+}
+
+// XF: the activations' form. PB > 0: the weights in the packed layout
+// (levo_hip_repack_q8_0): lane li of a row group loads blocks
+// kb0 + li + LPR * i (i < PB, the same blocks in the same order as the
+// block-layout path; PB = the span's blocks per lane, rounded up: every
+// geometry gives a lane at most 4) straight into registers: the first 16
+// quants, the last 16 and the F16 scale, each an aligned load; no LDS
+// stage, no realignment. PB = 0: Q8_0 blocks.
+template <int LPR, int WPR, int XF, int PB>
 __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch ml) {
+    constexpr bool FUSED = XF == kXF32;
+    constexpr bool PACKED = PB > 0;
+    constexpr int kPB = PACKED ? PB : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     // this workgroup's matrix, selected among arguments read at fixed
     // offsets (an index into the argument arrays would make the weight
@@ -165,8 +214,9 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
 
     // 1. the activation blocks' first chunks, then this wave's weight loads:
     //    loads complete in issue order, so the activations (a few KiB, from
-    //    L2) are unpacked while the weights are still in flight
-    const int64_t xbytes = static_cast<int64_t>(nvb) * kQ8Bytes;
+    //    L2) are unpacked while the weights are still in flight; columns
+    //    (kXColumns) already have the LDS form and are copied as they are
+    const int64_t xbytes = static_cast<int64_t>(nvb) * (XF == kXColumns ? 36 : kQ8Bytes);
     const int nchunks = static_cast<int>((xbytes + 15) >> 4);
     // FUSED: thread t < nvb quantizes activation block t (column t / nb,
     // block t % nb); other threads read block 0 and drop it
@@ -187,15 +237,52 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
     int64_t row0;
     int nrows, kb0, kb1;
     const bool have = wave_span<LPR, WPR>(p, grp, wave, row0, nrows, kb0, kb1);
+    const int g = lane / LPR;
+    const int li = lane % LPR;
     u32x4 regs[kChunksPerLane];
     const int64_t sb0 = (row0 * p.nb + kb0) * kQ8Bytes;
     const int64_t sb1 = (row0 * p.nb + (WPR > 1 ? kb1 : static_cast<int64_t>(nrows) * p.nb)) * kQ8Bytes;
-    load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
+    u32x4 wlo[kPB], whi[kPB];
+    uint16_t wd[kPB];
+    if constexpr (PACKED) {
+        // unconditional loads (see load_span): a block past the span re-reads
+        // the span's last one, a row group past the last row reads the
+        // wave's first row, an inactive wave reads block 0
+        const int64_t row = !have ? 0 : row0 + (WPR > 1 || g >= nrows ? 0 : g);
+        const int last = have ? kb1 - 1 : 0;
+        const uint8_t * qrow = p.w + row * p.nb * 32;
+        const uint16_t * drow = reinterpret_cast<const uint16_t *>(p.w + p.rows * p.nb * 32) + row * p.nb;
+#pragma unroll
+        for (int i = 0; i < kPB; ++i) {
+            const int kb = !have ? 0 : std::min(kb0 + li + LPR * i, last);
+            wlo[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(qrow + kb * 16));
+            whi[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(qrow + (p.nb + kb) * 16));
+            wd[i] = __builtin_nontemporal_load(drow + kb);
+        }
+    } else {
+        load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
+    }
 
     // 2. activation blocks -> LDS (raw, through the stage area), then
     //    unpacked to aligned quant dwords and F32 scales; or, FUSED,
-    //    quantized from F32 straight into that form
-    if constexpr (FUSED) {
+    //    quantized from F32 straight into that form; or columns copied to it
+    if constexpr (XF == kXColumns) {
+#pragma unroll
+        for (int i = 0; i < kXChunks; ++i) {
+            const int c = static_cast<int>(threadIdx.x) + kThreads * i;
+            if (c >= nchunks) continue;
+            if (16 * static_cast<int64_t>(c) + 16 <= xbytes) reinterpret_cast<u32x4 *>(smem)[c] = xr[i];
+            else copy_tail_dwords(smem, p.x, xbytes, c);
+        }
+        for (int c = threadIdx.x + kThreads * kXChunks; c < nchunks; c += kThreads) {
+            if (16 * static_cast<int64_t>(c) + 16 <= xbytes) {
+                reinterpret_cast<u32x4 *>(smem)[c] = *reinterpret_cast<const u32x4 *>(p.x + 16 * static_cast<int64_t>(c));
+            } else {
+                copy_tail_dwords(smem, p.x, xbytes, c);
+            }
+        }
+        lds_barrier();  // LDS only: the weight loads stay in flight
+    } else if constexpr (FUSED) {
         float xs[32];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -235,35 +322,29 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
     }
 
     // 3. the wave's blocks: lane li of row group g takes kb = kb0 + li + LPR * i
-    const int g = lane / LPR;
-    const int li = lane % LPR;
-    const int lead = static_cast<int>(sb0 & 15);
-    store_span<kChunksPerLane>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
-    wave_lds_fence();
     float acc[kMaxVectors];
 #pragma unroll
     for (int v = 0; v < kMaxVectors; ++v) acc[v] = 0.0f;
-    if (have && g < nrows) {
-        const int row_base = WPR > 1 ? 0 : g * p.nb;  // LDS block index of (row g, kb0)
-        for (int kb = kb0 + li; kb < kb1; kb += LPR) {
-            uint32_t q[8];
-            const float dw = read_block(stage, lead + (row_base + kb - kb0) * kQ8Bytes, q);
+    if constexpr (PACKED) {
+        if (have && g < nrows) {
 #pragma unroll
-            for (int v = 0; v < kMaxVectors; ++v) {
-                if (v >= p.n_vec) break;
-                const u32x4 * xb = reinterpret_cast<const u32x4 *>(xq + (v * p.nb + kb) * 8);
-                const u32x4 x0 = xb[0];
-                const u32x4 x1 = xb[1];
-                int s = 0;
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[0]), static_cast<int>(x0.x), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[1]), static_cast<int>(x0.y), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[2]), static_cast<int>(x0.z), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[3]), static_cast<int>(x0.w), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[4]), static_cast<int>(x1.x), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[5]), static_cast<int>(x1.y), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[6]), static_cast<int>(x1.z), s, false);
-                s = __builtin_amdgcn_sdot4(static_cast<int>(q[7]), static_cast<int>(x1.w), s, false);
-                acc[v] += static_cast<float>(s) * (dw * dx[v * p.nb + kb]);
+            for (int i = 0; i < kPB; ++i) {
+                const int kb = kb0 + li + LPR * i;
+                if (kb >= kb1) break;
+                const uint32_t q[8] = {wlo[i].x, wlo[i].y, wlo[i].z, wlo[i].w, whi[i].x, whi[i].y, whi[i].z, whi[i].w};
+                block_terms(q, h2f(wd[i]), xq, dx, p.nb, kb, p.n_vec, acc);
+            }
+        }
+    } else {
+        const int lead = static_cast<int>(sb0 & 15);
+        store_span<kChunksPerLane>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
+        wave_lds_fence();
+        if (have && g < nrows) {
+            const int row_base = WPR > 1 ? 0 : g * p.nb;  // LDS block index of (row g, kb0)
+            for (int kb = kb0 + li; kb < kb1; kb += LPR) {
+                uint32_t q[8];
+                const float dw = read_block(stage, lead + (row_base + kb - kb0) * kQ8Bytes, q);
+                block_terms(q, dw, xq, dx, p.nb, kb, p.n_vec, acc);
             }
         }
     }
@@ -299,16 +380,25 @@ constexpr int rows_per_workgroup() {
     return WPR > 1 ? kWaves / WPR : kWaves * (64 / LPR);
 }
 
+template <int LPR, int WPR, int PB>
+int launch_packed(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st, const char * what) {
+    if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB><<<blocks, kThreads, lds, st>>>(ml);
+    else mul_mat_q8_0_kernel<LPR, WPR, kXColumns, PB><<<blocks, kThreads, lds, st>>>(ml);
+    return launch_status(what);
+}
+
 template <int LPR, int WPR>
-int launch_mm(mm_launch ml, hipStream_t st, const char * what) {
+int launch_mm(mm_launch ml, bool packed, hipStream_t st, const char * what) {
     constexpr int rows_per_block = rows_per_workgroup<LPR, WPR>();
     mm_params & p = ml.p;
     const int span_blocks = WPR > 1 ? (p.nb + WPR - 1) / WPR : (64 / LPR) * p.nb;
-    p.stage_bytes = (span_blocks * kQ8Bytes + 32 + 15) & ~15;
+    p.stage_bytes = packed ? 0 : (span_blocks * kQ8Bytes + 32 + 15) & ~15;
     const int64_t nvb = static_cast<int64_t>(p.n_vec) * p.nb;
     // The raw activation blocks pass through the stage area before unpacking
-    // (unpacking the last one reads 4 bytes past it), so it holds both.
-    const int64_t stages = std::max<int64_t>(int64_t{kWaves} * p.stage_bytes, (nvb * kQ8Bytes + 16 + 15) & ~int64_t{15});
+    // (unpacking the last one reads 4 bytes past it), so it holds both; the
+    // packed path's activations (columns, or F32) go to their place directly.
+    const int64_t raw = packed ? 0 : (nvb * kQ8Bytes + 16 + 15) & ~int64_t{15};
+    const int64_t stages = std::max<int64_t>(int64_t{kWaves} * p.stage_bytes, raw);
     const size_t lds = ((static_cast<size_t>(nvb) * 36 + kWaves * kMaxVectors * 4 + 15) & ~size_t{15}) +
                        static_cast<size_t>(stages);
     LEVO_REQUIRE(lds <= 64 * 1024, "%s: n_vec * K too large for the workgroup's LDS", what);
@@ -321,8 +411,19 @@ int launch_mm(mm_launch ml, hipStream_t st, const char * what) {
     LEVO_REQUIRE(groups < (int64_t{1} << 31), "%s: too many rows", what);
     if (groups == 0) return LEVO_HIP_OK;
     const uint32_t blocks = static_cast<uint32_t>(groups);
-    if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, true><<<blocks, kThreads, lds, st>>>(ml);
-    else mul_mat_q8_0_kernel<LPR, WPR, false><<<blocks, kThreads, lds, st>>>(ml);
+    if (packed) {
+        // blocks per lane: the span over LPR lanes, 1-4 at 16 lanes per row,
+        // 3-4 for the longer rows (more than 64 blocks per 16 lanes)
+        const int64_t per_lane = ceil_div(WPR > 1 ? (p.nb + WPR - 1) / WPR : p.nb, LPR);
+        if constexpr (LPR == 16) {
+            if (per_lane == 1) return launch_packed<LPR, WPR, 1>(ml, blocks, lds, st, what);
+            if (per_lane == 2) return launch_packed<LPR, WPR, 2>(ml, blocks, lds, st, what);
+        }
+        if (per_lane == 3) return launch_packed<LPR, WPR, 3>(ml, blocks, lds, st, what);
+        return launch_packed<LPR, WPR, 4>(ml, blocks, lds, st, what);
+    }
+    if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, 0><<<blocks, kThreads, lds, st>>>(ml);
+    else mul_mat_q8_0_kernel<LPR, WPR, kXBlocks, 0><<<blocks, kThreads, lds, st>>>(ml);
     return launch_status(what);
 }
 
@@ -331,31 +432,74 @@ int launch_mm(mm_launch ml, hipStream_t st, const char * what) {
 // or in a multi launch with any others (the lanes per row fix the summation
 // order); 32 lanes per row would gain 0.2 us at 1536 x 1536 (4.0 -> 3.8 us)
 // and lose at 8960 rows and more.
-int launch_geometry(const mm_launch & ml, hipStream_t st, const char * what) {
+int launch_geometry(const mm_launch & ml, bool packed, hipStream_t st, const char * what) {
     const int nb = ml.p.nb;
-    if (nb <= 64) return launch_mm<16, 1>(ml, st, what);
-    if (nb <= 128) return launch_mm<32, 1>(ml, st, what);
-    if (nb <= 256) return launch_mm<64, 1>(ml, st, what);
-    if (nb <= 512) return launch_mm<64, 2>(ml, st, what);
-    return launch_mm<64, 4>(ml, st, what);
+    if (nb <= 64) return launch_mm<16, 1>(ml, packed, st, what);
+    if (nb <= 128) return launch_mm<32, 1>(ml, packed, st, what);
+    if (nb <= 256) return launch_mm<64, 1>(ml, packed, st, what);
+    if (nb <= 512) return launch_mm<64, 2>(ml, packed, st, what);
+    return launch_mm<64, 4>(ml, packed, st, what);
 }
 
-}  // namespace
-}  // namespace levo_hip
+// levo_hip_quantize_q8_0_columns: thread t quantizes block t of the n_vec
+// columns (column t / nb, block t % nb) with the block function of
+// levo_hip_quantize_chunk; its quants go to byte 32 t, its scale, widened
+// to F32, to the scale array after all quants.
+__global__ __launch_bounds__(kThreads) void quantize_columns_kernel(const float * __restrict__ x, int64_t x_pitch,
+                                                                    uint8_t * __restrict__ cols, int32_t nvb, int32_t nb) {
+    const int t = static_cast<int>(blockIdx.x) * kThreads + static_cast<int>(threadIdx.x);
+    if (t >= nvb) return;
+    const u32x4 * src = reinterpret_cast<const u32x4 *>(x + (t / nb) * x_pitch + static_cast<int64_t>(t % nb) * 32);
+    float xs[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const u32x4 v = src[i];
+        xs[4 * i] = __uint_as_float(v.x);
+        xs[4 * i + 1] = __uint_as_float(v.y);
+        xs[4 * i + 2] = __uint_as_float(v.z);
+        xs[4 * i + 3] = __uint_as_float(v.w);
+    }
+    uint32_t q[8];
+    const uint16_t d = quantize_q8_0_block(xs, q);
+    u32x4 * dst = reinterpret_cast<u32x4 *>(cols + static_cast<int64_t>(t) * 32);
+    dst[0] = u32x4{q[0], q[1], q[2], q[3]};
+    dst[1] = u32x4{q[4], q[5], q[6], q[7]};
+    reinterpret_cast<float *>(cols + static_cast<int64_t>(nvb) * 32)[t] = h2f(d);
+}
 
-using namespace levo_hip;
+// levo_hip_repack_q8_0: thread t moves block t (17 aligned half-words at
+// byte 34 t) to its row's two quant halves and the scale array.
+__global__ __launch_bounds__(kThreads) void repack_q8_0_kernel(const uint8_t * __restrict__ blocks,
+                                                               uint8_t * __restrict__ packed, int64_t rows, int32_t nb) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (b >= rows * nb) return;
+    const uint16_t * src = reinterpret_cast<const uint16_t *>(blocks + b * kQ8Bytes);
+    uint32_t h[17];
+#pragma unroll
+    for (int i = 0; i < 17; ++i) h[i] = src[i];
+    const int64_t row = b / nb;
+    const int64_t kb = b - row * nb;
+    uint8_t * qrow = packed + row * nb * 32;
+    *reinterpret_cast<u32x4 *>(qrow + kb * 16) =
+        u32x4{h[1] | (h[2] << 16), h[3] | (h[4] << 16), h[5] | (h[6] << 16), h[7] | (h[8] << 16)};
+    *reinterpret_cast<u32x4 *>(qrow + (nb + kb) * 16) =
+        u32x4{h[9] | (h[10] << 16), h[11] | (h[12] << 16), h[13] | (h[14] << 16), h[15] | (h[16] << 16)};
+    reinterpret_cast<uint16_t *>(packed + rows * nb * 32)[b] = static_cast<uint16_t>(h[0]);
+}
 
-extern "C" int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks, float * y, int64_t y_pitch,
-                                     int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream) {
-    LEVO_REQUIRE(rows >= 0 && n_vec >= 0, "mul_mat_q8_0: negative size");
+// packed: the weights from levo_hip_repack_q8_0 and the activations as
+// columns (levo_hip_quantize_q8_0_columns), else both as Q8_0 blocks.
+int mul_mat_one(const void * weight, const void * x_blocks, float * y, int64_t y_pitch, int64_t rows, int64_t k,
+                int64_t n_vec, bool packed, hipStream_t st, const char * what) {
+    LEVO_REQUIRE(rows >= 0 && n_vec >= 0, "%s: negative size", what);
     if (rows == 0 || n_vec == 0) return LEVO_HIP_OK;
-    LEVO_REQUIRE(k > 0 && k % 32 == 0, "mul_mat_q8_0: K must be a positive multiple of 32 (pad the rows)");
-    LEVO_REQUIRE(k / 32 <= kMaxBlocksPerRow, "mul_mat_q8_0: K exceeds %d", kMaxBlocksPerRow * 32);
-    LEVO_REQUIRE(n_vec <= kMaxVectors, "mul_mat_q8_0: at most %d activation columns", kMaxVectors);
-    LEVO_REQUIRE(rows < (int64_t{1} << 31) / 4, "mul_mat_q8_0: too many rows");
-    LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "mul_mat_q8_0: null tensor");
-    LEVO_REQUIRE(aligned16(weight) && aligned16(x_blocks), "mul_mat_q8_0: block buffers must be 16-byte aligned");
-    LEVO_REQUIRE(y_pitch >= rows, "mul_mat_q8_0: y pitch smaller than the row count");
+    LEVO_REQUIRE(k > 0 && k % 32 == 0, "%s: K must be a positive multiple of 32 (pad the rows)", what);
+    LEVO_REQUIRE(k / 32 <= kMaxBlocksPerRow, "%s: K exceeds %d", what, kMaxBlocksPerRow * 32);
+    LEVO_REQUIRE(n_vec <= kMaxVectors, "%s: at most %d activation columns", what, kMaxVectors);
+    LEVO_REQUIRE(rows < (int64_t{1} << 31) / 4, "%s: too many rows", what);
+    LEVO_REQUIRE(weight != nullptr && x_blocks != nullptr && y != nullptr, "%s: null tensor", what);
+    LEVO_REQUIRE(aligned16(weight) && aligned16(x_blocks), "%s: block buffers must be 16-byte aligned", what);
+    LEVO_REQUIRE(y_pitch >= rows, "%s: y pitch smaller than the row count", what);
     mm_launch ml{};
     ml.p.x = static_cast<const uint8_t *>(x_blocks);
     ml.p.nb = static_cast<int32_t>(k / 32);
@@ -365,13 +509,11 @@ extern "C" int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks,
     ml.y[0] = y;
     ml.rows[0] = rows;
     ml.y_pitch[0] = y_pitch;
-    return launch_geometry(ml, as_hip(stream), "levo_hip_mul_mat_q8_0");
+    return launch_geometry(ml, packed, st, what);
 }
 
-extern "C" int levo_hip_mul_mat_q8_0_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, const void * x_blocks,
-                                           const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
-                                           levo_hip_stream_t stream) {
-    const char * what = "mul_mat_q8_0_multi";
+int mul_mat_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, const void * x_blocks, const float * x,
+                  int64_t x_pitch, int64_t k, int64_t n_vec, bool packed, hipStream_t st, const char * what) {
     LEVO_REQUIRE(n_mats >= 1 && n_mats <= kMaxMats, "%s: 1 to %d matrices", what, kMaxMats);
     LEVO_REQUIRE(mats != nullptr, "%s: null matrix list", what);
     LEVO_REQUIRE(n_vec >= 0, "%s: negative size", what);
@@ -410,5 +552,71 @@ extern "C" int levo_hip_mul_mat_q8_0_multi(const levo_hip_mat_q8_0 * mats, int32
         ++ml.n_mats;
     }
     if (ml.n_mats == 0 || n_vec == 0) return LEVO_HIP_OK;
-    return launch_geometry(ml, as_hip(stream), what);
+    return launch_geometry(ml, packed, st, what);
+}
+
+}  // namespace
+}  // namespace levo_hip
+
+using namespace levo_hip;
+
+extern "C" int levo_hip_mul_mat_q8_0(const void * weight, const void * x_blocks, float * y, int64_t y_pitch,
+                                     int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream) {
+    return mul_mat_one(weight, x_blocks, y, y_pitch, rows, k, n_vec, false, as_hip(stream), "mul_mat_q8_0");
+}
+
+extern "C" int levo_hip_mul_mat_q8_0_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats, const void * x_blocks,
+                                           const float * x, int64_t x_pitch, int64_t k, int64_t n_vec,
+                                           levo_hip_stream_t stream) {
+    return mul_mat_multi(mats, n_mats, x_blocks, x, x_pitch, k, n_vec, false, as_hip(stream), "mul_mat_q8_0_multi");
+}
+
+extern "C" int levo_hip_repack_q8_0(const void * blocks, void * packed, int64_t rows, int64_t k,
+                                    levo_hip_stream_t stream) {
+    const char * what = "repack_q8_0";
+    LEVO_REQUIRE(rows >= 0, "%s: negative size", what);
+    if (rows == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(k > 0 && k % 32 == 0, "%s: K must be a positive multiple of 32 (pad the rows)", what);
+    LEVO_REQUIRE(k / 32 <= kMaxBlocksPerRow, "%s: K exceeds %d", what, kMaxBlocksPerRow * 32);
+    LEVO_REQUIRE(rows * (k / 32) < (int64_t{1} << 31), "%s: too many blocks", what);
+    LEVO_REQUIRE(blocks != nullptr && packed != nullptr, "%s: null tensor", what);
+    LEVO_REQUIRE(aligned16(blocks) && aligned16(packed), "%s: buffers must be 16-byte aligned", what);
+    const int64_t bytes = rows * (k / 32) * kQ8Bytes;
+    const uint8_t * a = static_cast<const uint8_t *>(blocks);
+    const uint8_t * b = static_cast<const uint8_t *>(packed);
+    LEVO_REQUIRE(a + bytes <= b || b + bytes <= a, "%s: the packed matrix must not overlap the blocks", what);
+    const int64_t n = rows * (k / 32);
+    repack_q8_0_kernel<<<static_cast<uint32_t>(ceil_div(n, kThreads)), kThreads, 0, as_hip(stream)>>>(
+        a, static_cast<uint8_t *>(packed), rows, static_cast<int32_t>(k / 32));
+    return launch_status(what);
+}
+
+extern "C" int levo_hip_quantize_q8_0_columns(const float * x, int64_t x_pitch, void * columns, int64_t n_vec,
+                                              int64_t k, levo_hip_stream_t stream) {
+    const char * what = "quantize_q8_0_columns";
+    LEVO_REQUIRE(n_vec >= 0, "%s: negative size", what);
+    if (n_vec == 0) return LEVO_HIP_OK;
+    LEVO_REQUIRE(k > 0 && k % 32 == 0, "%s: K must be a positive multiple of 32 (pad the rows)", what);
+    LEVO_REQUIRE(k / 32 <= kMaxBlocksPerRow, "%s: K exceeds %d", what, kMaxBlocksPerRow * 32);
+    LEVO_REQUIRE(n_vec <= kMaxVectors, "%s: at most %d activation columns", what, kMaxVectors);
+    LEVO_REQUIRE(x != nullptr && columns != nullptr, "%s: null tensor", what);
+    LEVO_REQUIRE(aligned16(x) && x_pitch >= k && x_pitch % 4 == 0,
+                 "%s: F32 activations need 16-byte aligned rows of at least K values", what);
+    LEVO_REQUIRE(aligned16(columns), "%s: the columns buffer must be 16-byte aligned", what);
+    const int32_t nvb = static_cast<int32_t>(n_vec * (k / 32));
+    quantize_columns_kernel<<<static_cast<uint32_t>(ceil_div(nvb, kThreads)), kThreads, 0, as_hip(stream)>>>(
+        x, x_pitch, static_cast<uint8_t *>(columns), nvb, static_cast<int32_t>(k / 32));
+    return launch_status(what);
+}
+
+extern "C" int levo_hip_mul_mat_q8_0_packed(const void * packed, const void * x_blocks, float * y, int64_t y_pitch,
+                                            int64_t rows, int64_t k, int64_t n_vec, levo_hip_stream_t stream) {
+    return mul_mat_one(packed, x_blocks, y, y_pitch, rows, k, n_vec, true, as_hip(stream), "mul_mat_q8_0_packed");
+}
+
+extern "C" int levo_hip_mul_mat_q8_0_packed_multi(const levo_hip_mat_q8_0 * mats, int32_t n_mats,
+                                                  const void * x_blocks, const float * x, int64_t x_pitch, int64_t k,
+                                                  int64_t n_vec, levo_hip_stream_t stream) {
+    return mul_mat_multi(mats, n_mats, x_blocks, x, x_pitch, k, n_vec, true, as_hip(stream),
+                         "mul_mat_q8_0_packed_multi");
 }

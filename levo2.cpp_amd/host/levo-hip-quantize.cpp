@@ -47,6 +47,35 @@ void mul_mat_q8_0_shared_input(const q8_0_matrix * mats, int n_mats, const float
     check_status(levo_hip_mul_mat_q8_0_multi(m, n_mats, nullptr, x, k, k, n_vec, stream));
 }
 
+void repack_q8_0(const void * weight, void * packed, int64_t rows, int64_t k, stream_t stream) {
+    check_status(levo_hip_repack_q8_0(weight, packed, rows, k, stream));
+}
+
+std::size_t q8_0_columns_size(int64_t n_vec, int64_t k) {
+    if (n_vec < 0 || k < 0 || k % 32 != 0) throw std::invalid_argument("q8_0_columns_size: bad size");
+    return static_cast<std::size_t>(n_vec) * static_cast<std::size_t>(k / 32) * 36;
+}
+
+void mul_mat_q8_0_packed(const void * packed, const float * x, void * x_columns, float * y, int64_t rows, int64_t k,
+                         int64_t n_vec, stream_t stream) {
+    if (rows == 0 || n_vec == 0) return;
+    check_status(levo_hip_quantize_q8_0_columns(x, k, x_columns, n_vec, k, stream));
+    mul_mat_q8_0_packed_quantized(packed, x_columns, y, rows, k, n_vec, stream);
+}
+
+void mul_mat_q8_0_packed_quantized(const void * packed, const void * x_columns, float * y, int64_t rows, int64_t k,
+                                   int64_t n_vec, stream_t stream) {
+    check_status(levo_hip_mul_mat_q8_0_packed(packed, x_columns, y, rows, rows, k, n_vec, stream));
+}
+
+void mul_mat_q8_0_packed_shared_input(const q8_0_matrix * mats, int n_mats, const float * x, int64_t k,
+                                      int64_t n_vec, stream_t stream) {
+    levo_hip_mat_q8_0 m[4] = {};
+    const int n = n_mats < 0 ? 0 : n_mats;
+    for (int i = 0; i < n && i < 4; ++i) m[i] = levo_hip_mat_q8_0{mats[i].weight, mats[i].y, mats[i].rows, mats[i].rows};
+    check_status(levo_hip_mul_mat_q8_0_packed_multi(m, n_mats, nullptr, x, k, k, n_vec, stream));
+}
+
 void mul_mat_kquant(levo_hip_type type, const void * weight, const float * x, void * x_blocks, float * y,
                     int64_t rows, int64_t k, int64_t n_vec, stream_t stream) {
     if (rows == 0 || n_vec == 0) return;

@@ -225,6 +225,10 @@ class LevoHip:
             "levo_hip_flow_denormalize": (ctypes.c_int, [_P, _P, _P, _P, _I64, _I64, _P, _P]),
             "levo_hip_mul_mat_q8_0": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
             "levo_hip_mul_mat_q8_0_multi": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I64, _I64, _P]),
+            "levo_hip_repack_q8_0": (ctypes.c_int, [_P, _P, _I64, _I64, _P]),
+            "levo_hip_quantize_q8_0_columns": (ctypes.c_int, [_P, _I64, _P, _I64, _I64, _P]),
+            "levo_hip_mul_mat_q8_0_packed": (ctypes.c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+            "levo_hip_mul_mat_q8_0_packed_multi": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I64, _I64, _P]),
             "levo_hip_quantize_q8_K": (ctypes.c_int, [_P, _P, _I64, _P]),
             "levo_hip_mul_mat_kquant": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
             "levo_hip_mul_mat_kquant_multi": (ctypes.c_int, [_P, _I32, _P, _P, _I64, _I64, _I64, _P]),
@@ -413,14 +417,27 @@ class LevoHip:
         return self._check(self.lib.levo_hip_mul_mat_q8_0(_addr(weight), _addr(x_blocks), _addr(y), y_pitch,
                                                           rows, k, n_vec, _stream(stream)))
 
-    def mul_mat_q8_0_multi(self, mats, k, n_vec, x_blocks=None, x=None, x_pitch=0, stream=None):
+    def mul_mat_q8_0_multi(self, mats, k, n_vec, x_blocks=None, x=None, x_pitch=0, stream=None, packed=False):
         """mats: (weight, y, y_pitch, rows) tuples sharing the activations,
-        given as Q8_0 blocks (x_blocks) or as F32 rows (x, x_pitch)."""
+        given as Q8_0 blocks (x_blocks) or as F32 rows (x, x_pitch); packed:
+        the weights come from repack_q8_0 and x_blocks holds columns
+        (quantize_q8_0_columns)."""
         arr = (MatQ8_0 * max(len(mats), 1))()
         for i, (w, y, y_pitch, rows) in enumerate(mats):
             arr[i] = MatQ8_0(_addr(w), _addr(y), y_pitch, rows)
-        return self._check(self.lib.levo_hip_mul_mat_q8_0_multi(arr, len(mats), _addr(x_blocks), _addr(x), x_pitch,
-                                                                k, n_vec, _stream(stream)))
+        fn = self.lib.levo_hip_mul_mat_q8_0_packed_multi if packed else self.lib.levo_hip_mul_mat_q8_0_multi
+        return self._check(fn(arr, len(mats), _addr(x_blocks), _addr(x), x_pitch, k, n_vec, _stream(stream)))
+
+    def repack_q8_0(self, blocks, packed, rows, k, stream=None):
+        return self._check(self.lib.levo_hip_repack_q8_0(_addr(blocks), _addr(packed), rows, k, _stream(stream)))
+
+    def quantize_q8_0_columns(self, x, x_pitch, columns, n_vec, k, stream=None):
+        return self._check(self.lib.levo_hip_quantize_q8_0_columns(_addr(x), x_pitch, _addr(columns), n_vec, k,
+                                                                   _stream(stream)))
+
+    def mul_mat_q8_0_packed(self, packed, x_columns, y, y_pitch, rows, k, n_vec, stream=None):
+        return self._check(self.lib.levo_hip_mul_mat_q8_0_packed(_addr(packed), _addr(x_columns), _addr(y), y_pitch,
+                                                                 rows, k, n_vec, _stream(stream)))
 
     def quantize_q8_K(self, x, y, k, stream=None):
         return self._check(self.lib.levo_hip_quantize_q8_K(_addr(x), _addr(y), k, _stream(stream)))

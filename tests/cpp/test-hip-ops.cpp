@@ -359,6 +359,20 @@ void mul_mat_surface() {
         const q8_0_matrix big[1] = {{dw.data(), dy.data(), rows}};
         mul_mat_q8_0_shared_input(big, 1, dx.data(), k, n_vec);
     });
+
+    // the packed matrices: the same y, bit for bit
+    device_vec<uint8_t> dp(wb.size()), dxc(q8_0_columns_size(n_vec, k));
+    device_vec<float> dyp(static_cast<std::size_t>(n_vec * rows));
+    repack_q8_0(dw.data(), dp.data(), rows, k);
+    mul_mat_q8_0_packed(dp.data(), dx.data(), dxc.data(), dyp.data(), rows, k, n_vec);
+    CHECK(bit_equal(dyp.get().data(), got.data(), got.size()));
+    device_vec<uint8_t> dip(iwb.size());
+    device_vec<float> dyp40(static_cast<std::size_t>(2 * ir));
+    repack_q8_0(diw.data(), dip.data(), ir, ik);
+    const q8_0_matrix pmats[1] = {{dip.data(), dyp40.data(), ir}};
+    mul_mat_q8_0_packed_shared_input(pmats, 1, dix.data(), ik, 2);
+    CHECK(bit_equal(dyp40.get().data(), igot.data(), igot.size()));
+    expect_throw<std::invalid_argument>("must not overlap", [&] { repack_q8_0(dw.data(), dw.data(), rows, k); });
 }
 
 // K-quant decode path: padded_input_columns for 256-value blocks
