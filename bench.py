@@ -1323,6 +1323,15 @@ def traffic_probe(torch, hip, binding, dev) -> None:
     order.append(("prep_q8_0_activations", 4 * NV * Kw + xq8.numel()))
     hip.mul_mat_q8_0(wq8, xq8, yv, Rw, Rw, Kw, NV)
     order.append(("mul_mat_q8_0_ffn_down_1536x8960", wq8.numel() + xq8.numel() + 4 * NV * Rw))
+    wp8 = torch.empty_like(wq8)
+    hip.repack_q8_0(wq8, wp8, Rw, Kw)
+    order.append(("repack_q8_0_weights", 2 * wq8.numel()))
+    xc8 = torch.empty(NV * Kw // 32 * 36, dtype=torch.uint8, device=dev)
+    hip.quantize_q8_0_columns(xf, Kw, xc8, NV, Kw)
+    order.append(("prep_q8_0_columns", 4 * NV * Kw + xc8.numel()))
+    hip.mul_mat_q8_0_packed(wp8, xc8, yv, Rw, Rw, Kw, NV)
+    order.append(("mul_mat_q8_0_packed_ffn_down_1536x8960", wp8.numel() + xc8.numel() + 4 * NV * Rw))
+    del wp8, xc8
     wq4k = torch.empty(Rw * Kw // 256 * 144, dtype=torch.uint8, device=dev)
     hip.quantize_rows(12, wf, 1, Kw, Kw, wq4k, Rw, Kw)
     order.append(("prep_q4_K_weights", 2 * Rw * Kw + wq4k.numel()))
