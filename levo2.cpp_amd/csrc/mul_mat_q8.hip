@@ -234,6 +234,10 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
             xr[i] = *reinterpret_cast<const u32x4 *>(p.x + (whole ? 16 * static_cast<int64_t>(c) : 0));
         }
     }
+    // the activation requests go out before any weight request: loads
+    // complete in issue order, so a weight load scheduled among them would
+    // make the staging wait for HBM
+    __builtin_amdgcn_sched_barrier(0);
     int64_t row0;
     int nrows, kb0, kb1;
     const bool have = wave_span<LPR, WPR>(p, grp, wave, row0, nrows, kb0, kb1);
