@@ -27,10 +27,11 @@
 // levo_hip_mul_mat_q8_0_multi runs up to four matrices that read the same
 // activation columns (q / k / v, gate / up) in one launch: each matrix owns
 // a contiguous range of workgroups. It can also take the activations in F32
-// and quantize them inside the launch (one block per thread, the block
-// function of levo_hip_quantize_chunk, requested before the weights and
-// computed while they are in flight), for n_vec * K / 32 <= 256 blocks; the
-// results equal levo_hip_quantize_chunk + levo_hip_mul_mat_q8_0 bit for bit.
+// and quantize them inside the launch (the block function of
+// levo_hip_quantize_chunk, two lanes per block up to 128 blocks, one lane
+// per block up to 256; requested before the weights and computed while they
+// are in flight), for n_vec * K / 32 <= 256 blocks; the results equal
+// levo_hip_quantize_chunk + levo_hip_mul_mat_q8_0 bit for bit.
 #include "common.hpp"
 #include "quant_block.hpp"
 #include "span_load.hpp"
@@ -55,6 +56,7 @@ constexpr int kMaxMats = 4;
 constexpr int kXBlocks = 0;
 constexpr int kXF32 = 1;
 constexpr int kXColumns = 2;
+constexpr int kXF32Pair = 3;  // F32 values, two lanes per block (n_vec * K / 32 <= 128)
 
 struct mm_params {
     const uint8_t * w;    // [rows][nb] weight blocks, 16-byte aligned
@@ -169,6 +171,65 @@ __device__ __forceinline__ void block_terms(const uint32_t (&q)[8], float dw, co
     }
 }
 
+// quantize_q8_0_block over the two lanes of a pair (lane h of the pair
+// holds values 16 h .. 16 h + 15 in v): the |x| maximum joined by one DPP
+// step, the index-order NaN scan (rare) reading the pair's values lane by
+// lane; each lane's 16 quants as 4 dwords; d as F16 in both lanes. The
+// same bits as quantize_q8_0_block; half its dependent chain per lane and
+// half the loads per thread (ffn gate/up 8960 x 1536 with its input
+// quantized in the launch 6.16 -> 5.54 us). Every lane of the wave runs it
+// (the DPP step reads the partner lane).
+__device__ __forceinline__ uint16_t quantize_q8_0_block_x2(const u32x4 (&v)[4], uint32_t (&pk)[4]) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[4 * i] = __uint_as_float(v[i].x);
+        x[4 * i + 1] = __uint_as_float(v[i].y);
+        x[4 * i + 2] = __uint_as_float(v[i].z);
+        x[4 * i + 3] = __uint_as_float(v[i].w);
+    }
+    uint32_t bits_max = 0u;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) bits_max = __builtin_elementwise_max(bits_max, __float_as_uint(x[k]) & 0x7fffffffu);
+    bits_max = __builtin_elementwise_max(bits_max, dpp::mov<dpp::kQuadXor1>(bits_max));
+    const bool has_nan = bits_max > 0x7f800000u;
+    float amax = __uint_as_float(bits_max);
+    if (has_nan) {
+        const int base = static_cast<int>(__lane_id()) & ~1;
+        amax = 0.0f;
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const float w = fabsf(__shfl(x[k], base + t, 64));
+                amax = amax > w ? amax : w;
+            }
+        }
+    }
+    const float d = amax / 127.0f;
+    const float id = nan_if_inf(d != 0.0f ? 1.0f / d : 0.0f);
+    if (!has_nan) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            uint32_t q[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = trunc_i32(half_away_offset(x[4 * w + k] * id));
+            pk[w] = pack_low_bytes(q[0], q[1], q[2], q[3]);
+        }
+    } else {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            uint32_t q[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float t = half_away_offset(x[4 * w + k] * id);
+                q[k] = __builtin_fabsf(t) < 0x1p31f ? low_byte_i8(t) : 0u;
+            }
+            pk[w] = pack4(q[0], q[1], q[2], q[3]);
+        }
+    }
+    return f2h(d);
+}
+
 // XF: the activations' form. PB > 0: the weights in the packed layout
 // (levo_hip_repack_q8_0): lane li of a row group loads blocks
 // kb0 + li + LPR * i (i < PB, the same blocks in the same order as the
@@ -179,6 +240,7 @@ __device__ __forceinline__ void block_terms(const uint32_t (&q)[8], float dw, co
 template <int LPR, int WPR, int XF, int PB>
 __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch ml) {
     constexpr bool FUSED = XF == kXF32;
+    constexpr bool PAIR = XF == kXF32Pair;
     constexpr bool PACKED = PB > 0;
     constexpr int kPB = PACKED ? PB : 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -221,11 +283,15 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
     // FUSED: thread t < nvb quantizes activation block t (column t / nb,
     // block t % nb); other threads read block 0 and drop it
     const int xt = static_cast<int>(threadIdx.x) < nvb ? static_cast<int>(threadIdx.x) : 0;
-    constexpr int kXr = FUSED ? 8 : kXChunks;
+    constexpr int kXr = FUSED ? 8 : PAIR ? 4 : kXChunks;
+    const int xp = min(static_cast<int>(threadIdx.x) >> 1, nvb - 1);
     u32x4 xr[kXr];  // unconditional (see load_span): chunks past the end re-read chunk 0
 #pragma unroll
     for (int i = 0; i < kXr; ++i) {
-        if constexpr (FUSED) {
+        if constexpr (PAIR) {
+            const float * src = ml.xf + (xp / p.nb) * ml.x_pitch + (xp % p.nb) * 32 + 16 * (threadIdx.x & 1);
+            xr[i] = *reinterpret_cast<const u32x4 *>(src + 4 * i);
+        } else if constexpr (FUSED) {
             const float * src = ml.xf + (xt / p.nb) * ml.x_pitch + (xt % p.nb) * 32;
             xr[i] = *reinterpret_cast<const u32x4 *>(src + 4 * i);
         } else {
@@ -284,6 +350,14 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
             } else {
                 copy_tail_dwords(smem, p.x, xbytes, c);
             }
+        }
+        lds_barrier();  // LDS only: the weight loads stay in flight
+    } else if constexpr (PAIR) {
+        uint32_t pk[4];
+        const uint16_t d = quantize_q8_0_block_x2(xr, pk);
+        if ((static_cast<int>(threadIdx.x) >> 1) < nvb) {
+            reinterpret_cast<u32x4 *>(xq)[threadIdx.x] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+            if ((threadIdx.x & 1) == 0) dx[threadIdx.x >> 1] = h2f(d);
         }
         lds_barrier();  // LDS only: the weight loads stay in flight
     } else if constexpr (FUSED) {
@@ -386,7 +460,9 @@ constexpr int rows_per_workgroup() {
 
 template <int LPR, int WPR, int PB>
 int launch_packed(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st, const char * what) {
-    if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB><<<blocks, kThreads, lds, st>>>(ml);
+    if (ml.xf != nullptr && ml.p.n_vec * ml.p.nb <= kThreads / 2)
+        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, PB><<<blocks, kThreads, lds, st>>>(ml);
+    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB><<<blocks, kThreads, lds, st>>>(ml);
     else mul_mat_q8_0_kernel<LPR, WPR, kXColumns, PB><<<blocks, kThreads, lds, st>>>(ml);
     return launch_status(what);
 }
@@ -426,7 +502,9 @@ int launch_mm(mm_launch ml, bool packed, hipStream_t st, const char * what) {
         if (per_lane == 3) return launch_packed<LPR, WPR, 3>(ml, blocks, lds, st, what);
         return launch_packed<LPR, WPR, 4>(ml, blocks, lds, st, what);
     }
-    if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, 0><<<blocks, kThreads, lds, st>>>(ml);
+    if (ml.xf != nullptr && ml.p.n_vec * ml.p.nb <= kThreads / 2)
+        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, 0><<<blocks, kThreads, lds, st>>>(ml);
+    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, 0><<<blocks, kThreads, lds, st>>>(ml);
     else mul_mat_q8_0_kernel<LPR, WPR, kXBlocks, 0><<<blocks, kThreads, lds, st>>>(ml);
     return launch_status(what);
 }

@@ -197,12 +197,13 @@ def test_multi_wide_k_from_blocks(hip, dev, oracle):
         assert _bits_equal(g, w)
 
 
-def test_multi_fused_quantization_special_values_and_pitch(hip, dev, oracle):
+@pytest.mark.parametrize("k,n_vec", [(256, 2), (4096, 2)])
+def test_multi_fused_quantization_special_values_and_pitch(hip, dev, oracle, k, n_vec):
     """Zero blocks, tiny blocks (1/d overflows), ties at k + 0.5, NaN and inf
-    quantize in the launch as levo_hip_quantize_chunk does; rows of x and y
-    with a pitch; a matrix of zero rows is skipped."""
+    quantize in the launch as levo_hip_quantize_chunk does, with two lanes
+    per block (16 blocks) and one lane per block (256 blocks); rows of x and
+    y with a pitch; a matrix of zero rows is skipped."""
     import torch
-    k, n_vec = 256, 2
     x = oracle.gaussian(n_vec * k, 5).reshape(n_vec, k)
     x[0, :32] = 0.0
     x[0, 32:64] = 1e-41
@@ -210,6 +211,9 @@ def test_multi_fused_quantization_special_values_and_pitch(hip, dev, oracle):
     x[1, 96:128] = np.float32(127.0) * (np.arange(32) % 3 - 1) + np.float32(0.5) * (np.arange(32) % 2)
     x[0, 130] = np.nan
     x[1, 200] = np.inf
+    x[1, 160] = np.nan   # a block's first value: the index-order MAX restarts after it
+    x[0, 180] = np.nan   # in the second half of a block (the other lane of a pair)
+    x[1, 250] = np.nan
     xp = np.zeros((n_vec, k + 12), np.float32)
     xp[:, :k] = x
     mats = [(to_dev(oracle.quantize(8, (oracle.gaussian(r * k, r) * np.float32(0.02)).reshape(r, k)), dev), r)
