@@ -70,7 +70,7 @@ void mul_mat_q8_0_shared_input(const q8_0_matrix * mats, int n_mats, const float
 // (q8_0_columns_size(n_vec, k) bytes, 16-byte aligned): the Q8_0
 // quantization of x in the form the mat-vec keeps on chip. Each y equals
 // mul_mat_q8_0's on the original blocks, bit for bit; the launch that reads
-// the weights is 8-17 % shorter at LeLM's matrices.
+// the weights is 15-25 % shorter at LeLM's matrices.
 void repack_q8_0(const void * weight, void * packed, int64_t rows, int64_t k, stream_t stream = nullptr);
 std::size_t q8_0_columns_size(int64_t n_vec, int64_t k);
 void mul_mat_q8_0_packed(const void * packed, const float * x, void * x_columns, float * y, int64_t rows,
