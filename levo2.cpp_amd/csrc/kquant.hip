@@ -29,39 +29,37 @@ __device__ __forceinline__ int nearest_int(float fval) {
     return static_cast<int>(__builtin_bit_cast(uint32_t, val) & 0x007fffffu) - 0x00400000;
 }
 
-// Byte s (0..11) of the packed scales held in three dwords.
-__device__ __forceinline__ int scale_byte(uint32_t s0, uint32_t s1, uint32_t s2, int s) {
-    const uint32_t w = s < 4 ? s0 : s < 8 ? s1 : s2;
-    return static_cast<int>((w >> (8 * (s & 3))) & 0xffu);
-}
-
-// get_scale_min_k4: sub-block j's 6-bit scale and min.
+// get_scale_min_k4: sub-block j's 6-bit scale and min, without a branch
+// (the lanes of a block take sub-blocks on both sides of j = 4; a branch ran
+// both paths: Q4_K / Q5_K mat-vecs 2-4 % slower): with a, b, c byte j % 4 of
+// the three dwords (bytes j % 4, 4 + j % 4, 8 + j % 4 of the twelve), j < 4
+// takes sc = a & 63, m = b & 63; j >= 4 takes sc = (c & 15) | (a >> 6) << 4,
+// m = (c >> 4) | (b >> 6) << 4.
 __device__ __forceinline__ void scale_min_k4(uint32_t s0, uint32_t s1, uint32_t s2, int j, int & sc, int & m) {
-    if (j < 4) {
-        sc = scale_byte(s0, s1, s2, j) & 63;
-        m = scale_byte(s0, s1, s2, j + 4) & 63;
-    } else {
-        const int b = scale_byte(s0, s1, s2, j + 4);
-        sc = (b & 0xF) | ((scale_byte(s0, s1, s2, j - 4) >> 6) << 4);
-        m = (b >> 4) | ((scale_byte(s0, s1, s2, j) >> 6) << 4);
-    }
+    const uint32_t sh = 8u * static_cast<uint32_t>(j & 3);
+    const int a = static_cast<int>((s0 >> sh) & 0xffu);
+    const int b = static_cast<int>((s1 >> sh) & 0xffu);
+    const int c = static_cast<int>((s2 >> sh) & 0xffu);
+    const bool lo = j < 4;
+    sc = lo ? (a & 63) : ((c & 0xF) | ((a >> 6) << 4));
+    m = lo ? (b & 63) : ((c >> 4) | ((b >> 6) << 4));
 }
 
 // Two dwords at byte offset `off` of a block whose start is 2 mod 4 when
-// `odd` (Q6_K's 210-byte blocks): aligned dword loads and a 16-bit funnel
-// shift. off is a multiple of 4 and off + 10 <= 210; for odd blocks the two
-// bytes before the block (the previous block's tail: the buffer itself is
-// 16-byte aligned, so its first block is never odd) are read and discarded.
+// `odd` (Q6_K's 210-byte blocks): aligned dword loads and a funnel shift of
+// 16 bits (odd) or none, with no branch (lanes of one wave hold blocks of
+// both kinds; a branch ran both paths: Q6_K mat-vecs 3-6 % slower). Odd
+// blocks read three dwords, even ones the second dword again, so nothing
+// past the block is read. off is a multiple of 4 and off + 10 <= 210; for
+// odd blocks the two bytes before the block (the previous block's tail: the
+// buffer itself is 16-byte aligned, so its first block is never odd) are
+// read and discarded.
 __device__ __forceinline__ void load_u32x2(const uint8_t * blk, int off, bool odd, uint32_t & a, uint32_t & b) {
     const uint32_t * p = reinterpret_cast<const uint32_t *>(blk + off - (odd ? 2 : 0));
-    if (!odd) {
-        a = p[0];
-        b = p[1];
-    } else {
-        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
-        a = __builtin_amdgcn_alignbit(w1, w0, 16);
-        b = __builtin_amdgcn_alignbit(w2, w1, 16);
-    }
+    const uint32_t w0 = p[0], w1 = p[1], w2 = p[odd ? 2 : 1];
+    const uint32_t sh = odd ? 16u : 0u;
+    a = __builtin_amdgcn_alignbit(w1, w0, sh);
+    b = __builtin_amdgcn_alignbit(w2, w1, sh);
 }
 
 __device__ __forceinline__ uint32_t load_u32(const uint8_t * blk, int off, bool odd) {
@@ -313,8 +311,10 @@ __device__ __forceinline__ void kq_compute(const kq_unit<TYPE> & w, int ib, int 
                 const uint2 x1 = *reinterpret_cast<const uint2 *>(q8 + 32);
                 const uint2 x2 = *reinterpret_cast<const uint2 *>(q8 + 64);
                 const uint2 x3 = *reinterpret_cast<const uint2 *>(q8 + 96);
-                const int isum = sc0 * dot4(c00, x0.x, dot4(c01, x0.y, 0)) + sc1 * dot4(c10, x1.x, dot4(c11, x1.y, 0)) +
-                                 sc2 * dot4(c20, x2.x, dot4(c21, x2.y, 0)) + sc3 * dot4(c30, x3.x, dot4(c31, x3.y, 0));
+                const int isum = __mul24(sc0, dot4(c00, x0.x, dot4(c01, x0.y, 0))) +
+                                 __mul24(sc1, dot4(c10, x1.x, dot4(c11, x1.y, 0))) +
+                                 __mul24(sc2, dot4(c20, x2.x, dot4(c21, x2.y, 0))) +
+                                 __mul24(sc3, dot4(c30, x3.x, dot4(c31, x3.y, 0)));
                 acc_d[v] += (dw * xd[v * nb + ib]) * static_cast<float>(isum);
             }
         }
@@ -351,8 +351,8 @@ __device__ __forceinline__ void kq_compute(const kq_unit<TYPE> & w, int ib, int 
                     dh = dot4(hi[q], x1[q], dh);
                 }
                 const int16_t * bs = xs + (v * nb + ib) * 16;
-                const int isum = sc0 * dl + sc1 * dh;
-                const int msum = m0 * bs[4 * g + h] + m1 * bs[4 * g + 2 + h];
+                const int isum = __mul24(sc0, dl) + __mul24(sc1, dh);
+                const int msum = __mul24(m0, static_cast<int>(bs[4 * g + h])) + __mul24(m1, static_cast<int>(bs[4 * g + 2 + h]));
                 const float dx = xd[v * nb + ib];
                 acc_d[v] += (dw * dx) * static_cast<float>(isum);
                 acc_m[v] += (dminw * dx) * static_cast<float>(msum);
