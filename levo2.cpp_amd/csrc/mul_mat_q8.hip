@@ -150,10 +150,11 @@ __device__ __forceinline__ bool wave_span(const mm_params & p, int64_t grp, int 
 
 // One block's terms for every activation column: sumi by 8 v_dot4 over the
 // block's quant dwords q, then acc[v] += sumi * (d_w * d_x).
+template <int NV>
 __device__ __forceinline__ void block_terms(const uint32_t (&q)[8], float dw, const uint32_t * xq, const float * dx,
-                                            int nb, int kb, int n_vec, float (&acc)[kMaxVectors]) {
+                                            int nb, int kb, int n_vec, float (&acc)[NV]) {
 #pragma unroll
-    for (int v = 0; v < kMaxVectors; ++v) {
+    for (int v = 0; v < NV; ++v) {
         if (v >= n_vec) break;
         const u32x4 * xb = reinterpret_cast<const u32x4 *>(xq + (v * nb + kb) * 8);
         const u32x4 x0 = xb[0];
@@ -237,7 +238,8 @@ __device__ __forceinline__ uint16_t quantize_q8_0_block_x2(const u32x4 (&v)[4], 
 // geometry gives a lane at most 4) straight into registers: the first 16
 // quants, the last 16 and the F16 scale, each an aligned load; no LDS
 // stage, no realignment. PB = 0: Q8_0 blocks.
-template <int LPR, int WPR, int XF, int PB>
+// NV: accumulators per lane, 2 for the CFG pair (n_vec <= 2), else 8.
+template <int LPR, int WPR, int XF, int PB, int NV>
 __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch ml) {
     constexpr bool FUSED = XF == kXF32;
     constexpr bool PAIR = XF == kXF32Pair;
@@ -400,9 +402,9 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
     }
 
     // 3. the wave's blocks: lane li of row group g takes kb = kb0 + li + LPR * i
-    float acc[kMaxVectors];
+    float acc[NV];
 #pragma unroll
-    for (int v = 0; v < kMaxVectors; ++v) acc[v] = 0.0f;
+    for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
     if constexpr (PACKED) {
         if (have && g < nrows) {
 #pragma unroll
@@ -410,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
                 const int kb = kb0 + li + LPR * i;
                 if (kb >= kb1) break;
                 const uint32_t q[8] = {wlo[i].x, wlo[i].y, wlo[i].z, wlo[i].w, whi[i].x, whi[i].y, whi[i].z, whi[i].w};
-                block_terms(q, h2f(wd[i]), xq, dx, p.nb, kb, p.n_vec, acc);
+                block_terms<NV>(q, h2f(wd[i]), xq, dx, p.nb, kb, p.n_vec, acc);
             }
         }
     } else {
@@ -422,12 +424,12 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
             for (int kb = kb0 + li; kb < kb1; kb += LPR) {
                 uint32_t q[8];
                 const float dw = read_block(stage, lead + (row_base + kb - kb0) * kQ8Bytes, q);
-                block_terms(q, dw, xq, dx, p.nb, kb, p.n_vec, acc);
+                block_terms<NV>(q, dw, xq, dx, p.nb, kb, p.n_vec, acc);
             }
         }
     }
 #pragma unroll
-    for (int v = 0; v < kMaxVectors; ++v) {
+    for (int v = 0; v < NV; ++v) {
         if (v >= p.n_vec) break;
         acc[v] = group_sum<LPR>(acc[v]);
     }
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
         // the row's parts meet in LDS, summed in wave order
         if (lane == 0) {
 #pragma unroll
-            for (int v = 0; v < kMaxVectors; ++v) part[wave * kMaxVectors + v] = acc[v];
+            for (int v = 0; v < NV; ++v) part[wave * kMaxVectors + v] = acc[v];
         }
         __syncthreads();
         if (wave % WPR == 0 && lane < p.n_vec && row0 < p.rows) {
@@ -446,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
         }
     } else if (have && g < nrows && li == 0) {
 #pragma unroll
-        for (int v = 0; v < kMaxVectors; ++v) {
+        for (int v = 0; v < NV; ++v) {
             if (v >= p.n_vec) break;
             p.y[v * p.y_pitch + row0 + g] = acc[v];
         }
@@ -458,12 +460,22 @@ constexpr int rows_per_workgroup() {
     return WPR > 1 ? kWaves / WPR : kWaves * (64 / LPR);
 }
 
-template <int LPR, int WPR, int PB>
-int launch_packed(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st, const char * what) {
+// The instance for the activations' form (F32 values: two lanes per block up
+// to 128 blocks; else columns for packed matrices, Q8_0 blocks otherwise)
+// and the accumulator count.
+template <int LPR, int WPR, int PB, int NV>
+void launch_form(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st) {
     if (ml.xf != nullptr && ml.p.n_vec * ml.p.nb <= kThreads / 2)
-        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, PB><<<blocks, kThreads, lds, st>>>(ml);
-    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB><<<blocks, kThreads, lds, st>>>(ml);
-    else mul_mat_q8_0_kernel<LPR, WPR, kXColumns, PB><<<blocks, kThreads, lds, st>>>(ml);
+        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
+    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
+    else if constexpr (PB > 0) mul_mat_q8_0_kernel<LPR, WPR, kXColumns, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
+    else mul_mat_q8_0_kernel<LPR, WPR, kXBlocks, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
+}
+
+template <int LPR, int WPR, int PB>
+int launch_pb(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st, const char * what) {
+    if (ml.p.n_vec <= 2) launch_form<LPR, WPR, PB, 2>(ml, blocks, lds, st);
+    else launch_form<LPR, WPR, PB, kMaxVectors>(ml, blocks, lds, st);
     return launch_status(what);
 }
 
@@ -496,17 +508,13 @@ int launch_mm(mm_launch ml, bool packed, hipStream_t st, const char * what) {
         // 3-4 for the longer rows (more than 64 blocks per 16 lanes)
         const int64_t per_lane = ceil_div(WPR > 1 ? (p.nb + WPR - 1) / WPR : p.nb, LPR);
         if constexpr (LPR == 16) {
-            if (per_lane == 1) return launch_packed<LPR, WPR, 1>(ml, blocks, lds, st, what);
-            if (per_lane == 2) return launch_packed<LPR, WPR, 2>(ml, blocks, lds, st, what);
+            if (per_lane == 1) return launch_pb<LPR, WPR, 1>(ml, blocks, lds, st, what);
+            if (per_lane == 2) return launch_pb<LPR, WPR, 2>(ml, blocks, lds, st, what);
         }
-        if (per_lane == 3) return launch_packed<LPR, WPR, 3>(ml, blocks, lds, st, what);
-        return launch_packed<LPR, WPR, 4>(ml, blocks, lds, st, what);
+        if (per_lane == 3) return launch_pb<LPR, WPR, 3>(ml, blocks, lds, st, what);
+        return launch_pb<LPR, WPR, 4>(ml, blocks, lds, st, what);
     }
-    if (ml.xf != nullptr && ml.p.n_vec * ml.p.nb <= kThreads / 2)
-        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, 0><<<blocks, kThreads, lds, st>>>(ml);
-    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, 0><<<blocks, kThreads, lds, st>>>(ml);
-    else mul_mat_q8_0_kernel<LPR, WPR, kXBlocks, 0><<<blocks, kThreads, lds, st>>>(ml);
-    return launch_status(what);
+    return launch_pb<LPR, WPR, 0>(ml, blocks, lds, st, what);
 }
 
 // The fewest lanes per row that hold the row's blocks in one wave's span.
