@@ -107,9 +107,11 @@ constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
 constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
 constexpr int kRowRor4 = 0x124;  // row_ror:4
 constexpr int kRowRor8 = 0x128;  // row_ror:8
+constexpr int kRowMirror = 0x140;      // row_mirror: lane i of each 16 takes lane 15 - i
+constexpr int kRowHalfMirror = 0x141;  // row_half_mirror: lane i of each 8 takes lane 7 - i
 
-// Every control used through mov (quad permutes, row rotations) gives each
-// lane a source inside its row, so no "old" value is needed: v_mov_b32_dpp
+// Every control used through mov (quad permutes, row rotations and mirrors)
+// gives each lane a source inside its row, so no "old" value is needed: v_mov_b32_dpp
 // without one spares the register a zero (or a copy) would take.
 template <int kCtrl>
 __device__ __forceinline__ uint32_t mov(uint32_t v) {

@@ -78,67 +78,84 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
 
 // ---- Q8_K quantizer: one wave per 256-value block ----------------------------
 
-// quantize_row_q8_K_ref for the block whose values 4 lane .. 4 lane + 3 this
-// lane holds: its 4 quants packed in a dword, the block's scale d and, in
-// lanes 0-7, bsums 2 lane and 2 lane + 1 packed in a dword. A block of zeros
-// gives d = 0, zero quants and zero bsums.
-__device__ __forceinline__ void q8_K_block(const f32x4 v, int lane, uint32_t & packed, float & d,
-                                           uint32_t & bsum_pair) {
-    // first element of largest |x| (NaN never compares larger), as the
-    // reference's `if (ax > amax)` scan: key = |x| bits, then lowest index
-    uint64_t key = 0;
+// quantize_row_q8_K_ref for the block whose values 16 s .. 16 s + 15 this
+// lane holds (s = lane % 16: sixteen lanes per block, four blocks per wave):
+// its 16 quants as 4 dwords, its bsum s (elements 16 s .. 16 s + 15 are this
+// lane's own) and the block's scale d. Every reduction stays inside the
+// lane's row of 16, as DPP steps: the largest |x| bits (NaN counting as 0,
+// so it never compares larger, as the reference's `if (ax > amax)` scan),
+// the first index holding it, and that value's sign. A block of zeros gives
+// d = 0, zero quants and a zero bsum. Every lane of the wave runs it.
+__device__ __forceinline__ void q8_K_block16(const f32x4 (&v)[4], int s, uint32_t (&pk)[4], int & bsum,
+                                             float & d) {
+    uint32_t lmax = 0u, lval = 0u;
+    int lidx = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float ax = __builtin_fabsf(v[q]);
+    for (int q = 0; q < 16; ++q) {
+        const float x = v[q >> 2][q & 3];
+        const float ax = __builtin_fabsf(x);
         const uint32_t bits = ax == ax ? __builtin_bit_cast(uint32_t, ax) : 0u;
-        const uint64_t k = (static_cast<uint64_t>(bits) << 32) | static_cast<uint32_t>(255 - (4 * lane + q));
-        key = k > key ? k : key;
+        const bool more = bits > lmax;
+        lmax = more ? bits : lmax;
+        lidx = more ? q : lidx;
+        lval = more ? __builtin_bit_cast(uint32_t, x) : lval;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint64_t other = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(key), o, 64));
-        key = other > key ? other : key;
-    }
-    if ((key >> 32) == 0) {  // amax == 0: an all-zero block
-        packed = 0u;
-        d = 0.0f;
-        bsum_pair = 0u;
-        return;
-    }
-    const int arg = 255 - static_cast<int>(key & 0xffu);
-    const float max = __shfl(v[arg & 3], arg >> 2, 64);
-    const float iscale = -127.0f / max;
-    packed = 0;
+    uint32_t gmax = lmax;
+    gmax = __builtin_elementwise_max(gmax, dpp::mov<dpp::kQuadXor1>(gmax));
+    gmax = __builtin_elementwise_max(gmax, dpp::mov<dpp::kQuadXor2>(gmax));
+    gmax = __builtin_elementwise_max(gmax, dpp::mov<dpp::kRowHalfMirror>(gmax));
+    gmax = __builtin_elementwise_max(gmax, dpp::mov<dpp::kRowMirror>(gmax));
+    const uint32_t mine = static_cast<uint32_t>(16 * s + lidx);
+    uint32_t gidx = lmax == gmax ? mine : 256u;
+    gidx = __builtin_elementwise_min(gidx, dpp::mov<dpp::kQuadXor1>(gidx));
+    gidx = __builtin_elementwise_min(gidx, dpp::mov<dpp::kQuadXor2>(gidx));
+    gidx = __builtin_elementwise_min(gidx, dpp::mov<dpp::kRowHalfMirror>(gidx));
+    gidx = __builtin_elementwise_min(gidx, dpp::mov<dpp::kRowMirror>(gidx));
+    uint32_t mbits = mine == gidx ? lval : 0u;
+    mbits |= dpp::mov<dpp::kQuadXor1>(mbits);
+    mbits |= dpp::mov<dpp::kQuadXor2>(mbits);
+    mbits |= dpp::mov<dpp::kRowHalfMirror>(mbits);
+    mbits |= dpp::mov<dpp::kRowMirror>(mbits);
+    const bool zero = gmax == 0u;  // amax == 0: an all-zero (or all-NaN) block
+    const float iscale = -127.0f / __builtin_bit_cast(float, mbits);
     int sum = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        int l = nearest_int(iscale * v[q]);
-        l = l < 127 ? l : 127;
-        sum += l;
-        packed |= (static_cast<uint32_t>(l) & 0xffu) << (8 * q);
+    for (int w = 0; w < 4; ++w) {
+        uint32_t packed = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            int l = nearest_int(iscale * v[w][q]);
+            l = l < 127 ? l : 127;
+            l = zero ? 0 : l;
+            sum += l;
+            packed |= (static_cast<uint32_t>(l) & 0xffu) << (8 * q);
+        }
+        pk[w] = packed;
     }
-    // bsums[j]: elements 16 j .. 16 j + 15 = lanes 4 j .. 4 j + 3
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    const int lo = __shfl(sum, 8 * (lane & 7), 64);
-    const int hi = __shfl(sum, 8 * (lane & 7) + 4, 64);
-    bsum_pair = (static_cast<uint32_t>(lo) & 0xffffu) | (static_cast<uint32_t>(hi) << 16);
-    d = 1.0f / iscale;
+    bsum = sum;
+    d = zero ? 0.0f : 1.0f / iscale;
 }
 
+// Sixteen blocks per workgroup, sixteen lanes each (q8_K_block16); a group
+// past the last block computes on the last one and stores nothing.
 __global__ __launch_bounds__(kThreads) void quantize_q8_K_kernel(const float * __restrict__ x, uint8_t * y,
                                                                   int64_t nb) {
-    const int lane = threadIdx.x & 63;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
-    if (i >= nb) return;
-    const f32x4 v = *reinterpret_cast<const f32x4 *>(x + i * kQK + 4 * lane);
-    uint32_t packed, bsum_pair;
+    const int s = threadIdx.x & 15;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * (kThreads / 16) + (threadIdx.x >> 4);
+    const int64_t ic = i < nb ? i : nb - 1;
+    const f32x4 * src = reinterpret_cast<const f32x4 *>(x + ic * kQK + 16 * s);
+    const f32x4 v[4] = {src[0], src[1], src[2], src[3]};
+    uint32_t pk[4];
+    int bsum;
     float d;
-    q8_K_block(v, lane, packed, d, bsum_pair);
+    q8_K_block16(v, s, pk, bsum, d);
+    if (i >= nb) return;
     uint8_t * blk = y + i * 292;
-    reinterpret_cast<uint32_t *>(blk + 4)[lane] = packed;
-    if (lane < 8) reinterpret_cast<uint32_t *>(blk + 260)[lane] = bsum_pair;
-    if (lane == 0) *reinterpret_cast<float *>(blk) = d;
+    uint32_t * q = reinterpret_cast<uint32_t *>(blk + 4 + 16 * s);  // 4-byte aligned (292 i + 4)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) q[w] = pk[w];
+    reinterpret_cast<int16_t *>(blk + 260)[s] = static_cast<int16_t>(bsum);
+    if (s == 0) *reinterpret_cast<float *>(blk) = d;
 }
 
 // ---- dequantizers: 8 outputs per thread --------------------------------------
@@ -463,25 +480,25 @@ __global__ __launch_bounds__(kThreads) void mul_mat_kquant_kernel(const kq_param
                                 : sb0 + nrows * M.row_bytes;
     u32x4 regs[CH];
     if constexpr (FUSED) {
-        // F32 activations, block b = (vector b / nb, super-block b % nb): the
-        // wave's blocks b = wave + 4 i are requested first, then the weights
-        f32x4 xv[kFusedBlocks / 4];
-#pragma unroll
-        for (int i = 0; i < kFusedBlocks / 4; ++i) {
-            const int b = min(wave + 4 * i, nblk - 1);
-            xv[i] = *reinterpret_cast<const f32x4 *>(p.xf + (b / nb) * p.xf_pitch + (b % nb) * kQK + 4 * lane);
-        }
+        // F32 activations, block b = (vector b / nb, super-block b % nb),
+        // sixteen lanes per block (q8_K_block16): block 4 wave + lane / 16,
+        // requested first, then the weights; a group past the last block
+        // computes on it and stores nothing
+        const int fb = 4 * wave + (lane >> 4);
+        const int fs = lane & 15;
+        const int fbc = min(fb, nblk - 1);
+        const f32x4 * fsrc = reinterpret_cast<const f32x4 *>(p.xf + (fbc / nb) * p.xf_pitch + (fbc % nb) * kQK + 16 * fs);
+        const f32x4 xv[4] = {fsrc[0], fsrc[1], fsrc[2], fsrc[3]};
         load_span<CH>(M.w, M.w_bytes, sb0 & ~int64_t{15}, sb1, nrows > 0, lane, regs);
-#pragma unroll
-        for (int i = 0; i < kFusedBlocks / 4; ++i) {
-            const int b = wave + 4 * i;
-            if (b < nblk) {
-                uint32_t packed, bsum_pair;
-                float d;
-                q8_K_block(xv[i], lane, packed, d, bsum_pair);
-                reinterpret_cast<uint32_t *>(xq)[b * 64 + lane] = packed;
-                if (lane < 8) reinterpret_cast<uint32_t *>(xs)[b * 8 + lane] = bsum_pair;
-                if (lane == 0) xd[b] = d;
+        {
+            uint32_t pk[4];
+            int bsum;
+            float d;
+            q8_K_block16(xv, fs, pk, bsum, d);
+            if (fb < nblk) {
+                reinterpret_cast<u32x4 *>(xq)[fb * 16 + fs] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+                xs[fb * 16 + fs] = static_cast<int16_t>(bsum);
+                if (fs == 0) xd[fb] = d;
             }
         }
     } else {
@@ -731,7 +748,7 @@ extern "C" int levo_hip_quantize_q8_K(const float * x, void * y, int64_t k, levo
     LEVO_REQUIRE(aligned16(x), "quantize_q8_K: x must be 16-byte aligned");
     LEVO_REQUIRE((reinterpret_cast<uintptr_t>(y) & 3u) == 0, "quantize_q8_K: y must be 4-byte aligned");
     const int64_t nb = k / kQK;
-    quantize_q8_K_kernel<<<static_cast<uint32_t>(ceil_div(nb, kThreads / 64)), kThreads, 0, as_hip(stream)>>>(
+    quantize_q8_K_kernel<<<static_cast<uint32_t>(ceil_div(nb, kThreads / 16)), kThreads, 0, as_hip(stream)>>>(
             x, static_cast<uint8_t *>(y), nb);
     return launch_status("levo_hip_quantize_q8_K");
 }
