@@ -76,7 +76,7 @@ __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-// ---- Q8_K quantizer: one wave per 256-value block ----------------------------
+// ---- Q8_K quantizer: sixteen lanes per 256-value block -----------------------
 
 // quantize_row_q8_K_ref for the block whose values 16 s .. 16 s + 15 this
 // lane holds (s = lane % 16: sixteen lanes per block, four blocks per wave):
@@ -419,8 +419,8 @@ __device__ __forceinline__ void kq_units(const uint8_t * stage, int lead, int g,
 //   2. meanwhile the workgroup stages the Q8_K activations in LDS, laid out
 //      so that each lane's quants are aligned: xq [n_vec][256 nb] int8, then
 //      xd [n_vec][nb] float, xs [n_vec][16 nb] int16 (the bsums); FUSED: it
-//      quantizes F32 activations into that layout itself, one wave per block
-//      as levo_hip_quantize_q8_K does;
+//      quantizes F32 activations into that layout itself, sixteen lanes per
+//      block as levo_hip_quantize_q8_K does;
 //   3. each wave stores its span to its LDS stage area; each lane parses its
 //      units there and adds their terms; a reduction over the row's LPR lanes
 //      gives y.
