@@ -684,12 +684,26 @@ int launch_mul_mat(kq_params & p, hipStream_t st) {
         // workgroups or more: 16 rows per workgroup from 4096 rows, 8 from
         // 2048, else 4 (1536 x 1536 Q4_K 4.69 -> 3.68 us, Q6_K 5.29 -> 3.99;
         // at 8960 and 16385 rows 16 lanes per row stay fastest)
-        if (rows >= 4096) return launch_mul_mat_u<16, 4, 8>(p, rb, st);
+        // Instances sized to the span where it is smaller: every lane issues
+        // all CH chunk loads and U unit iterations, so surplus ones cost
+        // issue slots (K = 1536: 3 units and 5 chunks instead of 4 and 8,
+        // 3-5 % at 8960 and 16385 rows; K = 2304 / 4608 below 11-13 %); the
+        // lanes' units, and so the sums, stay the same.
+        if (rows >= 4096) {
+            if (units <= 48 && 4 * rb + 30 <= 5 * 64 * 16) return launch_mul_mat_u<16, 3, 5>(p, rb, st);
+            return launch_mul_mat_u<16, 4, 8>(p, rb, st);
+        }
         if (rows >= 2048) return launch_mul_mat_u<32, 2, 4>(p, rb, st);
         return launch_mul_mat_u<64, 1, 2>(p, rb, st);
     }
-    if (units <= 128) return launch_mul_mat_u<16, 8, 16>(p, rb, st);
-    if (units <= 256) return launch_mul_mat_u<32, 8, 16>(p, rb, st);
+    if (units <= 128) {
+        if (units <= 80 && 4 * rb + 30 <= 8 * 64 * 16) return launch_mul_mat_u<16, 5, 8>(p, rb, st);
+        return launch_mul_mat_u<16, 8, 16>(p, rb, st);
+    }
+    if (units <= 256) {
+        if (units <= 160 && 2 * rb + 30 <= 8 * 64 * 16) return launch_mul_mat_u<32, 5, 8>(p, rb, st);
+        return launch_mul_mat_u<32, 8, 16>(p, rb, st);
+    }
     // K > 8192 (LeLM's ffn_down, K = 8960): a row over two waves, each half
     // its super-blocks, so each lane takes ~2 units instead of ~4 (Q4_K
     // 10.2 -> 9.4 us). Up to 38 super-blocks the half-row spans fit 4 chunks

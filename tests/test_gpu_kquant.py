@@ -172,7 +172,8 @@ def test_mul_mat_matches_oracle(hip, dev, oracle, qtype, rows, k, n_vec):
 @pytest.mark.parametrize("qtype", [Q4_K, Q5_K, Q6_K])
 @pytest.mark.parametrize("rows,k,n_vec", [(1, 256, 1), (3, 256, 2), (7, 2304, 3), (65, 512, 2), (5, 8960, 8),
                                           (2049, 768, 2), (4095, 256, 1),  # 32 lanes per row, last workgroup short
-                                          (9, 9728, 2), (11, 9984, 3), (6, 16384, 4)])  # half-row instances
+                                          (9, 9728, 2), (11, 9984, 3), (6, 16384, 4),  # half-row instances
+                                          (4097, 1536, 2), (17, 2560, 2), (13, 5120, 2)])  # the tight instances' edges
 def test_mul_mat_ragged(hip, dev, oracle, qtype, rows, k, n_vec):
     w = oracle.gaussian(rows * k, 7 * rows + k + qtype) * np.float32(0.02)
     wb = realistic_blocks(qtype, w.reshape(-1, 256))
