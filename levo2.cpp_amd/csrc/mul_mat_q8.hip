@@ -239,7 +239,8 @@ __device__ __forceinline__ uint16_t quantize_q8_0_block_x2(const u32x4 (&v)[4], 
 // quants, the last 16 and the F16 scale, each an aligned load; no LDS
 // stage, no realignment. PB = 0: Q8_0 blocks.
 // NV: accumulators per lane, 2 for the CFG pair (n_vec <= 2), else 8.
-template <int LPR, int WPR, int XF, int PB, int NV>
+// CH: chunk loads per lane of the block layout's span (1 for packed weights).
+template <int LPR, int WPR, int XF, int PB, int NV, int CH>
 __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch ml) {
     constexpr bool FUSED = XF == kXF32;
     constexpr bool PAIR = XF == kXF32Pair;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
     const bool have = wave_span<LPR, WPR>(p, grp, wave, row0, nrows, kb0, kb1);
     const int g = lane / LPR;
     const int li = lane % LPR;
-    u32x4 regs[kChunksPerLane];
+    u32x4 regs[CH];
     const int64_t sb0 = (row0 * p.nb + kb0) * kQ8Bytes;
     const int64_t sb1 = (row0 * p.nb + (WPR > 1 ? kb1 : static_cast<int64_t>(nrows) * p.nb)) * kQ8Bytes;
     u32x4 wlo[kPB], whi[kPB];
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
             wd[i] = __builtin_nontemporal_load(drow + kb);
         }
     } else {
-        load_span<kChunksPerLane>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
+        load_span<CH>(p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
     }
 
     // 2. activation blocks -> LDS (raw, through the stage area), then
@@ -417,7 +418,7 @@ __global__ __launch_bounds__(kThreads) void mul_mat_q8_0_kernel(const mm_launch 
         }
     } else {
         const int lead = static_cast<int>(sb0 & 15);
-        store_span<kChunksPerLane>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
+        store_span<CH>(stage, p.w, p.w_bytes, sb0 & ~int64_t{15}, sb1, have, lane, regs);
         wave_lds_fence();
         if (have && g < nrows) {
             const int row_base = WPR > 1 ? 0 : g * p.nb;  // LDS block index of (row g, kb0)
@@ -463,19 +464,19 @@ constexpr int rows_per_workgroup() {
 // The instance for the activations' form (F32 values: two lanes per block up
 // to 128 blocks; else columns for packed matrices, Q8_0 blocks otherwise)
 // and the accumulator count.
-template <int LPR, int WPR, int PB, int NV>
+template <int LPR, int WPR, int PB, int NV, int CH>
 void launch_form(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st) {
     if (ml.xf != nullptr && ml.p.n_vec * ml.p.nb <= kThreads / 2)
-        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
-    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
-    else if constexpr (PB > 0) mul_mat_q8_0_kernel<LPR, WPR, kXColumns, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
-    else mul_mat_q8_0_kernel<LPR, WPR, kXBlocks, PB, NV><<<blocks, kThreads, lds, st>>>(ml);
+        mul_mat_q8_0_kernel<LPR, WPR, kXF32Pair, PB, NV, CH><<<blocks, kThreads, lds, st>>>(ml);
+    else if (ml.xf != nullptr) mul_mat_q8_0_kernel<LPR, WPR, kXF32, PB, NV, CH><<<blocks, kThreads, lds, st>>>(ml);
+    else if constexpr (PB > 0) mul_mat_q8_0_kernel<LPR, WPR, kXColumns, PB, NV, CH><<<blocks, kThreads, lds, st>>>(ml);
+    else mul_mat_q8_0_kernel<LPR, WPR, kXBlocks, PB, NV, CH><<<blocks, kThreads, lds, st>>>(ml);
 }
 
-template <int LPR, int WPR, int PB>
+template <int LPR, int WPR, int PB, int CH = 1>
 int launch_pb(const mm_launch & ml, uint32_t blocks, size_t lds, hipStream_t st, const char * what) {
-    if (ml.p.n_vec <= 2) launch_form<LPR, WPR, PB, 2>(ml, blocks, lds, st);
-    else launch_form<LPR, WPR, PB, kMaxVectors>(ml, blocks, lds, st);
+    if (ml.p.n_vec <= 2) launch_form<LPR, WPR, PB, 2, CH>(ml, blocks, lds, st);
+    else launch_form<LPR, WPR, PB, kMaxVectors, CH>(ml, blocks, lds, st);
     return launch_status(what);
 }
 
@@ -514,7 +515,18 @@ int launch_mm(mm_launch ml, bool packed, hipStream_t st, const char * what) {
         if (per_lane == 3) return launch_pb<LPR, WPR, 3>(ml, blocks, lds, st, what);
         return launch_pb<LPR, WPR, 4>(ml, blocks, lds, st, what);
     }
-    return launch_pb<LPR, WPR, 0>(ml, blocks, lds, st, what);
+    // Block layout: chunk loads per lane sized to the span where it is
+    // smaller than the general instance's (every lane issues all of them):
+    // 5 for half rows up to 294 blocks (ffn_down), 7 for four rows of up to
+    // 52 blocks (K = 1536)
+    const int64_t span_bytes = static_cast<int64_t>(span_blocks) * kQ8Bytes;
+    if constexpr (WPR == 2) {
+        if (span_bytes + 30 <= 5 * 64 * 16) return launch_pb<LPR, WPR, 0, 5>(ml, blocks, lds, st, what);
+    }
+    if constexpr (LPR == 16 && WPR == 1) {
+        if (span_bytes + 30 <= 7 * 64 * 16) return launch_pb<LPR, WPR, 0, 7>(ml, blocks, lds, st, what);
+    }
+    return launch_pb<LPR, WPR, 0, kChunksPerLane>(ml, blocks, lds, st, what);
 }
 
 // The fewest lanes per row that hold the row's blocks in one wave's span.
